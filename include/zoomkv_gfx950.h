@@ -1,0 +1,110 @@
+/*
+ * zoomkv_gfx950.h -- C ABI of libzoomkv_gfx950.so, the MI355X (gfx950)
+ * implementation of ZoomKV's quantized and sparse KV-cache decode path.
+ *
+ * All pointers are device pointers unless stated otherwise; all sizes are in
+ * elements; strides are in elements of the pointed-to type.  Every entry point
+ * launches asynchronously on the given HIP stream (0 = the legacy default
+ * stream), never synchronises the host, never allocates device memory, and
+ * returns 0 on success or a ZKV_E* code; zkv_last_error() then returns the
+ * message of the last failure on the calling thread.
+ *
+ * dtypes: bf16 and fp16 values are passed as uint16_t bit patterns.
+ *
+ * Reference citations use Z/ = runtime/zoomkv_urania_runtime_20261011/ and
+ * S = Z/cache_hub/polar_cache_quest_density_single_layer_kivi.py of
+ * amy-77/zoomkv_revision.
+ */
+#ifndef ZOOMKV_GFX950_H_
+#define ZOOMKV_GFX950_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* zkv_stream_t; /* == hipStream_t */
+
+#define ZKV_OK 0
+#define ZKV_EINVAL 1   /* bad shape / dtype / argument (TORCH_CHECK in the reference) */
+#define ZKV_ELAUNCH 2  /* kernel launch failed (cudaGetLastError in the reference) */
+#define ZKV_ESPACE 3   /* caller-provided workspace / output too small */
+
+/* Message of the last failure on this thread ("" if none). */
+const char* zkv_last_error(void);
+/* Library / format version string. */
+const char* zkv_version(void);
+
+/* ------------------------------------------------------------------------
+ * Format R: the reference's chunk-major KIVI K cache.
+ *
+ * zkv_chunk_encode replaces the full-chunk branch of
+ * _compute_and_store_chunk_minmax + _kivi_pack_chunks (S:2119-2143,
+ * S:1965-2020), which are pure torch in the reference.  For each of the
+ * n_chunks chunks of g consecutive tokens of `keys` it writes, at chunk index
+ * chunk_start + c: per-channel min / max / mean (bf16), valid = 1, and the
+ * 4-bit codes in the chunk-major layout [.., n_chunks_max, 16, g] int32.
+ *
+ * keys      bf16 [bs, kv, n_tok >= n_chunks*g, 128] with strides
+ *           (k_sb, k_sh, k_st), channel stride 1
+ * chunk_min/chunk_max/chunk_centroid  bf16 [bs, kv, n_chunks_max, 128] contiguous
+ * chunk_valid  uint8 (bool) [bs, kv, n_chunks_max]
+ * packed_K  int32 [bs, kv, n_chunks_max, 16, g] contiguous
+ * g in {8, 16, 32}.
+ * ------------------------------------------------------------------------ */
+int zkv_chunk_encode(const uint16_t* keys, int64_t k_sb, int64_t k_sh, int64_t k_st,
+                     int bs, int kv, int g, int n_chunks, int chunk_start, int n_chunks_max,
+                     uint16_t* chunk_min, uint16_t* chunk_max, uint16_t* chunk_centroid,
+                     uint8_t* chunk_valid, int32_t* packed_K, zkv_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Format Q: 4-bit K (per channel, groups of 32 tokens) and V (per token,
+ * groups of 32 channels) with fp16 scale / zero.  No reference counterpart
+ * (the reference keeps V in bf16, S:561-571); the code ladder is the
+ * reference's (S:2003-2009) and the layouts are:
+ *   k_codes int32 [bs, kv, G_cap, 16, 32]      k_meta fp16 [bs, kv, G_cap, 16, 2, 8]
+ *   v_codes int32 [bs, kv, G_cap, 4, 128]      v_meta fp16 [bs, kv, G_cap, 4, 4, 2, 8]
+ * (word / slot order documented with the kernel).
+ *
+ * zkv_kivi4_pack quantizes tokens [32*g0, 32*(g0+n_groups)) of the cache
+ * from src tokens [0, 32*n_groups) of k / v.
+ * k, v     bf16 [bs, kv, n_tok, 128], strides (sb, sh, st), channel stride 1
+ * ------------------------------------------------------------------------ */
+int zkv_kivi4_pack(const uint16_t* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
+                   const uint16_t* v, int64_t v_sb, int64_t v_sh, int64_t v_st,
+                   int bs, int kv, int n_groups, int g0, int g_cap,
+                   int32_t* k_codes, uint16_t* k_meta, int32_t* v_codes, uint16_t* v_meta,
+                   zkv_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Fused 4-bit decode attention over a Format Q cache plus a bf16 residual
+ * window: out = softmax(q K^T * sm_scale) V, causal = False, with GQA
+ * (hq / kv query heads per KV head, hq / kv <= 16, consecutive query heads
+ * share a KV head).  Replaces flash_attn_with_kvcache_compat(q, k, v,
+ * causal=False) (Z/attn_hub/flash_attn_compat.py:44-100, called at
+ * S:1742-1747) for a quantized cache.
+ *
+ * q        bf16 [bs, hq, 128] with strides (q_sb, q_sh), channel stride 1
+ * k_res, v_res  bf16 [bs, kv, R_cap, 128] contiguous; tokens [0, res_len) used
+ * n_groups groups of the Format Q cache are attended (all bs share lengths)
+ * out      [bs, hq, 128] contiguous, bf16 (out_f32 == 0) or fp32 (out_f32 != 0)
+ * n_splits context splits per (b, kv head); 0 = automatic
+ * workspace device scratch of zkv_kivi4_attention_workspace_size() bytes
+ * ------------------------------------------------------------------------ */
+size_t zkv_kivi4_attention_workspace_size(int bs, int hq, int kv, int n_groups, int res_len,
+                                          int n_splits);
+int zkv_kivi4_decode_attention(const uint16_t* q, int64_t q_sb, int64_t q_sh,
+                               const int32_t* k_codes, const uint16_t* k_meta,
+                               const int32_t* v_codes, const uint16_t* v_meta, int g_cap,
+                               const uint16_t* k_res, const uint16_t* v_res, int r_cap,
+                               int bs, int hq, int kv, int n_groups, int res_len,
+                               float sm_scale, void* out, int out_f32, int n_splits,
+                               void* workspace, size_t workspace_bytes, zkv_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ZOOMKV_GFX950_H_ */

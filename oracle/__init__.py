@@ -1,0 +1,45 @@
+"""CPU oracle for the ZoomKV quantized / sparse KV decode path.
+
+TEST INFRASTRUCTURE ONLY.  Nothing in the product (``zoomkv_revision_amd``)
+imports, links or executes anything under ``oracle/``; only ``tests/``,
+``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` use
+it, and only as the checker (or the timed CPU baseline), never as the thing
+measured or shipped.
+
+Every function restates an algorithm of the reference
+(amy-77/zoomkv_revision, runtime/zoomkv_urania_runtime_20261011) in plain
+numpy, with each floating-point operation written out and rounded
+explicitly, and cites the reference file:line it follows.  Citation prefixes:
+
+  Z/  = runtime/zoomkv_urania_runtime_20261011/
+  S   = Z/cache_hub/polar_cache_quest_density_single_layer_kivi.py
+  PC  = Z/cache_hub/polar_cache.py
+
+How each part is pinned (beyond the reference's own tests, which hold no
+golden vectors for this path) is listed in ``PINNING`` below and checked by
+``tests/test_oracle_*.py``.
+"""
+
+PINNING = {
+    "numerics.bf16_round": "exhaustive against torch's float32->bfloat16 cast",
+    "kivi.kivi_codes": "op-by-op against torch-CPU bfloat16 ops mirroring "
+                       "S:2003-2009 and quant_pack.py:112-121; exhaustive "
+                       "divide-vs-reciprocal check over all bf16 diffs; "
+                       "invariants (flat group -> 0, max -> 15, range)",
+    "kivi.pack_last_dim": "closed form + brute-force round trip of all 16 "
+                          "code values at every nibble position",
+    "kivi.kivi4_dequant / attention": "textbook softmax attention in float64 "
+                                      "over dequantized K/V; LSE split "
+                                      "invariance; GQA head independence",
+    "quest.quest_chunk_score": "upper-bound invariant vs brute force "
+                               "max_t q.k_t; order-independence where sums "
+                               "are exact; torch-CPU product identity",
+    "topk": "set equality with numpy argsort on tie-free inputs; planted "
+            "selections",
+    "stage2.kivi_qk_dense_sparse": "op-by-op bf16 ladder vs torch-CPU "
+                                   "(quant_pack/qk_dot ops); bitonic network "
+                                   "vs stable sort on tie-free inputs",
+    "density": "tree sum equals fsum within 1 ulp; exact on dyadic inputs",
+    "rabitq": "popcount identity vs brute-force +-1 dot products; FWHT vs "
+              "explicit Hadamard matrix; correction factor closed form",
+}

@@ -1,0 +1,134 @@
+"""GPU parity: Format R encode, Format Q pack and fused 4-bit decode attention
+against the CPU oracle (bit-exact codes / metadata; attention within 2e-3)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import kivi as okivi
+from oracle.numerics import bf16_bits
+from tests.helpers import from_torch, gaussian_bf16, to_bf16
+
+pytestmark = pytest.mark.gpu
+
+ATOL = 2e-3  # north-star tolerance for attention outputs
+
+
+def _zk():
+    from zoomkv_revision_amd import kivi
+    return kivi
+
+
+@pytest.mark.parametrize("g", [8, 16, 32])
+def test_chunk_encode_bit_exact(rng, g):
+    zk = _zk()
+    bs, kv, n_tok, n_max, start = 2, 3, 5 * g + 3, 12, 4
+    keys = gaussian_bf16(rng, (bs, kv, n_tok, 128), outlier_channels=4)
+    mn, mx, mean, packed = okivi.encode_chunks_ref(keys, g)
+    # keys handed over with a non-contiguous token stride (a [bs, n, kv, 128] view)
+    kt = to_bf16(np.ascontiguousarray(np.swapaxes(keys, 1, 2))).transpose(1, 2)
+    cmin = torch.zeros(bs, kv, n_max, 128, dtype=torch.bfloat16, device="cuda")
+    cmax, ccen = torch.zeros_like(cmin), torch.zeros_like(cmin)
+    valid = torch.zeros(bs, kv, n_max, dtype=torch.bool, device="cuda")
+    pk = torch.zeros(bs, kv, n_max, 16, g, dtype=torch.int32, device="cuda")
+    n = zk.chunk_encode(kt, g, start, cmin, cmax, ccen, valid, pk)
+    torch.cuda.synchronize()
+    assert n == 5
+    sl = slice(start, start + 5)
+    assert np.array_equal(from_torch(pk)[:, :, sl], packed)
+    assert np.array_equal(bf16_bits(from_torch(cmin)[:, :, sl]), bf16_bits(mn))
+    assert np.array_equal(bf16_bits(from_torch(cmax)[:, :, sl]), bf16_bits(mx))
+    assert np.array_equal(bf16_bits(from_torch(ccen)[:, :, sl]), bf16_bits(mean))
+    v = from_torch(valid)
+    assert v[:, :, sl].all() and not v[:, :, :start].any() and not v[:, :, start + 5:].any()
+
+
+def _pack(rng, bs, kv, ng, outliers=1, g_cap=None, g0=0):
+    zk = _zk()
+    n = ng * 32
+    k = gaussian_bf16(rng, (bs, kv, n, 128), outlier_channels=outliers)
+    v = gaussian_bf16(rng, (bs, kv, n, 128), outlier_channels=outliers)
+    cache = zk.Kivi4Cache.allocate(bs, kv, g_cap or ng + g0, 128)
+    zk.kivi4_pack(to_bf16(k), to_bf16(v), cache, g0)
+    return k, v, cache
+
+
+def test_kivi4_pack_bit_exact(rng):
+    k, v, cache = _pack(rng, 2, 3, 5, outliers=2, g_cap=9, g0=3)
+    torch.cuda.synchronize()
+    ref = okivi.quantize_kivi4(k, v)
+    sl = slice(3, 8)
+    assert np.array_equal(from_torch(cache.k_codes)[:, :, sl], ref.k_codes)
+    assert np.array_equal(from_torch(cache.k_meta)[:, :, sl], ref.k_meta)
+    assert np.array_equal(from_torch(cache.v_codes)[:, :, sl], ref.v_codes)
+    assert np.array_equal(from_torch(cache.v_meta)[:, :, sl], ref.v_meta)
+    assert not from_torch(cache.k_codes)[:, :, :3].any()
+
+
+def test_kivi4_pack_strided_input(rng):
+    zk = _zk()
+    bs, kv, n = 2, 2, 64
+    k = gaussian_bf16(rng, (bs, n, kv, 128))          # [bs, n, kv, d] like the model's layout
+    v = gaussian_bf16(rng, (bs, n, kv, 128))
+    cache = zk.Kivi4Cache.allocate(bs, kv, 2)
+    zk.kivi4_pack(to_bf16(k).transpose(1, 2), to_bf16(v).transpose(1, 2), cache, 0)
+    torch.cuda.synchronize()
+    ref = okivi.quantize_kivi4(np.swapaxes(k, 1, 2), np.swapaxes(v, 1, 2))
+    assert np.array_equal(from_torch(cache.k_codes), ref.k_codes)
+    assert np.array_equal(from_torch(cache.v_meta), ref.v_meta)
+
+
+@pytest.mark.parametrize("bs,hq,kv,ng,res,splits", [
+    (2, 8, 2, 5, 40, 0),      # GQA 4, ragged residual
+    (2, 8, 2, 5, 40, 1),      # single split
+    (1, 32, 8, 9, 128, 3),    # Qwen3-8B heads, full residual window
+    (3, 4, 4, 4, 0, 0),       # MHA, no residual
+    (1, 16, 1, 3, 17, 2),     # 16 query heads per KV head
+    (2, 8, 2, 0, 77, 0),      # residual only
+])
+def test_decode_attention_matches_oracle(rng, bs, hq, kv, ng, res, splits):
+    zk = _zk()
+    k, v, cache = _pack(rng, bs, kv, ng, outliers=1) if ng else (None, None, zk.Kivi4Cache.allocate(bs, kv, 1))
+    kr = gaussian_bf16(rng, (bs, kv, 128, 128))
+    vr = gaussian_bf16(rng, (bs, kv, 128, 128))
+    cache.k_res.copy_(to_bf16(kr))
+    cache.v_res.copy_(to_bf16(vr))
+    q = gaussian_bf16(rng, (bs, hq, 128))
+    qt = to_bf16(q)
+    out32 = zk.kivi4_decode_attention(qt, cache, ng, res, out_dtype=torch.float32, n_splits=splits)
+    out16 = zk.kivi4_decode_attention(qt.unsqueeze(1), cache, ng, res, n_splits=splits)
+    torch.cuda.synchronize()
+    if ng:
+        ref_cache = okivi.quantize_kivi4(k, v)
+    else:
+        ref_cache = okivi.Kivi4Cache(*(np.zeros((bs, kv, 0) + s, dtype=d) for s, d in
+                                       (((16, 32), np.int32), ((16, 2, 8), np.uint16),
+                                        ((4, 128), np.int32), ((4, 4, 2, 8), np.uint16))))
+    ref = okivi.kivi4_decode_attention(q, ref_cache, ng, kr, vr, res, 1 / np.sqrt(128))
+    got = from_torch(out32)
+    assert got.shape == ref.shape
+    err = np.abs(got - ref).max()
+    assert err <= ATOL, f"max abs err {err}"
+    got16 = from_torch(out16)[:, 0]
+    assert np.abs(got16 - ref).max() <= ATOL + np.abs(ref).max() * 2 ** -8
+
+
+def test_decode_attention_split_invariance(rng):
+    zk = _zk()
+    _, _, cache = _pack(rng, 1, 2, 12)
+    q = to_bf16(gaussian_bf16(rng, (1, 8, 128)))
+    outs = [from_torch(zk.kivi4_decode_attention(q, cache, 12, 0, out_dtype=torch.float32, n_splits=s))
+            for s in (1, 2, 5, 12)]
+    for o in outs[1:]:
+        assert np.abs(o - outs[0]).max() <= 1e-5
+
+
+def test_decode_attention_rejects_bad_shapes(rng):
+    zk = _zk()
+    cache = zk.Kivi4Cache.allocate(1, 2, 4)
+    q = torch.zeros(1, 6, 128, dtype=torch.bfloat16, device="cuda")   # 6 % 4 != 0 ... hq % kv ok but
+    with pytest.raises(ValueError):
+        zk.kivi4_decode_attention(torch.zeros(1, 5, 128, dtype=torch.bfloat16, device="cuda"), cache, 2, 0)
+    with pytest.raises(RuntimeError):
+        zk.kivi4_decode_attention(q, cache, 5, 0)          # n_groups > capacity
+    with pytest.raises(RuntimeError):
+        zk.kivi4_decode_attention(q, cache, 0, 0)          # empty context

@@ -1,0 +1,171 @@
+"""Pins of the KIVI oracle (CPU).  See oracle/__init__.py PINNING."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import kivi
+from oracle.numerics import BF16_1EM8, bf16_bits, bf16_to_f32, bf16r, f16_bits
+from tests.helpers import gaussian_bf16
+
+
+def test_bf16_round_matches_torch_on_all_bf16_neighbourhoods():
+    hi = np.arange(1 << 16, dtype=np.uint32)
+    hi = hi[((hi << 16) & 0x7F800000) != 0x7F800000]          # finite only
+    lows = np.array([0x0000, 0x0001, 0x7FFF, 0x8000, 0x8001, 0xFFFF], dtype=np.uint32)
+    u = ((hi[:, None] << 16) | lows[None, :]).reshape(-1)
+    x = u.view(np.float32)
+    ours = bf16_bits(x)
+    ref = torch.from_numpy(x.copy()).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(ours, ref)
+
+
+def test_scale_division_equals_reciprocal_multiply_for_every_bf16():
+    """torch on CUDA computes bf16 / python-scalar as x * fp32(1/15) (the
+    reference's production path, S:2003); torch on CPU and this oracle divide.
+    Both round to the same bf16 for every non-negative finite bf16 diff."""
+    u = np.arange(0, 0x7F80, dtype=np.uint32)
+    d = bf16_to_f32(u.astype(np.uint16))
+    div = bf16_bits(d / np.float32(15.0))
+    mul = bf16_bits(d * (np.float32(1.0) / np.float32(15.0)))
+    assert np.array_equal(div, mul)
+
+
+def _torch_ladder(K, mn, mx):
+    """The reference's torch op sequence (S:2003-2009 / quant_pack.py:112-121) on CPU bf16."""
+    scale = (mx - mn) / float(15)
+    scale_safe = scale.clamp(min=1e-8)
+    return ((K - mn) / scale_safe).clamp_(0.0, 15.0).round_().to(torch.int32)
+
+
+@pytest.mark.parametrize("g", [8, 16, 32])
+def test_kivi_codes_match_torch_bf16_ops(rng, g):
+    k = gaussian_bf16(rng, (2, 3, 7 * g, 128), outlier_channels=4)
+    k[0, 0, :g, 5] = k[0, 0, 0, 5]                 # one flat chunk/channel
+    kc = k.reshape(2, 3, 7, g, 128)
+    mn = kc.min(axis=3, keepdims=True)
+    mx = kc.max(axis=3, keepdims=True)
+    ours = kivi.kivi_codes(kc, mn, mx)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(torch.bfloat16)
+    ref = _torch_ladder(t(kc), t(mn), t(mx)).numpy()
+    assert np.array_equal(ours, ref)
+    assert ours.min() >= 0 and ours.max() <= 15
+    assert np.all(ours[0, 0, 0, :, 5] == 0)        # flat group -> all zero codes
+    # the maximum of every (non-flat) group/channel encodes to 15, the minimum to 0
+    at_max = kc == mx
+    assert np.all(ours[at_max & (mx != mn)] == 15)
+    assert np.all(ours[kc == mn] == 0)
+
+
+def test_per_token_ladder_matches_torch(rng):
+    v = gaussian_bf16(rng, (2, 2, 40, 128), outlier_channels=2)
+    vg = v.reshape(2, 2, 40, 4, 32)
+    mn = vg.min(axis=4, keepdims=True)
+    mx = vg.max(axis=4, keepdims=True)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(torch.bfloat16)
+    assert np.array_equal(kivi.kivi_codes(vg, mn, mx), _torch_ladder(t(vg), t(mn), t(mx)).numpy())
+
+
+def test_clamp_constant_is_bf16_of_1e8():
+    assert float(BF16_1EM8) == float(torch.tensor(1e-8, dtype=torch.bfloat16).float())
+
+
+def test_pack_unpack_every_code_at_every_position():
+    codes = np.zeros((16, 8, 8), dtype=np.int32)
+    for val in range(16):
+        for pos in range(8):
+            codes[val, pos, pos] = val
+    packed = kivi.pack_last_dim(codes)
+    assert packed.shape == (16, 8, 1)
+    for val in range(16):
+        for pos in range(8):
+            w = int(packed[val, pos, 0]) & 0xFFFFFFFF
+            assert w == val << (4 * pos)
+    assert np.array_equal(kivi.unpack_last_dim(packed), codes)
+    # bit 31 set -> negative int32, exactly as torch's int32 sum (quant_pack.py:140)
+    assert packed[15, 7, 0] < 0
+
+
+def test_pack_matches_torch_shift_sum(rng):
+    codes = rng.integers(0, 16, size=(3, 5, 128), dtype=np.int32)
+    t = torch.from_numpy(codes).view(3, 5, 16, 8)
+    shifts = torch.arange(8, dtype=torch.int32) * 4
+    ref = (t << shifts).sum(dim=-1, dtype=torch.int32).numpy()
+    assert np.array_equal(kivi.pack_last_dim(codes), ref)
+
+
+def test_format_r_layout_is_chunk_major(rng):
+    k = gaussian_bf16(rng, (1, 2, 48, 128))
+    mn, mx, mean, packed = kivi.encode_chunks_ref(k, 16)
+    assert packed.shape == (1, 2, 3, 16, 16)
+    codes = kivi.kivi_codes(k.reshape(1, 2, 3, 16, 128), mn[:, :, :, None], mx[:, :, :, None])
+    tok = kivi.pack_last_dim(codes)               # [.., chunk, token, p]
+    assert np.array_equal(packed, np.swapaxes(tok, -1, -2))
+    t = torch.from_numpy(k.reshape(1, 2, 3, 16, 128)).to(torch.bfloat16)
+    assert np.array_equal(bf16_bits(mn), t.amin(dim=3).view(torch.int16).numpy().view(np.uint16))
+    assert np.array_equal(bf16_bits(mx), t.amax(dim=3).view(torch.int16).numpy().view(np.uint16))
+    # torch's bf16 mean agrees with the canonical sequential fp32 sum whenever the sum is exact
+    ref_mean = t.mean(dim=3).float().numpy()
+    assert np.max(np.abs(ref_mean - mean)) <= np.max(np.abs(mean)) * 2 ** -7
+
+
+def test_dequant_ref_is_two_rounding_bf16_ladder(rng):
+    k = gaussian_bf16(rng, (1, 1, 32, 128))
+    mn, mx, _, packed = kivi.encode_chunks_ref(k, 16)
+    kh = kivi.dequant_ref(packed, mn, mx)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(torch.bfloat16)
+    codes = kivi.unpack_last_dim(np.swapaxes(packed, -1, -2))
+    scale = (t(mx) - t(mn)) / 15.0
+    ref = (torch.from_numpy(codes).to(torch.bfloat16) * scale.unsqueeze(3) + t(mn).unsqueeze(3)).float().numpy()
+    assert np.array_equal(kh, ref)
+    assert np.max(np.abs(kh - k.reshape(kh.shape))) <= np.max(kivi.kivi_scale(mn, mx)) * 0.51 + 1e-2
+
+
+def test_format_q_k_codes_equal_format_r_with_group_32(rng):
+    k = gaussian_bf16(rng, (2, 2, 96, 128), outlier_channels=4)
+    v = gaussian_bf16(rng, (2, 2, 96, 128))
+    q = kivi.quantize_kivi4(k, v)
+    _, _, _, packed_r = kivi.encode_chunks_ref(k, 32)
+    assert np.array_equal(q.k_codes, packed_r)
+
+
+def test_format_q_metadata_and_codes_consistent(rng):
+    k = gaussian_bf16(rng, (1, 3, 64, 128), outlier_channels=2)
+    v = gaussian_bf16(rng, (1, 3, 64, 128), outlier_channels=2)
+    c = kivi.quantize_kivi4(k, v)
+    kc, ks, kz, vc, vs, vz = kivi.kivi4_codes_and_meta(k, v)
+    kh, vh = kivi.dequant_kivi4(c)
+    kh2 = (kc.reshape(1, 3, 2, 32, 128) * ks[:, :, :, None].astype(np.float64)
+           + kz[:, :, :, None]).reshape(kh.shape)
+    vh2 = vc * np.repeat(vs, 32, -1).astype(np.float64) + np.repeat(vz, 32, -1)
+    assert np.array_equal(kh, kh2) and np.array_equal(vh, vh2)
+    # zero == group minimum exactly (fp16 holds these bf16 values)
+    assert np.array_equal(kz, k.reshape(1, 3, 2, 32, 128).min(axis=3))
+    # reconstruction error: half a step plus the bf16 roundings of the ladder
+    assert np.all(np.abs(kh - k) <= np.repeat(ks, 32, axis=2) * 0.65 + 1e-3)
+    # every slot of k_meta points at the channel KSLOT says
+    for p in range(16):
+        for s in range(8):
+            ch = 8 * p + kivi.KSLOT[s]
+            assert np.array_equal(c.k_meta[..., p, 0, s], f16_bits(kivi.kivi_scale(
+                k.reshape(1, 3, 2, 32, 128).min(axis=3), k.reshape(1, 3, 2, 32, 128).max(axis=3))[..., ch]))
+
+
+def test_attention_oracle_textbook_and_lse_split(rng):
+    bs, hq, hkv, n = 2, 8, 2, 70
+    q = gaussian_bf16(rng, (bs, hq, 128))
+    k = rng.standard_normal((bs, hkv, n, 128))
+    v = rng.standard_normal((bs, hkv, n, 128))
+    sc = 1 / np.sqrt(128)
+    out, lse = kivi.attention(q, k, v, sc, return_lse=True)
+    # explicit loops for one head
+    b, h = 1, 5
+    s = np.array([np.dot(q[b, h].astype(np.float64), k[b, h // 4, t]) for t in range(n)]) * sc
+    w = np.exp(s - s.max())
+    ref = (w[:, None] * v[b, h // 4]).sum(0) / w.sum()
+    assert np.allclose(out[b, h], ref, atol=1e-12)
+    # split at an arbitrary point and LSE-merge (lse_merge.py:79-119)
+    o1, l1 = kivi.attention(q, k[:, :, :23], v[:, :, :23], sc, return_lse=True)
+    o2, l2 = kivi.attention(q, k[:, :, 23:], v[:, :, 23:], sc, return_lse=True)
+    m = np.maximum(l1, l2)
+    w1, w2 = np.exp(l1 - m)[..., None], np.exp(l2 - m)[..., None]
+    assert np.allclose((w1 * o1 + w2 * o2) / (w1 + w2), out, atol=1e-12)

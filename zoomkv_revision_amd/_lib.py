@@ -1,0 +1,81 @@
+"""ctypes binding of libzoomkv_gfx950.so (the C ABI declared in include/zoomkv_gfx950.h).
+
+There is no fallback: if the library is missing or fails to load, every op
+raises.  Errors returned by an entry point become ``RuntimeError`` carrying
+``zkv_last_error()``, mirroring the reference's TORCH_CHECK -> RuntimeError
+convention (e.g. Z/cache_hub/kivi/kivi_qk_dot.cu:338-394).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(os.environ.get("ZOOMKV_GFX950_LIB",
+                               Path(__file__).resolve().parent / "libzoomkv_gfx950.so"))
+
+P = C.c_void_p
+I32 = C.c_int
+I64 = C.c_int64
+F32 = C.c_float
+SZ = C.c_size_t
+
+# name -> (restype, argtypes); kept in the order of include/zoomkv_gfx950.h
+SIGNATURES = {
+    "zkv_last_error": (C.c_char_p, []),
+    "zkv_version": (C.c_char_p, []),
+    "zkv_chunk_encode": (I32, [P, I64, I64, I64, I32, I32, I32, I32, I32, I32,
+                               P, P, P, P, P, P]),
+    "zkv_kivi4_pack": (I32, [P, I64, I64, I64, P, I64, I64, I64, I32, I32, I32, I32, I32,
+                             P, P, P, P, P]),
+    "zkv_kivi4_attention_workspace_size": (SZ, [I32, I32, I32, I32, I32, I32]),
+    "zkv_kivi4_decode_attention": (I32, [P, I64, I64, P, P, P, P, I32, P, P, I32,
+                                         I32, I32, I32, I32, I32, F32, P, I32, I32,
+                                         P, SZ, P]),
+}
+
+_lib = None
+
+
+class ZkvError(RuntimeError):
+    pass
+
+
+def lib() -> C.CDLL:
+    """Load (once) and return the native library; raise if it is missing."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise ZkvError(
+                f"libzoomkv_gfx950.so not found at {LIB_PATH}; build it with "
+                "`python -m zoomkv_revision_amd.build` (no CPU fallback exists)")
+        handle = C.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = handle
+    return _lib
+
+
+def check(rc: int) -> None:
+    if rc != 0:
+        msg = lib().zkv_last_error().decode(errors="replace")
+        raise ZkvError(f"zoomkv_gfx950 error {rc}: {msg}")
+
+
+def stream_of(t: torch.Tensor) -> int:
+    """The current HIP stream of t's device (what the reference's kernels use)."""
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def require_gpu(*ts: torch.Tensor) -> None:
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise ZkvError("zoomkv_gfx950 ops take device tensors (no CPU path exists)")

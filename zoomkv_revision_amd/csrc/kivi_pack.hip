@@ -1,0 +1,221 @@
+// KIVI 4-bit quantize-and-pack kernels (gfx950).
+//
+// Format R (the reference's K cache): zkv_chunk_encode fuses the full-chunk
+// part of _compute_and_store_chunk_minmax (S:2119-2143) -- per-channel
+// amin / amax / mean over each chunk and the valid flag -- with
+// _kivi_pack_chunks (S:1965-2020): the bf16 quantisation ladder of S:2003-2009
+// and the chunk-major int32 packing of quant_pack.py:124-141 + S:2017.
+//
+// Format Q (north-star K + V cache): zkv_kivi4_pack quantizes K per channel
+// over groups of 32 tokens and V per token over groups of 32 channels with the
+// same ladder and stores fp16 scale / zero in the order the decode kernel's
+// MFMA operands consume them (see decode_attention.hip).
+//
+// Both kernels are HBM-bound elementwise / small-reduction work: one
+// workgroup of 128 lanes per (chunk | group, kv head, batch) reads the bf16
+// keys once (coalesced 256 B rows), keeps the 4-bit codes in LDS and writes
+// the packed words with coalesced dword stores.
+#include "zkv_common.hpp"
+
+namespace zkv {
+namespace {
+
+// ------------------------------- Format R ---------------------------------
+template <int G>
+__global__ __launch_bounds__(128) void chunk_encode_kernel(
+    const uint16_t* __restrict__ keys, int64_t k_sb, int64_t k_sh, int64_t k_st, int kv,
+    int chunk_start, int n_chunks_max, uint16_t* __restrict__ cmin, uint16_t* __restrict__ cmax,
+    uint16_t* __restrict__ ccent, uint8_t* __restrict__ cvalid, int32_t* __restrict__ packed) {
+  __shared__ uint8_t codes[G][128];
+  const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int d = threadIdx.x;
+  const uint16_t* src = keys + b * k_sb + h * k_sh + static_cast<int64_t>(c) * G * k_st + d;
+  float x[G];
+#pragma unroll
+  for (int t = 0; t < G; ++t) x[t] = bf16_to_f32(src[t * k_st]);
+  float mn = x[0], mx = x[0], acc = 0.0f;
+#pragma unroll
+  for (int t = 0; t < G; ++t) {
+    mn = fminf(mn, x[t]);
+    mx = fmaxf(mx, x[t]);
+    acc = acc + x[t];  // canonical sequential fp32 sum over the chunk's tokens
+  }
+  const float safe = kivi_safe(kivi_scale(mn, mx));
+#pragma unroll
+  for (int t = 0; t < G; ++t) codes[t][d] = static_cast<uint8_t>(kivi_code(x[t], mn, safe));
+
+  const int64_t bh = static_cast<int64_t>(b) * kv + h;
+  const int64_t chunk = bh * n_chunks_max + chunk_start + c;
+  cmin[chunk * 128 + d] = f32_to_bf16_bits(mn);
+  cmax[chunk * 128 + d] = f32_to_bf16_bits(mx);
+  ccent[chunk * 128 + d] = f32_to_bf16_bits(acc / static_cast<float>(G));
+  if (d == 0) cvalid[chunk] = 1;
+  __syncthreads();
+
+  // word (p, t) = sum_j code[t][8p + j] << 4j, stored p-major: index p*G + t
+  int32_t* dst = packed + chunk * (16 * G);
+#pragma unroll
+  for (int i = 0; i < (16 * G) / 128; ++i) {
+    const int w = d + 128 * i;
+    const int p = w / G, t = w % G;
+    const uint64_t cb = *reinterpret_cast<const uint64_t*>(&codes[t][8 * p]);
+    uint32_t word = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) word |= static_cast<uint32_t>((cb >> (8 * j)) & 0xF) << (4 * j);
+    dst[w] = static_cast<int32_t>(word);
+  }
+}
+
+// ------------------------------- Format Q ---------------------------------
+// k_meta slot s of dim-block p holds channel 8p + KSLOT[s]; the inverse map of
+// channel 8p + j is slot 2*(j % 4) + j / 4.  v words: nibble k of word (r, d)
+// holds token VTOK[r][k] = TAU[r][VELEM[k]].
+__constant__ uint8_t kVTok[4][8] = {
+    {0, 2, 16, 18, 1, 3, 17, 19},
+    {4, 6, 20, 22, 5, 7, 21, 23},
+    {8, 10, 24, 26, 9, 11, 25, 27},
+    {12, 14, 28, 30, 13, 15, 29, 31},
+};
+
+__global__ __launch_bounds__(128) void kivi4_pack_kernel(
+    const uint16_t* __restrict__ k, int64_t k_sb, int64_t k_sh, int64_t k_st,
+    const uint16_t* __restrict__ v, int64_t v_sb, int64_t v_sh, int64_t v_st, int kv, int g0,
+    int g_cap, int32_t* __restrict__ k_codes, uint16_t* __restrict__ k_meta,
+    int32_t* __restrict__ v_codes, uint16_t* __restrict__ v_meta) {
+  __shared__ uint8_t kc[32][128];
+  __shared__ uint8_t vc[32][128];
+  const int g = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x;
+  const int64_t bhg = (static_cast<int64_t>(b) * kv + h) * g_cap + g0 + g;
+
+  // ---- K: lane = channel d, 32 tokens of the group ----
+  {
+    const int d = tid;
+    const uint16_t* src = k + b * k_sb + h * k_sh + static_cast<int64_t>(g) * 32 * k_st + d;
+    float x[32];
+#pragma unroll
+    for (int t = 0; t < 32; ++t) x[t] = bf16_to_f32(src[t * k_st]);
+    float mn = x[0], mx = x[0];
+#pragma unroll
+    for (int t = 1; t < 32; ++t) {
+      mn = fminf(mn, x[t]);
+      mx = fmaxf(mx, x[t]);
+    }
+    const float scale = kivi_scale(mn, mx);
+    const float safe = kivi_safe(scale);
+#pragma unroll
+    for (int t = 0; t < 32; ++t) kc[t][d] = static_cast<uint8_t>(kivi_code(x[t], mn, safe));
+    const int p = d >> 3, j = d & 7;
+    const int slot = 2 * (j & 3) + (j >> 2);
+    uint16_t* km = k_meta + bhg * 256 + p * 16;
+    km[slot] = f32_to_f16_bits(scale);
+    km[8 + slot] = f32_to_f16_bits(mn);
+  }
+  // ---- V: lane = (token t, channel group gd), 32 channels ----
+  {
+    const int t = tid >> 2, gd = tid & 3;
+    const uint16_t* src = v + b * v_sb + h * v_sh + (static_cast<int64_t>(g) * 32 + t) * v_st + 32 * gd;
+    float x[32];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const u32x4_t w = *reinterpret_cast<const u32x4_t*>(src + 8 * i);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        x[8 * i + 2 * q] = __uint_as_float(w[q] << 16);
+        x[8 * i + 2 * q + 1] = __uint_as_float(w[q] & 0xFFFF0000u);
+      }
+    }
+    float mn = x[0], mx = x[0];
+#pragma unroll
+    for (int i = 1; i < 32; ++i) {
+      mn = fminf(mn, x[i]);
+      mx = fmaxf(mx, x[i]);
+    }
+    const float scale = kivi_scale(mn, mx);
+    const float safe = kivi_safe(scale);
+#pragma unroll
+    for (int i = 0; i < 32; ++i) vc[t][32 * gd + i] = static_cast<uint8_t>(kivi_code(x[i], mn, safe));
+    // token t sits in octet r at element e (TAU[r][e] == t)
+    const int r = (t & 15) >> 2;
+    const int e = (t & 3) + ((t >> 4) << 2);
+    uint16_t* vm = v_meta + bhg * 256 + (gd * 4 + r) * 16;
+    vm[e] = f32_to_f16_bits(scale);
+    vm[8 + e] = f32_to_f16_bits(mn);
+  }
+  __syncthreads();
+  // ---- K words: index p*32 + t ----
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int w = tid + 128 * i;
+    const int p = w >> 5, t = w & 31;
+    const uint64_t cb = *reinterpret_cast<const uint64_t*>(&kc[t][8 * p]);
+    uint32_t word = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) word |= static_cast<uint32_t>((cb >> (8 * j)) & 0xF) << (4 * j);
+    k_codes[bhg * 512 + w] = static_cast<int32_t>(word);
+  }
+  // ---- V words: index r*128 + d ----
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int w = tid + 128 * i;
+    const int r = w >> 7, d = w & 127;
+    uint32_t word = 0;
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) word |= static_cast<uint32_t>(vc[kVTok[r][kk]][d]) << (4 * kk);
+    v_codes[bhg * 512 + w] = static_cast<int32_t>(word);
+  }
+}
+
+}  // namespace
+}  // namespace zkv
+
+using namespace zkv;
+
+extern "C" int zkv_chunk_encode(const uint16_t* keys, int64_t k_sb, int64_t k_sh, int64_t k_st,
+                                int bs, int kv, int g, int n_chunks, int chunk_start,
+                                int n_chunks_max, uint16_t* chunk_min, uint16_t* chunk_max,
+                                uint16_t* chunk_centroid, uint8_t* chunk_valid, int32_t* packed_K,
+                                zkv_stream_t stream) {
+  ZKV_REQUIRE(keys && chunk_min && chunk_max && chunk_centroid && chunk_valid && packed_K,
+              "zkv_chunk_encode: null pointer");
+  ZKV_REQUIRE(g == 8 || g == 16 || g == 32, "zkv_chunk_encode: chunk size must be 8, 16 or 32; got %d", g);
+  ZKV_REQUIRE(bs > 0 && kv > 0 && n_chunks >= 0 && chunk_start >= 0,
+              "zkv_chunk_encode: bad sizes bs=%d kv=%d n_chunks=%d chunk_start=%d", bs, kv,
+              n_chunks, chunk_start);
+  ZKV_REQUIRE(chunk_start + n_chunks <= n_chunks_max,
+              "zkv_chunk_encode: chunk_end=%d exceeds n_chunks_max=%d", chunk_start + n_chunks,
+              n_chunks_max);
+  if (n_chunks == 0) return ZKV_OK;
+  dim3 grid(n_chunks, kv, bs);
+  auto s = reinterpret_cast<hipStream_t>(stream);
+  if (g == 8)
+    chunk_encode_kernel<8><<<grid, 128, 0, s>>>(keys, k_sb, k_sh, k_st, kv, chunk_start, n_chunks_max,
+                                                chunk_min, chunk_max, chunk_centroid, chunk_valid, packed_K);
+  else if (g == 16)
+    chunk_encode_kernel<16><<<grid, 128, 0, s>>>(keys, k_sb, k_sh, k_st, kv, chunk_start, n_chunks_max,
+                                                 chunk_min, chunk_max, chunk_centroid, chunk_valid, packed_K);
+  else
+    chunk_encode_kernel<32><<<grid, 128, 0, s>>>(keys, k_sb, k_sh, k_st, kv, chunk_start, n_chunks_max,
+                                                 chunk_min, chunk_max, chunk_centroid, chunk_valid, packed_K);
+  return check_launch("chunk_encode_kernel");
+}
+
+extern "C" int zkv_kivi4_pack(const uint16_t* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
+                              const uint16_t* v, int64_t v_sb, int64_t v_sh, int64_t v_st, int bs,
+                              int kv, int n_groups, int g0, int g_cap, int32_t* k_codes,
+                              uint16_t* k_meta, int32_t* v_codes, uint16_t* v_meta,
+                              zkv_stream_t stream) {
+  ZKV_REQUIRE(k && v && k_codes && k_meta && v_codes && v_meta, "zkv_kivi4_pack: null pointer");
+  ZKV_REQUIRE(bs > 0 && kv > 0 && n_groups >= 0 && g0 >= 0,
+              "zkv_kivi4_pack: bad sizes bs=%d kv=%d n_groups=%d g0=%d", bs, kv, n_groups, g0);
+  ZKV_REQUIRE(g0 + n_groups <= g_cap, "zkv_kivi4_pack: group end %d exceeds capacity %d",
+              g0 + n_groups, g_cap);
+  ZKV_REQUIRE((reinterpret_cast<uintptr_t>(v) & 15) == 0 && (v_st % 8) == 0 && (v_sh % 8) == 0 &&
+                  (v_sb % 8) == 0,
+              "zkv_kivi4_pack: v rows must be 16-byte aligned");
+  if (n_groups == 0) return ZKV_OK;
+  dim3 grid(n_groups, kv, bs);
+  kivi4_pack_kernel<<<grid, 128, 0, reinterpret_cast<hipStream_t>(stream)>>>(
+      k, k_sb, k_sh, k_st, v, v_sb, v_sh, v_st, kv, g0, g_cap, k_codes, k_meta, v_codes, v_meta);
+  return check_launch("kivi4_pack_kernel");
+}

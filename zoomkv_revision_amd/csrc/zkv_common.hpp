@@ -1,0 +1,105 @@
+// Shared helpers for the gfx950 ZoomKV decode-path kernels.
+//
+// Error convention of the C ABI: every entry point returns 0 on success and a
+// nonzero ZKV_E* code on failure; the message of the last failure on the
+// calling thread is available from zkv_last_error().
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+
+#include "../../include/zoomkv_gfx950.h"
+
+namespace zkv {
+
+// ---------------------------------------------------------------------------
+// Host-side error reporting
+// ---------------------------------------------------------------------------
+void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int check_launch(const char* what);
+
+#define ZKV_REQUIRE(cond, ...)                                   \
+  do {                                                           \
+    if (!(cond)) return ::zkv::fail(ZKV_EINVAL, __VA_ARGS__);    \
+  } while (0)
+
+// ---------------------------------------------------------------------------
+// Vector types
+// ---------------------------------------------------------------------------
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+// ---------------------------------------------------------------------------
+// Exact bf16 / fp16 arithmetic helpers (IEEE fp32 op, then RNE)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+
+// Round an fp32 value to the nearest bfloat16 (ties to even); NaN stays NaN.
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float x) {
+  uint32_t u = __float_as_uint(x);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ float bf16r(float x) { return bf16_to_f32(f32_to_bf16_bits(x)); }
+
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float x) {
+  _Float16 h = static_cast<_Float16>(x);
+  return __builtin_bit_cast(uint16_t, h);
+}
+
+__device__ __forceinline__ half2_t u32_as_half2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
+__device__ __forceinline__ uint32_t half2_as_u32(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
+
+// bf16(1e-8): torch's clamp(min=1e-8) on a bf16 tensor compares against the
+// scalar converted to bf16.
+constexpr float kBf16OneEm8 = __builtin_bit_cast(float, 0x322C0000u);  // bf16(1e-8)
+
+// One step of the KIVI bf16 ladder: integer code of x in [mn, mn + 15*scale].
+//   scale = bf16(bf16(mx - mn) / 15); safe = max(scale, bf16(1e-8))
+//   code  = rne(clamp(bf16(bf16(x - mn) / safe), 0, 15))
+__device__ __forceinline__ float kivi_safe(float scale) { return fmaxf(scale, kBf16OneEm8); }
+
+__device__ __forceinline__ uint32_t kivi_code(float x, float mn, float safe) {
+  float d = bf16r(x - mn);
+  float qv = bf16r(d / safe);
+  qv = fminf(fmaxf(qv, 0.0f), 15.0f);
+  return static_cast<uint32_t>(__builtin_rintf(qv));
+}
+
+__device__ __forceinline__ float kivi_scale(float mn, float mx) {
+  return bf16r(bf16r(mx - mn) / 15.0f);
+}
+
+// ---------------------------------------------------------------------------
+// Nibble word -> four fp16 pairs holding the exact codes.
+// Pair v (v = 0..3) holds (nibble v, nibble v + 4) as (lo, hi).
+// 0x6400 | n is 1024 + n in fp16; 0x4C00 | (n << 4) is 16 + n / 4.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void nibbles_to_half_pairs(uint32_t w, half2_t out[4]) {
+  const half2_t m1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+  const half2_t four = {(_Float16)4.0f, (_Float16)4.0f};
+  const half2_t m64 = {(_Float16)-64.0f, (_Float16)-64.0f};
+  const uint32_t w8 = w >> 8;
+  half2_t a = u32_as_half2((w & 0x000F000Fu) | 0x64006400u);
+  half2_t b = u32_as_half2((w & 0x00F000F0u) | 0x4C004C00u);
+  half2_t c = u32_as_half2((w8 & 0x000F000Fu) | 0x64006400u);
+  half2_t d = u32_as_half2((w8 & 0x00F000F0u) | 0x4C004C00u);
+  out[0] = a + m1024;
+  out[1] = __builtin_elementwise_fma(b, four, m64);
+  out[2] = c + m1024;
+  out[3] = __builtin_elementwise_fma(d, four, m64);
+}
+
+}  // namespace zkv

@@ -1,0 +1,195 @@
+"""Host side of the KIVI 4-bit cache: Format R chunk encode, Format Q pack and
+the fused 4-bit decode attention, over the gfx950 C ABI.
+
+Format R is the reference's K cache (S:646-744); ``chunk_encode`` replaces the
+aligned-chunk branch of ``_compute_and_store_chunk_minmax`` +
+``_kivi_pack_chunks`` (S:2119-2143, S:1965-2020).  Format Q is the north-star
+K+V cache with fp16 scale/zero (no reference counterpart; V is bf16 in the
+reference, S:561-571).
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+
+from ._lib import check, lib, ptr, require_gpu, stream_of
+
+HEAD_DIM = 128
+GROUP = 32  # Format Q tokens per group
+
+
+def _check_bf16(name: str, t: torch.Tensor) -> None:
+    if t.dtype != torch.bfloat16:
+        raise TypeError(f"{name} must be bfloat16; got {t.dtype}")
+
+
+def _check_last_contig(name: str, t: torch.Tensor) -> None:
+    if t.shape[-1] != HEAD_DIM or t.stride(-1) != 1:
+        raise ValueError(f"{name} must have a contiguous last dim of {HEAD_DIM}; "
+                         f"got shape {tuple(t.shape)} stride {t.stride()}")
+
+
+# ---------------------------------------------------------------------------
+# Format R
+# ---------------------------------------------------------------------------
+def chunk_encode(keys: torch.Tensor, chunk_size: int, chunk_start: int,
+                 chunk_min: torch.Tensor, chunk_max: torch.Tensor,
+                 chunk_centroid: torch.Tensor, chunk_valid: torch.Tensor,
+                 packed_K: torch.Tensor) -> int:
+    """Encode the ``keys.shape[2] // chunk_size`` full chunks of ``keys``.
+
+    keys [bs, kv, n_tok, 128] bf16 (any token / head / batch stride);
+    chunk_min/max/centroid [bs, kv, n_chunks_max, 128] bf16 contiguous;
+    chunk_valid [bs, kv, n_chunks_max] bool; packed_K [bs, kv, n_chunks_max,
+    16, chunk_size] int32 contiguous.  Writes chunks [chunk_start,
+    chunk_start + n) in place and returns n.
+    """
+    require_gpu(keys, chunk_min, chunk_max, chunk_centroid, chunk_valid, packed_K)
+    _check_bf16("keys", keys)
+    _check_last_contig("keys", keys)
+    for n, t in (("chunk_min", chunk_min), ("chunk_max", chunk_max), ("chunk_centroid", chunk_centroid)):
+        _check_bf16(n, t)
+        if not t.is_contiguous():
+            raise ValueError(f"{n} must be contiguous")
+    if chunk_valid.dtype != torch.bool or packed_K.dtype != torch.int32:
+        raise TypeError("chunk_valid must be bool and packed_K int32")
+    bs, kv, n_tok, _ = keys.shape
+    n_max = chunk_min.shape[2]
+    if tuple(packed_K.shape) != (bs, kv, n_max, 16, chunk_size) or not packed_K.is_contiguous():
+        raise ValueError(f"packed_K must be contiguous [{bs}, {kv}, {n_max}, 16, {chunk_size}]; "
+                         f"got {tuple(packed_K.shape)}")
+    n = n_tok // chunk_size
+    check(lib().zkv_chunk_encode(
+        ptr(keys), keys.stride(0), keys.stride(1), keys.stride(2), bs, kv, chunk_size, n,
+        chunk_start, n_max, ptr(chunk_min), ptr(chunk_max), ptr(chunk_centroid),
+        ptr(chunk_valid), ptr(packed_K), stream_of(keys)))
+    return n
+
+
+# ---------------------------------------------------------------------------
+# Format Q
+# ---------------------------------------------------------------------------
+@dataclass
+class Kivi4Cache:
+    """Device storage of a Format Q cache plus its bf16 residual window."""
+    k_codes: torch.Tensor   # int32   [bs, kv, G_cap, 16, 32]
+    k_meta: torch.Tensor    # float16 [bs, kv, G_cap, 16, 2, 8]
+    v_codes: torch.Tensor   # int32   [bs, kv, G_cap, 4, 128]
+    v_meta: torch.Tensor    # float16 [bs, kv, G_cap, 4, 4, 2, 8]
+    k_res: torch.Tensor     # bf16    [bs, kv, R_cap, 128]
+    v_res: torch.Tensor     # bf16    [bs, kv, R_cap, 128]
+    n_groups: int = 0
+    res_len: int = 0
+
+    @classmethod
+    def allocate(cls, bs: int, kv: int, g_cap: int, r_cap: int = 128,
+                 device: torch.device | str = "cuda") -> "Kivi4Cache":
+        z = dict(device=device)
+        return cls(
+            torch.zeros(bs, kv, g_cap, 16, GROUP, dtype=torch.int32, **z),
+            torch.zeros(bs, kv, g_cap, 16, 2, 8, dtype=torch.float16, **z),
+            torch.zeros(bs, kv, g_cap, 4, HEAD_DIM, dtype=torch.int32, **z),
+            torch.zeros(bs, kv, g_cap, 4, 4, 2, 8, dtype=torch.float16, **z),
+            torch.zeros(bs, kv, r_cap, HEAD_DIM, dtype=torch.bfloat16, **z),
+            torch.zeros(bs, kv, r_cap, HEAD_DIM, dtype=torch.bfloat16, **z),
+        )
+
+    @property
+    def g_cap(self) -> int:
+        return self.k_codes.shape[2]
+
+    @property
+    def r_cap(self) -> int:
+        return self.k_res.shape[2]
+
+    @property
+    def shape(self):
+        return self.k_codes.shape[0], self.k_codes.shape[1]
+
+    def nbytes_per_token(self) -> int:
+        return 160  # K codes 64 + K meta 16 + V codes 64 + V meta 16
+
+
+def kivi4_pack(k: torch.Tensor, v: torch.Tensor, cache: Kivi4Cache, g0: int) -> int:
+    """Quantize the leading full groups of k / v [bs, kv, n, 128] into groups
+    [g0, g0 + n // 32) of ``cache``; returns the number of groups written."""
+    require_gpu(k, v)
+    _check_bf16("k", k)
+    _check_bf16("v", v)
+    _check_last_contig("k", k)
+    _check_last_contig("v", v)
+    if k.shape != v.shape:
+        raise ValueError(f"k / v shape mismatch {tuple(k.shape)} vs {tuple(v.shape)}")
+    bs, kv, n, _ = k.shape
+    if (bs, kv) != tuple(cache.shape):
+        raise ValueError("cache batch / head shape mismatch")
+    ng = n // GROUP
+    check(lib().zkv_kivi4_pack(
+        ptr(k), k.stride(0), k.stride(1), k.stride(2),
+        ptr(v), v.stride(0), v.stride(1), v.stride(2),
+        bs, kv, ng, g0, cache.g_cap,
+        ptr(cache.k_codes), ptr(cache.k_meta), ptr(cache.v_codes), ptr(cache.v_meta),
+        stream_of(k)))
+    return ng
+
+
+_WORKSPACE: dict = {}
+
+
+def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    key = (device.type, device.index)
+    ws = _WORKSPACE.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _WORKSPACE[key] = ws
+    return ws
+
+
+def kivi4_decode_attention(q: torch.Tensor, cache: Kivi4Cache, n_groups: int | None = None,
+                           res_len: int | None = None, sm_scale: float | None = None,
+                           out: torch.Tensor | None = None, out_dtype: torch.dtype | None = None,
+                           n_splits: int = 0, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """Decode attention of q [bs, hq, 128] or [bs, 1, hq, 128] (bf16) over the
+    first ``n_groups`` groups and ``res_len`` residual tokens of ``cache``.
+
+    Output has q's shape and ``out_dtype`` (default q.dtype; float32 allowed).
+    """
+    require_gpu(q)
+    _check_bf16("q", q)
+    squeeze = False
+    if q.dim() == 4:
+        if q.shape[1] != 1:
+            raise ValueError("decode attention takes one query token per sequence")
+        q3 = q[:, 0]
+        squeeze = True
+    else:
+        q3 = q
+    _check_last_contig("q", q3)
+    bs, hq, _ = q3.shape
+    kbs, kv = cache.shape
+    if kbs != bs or hq % kv != 0:
+        raise ValueError(f"q {tuple(q.shape)} does not match cache (bs={kbs}, kv={kv})")
+    n_groups = cache.n_groups if n_groups is None else int(n_groups)
+    res_len = cache.res_len if res_len is None else int(res_len)
+    sm_scale = 1.0 / math.sqrt(HEAD_DIM) if sm_scale is None else float(sm_scale)
+    out_dtype = q.dtype if out_dtype is None else out_dtype
+    if out_dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"out_dtype must be bfloat16 or float32; got {out_dtype}")
+    if out is None:
+        out = torch.empty(bs, hq, HEAD_DIM, dtype=out_dtype, device=q.device)
+    elif out.dtype != out_dtype or not out.is_contiguous() or out.numel() != bs * hq * HEAD_DIM:
+        raise ValueError("out must be a contiguous [bs, hq, 128] tensor of out_dtype")
+    L = lib()
+    need = L.zkv_kivi4_attention_workspace_size(bs, hq, kv, n_groups, res_len, n_splits)
+    ws = _workspace(q.device, need) if workspace is None else workspace
+    check(L.zkv_kivi4_decode_attention(
+        ptr(q3), q3.stride(0), q3.stride(1),
+        ptr(cache.k_codes), ptr(cache.k_meta), ptr(cache.v_codes), ptr(cache.v_meta), cache.g_cap,
+        ptr(cache.k_res), ptr(cache.v_res), cache.r_cap,
+        bs, hq, kv, n_groups, res_len, sm_scale,
+        ptr(out), int(out_dtype == torch.float32), n_splits,
+        ptr(ws), ws.numel() * ws.element_size(), stream_of(q)))
+    out = out.view(bs, hq, HEAD_DIM)
+    return out.unsqueeze(1) if squeeze else out
