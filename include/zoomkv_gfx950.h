@@ -64,9 +64,14 @@ int zkv_chunk_encode(const uint16_t* keys, int64_t k_sb, int64_t k_sh, int64_t k
  * groups of 32 channels) with fp16 scale / zero.  No reference counterpart
  * (the reference keeps V in bf16, S:561-571); the code ladder is the
  * reference's (S:2003-2009) and the layouts are:
- *   k_codes int32 [bs, kv, G_cap, 16, 32]      k_meta fp16 [bs, kv, G_cap, 16, 2, 8]
- *   v_codes int32 [bs, kv, G_cap, 4, 128]      v_meta fp16 [bs, kv, G_cap, 4, 4, 2, 8]
- * (word / slot order documented with the kernel).
+ *   k_codes int32 [bs, kv, G_cap, 512]   word m*256 + l*4 + s, l = 16g + c: the
+ *           nibbles of channels 8p..8p+7 (p = 4s + g) of token 32G + 16m + c
+ *   k_meta  fp16  [bs, kv, G_cap, 16, 2, 8]  (p, scale|zero, slot): channel
+ *           8p + (0,4,1,5,2,6,3,7)[slot]
+ *   v_codes int32 [bs, kv, G_cap, 512]   word j*256 + l*4 + i, l = 16r + c:
+ *           channel 8c + 4j + i, nibble k = token 32G + TAU[r][2(k%4) + k/4]
+ *   v_meta  fp16  [bs, kv, G_cap, 4, 4, 2, 8] (channel group, r, scale|zero, e):
+ *           token 32G + TAU[r][e], TAU[r] = (4r..4r+3, 16+4r..16+4r+3)
  *
  * zkv_kivi4_pack quantizes tokens [32*g0, 32*(g0+n_groups)) of the cache
  * from src tokens [0, 32*n_groups) of k / v.
@@ -92,6 +97,7 @@ int zkv_kivi4_pack(const uint16_t* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
  * out      [bs, hq, 128] contiguous, bf16 (out_f32 == 0) or fp32 (out_f32 != 0)
  * n_splits context splits per (b, kv head); 0 = automatic
  * workspace device scratch of zkv_kivi4_attention_workspace_size() bytes
+ *          (split partials); calls that overlap on one workspace race.
  * ------------------------------------------------------------------------ */
 size_t zkv_kivi4_attention_workspace_size(int bs, int hq, int kv, int n_groups, int res_len,
                                           int n_splits);
@@ -102,6 +108,27 @@ int zkv_kivi4_decode_attention(const uint16_t* q, int64_t q_sb, int64_t q_sh,
                                int bs, int hq, int kv, int n_groups, int res_len,
                                float sm_scale, void* out, int out_f32, int n_splits,
                                void* workspace, size_t workspace_bytes, zkv_stream_t stream);
+
+/* Stage 1 of zkv_kivi4_decode_attention: per context split, the unnormalised
+ * partial output o, the running max m (log2 units, sm_scale*log2(e) folded in)
+ * and the softmax denominator l of every (b, query head), written to
+ * `workspace` as o fp32 [bs, kv, S, hq/kv, 128]
+ * followed by (m, l) fp32 [bs, kv, S, hq/kv, 2].  *n_splits_used (host pointer, may be NULL) receives
+ * the resolved split count S. */
+int zkv_kivi4_attention_partial(const uint16_t* q, int64_t q_sb, int64_t q_sh,
+                                const int32_t* k_codes, const uint16_t* k_meta,
+                                const int32_t* v_codes, const uint16_t* v_meta, int g_cap,
+                                const uint16_t* k_res, const uint16_t* v_res, int r_cap,
+                                int bs, int hq, int kv, int n_groups, int res_len,
+                                float sm_scale, int n_splits, void* workspace,
+                                size_t workspace_bytes, int* n_splits_used, zkv_stream_t stream);
+
+/* Stage 2: merge the n_splits partials of every (b, query head) with the LSE
+ * rule of lse_merge_torch (Z/cache_hub/lse_merge/lse_merge.py:79-119):
+ * out = sum_s 2^(m_s-M) o_s / sum_s 2^(m_s-M) l_s.  out as in
+ * zkv_kivi4_decode_attention. */
+int zkv_attention_merge(const void* workspace, int bs, int hq, int kv, int n_splits,
+                        void* out, int out_f32, zkv_stream_t stream);
 
 #ifdef __cplusplus
 }

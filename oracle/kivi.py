@@ -19,18 +19,22 @@ are the bf16 ladder's ``scale`` and ``mn`` converted to fp16 (RNE).  The word
 and metadata order is chosen so that the gfx950 decode kernel's MFMA operands
 need no cross-lane movement:
 
-  k_codes  int32 [bs, kv, G, 16, 32]   word (g, p, t): channel 8p+j of token
-           32g+t in bits [4j, 4j+4)  (Format R layout with g = 32)
+  k_codes  int32 [bs, kv, G, 512]  word m*256 + l*4 + s (l = 16g + c, g, c < 4, 16)
+           holds the codes of channels 8p..8p+7 of token 32G + 16m + c, p = 4s + g,
+           channel 8p+j in bits [4j, 4j+4)  (the reference's nibble packing)
   k_meta   fp16  [bs, kv, G, 16, 2, 8] [..., p, 0, s] = scale of channel
            8p + KSLOT[s], [..., p, 1, s] = zero (min) of that channel,
            KSLOT = (0, 4, 1, 5, 2, 6, 3, 7)
-  v_codes  int32 [bs, kv, G, 4, 128]   word (g, r, d): nibble k holds the code
-           of channel d for token 32g + TAU[r][VELEM[k]]
+  v_codes  int32 [bs, kv, G, 512]  word j*256 + l*4 + i (l = 16g + c) holds, for
+           channel d = 8c + 4j + i, in nibble k the code of token
+           32G + TAU[g][VELEM[k]]
   v_meta   fp16  [bs, kv, G, 4, 4, 2, 8] [..., gd, r, 0, e] = scale of token
-           32g + TAU[r][e] for channel group gd (channels 32gd..32gd+31),
+           32G + TAU[r][e] for channel group gd (channels 32gd..32gd+31),
            [..., 1, e] = zero
   TAU[r] = (4r, 4r+1, 4r+2, 4r+3, 16+4r, 17+4r, 18+4r, 19+4r)
   VELEM[k] = 2*(k % 4) + k // 4
+Word l*4 + s of each 1 KiB half is what MFMA lane l of the decode kernel
+consumes, so a lane's operands are two contiguous 16-byte reads.
 """
 from __future__ import annotations
 
@@ -153,14 +157,44 @@ def dequant_ref(packed: np.ndarray, mn: np.ndarray, mx: np.ndarray) -> np.ndarra
 # ---------------------------------------------------------------------------
 @dataclass
 class Kivi4Cache:
-    k_codes: np.ndarray   # int32  [bs, kv, G, 16, 32]
+    k_codes: np.ndarray   # int32  [bs, kv, G, 512] (lane order)
     k_meta: np.ndarray    # uint16 (fp16 bits) [bs, kv, G, 16, 2, 8]
-    v_codes: np.ndarray   # int32  [bs, kv, G, 4, 128]
+    v_codes: np.ndarray   # int32  [bs, kv, G, 512] (lane order)
     v_meta: np.ndarray    # uint16 (fp16 bits) [bs, kv, G, 4, 4, 2, 8]
 
     @property
     def n_groups(self) -> int:
         return self.k_codes.shape[2]
+
+
+def k_words_to_lane_order(words: np.ndarray) -> np.ndarray:
+    """[.., G, 16 (p), 32 (t)] chunk-major words -> [.., G, 512] lane order."""
+    sh = words.shape[:-2]
+    w = words.reshape(sh + (4, 4, 2, 16))                  # p = 4s + g, t = 16m + c
+    w = np.moveaxis(w, (-4, -3, -2, -1), (-1, -3, -4, -2))  # -> [m, g, c, s]
+    return np.ascontiguousarray(w).reshape(sh + (512,))
+
+
+def k_words_from_lane_order(words: np.ndarray) -> np.ndarray:
+    sh = words.shape[:-1]
+    w = words.reshape(sh + (2, 4, 16, 4))                   # [m, g, c, s]
+    w = np.moveaxis(w, (-4, -3, -2, -1), (-2, -3, -1, -4))  # -> [s, g, m, c]
+    return np.ascontiguousarray(w).reshape(sh + (16, 32))
+
+
+def v_words_to_lane_order(words: np.ndarray) -> np.ndarray:
+    """[.., G, 4 (r), 128 (d)] -> [.., G, 512] lane order (d = 8c + 4j + i)."""
+    sh = words.shape[:-2]
+    w = words.reshape(sh + (4, 16, 2, 4))                   # [r, c, j, i]
+    w = np.moveaxis(w, (-4, -3, -2, -1), (-3, -2, -4, -1))  # -> [j, r, c, i]
+    return np.ascontiguousarray(w).reshape(sh + (512,))
+
+
+def v_words_from_lane_order(words: np.ndarray) -> np.ndarray:
+    sh = words.shape[:-1]
+    w = words.reshape(sh + (2, 4, 16, 4))                   # [j, r, c, i]
+    w = np.moveaxis(w, (-4, -3, -2, -1), (-2, -4, -3, -1))  # -> [r, c, j, i]
+    return np.ascontiguousarray(w).reshape(sh + (4, 128))
 
 
 def quantize_kivi4(k: np.ndarray, v: np.ndarray) -> Kivi4Cache:
@@ -176,7 +210,7 @@ def quantize_kivi4(k: np.ndarray, v: np.ndarray) -> Kivi4Cache:
     kmn = kg.min(axis=3)
     kmx = kg.max(axis=3)
     kc = kivi_codes(kg, kmn[:, :, :, None, :], kmx[:, :, :, None, :])   # [.., ng, 32, 128]
-    k_codes = np.ascontiguousarray(np.swapaxes(pack_last_dim(kc), -1, -2))
+    k_codes = k_words_to_lane_order(np.swapaxes(pack_last_dim(kc), -1, -2))
     ksc = kivi_scale(kmn, kmx)                                          # [.., ng, 128]
     chan = (np.arange(16)[:, None] * 8 + KSLOT[None, :])                # [16, 8]
     k_meta = np.empty((bs, kv, ng, 16, 2, 8), dtype=np.uint16)
@@ -194,7 +228,7 @@ def quantize_kivi4(k: np.ndarray, v: np.ndarray) -> Kivi4Cache:
     for kk in range(8):
         nib = vc[:, :, :, tok[:, kk], :].astype(np.uint64)              # [.., ng, 4, 128]
         v_codes |= nib << np.uint64(4 * kk)
-    v_codes = v_codes.astype(np.uint32).view(np.int32)
+    v_codes = v_words_to_lane_order(v_codes.astype(np.uint32).view(np.int32))
     v_meta = np.empty((bs, kv, ng, 4, 4, 2, 8), dtype=np.uint16)
     # v_meta[..., gd, r, 0, e] = scale of token TAU[r][e], channel group gd
     sc_t = vsc[:, :, :, TAU, :]                                         # [.., ng, 4 r, 8 e, 4 gd]
@@ -230,7 +264,7 @@ def dequant_kivi4(c: Kivi4Cache, dtype=np.float64):
     """
     bs, kv, ng = c.k_codes.shape[:3]
     # K
-    kcodes = unpack_last_dim(np.swapaxes(c.k_codes, -1, -2)).astype(dtype)   # [.., ng, 32, 128]
+    kcodes = unpack_last_dim(np.swapaxes(k_words_from_lane_order(c.k_codes), -1, -2)).astype(dtype)
     kmeta = f16_to_f32(c.k_meta).astype(dtype)                               # [.., ng, 16, 2, 8]
     chan = (np.arange(16)[:, None] * 8 + KSLOT[None, :]).reshape(-1)
     ksc = np.empty((bs, kv, ng, 128), dtype=dtype)
@@ -239,7 +273,7 @@ def dequant_kivi4(c: Kivi4Cache, dtype=np.float64):
     kzr[..., chan] = kmeta[..., 1, :].reshape(bs, kv, ng, 128)
     k_hat = kcodes * ksc[:, :, :, None, :] + kzr[:, :, :, None, :]
     # V
-    vw = c.v_codes.view(np.uint32).astype(np.uint64)                          # [.., ng, 4, 128]
+    vw = v_words_from_lane_order(c.v_codes).view(np.uint32).astype(np.uint64)  # [.., ng, 4, 128]
     vcode = np.empty((bs, kv, ng, GROUP_Q, 128), dtype=dtype)
     tok = TAU[:, VELEM]
     for kk in range(8):

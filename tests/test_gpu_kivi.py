@@ -101,8 +101,8 @@ def test_decode_attention_matches_oracle(rng, bs, hq, kv, ng, res, splits):
         ref_cache = okivi.quantize_kivi4(k, v)
     else:
         ref_cache = okivi.Kivi4Cache(*(np.zeros((bs, kv, 0) + s, dtype=d) for s, d in
-                                       (((16, 32), np.int32), ((16, 2, 8), np.uint16),
-                                        ((4, 128), np.int32), ((4, 4, 2, 8), np.uint16))))
+                                       (((512,), np.int32), ((16, 2, 8), np.uint16),
+                                        ((512,), np.int32), ((4, 4, 2, 8), np.uint16))))
     ref = okivi.kivi4_decode_attention(q, ref_cache, ng, kr, vr, res, 1 / np.sqrt(128))
     got = from_torch(out32)
     assert got.shape == ref.shape
@@ -118,8 +118,38 @@ def test_decode_attention_split_invariance(rng):
     q = to_bf16(gaussian_bf16(rng, (1, 8, 128)))
     outs = [from_torch(zk.kivi4_decode_attention(q, cache, 12, 0, out_dtype=torch.float32, n_splits=s))
             for s in (1, 2, 5, 12)]
+    # P is fp16-rounded relative to each split's running max: splits differ at
+    # fp16 level (2^-11 relative per weight), a merge bug would show at ~1e-1
     for o in outs[1:]:
-        assert np.abs(o - outs[0]).max() <= 1e-5
+        assert np.abs(o - outs[0]).max() <= 1e-3
+
+
+def test_partial_then_merge_equals_fused(rng):
+    zk = _zk()
+    _, _, cache = _pack(rng, 2, 2, 7)
+    cache.k_res.copy_(to_bf16(gaussian_bf16(rng, (2, 2, 128, 128))))
+    cache.v_res.copy_(to_bf16(gaussian_bf16(rng, (2, 2, 128, 128))))
+    q = to_bf16(gaussian_bf16(rng, (2, 8, 128)))
+    fused = zk.kivi4_decode_attention(q, cache, 7, 33, out_dtype=torch.float32, n_splits=3)
+    ws = torch.zeros(1 << 20, dtype=torch.uint8, device="cuda")
+    _, used = zk.kivi4_attention_partial(q, cache, 7, 33, n_splits=3, workspace=ws)
+    out = torch.empty(2, 8, 128, dtype=torch.float32, device="cuda")
+    zk.attention_merge(ws, 2, 8, 2, used, out)
+    torch.cuda.synchronize()
+    assert used == 3
+    assert np.abs(from_torch(out) - from_torch(fused)).max() <= 1e-6
+
+
+def test_decode_attention_repeated_calls_reuse_workspace(rng):
+    """Repeated calls on one workspace give identical results."""
+    zk = _zk()
+    _, _, cache = _pack(rng, 1, 2, 9)
+    q = to_bf16(gaussian_bf16(rng, (1, 8, 128)))
+    ws = zk.attention_workspace(1, 8, 2, 9, 0, 4)
+    outs = [from_torch(zk.kivi4_decode_attention(q, cache, 9, 0, out_dtype=torch.float32,
+                                                 n_splits=4, workspace=ws)) for _ in range(3)]
+    torch.cuda.synchronize()
+    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[1], outs[2])
 
 
 def test_decode_attention_rejects_bad_shapes(rng):

@@ -125,7 +125,22 @@ def test_format_q_k_codes_equal_format_r_with_group_32(rng):
     v = gaussian_bf16(rng, (2, 2, 96, 128))
     q = kivi.quantize_kivi4(k, v)
     _, _, _, packed_r = kivi.encode_chunks_ref(k, 32)
-    assert np.array_equal(q.k_codes, packed_r)
+    assert np.array_equal(kivi.k_words_from_lane_order(q.k_codes), packed_r)
+
+
+def test_lane_order_relayouts_are_the_documented_bijections(rng):
+    w = rng.integers(0, 2 ** 31, size=(3, 16, 32)).astype(np.int32)
+    lo = kivi.k_words_to_lane_order(w)
+    assert np.array_equal(kivi.k_words_from_lane_order(lo), w)
+    v = rng.integers(0, 2 ** 31, size=(3, 4, 128)).astype(np.int32)
+    lv = kivi.v_words_to_lane_order(v)
+    assert np.array_equal(kivi.v_words_from_lane_order(lv), v)
+    for m in range(2):
+        for g in range(4):
+            for c in range(16):
+                for s in range(4):
+                    assert lo[1, m * 256 + (16 * g + c) * 4 + s] == w[1, 4 * s + g, 16 * m + c]
+                    assert lv[2, m * 256 + (16 * g + c) * 4 + s] == v[2, g, 8 * c + 4 * m + s]
 
 
 def test_format_q_metadata_and_codes_consistent(rng):

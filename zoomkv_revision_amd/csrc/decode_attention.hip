@@ -6,24 +6,27 @@
 //
 // K / V come from a Format Q cache (4-bit codes, fp16 scale / zero) plus a bf16
 // residual window.  The work is HBM-bound (160 B per cached token per KV head
-// against ~2 KFLOP), so the kernel is built to stream each 32-token tile from
-// HBM exactly once for all `gqa` query heads:
+// against ~2 KFLOP), so the kernel streams every 32-token tile from HBM
+// exactly once for all `gqa` query heads of its KV head:
 //
-//  * one wave64 per (context split, kv head, batch); each wave walks its
-//    tiles with the next tile's 5 KiB already in flight (register double
-//    buffer), and the launch has enough splits to give every CU several waves;
-//  * nibbles become exact fp16 codes with two bit ops (0x6400|n = 1024+n,
+//  * a workgroup of NW wave64s owns one (context split, kv head, batch); wave
+//    w walks tiles T0 + w, T0 + w + NW, ... through its own D-stage LDS ring
+//    filled by global_load_lds_dwordx4, so D-1 tiles per wave are in flight
+//    without costing VGPRs;
+//  * nibbles become exact fp16 codes with v_and_or_b32 (0x6400|n = 1024+n,
 //    0x4C00|n<<4 = 16+n/4) and one packed op, and are dequantized with one
 //    v_pk_fma_f16 per pair: code*scale + zero;
 //  * S^T[t, c] = sum_d Khat[t, d] q[c, d] and O^T[d, c] += sum_t Vhat[d, t] P[t, c]
 //    run on the matrix cores as v_mfma_f32_16x16x32_f16 (query heads on the N
 //    axis).  The Format Q word / metadata order is the MFMA operand order, so
-//    the K-MFMA result lands in exactly the lanes the V-MFMA B operand needs:
-//    no LDS round trip and no cross-lane shuffles except the softmax max/sum;
+//    the K-MFMA result lands in exactly the lanes the V-MFMA B operand needs;
 //  * online softmax in fp32 (base 2, log2(e)*sm_scale folded into q), with the
 //    O rescale skipped when no running max moved;
-//  * splits are merged by a second small kernel with the LSE rule of
-//    lse_merge_torch (Z/cache_hub/lse_merge/lse_merge.py:79-119).
+//  * the NW waves merge through LDS; with one split per KV head the kernel
+//    writes the output, otherwise a second small kernel merges the splits
+//    (a kernel boundary is the cheap cross-XCD fence: a device-scope
+//    __threadfence is an L2 writeback + invalidate on this part), both with
+//    the LSE rule of lse_merge_torch (Z/cache_hub/lse_merge/lse_merge.py:79-119).
 //
 // MFMA 16x16x32 operand layout (lane l, c = l % 16, g = l / 16):
 //   A: row c, k-slice g (8 halves);  B: k-slice g, column c;
@@ -35,6 +38,9 @@
 //   k-slice element e of lane group g is token TAU[g][e] = 4g+e | 16+4g+e-4,
 //   which is exactly where the K-MFMA left that token's score.
 #include "zkv_common.hpp"
+
+#include <algorithm>
+#include <cstdlib>
 
 namespace zkv {
 namespace {
@@ -55,46 +61,84 @@ struct AttnParams {
   int g_cap, r_cap;
   int kv, gqa, n_groups, res_len, n_splits, tiles_per_split;
   float qscale;
-  float* ws_o;   // [bs, kv, n_splits, gqa, 128]
-  float* ws_ml;  // [bs, kv, n_splits, gqa, 2]
+  float* ws_o;     // [bs, kv, n_splits, gqa, 128]
+  float* ws_ml;    // [bs, kv, n_splits, gqa, 2]
+  void* out;       // [bs, kv*gqa, 128], written directly when n_splits == 1
+  int out_f32;
 };
 
-struct TileRaw {
-  uint32_t kw[4][2];  // K words (dim block 4s+g, token c+16m)
-  u32x4_t ks[4];      // K scale slots of dim block 4s+g
-  u32x4_t kz[4];      // K zero slots
-  u32x4_t vw[2];      // V words (octet g, channels 8c..8c+7)
-  u32x4_t vs, vz;     // V scale / zero of octet g, channel group c/4
-};
+// One pipeline stage = one 32-token tile as it sits in HBM:
+//   [0, 2048)    K code words (lane order)   [2048, 4096) V code words
+//   [4096, 4608) K scale/zero slots          [4608, 5120) V scale/zero
+constexpr int kStageBytes = 5120;
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// 64 lanes x 16 B from per-lane global addresses straight into LDS at
+// dst + 16*lane (global_load_lds_dwordx4): the prefetch ring costs no VGPRs.
+__device__ __forceinline__ void dma16(const void* src, void* dst) {
+  __builtin_amdgcn_global_load_lds(src, (lds_void_t*)(dst), 16, 0, 0);
+}
+
+// s_waitcnt vmcnt(n) (gfx9 encoding: vmcnt[3:0] bits 3:0, vmcnt[5:4] bits
+// 15:14; expcnt / lgkmcnt left at "no wait").  The compiler does not track the
+// LDS side of global_load_lds, so the ring's waits are explicit.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N & 0x30) << 10) | 0x0F70);
+}
+
+__device__ __forceinline__ void wait_tiles_in_flight(int later) {
+  // 5 DMA ops per tile; `later` tiles were issued after the one needed now
+  switch (later) {
+    case 0: wait_vmcnt<0>(); break;
+    case 1: wait_vmcnt<5>(); break;
+    case 2: wait_vmcnt<10>(); break;
+    default: wait_vmcnt<15>(); break;
+  }
+  __builtin_amdgcn_sched_barrier(0);
+}
 
 __device__ __forceinline__ u32x4_t ld16(const void* p) {
   return *reinterpret_cast<const u32x4_t*>(p);
 }
 
-__device__ __forceinline__ void load_tile(const AttnParams& p, int64_t bh, int gi, int c, int g,
-                                          TileRaw& r) {
+__device__ __forceinline__ void issue_tile(const AttnParams& p, int64_t bh, int gi, int lane,
+                                           uint8_t* stage) {
   const int64_t tile = bh * p.g_cap + gi;
-  const int32_t* kc = p.k_codes + tile * 512;
-  const uint16_t* km = p.k_meta + tile * 256;
-#pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    const int blk = 4 * s + g;
-#pragma unroll
-    for (int m = 0; m < 2; ++m) r.kw[s][m] = static_cast<uint32_t>(kc[blk * 32 + c + 16 * m]);
-    r.ks[s] = ld16(km + blk * 16);
-    r.kz[s] = ld16(km + blk * 16 + 8);
-  }
-  const int32_t* vc = p.v_codes + tile * 512 + g * 128 + 8 * c;
-  r.vw[0] = ld16(vc);
-  r.vw[1] = ld16(vc + 4);
-  const uint16_t* vm = p.v_meta + tile * 256 + ((c >> 2) * 4 + g) * 16;
-  r.vs = ld16(vm);
-  r.vz = ld16(vm + 8);
+  const uint8_t* kc = reinterpret_cast<const uint8_t*>(p.k_codes + tile * 512);
+  const uint8_t* vc = reinterpret_cast<const uint8_t*>(p.v_codes + tile * 512);
+  const uint8_t* km = reinterpret_cast<const uint8_t*>(p.k_meta + tile * 256);
+  const uint8_t* vm = reinterpret_cast<const uint8_t*>(p.v_meta + tile * 256);
+  dma16(kc + 16 * lane, stage);
+  dma16(kc + 1024 + 16 * lane, stage + 1024);
+  dma16(vc + 16 * lane, stage + 2048);
+  dma16(vc + 1024 + 16 * lane, stage + 3072);
+  dma16(lane < 32 ? km + 16 * lane : vm + 16 * (lane - 32), stage + 4096);
 }
 
-__device__ __forceinline__ half8_t dequant8(uint32_t w, const u32x4_t& sc, const u32x4_t& zr) {
+// (a & m) | c in one VOP3 (gfx9 VOP3 takes no literal, so m and c live in VGPRs)
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t c) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(m), "v"(c));
+  return r;
+}
+
+struct NibbleConsts {
+  uint32_t m_lo, m_hi, x_lo, x_hi;
+};
+
+__device__ __forceinline__ half8_t dequant8(uint32_t w, const u32x4_t& sc, const u32x4_t& zr,
+                                            const NibbleConsts& k) {
+  const half2_t m1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+  const half2_t four = {(_Float16)4.0f, (_Float16)4.0f};
+  const half2_t m64 = {(_Float16)-64.0f, (_Float16)-64.0f};
+  const uint32_t w8 = w >> 8;
   half2_t code[4];
-  nibbles_to_half_pairs(w, code);
+  code[0] = u32_as_half2(and_or(w, k.m_lo, k.x_lo)) + m1024;                                  // n0, n4
+  code[1] = __builtin_elementwise_fma(u32_as_half2(and_or(w, k.m_hi, k.x_hi)), four, m64);    // n1, n5
+  code[2] = u32_as_half2(and_or(w8, k.m_lo, k.x_lo)) + m1024;                                 // n2, n6
+  code[3] = __builtin_elementwise_fma(u32_as_half2(and_or(w8, k.m_hi, k.x_hi)), four, m64);   // n3, n7
   half8_t a;
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
@@ -117,6 +161,8 @@ __device__ __forceinline__ float wave_sum16(float x) {
 // Online-softmax update for one tile: S holds the base-2 scores of tokens
 // TAU[g][0..7] for query head c (masked tokens are -inf).  Returns P as the
 // fp16 B operand of the V-MFMA and rescales O when a running max moved.
+// v_exp_f32 flushes results below 2^-126 to zero, which only drops
+// probabilities that are already far below fp16 resolution.
 __device__ __forceinline__ half8_t softmax_step(const float4_t S[2], float& m_run, float& l_run,
                                                 float4_t O[8]) {
   float sv[8];
@@ -125,18 +171,17 @@ __device__ __forceinline__ half8_t softmax_step(const float4_t S[2], float& m_ru
     sv[i] = S[0][i];
     sv[4 + i] = S[1][i];
   }
-  float mx = sv[0];
-#pragma unroll
-  for (int e = 1; e < 8; ++e) mx = fmaxf(mx, sv[e]);
+  float mx = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
+                   fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
   mx = wave_max16(mx);
   const float m_new = fmaxf(m_run, mx);
-  const float alpha = exp2f(m_run - m_new);
+  const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
   m_run = m_new;
   half8_t pb;
   float ps = 0.0f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const float pe = exp2f(sv[e] - m_new);
+    const float pe = __builtin_amdgcn_exp2f(sv[e] - m_new);
     ps += pe;
     pb[e] = static_cast<_Float16>(pe);
   }
@@ -148,128 +193,166 @@ __device__ __forceinline__ half8_t softmax_step(const float4_t S[2], float& m_ru
   return pb;
 }
 
-__global__ __launch_bounds__(64) void kivi4_attn_kernel(const AttnParams p) {
+// Tile compute from an LDS stage: K-MFMA, softmax, V-MFMA.
+__device__ __forceinline__ void compute_tile(const uint8_t* st, int lane, int c, int g,
+                                             const half8_t qB[4], const NibbleConsts& nk,
+                                             float& m_run, float& l_run, float4_t O[8]) {
+  const u32x4_t kq0 = ld16(st + 16 * lane);
+  const u32x4_t kq1 = ld16(st + 1024 + 16 * lane);
+  float4_t S[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const uint8_t* km = st + 4096 + (4 * s + g) * 32;
+    const u32x4_t ks = ld16(km), kz = ld16(km + 16);
+    S[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(dequant8(kq0[s], ks, kz, nk), qB[s], S[0], 0, 0, 0);
+    S[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(dequant8(kq1[s], ks, kz, nk), qB[s], S[1], 0, 0, 0);
+  }
+  const half8_t pb = softmax_step(S, m_run, l_run, O);
+  const u32x4_t vq0 = ld16(st + 2048 + 16 * lane);
+  const u32x4_t vq1 = ld16(st + 3072 + 16 * lane);
+  const uint8_t* vm = st + 4608 + ((c >> 2) * 4 + g) * 32;
+  const u32x4_t vs = ld16(vm), vz = ld16(vm + 16);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    O[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(dequant8(vq0[j], vs, vz, nk), pb, O[j], 0, 0, 0);
+    O[4 + j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(dequant8(vq1[j], vs, vz, nk), pb, O[4 + j], 0, 0, 0);
+  }
+}
+
+// One bf16 residual tile (tokens [base, base + valid) of the window).
+__device__ __forceinline__ void residual_tile(const AttnParams& p, int64_t bh, int base, int valid,
+                                              int c, int g, const half8_t qB[4], float& m_run,
+                                              float& l_run, float4_t O[8]) {
+  const uint16_t* kr = p.k_res + (bh * p.r_cap + base) * 128;
+  const uint16_t* vr = p.v_res + (bh * p.r_cap + base) * 128;
+  constexpr int kslot[8] = {0, 4, 1, 5, 2, 6, 3, 7};
+  float4_t S[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      const int tok = c + 16 * m;
+      u32x4_t raw = {0u, 0u, 0u, 0u};
+      if (tok < valid) raw = ld16(kr + tok * 128 + 8 * (4 * s + g));
+      half8_t a;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t wv = raw[kslot[e] >> 1];
+        a[e] = static_cast<_Float16>(__uint_as_float((kslot[e] & 1) ? (wv & 0xFFFF0000u) : (wv << 16)));
+      }
+      S[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qB[s], S[m], 0, 0, 0);
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < 2; ++m)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (4 * g + i + 16 * m >= valid) S[m][i] = -INFINITY;
+  const half8_t pb = softmax_step(S, m_run, l_run, O);
+  // V^T operand: element e = token TAU[g][e], row c of M-tile j = channel 8c + j
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    half8_t a;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int tok = (e < 4) ? (4 * g + e) : (16 + 4 * g + e - 4);
+      const float x = tok < valid ? bf16_to_f32(vr[tok * 128 + 8 * c + j]) : 0.0f;
+      a[e] = static_cast<_Float16>(x);
+    }
+    O[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb, O[j], 0, 0, 0);
+  }
+}
+
+__device__ __forceinline__ void store_out(const AttnParams& p, int64_t row, int d, float v) {
+  if (p.out_f32)
+    reinterpret_cast<float*>(p.out)[row * 128 + d] = v;
+  else
+    reinterpret_cast<uint16_t*>(p.out)[row * 128 + d] = f32_to_bf16_bits(v);
+}
+
+template <int NW, int D>
+struct KernelShape {
+  static constexpr int kLdsBytes = NW * D * kStageBytes;
+  // resident waves per SIMD when LDS (160 KiB per CU) is the limit
+  static constexpr int kWgPerCu = (160 * 1024) / kLdsBytes;
+  static constexpr int kWavesPerSimd = std::max(1, std::min(4, (kWgPerCu * NW) / 4));
+};
+
+template <int NW, int D>
+__global__ __launch_bounds__(64 * NW)
+__attribute__((amdgpu_waves_per_eu(KernelShape<NW, D>::kWavesPerSimd)))
+void kivi4_attn_kernel(const AttnParams p) {
+  __shared__ __attribute__((aligned(16))) uint8_t smem[NW][D][kStageBytes];
   const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-  const int lane = threadIdx.x;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int c = lane & 15, g = lane >> 4;
   const bool col_ok = c < p.gqa;
   const int64_t bh = static_cast<int64_t>(b) * p.kv + h;
+
+  const int n_tiles = p.n_groups + (p.res_len + kTile - 1) / kTile;
+  const int T0 = split * p.tiles_per_split;
+  const int T1 = min(T0 + p.tiles_per_split, n_tiles);
+  const int TQ = min(T1, p.n_groups);  // quantized tiles of this workgroup: [T0, TQ)
+  // this wave's quantized tiles: T0 + wave + NW*k, k < nq
+  const int nq = TQ > T0 + wave ? (TQ - (T0 + wave) + NW - 1) / NW : 0;
+  uint8_t (*ring)[kStageBytes] = smem[wave];
+
+  // Start the HBM stream before anything else.
+  int issued = 0;
+#pragma unroll
+  for (int k = 0; k < D - 1; ++k)
+    if (issued < nq) {
+      issue_tile(p, bh, T0 + wave + NW * issued, lane, ring[issued % D]);
+      ++issued;
+    }
 
   // ---- q as the K-MFMA B operand (element e of block 4s+g = channel 8(4s+g)+KSLOT[e]) ----
   half8_t qB[4];
   {
     const uint16_t* qp = p.q + b * p.q_sb + static_cast<int64_t>(h * p.gqa + (col_ok ? c : 0)) * p.q_sh;
+    constexpr int kslot[8] = {0, 4, 1, 5, 2, 6, 3, 7};
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const u32x4_t raw = ld16(qp + 8 * (4 * s + g));
-      float x[8];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        x[2 * i] = __uint_as_float(raw[i] << 16);
-        x[2 * i + 1] = __uint_as_float(raw[i] & 0xFFFF0000u);
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t wv = raw[kslot[e] >> 1];
+        const float x = __uint_as_float((kslot[e] & 1) ? (wv & 0xFFFF0000u) : (wv << 16));
+        qB[s][e] = static_cast<_Float16>(col_ok ? x * p.qscale : 0.0f);
       }
-      constexpr int kslot[8] = {0, 4, 1, 5, 2, 6, 3, 7};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) qB[s][e] = static_cast<_Float16>(col_ok ? x[kslot[e]] * p.qscale : 0.0f);
     }
   }
+  const NibbleConsts nk = {0x000F000Fu, 0x00F000F0u, 0x64006400u, 0x4C004C00u};
 
   float4_t O[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) O[j] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
   float m_run = kNegBig, l_run = 0.0f;
 
-  const int n_tiles = p.n_groups + (p.res_len + kTile - 1) / kTile;
-  const int t0 = split * p.tiles_per_split;
-  const int t1 = min(t0 + p.tiles_per_split, n_tiles);
-  const int tq1 = min(t1, p.n_groups);  // quantized tiles are [t0, tq1)
-
-  // ---- quantized tiles, next tile's raw data in flight ----
-  if (t0 < tq1) {
-    TileRaw cur;
-    load_tile(p, bh, t0, c, g, cur);
-    for (int t = t0; t < tq1; ++t) {
-      TileRaw nxt;
-      if (t + 1 < tq1) load_tile(p, bh, t + 1, c, g, nxt);
-      float4_t S[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-#pragma unroll
-        for (int m = 0; m < 2; ++m) {
-          const half8_t a = dequant8(cur.kw[s][m], cur.ks[s], cur.kz[s]);
-          S[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qB[s], S[m], 0, 0, 0);
-        }
-      }
-      const half8_t pb = softmax_step(S, m_run, l_run, O);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const half8_t a = dequant8(cur.vw[j >> 2][j & 3], cur.vs, cur.vz);
-        O[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb, O[j], 0, 0, 0);
-      }
-      if (t + 1 < tq1) cur = nxt;
+  // ---- quantized tiles through this wave's D-stage LDS ring ----
+  for (int k = 0; k < nq; ++k) {
+    if (issued < nq) {
+      issue_tile(p, bh, T0 + wave + NW * issued, lane, ring[issued % D]);
+      ++issued;
     }
+    wait_tiles_in_flight(issued - 1 - k);
+    compute_tile(ring[k % D], lane, c, g, qB, nk, m_run, l_run, O);
   }
 
-  // ---- bf16 residual tiles (at most r_cap / 32 of them, all in the last split) ----
-  for (int t = max(t0, p.n_groups); t < t1; ++t) {
+  // ---- bf16 residual tiles (at most r_cap / 32 of them, in the last split) ----
+  for (int t = max(T0, p.n_groups) + wave; t < T1; t += NW) {
     const int base = (t - p.n_groups) * kTile;
-    const int valid = min(kTile, p.res_len - base);
-    const uint16_t* kr = p.k_res + (bh * p.r_cap + base) * 128;
-    const uint16_t* vr = p.v_res + (bh * p.r_cap + base) * 128;
-    float4_t S[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-#pragma unroll
-      for (int m = 0; m < 2; ++m) {
-        const int tok = c + 16 * m;
-        u32x4_t raw = {0u, 0u, 0u, 0u};
-        if (tok < valid) raw = ld16(kr + tok * 128 + 8 * (4 * s + g));
-        float x[8];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          x[2 * i] = __uint_as_float(raw[i] << 16);
-          x[2 * i + 1] = __uint_as_float(raw[i] & 0xFFFF0000u);
-        }
-        constexpr int kslot[8] = {0, 4, 1, 5, 2, 6, 3, 7};
-        half8_t a;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) a[e] = static_cast<_Float16>(x[kslot[e]]);
-        S[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qB[s], S[m], 0, 0, 0);
-      }
-    }
-#pragma unroll
-    for (int m = 0; m < 2; ++m)
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (4 * g + i + 16 * m >= valid) S[m][i] = -INFINITY;
-    const half8_t pb = softmax_step(S, m_run, l_run, O);
-    // V^T operand: element e = token TAU[g][e], row c of M-tile j = channel 8c + j
-    float vx[8][8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int tok = (e < 4) ? (4 * g + e) : (16 + 4 * g + e - 4);
-      u32x4_t raw = {0u, 0u, 0u, 0u};
-      if (tok < valid) raw = ld16(vr + tok * 128 + 8 * c);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        vx[e][2 * i] = __uint_as_float(raw[i] << 16);
-        vx[e][2 * i + 1] = __uint_as_float(raw[i] & 0xFFFF0000u);
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      half8_t a;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) a[e] = static_cast<_Float16>(vx[e][j]);
-      O[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb, O[j], 0, 0, 0);
-    }
+    residual_tile(p, bh, base, min(kTile, p.res_len - base), c, g, qB, m_run, l_run, O);
   }
 
-  // ---- partial result of this split ----
+  // ---- merge the NW waves through LDS (the rings are free now) ----
   const float l_tot = wave_sum16(l_run);
+  __syncthreads();
+  float* red_o = reinterpret_cast<float*>(&smem[0][0][0]);  // [NW][gqa][128]
+  float* red_m = red_o + NW * p.gqa * 128;                    // [NW][gqa]
+  float* red_l = red_m + NW * p.gqa;                          // [NW][gqa]
   if (col_ok) {
-    const int64_t row = (bh * p.n_splits + split) * p.gqa + c;
-    float* o = p.ws_o + row * 128 + 32 * g;
+    float* o = red_o + (wave * p.gqa + c) * 128 + 32 * g;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       // lane holds channels 8(4g+i)+j = 32g + 8i + j for j = 0..7
@@ -277,13 +360,41 @@ __global__ __launch_bounds__(64) void kivi4_attn_kernel(const AttnParams p) {
       *reinterpret_cast<float4_t*>(o + 8 * i + 4) = float4_t{O[4][i], O[5][i], O[6][i], O[7][i]};
     }
     if (g == 0) {
-      p.ws_ml[row * 2] = m_run;
-      p.ws_ml[row * 2 + 1] = l_tot;
+      red_m[wave * p.gqa + c] = m_run;
+      red_l[wave * p.gqa + c] = l_tot;
+    }
+  }
+  __syncthreads();
+
+  const int n_out = p.gqa * 128;
+  const bool final_out = p.out != nullptr && p.n_splits == 1;
+  for (int idx = tid; idx < n_out; idx += 64 * NW) {
+    const int cc = idx >> 7, d = idx & 127;
+    float mm = kNegBig;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) mm = fmaxf(mm, red_m[w * p.gqa + cc]);
+    float ll = 0.0f, oo = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const float wt = __builtin_amdgcn_exp2f(red_m[w * p.gqa + cc] - mm);
+      ll += wt * red_l[w * p.gqa + cc];
+      oo += wt * red_o[(w * p.gqa + cc) * 128 + d];
+    }
+    if (final_out) {
+      store_out(p, bh * p.gqa + cc, d, ll > 0.0f ? oo / ll : 0.0f);  // row b*hq + h*gqa + cc
+    } else {
+      const int64_t row = (bh * p.n_splits + split) * p.gqa + cc;
+      p.ws_o[row * 128 + d] = oo;
+      if (d == 0) {
+        p.ws_ml[row * 2] = mm;
+        p.ws_ml[row * 2 + 1] = ll;
+      }
     }
   }
 }
 
-// Merge the n_splits partials of every (b, query head) with the LSE rule.
+// Merge the n_splits partials of every (b, query head) with the LSE rule
+// (standalone second stage, used when the caller runs the stages separately).
 __global__ __launch_bounds__(128) void kivi4_combine_kernel(const float* __restrict__ ws_o,
                                                             const float* __restrict__ ws_ml,
                                                             int kv, int gqa, int n_splits,
@@ -297,9 +408,10 @@ __global__ __launch_bounds__(128) void kivi4_combine_kernel(const float* __restr
   float mmax = kNegBig;
   for (int s = 0; s < n_splits; ++s) mmax = fmaxf(mmax, ws_ml[(row0 + s * gqa) * 2]);
   float num = 0.0f, den = 0.0f;
+#pragma unroll 4
   for (int s = 0; s < n_splits; ++s) {
     const int64_t row = row0 + static_cast<int64_t>(s) * gqa;
-    const float w = exp2f(ws_ml[row * 2] - mmax);
+    const float w = __builtin_amdgcn_exp2f(ws_ml[row * 2] - mmax);
     den += w * ws_ml[row * 2 + 1];
     num += w * ws_o[row * 128 + d];
   }
@@ -315,59 +427,94 @@ struct SplitPlan {
   int n_splits, tiles_per_split;
 };
 
+// Kernel shape: NW waves per workgroup, D ring stages per wave.
+// ZKV_ATTN_SHAPE=NWxD (e.g. 4x2) overrides the default for tuning sweeps.
+struct Shape {
+  int nw, d;
+};
+
+Shape attn_shape() {
+  static Shape sh = [] {
+    Shape s{8, 2};
+    if (const char* e = getenv("ZKV_ATTN_SHAPE")) {
+      int nw = 0, d = 0;
+      if (sscanf(e, "%dx%d", &nw, &d) == 2 &&
+          ((nw == 4 && (d == 2 || d == 3)) || (nw == 8 && d == 2) || (nw == 2 && (d == 3 || d == 4))))
+        s = {nw, d};
+    }
+    return s;
+  }();
+  return sh;
+}
+
 SplitPlan plan_splits(int bs, int kv, int n_groups, int res_len, int n_splits) {
-  const int n_tiles = n_groups + (res_len + kTile - 1) / kTile;
+  const int n_tiles = std::max(n_groups + (res_len + kTile - 1) / kTile, 1);
+  const Shape sh = attn_shape();
   int ns = n_splits;
   if (ns <= 0) {
-    const int target = 2048;  // ~8 single-wave workgroups per CU on 256 CUs
+    const int wg_per_cu = std::max(1, std::min((160 * 1024) / (sh.nw * sh.d * kStageBytes), 16 / sh.nw));
+    const int target = 256 * wg_per_cu;  // one resident workgroup per split on 256 CUs
     const int units = bs * kv;
     ns = (target + units - 1) / units;
+    // keep every wave busy for a few tiles at least
+    ns = std::min(ns, std::max(1, n_tiles / (2 * sh.nw)));
   }
-  ns = max(1, min(ns, max(n_tiles, 1)));
-  const int per = (max(n_tiles, 1) + ns - 1) / ns;
-  ns = (max(n_tiles, 1) + per - 1) / per;
+  ns = std::max(1, std::min(ns, n_tiles));
+  const int per = (n_tiles + ns - 1) / ns;
+  ns = (n_tiles + per - 1) / per;
   return {ns, per};
 }
 
-}  // namespace
-}  // namespace zkv
-
-using namespace zkv;
-
-extern "C" size_t zkv_kivi4_attention_workspace_size(int bs, int hq, int kv, int n_groups,
-                                                     int res_len, int n_splits) {
-  if (bs <= 0 || kv <= 0 || hq <= 0) return 0;
-  const SplitPlan sp = plan_splits(bs, kv, n_groups, res_len, n_splits);
-  return static_cast<size_t>(bs) * hq * sp.n_splits * (128 + 2) * sizeof(float);
+// Workspace layout: split partials o fp32 [bs, kv, S, gqa, 128] followed by
+// (m, l) fp32 [bs, kv, S, gqa, 2].
+size_t workspace_bytes_for(int bs, int hq, int /*kv*/, int n_splits) {
+  return static_cast<size_t>(bs) * hq * n_splits * (128 + 2) * sizeof(float);
 }
 
-extern "C" int zkv_kivi4_decode_attention(const uint16_t* q, int64_t q_sb, int64_t q_sh,
-                                          const int32_t* k_codes, const uint16_t* k_meta,
-                                          const int32_t* v_codes, const uint16_t* v_meta, int g_cap,
-                                          const uint16_t* k_res, const uint16_t* v_res, int r_cap,
-                                          int bs, int hq, int kv, int n_groups, int res_len,
-                                          float sm_scale, void* out, int out_f32, int n_splits,
-                                          void* workspace, size_t workspace_bytes,
-                                          zkv_stream_t stream) {
-  ZKV_REQUIRE(q && out && workspace, "zkv_kivi4_decode_attention: null pointer");
+void launch_attn(const AttnParams& p, int bs, hipStream_t s) {
+  const dim3 grid(p.n_splits, p.kv, bs);
+  const Shape sh = attn_shape();
+  if (sh.nw == 8) {
+    kivi4_attn_kernel<8, 2><<<grid, 512, 0, s>>>(p);
+  } else if (sh.nw == 2) {
+    if (sh.d == 4)
+      kivi4_attn_kernel<2, 4><<<grid, 128, 0, s>>>(p);
+    else
+      kivi4_attn_kernel<2, 3><<<grid, 128, 0, s>>>(p);
+  } else if (sh.d == 3) {
+    kivi4_attn_kernel<4, 3><<<grid, 256, 0, s>>>(p);
+  } else {
+    kivi4_attn_kernel<4, 2><<<grid, 256, 0, s>>>(p);
+  }
+}
+
+int attention_launch(const uint16_t* q, int64_t q_sb, int64_t q_sh, const int32_t* k_codes,
+                     const uint16_t* k_meta, const int32_t* v_codes, const uint16_t* v_meta,
+                     int g_cap, const uint16_t* k_res, const uint16_t* v_res, int r_cap, int bs,
+                     int hq, int kv, int n_groups, int res_len, float sm_scale, int n_splits,
+                     void* workspace, size_t workspace_bytes, int* n_splits_used, void* out,
+                     int out_f32, hipStream_t s) {
+  ZKV_REQUIRE(q && workspace, "zkv_kivi4_attention: null pointer");
   ZKV_REQUIRE(bs > 0 && kv > 0 && hq > 0 && hq % kv == 0,
-              "zkv_kivi4_decode_attention: bad heads bs=%d hq=%d kv=%d", bs, hq, kv);
+              "zkv_kivi4_attention: bad heads bs=%d hq=%d kv=%d", bs, hq, kv);
   const int gqa = hq / kv;
-  ZKV_REQUIRE(gqa <= 16, "zkv_kivi4_decode_attention: at most 16 query heads per KV head; got %d", gqa);
-  ZKV_REQUIRE(n_groups >= 0 && n_groups <= g_cap, "zkv_kivi4_decode_attention: n_groups=%d g_cap=%d",
+  ZKV_REQUIRE(gqa <= 16, "zkv_kivi4_attention: at most 16 query heads per KV head; got %d", gqa);
+  ZKV_REQUIRE(n_groups >= 0 && n_groups <= g_cap, "zkv_kivi4_attention: n_groups=%d g_cap=%d",
               n_groups, g_cap);
-  ZKV_REQUIRE(res_len >= 0 && res_len <= r_cap, "zkv_kivi4_decode_attention: res_len=%d r_cap=%d",
+  ZKV_REQUIRE(res_len >= 0 && res_len <= r_cap, "zkv_kivi4_attention: res_len=%d r_cap=%d",
               res_len, r_cap);
-  ZKV_REQUIRE(n_groups + res_len > 0, "zkv_kivi4_decode_attention: empty context");
+  ZKV_REQUIRE(n_groups + res_len > 0, "zkv_kivi4_attention: empty context");
   ZKV_REQUIRE(n_groups == 0 || (k_codes && k_meta && v_codes && v_meta),
-              "zkv_kivi4_decode_attention: null cache pointer");
-  ZKV_REQUIRE(res_len == 0 || (k_res && v_res), "zkv_kivi4_decode_attention: null residual pointer");
+              "zkv_kivi4_attention: null cache pointer");
+  ZKV_REQUIRE(res_len == 0 || (k_res && v_res), "zkv_kivi4_attention: null residual pointer");
   ZKV_REQUIRE((q_sh % 8) == 0 && (q_sb % 8) == 0 && (reinterpret_cast<uintptr_t>(q) & 15) == 0,
-              "zkv_kivi4_decode_attention: q rows must be 16-byte aligned");
+              "zkv_kivi4_attention: q rows must be 16-byte aligned");
+  ZKV_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 15) == 0,
+              "zkv_kivi4_attention: workspace must be 16-byte aligned");
   const SplitPlan sp = plan_splits(bs, kv, n_groups, res_len, n_splits);
-  const size_t need = static_cast<size_t>(bs) * hq * sp.n_splits * (128 + 2) * sizeof(float);
+  const size_t need = workspace_bytes_for(bs, hq, kv, sp.n_splits);
   if (workspace_bytes < need)
-    return fail(ZKV_ESPACE, "zkv_kivi4_decode_attention: workspace %zu < %zu bytes", workspace_bytes, need);
+    return fail(ZKV_ESPACE, "zkv_kivi4_attention: workspace %zu < %zu bytes", workspace_bytes, need);
   AttnParams p;
   p.q = q;
   p.q_sb = q_sb;
@@ -389,10 +536,65 @@ extern "C" int zkv_kivi4_decode_attention(const uint16_t* q, int64_t q_sb, int64
   p.qscale = sm_scale * kLog2e;
   p.ws_o = reinterpret_cast<float*>(workspace);
   p.ws_ml = p.ws_o + static_cast<size_t>(bs) * hq * sp.n_splits * 128;
-  auto s = reinterpret_cast<hipStream_t>(stream);
-  kivi4_attn_kernel<<<dim3(sp.n_splits, kv, bs), 64, 0, s>>>(p);
+  p.out = out;
+  p.out_f32 = out_f32;
+  if (n_splits_used) *n_splits_used = sp.n_splits;
+  launch_attn(p, bs, s);
   int rc = check_launch("kivi4_attn_kernel");
-  if (rc) return rc;
+  if (rc || out == nullptr || sp.n_splits == 1) return rc;
   kivi4_combine_kernel<<<bs * hq, 128, 0, s>>>(p.ws_o, p.ws_ml, kv, gqa, sp.n_splits, out, out_f32);
   return check_launch("kivi4_combine_kernel");
+}
+
+}  // namespace
+}  // namespace zkv
+
+using namespace zkv;
+
+extern "C" size_t zkv_kivi4_attention_workspace_size(int bs, int hq, int kv, int n_groups,
+                                                     int res_len, int n_splits) {
+  if (bs <= 0 || kv <= 0 || hq <= 0) return 0;
+  const SplitPlan sp = plan_splits(bs, kv, n_groups, res_len, n_splits);
+  return workspace_bytes_for(bs, hq, kv, sp.n_splits);
+}
+
+extern "C" int zkv_kivi4_attention_partial(const uint16_t* q, int64_t q_sb, int64_t q_sh,
+                                           const int32_t* k_codes, const uint16_t* k_meta,
+                                           const int32_t* v_codes, const uint16_t* v_meta, int g_cap,
+                                           const uint16_t* k_res, const uint16_t* v_res, int r_cap,
+                                           int bs, int hq, int kv, int n_groups, int res_len,
+                                           float sm_scale, int n_splits, void* workspace,
+                                           size_t workspace_bytes, int* n_splits_used,
+                                           zkv_stream_t stream) {
+  return attention_launch(q, q_sb, q_sh, k_codes, k_meta, v_codes, v_meta, g_cap, k_res, v_res,
+                          r_cap, bs, hq, kv, n_groups, res_len, sm_scale, n_splits, workspace,
+                          workspace_bytes, n_splits_used, nullptr, 0,
+                          reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int zkv_attention_merge(const void* workspace, int bs, int hq, int kv, int n_splits,
+                                   void* out, int out_f32, zkv_stream_t stream) {
+  ZKV_REQUIRE(workspace && out, "zkv_attention_merge: null pointer");
+  ZKV_REQUIRE(bs > 0 && kv > 0 && hq > 0 && hq % kv == 0 && n_splits > 0,
+              "zkv_attention_merge: bad sizes bs=%d hq=%d kv=%d n_splits=%d", bs, hq, kv, n_splits);
+  const float* ws_o = reinterpret_cast<const float*>(workspace);
+  const float* ws_ml = ws_o + static_cast<size_t>(bs) * hq * n_splits * 128;
+  kivi4_combine_kernel<<<bs * hq, 128, 0, reinterpret_cast<hipStream_t>(stream)>>>(
+      ws_o, ws_ml, kv, hq / kv, n_splits, out, out_f32);
+  return check_launch("kivi4_combine_kernel");
+}
+
+extern "C" int zkv_kivi4_decode_attention(const uint16_t* q, int64_t q_sb, int64_t q_sh,
+                                          const int32_t* k_codes, const uint16_t* k_meta,
+                                          const int32_t* v_codes, const uint16_t* v_meta, int g_cap,
+                                          const uint16_t* k_res, const uint16_t* v_res, int r_cap,
+                                          int bs, int hq, int kv, int n_groups, int res_len,
+                                          float sm_scale, void* out, int out_f32, int n_splits,
+                                          void* workspace, size_t workspace_bytes,
+                                          zkv_stream_t stream) {
+  ZKV_REQUIRE(out, "zkv_kivi4_decode_attention: null output");
+  return attention_launch(q, q_sb, q_sh, k_codes, k_meta, v_codes, v_meta, g_cap, k_res, v_res,
+                          r_cap, bs, hq, kv, n_groups, res_len, sm_scale, n_splits, workspace,
+                          workspace_bytes, nullptr, out, out_f32,
+                          reinterpret_cast<hipStream_t>(stream));
 }

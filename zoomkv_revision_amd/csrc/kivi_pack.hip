@@ -143,22 +143,26 @@ __global__ __launch_bounds__(128) void kivi4_pack_kernel(
     vm[8 + e] = f32_to_f16_bits(mn);
   }
   __syncthreads();
-  // ---- K words: index p*32 + t ----
+  // ---- K words in MFMA lane order: w = m*256 + l*4 + s, l = 16g + c,
+  //      word of dim block p = 4s + g for token t = 16m + c ----
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int w = tid + 128 * i;
-    const int p = w >> 5, t = w & 31;
+    const int m = w >> 8, l = (w >> 2) & 63, s = w & 3;
+    const int p = 4 * s + (l >> 4), t = 16 * m + (l & 15);
     const uint64_t cb = *reinterpret_cast<const uint64_t*>(&kc[t][8 * p]);
     uint32_t word = 0;
 #pragma unroll
     for (int j = 0; j < 8; ++j) word |= static_cast<uint32_t>((cb >> (8 * j)) & 0xF) << (4 * j);
     k_codes[bhg * 512 + w] = static_cast<int32_t>(word);
   }
-  // ---- V words: index r*128 + d ----
+  // ---- V words in MFMA lane order: w = j*256 + l*4 + i, l = 16r + c,
+  //      word of octet r for channel d = 8c + 4j + i ----
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int w = tid + 128 * i;
-    const int r = w >> 7, d = w & 127;
+    const int j = w >> 8, l = (w >> 2) & 63, ii = w & 3;
+    const int r = l >> 4, d = 8 * (l & 15) + 4 * j + ii;
     uint32_t word = 0;
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk) word |= static_cast<uint32_t>(vc[kVTok[r][kk]][d]) << (4 * kk);

@@ -74,9 +74,9 @@ def chunk_encode(keys: torch.Tensor, chunk_size: int, chunk_start: int,
 @dataclass
 class Kivi4Cache:
     """Device storage of a Format Q cache plus its bf16 residual window."""
-    k_codes: torch.Tensor   # int32   [bs, kv, G_cap, 16, 32]
+    k_codes: torch.Tensor   # int32   [bs, kv, G_cap, 512] (MFMA lane order)
     k_meta: torch.Tensor    # float16 [bs, kv, G_cap, 16, 2, 8]
-    v_codes: torch.Tensor   # int32   [bs, kv, G_cap, 4, 128]
+    v_codes: torch.Tensor   # int32   [bs, kv, G_cap, 512] (MFMA lane order)
     v_meta: torch.Tensor    # float16 [bs, kv, G_cap, 4, 4, 2, 8]
     k_res: torch.Tensor     # bf16    [bs, kv, R_cap, 128]
     v_res: torch.Tensor     # bf16    [bs, kv, R_cap, 128]
@@ -88,9 +88,9 @@ class Kivi4Cache:
                  device: torch.device | str = "cuda") -> "Kivi4Cache":
         z = dict(device=device)
         return cls(
-            torch.zeros(bs, kv, g_cap, 16, GROUP, dtype=torch.int32, **z),
+            torch.zeros(bs, kv, g_cap, 512, dtype=torch.int32, **z),
             torch.zeros(bs, kv, g_cap, 16, 2, 8, dtype=torch.float16, **z),
-            torch.zeros(bs, kv, g_cap, 4, HEAD_DIM, dtype=torch.int32, **z),
+            torch.zeros(bs, kv, g_cap, 512, dtype=torch.int32, **z),
             torch.zeros(bs, kv, g_cap, 4, 4, 2, 8, dtype=torch.float16, **z),
             torch.zeros(bs, kv, r_cap, HEAD_DIM, dtype=torch.bfloat16, **z),
             torch.zeros(bs, kv, r_cap, HEAD_DIM, dtype=torch.bfloat16, **z),
@@ -139,12 +139,20 @@ _WORKSPACE: dict = {}
 
 
 def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """Per-device attention workspace (split partials), grown on demand."""
     key = (device.type, device.index)
     ws = _WORKSPACE.get(key)
     if ws is None or ws.numel() < nbytes:
-        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
         _WORKSPACE[key] = ws
     return ws
+
+
+def attention_workspace(bs: int, hq: int, kv: int, n_groups: int, res_len: int,
+                        n_splits: int = 0, device="cuda") -> torch.Tensor:
+    """A dedicated workspace for ``kivi4_decode_attention``."""
+    n = lib().zkv_kivi4_attention_workspace_size(bs, hq, kv, n_groups, res_len, n_splits)
+    return torch.zeros(n, dtype=torch.uint8, device=device)
 
 
 def kivi4_decode_attention(q: torch.Tensor, cache: Kivi4Cache, n_groups: int | None = None,
@@ -193,3 +201,34 @@ def kivi4_decode_attention(q: torch.Tensor, cache: Kivi4Cache, n_groups: int | N
         ptr(ws), ws.numel() * ws.element_size(), stream_of(q)))
     out = out.view(bs, hq, HEAD_DIM)
     return out.unsqueeze(1) if squeeze else out
+
+
+def kivi4_attention_partial(q: torch.Tensor, cache: Kivi4Cache, n_groups: int, res_len: int,
+                            sm_scale: float | None = None, n_splits: int = 0,
+                            workspace: torch.Tensor | None = None):
+    """Stage 1 only (per-split partial o / m / l); returns (workspace, n_splits).
+    ``attention_merge`` finishes the op.  Used for split-level timing and as the
+    building block of a context-sharded decode."""
+    import ctypes
+    bs, hq, _ = q.shape
+    kv = cache.shape[1]
+    sm_scale = 1.0 / math.sqrt(HEAD_DIM) if sm_scale is None else float(sm_scale)
+    L = lib()
+    need = L.zkv_kivi4_attention_workspace_size(bs, hq, kv, n_groups, res_len, n_splits)
+    ws = _workspace(q.device, need) if workspace is None else workspace
+    used = ctypes.c_int(0)
+    check(L.zkv_kivi4_attention_partial(
+        ptr(q), q.stride(0), q.stride(1),
+        ptr(cache.k_codes), ptr(cache.k_meta), ptr(cache.v_codes), ptr(cache.v_meta), cache.g_cap,
+        ptr(cache.k_res), ptr(cache.v_res), cache.r_cap,
+        bs, hq, kv, n_groups, res_len, sm_scale, n_splits,
+        ptr(ws), ws.numel() * ws.element_size(), ctypes.addressof(used), stream_of(q)))
+    return ws, used.value
+
+
+def attention_merge(workspace: torch.Tensor, bs: int, hq: int, kv: int, n_splits: int,
+                    out: torch.Tensor) -> torch.Tensor:
+    """Stage 2: LSE merge of the split partials into ``out`` ([bs, hq, 128] bf16 or fp32)."""
+    check(lib().zkv_attention_merge(ptr(workspace), bs, hq, kv, n_splits, ptr(out),
+                                    int(out.dtype == torch.float32), stream_of(out)))
+    return out
