@@ -106,6 +106,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--splits", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run 5 device copies of 1 GiB (scale reference for rocprof "
+                         "FETCH_SIZE / WRITE_SIZE counters) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build runs on a "
@@ -116,6 +119,14 @@ def main():
     from zoomkv_revision_amd import kivi
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.calibrate_copy:
+        src = torch.ones(1 << 28, dtype=torch.float32, device=dev)      # 1 GiB
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_read": src.numel() * 4, "copy_bytes_written": dst.numel() * 4}))
+        return
     caches = [make_cache(1234 + i, dev) for i in range(2)]
     gq = torch.Generator(device=dev)
     gq.manual_seed(42)

@@ -1,0 +1,447 @@
+// Page scoring and selection kernels (gfx950): Quest chunk upper bounds, exact
+// top-k (with the fused LUT gather + skipped-tail concat), CDS density scores,
+// the dense mask, the GQA-mean query and the KIVI stage-2 scorer.
+//
+// Bit-exactness: every fp32 reduction follows the reference kernel's order
+// (cited per kernel), and bf16 rounding is RNE after every op as the
+// reference's bf16 intrinsics do.
+#include "zkv_common.hpp"
+
+namespace zkv {
+namespace {
+
+// ----------------------------------------------------------------------------
+// Quest chunk score (Z/cache_hub/quest/quest_chunk_score.cu:31-103)
+//   score = sum_d max(q_d * mn_d, q_d * mx_d); lane t of a 32-lane group sums
+//   dims 4t..4t+3 left to right, then xor butterfly 16, 8, 4, 2, 1.
+// Each wave64 scores two chunks at a time (one per 32-lane half); the grid
+// strides over all (b, kv, chunk).  HBM-bound: 512 B of metadata per chunk.
+// ----------------------------------------------------------------------------
+template <bool kFp16Meta>
+__device__ __forceinline__ float meta_to_f32(uint16_t v) {
+  if constexpr (kFp16Meta)
+    return static_cast<float>(__builtin_bit_cast(_Float16, v));
+  else
+    return bf16_to_f32(v);
+}
+
+template <bool kFp16Meta>
+__global__ __launch_bounds__(256) void quest_score_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ cmin,
+    const uint16_t* __restrict__ cmax, const uint8_t* __restrict__ valid, float* __restrict__ scores,
+    int n_chunks, int n_max, int64_t total) {
+  const int half = threadIdx.x >> 5;  // 8 halves of 32 lanes per block
+  const int t = threadIdx.x & 31;
+  for (int64_t item = static_cast<int64_t>(blockIdx.x) * 8 + half; item < total;
+       item += static_cast<int64_t>(gridDim.x) * 8) {
+    const int64_t bh = item / n_chunks;
+    const int chunk = static_cast<int>(item - bh * n_chunks);
+    const int64_t row = bh * n_max + chunk;
+    float sum;
+    if (valid != nullptr && !valid[row]) {
+      sum = -INFINITY;
+    } else {
+      const u32x2_t qv = *reinterpret_cast<const u32x2_t*>(q + bh * 128 + 4 * t);
+      const u32x2_t mv = *reinterpret_cast<const u32x2_t*>(cmin + row * 128 + 4 * t);
+      const u32x2_t xv = *reinterpret_cast<const u32x2_t*>(cmax + row * 128 + 4 * t);
+      float qq[4], mn[4], mx[4];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        qq[2 * i] = __uint_as_float(qv[i] << 16);
+        qq[2 * i + 1] = __uint_as_float(qv[i] & 0xFFFF0000u);
+        mn[2 * i] = meta_to_f32<kFp16Meta>(static_cast<uint16_t>(mv[i] & 0xFFFF));
+        mn[2 * i + 1] = meta_to_f32<kFp16Meta>(static_cast<uint16_t>(mv[i] >> 16));
+        mx[2 * i] = meta_to_f32<kFp16Meta>(static_cast<uint16_t>(xv[i] & 0xFFFF));
+        mx[2 * i + 1] = meta_to_f32<kFp16Meta>(static_cast<uint16_t>(xv[i] >> 16));
+      }
+      sum = fmaxf(qq[0] * mn[0], qq[0] * mx[0]);
+      sum = sum + fmaxf(qq[1] * mn[1], qq[1] * mx[1]);
+      sum = sum + fmaxf(qq[2] * mn[2], qq[2] * mx[2]);
+      sum = sum + fmaxf(qq[3] * mn[3], qq[3] * mx[3]);
+#pragma unroll
+      for (int off = 16; off > 0; off >>= 1) sum = sum + __shfl_xor(sum, off);
+    }
+    if (t == 0) scores[item] = sum;
+  }
+}
+
+// ----------------------------------------------------------------------------
+// Exact top-k of a row (float_topk.cu:51-271 semantics, deterministic):
+// radix select on order-preserving uint32 keys (4 rounds of 8 bits) finds the
+// k-th largest key T exactly; then one ordered pass keeps every key > T and
+// the lowest-index keys == T, writing them in increasing index order.
+// No candidate buffer, so no overflow at any length (the reference drops
+// candidates beyond 8192 per round, float_topk.cu:95).
+// Optional: out = lut[idx] (float_topk_gather_concat.cu:109-114) and the
+// skipped tail copied to out[k, k + sk).
+// ----------------------------------------------------------------------------
+constexpr int kTopkThreads = 1024;
+constexpr int kTopkWaves = kTopkThreads / 64;
+
+__device__ __forceinline__ uint32_t ordered_key(float x) {
+  const uint32_t b = __float_as_uint(x);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+__device__ __forceinline__ int block_exclusive_count(bool flag, int* s_wave, int& total) {
+  // exclusive rank of this thread's flag over the block (thread order), and
+  // the block total; s_wave holds kTopkWaves ints
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint64_t m = __ballot(flag);
+  const int in_wave = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
+                                                __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0));
+  if (lane == 0) s_wave[wave] = __popcll(m);
+  __syncthreads();
+  int before = 0;
+  total = 0;
+#pragma unroll
+  for (int w = 0; w < kTopkWaves; ++w) {
+    const int c = s_wave[w];
+    before += (w < wave) ? c : 0;
+    total += c;
+  }
+  __syncthreads();
+  return before + in_wave;
+}
+
+__global__ __launch_bounds__(kTopkThreads) void topk_kernel(
+    const float* __restrict__ in, int64_t in_stride, int L, int k, int64_t* __restrict__ out,
+    int64_t out_stride, const int64_t* __restrict__ lut, int64_t lut_stride,
+    const int64_t* __restrict__ skipped, int64_t sk_stride, int sk_count, int64_t sentinel) {
+  __shared__ int s_hist[kTopkWaves][256];
+  __shared__ int s_wave[kTopkWaves];
+  __shared__ int s_bin, s_remain;
+  const int row = blockIdx.x;
+  const int tid = threadIdx.x, wave = tid >> 6;
+  const float* x = in + row * in_stride;
+  int64_t* o = out + row * out_stride;
+  const int64_t* lrow = lut ? lut + row * lut_stride : nullptr;
+
+  for (int i = tid; i < sk_count; i += kTopkThreads) o[k + i] = skipped[row * sk_stride + i];
+  if (L <= k) {
+    for (int i = tid; i < k; i += kTopkThreads) o[i] = (i < L) ? (lrow ? lrow[i] : i) : sentinel;
+    return;
+  }
+
+  uint32_t prefix = 0, mask = 0;
+  int remain = k;  // how many of the candidates matching (prefix, mask) to keep
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    for (int i = tid; i < kTopkWaves * 256; i += kTopkThreads) (&s_hist[0][0])[i] = 0;
+    __syncthreads();
+    for (int i = tid; i < L; i += kTopkThreads) {
+      const uint32_t key = ordered_key(x[i]);
+      if ((key & mask) == prefix) atomicAdd(&s_hist[wave][(key >> shift) & 0xFF], 1);
+    }
+    __syncthreads();
+    if (tid < 256) {
+      int c = 0;
+#pragma unroll
+      for (int w = 0; w < kTopkWaves; ++w) c += s_hist[w][tid];
+      s_hist[0][tid] = c;
+    }
+    __syncthreads();
+    if (tid < 64) {
+      // suffix counts over the 256 bins, 4 bins per lane, highest bins first
+      int c[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) c[j] = s_hist[0][4 * tid + j];
+      int lane_sum = c[0] + c[1] + c[2] + c[3];
+      // inclusive suffix scan across lanes (lane 63 holds the top bins)
+      int suf = lane_sum;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const int v = __shfl_down(suf, off);
+        if (tid + off < 64) suf += v;
+      }
+      // bins above this lane's range: suf - lane_sum
+      int above = suf - lane_sum;
+#pragma unroll
+      for (int j = 3; j >= 0; --j) {
+        const int at_or_above = above + c[j];
+        if (at_or_above >= remain && above < remain) {
+          s_bin = 4 * tid + j;
+          s_remain = remain - above;
+        }
+        above = at_or_above;
+      }
+    }
+    __syncthreads();
+    prefix |= static_cast<uint32_t>(s_bin) << shift;
+    mask |= 0xFFu << shift;
+    remain = s_remain;
+    __syncthreads();
+  }
+  // prefix == T, remain = number of keys == T to keep (lowest indices first)
+  const uint32_t T = prefix;
+  int taken_eq = 0, written = 0;
+  for (int base = 0; base < L; base += kTopkThreads) {
+    const int i = base + tid;
+    const uint32_t key = i < L ? ordered_key(x[i]) : 0u;
+    const bool gt = i < L && key > T;
+    const bool eq = i < L && key == T;
+    int eq_total = 0;
+    const int eq_rank = block_exclusive_count(eq, s_wave, eq_total);
+    const bool sel = gt || (eq && taken_eq + eq_rank < remain);
+    int sel_total = 0;
+    const int pos = written + block_exclusive_count(sel, s_wave, sel_total);
+    if (sel) o[pos] = lrow ? lrow[i] : i;
+    taken_eq += eq_total;
+    written += sel_total;
+    if (written >= k) break;  // uniform across the block
+  }
+}
+
+// ----------------------------------------------------------------------------
+// CDS density: centroid[chunk_id] . q (rerank_topk.cu:560-624): buf[t] = c[t]q[t]
+// for t < 128, then buf[t] += buf[t+s], s = 64..1; invalid id -> -1e30.
+// One wave per (b, kv, slot): lane l starts with p[l] + p[l+64].
+// ----------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void density_kernel(
+    const int64_t* __restrict__ ids, int64_t id_sb, int64_t id_sh, const uint16_t* __restrict__ cent,
+    int64_t c_sb, int64_t c_sh, int64_t c_sc, const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_sh,
+    float* __restrict__ out, int64_t o_sb, int64_t o_sh, int kv, int nk, int n_chunks, int64_t total) {
+  const int lane = threadIdx.x & 63;
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (item >= total) return;
+  const int slot = static_cast<int>(item % nk);
+  const int64_t bh = item / nk;
+  const int b = static_cast<int>(bh / kv), h = static_cast<int>(bh % kv);
+  const int64_t cid = ids[b * id_sb + h * id_sh + slot];
+  const bool ok = cid >= 0 && cid < n_chunks;
+  float v = 0.0f;
+  if (ok) {
+    const uint16_t* c = cent + b * c_sb + h * c_sh + cid * c_sc;
+    const uint16_t* qq = q + b * q_sb + h * q_sh;
+    v = bf16_to_f32(c[lane]) * bf16_to_f32(qq[lane]) + 0.0f;
+    const float w = bf16_to_f32(c[lane + 64]) * bf16_to_f32(qq[lane + 64]);
+    v = v + w;
+  }
+#pragma unroll
+  for (int s = 32; s >= 1; s >>= 1) {
+    const float o = __shfl_down(v, s);
+    if (lane < s) v = v + o;
+  }
+  if (lane == 0) out[b * o_sb + h * o_sh + slot] = ok ? v : -1e30f;
+}
+
+// mask.fill_(False); mask.scatter_(2, positions, True) (rerank_topk.cu:926-954)
+__global__ __launch_bounds__(256) void dense_mask_kernel(const int64_t* __restrict__ pos,
+                                                         uint8_t* __restrict__ mask, int n_dense,
+                                                         int nk) {
+  const int row = blockIdx.x;
+  uint8_t* m = mask + static_cast<int64_t>(row) * nk;
+  for (int i = threadIdx.x; i < nk; i += blockDim.x) m[i] = 0;
+  __syncthreads();
+  for (int j = threadIdx.x; j < n_dense; j += blockDim.x) {
+    const int64_t p = pos[static_cast<int64_t>(row) * n_dense + j];
+    if (p >= 0 && p < nk) m[p] = 1;
+  }
+}
+
+// raw_q = bf16(sum_i q[group*h + i] / group), sum in head order (S:1621-1626)
+__global__ __launch_bounds__(128) void gqa_mean_kernel(const uint16_t* __restrict__ q, int64_t q_sb,
+                                                       int64_t q_sh, int kv, int group,
+                                                       uint16_t* __restrict__ out) {
+  const int bh = blockIdx.x, d = threadIdx.x;
+  const int b = bh / kv, h = bh % kv;
+  const uint16_t* qp = q + b * q_sb + static_cast<int64_t>(h * group) * q_sh + d;
+  float acc = bf16_to_f32(qp[0]);
+  for (int i = 1; i < group; ++i) acc = acc + bf16_to_f32(qp[i * q_sh]);
+  out[static_cast<int64_t>(bh) * 128 + d] = f32_to_bf16_bits(acc / static_cast<float>(group));
+}
+
+// ----------------------------------------------------------------------------
+// KIVI stage-2 (kivi_qk_dot.cu:108-320): per selected chunk and token,
+// k = bf16(bf16(code*scale) + mn), p = bf16(k*q), acc += p (fp32, d = 0..127),
+// scale = bf16(bf16(mx - mn)/15); then a G-lane descending bitonic sort and
+// keep dense_topk / sparse_topk per chunk, (-1e30, 0) elsewhere.
+// One lane per token; G lanes per chunk; 256 threads per block.
+// ----------------------------------------------------------------------------
+template <int G>
+__global__ __launch_bounds__(256) void kivi_qk_kernel(
+    const int64_t* __restrict__ ids, int64_t id_sb, int64_t id_sh, const uint8_t* __restrict__ dmask,
+    int64_t dm_sb, int64_t dm_sh, const int32_t* __restrict__ packed, int64_t pk_sb, int64_t pk_sh,
+    int n_packed, const uint16_t* __restrict__ cmin, const uint16_t* __restrict__ cmax, int64_t cm_sb,
+    int64_t cm_sh, int n_max, const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_sh,
+    float* __restrict__ out_s, int64_t* __restrict__ out_i, int64_t o_sb, int64_t o_sh, int nk,
+    int dense_topk, int sparse_topk) {
+  constexpr int kChunks = 256 / G;
+  __shared__ float s_q[kChunks][128];
+  __shared__ float s_mn[kChunks][128];
+  __shared__ float s_sc[kChunks][128];
+  const int b = blockIdx.z, h = blockIdx.y;
+  const int local = threadIdx.x / G, lane = threadIdx.x % G;
+  const int slot = blockIdx.x * kChunks + local;
+  const bool valid_slot = slot < nk;
+  int64_t cid = 0;
+  bool dense = false;
+  if (valid_slot) {
+    cid = ids[b * id_sb + h * id_sh + slot];
+    dense = dmask[b * dm_sb + h * dm_sh + slot] != 0;
+  }
+  const bool in_range = cid >= 0 && cid < n_packed;
+  if (valid_slot) {
+    const uint16_t* qp = q + b * q_sb + h * q_sh;
+    const int64_t mrow = (b * cm_sb + h * cm_sh) + (cid >= 0 && cid < n_max ? cid : 0) * 128;
+    for (int d = lane; d < 128; d += G) {
+      const float mn = bf16_to_f32(cmin[mrow + d]);
+      const float mx = bf16_to_f32(cmax[mrow + d]);
+      s_q[local][d] = bf16_to_f32(qp[d]);
+      s_mn[local][d] = mn;
+      s_sc[local][d] = bf16r(bf16r(mx - mn) / 15.0f);
+    }
+  }
+  __syncthreads();
+  float score = -1e30f;
+  int token = static_cast<int>(cid) * G + lane;
+  if (valid_slot && in_range) {
+    const int32_t* w = packed + b * pk_sb + h * pk_sh + cid * (16 * G) + lane;
+    float acc = 0.0f;
+#pragma unroll 2
+    for (int p = 0; p < 16; ++p) {
+      const uint32_t word = static_cast<uint32_t>(w[p * G]);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int d = 8 * p + j;
+        const float code = static_cast<float>((word >> (4 * j)) & 0xFu);
+        const float kd = bf16r(bf16r(code * s_sc[local][d]) + s_mn[local][d]);
+        acc = acc + bf16r(kd * s_q[local][d]);
+      }
+    }
+    score = acc;
+  }
+  // bitonic sort (descending) within the G lanes of this chunk (kivi_qk_dot.cu:286-303)
+#pragma unroll
+  for (int k2 = 2; k2 <= G; k2 <<= 1) {
+#pragma unroll
+    for (int j = k2 >> 1; j >= 1; j >>= 1) {
+      const float os = __shfl_xor(score, j);
+      const int ot = __shfl_xor(token, j);
+      const bool desc = (lane & k2) == 0;
+      const bool lower = (lane & j) == 0;
+      const bool swap = (desc == lower) ? (os > score) : (os < score);
+      if (swap) {
+        score = os;
+        token = ot;
+      }
+    }
+  }
+  if (valid_slot) {
+    const int64_t oi = b * o_sb + h * o_sh + static_cast<int64_t>(slot) * G + lane;
+    const int keep = dense ? dense_topk : sparse_topk;
+    out_s[oi] = lane < keep ? score : -1e30f;
+    out_i[oi] = lane < keep ? static_cast<int64_t>(token) : 0;
+  }
+}
+
+}  // namespace
+}  // namespace zkv
+
+using namespace zkv;
+
+extern "C" int zkv_quest_chunk_score(const uint16_t* q, const uint16_t* chunk_min,
+                                     const uint16_t* chunk_max, int meta_fp16, float* scores,
+                                     int bs, int kv, int n_chunks, int n_chunks_max,
+                                     const uint8_t* valid, zkv_stream_t stream) {
+  ZKV_REQUIRE(q && chunk_min && chunk_max && scores, "zkv_quest_chunk_score: null pointer");
+  ZKV_REQUIRE(bs > 0 && kv > 0 && n_chunks >= 0 && n_chunks <= n_chunks_max,
+              "zkv_quest_chunk_score: bad sizes bs=%d kv=%d n_chunks=%d n_chunks_max=%d", bs, kv,
+              n_chunks, n_chunks_max);
+  const int64_t total = static_cast<int64_t>(bs) * kv * n_chunks;
+  if (total == 0) return ZKV_OK;
+  const int64_t blocks64 = std::min<int64_t>((total + 7) / 8, 8192);
+  const int blocks = static_cast<int>(blocks64);
+  auto s = reinterpret_cast<hipStream_t>(stream);
+  if (meta_fp16)
+    quest_score_kernel<true><<<blocks, 256, 0, s>>>(q, chunk_min, chunk_max, valid, scores, n_chunks,
+                                                    n_chunks_max, total);
+  else
+    quest_score_kernel<false><<<blocks, 256, 0, s>>>(q, chunk_min, chunk_max, valid, scores, n_chunks,
+                                                     n_chunks_max, total);
+  return check_launch("quest_score_kernel");
+}
+
+extern "C" int zkv_topk(const float* scores, int64_t in_stride, int rows, int L, int k,
+                        int64_t* out, int64_t out_stride, const int64_t* lut, int64_t lut_stride,
+                        const int64_t* skipped, int64_t sk_stride, int sk_count, int64_t sentinel,
+                        zkv_stream_t stream) {
+  ZKV_REQUIRE(scores && out, "zkv_topk: null pointer");
+  ZKV_REQUIRE(rows >= 0 && L >= 0 && k > 0, "zkv_topk: bad sizes rows=%d L=%d k=%d", rows, L, k);
+  ZKV_REQUIRE(out_stride >= k + sk_count, "zkv_topk: out row of %lld < k + skipped = %d",
+              static_cast<long long>(out_stride), k + sk_count);
+  ZKV_REQUIRE(sk_count == 0 || skipped, "zkv_topk: null skipped");
+  if (rows == 0) return ZKV_OK;
+  topk_kernel<<<rows, kTopkThreads, 0, reinterpret_cast<hipStream_t>(stream)>>>(
+      scores, in_stride, L, k, out, out_stride, lut, lut_stride, skipped, sk_stride, sk_count, sentinel);
+  return check_launch("topk_kernel");
+}
+
+extern "C" int zkv_chunk_density_scores(const int64_t* chunk_ids, int64_t id_sb, int64_t id_sh,
+                                        const uint16_t* centroids, int64_t c_sb, int64_t c_sh,
+                                        int64_t c_sc, const uint16_t* raw_q, int64_t q_sb,
+                                        int64_t q_sh, float* out, int64_t o_sb, int64_t o_sh,
+                                        int bs, int kv, int nk, int n_chunks, zkv_stream_t stream) {
+  ZKV_REQUIRE(chunk_ids && centroids && raw_q && out, "zkv_chunk_density_scores: null pointer");
+  ZKV_REQUIRE(bs > 0 && kv > 0 && nk >= 0, "zkv_chunk_density_scores: bad sizes");
+  const int64_t total = static_cast<int64_t>(bs) * kv * nk;
+  if (total == 0) return ZKV_OK;
+  density_kernel<<<static_cast<int>((total + 3) / 4), 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(
+      chunk_ids, id_sb, id_sh, centroids, c_sb, c_sh, c_sc, raw_q, q_sb, q_sh, out, o_sb, o_sh, kv, nk,
+      n_chunks, total);
+  return check_launch("density_kernel");
+}
+
+extern "C" int zkv_dense_mask_from_topk(const int64_t* positions, uint8_t* mask, int rows,
+                                        int n_dense, int nk, zkv_stream_t stream) {
+  ZKV_REQUIRE(positions && mask, "zkv_dense_mask_from_topk: null pointer");
+  if (rows <= 0 || nk <= 0) return ZKV_OK;
+  dense_mask_kernel<<<rows, 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(positions, mask, n_dense, nk);
+  return check_launch("dense_mask_kernel");
+}
+
+extern "C" int zkv_gqa_mean_query(const uint16_t* q, int64_t q_sb, int64_t q_sh, int bs, int hq,
+                                  int kv, uint16_t* out, zkv_stream_t stream) {
+  ZKV_REQUIRE(q && out, "zkv_gqa_mean_query: null pointer");
+  ZKV_REQUIRE(bs > 0 && kv > 0 && hq % kv == 0, "zkv_gqa_mean_query: bad heads hq=%d kv=%d", hq, kv);
+  gqa_mean_kernel<<<bs * kv, 128, 0, reinterpret_cast<hipStream_t>(stream)>>>(q, q_sb, q_sh, kv,
+                                                                              hq / kv, out);
+  return check_launch("gqa_mean_kernel");
+}
+
+extern "C" int zkv_kivi_qk_dense_sparse(const int64_t* chunk_ids, int64_t id_sb, int64_t id_sh,
+                                        const uint8_t* dense_mask, int64_t dm_sb, int64_t dm_sh,
+                                        const int32_t* packed_K, int64_t pk_sb, int64_t pk_sh,
+                                        int n_packed, const uint16_t* chunk_min,
+                                        const uint16_t* chunk_max, int64_t cm_sb, int64_t cm_sh,
+                                        int n_chunks_max, const uint16_t* raw_q, int64_t q_sb,
+                                        int64_t q_sh, int dense_topk, int sparse_topk,
+                                        int group_size, float* out_scores, int64_t* out_indices,
+                                        int64_t o_sb, int64_t o_sh, int bs, int kv, int nk,
+                                        zkv_stream_t stream) {
+  ZKV_REQUIRE(chunk_ids && dense_mask && packed_K && chunk_min && chunk_max && raw_q && out_scores &&
+                  out_indices,
+              "zkv_kivi_qk_dense_sparse: null pointer");
+  ZKV_REQUIRE(group_size == 8 || group_size == 16,
+              "kivi cuda kernel: group_size must be 8 or 16; got %d", group_size);
+  ZKV_REQUIRE(dense_topk >= 1 && dense_topk <= group_size && sparse_topk >= 1 &&
+                  sparse_topk <= group_size,
+              "zkv_kivi_qk_dense_sparse: dense_topk=%d sparse_topk=%d out of [1, %d]", dense_topk,
+              sparse_topk, group_size);
+  ZKV_REQUIRE(bs > 0 && kv > 0 && nk >= 0, "zkv_kivi_qk_dense_sparse: bad sizes");
+  if (nk == 0) return ZKV_OK;
+  auto s = reinterpret_cast<hipStream_t>(stream);
+  if (group_size == 16) {
+    dim3 grid((nk + 15) / 16, kv, bs);
+    kivi_qk_kernel<16><<<grid, 256, 0, s>>>(chunk_ids, id_sb, id_sh, dense_mask, dm_sb, dm_sh,
+                                            packed_K, pk_sb, pk_sh, n_packed, chunk_min, chunk_max,
+                                            cm_sb, cm_sh, n_chunks_max, raw_q, q_sb, q_sh, out_scores,
+                                            out_indices, o_sb, o_sh, nk, dense_topk, sparse_topk);
+  } else {
+    dim3 grid((nk + 31) / 32, kv, bs);
+    kivi_qk_kernel<8><<<grid, 256, 0, s>>>(chunk_ids, id_sb, id_sh, dense_mask, dm_sb, dm_sh,
+                                           packed_K, pk_sb, pk_sh, n_packed, chunk_min, chunk_max,
+                                           cm_sb, cm_sh, n_chunks_max, raw_q, q_sb, q_sh, out_scores,
+                                           out_indices, o_sb, o_sh, nk, dense_topk, sparse_topk);
+  }
+  return check_launch("kivi_qk_kernel");
+}
