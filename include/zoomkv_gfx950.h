@@ -130,6 +130,73 @@ int zkv_kivi4_attention_partial(const uint16_t* q, int64_t q_sb, int64_t q_sh,
 int zkv_attention_merge(const void* workspace, int bs, int hq, int kv, int n_splits,
                         void* out, int out_f32, zkv_stream_t stream);
 
+/* ------------------------------------------------------------------------
+ * Page scoring and selection
+ * ------------------------------------------------------------------------ */
+
+/* Quest upper bound score[b,h,c] = sum_d max(q_d*mn_d, q_d*mx_d) for chunks
+ * c < n_chunks; invalid chunks (valid[b,h,c] == 0) score -inf.  Replaces
+ * quest_kernel.quest_chunk_score(q, chunk_min, chunk_max, scores, n_chunks,
+ * valid) (Z/cache_hub/quest/quest_chunk_score.cu:106-154, :536-540).
+ * q bf16 [bs, kv, 128]; chunk_min/max [bs, kv, n_chunks_max, 128] bf16
+ * (meta_fp16 == 0) or fp16 (meta_fp16 != 0); scores fp32 [bs, kv, n_chunks];
+ * valid uint8 [bs, kv, n_chunks_max] or NULL; all contiguous. */
+int zkv_quest_chunk_score(const uint16_t* q, const uint16_t* chunk_min, const uint16_t* chunk_max,
+                          int meta_fp16, float* scores, int bs, int kv, int n_chunks,
+                          int n_chunks_max, const uint8_t* valid, zkv_stream_t stream);
+
+/* Exact top-k of each of `rows` rows of L fp32 scores (row i at
+ * scores + i*in_stride): out[i, 0..k) = the indices (or lut[i, index] when lut
+ * != NULL) of the k largest scores, ties by lowest index, in increasing index
+ * order; when L <= k, indices 0..L-1 then `sentinel`.  out[i, k..k+sk_count)
+ * = skipped[i, 0..sk_count).  Replaces float_topk_3d (Z/cache_hub/topk/
+ * float_topk.cu:280-346, sentinel -1) and float_topk_gather_concat_3d
+ * (Z/cache_hub/topk/float_topk_gather_concat.cu:305-375, sentinel 0), whose
+ * outputs are the same sets in unspecified order. */
+int zkv_topk(const float* scores, int64_t in_stride, int rows, int L, int k, int64_t* out,
+             int64_t out_stride, const int64_t* lut, int64_t lut_stride, const int64_t* skipped,
+             int64_t sk_stride, int sk_count, int64_t sentinel, zkv_stream_t stream);
+
+/* CDS density out[b,h,j] = centroid[b,h,chunk_ids[b,h,j]] . raw_q[b,h] (fp32,
+ * 128-thread tree order), -1e30 for out-of-range ids.  Replaces
+ * partial_chunk_density_scores (Z/cache_hub/rerank/rerank_topk.cu:627-689).
+ * Strides are per batch / head (/ chunk) in elements; last dims contiguous. */
+int zkv_chunk_density_scores(const int64_t* chunk_ids, int64_t id_sb, int64_t id_sh,
+                             const uint16_t* centroids, int64_t c_sb, int64_t c_sh, int64_t c_sc,
+                             const uint16_t* raw_q, int64_t q_sb, int64_t q_sh, float* out,
+                             int64_t o_sb, int64_t o_sh, int bs, int kv, int nk, int n_chunks,
+                             zkv_stream_t stream);
+
+/* mask[r, :] = 0 then mask[r, positions[r, j]] = 1 for in-range positions;
+ * positions int64 [rows, n_dense], mask uint8 [rows, nk], contiguous.
+ * Replaces mask_from_topk (Z/cache_hub/rerank/rerank_topk.cu:926-998). */
+int zkv_dense_mask_from_topk(const int64_t* positions, uint8_t* mask, int rows, int n_dense, int nk,
+                             zkv_stream_t stream);
+
+/* GQA-mean query raw_q[b, h] = bf16(sum_i q[b, h*g + i] / g), g = hq / kv
+ * (the torch mean of S:1621-1626).  q bf16 [bs, hq, 128] with strides
+ * (q_sb, q_sh); out bf16 [bs, kv, 128] contiguous. */
+int zkv_gqa_mean_query(const uint16_t* q, int64_t q_sb, int64_t q_sh, int bs, int hq, int kv,
+                       uint16_t* out, zkv_stream_t stream);
+
+/* KIVI stage-2 scorer (Format R): per selected chunk, bf16 dequant + bf16
+ * products + fp32 sum, per-chunk descending bitonic sort, keep dense_topk /
+ * sparse_topk, (-1e30, 0) elsewhere.  Replaces
+ * partial_chunk_kivi_qk_dense_sparse (Z/cache_hub/kivi/kivi_qk_dot.cu:325-460):
+ * chunk_ids int64 / dense_mask uint8 [bs, kv, nk]; packed_K int32 [bs, kv,
+ * n_packed, 16, group_size] (chunk stride 16*group_size); chunk_min/max bf16
+ * [bs, kv, n_chunks_max, 128] (chunk stride 128); raw_q bf16 [bs, kv, 128];
+ * out_scores fp32 / out_indices int64 [bs, kv, >= nk*group_size].  Strides
+ * are per batch / head in elements; group_size in {8, 16}. */
+int zkv_kivi_qk_dense_sparse(const int64_t* chunk_ids, int64_t id_sb, int64_t id_sh,
+                             const uint8_t* dense_mask, int64_t dm_sb, int64_t dm_sh,
+                             const int32_t* packed_K, int64_t pk_sb, int64_t pk_sh, int n_packed,
+                             const uint16_t* chunk_min, const uint16_t* chunk_max, int64_t cm_sb,
+                             int64_t cm_sh, int n_chunks_max, const uint16_t* raw_q, int64_t q_sb,
+                             int64_t q_sh, int dense_topk, int sparse_topk, int group_size,
+                             float* out_scores, int64_t* out_indices, int64_t o_sb, int64_t o_sh,
+                             int bs, int kv, int nk, zkv_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

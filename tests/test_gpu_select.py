@@ -1,0 +1,118 @@
+"""GPU parity of the page-scoring / selection kernels against the CPU oracle
+(bit-exact scores, indices and masks)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import select as osel
+from oracle.kivi import encode_chunks_ref
+from oracle.numerics import bf16r, f16_bits, f16_to_f32
+from tests.helpers import from_torch, gaussian_bf16, to_bf16
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("fp16_meta", [False, True])
+def test_quest_chunk_score_bit_exact(rng, fp16_meta):
+    from zoomkv_revision_amd.quest import load_kernel_module
+    bs, kv, n_max, n = 2, 3, 40, 37
+    k = gaussian_bf16(rng, (bs, kv, n_max * 16, 128), outlier_channels=4)
+    mn, mx, _, _ = encode_chunks_ref(k, 16)
+    if fp16_meta:
+        mn, mx = f16_to_f32(f16_bits(mn)), f16_to_f32(f16_bits(mx))
+    q = gaussian_bf16(rng, (bs, kv, 128))
+    valid = rng.random((bs, kv, n_max)) > 0.1
+    ref = osel.quest_chunk_score(q, mn, mx, n, valid)
+    dt = torch.float16 if fp16_meta else torch.bfloat16
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to("cuda", dt)
+    scores = torch.empty(bs, kv, n, dtype=torch.float32, device="cuda")
+    load_kernel_module().quest_chunk_score(to_bf16(q), t(mn), t(mx), scores, n,
+                                           torch.from_numpy(valid).cuda())
+    torch.cuda.synchronize()
+    assert np.array_equal(from_torch(scores).view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("L,k", [(2048, 128), (13120, 100), (131072, 256), (50, 64), (3000, 1)])
+def test_topk_exact(rng, L, k):
+    from zoomkv_revision_amd.topk import float_topk_3d
+    x = rng.standard_normal((2, 3, L)).astype(np.float32)
+    x[0, 0, ::7] = 1.5                          # heavy ties
+    x[1, 2, : L // 2] = x[1, 2, 0]              # a tie block bigger than k
+    got = from_torch(float_topk_3d(torch.from_numpy(x).cuda(), k))
+    assert np.array_equal(got, osel.topk_indices(x, k))
+
+
+def test_topk_strided_and_bf16_input(rng):
+    from zoomkv_revision_amd.topk import float_topk, float_topk_3d
+    x = rng.standard_normal((4, 5, 300)).astype(np.float32)
+    xt = torch.from_numpy(x).cuda()
+    assert np.array_equal(from_torch(float_topk_3d(xt[:, 1:4], 17)), osel.topk_indices(x[:, 1:4], 17))
+    xb = bf16r(x[0])
+    assert np.array_equal(from_torch(float_topk(to_bf16(xb), 9)), osel.topk_indices(xb, 9))
+
+
+def test_topk_gather_concat(rng):
+    from zoomkv_revision_amd.topk import float_topk_gather_concat_3d
+    bs, kv, L, k, sk = 2, 4, 1600, 100, 5
+    sc = rng.standard_normal((bs, kv, L)).astype(np.float32)
+    lut = rng.integers(0, 10 ** 6, size=(bs, kv, L))
+    skipped = rng.integers(0, 99, size=(bs, kv, sk))
+    out = torch.full((bs, kv, 612), -7, dtype=torch.int64, device="cuda")
+    float_topk_gather_concat_3d(torch.from_numpy(sc).cuda(), torch.from_numpy(lut).cuda(),
+                                torch.from_numpy(skipped).cuda(), out, k)
+    got = from_torch(out)
+    ref = osel.topk_gather_concat(sc, lut, skipped, k, k + sk)
+    assert np.array_equal(got[..., :k + sk], ref)
+    assert np.all(got[..., k + sk:] == -7)
+    # L <= k: lut prefix then 0 sentinel
+    out2 = torch.full((1, 1, 10), -7, dtype=torch.int64, device="cuda")
+    float_topk_gather_concat_3d(torch.ones(1, 1, 3, device="cuda"),
+                                torch.tensor([[[5, 6, 7]]], device="cuda"),
+                                torch.zeros(1, 1, 0, dtype=torch.int64, device="cuda"), out2, 6)
+    assert from_torch(out2)[0, 0].tolist() == [5, 6, 7, 0, 0, 0, -7, -7, -7, -7]
+
+
+def test_density_and_mask_bit_exact(rng):
+    from zoomkv_revision_amd.rerank import dense_mask_from_topk_cuda, partial_chunk_density_scores_cuda
+    bs, kv, n, nk = 2, 3, 50, 21
+    cent = gaussian_bf16(rng, (bs, kv, n, 128))
+    q = gaussian_bf16(rng, (bs, kv, 128))
+    ids = rng.integers(-2, n + 2, size=(bs, kv, nk))
+    out = torch.empty(bs, kv, nk, dtype=torch.float32, device="cuda")
+    partial_chunk_density_scores_cuda(torch.from_numpy(ids).cuda(), to_bf16(cent), to_bf16(q), out)
+    ref = osel.chunk_density_scores(ids, cent, q)
+    assert np.array_equal(from_torch(out).view(np.uint32), ref.view(np.uint32))
+    pos = rng.integers(-1, nk + 1, size=(bs, kv, 6))
+    mask = torch.ones(bs, kv, nk, dtype=torch.bool, device="cuda")
+    dense_mask_from_topk_cuda(torch.from_numpy(pos).cuda(), mask)
+    assert np.array_equal(from_torch(mask), osel.dense_mask_from_topk(pos, nk))
+
+
+def test_gqa_mean_bit_exact(rng):
+    from zoomkv_revision_amd.rerank import gqa_mean_query
+    q = gaussian_bf16(rng, (3, 32, 128))
+    got = gqa_mean_query(to_bf16(q).unsqueeze(1), 8)
+    assert np.array_equal(from_torch(got), osel.gqa_mean_query(q, 8))
+
+
+@pytest.mark.parametrize("g", [8, 16])
+def test_kivi_qk_dense_sparse_bit_exact(rng, g):
+    from zoomkv_revision_amd.kivi import partial_chunk_kivi_qk_dense_sparse_cuda
+    bs, kv, n_chunks, nk = 2, 3, 60, 37
+    keys = gaussian_bf16(rng, (bs, kv, n_chunks * g, 128), outlier_channels=4)
+    mn, mx, _, packed = encode_chunks_ref(keys, g)
+    q = gaussian_bf16(rng, (bs, kv, 128))
+    ids = rng.integers(0, n_chunks, size=(bs, kv, nk))
+    ids[0, 1, 3] = n_chunks + 5                       # out of range -> -1e30 slots
+    dm = rng.random((bs, kv, nk)) > 0.7
+    dense_topk, sparse_topk = g, max(1, g // 2)
+    os_ = torch.full((bs, kv, nk * g + 4), 7.0, device="cuda")
+    oi = torch.full((bs, kv, nk * g + 4), -9, dtype=torch.int64, device="cuda")
+    partial_chunk_kivi_qk_dense_sparse_cuda(
+        torch.from_numpy(ids).cuda(), torch.from_numpy(dm).cuda(), torch.from_numpy(packed).cuda(),
+        to_bf16(mn), to_bf16(mx), to_bf16(q), dense_topk, sparse_topk, g, os_, oi)
+    rs, ri = osel.kivi_qk_dense_sparse(ids, dm, packed, mn, mx, q, dense_topk, sparse_topk, g)
+    gs, gi = from_torch(os_), from_torch(oi)
+    assert np.array_equal(gs[..., :nk * g].view(np.uint32), rs.view(np.uint32))
+    assert np.array_equal(gi[..., :nk * g], ri)
+    assert np.all(gs[..., nk * g:] == 7.0) and np.all(gi[..., nk * g:] == -9)

@@ -37,6 +37,15 @@ SIGNATURES = {
     "zkv_kivi4_attention_partial": (I32, [P, I64, I64, P, P, P, P, I32, P, P, I32,
                                           I32, I32, I32, I32, I32, F32, I32, P, SZ, P, P]),
     "zkv_attention_merge": (I32, [P, I32, I32, I32, I32, P, I32, P]),
+    "zkv_quest_chunk_score": (I32, [P, P, P, I32, P, I32, I32, I32, I32, P, P]),
+    "zkv_topk": (I32, [P, I64, I32, I32, I32, P, I64, P, I64, P, I64, I32, I64, P]),
+    "zkv_chunk_density_scores": (I32, [P, I64, I64, P, I64, I64, I64, P, I64, I64, P, I64, I64,
+                                       I32, I32, I32, I32, P]),
+    "zkv_dense_mask_from_topk": (I32, [P, P, I32, I32, I32, P]),
+    "zkv_gqa_mean_query": (I32, [P, I64, I64, I32, I32, I32, P, P]),
+    "zkv_kivi_qk_dense_sparse": (I32, [P, I64, I64, P, I64, I64, P, I64, I64, I32, P, P, I64, I64,
+                                       I32, P, I64, I64, I32, I32, I32, P, P, I64, I64,
+                                       I32, I32, I32, P]),
 }
 
 _lib = None

@@ -232,3 +232,49 @@ def attention_merge(workspace: torch.Tensor, bs: int, hq: int, kv: int, n_splits
     check(lib().zkv_attention_merge(ptr(workspace), bs, hq, kv, n_splits, ptr(out),
                                     int(out.dtype == torch.float32), stream_of(out)))
     return out
+
+
+def partial_chunk_kivi_qk_dense_sparse_cuda(chunk_ids, dense_mask, packed_K, chunk_min, chunk_max,
+                                            raw_q, dense_topk, sparse_topk, group_size, out_scores,
+                                            out_indices, kernel=None) -> None:
+    """KIVI stage-2 scorer on a Format R cache, in place (signature of
+    Z/cache_hub/kivi/kivi_qk_dot_ops.py:29-67; ``kernel`` is ignored)."""
+    require_gpu(chunk_ids, dense_mask, packed_K, chunk_min, chunk_max, raw_q, out_scores, out_indices)
+    if chunk_ids.dtype != torch.int64:
+        chunk_ids = chunk_ids.to(torch.int64)
+    if dense_mask.dtype != torch.bool:
+        dense_mask = dense_mask.bool()
+    if packed_K.dtype != torch.int32:
+        raise TypeError(f"packed_K must be int32; got {packed_K.dtype}")
+    for name, t in (("chunk_min", chunk_min), ("chunk_max", chunk_max), ("raw_q", raw_q)):
+        if t.dtype != torch.bfloat16:
+            raise TypeError(f"{name} must be bfloat16; got {t.dtype}")
+    if out_scores.dtype != torch.float32:
+        raise TypeError(f"out_scores must be float32; got {out_scores.dtype}")
+    if out_indices.dtype != torch.int64:
+        raise TypeError(f"out_indices must be int64; got {out_indices.dtype}")
+    g = int(group_size)
+    if g not in (8, 16):
+        raise ValueError(f"group_size must be 8 or 16; got {group_size}")
+    if packed_K.dim() != 5 or packed_K.shape[3] != 16 or packed_K.shape[4] != g:
+        raise RuntimeError("packed_K must be chunk-major [bs, kv, n_chunks, 16, group_size]")
+    if packed_K.stride(4) != 1 or packed_K.stride(3) != g or packed_K.stride(2) != 16 * g:
+        raise RuntimeError("packed_K inner [n_chunks, 16, group_size] must be contiguous")
+    if chunk_min.stride() != chunk_max.stride() or chunk_min.stride(3) != 1 or chunk_min.stride(2) != 128:
+        raise RuntimeError("chunk_min / chunk_max must share strides with contiguous [.., 128] rows")
+    for t in (chunk_ids, dense_mask, raw_q, out_scores, out_indices):
+        if t.stride(-1) != 1:
+            raise RuntimeError("last dims must be contiguous")
+    if out_scores.stride()[:2] != out_indices.stride()[:2]:
+        raise RuntimeError("out_scores / out_indices must share batch / head strides")
+    bs, kv, nk = chunk_ids.shape
+    if out_scores.shape[2] < nk * g or out_indices.shape[2] < nk * g:
+        raise RuntimeError(f"outputs too small: need {nk * g}")
+    check(lib().zkv_kivi_qk_dense_sparse(
+        ptr(chunk_ids), chunk_ids.stride(0), chunk_ids.stride(1),
+        ptr(dense_mask), dense_mask.stride(0), dense_mask.stride(1),
+        ptr(packed_K), packed_K.stride(0), packed_K.stride(1), packed_K.shape[2],
+        ptr(chunk_min), ptr(chunk_max), chunk_min.stride(0), chunk_min.stride(1), chunk_min.shape[2],
+        ptr(raw_q), raw_q.stride(0), raw_q.stride(1), int(dense_topk), int(sparse_topk), g,
+        ptr(out_scores), ptr(out_indices), out_scores.stride(0), out_scores.stride(1), bs, kv, nk,
+        stream_of(raw_q)))

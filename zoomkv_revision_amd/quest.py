@@ -1,0 +1,61 @@
+"""Quest page scoring over the gfx950 C ABI.
+
+Mirrors the reference's loader API: ``load_kernel_module()`` returns an object
+whose ``quest_chunk_score(q, chunk_min, chunk_max, scores, n_chunks, valid)``
+has the signature of the CUDA extension (Z/cache_hub/quest/quest_chunk_score.cu:536-540,
+loaded by Z/cache_hub/quest/quest_ops.py:89-107).  There is no PyTorch
+fallback: a missing library raises.
+"""
+from __future__ import annotations
+
+import torch
+
+from ._lib import check, lib, ptr, require_gpu, stream_of
+
+
+def quest_chunk_score(q: torch.Tensor, chunk_min: torch.Tensor, chunk_max: torch.Tensor,
+                      scores: torch.Tensor, n_chunks: int, valid: torch.Tensor | None = None) -> None:
+    """scores[b, h, c] = sum_d max(q_d mn_d, q_d mx_d) for c < n_chunks, in place.
+
+    q bf16 [bs, kv, 128]; chunk_min / chunk_max [bs, kv, n_max, 128] bf16 (the
+    reference) or fp16; scores fp32 [bs, kv, n_chunks]; valid bool
+    [bs, kv, n_max] or None (invalid chunks score -inf).
+    """
+    require_gpu(q, chunk_min, chunk_max, scores)
+    if q.dtype != torch.bfloat16:
+        raise RuntimeError(f"quest_chunk_score: only bf16 q is supported; got {q.dtype}")
+    if chunk_min.dtype != chunk_max.dtype or chunk_min.dtype not in (torch.bfloat16, torch.float16):
+        raise RuntimeError("quest_chunk_score: chunk_min / chunk_max must both be bf16 or fp16")
+    bs, kv, d = q.shape
+    if d != 128:
+        raise RuntimeError(f"quest_chunk_score: only head_dim==128 is supported; got {d}")
+    n_max = chunk_min.shape[2]
+    n_chunks = int(n_chunks)
+    if n_chunks > n_max:
+        raise RuntimeError("n_chunks must <= chunk_n_max")
+    for name, t in (("q", q), ("chunk_min", chunk_min), ("chunk_max", chunk_max), ("scores", scores)):
+        if not t.is_contiguous():
+            raise RuntimeError(f"{name} must be contiguous")
+    if tuple(chunk_min.shape) != (bs, kv, n_max, 128) or chunk_max.shape != chunk_min.shape:
+        raise RuntimeError("chunk_min / chunk_max must be [bs, kv, n_chunks_max, 128]")
+    if scores.dtype != torch.float32 or scores.numel() != bs * kv * n_chunks:
+        raise RuntimeError("scores must be fp32 [bs, kv, n_chunks]")
+    if valid is not None:
+        if valid.dtype != torch.bool or not valid.is_contiguous() or tuple(valid.shape) != (bs, kv, n_max):
+            raise RuntimeError("valid must be a contiguous bool [bs, kv, n_chunks_max]")
+    check(lib().zkv_quest_chunk_score(
+        ptr(q), ptr(chunk_min), ptr(chunk_max), int(chunk_min.dtype == torch.float16), ptr(scores),
+        bs, kv, n_chunks, n_max, ptr(valid), stream_of(q)))
+
+
+class QuestKernel:
+    """Drop-in for the module ``quest_ops.load_kernel_module()`` returns."""
+
+    @staticmethod
+    def quest_chunk_score(q, chunk_min, chunk_max, scores, n_chunks, valid=None):
+        quest_chunk_score(q, chunk_min, chunk_max, scores, n_chunks, valid)
+
+
+def load_kernel_module() -> QuestKernel:
+    lib()  # fail loudly now if the native library is missing
+    return QuestKernel()
