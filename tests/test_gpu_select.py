@@ -32,7 +32,7 @@ def test_quest_chunk_score_bit_exact(rng, fp16_meta):
     assert np.array_equal(from_torch(scores).view(np.uint32), ref.view(np.uint32))
 
 
-@pytest.mark.parametrize("L,k", [(2048, 128), (13120, 100), (131072, 256), (50, 64), (3000, 1)])
+@pytest.mark.parametrize("L,k", [(2048, 128), (13120, 100), (131072, 256), (64, 64), (3000, 1)])
 def test_topk_exact(rng, L, k):
     from zoomkv_revision_amd.topk import float_topk_3d
     x = rng.standard_normal((2, 3, L)).astype(np.float32)
@@ -40,6 +40,13 @@ def test_topk_exact(rng, L, k):
     x[1, 2, : L // 2] = x[1, 2, 0]              # a tie block bigger than k
     got = from_torch(float_topk_3d(torch.from_numpy(x).cuda(), k))
     assert np.array_equal(got, osel.topk_indices(x, k))
+
+
+def test_topk_rejects_k_above_length():
+    # float_topk_ops.py:103 asserts k <= n_chunks before launching
+    from zoomkv_revision_amd.topk import float_topk_3d
+    with pytest.raises(AssertionError):
+        float_topk_3d(torch.zeros(1, 1, 50, device="cuda"), 64)
 
 
 def test_topk_strided_and_bf16_input(rng):
@@ -64,12 +71,19 @@ def test_topk_gather_concat(rng):
     ref = osel.topk_gather_concat(sc, lut, skipped, k, k + sk)
     assert np.array_equal(got[..., :k + sk], ref)
     assert np.all(got[..., k + sk:] == -7)
-    # L <= k: lut prefix then 0 sentinel
-    out2 = torch.full((1, 1, 10), -7, dtype=torch.int64, device="cuda")
-    float_topk_gather_concat_3d(torch.ones(1, 1, 3, device="cuda"),
-                                torch.tensor([[[5, 6, 7]]], device="cuda"),
-                                torch.zeros(1, 1, 0, dtype=torch.int64, device="cuda"), out2, 6)
-    assert from_torch(out2)[0, 0].tolist() == [5, 6, 7, 0, 0, 0, -7, -7, -7, -7]
+    # L <= k (reachable through the C ABI; the Python wrappers assert k <= L
+    # like the reference's): lut prefix, skipped tail after k, 0 sentinel
+    from zoomkv_revision_amd._lib import check, lib, ptr, stream_of
+    sc2 = torch.ones(1, 3, device="cuda")
+    lut2 = torch.tensor([[5, 6, 7]], device="cuda")
+    sk2 = torch.tensor([[41, 42]], device="cuda")
+    out2 = torch.full((1, 10), -7, dtype=torch.int64, device="cuda")
+    check(lib().zkv_topk(ptr(sc2), 3, 1, 3, 6, ptr(out2), 10, ptr(lut2), 3, ptr(sk2), 2, 2, 0,
+                         stream_of(sc2)))
+    assert from_torch(out2)[0].tolist() == [5, 6, 7, 0, 0, 0, 41, 42, -7, -7]
+    out3 = torch.full((1, 6), -7, dtype=torch.int64, device="cuda")
+    check(lib().zkv_topk(ptr(sc2), 3, 1, 3, 5, ptr(out3), 6, None, 0, None, 0, 0, -1, stream_of(sc2)))
+    assert from_torch(out3)[0].tolist() == [0, 1, 2, -1, -1, -7]
 
 
 def test_density_and_mask_bit_exact(rng):
