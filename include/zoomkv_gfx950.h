@@ -197,6 +197,46 @@ int zkv_kivi_qk_dense_sparse(const int64_t* chunk_ids, int64_t id_sb, int64_t id
                              float* out_scores, int64_t* out_indices, int64_t o_sb, int64_t o_sh,
                              int bs, int kv, int nk, zkv_stream_t stream);
 
+/* ---- RaBitQ 1-bit sign codes -------------------------------------------------
+ * The reference's RaBitQ keys are 4-bit sign + magnitude codes (ParisKV,
+ * PC:1130-1195 batch_encode; rerank_rabitq_ref, Z/cache_hub/rerank/rerank.py:205-274).
+ * This path keeps 1 bit per dimension of the SRHT-rotated vector, 16 bytes per
+ * 128-dim key, plus fp16 (norm, correction) factors.
+ *
+ * Encode n fp16 vectors (rows of 128 at row_stride elements, 16-byte aligned)
+ * with the +-1 SRHT sign vector signs (fp32 [128], device):
+ *   codes uint8 [n, 16] (bit b of byte j = sign of rotated dim 8j + b),
+ *   factors fp16 [n, 2] = (||x||, ||y|| sqrt(128) / sum|y|).
+ * Replaces batch_encode (PC:1130-1195) / _encode_query_blocks (PC:1108-1124). */
+int zkv_rabitq_encode(const uint16_t* x, int64_t row_stride, int64_t n, const float* signs,
+                      uint8_t* codes, uint16_t* factors, zkv_stream_t stream);
+
+/* Estimate matrix out fp32 [pools, queries, n]:
+ *   ((nk*ck) * (nq*cq)) * (128 - 2 popc(xq ^ xk)) / 128
+ * (the sign-sign identity of Z/cache_hub/rerank/coarse_2bit_score.cu:12-16 with
+ * the RaBitQ corrections; counterpart of approx_scores in rerank.py:255-264).
+ * codes_q [pools, queries, 16], codes_k [pools, n, 16], factors likewise. */
+int zkv_rabitq_estimate(const uint8_t* codes_q, const uint16_t* factors_q, const uint8_t* codes_k,
+                        const uint16_t* factors_k, int pools, int queries, int64_t n, float* out,
+                        zkv_stream_t stream);
+
+/* Workspace bytes zkv_rabitq_search needs (0 for invalid sizes). */
+size_t zkv_rabitq_search_workspace_size(int pools, int queries, int64_t n, int topk);
+
+/* Search: encode the fp16 queries q [pools, queries, 128], take the top-topk
+ * keys by estimate (ties to the lower index) into cand_idx [pools, queries, topk]
+ * (increasing index order), rerank them by the exact fp32 dot with the fp16
+ * keys (keys + pool * k_pool_stride + index * k_row_stride) and write them in
+ * (score desc, index asc) order to final_idx / final_scores.  Counterpart of
+ * rerank_rabitq_ref's coarse filter -> score -> top-k
+ * (Z/cache_hub/rerank/rerank.py:205-274).  Limits: topk <= min(n, 1024) and
+ * ceil(n / 8192) * topk <= 8192. */
+int zkv_rabitq_search(const uint16_t* q, const uint16_t* keys, int64_t k_pool_stride,
+                      int64_t k_row_stride, const uint8_t* codes, const uint16_t* factors,
+                      const float* signs, int pools, int queries, int64_t n, int topk,
+                      int64_t* cand_idx, int64_t* final_idx, float* final_scores, void* workspace,
+                      size_t workspace_bytes, zkv_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

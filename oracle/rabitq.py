@@ -71,10 +71,15 @@ def encode(x_f16: np.ndarray, signs: np.ndarray):
     return codes, fac
 
 
+_POPC8 = np.array([bin(i).count("1") for i in range(256)], dtype=np.int32)
+
+
 def popcount_distance(codes_q: np.ndarray, codes_k: np.ndarray) -> np.ndarray:
-    """popc(xq ^ xk) for every (query, key): [Q, N] int32."""
-    x = np.bitwise_xor(codes_q[:, None, :], codes_k[None, :, :])
-    return np.unpackbits(x, axis=-1).sum(axis=-1).astype(np.int32)
+    """popc(xq ^ xk) for every (query, key): [Q, N] int32 (byte table lookup)."""
+    out = np.zeros((codes_q.shape[0], codes_k.shape[0]), dtype=np.int32)
+    for j in range(codes_q.shape[1]):
+        out += _POPC8[np.bitwise_xor(codes_q[:, None, j], codes_k[None, :, j])]
+    return out
 
 
 def estimate(codes_q, fac_q, codes_k, fac_k) -> np.ndarray:

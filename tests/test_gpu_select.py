@@ -130,3 +130,48 @@ def test_kivi_qk_dense_sparse_bit_exact(rng, g):
     assert np.array_equal(gs[..., :nk * g].view(np.uint32), rs.view(np.uint32))
     assert np.array_equal(gi[..., :nk * g], ri)
     assert np.all(gs[..., nk * g:] == 7.0) and np.all(gi[..., nk * g:] == -9)
+
+
+# The reference's own top-k cases (Z/cache_hub/topk/test_float_topk.py:38-149),
+# checked here against the exact oracle instead of an overlap count.
+@pytest.mark.parametrize("case", ["basic", "k1", "k_near_length", "k_equals_length", "negative",
+                                  "mixed_sign", "large_length", "repeated"])
+def test_topk_reference_cases(case):
+    from zoomkv_revision_amd.topk import float_topk
+    g = np.random.default_rng(sorted(["basic", "k1", "k_near_length", "k_equals_length", "negative",
+                                      "mixed_sign", "large_length", "repeated"]).index(case))
+    shapes = {"basic": (4, 3000, 64), "k1": (8, 500, 1), "k_near_length": (2, 300, 290),
+              "k_equals_length": (2, 128, 128), "negative": (4, 1000, 50), "mixed_sign": (4, 2000, 100),
+              "large_length": (1, 128 * 1024, 100), "repeated": (1, 1000, 50)}
+    B, L, k = shapes[case]
+    x = g.standard_normal((B, L)).astype(np.float32)
+    if case == "negative":
+        x = -g.random((B, L)).astype(np.float32) - 1.0
+    elif case == "mixed_sign":
+        x *= 100
+    elif case == "repeated":
+        x[:] = 0
+        x[0, :50], x[0, 50:100] = 1.0, 0.5
+    got = from_torch(float_topk(torch.from_numpy(x).cuda(), k))
+    assert np.array_equal(got, osel.topk_indices(x, k))
+    if case == "repeated":
+        assert np.all(x[0, got[0]] == 1.0)
+
+
+# Z/cache_hub/topk/test_float_topk_gather_concat.py:116-128 (same shapes, k, sk and slack)
+@pytest.mark.parametrize("bs,kv,L,k,sk,max_sk,seed", [
+    (1, 8, 6400, 100, 0, 0, 0), (1, 8, 6400, 100, 12, 12, 1), (8, 8, 6400, 100, 12, 12, 2),
+    (8, 8, 6400, 100, 0, 0, 3), (2, 4, 512, 64, 8, 8, 4), (1, 2, 1024, 1, 0, 0, 5),
+    (2, 4, 2048, 50, 8, 64, 6)])
+def test_gather_concat_reference_cases(bs, kv, L, k, sk, max_sk, seed):
+    from zoomkv_revision_amd.topk import float_topk_gather_concat_3d
+    g = np.random.default_rng(seed)
+    sc = g.standard_normal((bs, kv, L)).astype(np.float32)
+    lut = g.integers(0, 1 << 40, size=(bs, kv, L))
+    skipped = g.integers(0, 1 << 20, size=(bs, kv, sk))
+    out = torch.full((bs, kv, k + max_sk), -5, dtype=torch.int64, device="cuda")
+    float_topk_gather_concat_3d(torch.from_numpy(sc).cuda(), torch.from_numpy(lut).cuda(),
+                                torch.from_numpy(skipped).cuda(), out, k)
+    got = from_torch(out)
+    assert np.array_equal(got[..., :k + sk], osel.topk_gather_concat(sc, lut, skipped, k, k + sk))
+    assert np.all(got[..., k + sk:] == -5)

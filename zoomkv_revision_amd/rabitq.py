@@ -1,0 +1,134 @@
+"""RaBitQ 1-bit sign codes, estimate, top-k and exact rerank on gfx950.
+
+The reference's RaBitQ path (ParisKV) stores 4-bit sign + magnitude codes per
+8-dim block (``PC:1130-1195``) and reranks candidates with
+``rerank_rabitq_ref`` (``Z/cache_hub/rerank/rerank.py:205-274``: coarse filter ->
+approximate score -> top-k).  This module keeps one sign bit per rotated
+dimension (16 bytes per 128-dim key) with fp16 (norm, correction) factors:
+
+* ``rabitq_encode``: SRHT (one +-1 sign round, then the Walsh-Hadamard
+  butterfly of ``Z/cache_hub/hadamard_fallback.py:16-23``) and bit-pack of
+  ``y >= 0`` as in ``PC:1147-1160``;
+* ``rabitq_estimate``: ``((nk*ck) * (nq*cq)) * (128 - 2 popc(xq ^ xk)) / 128``;
+* ``rabitq_search``: top-k by estimate (ties to the lower index), exact fp32
+  rerank of the fp16 keys, output ordered by (score desc, index asc).
+
+Pools are independent key sets (e.g. one per (batch, kv head)); queries of a
+pool are searched against that pool only.
+"""
+from __future__ import annotations
+
+import torch
+
+from ._lib import check, lib, ptr, require_gpu, stream_of
+
+HEAD_DIM = 128
+CODE_BYTES = 16
+
+
+def srht_signs(seed: int = 42, device="cuda") -> torch.Tensor:
+    """Seeded +-1 SRHT diagonal (fp32 [128]); the reference draws its signs
+    from a seeded torch RNG the same way (``PC:79-93``)."""
+    g = torch.Generator(device="cpu")
+    g.manual_seed(seed)
+    s = torch.randint(0, 2, (HEAD_DIM,), generator=g).to(torch.float32) * 2 - 1
+    return s.to(device)
+
+
+def _check_signs(signs: torch.Tensor):
+    assert signs.dtype == torch.float32 and signs.shape == (HEAD_DIM,) and signs.is_contiguous(), \
+        "signs must be a contiguous fp32 [128] tensor"
+
+
+def rabitq_encode(x: torch.Tensor, signs: torch.Tensor, codes: torch.Tensor | None = None,
+                  factors: torch.Tensor | None = None):
+    """x fp16 [..., 128] -> (codes uint8 [..., 16], factors fp16 [..., 2] = (norm, corr))."""
+    require_gpu(x, signs)
+    _check_signs(signs)
+    assert x.dtype == torch.float16 and x.shape[-1] == HEAD_DIM, "x must be fp16 [..., 128]"
+    lead = x.shape[:-1]
+    rows = x.reshape(-1, HEAD_DIM)
+    if rows.stride(-1) != 1 or (rows.stride(0) % 8) or (rows.data_ptr() % 16):
+        rows = rows.contiguous()
+    n = rows.shape[0]
+    if codes is None:
+        codes = torch.empty(*lead, CODE_BYTES, dtype=torch.uint8, device=x.device)
+    if factors is None:
+        factors = torch.empty(*lead, 2, dtype=torch.float16, device=x.device)
+    assert codes.is_contiguous() and codes.dtype == torch.uint8 and codes.numel() == n * CODE_BYTES
+    assert factors.is_contiguous() and factors.dtype == torch.float16 and factors.numel() == n * 2
+    check(lib().zkv_rabitq_encode(ptr(rows), rows.stride(0) if n else HEAD_DIM, n, ptr(signs),
+                                  ptr(codes), ptr(factors), stream_of(x)))
+    return codes, factors
+
+
+def _pools(t: torch.Tensor, last: int) -> torch.Tensor:
+    """[N, last] -> [1, N, last]; [P, N, last] as is."""
+    assert t.dim() in (2, 3) and t.shape[-1] == last, f"expected [..., {last}], got {tuple(t.shape)}"
+    return t.unsqueeze(0) if t.dim() == 2 else t
+
+
+def rabitq_estimate(codes_q: torch.Tensor, factors_q: torch.Tensor, codes_k: torch.Tensor,
+                    factors_k: torch.Tensor) -> torch.Tensor:
+    """Estimate matrix fp32 [P, Q, N] (or [Q, N] for 2-D inputs)."""
+    require_gpu(codes_q, factors_q, codes_k, factors_k)
+    squeeze = codes_q.dim() == 2
+    cq, fq = _pools(codes_q, CODE_BYTES).contiguous(), _pools(factors_q, 2).contiguous()
+    ck, fk = _pools(codes_k, CODE_BYTES).contiguous(), _pools(factors_k, 2).contiguous()
+    P, Q, _ = cq.shape
+    assert ck.shape[0] == P and fq.shape[:2] == cq.shape[:2] and fk.shape[:2] == ck.shape[:2]
+    N = ck.shape[1]
+    out = torch.empty(P, Q, N, dtype=torch.float32, device=cq.device)
+    check(lib().zkv_rabitq_estimate(ptr(cq), ptr(fq), ptr(ck), ptr(fk), P, Q, N, ptr(out),
+                                    stream_of(cq)))
+    return out[0] if squeeze else out
+
+
+_WS: dict = {}
+
+
+def search_workspace(pools: int, queries: int, n: int, topk: int, device) -> torch.Tensor:
+    nbytes = lib().zkv_rabitq_search_workspace_size(pools, queries, n, topk)
+    key = torch.device(device)
+    ws = _WS.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=key)
+        _WS[key] = ws
+    return ws
+
+
+def rabitq_search(q: torch.Tensor, keys: torch.Tensor, codes: torch.Tensor, factors: torch.Tensor,
+                  signs: torch.Tensor, topk: int, workspace: torch.Tensor | None = None):
+    """Top-``topk`` keys per query by RaBitQ estimate, reranked exactly.
+
+    q fp16 [P, Q, 128] (or [Q, 128]); keys fp16 [P, N, 128] (or [N, 128]; row
+    views with a 16-byte aligned stride are used in place); codes uint8
+    [P, N, 16]; factors fp16 [P, N, 2].  Returns (cand_idx int64 [P, Q, topk]
+    in increasing index order, final_idx int64 [P, Q, topk], final_scores
+    fp32 [P, Q, topk]) with the final pair ordered by (score desc, index asc).
+    """
+    require_gpu(q, keys, codes, factors, signs)
+    _check_signs(signs)
+    squeeze = q.dim() == 2
+    qq = _pools(q, HEAD_DIM).contiguous()
+    kk = _pools(keys, HEAD_DIM)
+    cc = _pools(codes, CODE_BYTES).contiguous()
+    ff = _pools(factors, 2).contiguous()
+    assert qq.dtype == torch.float16 and kk.dtype == torch.float16, "q and keys must be fp16"
+    assert cc.dtype == torch.uint8 and ff.dtype == torch.float16
+    P, Q, _ = qq.shape
+    N = kk.shape[1]
+    assert kk.shape[0] == P and cc.shape[:2] == (P, N) and ff.shape[:2] == (P, N), "pool/key shape mismatch"
+    if kk.stride(-1) != 1 or kk.stride(1) % 8 or kk.stride(0) % 8 or kk.data_ptr() % 16:
+        kk = kk.contiguous()
+    assert 0 < topk <= N, f"topk={topk} must be in [1, {N}]"
+    ws = workspace if workspace is not None else search_workspace(P, Q, N, topk, q.device)
+    cand = torch.empty(P, Q, topk, dtype=torch.int64, device=q.device)
+    fidx = torch.empty_like(cand)
+    fsc = torch.empty(P, Q, topk, dtype=torch.float32, device=q.device)
+    check(lib().zkv_rabitq_search(ptr(qq), ptr(kk), kk.stride(0), kk.stride(1), ptr(cc), ptr(ff),
+                                  ptr(signs), P, Q, N, topk, ptr(cand), ptr(fidx), ptr(fsc), ptr(ws),
+                                  ws.numel(), stream_of(q)))
+    if squeeze:
+        return cand[0], fidx[0], fsc[0]
+    return cand, fidx, fsc
