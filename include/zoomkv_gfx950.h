@@ -197,6 +197,35 @@ int zkv_kivi_qk_dense_sparse(const int64_t* chunk_ids, int64_t id_sb, int64_t id
                              float* out_scores, int64_t* out_indices, int64_t o_sb, int64_t o_sh,
                              int bs, int kv, int nk, zkv_stream_t stream);
 
+/* Quest page metadata of a paged cache in fp16: per (b, kv, page, channel)
+ * min (rounded toward -inf) and max (toward +inf) of bf16 keys [bs, kv, n_tok,
+ * 128] at element strides (k_sb, k_sh, k_st), pages of page_size tokens ->
+ * page_min / page_max fp16 [bs, kv, n_pages_max, 128].  fp16 counterpart of
+ * the chunk amin / amax of _compute_and_store_chunk_minmax (S:2025-2157) feeding
+ * quest_chunk_score (Z/cache_hub/quest/quest_chunk_score.cu:31-154). */
+int zkv_page_minmax_f16(const uint16_t* keys, int64_t k_sb, int64_t k_sh, int64_t k_st, int bs,
+                        int kv, int page_size, int n_pages, int n_pages_max, uint16_t* page_min,
+                        uint16_t* page_max, zkv_stream_t stream);
+
+/* Page-sparse decode attention: as zkv_kivi4_decode_attention, but the
+ * quantized context of (b, kv) is the list pages int64 [bs, kv, n_sel]
+ * (element strides pg_sb, pg_sh) of 16-token pages (page P = tokens 16P ..
+ * 16P+15, i.e. half P & 1 of Format Q group P >> 1), followed by the bf16
+ * residual window.  Equals attention over the gathered tokens of the listed
+ * pages (a page listed twice counts twice; ids outside [0, 2 * n_groups) are
+ * skipped); sorted lists let both halves of a group share one tile.
+ * Counterpart of the Quest select -> gather -> flash_attn_with_kvcache
+ * sequence (S:2195-2240, S:1723-1772). */
+size_t zkv_kivi4_sparse_attention_workspace_size(int bs, int hq, int kv, int n_sel, int res_len,
+                                                 int n_splits);
+int zkv_kivi4_sparse_attention(const uint16_t* q, int64_t q_sb, int64_t q_sh, const int32_t* k_codes,
+                               const uint16_t* k_meta, const int32_t* v_codes, const uint16_t* v_meta,
+                               int g_cap, const uint16_t* k_res, const uint16_t* v_res, int r_cap,
+                               int bs, int hq, int kv, int n_groups, int res_len, const int64_t* pages,
+                               int64_t pg_sb, int64_t pg_sh, int n_sel, float sm_scale, void* out,
+                               int out_f32, int n_splits, void* workspace, size_t workspace_bytes,
+                               zkv_stream_t stream);
+
 /* ---- RaBitQ 1-bit sign codes -------------------------------------------------
  * The reference's RaBitQ keys are 4-bit sign + magnitude codes (ParisKV,
  * PC:1130-1195 batch_encode; rerank_rabitq_ref, Z/cache_hub/rerank/rerank.py:205-274).

@@ -326,3 +326,32 @@ def kivi4_decode_attention(q, cache: Kivi4Cache, n_groups: int, k_res, v_res,
     k = np.concatenate([kh, k_res[:, :, :res_len].astype(dtype)], axis=2)
     v = np.concatenate([vh, v_res[:, :, :res_len].astype(dtype)], axis=2)
     return attention(q, k, v, sm_scale, dtype=dtype)
+
+
+def kivi4_sparse_attention(q, cache: Kivi4Cache, n_groups: int, k_res, v_res, res_len: int,
+                           pages: np.ndarray, sm_scale: float, dtype=np.float64):
+    """Attention over the gathered tokens of the listed 16-token pages (page P =
+    tokens 16P .. 16P+15 of the quantized region; ids outside [0, 2 n_groups)
+    skipped, repeats kept) plus the residual window: the reference's
+    gather -> flash_attn_with_kvcache(causal=False) (S:1723-1772).
+    pages int [bs, Hkv, n_sel] -> out [bs, Hq, 128]."""
+    kh, vh = dequant_kivi4(Kivi4Cache(cache.k_codes[:, :, :n_groups],
+                                      cache.k_meta[:, :, :n_groups],
+                                      cache.v_codes[:, :, :n_groups],
+                                      cache.v_meta[:, :, :n_groups]), dtype=dtype)
+    bs, hq, d = q.shape
+    kv = kh.shape[1]
+    gqa = hq // kv
+    out = np.zeros((bs, hq, d), dtype=dtype)
+    for b in range(bs):
+        for h in range(kv):
+            p = np.asarray(pages[b, h]).astype(np.int64)
+            p = p[(p >= 0) & (p < 2 * n_groups)]
+            tok = (p[:, None] * 16 + np.arange(16)).reshape(-1)
+            k = np.concatenate([kh[b, h, tok], k_res[b, h, :res_len].astype(dtype)], axis=0)
+            v = np.concatenate([vh[b, h, tok], v_res[b, h, :res_len].astype(dtype)], axis=0)
+            if k.shape[0] == 0:
+                continue
+            out[b, h * gqa:(h + 1) * gqa] = attention(q[b:b + 1, h * gqa:(h + 1) * gqa], k[None, None],
+                                                      v[None, None], sm_scale, dtype=dtype)[0]
+    return out

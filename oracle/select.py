@@ -59,6 +59,31 @@ def quest_upper_bound_holds(q, keys_chunked, score) -> bool:
     return bool(np.all(score.astype(np.float64) >= exact - 1e-4 * (1 + np.abs(exact))))
 
 
+def f16_directed(x: np.ndarray, up: bool) -> np.ndarray:
+    """float32 -> fp16 bits rounded toward +inf (up) or -inf."""
+    x = f32(x)
+    with np.errstate(over="ignore"):
+        h = x.astype(np.float16)
+    hf = h.astype(np.float32)
+    bits = h.view(np.uint16).copy()
+    fix = (hf < x) if up else (hf > x)
+    fix &= ~np.isnan(x)
+    neg = (bits & 0x8000) != 0
+    zero = (bits & 0x7FFF) == 0
+    step_dn = np.where(neg == up, bits - 1, bits + 1).astype(np.uint16)   # away/toward zero per sign
+    step = np.where(zero, np.uint16(0x0001) if up else np.uint16(0x8001), step_dn).astype(np.uint16)
+    return np.where(fix, step, bits).astype(np.uint16)
+
+
+def page_minmax_f16(keys: np.ndarray, page: int = 16):
+    """Per-page per-channel min (rounded down) / max (rounded up) as fp16 bits.
+    keys [bs, kv, n_tok, 128] (bf16 values) -> [bs, kv, n_tok // page, 128] x2."""
+    bs, kv, n, d = keys.shape
+    n_pages = n // page
+    kp = f32(keys[:, :, :n_pages * page]).reshape(bs, kv, n_pages, page, d)
+    return f16_directed(kp.min(axis=3), False), f16_directed(kp.max(axis=3), True)
+
+
 # ---------------------------------------------------------------------------
 # Top-k
 # ---------------------------------------------------------------------------

@@ -1,0 +1,145 @@
+"""GPU parity of the C3 path: fp16 Quest page metadata (bit-exact), page-sparse
+4-bit decode attention (within 2e-3 of the oracle) and the planted-page
+select -> attend pipeline (selection equals the planted set)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import kivi as okivi
+from oracle import select as osel
+from tests.helpers import from_torch, gaussian_bf16, to_bf16
+
+pytestmark = pytest.mark.gpu
+
+ATOL = 2e-3
+
+
+def _bits16(t):
+    return from_torch(t.view(torch.int16)).view(np.uint16)
+
+
+def test_page_minmax_f16_bit_exact(rng):
+    from zoomkv_revision_amd.quest import page_minmax_f16
+    k = gaussian_bf16(rng, (2, 3, 40 * 16 + 5, 128), outlier_channels=3)
+    k[0, 1, 17, 9] = 2e5          # above fp16 max: max rounds to +inf, min of other pages unaffected
+    k[1, 2, 100, 4] = -7e-9       # below fp16 subnormals
+    k[1, 0, 33, 0] = 3.1e-6       # fp16 subnormal range: inexact, directed rounding matters
+    kt = to_bf16(np.ascontiguousarray(np.swapaxes(k, 1, 2))).transpose(1, 2)   # strided tokens
+    mn, mx = page_minmax_f16(kt, 16)
+    rmn, rmx = osel.page_minmax_f16(k, 16)
+    assert np.array_equal(_bits16(mn), rmn) and np.array_equal(_bits16(mx), rmx)
+
+
+def _pack(rng, bs, kv, ng):
+    from zoomkv_revision_amd import kivi
+    k = gaussian_bf16(rng, (bs, kv, ng * 32, 128), outlier_channels=1)
+    v = gaussian_bf16(rng, (bs, kv, ng * 32, 128), outlier_channels=1)
+    cache = kivi.Kivi4Cache.allocate(bs, kv, ng, 128)
+    kivi.kivi4_pack(to_bf16(k), to_bf16(v), cache, 0)
+    return okivi.quantize_kivi4(k, v), cache
+
+
+def _pages(rng, kind, bs, kv, ng, n_sel):
+    n_pages = 2 * ng
+    if kind == "sorted":
+        return np.sort(np.stack([[rng.choice(n_pages, n_sel, replace=False) for _ in range(kv)]
+                                 for _ in range(bs)]), -1)
+    if kind == "unsorted":
+        return np.stack([[rng.choice(n_pages, n_sel, replace=False) for _ in range(kv)] for _ in range(bs)])
+    if kind == "pairs":          # whole groups: every tile takes both halves
+        g = np.sort(np.stack([[rng.choice(ng, n_sel // 2, replace=False) for _ in range(kv)]
+                              for _ in range(bs)]), -1)
+        return np.stack([2 * g, 2 * g + 1], -1).reshape(bs, kv, -1)
+    if kind == "messy":          # duplicates, out-of-range ids, unsorted
+        p = rng.integers(-3, n_pages + 3, size=(bs, kv, n_sel))
+        p[..., 1] = p[..., 0]
+        return p
+    if kind == "all":
+        return np.broadcast_to(np.arange(n_pages), (bs, kv, n_pages)).copy()
+    raise ValueError(kind)
+
+
+@pytest.mark.parametrize("bs,hq,kv,ng,res,n_sel,kind,splits", [
+    (2, 32, 8, 40, 0, 24, "sorted", 0),
+    (2, 32, 8, 40, 50, 24, "unsorted", 0),
+    (1, 8, 2, 30, 0, 20, "pairs", 0),
+    (2, 8, 2, 30, 17, 40, "messy", 0),
+    (1, 8, 2, 12, 128, 24, "all", 0),
+    (1, 8, 2, 12, 0, 1, "sorted", 0),
+    (2, 8, 2, 20, 0, 16, "sorted", 1),
+    (1, 8, 2, 600, 0, 1100, "sorted", 1),   # > 512 tiles: the planner splits anyway
+])
+def test_sparse_attention_matches_oracle(rng, bs, hq, kv, ng, res, n_sel, kind, splits):
+    from zoomkv_revision_amd import kivi
+    ref_cache, cache = _pack(rng, bs, kv, ng)
+    kr = gaussian_bf16(rng, (bs, kv, 128, 128))
+    vr = gaussian_bf16(rng, (bs, kv, 128, 128))
+    cache.k_res.copy_(to_bf16(kr))
+    cache.v_res.copy_(to_bf16(vr))
+    q = gaussian_bf16(rng, (bs, hq, 128))
+    pages = _pages(rng, kind, bs, kv, ng, n_sel)
+    pt = torch.from_numpy(pages).cuda()
+    got = from_torch(kivi.kivi4_sparse_attention(to_bf16(q), cache, pt, ng, res, out_dtype=torch.float32,
+                                                 n_splits=splits))
+    ref = okivi.kivi4_sparse_attention(q, ref_cache, ng, kr, vr, res, pages, 1 / np.sqrt(128))
+    err = np.abs(got - ref).max()
+    assert err <= ATOL, f"max abs err {err}"
+    if kind == "all":
+        dense = from_torch(kivi.kivi4_decode_attention(to_bf16(q), cache, ng, res, out_dtype=torch.float32))
+        assert np.abs(got - dense).max() <= 1e-3
+
+
+def test_sparse_attention_empty_list_and_residual_only(rng):
+    from zoomkv_revision_amd import kivi
+    ref_cache, cache = _pack(rng, 1, 2, 4)
+    kr = gaussian_bf16(rng, (1, 2, 128, 128))
+    vr = gaussian_bf16(rng, (1, 2, 128, 128))
+    cache.k_res.copy_(to_bf16(kr))
+    cache.v_res.copy_(to_bf16(vr))
+    q = gaussian_bf16(rng, (1, 8, 128))
+    none = torch.full((1, 2, 3), -1, dtype=torch.int64, device="cuda")
+    got = from_torch(kivi.kivi4_sparse_attention(to_bf16(q), cache, none, 4, 33, out_dtype=torch.float32))
+    ref = okivi.kivi4_sparse_attention(q, ref_cache, 4, kr, vr, 33, -np.ones((1, 2, 3), int), 1 / np.sqrt(128))
+    assert np.abs(got - ref).max() <= ATOL
+    # nothing to attend: zeros (no NaN)
+    z = from_torch(kivi.kivi4_sparse_attention(to_bf16(q), cache, none, 4, 0, out_dtype=torch.float32))
+    assert np.all(z == 0)
+
+
+def test_c3_planted_pipeline_small(rng):
+    """GQA mean -> Quest over fp16 page metadata -> top-k pages -> sparse
+    attention, at a reduced C3 shape; the selection must be the planted set."""
+    from zoomkv_revision_amd import kivi, synthetic
+    from zoomkv_revision_amd.quest import quest_chunk_score
+    from zoomkv_revision_amd.topk import float_topk_3d
+    w = synthetic.c3_workload(7, 2, 32, 8, 4096, 24, "cuda", keep_keys=True)
+    bs, kv, n_pages = 2, 8, w["n_pages"]
+    scores = torch.empty(bs, kv, n_pages, device="cuda")
+    quest_chunk_score(w["raw_q"], w["page_min"], w["page_max"], scores, n_pages)
+    sel = float_topk_3d(scores, 24)
+    assert torch.equal(sel, w["planted"])
+    # scores: bit-exact against the oracle on the same metadata
+    f16 = lambda t: from_torch(t).view(np.float16).astype(np.float32)   # from_torch gives fp16 bits
+    ref_sc = osel.quest_chunk_score(from_torch(w["raw_q"]), f16(w["page_min"]), f16(w["page_max"]), n_pages)
+    assert np.array_equal(from_torch(scores).view(np.uint32), ref_sc.view(np.uint32))
+    out = from_torch(kivi.kivi4_sparse_attention(w["q"], w["cache"], sel, out_dtype=torch.float32))
+    ref_cache = okivi.quantize_kivi4(from_torch(w["k"]), from_torch(w["v"]))
+    z = np.zeros((bs, kv, 0, 128), np.float32)
+    ref = okivi.kivi4_sparse_attention(from_torch(w["q"]), ref_cache, 128, z, z, 0, from_torch(sel),
+                                       1 / np.sqrt(128))
+    assert np.abs(out - ref).max() <= ATOL
+
+
+def test_c3_full_size_selection_is_the_planted_set():
+    """BASELINE config 3 shape: batch 8, 32/8 heads, 32768 tokens = 2048 pages,
+    top-128 pages."""
+    from zoomkv_revision_amd import synthetic
+    from zoomkv_revision_amd.quest import quest_chunk_score
+    from zoomkv_revision_amd.topk import float_topk_3d
+    w = synthetic.c3_workload(42, 8, 32, 8, 32768, 128, "cuda")
+    scores = torch.empty(8, 8, 2048, device="cuda")
+    quest_chunk_score(w["raw_q"], w["page_min"], w["page_max"], scores, 2048)
+    assert torch.equal(float_topk_3d(scores, 128), w["planted"])
+    # margin of the planted construction: >= 5% between the sets
+    s = scores.sort(dim=-1, descending=True).values
+    assert bool((s[..., 127] >= 1.05 * s[..., 128]).all())

@@ -199,3 +199,69 @@ def test_estimate_tracks_inner_product_and_exact_rerank(rng):
     true16 = np.argsort(-exact, axis=-1)[:, :16]
     rec = np.mean([len(set(true16[i]) & set(cand[i])) / 16 for i in range(4)])
     assert rec >= 0.4
+
+
+# --------------------------- fp16 page metadata ----------------------------
+def test_f16_directed_rounding_is_tight_over_all_bf16():
+    from oracle.numerics import bf16_to_f32
+    x = bf16_to_f32(np.arange(65536, dtype=np.uint32).astype(np.uint16))
+    fin = np.isfinite(x)
+    x = x[fin]
+    dn = select.f16_directed(x, False).view(np.float16)
+    up = select.f16_directed(x, True).view(np.float16)
+    with np.errstate(over="ignore"):
+        assert np.all(dn.astype(np.float32) <= x) and np.all(up.astype(np.float32) >= x)
+        # tight: the next fp16 past each bound crosses x
+        nxt = np.nextafter(dn, np.float16(np.inf)).astype(np.float32)
+        prv = np.nextafter(up, np.float16(-np.inf)).astype(np.float32)
+    assert np.all(nxt[np.isfinite(dn)] > x[np.isfinite(dn)])
+    assert np.all(prv[np.isfinite(up)] < x[np.isfinite(up)])
+    # bf16 values inside fp16's normal range convert exactly
+    ok = (np.abs(x) >= 2.0 ** -14) & (np.abs(x) <= 65504)
+    assert np.array_equal(dn[ok].astype(np.float32), x[ok]) and np.array_equal(up[ok].astype(np.float32), x[ok])
+
+
+def test_page_minmax_brute_force(rng):
+    k = gaussian_bf16(rng, (1, 2, 48, 128))
+    k[0, 1, 5, 7] = 1e6                              # beyond fp16: max rounds up to +inf
+    k[0, 0, 20, 3] = -3e-9                           # below fp16 subnormals: min rounds down
+    mn, mx = select.page_minmax_f16(k, 16)
+    for h in range(2):
+        for p in range(3):
+            for d in (0, 3, 7, 127):
+                col = k[0, h, 16 * p:16 * p + 16, d]
+                lo, hi = np.float16(mn[0, h, p, d].view(np.float16)), np.float16(mx[0, h, p, d].view(np.float16))
+                assert float(lo) <= col.min() and float(hi) >= col.max()
+    assert np.isposinf(mx[0, 1, 0, 7].view(np.float16))
+    assert mn[0, 0, 1, 3].view(np.float16) < 0
+
+
+# --------------------------- sparse attention ------------------------------
+def test_sparse_attention_oracle_invariants(rng):
+    from oracle import kivi as okivi
+    bs, kv, hq, ng, res = 1, 2, 8, 6, 20
+    k = gaussian_bf16(rng, (bs, kv, ng * 32, 128), outlier_channels=2)
+    v = gaussian_bf16(rng, (bs, kv, ng * 32, 128))
+    cache = okivi.quantize_kivi4(k, v)
+    kr = gaussian_bf16(rng, (bs, kv, res, 128))
+    vr = gaussian_bf16(rng, (bs, kv, res, 128))
+    q = gaussian_bf16(rng, (bs, hq, 128))
+    sc = 1 / np.sqrt(128)
+    all_pages = np.broadcast_to(np.arange(2 * ng), (bs, kv, 2 * ng))
+    dense = okivi.kivi4_decode_attention(q, cache, ng, kr, vr, res, sc)
+    assert np.allclose(okivi.kivi4_sparse_attention(q, cache, ng, kr, vr, res, all_pages, sc), dense,
+                       atol=1e-12)
+    sub = np.array([[[0, 3, 4, 9], [11, 2, 5, 6]]])
+    a = okivi.kivi4_sparse_attention(q, cache, ng, kr, vr, res, sub, sc)
+    # order and out-of-range ids do not matter; without a residual window,
+    # listing every page twice does not either (all weights double)
+    b = okivi.kivi4_sparse_attention(q, cache, ng, kr, vr, res, sub[..., ::-1], sc)
+    assert np.allclose(a, b, atol=1e-12)
+    a0 = okivi.kivi4_sparse_attention(q, cache, ng, kr, vr, 0, sub, sc)
+    c0 = okivi.kivi4_sparse_attention(q, cache, ng, kr, vr, 0, np.concatenate([sub, sub, -sub - 1, sub + 99], -1), sc)
+    assert np.allclose(a0, c0, atol=1e-12)
+    # a single page equals dense attention over a cache truncated to that page
+    one = okivi.kivi4_sparse_attention(q, cache, ng, kr, vr, 0, np.zeros((1, 2, 1), int), sc)
+    kh, vh = okivi.dequant_kivi4(cache)
+    ref = okivi.attention(q, kh[:, :, :16], vh[:, :, :16], sc)
+    assert np.allclose(one, ref, atol=1e-12)

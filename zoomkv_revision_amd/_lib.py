@@ -46,6 +46,10 @@ SIGNATURES = {
     "zkv_kivi_qk_dense_sparse": (I32, [P, I64, I64, P, I64, I64, P, I64, I64, I32, P, P, I64, I64,
                                        I32, P, I64, I64, I32, I32, I32, P, P, I64, I64,
                                        I32, I32, I32, P]),
+    "zkv_page_minmax_f16": (I32, [P, I64, I64, I64, I32, I32, I32, I32, I32, P, P, P]),
+    "zkv_kivi4_sparse_attention_workspace_size": (SZ, [I32, I32, I32, I32, I32, I32]),
+    "zkv_kivi4_sparse_attention": (I32, [P, I64, I64, P, P, P, P, I32, P, P, I32, I32, I32, I32, I32,
+                                         I32, P, I64, I64, I32, F32, P, I32, I32, P, SZ, P]),
     "zkv_rabitq_encode": (I32, [P, I64, I64, P, P, P, P]),
     "zkv_rabitq_estimate": (I32, [P, P, P, P, I32, I32, I64, P, P]),
     "zkv_rabitq_search_workspace_size": (SZ, [I32, I32, I64, I32]),

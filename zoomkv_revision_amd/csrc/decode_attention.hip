@@ -65,6 +65,13 @@ struct AttnParams {
   float* ws_ml;    // [bs, kv, n_splits, gqa, 2]
   void* out;       // [bs, kv*gqa, 128], written directly when n_splits == 1
   int out_f32;
+  // page-sparse mode: quantized tile t of (b, kv) is Format Q group
+  // tile_group[bh * tile_cap + t] with halves tile_mask[...] (bit m = tokens
+  // 16m .. 16m+15 selected), tile_count[bh] tiles in all
+  const int32_t* tile_group;
+  const uint8_t* tile_mask;
+  const int32_t* tile_count;
+  int tile_cap;
 };
 
 // One pipeline stage = one 32-token tile as it sits in HBM:
@@ -196,7 +203,8 @@ __device__ __forceinline__ half8_t softmax_step(const float4_t S[2], float& m_ru
 // Tile compute from an LDS stage: K-MFMA, softmax, V-MFMA.
 __device__ __forceinline__ void compute_tile(const uint8_t* st, int lane, int c, int g,
                                              const half8_t qB[4], const NibbleConsts& nk,
-                                             float& m_run, float& l_run, float4_t O[8]) {
+                                             uint32_t half_mask, float& m_run, float& l_run,
+                                             float4_t O[8]) {
   const u32x4_t kq0 = ld16(st + 16 * lane);
   const u32x4_t kq1 = ld16(st + 1024 + 16 * lane);
   float4_t S[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
@@ -207,6 +215,9 @@ __device__ __forceinline__ void compute_tile(const uint8_t* st, int lane, int c,
     S[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(dequant8(kq0[s], ks, kz, nk), qB[s], S[0], 0, 0, 0);
     S[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(dequant8(kq1[s], ks, kz, nk), qB[s], S[1], 0, 0, 0);
   }
+  // S[m] holds tokens 16m + 4g + i: drop an unselected page (half)
+  if (!(half_mask & 1u)) S[0] = float4_t{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+  if (!(half_mask & 2u)) S[1] = float4_t{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
   const half8_t pb = softmax_step(S, m_run, l_run, O);
   const u32x4_t vq0 = ld16(st + 2048 + 16 * lane);
   const u32x4_t vq1 = ld16(st + 3072 + 16 * lane);
@@ -278,7 +289,7 @@ struct KernelShape {
   static constexpr int kWavesPerSimd = std::max(1, std::min(4, (kWgPerCu * NW) / 4));
 };
 
-template <int NW, int D>
+template <int NW, int D, bool kSparse>
 __global__ __launch_bounds__(64 * NW)
 __attribute__((amdgpu_waves_per_eu(KernelShape<NW, D>::kWavesPerSimd)))
 void kivi4_attn_kernel(const AttnParams p) {
@@ -289,20 +300,36 @@ void kivi4_attn_kernel(const AttnParams p) {
   const bool col_ok = c < p.gqa;
   const int64_t bh = static_cast<int64_t>(b) * p.kv + h;
 
-  const int n_tiles = p.n_groups + (p.res_len + kTile - 1) / kTile;
+  const int n_qt = kSparse ? p.tile_count[bh] : p.n_groups;  // quantized tiles of (b, kv)
+  const int n_tiles = n_qt + (p.res_len + kTile - 1) / kTile;
   const int T0 = split * p.tiles_per_split;
   const int T1 = min(T0 + p.tiles_per_split, n_tiles);
-  const int TQ = min(T1, p.n_groups);  // quantized tiles of this workgroup: [T0, TQ)
-  // this wave's quantized tiles: T0 + wave + NW*k, k < nq
+  const int TQ = min(T1, n_qt);  // quantized tiles of this workgroup: [T0, TQ)
+  // this wave's quantized tiles: T0 + wave + NW*k, k < nq (nq <= 64 in sparse mode)
   const int nq = TQ > T0 + wave ? (TQ - (T0 + wave) + NW - 1) / NW : 0;
   uint8_t (*ring)[kStageBytes] = smem[wave];
+  // sparse mode: lane k holds the group and half mask of this wave's tile k
+  int my_group = 0, my_mask = 3;
+  if constexpr (kSparse) {
+    if (lane < nq) {
+      const int64_t ti = bh * p.tile_cap + T0 + wave + NW * lane;
+      my_group = p.tile_group[ti];
+      my_mask = p.tile_mask[ti];
+    }
+  }
+  auto group_of = [&](int k) {
+    if constexpr (kSparse)
+      return __builtin_amdgcn_readlane(my_group, k);
+    else
+      return T0 + wave + NW * k;
+  };
 
   // Start the HBM stream before anything else.
   int issued = 0;
 #pragma unroll
   for (int k = 0; k < D - 1; ++k)
     if (issued < nq) {
-      issue_tile(p, bh, T0 + wave + NW * issued, lane, ring[issued % D]);
+      issue_tile(p, bh, group_of(issued), lane, ring[issued % D]);
       ++issued;
     }
 
@@ -332,16 +359,17 @@ void kivi4_attn_kernel(const AttnParams p) {
   // ---- quantized tiles through this wave's D-stage LDS ring ----
   for (int k = 0; k < nq; ++k) {
     if (issued < nq) {
-      issue_tile(p, bh, T0 + wave + NW * issued, lane, ring[issued % D]);
+      issue_tile(p, bh, group_of(issued), lane, ring[issued % D]);
       ++issued;
     }
+    const uint32_t half_mask = kSparse ? static_cast<uint32_t>(__builtin_amdgcn_readlane(my_mask, k)) : 3u;
     wait_tiles_in_flight(issued - 1 - k);
-    compute_tile(ring[k % D], lane, c, g, qB, nk, m_run, l_run, O);
+    compute_tile(ring[k % D], lane, c, g, qB, nk, half_mask, m_run, l_run, O);
   }
 
   // ---- bf16 residual tiles (at most r_cap / 32 of them, in the last split) ----
-  for (int t = max(T0, p.n_groups) + wave; t < T1; t += NW) {
-    const int base = (t - p.n_groups) * kTile;
+  for (int t = max(T0, n_qt) + wave; t < T1; t += NW) {
+    const int base = (t - n_qt) * kTile;
     residual_tile(p, bh, base, min(kTile, p.res_len - base), c, g, qB, m_run, l_run, O);
   }
 
@@ -423,6 +451,43 @@ __global__ __launch_bounds__(128) void kivi4_combine_kernel(const float* __restr
     reinterpret_cast<uint16_t*>(out)[oi] = f32_to_bf16_bits(r);
 }
 
+// Page list -> tiles for page-sparse attention.  Page P (16 tokens) is half
+// P & 1 of Format Q group P >> 1.  One wave per (b, kv): every listed page
+// starts a tile unless it is the odd half of a group whose even half is the
+// previous entry (then that tile takes both halves).  The tiles cover the
+// listed pages as a multiset: the result equals attention over the
+// concatenated tokens of the list (duplicates attended twice, as a gather
+// would); page ids outside [0, 2 * n_groups) are skipped.
+__global__ __launch_bounds__(64) void sparse_tiles_kernel(
+    const int64_t* __restrict__ pages, int64_t pg_sb, int64_t pg_sh, int n_sel, int kv, int n_groups,
+    int32_t* __restrict__ tile_group, uint8_t* __restrict__ tile_mask, int32_t* __restrict__ tile_count) {
+  const int bh = blockIdx.x;
+  const int b = bh / kv, h = bh - b * kv;
+  const int64_t* pg = pages + b * pg_sb + h * pg_sh;
+  const int lane = threadIdx.x;
+  const int64_t n_pages = 2ll * n_groups;
+  int base = 0;
+  for (int i0 = 0; i0 < n_sel; i0 += 64) {
+    const int i = i0 + lane;
+    const int64_t cur = i < n_sel ? pg[i] : -1;
+    const int64_t prev = (i > 0 && i < n_sel) ? pg[i - 1] : -1;
+    const int64_t next = (i + 1 < n_sel) ? pg[i + 1] : -1;
+    const bool valid = cur >= 0 && cur < n_pages;
+    const bool joins_prev = valid && (cur & 1) && prev == cur - 1;
+    const bool start = valid && !joins_prev;
+    const uint64_t m = __ballot(start);
+    const int rank = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
+                                               __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0));
+    if (start) {
+      const int64_t t = static_cast<int64_t>(bh) * n_sel + base + rank;
+      tile_group[t] = static_cast<int32_t>(cur >> 1);
+      tile_mask[t] = static_cast<uint8_t>((cur & 1) ? 2 : (next == cur + 1 ? 3 : 1));
+    }
+    base += __popcll(m);
+  }
+  if (lane == 0) tile_count[bh] = base;
+}
+
 struct SplitPlan {
   int n_splits, tiles_per_split;
 };
@@ -474,18 +539,58 @@ size_t workspace_bytes_for(int bs, int hq, int /*kv*/, int n_splits) {
 void launch_attn(const AttnParams& p, int bs, hipStream_t s) {
   const dim3 grid(p.n_splits, p.kv, bs);
   const Shape sh = attn_shape();
-  if (sh.nw == 8) {
-    kivi4_attn_kernel<8, 2><<<grid, 512, 0, s>>>(p);
+  if (p.tile_group != nullptr) {
+    kivi4_attn_kernel<8, 2, true><<<grid, 512, 0, s>>>(p);
+  } else if (sh.nw == 8) {
+    kivi4_attn_kernel<8, 2, false><<<grid, 512, 0, s>>>(p);
   } else if (sh.nw == 2) {
     if (sh.d == 4)
-      kivi4_attn_kernel<2, 4><<<grid, 128, 0, s>>>(p);
+      kivi4_attn_kernel<2, 4, false><<<grid, 128, 0, s>>>(p);
     else
-      kivi4_attn_kernel<2, 3><<<grid, 128, 0, s>>>(p);
+      kivi4_attn_kernel<2, 3, false><<<grid, 128, 0, s>>>(p);
   } else if (sh.d == 3) {
-    kivi4_attn_kernel<4, 3><<<grid, 256, 0, s>>>(p);
+    kivi4_attn_kernel<4, 3, false><<<grid, 256, 0, s>>>(p);
   } else {
-    kivi4_attn_kernel<4, 2><<<grid, 256, 0, s>>>(p);
+    kivi4_attn_kernel<4, 2, false><<<grid, 256, 0, s>>>(p);
   }
+}
+
+// Page list of the page-sparse mode (pages int64 [bs, kv, n_sel] at strides).
+struct SparsePages {
+  const int64_t* pages;
+  int64_t pg_sb, pg_sh;
+  int n_sel;
+};
+
+// Sparse-mode workspace tail after the split partials: tile groups int32,
+// tile masks uint8 (both [bs * kv, n_sel]) and tile counts int32 [bs * kv].
+struct SparseLayout {
+  size_t group, mask, count, total;
+};
+
+size_t align256(size_t b) { return (b + 255) & ~static_cast<size_t>(255); }
+
+SparseLayout sparse_layout(size_t partial_bytes, int bs, int kv, int n_sel) {
+  SparseLayout L;
+  const size_t units = static_cast<size_t>(bs) * kv;
+  L.group = align256(partial_bytes);
+  L.mask = L.group + align256(units * n_sel * 4);
+  L.count = L.mask + align256(units * n_sel);
+  L.total = L.count + align256(units * 4);
+  return L;
+}
+
+// Sparse mode: every split is planned for the longest page list (n_sel
+// tiles); each wave keeps at most 64 tile descriptors in its lanes.
+SplitPlan plan_sparse_splits(int bs, int kv, int n_sel, int res_len, int n_splits) {
+  SplitPlan sp = plan_splits(bs, kv, n_sel, res_len, n_splits);
+  constexpr int kMaxPerSplit = 64 * 8;
+  if (sp.tiles_per_split > kMaxPerSplit) {
+    const int n_tiles = n_sel + (res_len + kTile - 1) / kTile;
+    sp.n_splits = (n_tiles + kMaxPerSplit - 1) / kMaxPerSplit;
+    sp.tiles_per_split = (n_tiles + sp.n_splits - 1) / sp.n_splits;
+  }
+  return sp;
 }
 
 int attention_launch(const uint16_t* q, int64_t q_sb, int64_t q_sh, const int32_t* k_codes,
@@ -493,7 +598,7 @@ int attention_launch(const uint16_t* q, int64_t q_sb, int64_t q_sh, const int32_
                      int g_cap, const uint16_t* k_res, const uint16_t* v_res, int r_cap, int bs,
                      int hq, int kv, int n_groups, int res_len, float sm_scale, int n_splits,
                      void* workspace, size_t workspace_bytes, int* n_splits_used, void* out,
-                     int out_f32, hipStream_t s) {
+                     int out_f32, hipStream_t s, const SparsePages* sparse = nullptr) {
   ZKV_REQUIRE(q && workspace, "zkv_kivi4_attention: null pointer");
   ZKV_REQUIRE(bs > 0 && kv > 0 && hq > 0 && hq % kv == 0,
               "zkv_kivi4_attention: bad heads bs=%d hq=%d kv=%d", bs, hq, kv);
@@ -503,7 +608,7 @@ int attention_launch(const uint16_t* q, int64_t q_sb, int64_t q_sh, const int32_
               n_groups, g_cap);
   ZKV_REQUIRE(res_len >= 0 && res_len <= r_cap, "zkv_kivi4_attention: res_len=%d r_cap=%d",
               res_len, r_cap);
-  ZKV_REQUIRE(n_groups + res_len > 0, "zkv_kivi4_attention: empty context");
+  ZKV_REQUIRE(sparse != nullptr || n_groups + res_len > 0, "zkv_kivi4_attention: empty context");
   ZKV_REQUIRE(n_groups == 0 || (k_codes && k_meta && v_codes && v_meta),
               "zkv_kivi4_attention: null cache pointer");
   ZKV_REQUIRE(res_len == 0 || (k_res && v_res), "zkv_kivi4_attention: null residual pointer");
@@ -511,8 +616,15 @@ int attention_launch(const uint16_t* q, int64_t q_sb, int64_t q_sh, const int32_
               "zkv_kivi4_attention: q rows must be 16-byte aligned");
   ZKV_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 15) == 0,
               "zkv_kivi4_attention: workspace must be 16-byte aligned");
-  const SplitPlan sp = plan_splits(bs, kv, n_groups, res_len, n_splits);
-  const size_t need = workspace_bytes_for(bs, hq, kv, sp.n_splits);
+  if (sparse) {
+    ZKV_REQUIRE(sparse->n_sel >= 0 && (sparse->n_sel == 0 || sparse->pages),
+                "zkv_kivi4_sparse_attention: bad page list (n_sel=%d)", sparse->n_sel);
+    ZKV_REQUIRE(g_cap <= (1 << 30), "zkv_kivi4_sparse_attention: g_cap=%d too large", g_cap);
+  }
+  const SplitPlan sp = sparse ? plan_sparse_splits(bs, kv, sparse->n_sel, res_len, n_splits)
+                              : plan_splits(bs, kv, n_groups, res_len, n_splits);
+  const size_t partial = workspace_bytes_for(bs, hq, kv, sp.n_splits);
+  const size_t need = sparse ? sparse_layout(partial, bs, kv, sparse->n_sel).total : partial;
   if (workspace_bytes < need)
     return fail(ZKV_ESPACE, "zkv_kivi4_attention: workspace %zu < %zu bytes", workspace_bytes, need);
   AttnParams p;
@@ -538,6 +650,25 @@ int attention_launch(const uint16_t* q, int64_t q_sb, int64_t q_sh, const int32_
   p.ws_ml = p.ws_o + static_cast<size_t>(bs) * hq * sp.n_splits * 128;
   p.out = out;
   p.out_f32 = out_f32;
+  p.tile_group = nullptr;
+  p.tile_mask = nullptr;
+  p.tile_count = nullptr;
+  p.tile_cap = 0;
+  if (sparse) {
+    const SparseLayout L = sparse_layout(partial, bs, kv, sparse->n_sel);
+    uint8_t* ws = static_cast<uint8_t*>(workspace);
+    int32_t* tg = reinterpret_cast<int32_t*>(ws + L.group);
+    uint8_t* tm = ws + L.mask;
+    int32_t* tc = reinterpret_cast<int32_t*>(ws + L.count);
+    sparse_tiles_kernel<<<bs * kv, 64, 0, s>>>(sparse->pages, sparse->pg_sb, sparse->pg_sh, sparse->n_sel,
+                                              kv, n_groups, tg, tm, tc);
+    const int rc = check_launch("sparse_tiles_kernel");
+    if (rc) return rc;
+    p.tile_group = tg;
+    p.tile_mask = tm;
+    p.tile_count = tc;
+    p.tile_cap = sparse->n_sel;
+  }
   if (n_splits_used) *n_splits_used = sp.n_splits;
   launch_attn(p, bs, s);
   int rc = check_launch("kivi4_attn_kernel");
@@ -597,4 +728,30 @@ extern "C" int zkv_kivi4_decode_attention(const uint16_t* q, int64_t q_sb, int64
                           r_cap, bs, hq, kv, n_groups, res_len, sm_scale, n_splits, workspace,
                           workspace_bytes, nullptr, out, out_f32,
                           reinterpret_cast<hipStream_t>(stream));
+}
+
+// ---- page-sparse mode -----------------------------------------------------
+
+extern "C" size_t zkv_kivi4_sparse_attention_workspace_size(int bs, int hq, int kv, int n_sel,
+                                                            int res_len, int n_splits) {
+  if (bs <= 0 || kv <= 0 || hq <= 0 || n_sel < 0) return 0;
+  const SplitPlan sp = plan_sparse_splits(bs, kv, n_sel, res_len, n_splits);
+  return sparse_layout(workspace_bytes_for(bs, hq, kv, sp.n_splits), bs, kv, n_sel).total;
+}
+
+extern "C" int zkv_kivi4_sparse_attention(const uint16_t* q, int64_t q_sb, int64_t q_sh,
+                                          const int32_t* k_codes, const uint16_t* k_meta,
+                                          const int32_t* v_codes, const uint16_t* v_meta, int g_cap,
+                                          const uint16_t* k_res, const uint16_t* v_res, int r_cap,
+                                          int bs, int hq, int kv, int n_groups, int res_len,
+                                          const int64_t* pages, int64_t pg_sb, int64_t pg_sh,
+                                          int n_sel, float sm_scale, void* out, int out_f32,
+                                          int n_splits, void* workspace, size_t workspace_bytes,
+                                          zkv_stream_t stream) {
+  ZKV_REQUIRE(out, "zkv_kivi4_sparse_attention: null output");
+  const SparsePages sp{pages, pg_sb, pg_sh, n_sel};
+  return attention_launch(q, q_sb, q_sh, k_codes, k_meta, v_codes, v_meta, g_cap, k_res, v_res,
+                          r_cap, bs, hq, kv, n_groups, res_len, sm_scale, n_splits, workspace,
+                          workspace_bytes, nullptr, out, out_f32,
+                          reinterpret_cast<hipStream_t>(stream), &sp);
 }

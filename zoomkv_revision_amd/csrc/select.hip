@@ -334,6 +334,45 @@ __global__ __launch_bounds__(256) void kivi_qk_kernel(
   }
 }
 
+// ----------------------------------------------------------------------------
+// Per-page fp16 min / max of bf16 keys (the Quest metadata of a paged cache,
+// the fp16 counterpart of _compute_and_store_chunk_minmax's amin / amax,
+// S:2025-2157).  min is rounded toward -inf and max toward +inf, so the
+// Quest score stays an upper bound (every bf16 value inside fp16's normal
+// range converts exactly).  Thread per channel, block per (page, kv, b).
+// ----------------------------------------------------------------------------
+__device__ __forceinline__ uint16_t f16_step(uint16_t h, bool up) {
+  // next fp16 toward +inf (up) or -inf, for finite non-NaN h
+  const bool neg = (h & 0x8000u) != 0;
+  if ((h & 0x7FFFu) == 0) return up ? 0x0001u : 0x8001u;
+  return static_cast<uint16_t>((neg == up) ? h - 1 : h + 1);
+}
+
+__device__ __forceinline__ uint16_t f16_round_dir(float x, bool up) {
+  const _Float16 r = static_cast<_Float16>(x);
+  const float rf = static_cast<float>(r);
+  uint16_t h = __builtin_bit_cast(uint16_t, r);
+  if (x != x) return h;
+  if (up ? (rf < x) : (rf > x)) h = f16_step(h, up);
+  return h;
+}
+
+__global__ __launch_bounds__(128) void page_minmax_f16_kernel(
+    const uint16_t* __restrict__ keys, int64_t k_sb, int64_t k_sh, int64_t k_st, int page,
+    int n_pages_max, uint16_t* __restrict__ pmin, uint16_t* __restrict__ pmax) {
+  const int pg = blockIdx.x, h = blockIdx.y, b = blockIdx.z, ch = threadIdx.x;
+  const uint16_t* k = keys + b * k_sb + h * k_sh + static_cast<int64_t>(pg) * page * k_st + ch;
+  float mn = bf16_to_f32(k[0]), mx = mn;
+  for (int t = 1; t < page; ++t) {
+    const float v = bf16_to_f32(k[t * k_st]);
+    mn = fminf(mn, v);
+    mx = fmaxf(mx, v);
+  }
+  const int64_t o = ((static_cast<int64_t>(b) * gridDim.y + h) * n_pages_max + pg) * 128 + ch;
+  pmin[o] = f16_round_dir(mn, false);
+  pmax[o] = f16_round_dir(mx, true);
+}
+
 }  // namespace
 }  // namespace zkv
 
@@ -444,4 +483,18 @@ extern "C" int zkv_kivi_qk_dense_sparse(const int64_t* chunk_ids, int64_t id_sb,
                                            out_indices, o_sb, o_sh, nk, dense_topk, sparse_topk);
   }
   return check_launch("kivi_qk_kernel");
+}
+
+extern "C" int zkv_page_minmax_f16(const uint16_t* keys, int64_t k_sb, int64_t k_sh, int64_t k_st,
+                                   int bs, int kv, int page_size, int n_pages, int n_pages_max,
+                                   uint16_t* page_min, uint16_t* page_max, zkv_stream_t stream) {
+  ZKV_REQUIRE(keys && page_min && page_max, "zkv_page_minmax_f16: null pointer");
+  ZKV_REQUIRE(bs > 0 && kv > 0 && kv <= 65535 && bs <= 65535 && page_size > 0 && n_pages >= 0 &&
+                  n_pages <= n_pages_max,
+              "zkv_page_minmax_f16: bad sizes bs=%d kv=%d page=%d n_pages=%d n_pages_max=%d", bs, kv,
+              page_size, n_pages, n_pages_max);
+  if (n_pages == 0) return ZKV_OK;
+  page_minmax_f16_kernel<<<dim3(n_pages, kv, bs), 128, 0, reinterpret_cast<hipStream_t>(stream)>>>(
+      keys, k_sb, k_sh, k_st, page_size, n_pages_max, page_min, page_max);
+  return check_launch("page_minmax_f16_kernel");
 }

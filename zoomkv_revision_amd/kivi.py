@@ -203,6 +203,57 @@ def kivi4_decode_attention(q: torch.Tensor, cache: Kivi4Cache, n_groups: int | N
     return out.unsqueeze(1) if squeeze else out
 
 
+def kivi4_sparse_attention(q: torch.Tensor, cache: Kivi4Cache, pages: torch.Tensor,
+                           n_groups: int | None = None, res_len: int | None = None,
+                           sm_scale: float | None = None, out: torch.Tensor | None = None,
+                           out_dtype: torch.dtype | None = None, n_splits: int = 0,
+                           workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """Decode attention of q (bf16 [bs, hq, 128] or [bs, 1, hq, 128]) over the
+    16-token pages listed in ``pages`` (int64 [bs, kv, n_sel]; page P = tokens
+    16P .. 16P+15 of the quantized region) plus the bf16 residual window:
+    the result of gathering those tokens and attending over them
+    (S:1723-1772 after the Quest pick of S:2195-2240).  Sorted page lists let
+    both halves of a 32-token group share one tile."""
+    require_gpu(q, pages)
+    _check_bf16("q", q)
+    squeeze = q.dim() == 4
+    if squeeze and q.shape[1] != 1:
+        raise ValueError("decode attention takes one query token per sequence")
+    q3 = q[:, 0] if squeeze else q
+    _check_last_contig("q", q3)
+    bs, hq, _ = q3.shape
+    kbs, kv = cache.shape
+    if kbs != bs or hq % kv != 0:
+        raise ValueError(f"q {tuple(q.shape)} does not match cache (bs={kbs}, kv={kv})")
+    if pages.dtype != torch.int64 or pages.dim() != 3 or tuple(pages.shape[:2]) != (bs, kv):
+        raise ValueError("pages must be int64 [bs, kv, n_sel]")
+    if pages.shape[2] > 1 and pages.stride(2) != 1:
+        pages = pages.contiguous()
+    n_sel = pages.shape[2]
+    n_groups = cache.n_groups if n_groups is None else int(n_groups)
+    res_len = cache.res_len if res_len is None else int(res_len)
+    sm_scale = 1.0 / math.sqrt(HEAD_DIM) if sm_scale is None else float(sm_scale)
+    out_dtype = q.dtype if out_dtype is None else out_dtype
+    if out_dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"out_dtype must be bfloat16 or float32; got {out_dtype}")
+    if out is None:
+        out = torch.empty(bs, hq, HEAD_DIM, dtype=out_dtype, device=q.device)
+    elif out.dtype != out_dtype or not out.is_contiguous() or out.numel() != bs * hq * HEAD_DIM:
+        raise ValueError("out must be a contiguous [bs, hq, 128] tensor of out_dtype")
+    L = lib()
+    need = L.zkv_kivi4_sparse_attention_workspace_size(bs, hq, kv, n_sel, res_len, n_splits)
+    ws = _workspace(q.device, need) if workspace is None else workspace
+    check(L.zkv_kivi4_sparse_attention(
+        ptr(q3), q3.stride(0), q3.stride(1),
+        ptr(cache.k_codes), ptr(cache.k_meta), ptr(cache.v_codes), ptr(cache.v_meta), cache.g_cap,
+        ptr(cache.k_res), ptr(cache.v_res), cache.r_cap,
+        bs, hq, kv, n_groups, res_len, ptr(pages), pages.stride(0), pages.stride(1), n_sel, sm_scale,
+        ptr(out), int(out_dtype == torch.float32), n_splits,
+        ptr(ws), ws.numel() * ws.element_size(), stream_of(q)))
+    out = out.view(bs, hq, HEAD_DIM)
+    return out.unsqueeze(1) if squeeze else out
+
+
 def kivi4_attention_partial(q: torch.Tensor, cache: Kivi4Cache, n_groups: int, res_len: int,
                             sm_scale: float | None = None, n_splits: int = 0,
                             workspace: torch.Tensor | None = None):

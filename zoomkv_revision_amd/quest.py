@@ -48,6 +48,35 @@ def quest_chunk_score(q: torch.Tensor, chunk_min: torch.Tensor, chunk_max: torch
         bs, kv, n_chunks, n_max, ptr(valid), stream_of(q)))
 
 
+def page_minmax_f16(keys: torch.Tensor, page_size: int = 16, n_pages: int | None = None,
+                    page_min: torch.Tensor | None = None, page_max: torch.Tensor | None = None):
+    """Per-page fp16 (min rounded down, max rounded up) of bf16 keys
+    [bs, kv, n_tok, 128] (any strides with a contiguous last dim).
+
+    Returns (page_min, page_max) fp16 [bs, kv, n_pages_max, 128]; pages
+    [0, n_pages) are written (default n_tok // page_size).
+    """
+    require_gpu(keys)
+    if keys.dtype != torch.bfloat16 or keys.dim() != 4 or keys.shape[-1] != 128 or keys.stride(-1) != 1:
+        raise RuntimeError("keys must be bf16 [bs, kv, n_tok, 128] with a contiguous last dim")
+    bs, kv, n_tok, _ = keys.shape
+    n_pages = n_tok // page_size if n_pages is None else int(n_pages)
+    if n_pages * page_size > n_tok:
+        raise RuntimeError(f"{n_pages} pages of {page_size} exceed {n_tok} tokens")
+    if page_min is None:
+        page_min = torch.empty(bs, kv, n_pages, 128, dtype=torch.float16, device=keys.device)
+    if page_max is None:
+        page_max = torch.empty_like(page_min)
+    for t in (page_min, page_max):
+        if t.dtype != torch.float16 or not t.is_contiguous() or t.shape[:2] != (bs, kv) or t.shape[3] != 128:
+            raise RuntimeError("page_min / page_max must be contiguous fp16 [bs, kv, n_pages_max, 128]")
+    n_max = page_min.shape[2]
+    check(lib().zkv_page_minmax_f16(ptr(keys), keys.stride(0), keys.stride(1), keys.stride(2), bs, kv,
+                                    page_size, n_pages, n_max, ptr(page_min), ptr(page_max),
+                                    stream_of(keys)))
+    return page_min, page_max
+
+
 class QuestKernel:
     """Drop-in for the module ``quest_ops.load_kernel_module()`` returns."""
 
