@@ -13,6 +13,10 @@ previous step's data from cache.
 Prints one JSON line (the driver's contract) with the roofline of the main
 kernel (HIP events on the launch stream over the timed region) and the CPU
 baseline (the numpy oracle, one host thread, on a bounded sample).
+
+``--config c3`` (Quest page selection + page-sparse attention) and
+``--config c4`` (RaBitQ search) print the same kind of line for the other
+GPU configurations; the default is the headline configuration, C2.
 """
 from __future__ import annotations
 
@@ -37,27 +41,8 @@ METRIC = "decode attn tokens/s + achieved HBM GB/s (% peak), 4-bit KV, 32k ctx, 
 
 
 def make_cache(seed: int, device):
-    import torch
-    from zoomkv_revision_amd import kivi
-    g = torch.Generator(device=device)
-    g.manual_seed(seed)
-    cache = kivi.Kivi4Cache.allocate(B, HKV, NG, R, device=device)
-    n = NG * 32
-    n_out = max(1, round(0.01 * D))
-    for b in range(B):
-        k = torch.randn(HKV, n, D, generator=g, device=device, dtype=torch.float32)
-        v = torch.randn(HKV, n, D, generator=g, device=device, dtype=torch.float32)
-        for h in range(HKV):
-            ch = torch.randperm(D, generator=g, device=device)[:n_out]
-            k[h, :, ch] *= 10.0
-        view = kivi.Kivi4Cache(cache.k_codes[b:b + 1], cache.k_meta[b:b + 1], cache.v_codes[b:b + 1],
-                               cache.v_meta[b:b + 1], cache.k_res[b:b + 1], cache.v_res[b:b + 1])
-        kivi.kivi4_pack(k.to(torch.bfloat16)[None], v.to(torch.bfloat16)[None], view, 0)
-        del k, v
-    cache.k_res.copy_(torch.randn(B, HKV, R, D, generator=g, device=device).to(torch.bfloat16))
-    cache.v_res.copy_(torch.randn(B, HKV, R, D, generator=g, device=device).to(torch.bfloat16))
-    cache.n_groups, cache.res_len = NG, R
-    return cache
+    from zoomkv_revision_amd import synthetic
+    return synthetic.c2_cache(seed, B, HKV, NG, R, device)
 
 
 def cpu_baseline(cache, q, budget_s: float = 12.0):
@@ -99,12 +84,203 @@ def read_traffic():
         return None
 
 
+def timed_loop(step, steps: int, warmup: int):
+    """Warm up, then time `steps` calls of step(i, ev) bracketed by device
+    synchronisation; ev = a pair of events the step records around its
+    dominant kernel.  Returns (ms per step, mean dominant-kernel ms)."""
+    import torch
+    for i in range(warmup):
+        step(i, None)
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        step(i, events[i])
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    return ms, statistics.mean(a.elapsed_time(b) for a, b in events)
+
+
+def run_c3(args):
+    """C3: GQA-mean query -> Quest bounds over fp16 page metadata (2048 pages of
+    16 tokens) -> top-128 pages -> page-sparse 4-bit attention, batch 8,
+    32/8 heads, 32768 tokens; six planted workloads rotate between steps."""
+    import numpy as np
+    import torch
+    from zoomkv_revision_amd import kivi, synthetic
+    from zoomkv_revision_amd.quest import quest_chunk_score
+    from zoomkv_revision_amd.rerank import gqa_mean_query
+    from zoomkv_revision_amd.topk import float_topk_3d
+    bs, hq, kv, n_tok, n_sel = 8, 32, 8, 32768, 128
+    dev = torch.device("cuda:0")
+    ws = [synthetic.c3_workload(100 + i, bs, hq, kv, n_tok, n_sel, dev) for i in range(6)]
+    n_pages = ws[0]["n_pages"]
+    scores = torch.empty(bs, kv, n_pages, device=dev)
+    raw_q = torch.empty(bs, kv, 128, dtype=torch.bfloat16, device=dev)
+    out = torch.empty(bs, hq, 128, dtype=torch.bfloat16, device=dev)
+    sel_ok = []
+
+    def step(i, ev):
+        w = ws[i % len(ws)]
+        gqa_mean_query(w["q"], kv, out=raw_q)
+        if ev is not None:
+            ev[0].record()
+        quest_chunk_score(raw_q, w["page_min"], w["page_max"], scores, n_pages)
+        if ev is not None:
+            ev[1].record()
+        sel = float_topk_3d(scores, n_sel)
+        kivi.kivi4_sparse_attention(w["q"], w["cache"], sel, out=out)
+        if i < len(ws):
+            sel_ok.append(sel)
+
+    ms, k_ms = timed_loop(step, args.steps, args.warmup)
+    exact = all(torch.equal(s, ws[j]["planted"]) for j, s in enumerate(sel_ok[:len(ws)]))
+    nb = synthetic.c3_algorithmic_bytes(bs, hq, kv, n_pages, n_sel)
+    achieved = nb["quest"] / (k_ms * 1e-3) / 1e9
+    cpu = None
+    if not args.no_cpu:
+        cpu = c3_cpu_baseline(ws[0], n_sel)
+    return {
+        "metric": "C3 Quest page select + sparse 4-bit attention: decode tokens/s",
+        "value": bs / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "fp16 metadata / u4->fp16 (fp32 accumulate)",
+        "data": "synthetic (planted pages)",
+        "config": {"workload": "C3: GQA mean -> Quest (fp16 page min/max) -> top-128 of 2048 pages -> "
+                               "page-sparse 4-bit attention", "batch": bs, "q_heads": hq,
+                   "kv_heads": kv, "context": n_tok, "page_tokens": 16, "pages_selected": n_sel,
+                   "parallelism": "single GPU"},
+        "selection_equals_planted": exact,
+        "end_to_end_GBps": nb["total"] / (ms * 1e-3) / 1e9,
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel": "quest_score_kernel",
+                     "kernel_ms": k_ms, "algorithmic_bytes": nb["quest"]},
+        "algorithmic_bytes_per_step": nb,
+        "cpu_baseline": cpu,
+    }
+
+
+def c3_cpu_baseline(w, n_sel, budget_s: float = 10.0):
+    """numpy oracle of the C3 step (Quest bounds, top-k, dequant + sparse
+    attention) for one (batch, kv head) of the 64, one thread."""
+    import numpy as np
+    import torch
+    from threadpoolctl import threadpool_limits
+    from oracle import kivi as okivi
+    from oracle import select as osel
+    f16 = lambda t: t.cpu().view(torch.int16).numpy().view(np.uint16).view(np.float16).astype(np.float32)
+    raw_q = w["raw_q"][:1, :1].float().cpu().numpy()
+    pmin, pmax = f16(w["page_min"][:1, :1]), f16(w["page_max"][:1, :1])
+    c = w["cache"]
+    c0 = okivi.Kivi4Cache(c.k_codes[:1, :1].cpu().numpy(),
+                          c.k_meta[:1, :1].cpu().view(torch.int16).numpy().view(np.uint16),
+                          c.v_codes[:1, :1].cpu().numpy(),
+                          c.v_meta[:1, :1].cpu().view(torch.int16).numpy().view(np.uint16))
+    q = w["q"][:1, :4].float().cpu().numpy()
+    z = np.zeros((1, 1, 0, 128), np.float32)
+    times = []
+    with threadpool_limits(limits=1):
+        t_end = time.perf_counter() + budget_s
+        while time.perf_counter() < t_end or len(times) < 2:
+            t0 = time.perf_counter()
+            sc = osel.quest_chunk_score(raw_q, pmin, pmax, pmin.shape[2])
+            sel = osel.topk_indices(sc, n_sel)
+            okivi.kivi4_sparse_attention(q, c0, c0.k_codes.shape[2], z, z, 0, sel, 1 / np.sqrt(128),
+                                         dtype=np.float32)
+            times.append(time.perf_counter() - t0)
+            if len(times) >= 20:
+                break
+    t = statistics.median(times)
+    units = 8 * 8
+    return {"value": 8 / (t * units), "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"numpy oracle of one (batch, kv head) of {units}: Quest bounds over 2048 pages, "
+                      f"top-{n_sel}, dequant + float32 attention of 4 query heads; median of "
+                      f"{len(times)} calls ({t * 1e3:.0f} ms each), scaled to the batch of 8; "
+                      f"host {os.cpu_count()} logical CPUs, 1 used"}
+
+
+def run_c4(args):
+    """C4: RaBitQ search, 131072 clustered unit keys (16-byte sign codes + fp16
+    factors), 64 queries, top-256 by estimate, exact fp16 rerank; 80 key pools
+    rotate between steps (each pass reads ~7 MB, below the 256 MB MALL)."""
+    import torch
+    from zoomkv_revision_amd import rabitq, synthetic
+    n, nq, topk, n_pools = 131072, 64, 256, 80
+    dev = torch.device("cuda:0")
+    signs = rabitq.srht_signs(42, dev)
+    pools = []
+    for i in range(n_pools):
+        keys = synthetic.c4_keys(1000 + i, n, 64, dev)
+        codes, fac = rabitq.rabitq_encode(keys, signs)
+        pools.append((keys, codes, fac))
+    qs = synthetic.c4_keys(7, nq, 64, dev)
+    ws = rabitq.search_workspace(1, nq, n, topk, dev)
+
+    def step(i, ev):
+        keys, codes, fac = pools[i % n_pools]
+        if ev is not None:
+            ev[0].record()
+        rabitq.rabitq_search(qs, keys, codes, fac, signs, topk, workspace=ws)
+        if ev is not None:
+            ev[1].record()
+
+    ms, k_ms = timed_loop(step, args.steps, args.warmup)
+    algo = n * 20 + nq * topk * 256 + nq * 128 * 2 + nq * topk * 20
+    achieved = algo / (k_ms * 1e-3) / 1e9
+    cpu = None if args.no_cpu else c4_cpu_baseline(pools[0], qs, signs, topk)
+    return {
+        "metric": "C4 RaBitQ 1-bit search: queries/s (top-256 of 131072 + exact rerank)",
+        "value": nq / (ms * 1e-3), "unit": "queries/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "u1 codes (popcount) + fp16 rerank (fp32 accumulate)",
+        "data": "synthetic (seeded unit-norm clusters)",
+        "config": {"workload": "C4: encode queries -> estimate + exact top-256 -> fp16 rerank",
+                   "keys": n, "queries": nq, "topk": topk, "clusters": 64, "pools_rotated": n_pools,
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "kernel": "rabitq_search (encode + stage 1 + stage 2)", "kernel_ms": k_ms,
+                     "algorithmic_bytes": algo},
+        "cpu_baseline": cpu,
+    }
+
+
+def c4_cpu_baseline(pool, qs, signs, topk, budget_s: float = 10.0):
+    import numpy as np
+    import torch
+    from threadpoolctl import threadpool_limits
+    from oracle import rabitq as orq
+    keys, codes, fac = pool
+    kb = keys.cpu().view(torch.int16).numpy().view(np.uint16)
+    cb = codes.cpu().numpy()
+    fb = fac.cpu().view(torch.int16).numpy().view(np.uint16)
+    qb = qs[:4].cpu().view(torch.int16).numpy().view(np.uint16)
+    s = signs.cpu().numpy()
+    times = []
+    with threadpool_limits(limits=1):
+        t_end = time.perf_counter() + budget_s
+        while time.perf_counter() < t_end or len(times) < 2:
+            t0 = time.perf_counter()
+            orq.search(qb, kb, cb, fb, s, topk)
+            times.append(time.perf_counter() - t0)
+            if len(times) >= 20:
+                break
+    t = statistics.median(times)
+    return {"value": 4 / t, "unit": "queries/s", "cores": 1, "kind": "port",
+            "sample": f"numpy oracle search (encode, estimate over 131072 keys, top-{topk}, exact "
+                      f"rerank) for 4 of the 64 queries per call; median of {len(times)} calls "
+                      f"({t * 1e3:.0f} ms each); host {os.cpu_count()} logical CPUs, 1 used"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--splits", type=int, default=0)
+    ap.add_argument("--config", choices=["c2", "c3", "c4"], default="c2",
+                    help="c2 (default, the headline line), c3 or c4")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run 5 device copies of 1 GiB (scale reference for rocprof "
@@ -119,6 +295,9 @@ def main():
     from zoomkv_revision_amd import kivi
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.config != "c2":
+        print(json.dumps(run_c3(args) if args.config == "c3" else run_c4(args)))
+        return
     if args.calibrate_copy:
         src = torch.ones(1 << 28, dtype=torch.float32, device=dev)      # 1 GiB
         dst = torch.empty_like(src)
