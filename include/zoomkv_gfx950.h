@@ -226,6 +226,26 @@ int zkv_kivi4_sparse_attention(const uint16_t* q, int64_t q_sb, int64_t q_sh, co
                                int out_f32, int n_splits, void* workspace, size_t workspace_bytes,
                                zkv_stream_t stream);
 
+/* Decode attention over bf16 K / V caches k, v [bs, n, kv, 128] at element
+ * strides (sb = batch, st = token, sh = head; rows 16-byte aligned), causal
+ * off, GQA hq = kv * gqa: the flash_attn_with_kvcache call of
+ * flash_attn_with_kvcache_compat (Z/attn_hub/flash_attn_compat.py:44-100; call
+ * sites S:1742-1747, S:1767-1772).  out bf16 or fp32 [bs, hq, 128]; lse
+ * (optional, NULL to skip) fp32 [bs, hq] natural-log LSE of the scaled
+ * scores, the layout of flash-attn's softmax_lse. */
+size_t zkv_bf16_attention_workspace_size(int bs, int hq, int kv, int n, int n_splits);
+int zkv_bf16_decode_attention(const uint16_t* q, int64_t q_sb, int64_t q_sh, const uint16_t* k,
+                              int64_t k_sb, int64_t k_st, int64_t k_sh, const uint16_t* v,
+                              int64_t v_sb, int64_t v_st, int64_t v_sh, int bs, int hq, int kv, int n,
+                              float sm_scale, void* out, int out_f32, float* lse, int n_splits,
+                              void* workspace, size_t workspace_bytes, zkv_stream_t stream);
+
+/* LSE merge of two attention outputs [bs, 1, heads, dim] (contiguous, dtype 0
+ * bf16 / 1 fp16 / 2 fp32) with fp32 natural-log LSEs [bs, heads]:
+ * lse_merge_torch / lse_merge_cuda (Z/cache_hub/lse_merge/lse_merge.py:79-149). */
+int zkv_lse_merge(const void* out_a, const float* lse_a, const void* out_b, const float* lse_b,
+                  void* out, int dtype, int bs, int heads, int dim, zkv_stream_t stream);
+
 /* ---- RaBitQ 1-bit sign codes -------------------------------------------------
  * The reference's RaBitQ keys are 4-bit sign + magnitude codes (ParisKV,
  * PC:1130-1195 batch_encode; rerank_rabitq_ref, Z/cache_hub/rerank/rerank.py:205-274).

@@ -355,3 +355,13 @@ def kivi4_sparse_attention(q, cache: Kivi4Cache, n_groups: int, k_res, v_res, re
             out[b, h * gqa:(h + 1) * gqa] = attention(q[b:b + 1, h * gqa:(h + 1) * gqa], k[None, None],
                                                       v[None, None], sm_scale, dtype=dtype)[0]
     return out
+
+
+def lse_merge(out_a, lse_a, out_b, lse_b, dtype=np.float64):
+    """lse_merge_torch (Z/cache_hub/lse_merge/lse_merge.py:79-119):
+    out_* [bs, heads, dim], lse_* [bs, heads] (natural log)."""
+    la, lb = lse_a.astype(dtype), lse_b.astype(dtype)
+    m = np.maximum(la, lb)
+    wa, wb = np.exp(la - m), np.exp(lb - m)
+    return ((wa[..., None] * out_a.astype(dtype) + wb[..., None] * out_b.astype(dtype))
+            / (wa + wb)[..., None])

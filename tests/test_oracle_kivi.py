@@ -4,6 +4,7 @@ import pytest
 import torch
 
 from oracle import kivi
+from oracle import kivi as okivi
 from oracle.numerics import BF16_1EM8, bf16_bits, bf16_to_f32, bf16r, f16_bits
 from tests.helpers import gaussian_bf16
 
@@ -184,3 +185,20 @@ def test_attention_oracle_textbook_and_lse_split(rng):
     m = np.maximum(l1, l2)
     w1, w2 = np.exp(l1 - m)[..., None], np.exp(l2 - m)[..., None]
     assert np.allclose((w1 * o1 + w2 * o2) / (w1 + w2), out, atol=1e-12)
+
+
+def test_lse_merge_of_two_segments_is_attention_over_both(rng):
+    """Closed form: merging the normalised outputs of two KV segments by their
+    LSEs equals attention over the concatenated segments."""
+    q = gaussian_bf16(rng, (2, 8, 128))
+    k = gaussian_bf16(rng, (2, 2, 70, 128))
+    v = gaussian_bf16(rng, (2, 2, 70, 128))
+    sc = 1 / np.sqrt(128)
+    oa, la = okivi.attention(q, k[:, :, :23], v[:, :, :23], sc, return_lse=True)
+    ob, lb = okivi.attention(q, k[:, :, 23:], v[:, :, 23:], sc, return_lse=True)
+    full = okivi.attention(q, k, v, sc)
+    assert np.allclose(okivi.lse_merge(oa, la, ob, lb), full, atol=1e-12)
+    # the LSE itself: log of the softmax denominator
+    s = np.einsum("bhgd,bhnd->bhgn", q.reshape(2, 2, 4, 128).astype(np.float64), k.astype(np.float64)) * sc
+    _, lfull = okivi.attention(q, k, v, sc, return_lse=True)
+    assert np.allclose(lfull, np.log(np.exp(s).sum(-1)).reshape(2, 8), atol=1e-10)

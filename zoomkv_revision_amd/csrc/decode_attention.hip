@@ -20,8 +20,10 @@
 //    run on the matrix cores as v_mfma_f32_16x16x32_f16 (query heads on the N
 //    axis).  The Format Q word / metadata order is the MFMA operand order, so
 //    the K-MFMA result lands in exactly the lanes the V-MFMA B operand needs;
-//  * online softmax in fp32 (base 2, log2(e)*sm_scale folded into q), with the
-//    O rescale skipped when no running max moved;
+//  * online softmax in fp32, base 2: q enters the MFMA as fp16(q / 8) (exact
+//    for bf16 q in range) and the scale 8 * log2(e) * sm_scale is applied inside
+//    the exponent's fma, so scores are not rounded to fp16; the O rescale is
+//    skipped when no running max moved;
 //  * the NW waves merge through LDS; with one split per KV head the kernel
 //    writes the output, otherwise a second small kernel merges the splits
 //    (a kernel boundary is the cheap cross-XCD fence: a device-scope
@@ -47,6 +49,7 @@ namespace {
 
 constexpr int kTile = 32;
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kNegBig = -1.0e30f;
 
 struct AttnParams {
@@ -56,11 +59,13 @@ struct AttnParams {
   const uint16_t* k_meta;
   const int32_t* v_codes;
   const uint16_t* v_meta;
-  const uint16_t* k_res;
+  const uint16_t* k_res;  // bf16 tiles: token t of (b, kv) at b*kr_sb + kv*kr_sh + t*kr_st
   const uint16_t* v_res;
-  int g_cap, r_cap;
+  int g_cap;
+  int64_t kr_sb, kr_sh, kr_st, vr_sb, vr_sh, vr_st;
+  float* lse;      // optional natural-log LSE [bs, kv*gqa] of the scaled scores
   int kv, gqa, n_groups, res_len, n_splits, tiles_per_split;
-  float qscale;
+  float qscale;    // raw MFMA score * qscale = base-2 scaled score
   float* ws_o;     // [bs, kv, n_splits, gqa, 128]
   float* ws_ml;    // [bs, kv, n_splits, gqa, 2]
   void* out;       // [bs, kv*gqa, 128], written directly when n_splits == 1
@@ -165,13 +170,14 @@ __device__ __forceinline__ float wave_sum16(float x) {
   return x + __shfl_xor(x, 32);
 }
 
-// Online-softmax update for one tile: S holds the base-2 scores of tokens
-// TAU[g][0..7] for query head c (masked tokens are -inf).  Returns P as the
-// fp16 B operand of the V-MFMA and rescales O when a running max moved.
+// Online-softmax update for one tile: S holds the raw scores of tokens
+// TAU[g][0..7] for query head c (masked tokens are -inf); qs turns a raw score
+// into a base-2 exponent.  m_run is kept in raw units.  Returns P as the fp16
+// B operand of the V-MFMA and rescales O when a running max moved.
 // v_exp_f32 flushes results below 2^-126 to zero, which only drops
 // probabilities that are already far below fp16 resolution.
-__device__ __forceinline__ half8_t softmax_step(const float4_t S[2], float& m_run, float& l_run,
-                                                float4_t O[8]) {
+__device__ __forceinline__ half8_t softmax_step(const float4_t S[2], float qs, float& m_run,
+                                                float& l_run, float4_t O[8]) {
   float sv[8];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -182,13 +188,14 @@ __device__ __forceinline__ half8_t softmax_step(const float4_t S[2], float& m_ru
                    fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
   mx = wave_max16(mx);
   const float m_new = fmaxf(m_run, mx);
-  const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+  const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * qs);
   m_run = m_new;
+  const float mq = m_new * qs;
   half8_t pb;
   float ps = 0.0f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const float pe = __builtin_amdgcn_exp2f(sv[e] - m_new);
+    const float pe = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[e], qs, -mq));
     ps += pe;
     pb[e] = static_cast<_Float16>(pe);
   }
@@ -202,7 +209,7 @@ __device__ __forceinline__ half8_t softmax_step(const float4_t S[2], float& m_ru
 
 // Tile compute from an LDS stage: K-MFMA, softmax, V-MFMA.
 __device__ __forceinline__ void compute_tile(const uint8_t* st, int lane, int c, int g,
-                                             const half8_t qB[4], const NibbleConsts& nk,
+                                             const half8_t qB[4], float qs, const NibbleConsts& nk,
                                              uint32_t half_mask, float& m_run, float& l_run,
                                              float4_t O[8]) {
   const u32x4_t kq0 = ld16(st + 16 * lane);
@@ -218,7 +225,7 @@ __device__ __forceinline__ void compute_tile(const uint8_t* st, int lane, int c,
   // S[m] holds tokens 16m + 4g + i: drop an unselected page (half)
   if (!(half_mask & 1u)) S[0] = float4_t{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
   if (!(half_mask & 2u)) S[1] = float4_t{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-  const half8_t pb = softmax_step(S, m_run, l_run, O);
+  const half8_t pb = softmax_step(S, qs, m_run, l_run, O);
   const u32x4_t vq0 = ld16(st + 2048 + 16 * lane);
   const u32x4_t vq1 = ld16(st + 3072 + 16 * lane);
   const uint8_t* vm = st + 4608 + ((c >> 2) * 4 + g) * 32;
@@ -230,12 +237,12 @@ __device__ __forceinline__ void compute_tile(const uint8_t* st, int lane, int c,
   }
 }
 
-// One bf16 residual tile (tokens [base, base + valid) of the window).
-__device__ __forceinline__ void residual_tile(const AttnParams& p, int64_t bh, int base, int valid,
-                                              int c, int g, const half8_t qB[4], float& m_run,
-                                              float& l_run, float4_t O[8]) {
-  const uint16_t* kr = p.k_res + (bh * p.r_cap + base) * 128;
-  const uint16_t* vr = p.v_res + (bh * p.r_cap + base) * 128;
+// One bf16 tile (tokens [base, base + valid) of the window).
+__device__ __forceinline__ void residual_tile(const AttnParams& p, int b, int h, int base, int valid,
+                                              int c, int g, const half8_t qB[4], float qs,
+                                              float& m_run, float& l_run, float4_t O[8]) {
+  const uint16_t* kr = p.k_res + b * p.kr_sb + h * p.kr_sh + base * p.kr_st;
+  const uint16_t* vr = p.v_res + b * p.vr_sb + h * p.vr_sh + base * p.vr_st;
   constexpr int kslot[8] = {0, 4, 1, 5, 2, 6, 3, 7};
   float4_t S[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
 #pragma unroll
@@ -244,7 +251,7 @@ __device__ __forceinline__ void residual_tile(const AttnParams& p, int64_t bh, i
     for (int m = 0; m < 2; ++m) {
       const int tok = c + 16 * m;
       u32x4_t raw = {0u, 0u, 0u, 0u};
-      if (tok < valid) raw = ld16(kr + tok * 128 + 8 * (4 * s + g));
+      if (tok < valid) raw = ld16(kr + tok * p.kr_st + 8 * (4 * s + g));
       half8_t a;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
@@ -259,7 +266,7 @@ __device__ __forceinline__ void residual_tile(const AttnParams& p, int64_t bh, i
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       if (4 * g + i + 16 * m >= valid) S[m][i] = -INFINITY;
-  const half8_t pb = softmax_step(S, m_run, l_run, O);
+  const half8_t pb = softmax_step(S, qs, m_run, l_run, O);
   // V^T operand: element e = token TAU[g][e], row c of M-tile j = channel 8c + j
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
@@ -267,7 +274,7 @@ __device__ __forceinline__ void residual_tile(const AttnParams& p, int64_t bh, i
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const int tok = (e < 4) ? (4 * g + e) : (16 + 4 * g + e - 4);
-      const float x = tok < valid ? bf16_to_f32(vr[tok * 128 + 8 * c + j]) : 0.0f;
+      const float x = tok < valid ? bf16_to_f32(vr[tok * p.vr_st + 8 * c + j]) : 0.0f;
       a[e] = static_cast<_Float16>(x);
     }
     O[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb, O[j], 0, 0, 0);
@@ -345,7 +352,7 @@ void kivi4_attn_kernel(const AttnParams p) {
       for (int e = 0; e < 8; ++e) {
         const uint32_t wv = raw[kslot[e] >> 1];
         const float x = __uint_as_float((kslot[e] & 1) ? (wv & 0xFFFF0000u) : (wv << 16));
-        qB[s][e] = static_cast<_Float16>(col_ok ? x * p.qscale : 0.0f);
+        qB[s][e] = static_cast<_Float16>(col_ok ? x * 0.125f : 0.0f);
       }
     }
   }
@@ -364,13 +371,13 @@ void kivi4_attn_kernel(const AttnParams p) {
     }
     const uint32_t half_mask = kSparse ? static_cast<uint32_t>(__builtin_amdgcn_readlane(my_mask, k)) : 3u;
     wait_tiles_in_flight(issued - 1 - k);
-    compute_tile(ring[k % D], lane, c, g, qB, nk, half_mask, m_run, l_run, O);
+    compute_tile(ring[k % D], lane, c, g, qB, p.qscale, nk, half_mask, m_run, l_run, O);
   }
 
   // ---- bf16 residual tiles (at most r_cap / 32 of them, in the last split) ----
   for (int t = max(T0, n_qt) + wave; t < T1; t += NW) {
     const int base = (t - n_qt) * kTile;
-    residual_tile(p, bh, base, min(kTile, p.res_len - base), c, g, qB, m_run, l_run, O);
+    residual_tile(p, b, h, base, min(kTile, p.res_len - base), c, g, qB, p.qscale, m_run, l_run, O);
   }
 
   // ---- merge the NW waves through LDS (the rings are free now) ----
@@ -388,7 +395,7 @@ void kivi4_attn_kernel(const AttnParams p) {
       *reinterpret_cast<float4_t*>(o + 8 * i + 4) = float4_t{O[4][i], O[5][i], O[6][i], O[7][i]};
     }
     if (g == 0) {
-      red_m[wave * p.gqa + c] = m_run;
+      red_m[wave * p.gqa + c] = m_run * p.qscale;  // base-2 scaled units from here on
       red_l[wave * p.gqa + c] = l_tot;
     }
   }
@@ -410,6 +417,7 @@ void kivi4_attn_kernel(const AttnParams p) {
     }
     if (final_out) {
       store_out(p, bh * p.gqa + cc, d, ll > 0.0f ? oo / ll : 0.0f);  // row b*hq + h*gqa + cc
+      if (p.lse != nullptr && d == 0) p.lse[bh * p.gqa + cc] = (mm + __log2f(ll)) * kLn2;
     } else {
       const int64_t row = (bh * p.n_splits + split) * p.gqa + cc;
       p.ws_o[row * 128 + d] = oo;
@@ -426,7 +434,8 @@ void kivi4_attn_kernel(const AttnParams p) {
 __global__ __launch_bounds__(128) void kivi4_combine_kernel(const float* __restrict__ ws_o,
                                                             const float* __restrict__ ws_ml,
                                                             int kv, int gqa, int n_splits,
-                                                            void* __restrict__ out, int out_f32) {
+                                                            void* __restrict__ out, int out_f32,
+                                                            float* __restrict__ lse) {
   const int bq = blockIdx.x;  // b * hq + hq_idx
   const int hq = kv * gqa;
   const int b = bq / hq, qh = bq % hq;
@@ -444,6 +453,7 @@ __global__ __launch_bounds__(128) void kivi4_combine_kernel(const float* __restr
     num += w * ws_o[row * 128 + d];
   }
   const float r = den > 0.0f ? num / den : 0.0f;
+  if (lse != nullptr && d == 0) lse[bq] = (mmax + __log2f(den)) * kLn2;
   const int64_t oi = static_cast<int64_t>(bq) * 128 + d;
   if (out_f32)
     reinterpret_cast<float*>(out)[oi] = r;
@@ -486,6 +496,45 @@ __global__ __launch_bounds__(64) void sparse_tiles_kernel(
     base += __popcll(m);
   }
   if (lane == 0) tile_count[bh] = base;
+}
+
+// Merge of two independently normalised attention outputs by their natural
+// LSEs (lse_merge_torch, Z/cache_hub/lse_merge/lse_merge.py:79-119):
+//   m = max(la, lb), wa = exp(la - m), wb = exp(lb - m),
+//   out = (wa * a + wb * b) / (wa + wb), computed in fp32, stored as the inputs' type.
+// Elementwise over [bs, 1, heads, dim]; lse [bs, heads].  dtype 0 bf16, 1 fp16, 2 fp32.
+template <int kType>
+__device__ __forceinline__ float load_val(const void* p, int64_t i) {
+  if constexpr (kType == 0)
+    return bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
+  else if constexpr (kType == 1)
+    return static_cast<float>(static_cast<const _Float16*>(p)[i]);
+  else
+    return static_cast<const float*>(p)[i];
+}
+
+template <int kType>
+__device__ __forceinline__ void store_val(void* p, int64_t i, float v) {
+  if constexpr (kType == 0)
+    static_cast<uint16_t*>(p)[i] = f32_to_bf16_bits(v);
+  else if constexpr (kType == 1)
+    static_cast<_Float16*>(p)[i] = static_cast<_Float16>(v);
+  else
+    static_cast<float*>(p)[i] = v;
+}
+
+template <int kType>
+__global__ __launch_bounds__(256) void lse_merge_kernel(const void* __restrict__ a, const float* __restrict__ la,
+                                                        const void* __restrict__ b, const float* __restrict__ lb,
+                                                        void* __restrict__ out, int64_t total, int dim) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int64_t row = i / dim;  // b * heads + h
+  const float x = la[row], y = lb[row];
+  const float m = fmaxf(x, y);
+  const float wa = expf(x - m), wb = expf(y - m);
+  const float den = wa + wb;
+  store_val<kType>(out, i, (wa * load_val<kType>(a, i) + wb * load_val<kType>(b, i)) / den);
 }
 
 struct SplitPlan {
@@ -555,6 +604,11 @@ void launch_attn(const AttnParams& p, int bs, hipStream_t s) {
   }
 }
 
+// Element strides of the bf16 tiles: residual window or a whole bf16 cache.
+struct ResidualLayout {
+  int64_t k_sb, k_sh, k_st, v_sb, v_sh, v_st;
+};
+
 // Page list of the page-sparse mode (pages int64 [bs, kv, n_sel] at strides).
 struct SparsePages {
   const int64_t* pages;
@@ -598,7 +652,8 @@ int attention_launch(const uint16_t* q, int64_t q_sb, int64_t q_sh, const int32_
                      int g_cap, const uint16_t* k_res, const uint16_t* v_res, int r_cap, int bs,
                      int hq, int kv, int n_groups, int res_len, float sm_scale, int n_splits,
                      void* workspace, size_t workspace_bytes, int* n_splits_used, void* out,
-                     int out_f32, hipStream_t s, const SparsePages* sparse = nullptr) {
+                     int out_f32, hipStream_t s, const SparsePages* sparse = nullptr,
+                     const ResidualLayout* rl = nullptr, float* lse = nullptr) {
   ZKV_REQUIRE(q && workspace, "zkv_kivi4_attention: null pointer");
   ZKV_REQUIRE(bs > 0 && kv > 0 && hq > 0 && hq % kv == 0,
               "zkv_kivi4_attention: bad heads bs=%d hq=%d kv=%d", bs, hq, kv);
@@ -606,8 +661,17 @@ int attention_launch(const uint16_t* q, int64_t q_sb, int64_t q_sh, const int32_
   ZKV_REQUIRE(gqa <= 16, "zkv_kivi4_attention: at most 16 query heads per KV head; got %d", gqa);
   ZKV_REQUIRE(n_groups >= 0 && n_groups <= g_cap, "zkv_kivi4_attention: n_groups=%d g_cap=%d",
               n_groups, g_cap);
-  ZKV_REQUIRE(res_len >= 0 && res_len <= r_cap, "zkv_kivi4_attention: res_len=%d r_cap=%d",
-              res_len, r_cap);
+  ZKV_REQUIRE(res_len >= 0 && (rl != nullptr || res_len <= r_cap),
+              "zkv_kivi4_attention: res_len=%d r_cap=%d", res_len, r_cap);
+  const ResidualLayout res = rl ? *rl
+                                : ResidualLayout{static_cast<int64_t>(kv) * r_cap * 128,
+                                                 static_cast<int64_t>(r_cap) * 128, 128,
+                                                 static_cast<int64_t>(kv) * r_cap * 128,
+                                                 static_cast<int64_t>(r_cap) * 128, 128};
+  ZKV_REQUIRE(res_len == 0 || ((res.k_sb | res.k_sh | res.k_st) % 8 == 0 &&
+                               (reinterpret_cast<uintptr_t>(k_res) & 15) == 0),
+              "zkv_kivi4_attention: bf16 K rows must be 16-byte aligned (strides %lld %lld %lld)",
+              (long long)res.k_sb, (long long)res.k_sh, (long long)res.k_st);
   ZKV_REQUIRE(sparse != nullptr || n_groups + res_len > 0, "zkv_kivi4_attention: empty context");
   ZKV_REQUIRE(n_groups == 0 || (k_codes && k_meta && v_codes && v_meta),
               "zkv_kivi4_attention: null cache pointer");
@@ -638,14 +702,20 @@ int attention_launch(const uint16_t* q, int64_t q_sb, int64_t q_sh, const int32_
   p.k_res = k_res;
   p.v_res = v_res;
   p.g_cap = g_cap;
-  p.r_cap = r_cap;
+  p.kr_sb = res.k_sb;
+  p.kr_sh = res.k_sh;
+  p.kr_st = res.k_st;
+  p.vr_sb = res.v_sb;
+  p.vr_sh = res.v_sh;
+  p.vr_st = res.v_st;
+  p.lse = lse;
   p.kv = kv;
   p.gqa = gqa;
   p.n_groups = n_groups;
   p.res_len = res_len;
   p.n_splits = sp.n_splits;
   p.tiles_per_split = sp.tiles_per_split;
-  p.qscale = sm_scale * kLog2e;
+  p.qscale = sm_scale * kLog2e * 8.0f;  // q enters the MFMA as q / 8
   p.ws_o = reinterpret_cast<float*>(workspace);
   p.ws_ml = p.ws_o + static_cast<size_t>(bs) * hq * sp.n_splits * 128;
   p.out = out;
@@ -673,7 +743,7 @@ int attention_launch(const uint16_t* q, int64_t q_sb, int64_t q_sh, const int32_
   launch_attn(p, bs, s);
   int rc = check_launch("kivi4_attn_kernel");
   if (rc || out == nullptr || sp.n_splits == 1) return rc;
-  kivi4_combine_kernel<<<bs * hq, 128, 0, s>>>(p.ws_o, p.ws_ml, kv, gqa, sp.n_splits, out, out_f32);
+  kivi4_combine_kernel<<<bs * hq, 128, 0, s>>>(p.ws_o, p.ws_ml, kv, gqa, sp.n_splits, out, out_f32, lse);
   return check_launch("kivi4_combine_kernel");
 }
 
@@ -711,7 +781,7 @@ extern "C" int zkv_attention_merge(const void* workspace, int bs, int hq, int kv
   const float* ws_o = reinterpret_cast<const float*>(workspace);
   const float* ws_ml = ws_o + static_cast<size_t>(bs) * hq * n_splits * 128;
   kivi4_combine_kernel<<<bs * hq, 128, 0, reinterpret_cast<hipStream_t>(stream)>>>(
-      ws_o, ws_ml, kv, hq / kv, n_splits, out, out_f32);
+      ws_o, ws_ml, kv, hq / kv, n_splits, out, out_f32, nullptr);
   return check_launch("kivi4_combine_kernel");
 }
 
@@ -754,4 +824,46 @@ extern "C" int zkv_kivi4_sparse_attention(const uint16_t* q, int64_t q_sb, int64
                           r_cap, bs, hq, kv, n_groups, res_len, sm_scale, n_splits, workspace,
                           workspace_bytes, nullptr, out, out_f32,
                           reinterpret_cast<hipStream_t>(stream), &sp);
+}
+
+// ---- bf16 K/V decode attention (flash_attn_with_kvcache counterpart) ------
+
+extern "C" size_t zkv_bf16_attention_workspace_size(int bs, int hq, int kv, int n, int n_splits) {
+  if (bs <= 0 || kv <= 0 || hq <= 0 || n < 0) return 0;
+  const SplitPlan sp = plan_splits(bs, kv, 0, n, n_splits);
+  return workspace_bytes_for(bs, hq, kv, sp.n_splits);
+}
+
+extern "C" int zkv_bf16_decode_attention(const uint16_t* q, int64_t q_sb, int64_t q_sh,
+                                         const uint16_t* k, int64_t k_sb, int64_t k_st, int64_t k_sh,
+                                         const uint16_t* v, int64_t v_sb, int64_t v_st, int64_t v_sh,
+                                         int bs, int hq, int kv, int n, float sm_scale, void* out,
+                                         int out_f32, float* lse, int n_splits, void* workspace,
+                                         size_t workspace_bytes, zkv_stream_t stream) {
+  ZKV_REQUIRE(out, "zkv_bf16_decode_attention: null output");
+  ZKV_REQUIRE(n > 0, "zkv_bf16_decode_attention: empty key cache");
+  const ResidualLayout rl{k_sb, k_sh, k_st, v_sb, v_sh, v_st};
+  return attention_launch(q, q_sb, q_sh, nullptr, nullptr, nullptr, nullptr, 0, k, v, n, bs, hq, kv, 0,
+                          n, sm_scale, n_splits, workspace, workspace_bytes, nullptr, out, out_f32,
+                          reinterpret_cast<hipStream_t>(stream), nullptr, &rl, lse);
+}
+
+extern "C" int zkv_lse_merge(const void* out_a, const float* lse_a, const void* out_b, const float* lse_b,
+                             void* out, int dtype, int bs, int heads, int dim, zkv_stream_t stream) {
+  ZKV_REQUIRE(out_a && lse_a && out_b && lse_b && out, "zkv_lse_merge: null pointer");
+  ZKV_REQUIRE(bs >= 0 && heads >= 0 && dim > 0, "zkv_lse_merge: bad sizes bs=%d heads=%d dim=%d", bs,
+              heads, dim);
+  ZKV_REQUIRE(dtype >= 0 && dtype <= 2, "zkv_lse_merge: dtype %d is not 0 (bf16), 1 (fp16) or 2 (fp32)",
+              dtype);
+  const int64_t total = static_cast<int64_t>(bs) * heads * dim;
+  if (total == 0) return ZKV_OK;
+  const unsigned blocks = static_cast<unsigned>((total + 255) / 256);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (dtype == 0)
+    lse_merge_kernel<0><<<blocks, 256, 0, s>>>(out_a, lse_a, out_b, lse_b, out, total, dim);
+  else if (dtype == 1)
+    lse_merge_kernel<1><<<blocks, 256, 0, s>>>(out_a, lse_a, out_b, lse_b, out, total, dim);
+  else
+    lse_merge_kernel<2><<<blocks, 256, 0, s>>>(out_a, lse_a, out_b, lse_b, out, total, dim);
+  return check_launch("lse_merge_kernel");
 }
