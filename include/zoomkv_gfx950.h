@@ -240,6 +240,20 @@ int zkv_bf16_decode_attention(const uint16_t* q, int64_t q_sb, int64_t q_sh, con
                               float sm_scale, void* out, int out_f32, float* lse, int n_splits,
                               void* workspace, size_t workspace_bytes, zkv_stream_t stream);
 
+/* bf16 decode attention over a gathered token list without materialising the
+ * gather: token t < n_idx of (b, kv) is row idx[b*idx_sb + kv*idx_sh + t] of
+ * k / v (rows outside [0, n_rows) are masked out), and tokens n_idx ..
+ * n_idx + tail_len - 1 are the contiguous rows tail_start ..  Replaces the
+ * h2d_gather_kv / torch.gather -> torch.cat -> flash_attn_with_kvcache
+ * sequence of compute() (S:1723-1747 offload, S:1752-1772 on-GPU).  Sizes
+ * and workspace as zkv_bf16_decode_attention with n = n_idx + tail_len. */
+int zkv_bf16_gather_attention(const uint16_t* q, int64_t q_sb, int64_t q_sh, const uint16_t* k,
+                              int64_t k_sb, int64_t k_st, int64_t k_sh, const uint16_t* v,
+                              int64_t v_sb, int64_t v_st, int64_t v_sh, int n_rows, const int64_t* idx,
+                              int64_t idx_sb, int64_t idx_sh, int n_idx, int tail_start, int tail_len,
+                              int bs, int hq, int kv, float sm_scale, void* out, int out_f32, float* lse,
+                              int n_splits, void* workspace, size_t workspace_bytes, zkv_stream_t stream);
+
 /* LSE merge of two attention outputs [bs, 1, heads, dim] (contiguous, dtype 0
  * bf16 / 1 fp16 / 2 fp32) with fp32 natural-log LSEs [bs, heads]:
  * lse_merge_torch / lse_merge_cuda (Z/cache_hub/lse_merge/lse_merge.py:79-149). */

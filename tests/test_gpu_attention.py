@@ -82,3 +82,32 @@ def test_split_attention_merged_by_lse_equals_full(rng):
     full = fa32(flash_attn_with_kvcache_compat(q, k, v))[:, 0]
     assert np.abs(merged - full).max() <= ATOL
     assert np.abs(fa32(lse_merge(oa, la, ob, lb))[:, 0] - full).max() <= ATOL
+
+
+@pytest.mark.parametrize("n_idx,tail_start,tail_len", [(100, 300, 40), (0, 10, 77), (64, 0, 0), (5, 499, 1)])
+def test_gather_attention_matches_gathered_oracle(rng, n_idx, tail_start, tail_len):
+    """Index list (with invalid ids masked) + contiguous tail == gather, cat,
+    attend (the reference's compute() tail)."""
+    from zoomkv_revision_amd.attention import gather_attention
+    bs, hq, kv, rows = 2, 32, 8, 500
+    q = gaussian_bf16(rng, (bs, hq, 128))
+    k = gaussian_bf16(rng, (bs, kv, rows, 128))
+    v = gaussian_bf16(rng, (bs, kv, rows, 128))
+    idx = rng.integers(0, rows, size=(bs, kv, n_idx))
+    if n_idx > 3:
+        idx[0, 1, 2] = -1           # masked
+        idx[1, 3, 0] = rows + 7     # masked
+    out, lse = gather_attention(to_bf16(q).unsqueeze(1), to_bf16(k), to_bf16(v),
+                                torch.from_numpy(idx).cuda() if n_idx else None, tail_start, tail_len,
+                                return_softmax_lse=True)
+    ref = np.zeros((bs, hq, 128))
+    rlse = np.zeros((bs, hq))
+    g = hq // kv
+    for b in range(bs):
+        for h in range(kv):
+            sel = [r for r in idx[b, h] if 0 <= r < rows] + list(range(tail_start, tail_start + tail_len))
+            o, l = okivi.attention(q[b:b + 1, h * g:(h + 1) * g], k[b, h, sel][None, None], v[b, h, sel][None, None],
+                                   1 / np.sqrt(128), return_lse=True)
+            ref[b, h * g:(h + 1) * g], rlse[b, h * g:(h + 1) * g] = o[0], l[0]
+    assert np.abs(from_torch(out)[:, 0] - ref).max() <= ATOL + np.abs(ref).max() * 2 ** -8
+    assert np.allclose(from_torch(lse)[..., 0], rlse, rtol=1e-4, atol=1e-4)

@@ -53,6 +53,8 @@ SIGNATURES = {
     "zkv_bf16_attention_workspace_size": (SZ, [I32, I32, I32, I32, I32]),
     "zkv_bf16_decode_attention": (I32, [P, I64, I64, P, I64, I64, I64, P, I64, I64, I64, I32, I32, I32, I32,
                                         F32, P, I32, P, I32, P, SZ, P]),
+    "zkv_bf16_gather_attention": (I32, [P, I64, I64, P, I64, I64, I64, P, I64, I64, I64, I32, P, I64, I64,
+                                        I32, I32, I32, I32, I32, I32, F32, P, I32, P, I32, P, SZ, P]),
     "zkv_lse_merge": (I32, [P, P, P, P, P, I32, I32, I32, I32, P]),
     "zkv_rabitq_encode": (I32, [P, I64, I64, P, P, P, P]),
     "zkv_rabitq_estimate": (I32, [P, P, P, P, I32, I32, I64, P, P]),

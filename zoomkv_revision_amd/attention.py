@@ -60,7 +60,7 @@ def flash_attn_with_kvcache_compat(q: torch.Tensor, k_cache: torch.Tensor, v_cac
         q3 = q3.contiguous()
     if k_cache.stride(-1) != 1 or any(s % 8 for s in k_cache.stride()[:3]) or k_cache.data_ptr() % 16:
         k_cache = k_cache.contiguous()
-    if v_cache.stride(-1) != 1:
+    if v_cache.stride(-1) != 1 or any(s % 8 for s in v_cache.stride()[:3]) or v_cache.data_ptr() % 16:
         v_cache = v_cache.contiguous()
     scale = 1.0 / math.sqrt(HEAD_DIM) if softmax_scale is None else float(softmax_scale)
     if out is None:
@@ -75,6 +75,55 @@ def flash_attn_with_kvcache_compat(q: torch.Tensor, k_cache: torch.Tensor, v_cac
         ptr(k_cache), k_cache.stride(0), k_cache.stride(1), k_cache.stride(2),
         ptr(v_cache), v_cache.stride(0), v_cache.stride(1), v_cache.stride(2),
         bs, hq, kv, n, scale, ptr(out), 0, ptr(lse), n_splits, ptr(ws), ws.numel(), stream_of(q)))
+    return (out, lse) if return_softmax_lse else out
+
+
+def gather_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, idx: torch.Tensor | None,
+                     tail_start: int = 0, tail_len: int = 0, softmax_scale: float | None = None,
+                     return_softmax_lse: bool = False, out: torch.Tensor | None = None,
+                     n_splits: int = 0):
+    """Decode attention over rows of a bf16 buffer without materialising the
+    gather: for (b, kv), the rows idx[b, kv, :] (rows outside the buffer are
+    masked out) followed by the contiguous rows [tail_start, tail_start +
+    tail_len).  q [bs, 1, hq, 128] bf16; k, v [bs, kv, n_rows, 128] bf16 (any
+    strides, rows 16-byte aligned); idx int64 [bs, kv, n_idx] or None.
+    Equivalent to gathering those rows, concatenating and calling
+    flash_attn_with_kvcache_compat (S:1723-1772)."""
+    require_gpu(q, k, v)
+    if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
+        raise TypeError("q, k and v must be bfloat16")
+    if q.dim() != 4 or q.shape[1] != 1 or q.shape[-1] != HEAD_DIM:
+        raise ValueError(f"q must be [bs, 1, hq, 128]; got {tuple(q.shape)}")
+    if k.dim() != 4 or k.shape != v.shape or k.shape[-1] != HEAD_DIM:
+        raise ValueError(f"k / v must be [bs, kv, n_rows, 128]; got {tuple(k.shape)}, {tuple(v.shape)}")
+    bs, _, hq, _ = q.shape
+    kbs, kv, n_rows, _ = k.shape
+    if kbs != bs or hq % kv != 0:
+        raise ValueError(f"q {tuple(q.shape)} does not match k {tuple(k.shape)}")
+    for t in (k, v):
+        if t.stride(-1) != 1 or any(st % 8 for st in t.stride()[:3]) or t.data_ptr() % 16:
+            raise ValueError("k / v rows must be 16-byte aligned with a contiguous last dim")
+    n_idx = 0 if idx is None else idx.shape[-1]
+    if idx is not None:
+        if idx.dtype != torch.int64 or idx.dim() != 3 or tuple(idx.shape[:2]) != (bs, kv):
+            raise ValueError("idx must be int64 [bs, kv, n_idx]")
+        if n_idx > 1 and idx.stride(2) != 1:
+            idx = idx.contiguous()
+    q3 = q[:, 0]
+    if q3.stride(-1) != 1 or q3.stride(1) % 8 or q3.stride(0) % 8 or q3.data_ptr() % 16:
+        q3 = q3.contiguous()
+    scale = 1.0 / math.sqrt(HEAD_DIM) if softmax_scale is None else float(softmax_scale)
+    if out is None:
+        out = torch.empty(bs, 1, hq, HEAD_DIM, dtype=q.dtype, device=q.device)
+    lse = torch.empty(bs, hq, 1, dtype=torch.float32, device=q.device) if return_softmax_lse else None
+    L = lib()
+    ws = _workspace(q.device, L.zkv_bf16_attention_workspace_size(bs, hq, kv, n_idx + tail_len, n_splits))
+    check(L.zkv_bf16_gather_attention(
+        ptr(q3), q3.stride(0), q3.stride(1),
+        ptr(k), k.stride(0), k.stride(2), k.stride(1), ptr(v), v.stride(0), v.stride(2), v.stride(1),
+        n_rows, ptr(idx), idx.stride(0) if idx is not None else 0, idx.stride(1) if idx is not None else 0,
+        n_idx, int(tail_start), int(tail_len), bs, hq, kv, scale, ptr(out), 0, ptr(lse), n_splits,
+        ptr(ws), ws.numel(), stream_of(q)))
     return (out, lse) if return_softmax_lse else out
 
 

@@ -64,6 +64,10 @@ struct AttnParams {
   int g_cap;
   int64_t kr_sb, kr_sh, kr_st, vr_sb, vr_sh, vr_st;
   float* lse;      // optional natural-log LSE [bs, kv*gqa] of the scaled scores
+  // optional index list of the bf16 tokens (see bf16_row)
+  const int64_t* res_idx;
+  int64_t ri_sb, ri_sh;
+  int n_idx, tail_start, row_limit;
   int kv, gqa, n_groups, res_len, n_splits, tiles_per_split;
   float qscale;    // raw MFMA score * qscale = base-2 scaled score
   float* ws_o;     // [bs, kv, n_splits, gqa, 128]
@@ -237,21 +241,43 @@ __device__ __forceinline__ void compute_tile(const uint8_t* st, int lane, int c,
   }
 }
 
-// One bf16 tile (tokens [base, base + valid) of the window).
+// Row in the bf16 buffer of token t of (b, kv)'s bf16 list, or -1 (masked):
+// tokens [0, n_idx) are the listed rows (rows outside [0, row_limit) masked),
+// the rest are the contiguous rows tail_start, tail_start + 1, ...  Without a
+// row index (n_idx = 0, tail_start = 0) token t is row t.
+__device__ __forceinline__ int bf16_row(const AttnParams& p, const int64_t* idx_bh, int t) {
+  if (t < p.n_idx) {  // n_idx > 0 only with a list (checked on the host)
+    const int64_t r = idx_bh[t];
+    return (r >= 0 && r < p.row_limit) ? static_cast<int>(r) : -1;
+  }
+  return p.tail_start + (t - p.n_idx);
+}
+
+// One bf16 tile: tokens [base, base + valid) of the list.  Lane (c, g) loads
+// K rows of tokens c and c + 16 (the K-MFMA A rows) and V rows of tokens
+// TAU[g][e] (its V-MFMA k-slice), 16 B per row.
 __device__ __forceinline__ void residual_tile(const AttnParams& p, int b, int h, int base, int valid,
                                               int c, int g, const half8_t qB[4], float qs,
                                               float& m_run, float& l_run, float4_t O[8]) {
-  const uint16_t* kr = p.k_res + b * p.kr_sb + h * p.kr_sh + base * p.kr_st;
-  const uint16_t* vr = p.v_res + b * p.vr_sb + h * p.vr_sh + base * p.vr_st;
+  const uint16_t* kr = p.k_res + b * p.kr_sb + h * p.kr_sh;
+  const uint16_t* vr = p.v_res + b * p.vr_sb + h * p.vr_sh;
+  const int64_t* idx_bh = p.res_idx ? p.res_idx + b * p.ri_sb + h * p.ri_sh : nullptr;
   constexpr int kslot[8] = {0, 4, 1, 5, 2, 6, 3, 7};
+  int krow[2], vrow[8];
+#pragma unroll
+  for (int m = 0; m < 2; ++m) krow[m] = c + 16 * m < valid ? bf16_row(p, idx_bh, base + c + 16 * m) : -1;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int tok = (e < 4) ? (4 * g + e) : (16 + 4 * g + e - 4);
+    vrow[e] = tok < valid ? bf16_row(p, idx_bh, base + tok) : -1;
+  }
   float4_t S[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
-      const int tok = c + 16 * m;
       u32x4_t raw = {0u, 0u, 0u, 0u};
-      if (tok < valid) raw = ld16(kr + tok * p.kr_st + 8 * (4 * s + g));
+      if (krow[m] >= 0) raw = ld16(kr + krow[m] * p.kr_st + 8 * (4 * s + g));
       half8_t a;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
@@ -261,21 +287,27 @@ __device__ __forceinline__ void residual_tile(const AttnParams& p, int b, int h,
       S[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qB[s], S[m], 0, 0, 0);
     }
   }
+  // S[m][i] is token 4g + i + 16m = TAU[g][i + 4m]
 #pragma unroll
   for (int m = 0; m < 2; ++m)
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      if (4 * g + i + 16 * m >= valid) S[m][i] = -INFINITY;
+      if (vrow[i + 4 * m] < 0) S[m][i] = -INFINITY;
   const half8_t pb = softmax_step(S, qs, m_run, l_run, O);
   // V^T operand: element e = token TAU[g][e], row c of M-tile j = channel 8c + j
+  u32x4_t vx[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    vx[e] = u32x4_t{0u, 0u, 0u, 0u};
+    if (vrow[e] >= 0) vx[e] = ld16(vr + vrow[e] * p.vr_st + 8 * c);
+  }
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     half8_t a;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const int tok = (e < 4) ? (4 * g + e) : (16 + 4 * g + e - 4);
-      const float x = tok < valid ? bf16_to_f32(vr[tok * p.vr_st + 8 * c + j]) : 0.0f;
-      a[e] = static_cast<_Float16>(x);
+      const uint32_t wv = vx[e][j >> 1];
+      a[e] = static_cast<_Float16>(__uint_as_float((j & 1) ? (wv & 0xFFFF0000u) : (wv << 16)));
     }
     O[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb, O[j], 0, 0, 0);
   }
@@ -609,6 +641,13 @@ struct ResidualLayout {
   int64_t k_sb, k_sh, k_st, v_sb, v_sh, v_st;
 };
 
+// Index list of the bf16 tokens: res_len = n_idx listed rows (+ tail).
+struct RowIndex {
+  const int64_t* idx;
+  int64_t sb, sh;
+  int n_idx, tail_start, row_limit;
+};
+
 // Page list of the page-sparse mode (pages int64 [bs, kv, n_sel] at strides).
 struct SparsePages {
   const int64_t* pages;
@@ -653,7 +692,8 @@ int attention_launch(const uint16_t* q, int64_t q_sb, int64_t q_sh, const int32_
                      int hq, int kv, int n_groups, int res_len, float sm_scale, int n_splits,
                      void* workspace, size_t workspace_bytes, int* n_splits_used, void* out,
                      int out_f32, hipStream_t s, const SparsePages* sparse = nullptr,
-                     const ResidualLayout* rl = nullptr, float* lse = nullptr) {
+                     const ResidualLayout* rl = nullptr, float* lse = nullptr,
+                     const RowIndex* ri = nullptr) {
   ZKV_REQUIRE(q && workspace, "zkv_kivi4_attention: null pointer");
   ZKV_REQUIRE(bs > 0 && kv > 0 && hq > 0 && hq % kv == 0,
               "zkv_kivi4_attention: bad heads bs=%d hq=%d kv=%d", bs, hq, kv);
@@ -668,10 +708,12 @@ int attention_launch(const uint16_t* q, int64_t q_sb, int64_t q_sh, const int32_
                                                  static_cast<int64_t>(r_cap) * 128, 128,
                                                  static_cast<int64_t>(kv) * r_cap * 128,
                                                  static_cast<int64_t>(r_cap) * 128, 128};
-  ZKV_REQUIRE(res_len == 0 || ((res.k_sb | res.k_sh | res.k_st) % 8 == 0 &&
-                               (reinterpret_cast<uintptr_t>(k_res) & 15) == 0),
-              "zkv_kivi4_attention: bf16 K rows must be 16-byte aligned (strides %lld %lld %lld)",
-              (long long)res.k_sb, (long long)res.k_sh, (long long)res.k_st);
+  ZKV_REQUIRE(res_len == 0 || ((res.k_sb | res.k_sh | res.k_st | res.v_sb | res.v_sh | res.v_st) % 8 == 0 &&
+                               (reinterpret_cast<uintptr_t>(k_res) & 15) == 0 &&
+                               (reinterpret_cast<uintptr_t>(v_res) & 15) == 0),
+              "zkv_kivi4_attention: bf16 K / V rows must be 16-byte aligned (K strides %lld %lld %lld, "
+              "V strides %lld %lld %lld)", (long long)res.k_sb, (long long)res.k_sh, (long long)res.k_st,
+              (long long)res.v_sb, (long long)res.v_sh, (long long)res.v_st);
   ZKV_REQUIRE(sparse != nullptr || n_groups + res_len > 0, "zkv_kivi4_attention: empty context");
   ZKV_REQUIRE(n_groups == 0 || (k_codes && k_meta && v_codes && v_meta),
               "zkv_kivi4_attention: null cache pointer");
@@ -709,6 +751,12 @@ int attention_launch(const uint16_t* q, int64_t q_sb, int64_t q_sh, const int32_
   p.vr_sh = res.v_sh;
   p.vr_st = res.v_st;
   p.lse = lse;
+  p.res_idx = ri ? ri->idx : nullptr;
+  p.ri_sb = ri ? ri->sb : 0;
+  p.ri_sh = ri ? ri->sh : 0;
+  p.n_idx = ri ? ri->n_idx : 0;
+  p.tail_start = ri ? ri->tail_start : 0;
+  p.row_limit = ri ? ri->row_limit : 0;
   p.kv = kv;
   p.gqa = gqa;
   p.n_groups = n_groups;
@@ -866,4 +914,27 @@ extern "C" int zkv_lse_merge(const void* out_a, const float* lse_a, const void* 
   else
     lse_merge_kernel<2><<<blocks, 256, 0, s>>>(out_a, lse_a, out_b, lse_b, out, total, dim);
   return check_launch("lse_merge_kernel");
+}
+
+// ---- bf16 attention over an index list + a contiguous tail -----------------
+
+extern "C" int zkv_bf16_gather_attention(const uint16_t* q, int64_t q_sb, int64_t q_sh,
+                                         const uint16_t* k, int64_t k_sb, int64_t k_st, int64_t k_sh,
+                                         const uint16_t* v, int64_t v_sb, int64_t v_st, int64_t v_sh,
+                                         int n_rows, const int64_t* idx, int64_t idx_sb, int64_t idx_sh,
+                                         int n_idx, int tail_start, int tail_len, int bs, int hq, int kv,
+                                         float sm_scale, void* out, int out_f32, float* lse, int n_splits,
+                                         void* workspace, size_t workspace_bytes, zkv_stream_t stream) {
+  ZKV_REQUIRE(out, "zkv_bf16_gather_attention: null output");
+  ZKV_REQUIRE(n_idx >= 0 && tail_len >= 0 && n_idx + tail_len > 0 && n_rows > 0,
+              "zkv_bf16_gather_attention: bad sizes n_idx=%d tail_len=%d n_rows=%d", n_idx, tail_len, n_rows);
+  ZKV_REQUIRE(n_idx == 0 || idx, "zkv_bf16_gather_attention: null index list");
+  ZKV_REQUIRE(tail_len == 0 || (tail_start >= 0 && static_cast<int64_t>(tail_start) + tail_len <= n_rows),
+              "zkv_bf16_gather_attention: tail [%d, %d) outside the %d rows", tail_start, tail_start + tail_len,
+              n_rows);
+  const ResidualLayout rl{k_sb, k_sh, k_st, v_sb, v_sh, v_st};
+  const RowIndex ri{idx, idx_sb, idx_sh, n_idx, tail_start, n_rows};
+  return attention_launch(q, q_sb, q_sh, nullptr, nullptr, nullptr, nullptr, 0, k, v, n_idx + tail_len, bs, hq,
+                          kv, 0, n_idx + tail_len, sm_scale, n_splits, workspace, workspace_bytes, nullptr, out,
+                          out_f32, reinterpret_cast<hipStream_t>(stream), nullptr, &rl, lse, &ri);
 }
