@@ -63,15 +63,19 @@ int zkv_chunk_encode(const uint16_t* keys, int64_t k_sb, int64_t k_sh, int64_t k
  * Format Q: 4-bit K (per channel, groups of 32 tokens) and V (per token,
  * groups of 32 channels) with fp16 scale / zero.  No reference counterpart
  * (the reference keeps V in bf16, S:561-571); the code ladder is the
- * reference's (S:2003-2009) and the layouts are:
- *   k_codes int32 [bs, kv, G_cap, 512]   word m*256 + l*4 + s, l = 16g + c: the
+ * reference's (S:2003-2009).  The cache is `groups` int32
+ * [bs, kv, G_cap, 1280]: one contiguous 5120-byte record per 32-token group of
+ * one KV head, holding
+ *   words [0, 512)      K codes: word m*256 + l*4 + s, l = 16g + c: the
  *           nibbles of channels 8p..8p+7 (p = 4s + g) of token 32G + 16m + c
- *   k_meta  fp16  [bs, kv, G_cap, 16, 2, 8]  (p, scale|zero, slot): channel
- *           8p + (0,4,1,5,2,6,3,7)[slot]
- *   v_codes int32 [bs, kv, G_cap, 512]   word j*256 + l*4 + i, l = 16r + c:
+ *   words [512, 1024)   V codes: word j*256 + l*4 + i, l = 16r + c:
  *           channel 8c + 4j + i, nibble k = token 32G + TAU[r][2(k%4) + k/4]
- *   v_meta  fp16  [bs, kv, G_cap, 4, 4, 2, 8] (channel group, r, scale|zero, e):
- *           token 32G + TAU[r][e], TAU[r] = (4r..4r+3, 16+4r..16+4r+3)
+ *   words [1024, 1152)  K scale / zero, fp16 [16, 2, 8] (p, scale|zero, slot):
+ *           channel 8p + (0,4,1,5,2,6,3,7)[slot]
+ *   words [1152, 1280)  V scale / zero, fp16 [4, 4, 2, 8] (channel group, r,
+ *           scale|zero, e): token 32G + TAU[r][e], TAU[r] = (4r..4r+3, 16+4r..16+4r+3)
+ * The code / metadata order is the MFMA operand order of the decode kernel,
+ * and one record is one contiguous 5 KiB load.
  *
  * zkv_kivi4_pack quantizes tokens [32*g0, 32*(g0+n_groups)) of the cache
  * from src tokens [0, 32*n_groups) of k / v.
@@ -79,8 +83,7 @@ int zkv_chunk_encode(const uint16_t* keys, int64_t k_sb, int64_t k_sh, int64_t k
  * ------------------------------------------------------------------------ */
 int zkv_kivi4_pack(const uint16_t* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
                    const uint16_t* v, int64_t v_sb, int64_t v_sh, int64_t v_st,
-                   int bs, int kv, int n_groups, int g0, int g_cap,
-                   int32_t* k_codes, uint16_t* k_meta, int32_t* v_codes, uint16_t* v_meta,
+                   int bs, int kv, int n_groups, int g0, int g_cap, int32_t* groups,
                    zkv_stream_t stream);
 
 /* ------------------------------------------------------------------------
@@ -102,8 +105,7 @@ int zkv_kivi4_pack(const uint16_t* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
 size_t zkv_kivi4_attention_workspace_size(int bs, int hq, int kv, int n_groups, int res_len,
                                           int n_splits);
 int zkv_kivi4_decode_attention(const uint16_t* q, int64_t q_sb, int64_t q_sh,
-                               const int32_t* k_codes, const uint16_t* k_meta,
-                               const int32_t* v_codes, const uint16_t* v_meta, int g_cap,
+                               const int32_t* groups, int g_cap,
                                const uint16_t* k_res, const uint16_t* v_res, int r_cap,
                                int bs, int hq, int kv, int n_groups, int res_len,
                                float sm_scale, void* out, int out_f32, int n_splits,
@@ -116,8 +118,7 @@ int zkv_kivi4_decode_attention(const uint16_t* q, int64_t q_sb, int64_t q_sh,
  * followed by (m, l) fp32 [bs, kv, S, hq/kv, 2].  *n_splits_used (host pointer, may be NULL) receives
  * the resolved split count S. */
 int zkv_kivi4_attention_partial(const uint16_t* q, int64_t q_sb, int64_t q_sh,
-                                const int32_t* k_codes, const uint16_t* k_meta,
-                                const int32_t* v_codes, const uint16_t* v_meta, int g_cap,
+                                const int32_t* groups, int g_cap,
                                 const uint16_t* k_res, const uint16_t* v_res, int r_cap,
                                 int bs, int hq, int kv, int n_groups, int res_len,
                                 float sm_scale, int n_splits, void* workspace,
@@ -218,8 +219,7 @@ int zkv_page_minmax_f16(const uint16_t* keys, int64_t k_sb, int64_t k_sh, int64_
  * sequence (S:2195-2240, S:1723-1772). */
 size_t zkv_kivi4_sparse_attention_workspace_size(int bs, int hq, int kv, int n_sel, int res_len,
                                                  int n_splits);
-int zkv_kivi4_sparse_attention(const uint16_t* q, int64_t q_sb, int64_t q_sh, const int32_t* k_codes,
-                               const uint16_t* k_meta, const int32_t* v_codes, const uint16_t* v_meta,
+int zkv_kivi4_sparse_attention(const uint16_t* q, int64_t q_sb, int64_t q_sh, const int32_t* groups,
                                int g_cap, const uint16_t* k_res, const uint16_t* v_res, int r_cap,
                                int bs, int hq, int kv, int n_groups, int res_len, const int64_t* pages,
                                int64_t pg_sb, int64_t pg_sh, int n_sel, float sm_scale, void* out,

@@ -29,12 +29,12 @@ SIGNATURES = {
     "zkv_chunk_encode": (I32, [P, I64, I64, I64, I32, I32, I32, I32, I32, I32,
                                P, P, P, P, P, P]),
     "zkv_kivi4_pack": (I32, [P, I64, I64, I64, P, I64, I64, I64, I32, I32, I32, I32, I32,
-                             P, P, P, P, P]),
+                             P, P]),
     "zkv_kivi4_attention_workspace_size": (SZ, [I32, I32, I32, I32, I32, I32]),
-    "zkv_kivi4_decode_attention": (I32, [P, I64, I64, P, P, P, P, I32, P, P, I32,
+    "zkv_kivi4_decode_attention": (I32, [P, I64, I64, P, I32, P, P, I32,
                                          I32, I32, I32, I32, I32, F32, P, I32, I32,
                                          P, SZ, P]),
-    "zkv_kivi4_attention_partial": (I32, [P, I64, I64, P, P, P, P, I32, P, P, I32,
+    "zkv_kivi4_attention_partial": (I32, [P, I64, I64, P, I32, P, P, I32,
                                           I32, I32, I32, I32, I32, F32, I32, P, SZ, P, P]),
     "zkv_attention_merge": (I32, [P, I32, I32, I32, I32, P, I32, P]),
     "zkv_quest_chunk_score": (I32, [P, P, P, I32, P, I32, I32, I32, I32, P, P]),
@@ -48,7 +48,7 @@ SIGNATURES = {
                                        I32, I32, I32, P]),
     "zkv_page_minmax_f16": (I32, [P, I64, I64, I64, I32, I32, I32, I32, I32, P, P, P]),
     "zkv_kivi4_sparse_attention_workspace_size": (SZ, [I32, I32, I32, I32, I32, I32]),
-    "zkv_kivi4_sparse_attention": (I32, [P, I64, I64, P, P, P, P, I32, P, P, I32, I32, I32, I32, I32,
+    "zkv_kivi4_sparse_attention": (I32, [P, I64, I64, P, I32, P, P, I32, I32, I32, I32, I32,
                                          I32, P, I64, I64, I32, F32, P, I32, I32, P, SZ, P]),
     "zkv_bf16_attention_workspace_size": (SZ, [I32, I32, I32, I32, I32]),
     "zkv_bf16_decode_attention": (I32, [P, I64, I64, P, I64, I64, I64, P, I64, I64, I64, I32, I32, I32, I32,

@@ -55,10 +55,7 @@ constexpr float kNegBig = -1.0e30f;
 struct AttnParams {
   const uint16_t* q;
   int64_t q_sb, q_sh;
-  const int32_t* k_codes;
-  const uint16_t* k_meta;
-  const int32_t* v_codes;
-  const uint16_t* v_meta;
+  const int32_t* groups;  // Format Q records [bs, kv, g_cap, 1280] int32
   const uint16_t* k_res;  // bf16 tiles: token t of (b, kv) at b*kr_sb + kv*kr_sh + t*kr_st
   const uint16_t* v_res;
   int g_cap;
@@ -83,17 +80,20 @@ struct AttnParams {
   int tile_cap;
 };
 
-// One pipeline stage = one 32-token tile as it sits in HBM:
+// One pipeline stage = one 32-token tile, a byte copy of its Format Q record:
 //   [0, 2048)    K code words (lane order)   [2048, 4096) V code words
 //   [4096, 4608) K scale/zero slots          [4608, 5120) V scale/zero
 constexpr int kStageBytes = 5120;
+constexpr int kRecordWords = kStageBytes / 4;
+// cache policy of the tile loads: nt (streamed once, not kept in the caches)
+constexpr int kCachePolicyNT = 2;
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
 // 64 lanes x 16 B from per-lane global addresses straight into LDS at
 // dst + 16*lane (global_load_lds_dwordx4): the prefetch ring costs no VGPRs.
 __device__ __forceinline__ void dma16(const void* src, void* dst) {
-  __builtin_amdgcn_global_load_lds(src, (lds_void_t*)(dst), 16, 0, 0);
+  __builtin_amdgcn_global_load_lds(src, (lds_void_t*)(dst), 16, 0, kCachePolicyNT);
 }
 
 // s_waitcnt vmcnt(n) (gfx9 encoding: vmcnt[3:0] bits 3:0, vmcnt[5:4] bits
@@ -121,16 +121,10 @@ __device__ __forceinline__ u32x4_t ld16(const void* p) {
 
 __device__ __forceinline__ void issue_tile(const AttnParams& p, int64_t bh, int gi, int lane,
                                            uint8_t* stage) {
-  const int64_t tile = bh * p.g_cap + gi;
-  const uint8_t* kc = reinterpret_cast<const uint8_t*>(p.k_codes + tile * 512);
-  const uint8_t* vc = reinterpret_cast<const uint8_t*>(p.v_codes + tile * 512);
-  const uint8_t* km = reinterpret_cast<const uint8_t*>(p.k_meta + tile * 256);
-  const uint8_t* vm = reinterpret_cast<const uint8_t*>(p.v_meta + tile * 256);
-  dma16(kc + 16 * lane, stage);
-  dma16(kc + 1024 + 16 * lane, stage + 1024);
-  dma16(vc + 16 * lane, stage + 2048);
-  dma16(vc + 1024 + 16 * lane, stage + 3072);
-  dma16(lane < 32 ? km + 16 * lane : vm + 16 * (lane - 32), stage + 4096);
+  // the record is 5 contiguous KiB: 5 loads of 64 lanes x 16 B
+  const uint8_t* rec = reinterpret_cast<const uint8_t*>(p.groups + (bh * p.g_cap + gi) * kRecordWords) + 16 * lane;
+#pragma unroll
+  for (int i = 0; i < 5; ++i) dma16(rec + 1024 * i, stage + 1024 * i);
 }
 
 // (a & m) | c in one VOP3 (gfx9 VOP3 takes no literal, so m and c live in VGPRs)
@@ -686,8 +680,7 @@ SplitPlan plan_sparse_splits(int bs, int kv, int n_sel, int res_len, int n_split
   return sp;
 }
 
-int attention_launch(const uint16_t* q, int64_t q_sb, int64_t q_sh, const int32_t* k_codes,
-                     const uint16_t* k_meta, const int32_t* v_codes, const uint16_t* v_meta,
+int attention_launch(const uint16_t* q, int64_t q_sb, int64_t q_sh, const int32_t* groups,
                      int g_cap, const uint16_t* k_res, const uint16_t* v_res, int r_cap, int bs,
                      int hq, int kv, int n_groups, int res_len, float sm_scale, int n_splits,
                      void* workspace, size_t workspace_bytes, int* n_splits_used, void* out,
@@ -715,8 +708,8 @@ int attention_launch(const uint16_t* q, int64_t q_sb, int64_t q_sh, const int32_
               "V strides %lld %lld %lld)", (long long)res.k_sb, (long long)res.k_sh, (long long)res.k_st,
               (long long)res.v_sb, (long long)res.v_sh, (long long)res.v_st);
   ZKV_REQUIRE(sparse != nullptr || n_groups + res_len > 0, "zkv_kivi4_attention: empty context");
-  ZKV_REQUIRE(n_groups == 0 || (k_codes && k_meta && v_codes && v_meta),
-              "zkv_kivi4_attention: null cache pointer");
+  ZKV_REQUIRE(n_groups == 0 || groups, "zkv_kivi4_attention: null cache pointer");
+  ZKV_REQUIRE((reinterpret_cast<uintptr_t>(groups) & 15) == 0, "zkv_kivi4_attention: records must be 16-byte aligned");
   ZKV_REQUIRE(res_len == 0 || (k_res && v_res), "zkv_kivi4_attention: null residual pointer");
   ZKV_REQUIRE((q_sh % 8) == 0 && (q_sb % 8) == 0 && (reinterpret_cast<uintptr_t>(q) & 15) == 0,
               "zkv_kivi4_attention: q rows must be 16-byte aligned");
@@ -737,10 +730,7 @@ int attention_launch(const uint16_t* q, int64_t q_sb, int64_t q_sh, const int32_
   p.q = q;
   p.q_sb = q_sb;
   p.q_sh = q_sh;
-  p.k_codes = k_codes;
-  p.k_meta = k_meta;
-  p.v_codes = v_codes;
-  p.v_meta = v_meta;
+  p.groups = groups;
   p.k_res = k_res;
   p.v_res = v_res;
   p.g_cap = g_cap;
@@ -808,14 +798,13 @@ extern "C" size_t zkv_kivi4_attention_workspace_size(int bs, int hq, int kv, int
 }
 
 extern "C" int zkv_kivi4_attention_partial(const uint16_t* q, int64_t q_sb, int64_t q_sh,
-                                           const int32_t* k_codes, const uint16_t* k_meta,
-                                           const int32_t* v_codes, const uint16_t* v_meta, int g_cap,
+                                           const int32_t* groups, int g_cap,
                                            const uint16_t* k_res, const uint16_t* v_res, int r_cap,
                                            int bs, int hq, int kv, int n_groups, int res_len,
                                            float sm_scale, int n_splits, void* workspace,
                                            size_t workspace_bytes, int* n_splits_used,
                                            zkv_stream_t stream) {
-  return attention_launch(q, q_sb, q_sh, k_codes, k_meta, v_codes, v_meta, g_cap, k_res, v_res,
+  return attention_launch(q, q_sb, q_sh, groups, g_cap, k_res, v_res,
                           r_cap, bs, hq, kv, n_groups, res_len, sm_scale, n_splits, workspace,
                           workspace_bytes, n_splits_used, nullptr, 0,
                           reinterpret_cast<hipStream_t>(stream));
@@ -834,15 +823,14 @@ extern "C" int zkv_attention_merge(const void* workspace, int bs, int hq, int kv
 }
 
 extern "C" int zkv_kivi4_decode_attention(const uint16_t* q, int64_t q_sb, int64_t q_sh,
-                                          const int32_t* k_codes, const uint16_t* k_meta,
-                                          const int32_t* v_codes, const uint16_t* v_meta, int g_cap,
+                                          const int32_t* groups, int g_cap,
                                           const uint16_t* k_res, const uint16_t* v_res, int r_cap,
                                           int bs, int hq, int kv, int n_groups, int res_len,
                                           float sm_scale, void* out, int out_f32, int n_splits,
                                           void* workspace, size_t workspace_bytes,
                                           zkv_stream_t stream) {
   ZKV_REQUIRE(out, "zkv_kivi4_decode_attention: null output");
-  return attention_launch(q, q_sb, q_sh, k_codes, k_meta, v_codes, v_meta, g_cap, k_res, v_res,
+  return attention_launch(q, q_sb, q_sh, groups, g_cap, k_res, v_res,
                           r_cap, bs, hq, kv, n_groups, res_len, sm_scale, n_splits, workspace,
                           workspace_bytes, nullptr, out, out_f32,
                           reinterpret_cast<hipStream_t>(stream));
@@ -858,8 +846,7 @@ extern "C" size_t zkv_kivi4_sparse_attention_workspace_size(int bs, int hq, int 
 }
 
 extern "C" int zkv_kivi4_sparse_attention(const uint16_t* q, int64_t q_sb, int64_t q_sh,
-                                          const int32_t* k_codes, const uint16_t* k_meta,
-                                          const int32_t* v_codes, const uint16_t* v_meta, int g_cap,
+                                          const int32_t* groups, int g_cap,
                                           const uint16_t* k_res, const uint16_t* v_res, int r_cap,
                                           int bs, int hq, int kv, int n_groups, int res_len,
                                           const int64_t* pages, int64_t pg_sb, int64_t pg_sh,
@@ -868,7 +855,7 @@ extern "C" int zkv_kivi4_sparse_attention(const uint16_t* q, int64_t q_sb, int64
                                           zkv_stream_t stream) {
   ZKV_REQUIRE(out, "zkv_kivi4_sparse_attention: null output");
   const SparsePages sp{pages, pg_sb, pg_sh, n_sel};
-  return attention_launch(q, q_sb, q_sh, k_codes, k_meta, v_codes, v_meta, g_cap, k_res, v_res,
+  return attention_launch(q, q_sb, q_sh, groups, g_cap, k_res, v_res,
                           r_cap, bs, hq, kv, n_groups, res_len, sm_scale, n_splits, workspace,
                           workspace_bytes, nullptr, out, out_f32,
                           reinterpret_cast<hipStream_t>(stream), &sp);
@@ -891,7 +878,7 @@ extern "C" int zkv_bf16_decode_attention(const uint16_t* q, int64_t q_sb, int64_
   ZKV_REQUIRE(out, "zkv_bf16_decode_attention: null output");
   ZKV_REQUIRE(n > 0, "zkv_bf16_decode_attention: empty key cache");
   const ResidualLayout rl{k_sb, k_sh, k_st, v_sb, v_sh, v_st};
-  return attention_launch(q, q_sb, q_sh, nullptr, nullptr, nullptr, nullptr, 0, k, v, n, bs, hq, kv, 0,
+  return attention_launch(q, q_sb, q_sh, nullptr, 0, k, v, n, bs, hq, kv, 0,
                           n, sm_scale, n_splits, workspace, workspace_bytes, nullptr, out, out_f32,
                           reinterpret_cast<hipStream_t>(stream), nullptr, &rl, lse);
 }
@@ -934,7 +921,7 @@ extern "C" int zkv_bf16_gather_attention(const uint16_t* q, int64_t q_sb, int64_
               n_rows);
   const ResidualLayout rl{k_sb, k_sh, k_st, v_sb, v_sh, v_st};
   const RowIndex ri{idx, idx_sb, idx_sh, n_idx, tail_start, n_rows};
-  return attention_launch(q, q_sb, q_sh, nullptr, nullptr, nullptr, nullptr, 0, k, v, n_idx + tail_len, bs, hq,
+  return attention_launch(q, q_sb, q_sh, nullptr, 0, k, v, n_idx + tail_len, bs, hq,
                           kv, 0, n_idx + tail_len, sm_scale, n_splits, workspace, workspace_bytes, nullptr, out,
                           out_f32, reinterpret_cast<hipStream_t>(stream), nullptr, &rl, lse, &ri);
 }

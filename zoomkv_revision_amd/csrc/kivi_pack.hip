@@ -67,6 +67,10 @@ __global__ __launch_bounds__(128) void chunk_encode_kernel(
 }
 
 // ------------------------------- Format Q ---------------------------------
+// One 32-token group of one KV head is a 5120-byte record (int32 words):
+//   [0, 512) K code words, [512, 1024) V code words,
+//   [1024, 1152) K scale/zero (fp16 pairs), [1152, 1280) V scale/zero.
+constexpr int kRecordWords = 1280;
 // k_meta slot s of dim-block p holds channel 8p + KSLOT[s]; the inverse map of
 // channel 8p + j is slot 2*(j % 4) + j / 4.  v words: nibble k of word (r, d)
 // holds token VTOK[r][k] = TAU[r][VELEM[k]].
@@ -80,13 +84,17 @@ __constant__ uint8_t kVTok[4][8] = {
 __global__ __launch_bounds__(128) void kivi4_pack_kernel(
     const uint16_t* __restrict__ k, int64_t k_sb, int64_t k_sh, int64_t k_st,
     const uint16_t* __restrict__ v, int64_t v_sb, int64_t v_sh, int64_t v_st, int kv, int g0,
-    int g_cap, int32_t* __restrict__ k_codes, uint16_t* __restrict__ k_meta,
-    int32_t* __restrict__ v_codes, uint16_t* __restrict__ v_meta) {
+    int g_cap, int32_t* __restrict__ groups) {
   __shared__ uint8_t kc[32][128];
   __shared__ uint8_t vc[32][128];
   const int g = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x;
   const int64_t bhg = (static_cast<int64_t>(b) * kv + h) * g_cap + g0 + g;
+  int32_t* const rec = groups + bhg * kRecordWords;
+  int32_t* const k_codes = rec;
+  int32_t* const v_codes = rec + 512;
+  uint16_t* const k_meta = reinterpret_cast<uint16_t*>(rec + 1024);
+  uint16_t* const v_meta = reinterpret_cast<uint16_t*>(rec + 1152);
 
   // ---- K: lane = channel d, 32 tokens of the group ----
   {
@@ -107,7 +115,7 @@ __global__ __launch_bounds__(128) void kivi4_pack_kernel(
     for (int t = 0; t < 32; ++t) kc[t][d] = static_cast<uint8_t>(kivi_code(x[t], mn, safe));
     const int p = d >> 3, j = d & 7;
     const int slot = 2 * (j & 3) + (j >> 2);
-    uint16_t* km = k_meta + bhg * 256 + p * 16;
+    uint16_t* km = k_meta + p * 16;
     km[slot] = f32_to_f16_bits(scale);
     km[8 + slot] = f32_to_f16_bits(mn);
   }
@@ -138,7 +146,7 @@ __global__ __launch_bounds__(128) void kivi4_pack_kernel(
     // token t sits in octet r at element e (TAU[r][e] == t)
     const int r = (t & 15) >> 2;
     const int e = (t & 3) + ((t >> 4) << 2);
-    uint16_t* vm = v_meta + bhg * 256 + (gd * 4 + r) * 16;
+    uint16_t* vm = v_meta + (gd * 4 + r) * 16;
     vm[e] = f32_to_f16_bits(scale);
     vm[8 + e] = f32_to_f16_bits(mn);
   }
@@ -154,7 +162,7 @@ __global__ __launch_bounds__(128) void kivi4_pack_kernel(
     uint32_t word = 0;
 #pragma unroll
     for (int j = 0; j < 8; ++j) word |= static_cast<uint32_t>((cb >> (8 * j)) & 0xF) << (4 * j);
-    k_codes[bhg * 512 + w] = static_cast<int32_t>(word);
+    k_codes[w] = static_cast<int32_t>(word);
   }
   // ---- V words in MFMA lane order: w = j*256 + l*4 + i, l = 16r + c,
   //      word of octet r for channel d = 8c + 4j + i ----
@@ -166,7 +174,7 @@ __global__ __launch_bounds__(128) void kivi4_pack_kernel(
     uint32_t word = 0;
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk) word |= static_cast<uint32_t>(vc[kVTok[r][kk]][d]) << (4 * kk);
-    v_codes[bhg * 512 + w] = static_cast<int32_t>(word);
+    v_codes[w] = static_cast<int32_t>(word);
   }
 }
 
@@ -206,10 +214,9 @@ extern "C" int zkv_chunk_encode(const uint16_t* keys, int64_t k_sb, int64_t k_sh
 
 extern "C" int zkv_kivi4_pack(const uint16_t* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
                               const uint16_t* v, int64_t v_sb, int64_t v_sh, int64_t v_st, int bs,
-                              int kv, int n_groups, int g0, int g_cap, int32_t* k_codes,
-                              uint16_t* k_meta, int32_t* v_codes, uint16_t* v_meta,
+                              int kv, int n_groups, int g0, int g_cap, int32_t* groups,
                               zkv_stream_t stream) {
-  ZKV_REQUIRE(k && v && k_codes && k_meta && v_codes && v_meta, "zkv_kivi4_pack: null pointer");
+  ZKV_REQUIRE(k && v && groups, "zkv_kivi4_pack: null pointer");
   ZKV_REQUIRE(bs > 0 && kv > 0 && n_groups >= 0 && g0 >= 0,
               "zkv_kivi4_pack: bad sizes bs=%d kv=%d n_groups=%d g0=%d", bs, kv, n_groups, g0);
   ZKV_REQUIRE(g0 + n_groups <= g_cap, "zkv_kivi4_pack: group end %d exceeds capacity %d",
@@ -220,6 +227,6 @@ extern "C" int zkv_kivi4_pack(const uint16_t* k, int64_t k_sb, int64_t k_sh, int
   if (n_groups == 0) return ZKV_OK;
   dim3 grid(n_groups, kv, bs);
   kivi4_pack_kernel<<<grid, 128, 0, reinterpret_cast<hipStream_t>(stream)>>>(
-      k, k_sb, k_sh, k_st, v, v_sb, v_sh, v_st, kv, g0, g_cap, k_codes, k_meta, v_codes, v_meta);
+      k, k_sb, k_sh, k_st, v, v_sb, v_sh, v_st, kv, g0, g_cap, groups);
   return check_launch("kivi4_pack_kernel");
 }

@@ -71,15 +71,21 @@ def chunk_encode(keys: torch.Tensor, chunk_size: int, chunk_start: int,
 # ---------------------------------------------------------------------------
 # Format Q
 # ---------------------------------------------------------------------------
+RECORD_WORDS = 1280   # one 32-token group of one KV head: 5120 bytes
+
+
 @dataclass
 class Kivi4Cache:
-    """Device storage of a Format Q cache plus its bf16 residual window."""
-    k_codes: torch.Tensor   # int32   [bs, kv, G_cap, 512] (MFMA lane order)
-    k_meta: torch.Tensor    # float16 [bs, kv, G_cap, 16, 2, 8]
-    v_codes: torch.Tensor   # int32   [bs, kv, G_cap, 512] (MFMA lane order)
-    v_meta: torch.Tensor    # float16 [bs, kv, G_cap, 4, 4, 2, 8]
-    k_res: torch.Tensor     # bf16    [bs, kv, R_cap, 128]
-    v_res: torch.Tensor     # bf16    [bs, kv, R_cap, 128]
+    """Device storage of a Format Q cache plus its bf16 residual window.
+
+    ``groups`` int32 [bs, kv, G_cap, 1280] holds one contiguous 5120-byte
+    record per 32-token group: K codes (words 0-511), V codes (512-1023),
+    K scale/zero (1024-1151) and V scale/zero (1152-1279), each in the decode
+    kernel's MFMA operand order; ``k_codes`` / ``v_codes`` / ``k_meta`` /
+    ``v_meta`` are views of those parts."""
+    groups: torch.Tensor    # int32 [bs, kv, G_cap, 1280]
+    k_res: torch.Tensor     # bf16  [bs, kv, R_cap, 128]
+    v_res: torch.Tensor     # bf16  [bs, kv, R_cap, 128]
     n_groups: int = 0
     res_len: int = 0
 
@@ -88,17 +94,35 @@ class Kivi4Cache:
                  device: torch.device | str = "cuda") -> "Kivi4Cache":
         z = dict(device=device)
         return cls(
-            torch.zeros(bs, kv, g_cap, 512, dtype=torch.int32, **z),
-            torch.zeros(bs, kv, g_cap, 16, 2, 8, dtype=torch.float16, **z),
-            torch.zeros(bs, kv, g_cap, 512, dtype=torch.int32, **z),
-            torch.zeros(bs, kv, g_cap, 4, 4, 2, 8, dtype=torch.float16, **z),
+            torch.zeros(bs, kv, g_cap, RECORD_WORDS, dtype=torch.int32, **z),
             torch.zeros(bs, kv, r_cap, HEAD_DIM, dtype=torch.bfloat16, **z),
             torch.zeros(bs, kv, r_cap, HEAD_DIM, dtype=torch.bfloat16, **z),
         )
 
+    def rows(self, b0: int, b1: int) -> "Kivi4Cache":
+        """The cache of batch rows [b0, b1) (views)."""
+        return Kivi4Cache(self.groups[b0:b1], self.k_res[b0:b1], self.v_res[b0:b1], self.n_groups,
+                          self.res_len)
+
+    @property
+    def k_codes(self) -> torch.Tensor:   # int32 [bs, kv, G_cap, 512]
+        return self.groups[..., 0:512]
+
+    @property
+    def v_codes(self) -> torch.Tensor:   # int32 [bs, kv, G_cap, 512]
+        return self.groups[..., 512:1024]
+
+    @property
+    def k_meta(self) -> torch.Tensor:    # fp16 [bs, kv, G_cap, 16, 2, 8]
+        return self.groups[..., 1024:1152].view(torch.float16).unflatten(-1, (16, 2, 8))
+
+    @property
+    def v_meta(self) -> torch.Tensor:    # fp16 [bs, kv, G_cap, 4, 4, 2, 8]
+        return self.groups[..., 1152:1280].view(torch.float16).unflatten(-1, (4, 4, 2, 8))
+
     @property
     def g_cap(self) -> int:
-        return self.k_codes.shape[2]
+        return self.groups.shape[2]
 
     @property
     def r_cap(self) -> int:
@@ -106,7 +130,7 @@ class Kivi4Cache:
 
     @property
     def shape(self):
-        return self.k_codes.shape[0], self.k_codes.shape[1]
+        return self.groups.shape[0], self.groups.shape[1]
 
     def nbytes_per_token(self) -> int:
         return 160  # K codes 64 + K meta 16 + V codes 64 + V meta 16
@@ -130,8 +154,7 @@ def kivi4_pack(k: torch.Tensor, v: torch.Tensor, cache: Kivi4Cache, g0: int) -> 
         ptr(k), k.stride(0), k.stride(1), k.stride(2),
         ptr(v), v.stride(0), v.stride(1), v.stride(2),
         bs, kv, ng, g0, cache.g_cap,
-        ptr(cache.k_codes), ptr(cache.k_meta), ptr(cache.v_codes), ptr(cache.v_meta),
-        stream_of(k)))
+        ptr(cache.groups), stream_of(k)))
     return ng
 
 
@@ -194,7 +217,7 @@ def kivi4_decode_attention(q: torch.Tensor, cache: Kivi4Cache, n_groups: int | N
     ws = _workspace(q.device, need) if workspace is None else workspace
     check(L.zkv_kivi4_decode_attention(
         ptr(q3), q3.stride(0), q3.stride(1),
-        ptr(cache.k_codes), ptr(cache.k_meta), ptr(cache.v_codes), ptr(cache.v_meta), cache.g_cap,
+        ptr(cache.groups), cache.g_cap,
         ptr(cache.k_res), ptr(cache.v_res), cache.r_cap,
         bs, hq, kv, n_groups, res_len, sm_scale,
         ptr(out), int(out_dtype == torch.float32), n_splits,
@@ -245,7 +268,7 @@ def kivi4_sparse_attention(q: torch.Tensor, cache: Kivi4Cache, pages: torch.Tens
     ws = _workspace(q.device, need) if workspace is None else workspace
     check(L.zkv_kivi4_sparse_attention(
         ptr(q3), q3.stride(0), q3.stride(1),
-        ptr(cache.k_codes), ptr(cache.k_meta), ptr(cache.v_codes), ptr(cache.v_meta), cache.g_cap,
+        ptr(cache.groups), cache.g_cap,
         ptr(cache.k_res), ptr(cache.v_res), cache.r_cap,
         bs, hq, kv, n_groups, res_len, ptr(pages), pages.stride(0), pages.stride(1), n_sel, sm_scale,
         ptr(out), int(out_dtype == torch.float32), n_splits,
@@ -270,7 +293,7 @@ def kivi4_attention_partial(q: torch.Tensor, cache: Kivi4Cache, n_groups: int, r
     used = ctypes.c_int(0)
     check(L.zkv_kivi4_attention_partial(
         ptr(q), q.stride(0), q.stride(1),
-        ptr(cache.k_codes), ptr(cache.k_meta), ptr(cache.v_codes), ptr(cache.v_meta), cache.g_cap,
+        ptr(cache.groups), cache.g_cap,
         ptr(cache.k_res), ptr(cache.v_res), cache.r_cap,
         bs, hq, kv, n_groups, res_len, sm_scale, n_splits,
         ptr(ws), ws.numel() * ws.element_size(), ctypes.addressof(used), stream_of(q)))

@@ -44,9 +44,7 @@ def c2_cache(seed: int, bs: int, kv: int, n_groups: int, res_len: int, device,
         for h in range(kv):
             ch = torch.randperm(HEAD_DIM, generator=g, device=device)[:n_out]
             k[h, :, ch] *= 10.0
-        view = kivi.Kivi4Cache(cache.k_codes[b:b + 1], cache.k_meta[b:b + 1], cache.v_codes[b:b + 1],
-                               cache.v_meta[b:b + 1], cache.k_res[b:b + 1], cache.v_res[b:b + 1])
-        kivi.kivi4_pack(k.to(torch.bfloat16)[None], v.to(torch.bfloat16)[None], view, 0)
+        kivi.kivi4_pack(k.to(torch.bfloat16)[None], v.to(torch.bfloat16)[None], cache.rows(b, b + 1), 0)
         del k, v
     if res_len:
         cache.k_res[:, :, :res_len].copy_(
