@@ -42,11 +42,14 @@ def test_chunk_encode_bit_exact(rng, g):
     assert v[:, :, sl].all() and not v[:, :, :start].any() and not v[:, :, start + 5:].any()
 
 
-def _pack(rng, bs, kv, ng, outliers=1, g_cap=None, g0=0):
+def _pack(rng, bs, kv, ng, outliers=1, g_cap=None, g0=0, v_outliers=None):
+    """Pack seeded K / V.  Attention tests keep V at N(0, 1) (outlier channels
+    are a K phenomenon, as in the benchmark data): the 2e-3 absolute bound is
+    meaningful only for outputs of order one."""
     zk = _zk()
     n = ng * 32
     k = gaussian_bf16(rng, (bs, kv, n, 128), outlier_channels=outliers)
-    v = gaussian_bf16(rng, (bs, kv, n, 128), outlier_channels=outliers)
+    v = gaussian_bf16(rng, (bs, kv, n, 128), outlier_channels=outliers if v_outliers is None else v_outliers)
     cache = zk.Kivi4Cache.allocate(bs, kv, g_cap or ng + g0, 128)
     zk.kivi4_pack(to_bf16(k), to_bf16(v), cache, g0)
     return k, v, cache
@@ -87,7 +90,7 @@ def test_kivi4_pack_strided_input(rng):
 ])
 def test_decode_attention_matches_oracle(rng, bs, hq, kv, ng, res, splits):
     zk = _zk()
-    k, v, cache = _pack(rng, bs, kv, ng, outliers=1) if ng else (None, None, zk.Kivi4Cache.allocate(bs, kv, 1))
+    k, v, cache = _pack(rng, bs, kv, ng, outliers=1, v_outliers=0) if ng else (None, None, zk.Kivi4Cache.allocate(bs, kv, 1))
     kr = gaussian_bf16(rng, (bs, kv, 128, 128))
     vr = gaussian_bf16(rng, (bs, kv, 128, 128))
     cache.k_res.copy_(to_bf16(kr))

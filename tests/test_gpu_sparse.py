@@ -33,7 +33,7 @@ def test_page_minmax_f16_bit_exact(rng):
 def _pack(rng, bs, kv, ng):
     from zoomkv_revision_amd import kivi
     k = gaussian_bf16(rng, (bs, kv, ng * 32, 128), outlier_channels=1)
-    v = gaussian_bf16(rng, (bs, kv, ng * 32, 128), outlier_channels=1)
+    v = gaussian_bf16(rng, (bs, kv, ng * 32, 128))      # outlier channels are a K phenomenon
     cache = kivi.Kivi4Cache.allocate(bs, kv, ng, 128)
     kivi.kivi4_pack(to_bf16(k), to_bf16(v), cache, 0)
     return okivi.quantize_kivi4(k, v), cache
