@@ -159,23 +159,35 @@ __device__ __forceinline__ half8_t dequant8(uint32_t w, const u32x4_t& sc, const
   return a;
 }
 
+__device__ __forceinline__ float vmax(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+
+// Max over the four 16-lane rows, for each lane position c: two gfx950
+// permlane swaps (rows 0<->1 / 2<->3, then halves), no LDS round trip.
 __device__ __forceinline__ float wave_max16(float x) {
-  x = fmaxf(x, __shfl_xor(x, 16));
-  return fmaxf(x, __shfl_xor(x, 32));
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  const float a = vmax(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  const auto r2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(a), false, false);
+  return vmax(__uint_as_float(r2[0]), __uint_as_float(r2[1]));
 }
-__device__ __forceinline__ float wave_sum16(float x) {
-  x = x + __shfl_xor(x, 16);
-  return x + __shfl_xor(x, 32);
-}
+
+// A running max is kept while a tile's max exceeds it by at most this many
+// base-2 units (probabilities up to 2^8 in fp16, exact in relative terms);
+// O and L are rescaled only when some lane's max jumps further.
+constexpr float kLazyMaxBits = 8.0f;
 
 // Online-softmax update for one tile: S holds the raw scores of tokens
 // TAU[g][0..7] for query head c (masked tokens are -inf); qs turns a raw score
 // into a base-2 exponent.  m_run is kept in raw units.  Returns P as the fp16
-// B operand of the V-MFMA and rescales O when a running max moved.
-// v_exp_f32 flushes results below 2^-126 to zero, which only drops
-// probabilities that are already far below fp16 resolution.
+// B operand of the V-MFMA; L accumulates sum(P) with a ones-row MFMA on that
+// same fp16 P (every row of L holds the column sum).  v_exp_f32 flushes
+// results below 2^-126 to zero, which only drops probabilities that are
+// already far below fp16 resolution.
 __device__ __forceinline__ half8_t softmax_step(const float4_t S[2], float qs, float& m_run,
-                                                float& l_run, float4_t O[8]) {
+                                                float4_t& L, float4_t O[8]) {
   float sv[8];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -185,30 +197,28 @@ __device__ __forceinline__ half8_t softmax_step(const float4_t S[2], float qs, f
   float mx = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
                    fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
   mx = wave_max16(mx);
-  const float m_new = fmaxf(m_run, mx);
-  const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * qs);
-  m_run = m_new;
-  const float mq = m_new * qs;
-  half8_t pb;
-  float ps = 0.0f;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const float pe = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[e], qs, -mq));
-    ps += pe;
-    pb[e] = static_cast<_Float16>(pe);
-  }
-  l_run = l_run * alpha + ps;
-  if (__any(alpha != 1.0f)) {
+  const bool up = (mx - m_run) * qs > kLazyMaxBits;
+  if (__any(up)) {
+    const float m_new = up ? mx : m_run;
+    const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * qs);
+    m_run = m_new;
+    L *= alpha;
 #pragma unroll
     for (int j = 0; j < 8; ++j) O[j] *= alpha;
   }
+  const float mq = m_run * qs;
+  half8_t pb;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) pb[e] = static_cast<_Float16>(__builtin_amdgcn_exp2f(__builtin_fmaf(sv[e], qs, -mq)));
+  const half8_t ones = {1, 1, 1, 1, 1, 1, 1, 1};
+  L = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pb, L, 0, 0, 0);
   return pb;
 }
 
 // Tile compute from an LDS stage: K-MFMA, softmax, V-MFMA.
 __device__ __forceinline__ void compute_tile(const uint8_t* st, int lane, int c, int g,
                                              const half8_t qB[4], float qs, const NibbleConsts& nk,
-                                             uint32_t half_mask, float& m_run, float& l_run,
+                                             uint32_t half_mask, float& m_run, float4_t& L,
                                              float4_t O[8]) {
   const u32x4_t kq0 = ld16(st + 16 * lane);
   const u32x4_t kq1 = ld16(st + 1024 + 16 * lane);
@@ -223,7 +233,7 @@ __device__ __forceinline__ void compute_tile(const uint8_t* st, int lane, int c,
   // S[m] holds tokens 16m + 4g + i: drop an unselected page (half)
   if (!(half_mask & 1u)) S[0] = float4_t{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
   if (!(half_mask & 2u)) S[1] = float4_t{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-  const half8_t pb = softmax_step(S, qs, m_run, l_run, O);
+  const half8_t pb = softmax_step(S, qs, m_run, L, O);
   const u32x4_t vq0 = ld16(st + 2048 + 16 * lane);
   const u32x4_t vq1 = ld16(st + 3072 + 16 * lane);
   const uint8_t* vm = st + 4608 + ((c >> 2) * 4 + g) * 32;
@@ -252,7 +262,7 @@ __device__ __forceinline__ int bf16_row(const AttnParams& p, const int64_t* idx_
 // TAU[g][e] (its V-MFMA k-slice), 16 B per row.
 __device__ __forceinline__ void residual_tile(const AttnParams& p, int b, int h, int base, int valid,
                                               int c, int g, const half8_t qB[4], float qs,
-                                              float& m_run, float& l_run, float4_t O[8]) {
+                                              float& m_run, float4_t& L, float4_t O[8]) {
   const uint16_t* kr = p.k_res + b * p.kr_sb + h * p.kr_sh;
   const uint16_t* vr = p.v_res + b * p.vr_sb + h * p.vr_sh;
   const int64_t* idx_bh = p.res_idx ? p.res_idx + b * p.ri_sb + h * p.ri_sh : nullptr;
@@ -287,7 +297,7 @@ __device__ __forceinline__ void residual_tile(const AttnParams& p, int b, int h,
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       if (vrow[i + 4 * m] < 0) S[m][i] = -INFINITY;
-  const half8_t pb = softmax_step(S, qs, m_run, l_run, O);
+  const half8_t pb = softmax_step(S, qs, m_run, L, O);
   // V^T operand: element e = token TAU[g][e], row c of M-tile j = channel 8c + j
   u32x4_t vx[8];
 #pragma unroll
@@ -328,7 +338,9 @@ __attribute__((amdgpu_waves_per_eu(KernelShape<NW, D>::kWavesPerSimd)))
 void kivi4_attn_kernel(const AttnParams p) {
   __shared__ __attribute__((aligned(16))) uint8_t smem[NW][D][kStageBytes];
   const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  // wave index through readfirstlane: the compiler then keeps the ring and
+  // tile bookkeeping in SGPRs (scalar branches, scalar DMA base addresses)
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int c = lane & 15, g = lane >> 4;
   const bool col_ok = c < p.gqa;
   const int64_t bh = static_cast<int64_t>(b) * p.kv + h;
@@ -387,7 +399,8 @@ void kivi4_attn_kernel(const AttnParams p) {
   float4_t O[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) O[j] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
-  float m_run = kNegBig, l_run = 0.0f;
+  float m_run = kNegBig;
+  float4_t L = {0.0f, 0.0f, 0.0f, 0.0f};
 
   // ---- quantized tiles through this wave's D-stage LDS ring ----
   for (int k = 0; k < nq; ++k) {
@@ -397,17 +410,17 @@ void kivi4_attn_kernel(const AttnParams p) {
     }
     const uint32_t half_mask = kSparse ? static_cast<uint32_t>(__builtin_amdgcn_readlane(my_mask, k)) : 3u;
     wait_tiles_in_flight(issued - 1 - k);
-    compute_tile(ring[k % D], lane, c, g, qB, p.qscale, nk, half_mask, m_run, l_run, O);
+    compute_tile(ring[k % D], lane, c, g, qB, p.qscale, nk, half_mask, m_run, L, O);
   }
 
   // ---- bf16 residual tiles (at most r_cap / 32 of them, in the last split) ----
   for (int t = max(T0, n_qt) + wave; t < T1; t += NW) {
     const int base = (t - n_qt) * kTile;
-    residual_tile(p, b, h, base, min(kTile, p.res_len - base), c, g, qB, p.qscale, m_run, l_run, O);
+    residual_tile(p, b, h, base, min(kTile, p.res_len - base), c, g, qB, p.qscale, m_run, L, O);
   }
 
   // ---- merge the NW waves through LDS (the rings are free now) ----
-  const float l_tot = wave_sum16(l_run);
+  const float l_tot = L[0];
   __syncthreads();
   float* red_o = reinterpret_cast<float*>(&smem[0][0][0]);  // [NW][gqa][128]
   float* red_m = red_o + NW * p.gqa * 128;                    // [NW][gqa]
