@@ -68,8 +68,8 @@ int zkv_chunk_encode(const uint16_t* keys, int64_t k_sb, int64_t k_sh, int64_t k
  * one KV head, holding
  *   words [0, 512)      K codes: word m*256 + l*4 + s, l = 16g + c: the
  *           nibbles of channels 8p..8p+7 (p = 4s + g) of token 32G + 16m + c
- *   words [512, 1024)   V codes: word j*256 + l*4 + i, l = 16r + c:
- *           channel 8c + 4j + i, nibble k = token 32G + TAU[r][2(k%4) + k/4]
+ *   words [512, 1024)   V codes: word (j/4)*256 + l*4 + j%4, l = 16r + c:
+ *           channel 32(j/2) + 2c + j%2, nibble k = token 32G + TAU[r][2(k%4) + k/4]
  *   words [1024, 1152)  K scale / zero, fp16 [16, 2, 8] (p, scale|zero, slot):
  *           channel 8p + (0,4,1,5,2,6,3,7)[slot]
  *   words [1152, 1280)  V scale / zero, fp16 [4, 4, 2, 8] (channel group, r,

@@ -25,8 +25,8 @@ need no cross-lane movement:
   k_meta   fp16  [bs, kv, G, 16, 2, 8] [..., p, 0, s] = scale of channel
            8p + KSLOT[s], [..., p, 1, s] = zero (min) of that channel,
            KSLOT = (0, 4, 1, 5, 2, 6, 3, 7)
-  v_codes  int32 [bs, kv, G, 512]  word j*256 + l*4 + i (l = 16g + c) holds, for
-           channel d = 8c + 4j + i, in nibble k the code of token
+  v_codes  int32 [bs, kv, G, 512]  word (j//4)*256 + l*4 + j%4 (l = 16g + c) holds,
+           for channel d = 32(j//2) + 2c + j%2, in nibble k the code of token
            32G + TAU[g][VELEM[k]]
   v_meta   fp16  [bs, kv, G, 4, 4, 2, 8] [..., gd, r, 0, e] = scale of token
            32G + TAU[r][e] for channel group gd (channels 32gd..32gd+31),
@@ -183,17 +183,21 @@ def k_words_from_lane_order(words: np.ndarray) -> np.ndarray:
 
 
 def v_words_to_lane_order(words: np.ndarray) -> np.ndarray:
-    """[.., G, 4 (r), 128 (d)] -> [.., G, 512] lane order (d = 8c + 4j + i)."""
+    """[.., G, 4 (r), 128 (d)] -> [.., G, 512] lane order.
+
+    Word (M-tile j, lane 16r + c) sits at (j // 4) * 256 + (16r + c) * 4 + j % 4
+    and holds channel d = 32 (j // 2) + 2c + j % 2.
+    """
     sh = words.shape[:-2]
-    w = words.reshape(sh + (4, 16, 2, 4))                   # [r, c, j, i]
-    w = np.moveaxis(w, (-4, -3, -2, -1), (-3, -2, -4, -1))  # -> [j, r, c, i]
+    w = words.reshape(sh + (4, 2, 2, 16, 2))                # [r, jh, gl, c, jp], j = 4jh + 2gl + jp
+    w = np.moveaxis(w, (-5, -4, -3, -2, -1), (-4, -5, -2, -3, -1))  # -> [jh, r, c, gl, jp]
     return np.ascontiguousarray(w).reshape(sh + (512,))
 
 
 def v_words_from_lane_order(words: np.ndarray) -> np.ndarray:
     sh = words.shape[:-1]
-    w = words.reshape(sh + (2, 4, 16, 4))                   # [j, r, c, i]
-    w = np.moveaxis(w, (-4, -3, -2, -1), (-2, -4, -3, -1))  # -> [r, c, j, i]
+    w = words.reshape(sh + (2, 4, 16, 2, 2))                # [jh, r, c, gl, jp]
+    w = np.moveaxis(w, (-5, -4, -3, -2, -1), (-4, -5, -2, -3, -1))  # -> [r, jh, gl, c, jp]
     return np.ascontiguousarray(w).reshape(sh + (4, 128))
 
 

@@ -141,7 +141,14 @@ def test_lane_order_relayouts_are_the_documented_bijections(rng):
             for c in range(16):
                 for s in range(4):
                     assert lo[1, m * 256 + (16 * g + c) * 4 + s] == w[1, 4 * s + g, 16 * m + c]
-                    assert lv[2, m * 256 + (16 * g + c) * 4 + s] == v[2, g, 8 * c + 4 * m + s]
+    # V: word of M-tile j, lane 16g + c is channel 32(j // 2) + 2c + j % 2, so
+    # each 16-row M-tile stays inside one 32-channel scale group
+    for j in range(8):
+        for g in range(4):
+            for c in range(16):
+                d = 32 * (j // 2) + 2 * c + j % 2
+                assert lv[2, (j // 4) * 256 + (16 * g + c) * 4 + j % 4] == v[2, g, d]
+                assert d // 32 == j // 2
 
 
 def test_format_q_metadata_and_codes_consistent(rng):

@@ -13,9 +13,16 @@
 //    w walks tiles T0 + w, T0 + w + NW, ... through its own D-stage LDS ring
 //    filled by global_load_lds_dwordx4, so D-1 tiles per wave are in flight
 //    without costing VGPRs;
-//  * nibbles become exact fp16 codes with v_and_or_b32 (0x6400|n = 1024+n,
-//    0x4C00|n<<4 = 16+n/4) and one packed op, and are dequantized with one
-//    v_pk_fma_f16 per pair: code*scale + zero;
+//  * nibbles enter the matrix cores undequantized: one v_and_b32 per pair
+//    turns them into exact fp16 subnormals (n * 2^-24 for the low nibble of a
+//    byte, 16n * 2^-24 for the high one) and the scales move to the B operand:
+//      S[t, c]  = sum_d n[t,d] (q[c,d] s_d)       + sum_d q[c,d] (z_d + 8 s_d) - 8 sum_d q[c,d] s_d
+//      O[d, c] += sum_t n[d,t] (P[t,c] s_t,G(d))  + sum_t P[t,c] z_t,G(d)      - ...
+//    with the fp16-rounded products q*s (per channel) and P*s (per token and
+//    32-channel group) shared by the code MFMA and a "-8" centring MFMA, so
+//    the rounding error is that of (n - 8) * q * s, the size of the error of
+//    rounding code*scale + zero to fp16.  Zero points go through their own
+//    MFMAs on exact fp16 products;
 //  * S^T[t, c] = sum_d Khat[t, d] q[c, d] and O^T[d, c] += sum_t Vhat[d, t] P[t, c]
 //    run on the matrix cores as v_mfma_f32_16x16x32_f16 (query heads on the N
 //    axis).  The Format Q word / metadata order is the MFMA operand order, so
@@ -36,9 +43,13 @@
 // K-MFMA: A = Khat (row = token c + 16m), B = q (column = query head c),
 //   k-slice element e of dim block p = 4s + g is channel 8p + KSLOT[e],
 //   KSLOT = (0,4,1,5,2,6,3,7).
-// V-MFMA (one per j = 0..7): A = Vhat^T (row c = channel 8c + j), B = P,
+// V-MFMA (one per j = 0..7): A = V codes^T (row c = channel 32(j/2) + 2c +
+//   j%2, so each M-tile lies in one 32-channel scale group), B = P * scale,
 //   k-slice element e of lane group g is token TAU[g][e] = 4g+e | 16+4g+e-4,
 //   which is exactly where the K-MFMA left that token's score.
+// Code operand element order (one int32 word, nibble k = bits 4k..4k+3):
+//   (n0, n4, n1, n5, n2, n6, n3, n7); elements 2, 3, 6, 7 carry a factor 16,
+//   which the B operands undo (1/16 on K's, 16 on V's other elements).
 #include "zkv_common.hpp"
 
 #include <algorithm>
@@ -127,37 +138,16 @@ __device__ __forceinline__ void issue_tile(const AttnParams& p, int64_t bh, int 
   for (int i = 0; i < 5; ++i) dma16(rec + 1024 * i, stage + 1024 * i);
 }
 
-// (a & m) | c in one VOP3 (gfx9 VOP3 takes no literal, so m and c live in VGPRs)
-__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t c) {
-  uint32_t r;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(m), "v"(c));
-  return r;
-}
-
-struct NibbleConsts {
-  uint32_t m_lo, m_hi, x_lo, x_hi;
-};
-
-__device__ __forceinline__ half8_t dequant8(uint32_t w, const u32x4_t& sc, const u32x4_t& zr,
-                                            const NibbleConsts& k) {
-  const half2_t m1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
-  const half2_t four = {(_Float16)4.0f, (_Float16)4.0f};
-  const half2_t m64 = {(_Float16)-64.0f, (_Float16)-64.0f};
+// One code word as an MFMA operand of exact fp16 subnormals:
+// (n0, n4) * 2^-24, (n1, n5) * 16 * 2^-24, (n2, n6) * 2^-24, (n3, n7) * 16 * 2^-24.
+// fp16 subnormal inputs are exact on the gfx950 matrix cores.
+__device__ __forceinline__ half8_t codes8(uint32_t w) {
   const uint32_t w8 = w >> 8;
-  half2_t code[4];
-  code[0] = u32_as_half2(and_or(w, k.m_lo, k.x_lo)) + m1024;                                  // n0, n4
-  code[1] = __builtin_elementwise_fma(u32_as_half2(and_or(w, k.m_hi, k.x_hi)), four, m64);    // n1, n5
-  code[2] = u32_as_half2(and_or(w8, k.m_lo, k.x_lo)) + m1024;                                 // n2, n6
-  code[3] = __builtin_elementwise_fma(u32_as_half2(and_or(w8, k.m_hi, k.x_hi)), four, m64);   // n3, n7
-  half8_t a;
-#pragma unroll
-  for (int v = 0; v < 4; ++v) {
-    const half2_t x = __builtin_elementwise_fma(code[v], u32_as_half2(sc[v]), u32_as_half2(zr[v]));
-    a[2 * v] = x[0];
-    a[2 * v + 1] = x[1];
-  }
-  return a;
+  const u32x4_t r = {w & 0x000F000Fu, w & 0x00F000F0u, w8 & 0x000F000Fu, w8 & 0x00F000F0u};
+  return __builtin_bit_cast(half8_t, r);
 }
+
+__device__ __forceinline__ half8_t as_half8(const u32x4_t& x) { return __builtin_bit_cast(half8_t, x); }
 
 __device__ __forceinline__ float vmax(float a, float b) {
   float r;
@@ -175,73 +165,123 @@ __device__ __forceinline__ float wave_max16(float x) {
 }
 
 // A running max is kept while a tile's max exceeds it by at most this many
-// base-2 units (probabilities up to 2^8 in fp16, exact in relative terms);
-// O and L are rescaled only when some lane's max jumps further.
-constexpr float kLazyMaxBits = 8.0f;
+// base-2 units (probabilities up to 2^4 in fp16, exact in relative terms);
+// O, L and OZ are rescaled only when some lane's max jumps further.  The
+// bound also keeps the V-side products 16 * P * scale inside fp16 for scales
+// up to 255 (V ranges up to 3800).
+constexpr float kLazyMaxBits = 4.0f;
 
-// Online-softmax update for one tile: S holds the raw scores of tokens
-// TAU[g][0..7] for query head c (masked tokens are -inf); qs turns a raw score
-// into a base-2 exponent.  m_run is kept in raw units.  Returns P as the fp16
-// B operand of the V-MFMA; L accumulates sum(P) with a ones-row MFMA on that
-// same fp16 P (every row of L holds the column sum).  v_exp_f32 flushes
-// results below 2^-126 to zero, which only drops probabilities that are
-// already far below fp16 resolution.
-__device__ __forceinline__ half8_t softmax_step(const float4_t S[2], float qs, float& m_run,
-                                                float4_t& L, float4_t O[8]) {
+// Online-softmax update for one tile.  The raw score of token TAU[g][e] for
+// query head c is S * sc + bias (masked tokens have S = -inf); qs turns a raw
+// score into a base-2 exponent and qsc = qs * sc.  m_run is kept in raw
+// units.  Returns P as the fp16 B operand of the V-MFMA; L accumulates sum(P)
+// with a ones-row MFMA on that same fp16 P (every row of L holds the column
+// sum).  v_exp_f32 flushes results below 2^-126 to zero, which only drops
+// probabilities that are already far below fp16 resolution.
+__device__ __forceinline__ half8_t softmax_step(const float4_t S[2], float sc, float bias, float qs,
+                                                float qsc, float& m_run, float4_t& L, float4_t O[8],
+                                                float4_t& OZ) {
   float sv[8];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     sv[i] = S[0][i];
     sv[4 + i] = S[1][i];
   }
-  float mx = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
-                   fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
-  mx = wave_max16(mx);
+  const float mx8 = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
+                          fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
+  const float mx = wave_max16(__builtin_fmaf(mx8, sc, bias));
   const bool up = (mx - m_run) * qs > kLazyMaxBits;
   if (__any(up)) {
     const float m_new = up ? mx : m_run;
     const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * qs);
     m_run = m_new;
     L *= alpha;
+    OZ *= alpha;
 #pragma unroll
     for (int j = 0; j < 8; ++j) O[j] *= alpha;
   }
-  const float mq = m_run * qs;
+  const float b2 = (bias - m_run) * qs;
   half8_t pb;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) pb[e] = static_cast<_Float16>(__builtin_amdgcn_exp2f(__builtin_fmaf(sv[e], qs, -mq)));
+  for (int e = 0; e < 8; ++e) pb[e] = static_cast<_Float16>(__builtin_amdgcn_exp2f(__builtin_fmaf(sv[e], qsc, b2)));
   const half8_t ones = {1, 1, 1, 1, 1, 1, 1, 1};
   L = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pb, L, 0, 0, 0);
   return pb;
 }
 
-// Tile compute from an LDS stage: K-MFMA, softmax, V-MFMA.
+constexpr float kTwo20 = 1048576.0f;
+constexpr float kTwo24 = 16777216.0f;
+
+// Per-lane constants of the quantized tiles.
+struct TileConsts {
+  half8_t qB[4];   // q / 8 (K-MFMA B operand for the zero points)
+  half8_t qBm[4];  // q / 8 with 1/16 on elements 2, 3, 6, 7 (times the K scales)
+  half8_t kcen;    // rows c < 8: -8 / -128 (raw-unit K centring); rows c >= 8: 0
+  float qs, qs24;  // raw score -> base-2; the same for 2^-24-unit scores
+};
+
+// Tile compute from an LDS stage.
+//   K: S = sum n * fp16(q s) in 2^-24 units (codes are subnormals);
+//      Z rows c < 8: sum q z - 8 sum fp16(q s) (raw units), rows c >= 8:
+//      sum q s (exact products); score = S * 2^24 + Zlow + 8 Zhigh.
+//   V: O[j] += sum n * fp16(16 P s) - 8 sum fp16(16 P s) in 2^-20 units;
+//      OZ rows with bit 2 clear: sum P z of group (row & 3), set: sum P s.
 __device__ __forceinline__ void compute_tile(const uint8_t* st, int lane, int c, int g,
-                                             const half8_t qB[4], float qs, const NibbleConsts& nk,
-                                             uint32_t half_mask, float& m_run, float4_t& L,
-                                             float4_t O[8]) {
+                                             const TileConsts& tc, uint32_t half_mask,
+                                             float& m_run, float4_t& L, float4_t O[8],
+                                             float4_t& OZ) {
   const u32x4_t kq0 = ld16(st + 16 * lane);
   const u32x4_t kq1 = ld16(st + 1024 + 16 * lane);
   float4_t S[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
+  float4_t Z = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
     const uint8_t* km = st + 4096 + (4 * s + g) * 32;
-    const u32x4_t ks = ld16(km), kz = ld16(km + 16);
-    S[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(dequant8(kq0[s], ks, kz, nk), qB[s], S[0], 0, 0, 0);
-    S[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(dequant8(kq1[s], ks, kz, nk), qB[s], S[1], 0, 0, 0);
+    const u32x4_t ks = ld16(km);
+    const u32x4_t kzs = ld16(km + (c < 8 ? 16 : 0));  // zero points (rows < 8) or scales
+    const half8_t bp = as_half8(ks) * tc.qBm[s];
+    Z = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(kzs), tc.qB[s], Z, 0, 0, 0);
+    Z = __builtin_amdgcn_mfma_f32_16x16x32_f16(tc.kcen, bp, Z, 0, 0, 0);
+    S[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(codes8(kq0[s]), bp, S[0], 0, 0, 0);
+    S[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(codes8(kq1[s]), bp, S[1], 0, 0, 0);
   }
+  // rows 0-7 sit in lanes g < 2, rows 8-15 in lanes g >= 2
+  const auto zr = __builtin_amdgcn_permlane32_swap(__float_as_uint(Z[0]), __float_as_uint(Z[0]), false, false);
+  const float zc = __builtin_fmaf(8.0f, __uint_as_float(zr[1]), __uint_as_float(zr[0]));
   // S[m] holds tokens 16m + 4g + i: drop an unselected page (half)
   if (!(half_mask & 1u)) S[0] = float4_t{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
   if (!(half_mask & 2u)) S[1] = float4_t{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-  const half8_t pb = softmax_step(S, qs, m_run, L, O);
+  const half8_t pb = softmax_step(S, kTwo24, zc, tc.qs, tc.qs24, m_run, L, O, OZ);
+
   const u32x4_t vq0 = ld16(st + 2048 + 16 * lane);
   const u32x4_t vq1 = ld16(st + 3072 + 16 * lane);
-  const uint8_t* vm = st + 4608 + ((c >> 2) * 4 + g) * 32;
-  const u32x4_t vs = ld16(vm), vz = ld16(vm + 16);
+  const uint8_t* vm = st + 4608;
+  const u32x4_t vzs = ld16(vm + ((c & 3) * 4 + g) * 32 + ((c & 4) ? 0 : 16));
+  OZ = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(vzs), pb, OZ, 0, 0, 0);
+  // P * 16 on the low-nibble elements 0, 1, 4, 5
+  half8_t pm = pb;
+  const half2_t sixteen = {(_Float16)16.0f, (_Float16)16.0f};
+  {
+    half2_t a = {pb[0], pb[1]}, b2 = {pb[4], pb[5]};
+    a = a * sixteen;
+    b2 = b2 * sixteen;
+    pm[0] = a[0];
+    pm[1] = a[1];
+    pm[4] = b2[0];
+    pm[5] = b2[1];
+  }
+  const u32x4_t vcen_bits = {0x80088008u, 0x80808080u, 0x80088008u, 0x80808080u};  // -8, -128 (x 2^-24)
+  const half8_t vcen = as_half8(vcen_bits);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    O[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(dequant8(vq0[j], vs, vz, nk), pb, O[j], 0, 0, 0);
-    O[4 + j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(dequant8(vq1[j], vs, vz, nk), pb, O[4 + j], 0, 0, 0);
+  for (int G = 0; G < 4; ++G) {
+    const half8_t bv = as_half8(ld16(vm + (4 * G + g) * 32)) * pm;
+#pragma unroll
+    for (int jp = 0; jp < 2; ++jp) {
+      const int j = 2 * G + jp;
+      const uint32_t w = j < 4 ? vq0[j] : vq1[j - 4];
+      O[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(codes8(w), bv, O[j], 0, 0, 0);
+      O[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vcen, bv, O[j], 0, 0, 0);
+    }
   }
 }
 
@@ -262,7 +302,8 @@ __device__ __forceinline__ int bf16_row(const AttnParams& p, const int64_t* idx_
 // TAU[g][e] (its V-MFMA k-slice), 16 B per row.
 __device__ __forceinline__ void residual_tile(const AttnParams& p, int b, int h, int base, int valid,
                                               int c, int g, const half8_t qB[4], float qs,
-                                              float& m_run, float4_t& L, float4_t O[8]) {
+                                              float& m_run, float4_t& L, float4_t O[8],
+                                              float4_t& OZ) {
   const uint16_t* kr = p.k_res + b * p.kr_sb + h * p.kr_sh;
   const uint16_t* vr = p.v_res + b * p.vr_sb + h * p.vr_sh;
   const int64_t* idx_bh = p.res_idx ? p.res_idx + b * p.ri_sb + h * p.ri_sh : nullptr;
@@ -297,13 +338,19 @@ __device__ __forceinline__ void residual_tile(const AttnParams& p, int b, int h,
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       if (vrow[i + 4 * m] < 0) S[m][i] = -INFINITY;
-  const half8_t pb = softmax_step(S, qs, m_run, L, O);
-  // V^T operand: element e = token TAU[g][e], row c of M-tile j = channel 8c + j
+  const half8_t pb = softmax_step(S, 1.0f, 0.0f, qs, qs, m_run, L, O, OZ);
+  // V^T operand: element e = token TAU[g][e], row c of M-tile j = channel
+  // 32(j/2) + 2c + j%2 (the quantized tiles' row order): dword 16(j/2) + c of
+  // the row, half j%2
   u32x4_t vx[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     vx[e] = u32x4_t{0u, 0u, 0u, 0u};
-    if (vrow[e] >= 0) vx[e] = ld16(vr + vrow[e] * p.vr_st + 8 * c);
+    if (vrow[e] >= 0) {
+      const uint32_t* row = reinterpret_cast<const uint32_t*>(vr + vrow[e] * p.vr_st) + c;
+#pragma unroll
+      for (int G = 0; G < 4; ++G) vx[e][G] = row[16 * G];
+    }
   }
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
@@ -379,7 +426,8 @@ void kivi4_attn_kernel(const AttnParams p) {
     }
 
   // ---- q as the K-MFMA B operand (element e of block 4s+g = channel 8(4s+g)+KSLOT[e]) ----
-  half8_t qB[4];
+  TileConsts tc;
+  half8_t (&qB)[4] = tc.qB;
   {
     const uint16_t* qp = p.q + b * p.q_sb + static_cast<int64_t>(h * p.gqa + (col_ok ? c : 0)) * p.q_sh;
     constexpr int kslot[8] = {0, 4, 1, 5, 2, 6, 3, 7};
@@ -394,11 +442,21 @@ void kivi4_attn_kernel(const AttnParams p) {
       }
     }
   }
-  const NibbleConsts nk = {0x000F000Fu, 0x00F000F0u, 0x64006400u, 0x4C004C00u};
+  {
+    const half8_t inv16 = {1, 1, 0.0625, 0.0625, 1, 1, 0.0625, 0.0625};
+    const half8_t cen = {-8, -8, -128, -128, -8, -8, -128, -128};
+    const half8_t zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int s = 0; s < 4; ++s) tc.qBm[s] = qB[s] * inv16;
+    tc.kcen = c < 8 ? cen : zero8;
+    tc.qs = p.qscale;
+    tc.qs24 = p.qscale * kTwo24;
+  }
 
   float4_t O[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) O[j] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  float4_t OZ = {0.0f, 0.0f, 0.0f, 0.0f};
   float m_run = kNegBig;
   float4_t L = {0.0f, 0.0f, 0.0f, 0.0f};
 
@@ -410,13 +468,28 @@ void kivi4_attn_kernel(const AttnParams p) {
     }
     const uint32_t half_mask = kSparse ? static_cast<uint32_t>(__builtin_amdgcn_readlane(my_mask, k)) : 3u;
     wait_tiles_in_flight(issued - 1 - k);
-    compute_tile(ring[k % D], lane, c, g, qB, p.qscale, nk, half_mask, m_run, L, O);
+    compute_tile(ring[k % D], lane, c, g, tc, half_mask, m_run, L, O, OZ);
+  }
+  // O to real units: O * 2^20 + sum P z + 8 sum P s of the row's group (OZ
+  // holds the z sums in rows with bit 2 clear = lanes of even g, the s sums in
+  // the others; group = row & 3 = component)
+  {
+    float zw[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(OZ[i]), __float_as_uint(OZ[i]), false, false);
+      zw[i] = __builtin_fmaf(8.0f, __uint_as_float(r[1]), __uint_as_float(r[0]));
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) O[j][i] = __builtin_fmaf(O[j][i], kTwo20, zw[j >> 1]);
   }
 
   // ---- bf16 residual tiles (at most r_cap / 32 of them, in the last split) ----
   for (int t = max(T0, n_qt) + wave; t < T1; t += NW) {
     const int base = (t - n_qt) * kTile;
-    residual_tile(p, b, h, base, min(kTile, p.res_len - base), c, g, qB, p.qscale, m_run, L, O);
+    residual_tile(p, b, h, base, min(kTile, p.res_len - base), c, g, qB, p.qscale, m_run, L, O, OZ);
   }
 
   // ---- merge the NW waves through LDS (the rings are free now) ----
@@ -426,12 +499,12 @@ void kivi4_attn_kernel(const AttnParams p) {
   float* red_m = red_o + NW * p.gqa * 128;                    // [NW][gqa]
   float* red_l = red_m + NW * p.gqa;                          // [NW][gqa]
   if (col_ok) {
-    float* o = red_o + (wave * p.gqa + c) * 128 + 32 * g;
+    float* o = red_o + (wave * p.gqa + c) * 128 + 8 * g;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      // lane holds channels 8(4g+i)+j = 32g + 8i + j for j = 0..7
-      *reinterpret_cast<float4_t*>(o + 8 * i) = float4_t{O[0][i], O[1][i], O[2][i], O[3][i]};
-      *reinterpret_cast<float4_t*>(o + 8 * i + 4) = float4_t{O[4][i], O[5][i], O[6][i], O[7][i]};
+    for (int G = 0; G < 4; ++G) {
+      // O[2G + jp][i] is channel 32G + 8g + 2i + jp
+      *reinterpret_cast<float4_t*>(o + 32 * G) = float4_t{O[2 * G][0], O[2 * G + 1][0], O[2 * G][1], O[2 * G + 1][1]};
+      *reinterpret_cast<float4_t*>(o + 32 * G + 4) = float4_t{O[2 * G][2], O[2 * G + 1][2], O[2 * G][3], O[2 * G + 1][3]};
     }
     if (g == 0) {
       red_m[wave * p.gqa + c] = m_run * p.qscale;  // base-2 scaled units from here on

@@ -164,13 +164,14 @@ __global__ __launch_bounds__(128) void kivi4_pack_kernel(
     for (int j = 0; j < 8; ++j) word |= static_cast<uint32_t>((cb >> (8 * j)) & 0xF) << (4 * j);
     k_codes[w] = static_cast<int32_t>(word);
   }
-  // ---- V words in MFMA lane order: w = j*256 + l*4 + i, l = 16r + c,
-  //      word of octet r for channel d = 8c + 4j + i ----
+  // ---- V words in MFMA lane order: w = (j/4)*256 + l*4 + j%4, l = 16r + c,
+  //      word of octet r for channel d = 32(j/2) + 2c + j%2 (M-tile j, row c:
+  //      every M-tile inside one 32-channel scale group) ----
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int w = tid + 128 * i;
-    const int j = w >> 8, l = (w >> 2) & 63, ii = w & 3;
-    const int r = l >> 4, d = 8 * (l & 15) + 4 * j + ii;
+    const int j = 4 * (w >> 8) + (w & 3), l = (w >> 2) & 63;
+    const int r = l >> 4, d = 32 * (j >> 1) + 2 * (l & 15) + (j & 1);
     uint32_t word = 0;
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk) word |= static_cast<uint32_t>(vc[kVTok[r][kk]][d]) << (4 * kk);
