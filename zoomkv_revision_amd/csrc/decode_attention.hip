@@ -408,6 +408,9 @@ void kivi4_attn_kernel(const AttnParams p) {
       my_group = p.tile_group[ti];
       my_mask = p.tile_mask[ti];
     }
+    // the tile addresses need the list anyway; waiting here (a wait the
+    // compiler sees) keeps it from draining the ring at the mask's first use
+    wait_vmcnt<0>();
   }
   auto group_of = [&](int k) {
     if constexpr (kSparse)
