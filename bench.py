@@ -86,22 +86,18 @@ def read_traffic():
         return None
 
 
-def timed_loop(step, steps: int, warmup: int):
-    """Warm up, then time `steps` calls of step(i, ev) bracketed by device
-    synchronisation; ev = a pair of events the step records around its
-    dominant kernel.  Returns (ms per step, mean dominant-kernel ms)."""
+def timed_loop(step, steps: int, warmup: int) -> float:
+    """Warm up, then time `steps` calls of step(i) bracketed by device
+    synchronisation; returns wall-clock ms per step."""
     import torch
     for i in range(warmup):
-        step(i, None)
-    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-              for _ in range(steps)]
+        step(i)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(steps):
-        step(i, events[i])
+        step(i)
     torch.cuda.synchronize()
-    ms = (time.perf_counter() - t0) * 1e3 / steps
-    return ms, statistics.mean(a.elapsed_time(b) for a, b in events)
+    return (time.perf_counter() - t0) * 1e3 / steps
 
 
 def kernel_batch_ms(launch, n: int) -> float:
@@ -120,6 +116,83 @@ def kernel_batch_ms(launch, n: int) -> float:
     e1.record()
     e1.synchronize()
     return e0.elapsed_time(e1) / n
+
+
+def run_c1(args):
+    """C1: one layer, batch 1, 32 / 8 heads, 4096 tokens: KIVI 4-bit pack of the
+    first 3968 tokens (124 groups), the 128-token bf16 residual window, then
+    decode attention for one query token (inputs seeded on the CPU, seed 42)."""
+    import torch
+    from zoomkv_revision_amd import kivi, synthetic
+    w = synthetic.c1_workload(42)
+    nq, ng, res = w["n_quant"], w["n_groups"], w["res_len"]
+    dev = torch.device("cuda:0")
+    kd, vd, qd = w["k"].to(dev), w["v"].to(dev), w["q"].to(dev)
+    cache = kivi.Kivi4Cache.allocate(1, 8, ng, res, device=dev)
+    out = torch.empty(1, 32, 128, dtype=torch.bfloat16, device=dev)
+    ws = kivi.attention_workspace(1, 32, 8, ng, res, 0, device=dev)
+
+    def step(i):
+        kivi.kivi4_pack(kd[:, :, :nq], vd[:, :, :nq], cache, 0)
+        cache.k_res[:, :, :res].copy_(kd[:, :, nq:])
+        cache.v_res[:, :, :res].copy_(vd[:, :, nq:])
+        kivi.kivi4_decode_attention(qd, cache, ng, res, out=out, workspace=ws)
+
+    ms = timed_loop(step, args.steps, args.warmup)
+    k_ms = kernel_batch_ms(lambda i: kivi.kivi4_pack(kd[:, :, :nq], vd[:, :, :nq], cache, 0), args.steps)
+    pack_bytes = 8 * nq * 512 + 8 * nq * 160          # bf16 K/V in, Format Q out
+    attn_bytes = 8 * nq * 160 + 8 * res * 512 + 2 * 32 * 128 * 2
+    cpu = None if args.no_cpu else c1_cpu_baseline(w)
+    return {
+        "metric": "C1 one layer: KIVI 4-bit pack + decode attention, layer calls/s",
+        "value": 1.0 / (ms * 1e-3), "unit": "layer calls/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16 -> u4 codes + fp16 scale/zero; u4->fp16 attention (fp32 accumulate)",
+        "data": "synthetic (seed 42, CPU generator)",
+        "config": {"workload": "C1: pack 3968 tokens (124 groups) + 128-token bf16 residual + decode attention",
+                   "batch": 1, "q_heads": 32, "kv_heads": 8, "head_dim": 128, "context": 4096,
+                   "outlier_key_channels": 4, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": pack_bytes / (k_ms * 1e-3) / 1e9, "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": pack_bytes / (k_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, "traffic": None,
+                     "kernel": "kivi4_pack_kernel", "kernel_ms": k_ms, "algorithmic_bytes": pack_bytes},
+        "algorithmic_bytes_per_step": {"pack": pack_bytes, "attention": attn_bytes},
+        "cpu_baseline": cpu,
+    }
+
+
+def c1_cpu_baseline(w, budget_s: float = 20.0):
+    """numpy oracle of the whole C1 step (pack + attention) at full shape, timed
+    with one thread and with every host core."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+    from oracle import kivi as okivi
+    k, v, q = w["k"].float().numpy(), w["v"].float().numpy(), w["q"].float().numpy()
+    nq, ng, res = w["n_quant"], w["n_groups"], w["res_len"]
+
+    def once():
+        c = okivi.quantize_kivi4(k[:, :, :nq], v[:, :, :nq])
+        okivi.kivi4_decode_attention(q, c, ng, k[:, :, nq:], v[:, :, nq:], res, 1 / np.sqrt(128),
+                                     dtype=np.float32)
+
+    res_t = {}
+    for threads in (1, os.cpu_count()):
+        times = []
+        with threadpool_limits(limits=threads):
+            once()
+            t_end = time.perf_counter() + budget_s / 2
+            while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 20):
+                t0 = time.perf_counter()
+                once()
+                times.append(time.perf_counter() - t0)
+        res_t[threads] = (statistics.median(times), len(times))
+    t1, n1 = res_t[1]
+    tn, nn = res_t[os.cpu_count()]
+    return {"value": 1.0 / t1, "unit": "layer calls/s", "cores": 1, "kind": "port",
+            "all_cores": {"value": 1.0 / tn, "cores": os.cpu_count()},
+            "sample": f"numpy oracle of the full C1 step (Format Q pack of 3968 tokens x 8 heads + "
+                      f"float32 attention of 32 heads over 4096 tokens); median of {n1} calls "
+                      f"({t1 * 1e3:.0f} ms) on 1 thread, {nn} calls ({tn * 1e3:.0f} ms) on "
+                      f"{os.cpu_count()} threads"}
 
 
 def run_c3(args):
@@ -141,20 +214,16 @@ def run_c3(args):
     out = torch.empty(bs, hq, 128, dtype=torch.bfloat16, device=dev)
     sel_ok = []
 
-    def step(i, ev):
+    def step(i):
         w = ws[i % len(ws)]
         gqa_mean_query(w["q"], kv, out=raw_q)
-        if ev is not None:
-            ev[0].record()
         quest_chunk_score(raw_q, w["page_min"], w["page_max"], scores, n_pages)
-        if ev is not None:
-            ev[1].record()
         sel = float_topk_3d(scores, n_sel)
         kivi.kivi4_sparse_attention(w["q"], w["cache"], sel, out=out)
         if i < len(ws):
             sel_ok.append(sel)
 
-    ms, _ = timed_loop(step, args.steps, args.warmup)
+    ms = timed_loop(step, args.steps, args.warmup)
     k_ms = kernel_batch_ms(lambda i: quest_chunk_score(raw_q, ws[i % len(ws)]["page_min"],
                                                        ws[i % len(ws)]["page_max"], scores, n_pages),
                            args.steps)
@@ -240,15 +309,11 @@ def run_c4(args):
     qs = synthetic.c4_keys(7, nq, 64, dev)
     ws = rabitq.search_workspace(1, nq, n, topk, dev)
 
-    def step(i, ev):
+    def step(i):
         keys, codes, fac = pools[i % n_pools]
-        if ev is not None:
-            ev[0].record()
         rabitq.rabitq_search(qs, keys, codes, fac, signs, topk, workspace=ws)
-        if ev is not None:
-            ev[1].record()
 
-    ms, _ = timed_loop(step, args.steps, args.warmup)
+    ms = timed_loop(step, args.steps, args.warmup)
     k_ms = kernel_batch_ms(lambda i: rabitq.rabitq_search(qs, *pools[i % n_pools][:3], signs, topk, workspace=ws),
                            args.steps)
     algo = n * 20 + nq * topk * 256 + nq * 128 * 2 + nq * topk * 20
@@ -304,8 +369,8 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--splits", type=int, default=0)
-    ap.add_argument("--config", choices=["c2", "c3", "c4"], default="c2",
-                    help="c2 (default, the headline line), c3 or c4")
+    ap.add_argument("--config", choices=["c1", "c2", "c3", "c4"], default="c2",
+                    help="c2 (default, the headline line), c1, c3 or c4")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run 5 device copies of 1 GiB (scale reference for rocprof "
@@ -321,7 +386,8 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     if args.config != "c2":
-        print(json.dumps(run_c3(args) if args.config == "c3" else run_c4(args)))
+        run = {"c1": run_c1, "c3": run_c3, "c4": run_c4}[args.config]
+        print(json.dumps(run(args)))
         return
     if args.calibrate_copy:
         src = torch.ones(1 << 28, dtype=torch.float32, device=dev)      # 1 GiB

@@ -165,3 +165,31 @@ def test_decode_attention_rejects_bad_shapes(rng):
         zk.kivi4_decode_attention(q, cache, 5, 0)          # n_groups > capacity
     with pytest.raises(RuntimeError):
         zk.kivi4_decode_attention(q, cache, 0, 0)          # empty context
+
+
+def test_c1_full_shape_pack_and_attention():
+    """Configuration C1 at its full shape: batch 1, 32 / 8 heads, 4096 tokens
+    (124 groups of 32 packed, 128 bf16 residual), 4 key outlier channels x10,
+    seed 42 -- pack bit-exact, attention within 2e-3 of the oracle."""
+    zk = _zk()
+    from zoomkv_revision_amd import synthetic
+    w = synthetic.c1_workload(42)
+    nq, ng, res = w["n_quant"], w["n_groups"], w["res_len"]
+    k = w["k"].float().numpy()
+    v = w["v"].float().numpy()
+    q = w["q"].float().numpy()
+    cache = zk.Kivi4Cache.allocate(1, 8, ng, res)
+    kd, vd = w["k"].cuda(), w["v"].cuda()
+    zk.kivi4_pack(kd[:, :, :nq], vd[:, :, :nq], cache, 0)
+    cache.k_res[:, :, :res].copy_(kd[:, :, nq:])
+    cache.v_res[:, :, :res].copy_(vd[:, :, nq:])
+    out = zk.kivi4_decode_attention(w["q"].cuda(), cache, ng, res, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    ref_cache = okivi.quantize_kivi4(k[:, :, :nq], v[:, :, :nq])
+    assert np.array_equal(from_torch(cache.k_codes), ref_cache.k_codes)
+    assert np.array_equal(from_torch(cache.k_meta), ref_cache.k_meta)
+    assert np.array_equal(from_torch(cache.v_codes), ref_cache.v_codes)
+    assert np.array_equal(from_torch(cache.v_meta), ref_cache.v_meta)
+    ref = okivi.kivi4_decode_attention(q, ref_cache, ng, k[:, :, nq:], v[:, :, nq:], res, 1 / np.sqrt(128))
+    err = np.abs(from_torch(out) - ref).max()
+    assert err <= ATOL, f"max abs err {err}"

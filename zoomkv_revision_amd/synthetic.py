@@ -2,6 +2,10 @@
 checkpoints are available offline; shapes follow the reference's headline
 configurations).
 
+* C1: one layer, batch 1, 32 / 8 heads, 4096 tokens of N(0, 1) bf16 K / V with
+  4 key channels x10 (the same channels for every head); the first 3968
+  tokens (124 groups of 32) go to the 4-bit cache, the last 128 stay bf16.
+
 * C2: Format Q cache of Gaussian bf16 K/V with 1% outlier K channels x10 plus
   a bf16 residual window (fused 4-bit decode attention).
 * C3: paged 4-bit cache with per-page fp16 Quest min/max and planted pages:
@@ -28,6 +32,21 @@ def _gen(seed: int, device) -> torch.Generator:
     g = torch.Generator(device=device)
     g.manual_seed(seed)
     return g
+
+
+def c1_workload(seed: int = 42) -> dict:
+    """C1 inputs on the CPU (torch.Generator seeded on the CPU, as the
+    measurement definition asks): q [1, 32, 128], k / v [1, 8, 4096, 128]
+    bf16, the outlier channels, and the quantized / residual split."""
+    g = torch.Generator()
+    g.manual_seed(seed)
+    q = torch.randn(1, 32, HEAD_DIM, generator=g).to(torch.bfloat16)
+    k = torch.randn(1, 8, 4096, HEAD_DIM, generator=g)
+    v = torch.randn(1, 8, 4096, HEAD_DIM, generator=g)
+    ch = torch.randperm(HEAD_DIM, generator=g)[:4]
+    k[..., ch] *= 10.0
+    return {"q": q, "k": k.to(torch.bfloat16), "v": v.to(torch.bfloat16), "outlier_channels": ch,
+            "n_quant": 3968, "n_groups": 124, "res_len": 128}
 
 
 def c2_cache(seed: int, bs: int, kv: int, n_groups: int, res_len: int, device,
