@@ -100,16 +100,16 @@ def timed_loop(step, steps: int, warmup: int) -> float:
     return (time.perf_counter() - t0) * 1e3 / steps
 
 
-def kernel_batch_ms(launch, n: int) -> float:
+def kernel_batch_ms(launch, n: int, host_us: float = 100.0) -> float:
     """Mean device time of the dominant kernel: n back-to-back launches between
-    one pair of events on the launch stream.  A short spin kernel ahead of the
-    batch lets the host queue all n launches first, so host launch gaps are
-    not counted (the figure rocprof's dispatch durations give)."""
+    one pair of events on the launch stream.  A spin kernel ahead of the batch
+    (host_us per launch) lets the host queue all n launches first, so host
+    launch gaps are not counted (the figure rocprof's dispatch durations give)."""
     import torch
     launch(0)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda._sleep(int(2e5) * n)  # ~100 us per queued launch at ~2 GHz
+    torch.cuda._sleep(int(2e3 * host_us) * n)  # ~2 GHz
     e0.record()
     for i in range(n):
         launch(i)
@@ -193,6 +193,79 @@ def c1_cpu_baseline(w, budget_s: float = 20.0):
                       f"float32 attention of 32 heads over 4096 tokens); median of {n1} calls "
                       f"({t1 * 1e3:.0f} ms) on 1 thread, {nn} calls ({tn * 1e3:.0f} ms) on "
                       f"{os.cpu_count()} threads"}
+
+
+def run_c5(args):
+    """C5: full decode step, Qwen3-4B geometry (36 layers, 32 / 8 heads of 128,
+    hidden 2560, FFN 9728, vocabulary 151936) with random-init bf16 weights,
+    batch 4, 65536-token context in polar_cache (production knobs: chunk 16,
+    dynamic candidate ratio, CDS 0.3 / 8 / 8, sink 64, local 256, top-100,
+    update interval 512, full-attention threshold 2048), sampling at
+    temperature 0.6 / top-p 0.95 / top-k 20, seed 42."""
+    import torch
+    from zoomkv_revision_amd import decode_step as ds
+    ds.apply_production_env()
+    geo = ds.Qwen3Geometry()
+    batch, context, interval, threshold = 4, 65536, 512, 2048
+    dev = torch.device("cuda:0")
+    max_new = args.warmup + args.steps + 64
+    t0 = time.perf_counter()
+    model = ds.RandomQwen3(geo, dev, seed=42)
+    cache = ds.build_cache(geo, batch, context, max_new, interval, threshold, dev)
+    ds.fill_cache(cache, geo, batch, context, 43, dev)
+    torch.cuda.synchronize()
+    setup_s = time.perf_counter() - t0
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(42)
+    state = {"tok": torch.randint(0, geo.vocab, (batch,), generator=gen, device=dev)}
+
+    def step(i):
+        logits = model.decode_step(state["tok"], cache)
+        state["tok"] = ds.sample_next_token(logits, 0.6, 0.95, 20, generator=gen)
+
+    ms = timed_loop(step, args.steps, args.warmup)
+    flushes = cache._decode_step_counter // interval
+    # device time of one step and of its attention path alone (36 x cache.compute),
+    # each queued behind a spin kernel so host launch gaps are not counted
+    step_ms = kernel_batch_ms(step, 8, host_us=20000.0)
+    qs = [torch.randn(batch, 1, geo.heads, geo.head_dim, device=dev).to(torch.bfloat16) for _ in range(geo.layers)]
+
+    def attn_pass(i):
+        for ldx in range(geo.layers):
+            cache.compute(qs[ldx], ldx)
+
+    attn_ms = kernel_batch_ms(attn_pass, 8, host_us=15000.0)
+    per_layer = [ds.attention_path_bytes(cache, ldx) for ldx in range(geo.layers)]
+    attn_bytes = sum(p["total"] for p in per_layer)
+    weight_bytes = model.parameter_bytes()
+    return {
+        "metric": "C5 full decode step (Qwen3-4B geometry, 36 layers): per-token latency, tokens/s",
+        "value": batch / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16 model; 4-bit K (Format R) stage-2 scoring + bf16 K/V attention",
+        "data": "synthetic (random-init weights seed 42; cache prefilled with seeded N(0,1) K/V)",
+        "config": {"workload": "C5: one decode token through 36 layers + sampling, polar_cache sparse path",
+                   "batch": batch, "context": context, "layers": geo.layers, "hidden": geo.hidden,
+                   "ffn": geo.ffn, "vocab": geo.vocab, "q_heads": geo.heads, "kv_heads": geo.kv_heads,
+                   "head_dim": geo.head_dim, "update_interval": interval, "full_attention_threshold": threshold,
+                   "sampling": {"temperature": 0.6, "top_p": 0.95, "top_k": 20, "seed": 42},
+                   "attention_path": "polar_cache.compute: Quest stage 1 + CDS density + KIVI 4-bit stage 2 "
+                                     "+ top-100 + gather-free bf16 attention",
+                   "parallelism": "single GPU"},
+        "per_token_latency_ms": ms,
+        "flushes_in_timed_region": flushes,
+        "device_ms_per_step": step_ms,
+        "attention_path": {"device_ms_per_step": attn_ms, "bytes_per_step": attn_bytes,
+                           "GBps": attn_bytes / (attn_ms * 1e-3) / 1e9,
+                           "bytes_per_layer": per_layer[0]},
+        "weight_bytes_per_step": weight_bytes,
+        "roofline": {"bound": "hbm", "achieved": attn_bytes / (attn_ms * 1e-3) / 1e9, "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": attn_bytes / (attn_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                     "traffic": None, "kernel": "attention path (36 x polar_cache.compute)",
+                     "kernel_ms": attn_ms, "algorithmic_bytes": attn_bytes},
+        "setup_s": setup_s,
+        "cpu_baseline": None,
+    }
 
 
 def run_c3(args):
@@ -369,8 +442,8 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--splits", type=int, default=0)
-    ap.add_argument("--config", choices=["c1", "c2", "c3", "c4"], default="c2",
-                    help="c2 (default, the headline line), c1, c3 or c4")
+    ap.add_argument("--config", choices=["c1", "c2", "c3", "c4", "c5"], default="c2",
+                    help="c2 (default, the headline line), c1, c3, c4 or c5")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run 5 device copies of 1 GiB (scale reference for rocprof "
@@ -386,7 +459,7 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     if args.config != "c2":
-        run = {"c1": run_c1, "c3": run_c3, "c4": run_c4}[args.config]
+        run = {"c1": run_c1, "c3": run_c3, "c4": run_c4, "c5": run_c5}[args.config]
         print(json.dumps(run(args)))
         return
     if args.calibrate_copy:

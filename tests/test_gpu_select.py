@@ -32,7 +32,8 @@ def test_quest_chunk_score_bit_exact(rng, fp16_meta):
     assert np.array_equal(from_torch(scores).view(np.uint32), ref.view(np.uint32))
 
 
-@pytest.mark.parametrize("L,k", [(2048, 128), (13120, 100), (131072, 256), (64, 64), (3000, 1)])
+@pytest.mark.parametrize("L,k", [(2048, 128), (13120, 100), (131072, 256), (64, 64), (3000, 1),
+                                 (4096, 1638), (1638, 491), (26208, 100), (32768, 7), (32769, 300)])
 def test_topk_exact(rng, L, k):
     from zoomkv_revision_amd.topk import float_topk_3d
     x = rng.standard_normal((2, 3, L)).astype(np.float32)
@@ -54,6 +55,10 @@ def test_topk_strided_and_bf16_input(rng):
     x = rng.standard_normal((4, 5, 300)).astype(np.float32)
     xt = torch.from_numpy(x).cuda()
     assert np.array_equal(from_torch(float_topk_3d(xt[:, 1:4], 17)), osel.topk_indices(x[:, 1:4], 17))
+    # rows that are not 16-byte aligned (scalar loads)
+    y = rng.standard_normal((3, 9001)).astype(np.float32)
+    yt = torch.from_numpy(y).cuda()
+    assert np.array_equal(from_torch(float_topk(yt[:, 1:], 40)), osel.topk_indices(y[:, 1:], 40))
     xb = bf16r(x[0])
     assert np.array_equal(from_torch(float_topk(to_bf16(xb), 9)), osel.topk_indices(xb, 9))
 

@@ -192,6 +192,143 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(
 }
 
 // ----------------------------------------------------------------------------
+// The same selection for rows of at most 1024 * R elements with the row held
+// in registers (thread t keeps indices t + 1024 j, j < R: coalesced loads,
+// one read of the row for all four radix rounds).  The ordered output needs
+// one scan: for each register row j a wave ballots its greater-than-T and
+// equal-to-T bits; the (row j, wave w) counts, in index order j-major then
+// w, are scanned once, giving every element its rank among the gt and the
+// eq elements of lower index:  pos(i) = #gt below i + min(#eq below i, remain).
+// ----------------------------------------------------------------------------
+template <int R>
+__global__ __launch_bounds__(kTopkThreads) void topk_reg_kernel(
+    const float* __restrict__ in, int64_t in_stride, int L, int k, int64_t* __restrict__ out,
+    int64_t out_stride, const int64_t* __restrict__ lut, int64_t lut_stride,
+    const int64_t* __restrict__ skipped, int64_t sk_stride, int sk_count, int64_t sentinel) {
+  __shared__ int s_hist[2][kTopkWaves][256];
+  __shared__ int s_merged[256];
+  __shared__ uint32_t s_cnt[R * kTopkWaves];  // (j, w) -> gt | eq << 16, then its exclusive prefix
+  __shared__ int s_bin, s_remain;
+  const int row = blockIdx.x;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const float* x = in + row * in_stride;
+  int64_t* o = out + row * out_stride;
+  const int64_t* lrow = lut ? lut + row * lut_stride : nullptr;
+
+  for (int i = tid; i < sk_count; i += kTopkThreads) o[k + i] = skipped[row * sk_stride + i];
+  if (L <= k) {
+    for (int i = tid; i < k; i += kTopkThreads) o[i] = (i < L) ? (lrow ? lrow[i] : i) : sentinel;
+    return;
+  }
+  uint32_t key[R];
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    const int i = tid + kTopkThreads * j;
+    key[j] = i < L ? ordered_key(x[i]) : 0u;
+  }
+  for (int i = tid; i < kTopkWaves * 256; i += kTopkThreads) (&s_hist[0][0][0])[i] = 0;
+  __syncthreads();
+
+  uint32_t prefix = 0, mask = 0;
+  int remain = k;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int shift = 24 - 8 * r;
+    int (*hist)[256] = s_hist[r & 1];
+    // clear the other buffer (last read two barriers ago) for the next round
+    for (int i = tid; i < kTopkWaves * 256; i += kTopkThreads) (&s_hist[(r + 1) & 1][0][0])[i] = 0;
+#pragma unroll
+    for (int j = 0; j < R; ++j)
+      if (tid + kTopkThreads * j < L && (key[j] & mask) == prefix)
+        atomicAdd(&hist[wave][(key[j] >> shift) & 0xFF], 1);
+    __syncthreads();
+    if (tid < 256) {
+      int c = 0;
+#pragma unroll
+      for (int w = 0; w < kTopkWaves; ++w) c += hist[w][tid];
+      s_merged[tid] = c;
+    }
+    __syncthreads();
+    if (tid < 64) {
+      int c[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) c[j] = s_merged[4 * tid + j];
+      const int lane_sum = c[0] + c[1] + c[2] + c[3];
+      int suf = lane_sum;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const int v = __shfl_down(suf, off);
+        if (tid + off < 64) suf += v;
+      }
+      int above = suf - lane_sum;
+#pragma unroll
+      for (int j = 3; j >= 0; --j) {
+        const int at_or_above = above + c[j];
+        if (at_or_above >= remain && above < remain) {
+          s_bin = 4 * tid + j;
+          s_remain = remain - above;
+        }
+        above = at_or_above;
+      }
+    }
+    __syncthreads();
+    prefix |= static_cast<uint32_t>(s_bin) << shift;
+    mask |= 0xFFu << shift;
+    remain = s_remain;
+  }
+  const uint32_t T = prefix;
+  uint64_t bgt[R], beq[R];
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    const bool in_row = tid + kTopkThreads * j < L;
+    bgt[j] = __ballot(in_row && key[j] > T);
+    beq[j] = __ballot(in_row && key[j] == T);
+    if (lane == 0)
+      s_cnt[j * kTopkWaves + wave] = static_cast<uint32_t>(__popcll(bgt[j])) |
+                                     (static_cast<uint32_t>(__popcll(beq[j])) << 16);
+  }
+  __syncthreads();
+  if (tid < 64) {
+    // exclusive scan of the R * 16 entries (at most 512: 8 per lane, in order)
+    constexpr int kPer = (R * kTopkWaves + 63) / 64;
+    uint32_t v[kPer];
+    uint32_t sum = 0;
+#pragma unroll
+    for (int e = 0; e < kPer; ++e) {
+      const int idx = tid * kPer + e;
+      v[e] = idx < R * kTopkWaves ? s_cnt[idx] : 0u;
+      sum += v[e];
+    }
+    uint32_t inc = sum;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const uint32_t t = __shfl_up(inc, off);
+      if (tid >= off) inc += t;
+    }
+    uint32_t run = inc - sum;
+#pragma unroll
+    for (int e = 0; e < kPer; ++e) {
+      const int idx = tid * kPer + e;
+      if (idx < R * kTopkWaves) s_cnt[idx] = run;
+      run += v[e];
+    }
+  }
+  __syncthreads();
+  const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    const uint32_t pre = s_cnt[j * kTopkWaves + wave];
+    const int gt_rank = static_cast<int>(pre & 0xFFFFu) + __popcll(bgt[j] & below);
+    const int eq_rank = static_cast<int>(pre >> 16) + __popcll(beq[j] & below);
+    const bool is_gt = (bgt[j] >> lane) & 1ull, is_eq = (beq[j] >> lane) & 1ull;
+    if (is_gt || (is_eq && eq_rank < remain)) {
+      const int i = tid + kTopkThreads * j;
+      o[gt_rank + min(eq_rank, remain)] = lrow ? lrow[i] : i;
+    }
+  }
+}
+
+// ----------------------------------------------------------------------------
 // CDS density: centroid[chunk_id] . q (rerank_topk.cu:560-624): buf[t] = c[t]q[t]
 // for t < 128, then buf[t] += buf[t+s], s = 64..1; invalid id -> -1e30.
 // One wave per (b, kv, slot): lane l starts with p[l] + p[l+64].
@@ -301,11 +438,19 @@ __global__ __launch_bounds__(256) void kivi_qk_kernel(
     for (int p = 0; p < 16; ++p) {
       const uint32_t word = static_cast<uint32_t>(w[p * G]);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
+      for (int j = 0; j < 8; j += 2) {
+        // channels d, d + 1 side by side (each rounding of the pair is one
+        // packed conversion); the sum stays sequential in d
         const int d = 8 * p + j;
-        const float code = static_cast<float>((word >> (4 * j)) & 0xFu);
-        const float kd = bf16r(bf16r(code * s_sc[local][d]) + s_mn[local][d]);
-        acc = acc + bf16r(kd * s_q[local][d]);
+        const float2_t code = {static_cast<float>((word >> (4 * j)) & 0xFu),
+                               static_cast<float>((word >> (4 * j + 4)) & 0xFu)};
+        const float2_t sc = {s_sc[local][d], s_sc[local][d + 1]};
+        const float2_t mn = {s_mn[local][d], s_mn[local][d + 1]};
+        const float2_t qq = {s_q[local][d], s_q[local][d + 1]};
+        const float2_t kd = bf16r2(bf16r2(code * sc) + mn);
+        const float2_t pr = bf16r2(kd * qq);
+        acc = acc + pr[0];
+        acc = acc + pr[1];
       }
     }
     score = acc;
@@ -410,8 +555,22 @@ extern "C" int zkv_topk(const float* scores, int64_t in_stride, int rows, int L,
               static_cast<long long>(out_stride), k + sk_count);
   ZKV_REQUIRE(sk_count == 0 || skipped, "zkv_topk: null skipped");
   if (rows == 0) return ZKV_OK;
-  topk_kernel<<<rows, kTopkThreads, 0, reinterpret_cast<hipStream_t>(stream)>>>(
-      scores, in_stride, L, k, out, out_stride, lut, lut_stride, skipped, sk_stride, sk_count, sentinel);
+  auto s = reinterpret_cast<hipStream_t>(stream);
+#define ZKV_TOPK_REG(R)                                                                          \
+  topk_reg_kernel<R><<<rows, kTopkThreads, 0, s>>>(scores, in_stride, L, k, out, out_stride, lut, \
+                                                   lut_stride, skipped, sk_stride, sk_count, sentinel)
+  if (L <= 4 * kTopkThreads)
+    ZKV_TOPK_REG(4);
+  else if (L <= 8 * kTopkThreads)
+    ZKV_TOPK_REG(8);
+  else if (L <= 16 * kTopkThreads)
+    ZKV_TOPK_REG(16);
+  else if (L <= 32 * kTopkThreads)
+    ZKV_TOPK_REG(32);
+  else
+    topk_kernel<<<rows, kTopkThreads, 0, s>>>(scores, in_stride, L, k, out, out_stride, lut, lut_stride,
+                                              skipped, sk_stride, sk_count, sentinel);
+#undef ZKV_TOPK_REG
   return check_launch("topk_kernel");
 }
 

@@ -44,15 +44,22 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t b) {
   return __uint_as_float(static_cast<uint32_t>(b) << 16);
 }
 
-// Round an fp32 value to the nearest bfloat16 (ties to even); NaN stays NaN.
+// Round an fp32 value to the nearest bfloat16, ties to even (NaN stays NaN).
+// gfx950 does this in hardware (v_cvt_pk_bf16_f32); it agrees bit for bit
+// with the integer form  u += 0x7fff + ((u >> 16) & 1), u >>= 16  on every
+// finite input, fp32 subnormals included (built without denormal flushing).
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float x) {
-  uint32_t u = __float_as_uint(x);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(x));
 }
 
-__device__ __forceinline__ float bf16r(float x) { return bf16_to_f32(f32_to_bf16_bits(x)); }
+__device__ __forceinline__ float bf16r(float x) { return static_cast<float>(static_cast<__bf16>(x)); }
+
+// Two roundings in one v_cvt_pk_bf16_f32.
+typedef float float2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float2_t bf16r2(float2_t x) {
+  return __builtin_convertvector(__builtin_convertvector(x, bf16x2_t), float2_t);
+}
 
 __device__ __forceinline__ uint16_t f32_to_f16_bits(float x) {
   _Float16 h = static_cast<_Float16>(x);

@@ -1,0 +1,238 @@
+"""Decode-step counterpart of the reference runtime for the C5 configuration.
+
+One decode step of a Qwen3-geometry model over the drop-in ``polar_cache``,
+in the order of the reference's ``layer_decode``
+(Z/model_hub/LLM.py:208-251) with the layer pieces of
+Z/model_hub/qwen.py:439-604:
+
+  rmsnorm -> fused QKV linear -> per-head q / k rmsnorm -> RoPE at position
+  ``cache.context`` -> ``cache.decode_update_kv_cache`` -> ``cache.compute``
+  -> o-projection + residual -> rmsnorm -> gate/up linear, silu * up, down
+  linear + residual;
+
+then the final norm, the tied LM head and ``sample_next_token``
+(LLM.py:63-139: temperature, top-k, top-p, multinomial).
+
+The weights are random-init bf16 stand-ins (no checkpoint is available
+offline).  The linear layers are plain library GEMMs (torch.nn.functional
+.linear on hipBLASLt); rmsnorm, RoPE and silu are torch ops (the reference
+calls flashinfer for them, which has no ROCm build).  The attention path --
+the part this package accelerates -- is the cache's own kernels.
+"""
+from __future__ import annotations
+
+import os
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+
+# The reference runner's ZoomKV environment (Z/run/eval_math_aime.py:216-238)
+# and cache knobs (polar_config, :177-213), restricted to what polar_cache reads.
+PRODUCTION_ENV = {
+    "POLAR_QUEST_CHUNK": "16",
+    "POLAR_QUEST_CAND_RATIO": "0.4",
+    "POLAR_QUEST_DYNAMIC_CAND_RATIO": "1",
+    "POLAR_QUEST_DYNAMIC_CAND_THRESHOLDS": "5000,10001",
+    "POLAR_QUEST_DYNAMIC_CAND_RATIOS": "0.7,0.5,0.4",
+    "POLAR_CDS_DENSE_RATIO": "0.3",
+    "POLAR_CDS_DENSE_TOPK": "8",
+    "POLAR_CDS_SPARSE_TOPK": "8",
+}
+PRODUCTION_CACHE_KNOBS = {"sink_size": 64, "local_size": 256, "final_topk": 100,
+                          "collision_ratio": 0.3, "candidate_ratio": 0.4, "enable_offload": True}
+
+
+def apply_production_env() -> None:
+    """Set the reference's production ZoomKV environment (before building a cache)."""
+    os.environ.update(PRODUCTION_ENV)
+    os.environ.pop("POLAR_FORCE_CAND_TOKENS", None)
+
+
+@dataclass(frozen=True)
+class Qwen3Geometry:
+    """Qwen3-4B: 36 layers, 32 / 8 heads of 128 (from the reference's
+    configuration); hidden / FFN / vocabulary sizes are the public Qwen3-4B
+    values, used as random-init stand-ins."""
+    layers: int = 36
+    hidden: int = 2560
+    heads: int = 32
+    kv_heads: int = 8
+    head_dim: int = 128
+    ffn: int = 9728
+    vocab: int = 151936
+    rope_theta: float = 1.0e6
+    eps: float = 1.0e-6
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """RMSNorm over the last dim in fp32, weight applied in fp32, result in x's dtype."""
+    xf = x.float()
+    xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
+    return (xf * weight.float()).to(x.dtype)
+
+
+class RandomQwen3:
+    """Random-init bf16 weights of a Qwen3 decoder (std 0.02, norms at 1), on one GPU."""
+
+    def __init__(self, geo: Qwen3Geometry, device, seed: int = 42, max_position: int = 1 << 17):
+        self.geo = geo
+        self.device = torch.device(device)
+        g = torch.Generator(device=self.device)
+        g.manual_seed(seed)
+        bf = dict(dtype=torch.bfloat16, device=self.device)
+
+        def w(*shape):
+            return (torch.randn(*shape, generator=g, device=self.device) * 0.02).to(torch.bfloat16)
+
+        qd, kd = geo.heads * geo.head_dim, geo.kv_heads * geo.head_dim
+        self.embed = w(geo.vocab, geo.hidden)             # tied with the LM head
+        self.final_norm = torch.ones(geo.hidden, **bf)
+        self.layers = []
+        for _ in range(geo.layers):
+            self.layers.append({
+                "input_ln": torch.ones(geo.hidden, **bf),
+                "post_ln": torch.ones(geo.hidden, **bf),
+                "wqkv": w(qd + 2 * kd, geo.hidden),
+                "q_norm": torch.ones(geo.head_dim, **bf),
+                "k_norm": torch.ones(geo.head_dim, **bf),
+                "wo": w(geo.hidden, qd),
+                "gate_up": w(2 * geo.ffn, geo.hidden),
+                "down": w(geo.hidden, geo.ffn),
+            })
+        # RoPE cos / sin (rotate-half form), fp32 [max_position, head_dim / 2]
+        inv = 1.0 / (geo.rope_theta ** (torch.arange(0, geo.head_dim, 2, dtype=torch.float32,
+                                                     device=self.device) / geo.head_dim))
+        t = torch.arange(max_position, dtype=torch.float32, device=self.device)
+        freqs = torch.outer(t, inv)
+        self.cos, self.sin = freqs.cos(), freqs.sin()
+
+    def parameter_bytes(self) -> int:
+        n = self.embed.numel() + self.final_norm.numel()
+        for L in self.layers:
+            n += sum(t.numel() for t in L.values())
+        return 2 * n
+
+    def _rope(self, x: torch.Tensor, pos: int) -> torch.Tensor:
+        """x [bs, 1, heads, 128] rotated at position pos (rotate-half, as the
+        reference's fp32 path and flashinfer's is_neox=True)."""
+        h = self.geo.head_dim // 2
+        cos, sin = self.cos[pos], self.sin[pos]
+        xf = x.float()
+        x1, x2 = xf[..., :h], xf[..., h:]
+        return torch.cat((x1 * cos - x2 * sin, x2 * cos + x1 * sin), dim=-1).to(x.dtype)
+
+    def layer_decode(self, ldx: int, hidden: torch.Tensor, cache) -> torch.Tensor:
+        """One layer of one decode token (LLM.py:208-251); hidden [bs, 1, hidden]."""
+        geo, L = self.geo, self.layers[ldx]
+        bs = hidden.shape[0]
+        residual = hidden
+        x = rms_norm(hidden, L["input_ln"], geo.eps)
+        qkv = F.linear(x, L["wqkv"])
+        qd, kd = geo.heads * geo.head_dim, geo.kv_heads * geo.head_dim
+        q, k, v = qkv.split([qd, kd, kd], dim=-1)
+        q = rms_norm(q.reshape(bs, 1, geo.heads, geo.head_dim), L["q_norm"], geo.eps)
+        k = rms_norm(k.reshape(bs, 1, geo.kv_heads, geo.head_dim), L["k_norm"], geo.eps)
+        pos = cache.context
+        q, k = self._rope(q, pos), self._rope(k, pos)
+        v = v.reshape(bs, 1, geo.kv_heads, geo.head_dim)
+        cache.decode_update_kv_cache(k, v, ldx)
+        attn = cache.compute(q, ldx)                                   # [bs, 1, heads, 128]
+        hidden = residual + F.linear(attn.reshape(bs, 1, qd), L["wo"])
+        residual = hidden
+        x = rms_norm(hidden, L["post_ln"], geo.eps)
+        gate, up = F.linear(x, L["gate_up"]).chunk(2, dim=-1)
+        hidden = residual + F.linear(F.silu(gate) * up, L["down"])
+        return hidden
+
+    def decode_step(self, tokens: torch.Tensor, cache) -> torch.Tensor:
+        """tokens [bs] int64 -> logits [bs, vocab] (fp32)."""
+        hidden = self.embed[tokens].unsqueeze(1)
+        for ldx in range(self.geo.layers):
+            hidden = self.layer_decode(ldx, hidden, cache)
+        hidden = rms_norm(hidden, self.final_norm, self.geo.eps)
+        return F.linear(hidden[:, 0], self.embed).float()
+
+
+def sample_next_token(logits: torch.Tensor, temperature: float = 1.0, top_p: float = 0.0,
+                      top_k: int = 0, generator: torch.Generator | None = None) -> torch.Tensor:
+    """Sampling of LLM.py:63-139: greedy below temperature 1e-5, else
+    temperature, top-k (ties at the k-th value kept), top-p (the token that
+    crosses top_p kept), softmax, one multinomial draw per row."""
+    if logits.dim() == 3:
+        logits = logits.squeeze(1)
+    elif logits.dim() == 1:
+        logits = logits.unsqueeze(0)
+    if temperature < 1e-5:
+        return logits.argmax(dim=-1)
+    logits = logits / temperature
+    if top_k > 0:
+        top_k = min(top_k, logits.size(-1))
+        logits = logits.masked_fill(logits < torch.topk(logits, top_k)[0][..., -1, None], float("-inf"))
+    if 0.0 < top_p < 1.0:
+        sorted_logits, sorted_idx = torch.sort(logits, descending=True, dim=-1)
+        cum = torch.cumsum(F.softmax(sorted_logits, dim=-1), dim=-1)
+        remove = cum > top_p
+        remove[..., 1:] = remove[..., :-1].clone()
+        remove[..., 0] = False
+        logits = logits.masked_fill(remove.scatter(-1, sorted_idx, remove), float("-inf"))
+    probs = F.softmax(logits, dim=-1)
+    return torch.multinomial(probs, num_samples=1, generator=generator).squeeze(-1)
+
+
+def build_cache(geo: Qwen3Geometry, batch: int, context: int, max_new: int, interval: int,
+                full_threshold: int, device):
+    """polar_cache for `context` prompt tokens plus `max_new` generated ones,
+    with the reference's production knobs."""
+    from .cache import polar_cache
+    return polar_cache(
+        valid_start=[0] * batch, layer_num=geo.layers, batch_size=batch, max_length=context + max_new,
+        num_key_value_heads=geo.kv_heads, num_heads=geo.heads, head_dim=geo.head_dim,
+        dtype=torch.bfloat16, layer_mapping={str(i): str(device) for i in range(geo.layers)},
+        max_new_length=max_new, core=22, nprobe=150, cache_unit_size=8, cache_cluster_num=450,
+        num_gpus=1, model_size=4, dynamic_update_interval=interval, full_attention_threshold=full_threshold,
+        **PRODUCTION_CACHE_KNOBS)
+
+
+def fill_cache(cache, geo: Qwen3Geometry, batch: int, context: int, seed: int, device) -> None:
+    """Prefill every layer through prefill_update_kv_cache with seeded N(0, 1)
+    bf16 keys / values [batch, context, kv, 128] (what a prompt of `context`
+    tokens would leave; a 64K-token prefill of random weights adds nothing)."""
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    shape = (batch, context, geo.kv_heads, geo.head_dim)
+    for ldx in range(geo.layers):
+        k = torch.randn(*shape, generator=g, device=device).to(torch.bfloat16)
+        v = torch.randn(*shape, generator=g, device=device).to(torch.bfloat16)
+        cache.prefill_update_kv_cache(None, k, v, ldx, 0)
+        del k, v
+
+
+def attention_path_bytes(cache, layer: int) -> dict:
+    """Algorithmic HBM bytes of one layer's attention path (cache.compute with
+    the selection running): GQA mean, Quest bounds over the chunk metadata,
+    the two top-k passes, density, KIVI stage 2 over the candidate chunks, the
+    top-k + gather + concat, and the attention over the selected and near-zone
+    rows.  The decode append (one K / V row) is included."""
+    bs, kv, d = cache.batch_size, cache.kv_head, cache.head_dim
+    chunk = cache.quest_chunk_size
+    n_chunks, nk = cache._cached_quest_n_chunks, cache._cached_quest_nk
+    units = bs * kv
+    sk = cache._chunk_skipped_count[layer]
+    k_final = min(cache.final_topk, nk * chunk)
+    region = cache.get_region_indices(layer)
+    near = cache.sink_size + region["local_len"]
+    gq = bs * cache.num_heads * d * 2 + units * d * 2
+    quest = units * (n_chunks * (2 * d * 2 + 1 + 4) + d * 2)
+    topk1 = units * (n_chunks * 4 + nk * 8)
+    density = units * (nk * (8 + d * 2 + 4) + d * 2)
+    topk2 = units * (nk * 4 + nk)
+    stage2 = units * (nk * (8 + 1 + 16 * chunk * 4 + 2 * d * 2) + nk * chunk * 12)
+    gather = units * (nk * chunk * 12 + sk * 8 + (k_final + sk) * 8)
+    attn = units * ((k_final + sk + near) * 2 * d * 2 + (k_final + sk) * 8) + 2 * bs * cache.num_heads * d * 2
+    append = 2 * units * d * 2
+    parts = {"gqa_mean": gq, "quest": quest, "topk_chunks": topk1, "density": density,
+             "topk_dense": topk2, "kivi_stage2": stage2, "topk_gather_concat": gather,
+             "attention": attn, "append": append}
+    parts["total"] = sum(parts.values())
+    return parts
