@@ -268,6 +268,40 @@ def run_c5(args):
     }
 
 
+def run_h2d(args):
+    """Host-to-device gather (the reference's UVA path, trans_h2d.py): the
+    rows one decode layer gathers at C5's shape -- batch 4, 8 KV heads, 612
+    rows per head (top-100 + 512 skipped) of a 65536-row pinned host cache."""
+    import torch
+    from zoomkv_revision_amd.gather import h2d_gather_kv
+    bs, heads, src_len, topk = 4, 8, 65536, 612
+    dev = torch.device("cuda:0")
+    sk = torch.randn(bs, heads, src_len, 128).to(torch.bfloat16).pin_memory()
+    sv = torch.randn(bs, heads, src_len, 128).to(torch.bfloat16).pin_memory()
+    g = torch.Generator(device=dev)
+    g.manual_seed(42)
+    idxs = [torch.randint(0, src_len, (bs, heads, topk), generator=g, device=dev) for _ in range(8)]
+    dk = torch.empty(bs, heads, topk, 128, dtype=torch.bfloat16, device=dev)
+    dv = torch.empty_like(dk)
+
+    def step(i):
+        h2d_gather_kv(sk, sv, idxs[i % len(idxs)], dk, dv)
+
+    ms = timed_loop(step, args.steps, args.warmup)
+    k_ms = kernel_batch_ms(step, args.steps)
+    nbytes = bs * heads * topk * 2 * 256
+    return {
+        "metric": "host-to-device K/V row gather (pinned host cache): GB/s over the host link",
+        "value": nbytes / (k_ms * 1e-3) / 1e9, "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16 rows", "data": "synthetic",
+        "config": {"workload": "h2d_gather_kv: 612 rows of 256 B per (b, kv head), K and V",
+                   "batch": bs, "kv_heads": heads, "src_len": src_len, "rows": topk,
+                   "parallelism": "single GPU"},
+        "kernel_ms": k_ms, "bytes_per_call": nbytes, "cpu_baseline": None,
+    }
+
+
 def run_c3(args):
     """C3: GQA-mean query -> Quest bounds over fp16 page metadata (2048 pages of
     16 tokens) -> top-128 pages -> page-sparse 4-bit attention, batch 8,
@@ -442,8 +476,8 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--splits", type=int, default=0)
-    ap.add_argument("--config", choices=["c1", "c2", "c3", "c4", "c5"], default="c2",
-                    help="c2 (default, the headline line), c1, c3, c4 or c5")
+    ap.add_argument("--config", choices=["c1", "c2", "c3", "c4", "c5", "h2d"], default="c2",
+                    help="c2 (default, the headline line), c1, c3, c4, c5 or h2d")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run 5 device copies of 1 GiB (scale reference for rocprof "
@@ -459,7 +493,7 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     if args.config != "c2":
-        run = {"c1": run_c1, "c3": run_c3, "c4": run_c4, "c5": run_c5}[args.config]
+        run = {"c1": run_c1, "c3": run_c3, "c4": run_c4, "c5": run_c5, "h2d": run_h2d}[args.config]
         print(json.dumps(run(args)))
         return
     if args.calibrate_copy:

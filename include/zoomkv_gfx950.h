@@ -300,6 +300,35 @@ int zkv_rabitq_search(const uint16_t* q, const uint16_t* keys, int64_t k_pool_st
                       int64_t* cand_idx, int64_t* final_idx, float* final_scores, void* workspace,
                       size_t workspace_bytes, zkv_stream_t stream);
 
+/* ---------------------------------------------------------------------------
+ * Host-to-device row gather (the UVA gather of
+ * Z/cache_hub/gather_trans/trans_h2d.cu:43-188, trans_h2d.py:65-166).
+ * src_k / src_v are pinned, mapped host buffers of bf16 rows
+ * [bs, heads, src_len, 128] (the C ABI takes their host pointers and fails
+ * with ZKV_EINVAL when they have no device alias); every other pointer is
+ * device memory.  An index outside [0, src_len) leaves its destination row
+ * untouched.
+ * ------------------------------------------------------------------------- */
+
+/* dst[b, h, slot] = src[b, h, indices[b, h, slot]] for slot < topk; dst is
+ * [bs, heads, dst_len, 128], indices [bs, heads, topk] int64 (contiguous).
+ * Replaces h2d_gather_kv (trans_h2d.py:65-103 -> trans_h2d.cu:84-188). */
+int zkv_h2d_gather_kv(const void* src_k, const void* src_v, int bs, int heads, int src_len,
+                      const int64_t* indices, int topk, void* dst_k, void* dst_v, int dst_len,
+                      zkv_stream_t stream);
+
+/* Variable-K gather into a packed varlen buffer [total_k, 128]: segment
+ * vh = b * kv_heads + h takes indices_packed[cu_seqlens_topk[vh] ..
+ * cu_seqlens_topk[vh + 1]) into rows cu_seqlens_k[vh] + sl_end + slot
+ * (the first sl_end rows of each segment are the caller's).  global_k bounds
+ * every segment's length.  Replaces h2d_gather_kv_packed
+ * (trans_h2d.py:106-166 -> trans_h2d.cu:229-333). */
+int zkv_h2d_gather_kv_packed(const void* src_k, const void* src_v, int bs, int kv_heads, int src_len,
+                             void* dst_k_packed, void* dst_v_packed, int64_t total_k,
+                             const int64_t* indices_packed, int64_t total_topk,
+                             const int32_t* cu_seqlens_topk, const int32_t* cu_seqlens_k, int sl_end,
+                             int global_k, zkv_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
