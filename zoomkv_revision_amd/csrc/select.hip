@@ -14,7 +14,8 @@ namespace {
 // Quest chunk score (Z/cache_hub/quest/quest_chunk_score.cu:31-103)
 //   score = sum_d max(q_d * mn_d, q_d * mx_d); lane t of a 32-lane group sums
 //   dims 4t..4t+3 left to right, then xor butterfly 16, 8, 4, 2, 1.
-// Each wave64 scores two chunks at a time (one per 32-lane half); the grid
+// Each 32-lane half of a wave64 scores 4 adjacent chunks per trip, issuing
+// all their loads first (the valid flag is applied at the end), and the grid
 // strides over all (b, kv, chunk).  HBM-bound: 512 B of metadata per chunk.
 // ----------------------------------------------------------------------------
 template <bool kFp16Meta>
@@ -25,6 +26,8 @@ __device__ __forceinline__ float meta_to_f32(uint16_t v) {
     return bf16_to_f32(v);
 }
 
+constexpr int kQuestUnroll = 4;  // chunks per 32-lane half per trip, loads issued together
+
 template <bool kFp16Meta>
 __global__ __launch_bounds__(256) void quest_score_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ cmin,
@@ -32,36 +35,61 @@ __global__ __launch_bounds__(256) void quest_score_kernel(
     int n_chunks, int n_max, int64_t total) {
   const int half = threadIdx.x >> 5;  // 8 halves of 32 lanes per block
   const int t = threadIdx.x & 31;
-  for (int64_t item = static_cast<int64_t>(blockIdx.x) * 8 + half; item < total;
-       item += static_cast<int64_t>(gridDim.x) * 8) {
-    const int64_t bh = item / n_chunks;
-    const int chunk = static_cast<int>(item - bh * n_chunks);
-    const int64_t row = bh * n_max + chunk;
-    float sum;
-    if (valid != nullptr && !valid[row]) {
-      sum = -INFINITY;
-    } else {
-      const u32x2_t qv = *reinterpret_cast<const u32x2_t*>(q + bh * 128 + 4 * t);
-      const u32x2_t mv = *reinterpret_cast<const u32x2_t*>(cmin + row * 128 + 4 * t);
-      const u32x2_t xv = *reinterpret_cast<const u32x2_t*>(cmax + row * 128 + 4 * t);
+  constexpr int U = kQuestUnroll;
+  for (int64_t item0 = (static_cast<int64_t>(blockIdx.x) * 8 + half) * U; item0 < total;
+       item0 += static_cast<int64_t>(gridDim.x) * 8 * U) {
+    u32x2_t qv[U], mv[U], xv[U];
+    int64_t row[U];
+    // all loads of the U chunks first (rows past the end re-read the last one)
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t item = min(item0 + u, total - 1);
+      const int64_t bh = item / n_chunks;
+      const int chunk = static_cast<int>(item - bh * n_chunks);
+      row[u] = bh * n_max + chunk;
+      qv[u] = *reinterpret_cast<const u32x2_t*>(q + bh * 128 + 4 * t);
+      mv[u] = *reinterpret_cast<const u32x2_t*>(cmin + row[u] * 128 + 4 * t);
+      xv[u] = *reinterpret_cast<const u32x2_t*>(cmax + row[u] * 128 + 4 * t);
+    }
+    float sum[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
       float qq[4], mn[4], mx[4];
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
-        qq[2 * i] = __uint_as_float(qv[i] << 16);
-        qq[2 * i + 1] = __uint_as_float(qv[i] & 0xFFFF0000u);
-        mn[2 * i] = meta_to_f32<kFp16Meta>(static_cast<uint16_t>(mv[i] & 0xFFFF));
-        mn[2 * i + 1] = meta_to_f32<kFp16Meta>(static_cast<uint16_t>(mv[i] >> 16));
-        mx[2 * i] = meta_to_f32<kFp16Meta>(static_cast<uint16_t>(xv[i] & 0xFFFF));
-        mx[2 * i + 1] = meta_to_f32<kFp16Meta>(static_cast<uint16_t>(xv[i] >> 16));
+        qq[2 * i] = __uint_as_float(qv[u][i] << 16);
+        qq[2 * i + 1] = __uint_as_float(qv[u][i] & 0xFFFF0000u);
+        mn[2 * i] = meta_to_f32<kFp16Meta>(static_cast<uint16_t>(mv[u][i] & 0xFFFF));
+        mn[2 * i + 1] = meta_to_f32<kFp16Meta>(static_cast<uint16_t>(mv[u][i] >> 16));
+        mx[2 * i] = meta_to_f32<kFp16Meta>(static_cast<uint16_t>(xv[u][i] & 0xFFFF));
+        mx[2 * i + 1] = meta_to_f32<kFp16Meta>(static_cast<uint16_t>(xv[u][i] >> 16));
       }
-      sum = fmaxf(qq[0] * mn[0], qq[0] * mx[0]);
-      sum = sum + fmaxf(qq[1] * mn[1], qq[1] * mx[1]);
-      sum = sum + fmaxf(qq[2] * mn[2], qq[2] * mx[2]);
-      sum = sum + fmaxf(qq[3] * mn[3], qq[3] * mx[3]);
-#pragma unroll
-      for (int off = 16; off > 0; off >>= 1) sum = sum + __shfl_xor(sum, off);
+      float sm = fmaxf(qq[0] * mn[0], qq[0] * mx[0]);
+      sm = sm + fmaxf(qq[1] * mn[1], qq[1] * mx[1]);
+      sm = sm + fmaxf(qq[2] * mn[2], qq[2] * mx[2]);
+      sm = sm + fmaxf(qq[3] * mn[3], qq[3] * mx[3]);
+      sum[u] = sm;
     }
-    if (t == 0) scores[item] = sum;
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1)
+#pragma unroll
+      for (int u = 0; u < U; ++u) sum[u] = sum[u] + __shfl_xor(sum[u], off);
+    if (t < U) {
+      // lane u stores chunk u (every lane holds every sum after the butterfly)
+      float out = sum[0];
+      int64_t r = row[0];
+#pragma unroll
+      for (int u = 1; u < U; ++u)
+        if (t == u) {
+          out = sum[u];
+          r = row[u];
+        }
+      const int64_t item = item0 + t;
+      if (item < total) {
+        if (valid != nullptr && !valid[r]) out = -INFINITY;
+        scores[item] = out;
+      }
+    }
   }
 }
 
@@ -533,7 +561,7 @@ extern "C" int zkv_quest_chunk_score(const uint16_t* q, const uint16_t* chunk_mi
               n_chunks, n_chunks_max);
   const int64_t total = static_cast<int64_t>(bs) * kv * n_chunks;
   if (total == 0) return ZKV_OK;
-  const int64_t blocks64 = std::min<int64_t>((total + 7) / 8, 8192);
+  const int64_t blocks64 = std::min<int64_t>((total + 8 * kQuestUnroll - 1) / (8 * kQuestUnroll), 8192);
   const int blocks = static_cast<int>(blocks64);
   auto s = reinterpret_cast<hipStream_t>(stream);
   if (meta_fp16)
