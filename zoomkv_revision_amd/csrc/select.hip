@@ -359,34 +359,57 @@ __global__ __launch_bounds__(kTopkThreads) void topk_reg_kernel(
 // ----------------------------------------------------------------------------
 // CDS density: centroid[chunk_id] . q (rerank_topk.cu:560-624): buf[t] = c[t]q[t]
 // for t < 128, then buf[t] += buf[t+s], s = 64..1; invalid id -> -1e30.
-// One wave per (b, kv, slot): lane l starts with p[l] + p[l+64].
+// A wave scores kDensityItems slots (lane l starts with p[l] + p[l+64] of
+// each), their loads issued together and their trees interleaved.
 // ----------------------------------------------------------------------------
+constexpr int kDensityItems = 4;
+
 __global__ __launch_bounds__(256) void density_kernel(
     const int64_t* __restrict__ ids, int64_t id_sb, int64_t id_sh, const uint16_t* __restrict__ cent,
     int64_t c_sb, int64_t c_sh, int64_t c_sc, const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_sh,
     float* __restrict__ out, int64_t o_sb, int64_t o_sh, int kv, int nk, int n_chunks, int64_t total) {
+  constexpr int U = kDensityItems;
   const int lane = threadIdx.x & 63;
-  const int64_t item = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  if (item >= total) return;
-  const int slot = static_cast<int>(item % nk);
-  const int64_t bh = item / nk;
-  const int b = static_cast<int>(bh / kv), h = static_cast<int>(bh % kv);
-  const int64_t cid = ids[b * id_sb + h * id_sh + slot];
-  const bool ok = cid >= 0 && cid < n_chunks;
-  float v = 0.0f;
-  if (ok) {
-    const uint16_t* c = cent + b * c_sb + h * c_sh + cid * c_sc;
+  const int64_t item0 = (static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * U;
+  if (item0 >= total) return;
+  float v[U];
+  bool ok[U];
+  int64_t oidx[U];
+  uint16_t c0[U], c1[U], q0[U], q1[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int64_t item = min(item0 + u, total - 1);
+    const int slot = static_cast<int>(item % nk);
+    const int64_t bh = item / nk;
+    const int b = static_cast<int>(bh / kv), h = static_cast<int>(bh % kv);
+    const int64_t cid = ids[b * id_sb + h * id_sh + slot];
+    ok[u] = cid >= 0 && cid < n_chunks;
+    const uint16_t* c = cent + b * c_sb + h * c_sh + (ok[u] ? cid : 0) * c_sc;
     const uint16_t* qq = q + b * q_sb + h * q_sh;
-    v = bf16_to_f32(c[lane]) * bf16_to_f32(qq[lane]) + 0.0f;
-    const float w = bf16_to_f32(c[lane + 64]) * bf16_to_f32(qq[lane + 64]);
-    v = v + w;
+    c0[u] = c[lane];
+    c1[u] = c[lane + 64];
+    q0[u] = qq[lane];
+    q1[u] = qq[lane + 64];
+    oidx[u] = b * o_sb + h * o_sh + slot;
   }
 #pragma unroll
-  for (int s = 32; s >= 1; s >>= 1) {
-    const float o = __shfl_down(v, s);
-    if (lane < s) v = v + o;
+  for (int u = 0; u < U; ++u) {
+    const float a = bf16_to_f32(c0[u]) * bf16_to_f32(q0[u]) + 0.0f;
+    const float w = bf16_to_f32(c1[u]) * bf16_to_f32(q1[u]);
+    v[u] = a + w;
   }
-  if (lane == 0) out[b * o_sb + h * o_sh + slot] = ok ? v : -1e30f;
+#pragma unroll
+  for (int s = 32; s >= 1; s >>= 1)
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const float o = __shfl_down(v[u], s);
+      if (lane < s) v[u] = v[u] + o;
+    }
+  if (lane == 0) {
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (item0 + u < total) out[oidx[u]] = ok[u] ? v[u] : -1e30f;
+  }
 }
 
 // mask.fill_(False); mask.scatter_(2, positions, True) (rerank_topk.cu:926-954)
@@ -611,7 +634,8 @@ extern "C" int zkv_chunk_density_scores(const int64_t* chunk_ids, int64_t id_sb,
   ZKV_REQUIRE(bs > 0 && kv > 0 && nk >= 0, "zkv_chunk_density_scores: bad sizes");
   const int64_t total = static_cast<int64_t>(bs) * kv * nk;
   if (total == 0) return ZKV_OK;
-  density_kernel<<<static_cast<int>((total + 3) / 4), 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(
+  density_kernel<<<static_cast<int>((total + 4 * kDensityItems - 1) / (4 * kDensityItems)), 256, 0,
+                   reinterpret_cast<hipStream_t>(stream)>>>(
       chunk_ids, id_sb, id_sh, centroids, c_sb, c_sh, c_sc, raw_q, q_sb, q_sh, out, o_sb, o_sh, kv, nk,
       n_chunks, total);
   return check_launch("density_kernel");
