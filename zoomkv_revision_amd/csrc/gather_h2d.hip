@@ -63,9 +63,11 @@ __global__ __launch_bounds__(256) void h2d_gather_packed_kernel(
 int device_alias(const void* host, const char* name, const u32x4_t** out) {
   void* d = nullptr;
   const hipError_t e = hipHostGetDevicePointer(&d, const_cast<void*>(host), 0);
-  if (e != hipSuccess || d == nullptr)
+  if (e != hipSuccess || d == nullptr) {
+    (void)hipGetLastError();  // the failed lookup must not surface at the caller's next HIP call
     return fail(ZKV_EINVAL, "zkv_h2d_gather: %s is not pinned, mapped host memory (%s)", name,
                 hipGetErrorString(e));
+  }
   if ((reinterpret_cast<uintptr_t>(d) & 15) != 0)
     return fail(ZKV_EINVAL, "zkv_h2d_gather: %s must be 16-byte aligned", name);
   *out = static_cast<const u32x4_t*>(d);

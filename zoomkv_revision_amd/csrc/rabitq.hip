@@ -364,8 +364,8 @@ __global__ __launch_bounds__(kNT1) void rabitq_stage1_kernel(
 __global__ __launch_bounds__(kNT2) void rabitq_stage2_kernel(
     const uint32_t* __restrict__ cand_key, const int32_t* __restrict__ cand_idx, int n_cand, int n_real,
     int k, const uint16_t* __restrict__ q, const uint16_t* __restrict__ keys, int64_t k_pool_stride,
-    int64_t k_row_stride, int queries, int64_t* __restrict__ out_cand, int64_t* __restrict__ out_idx,
-    float* __restrict__ out_score) {
+    int64_t k_row_stride, int64_t n_keys, int queries, int64_t* __restrict__ out_cand,
+    int64_t* __restrict__ out_idx, float* __restrict__ out_score) {
   constexpr int W = Block<kNT2>::kWaves;
   __shared__ int s_hist[W * 256];
   __shared__ uint32_t s_tmp[2 * W + 2];
@@ -404,8 +404,11 @@ __global__ __launch_bounds__(kNT2) void rabitq_stage2_kernel(
   for (int c0 = 0; c0 < k; c0 += kNT2 / 16) {
     const int c = c0 + (tid >> 4);
     float s = 0.0f;
-    if (c < k) {
-      const u32x4_t kw = *reinterpret_cast<const u32x4_t*>(kp + static_cast<int64_t>(s_sel[c]) * k_row_stride + 8 * l);
+    // stage 1 always writes valid indices; a key row is read only for an
+    // index inside the pool all the same
+    const int64_t ki = c < k ? static_cast<int64_t>(s_sel[c]) : -1;
+    if (ki >= 0 && ki < n_keys) {
+      const u32x4_t kw = *reinterpret_cast<const u32x4_t*>(kp + ki * k_row_stride + 8 * l);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float pe = qf[e] * f16_to_f32(static_cast<uint16_t>(kw[e >> 1] >> (16 * (e & 1))));
@@ -553,6 +556,6 @@ extern "C" int zkv_rabitq_search(const uint16_t* q, const uint16_t* keys, int64_
   const int n_pad = n_last < topk ? topk - static_cast<int>(n_last) : 0;
   rabitq_stage2_kernel<<<g2, kNT2, 0, s>>>(c_key, c_idx, L.n_slices * topk, L.n_slices * topk - n_pad,
                                            topk, q, keys, k_pool_stride,
-                                           k_row_stride, queries, cand_idx, final_idx, final_scores);
+                                           k_row_stride, n, queries, cand_idx, final_idx, final_scores);
   return check_launch("rabitq_stage2_kernel");
 }
