@@ -685,8 +685,9 @@ SplitPlan plan_splits(int bs, int kv, int n_groups, int res_len, int n_splits) {
     const int target = 256 * wg_per_cu;  // one resident workgroup per split on 256 CUs
     const int units = bs * kv;
     ns = (target + units - 1) / units;
-    // keep every wave busy for a few tiles at least
-    ns = std::min(ns, std::max(1, n_tiles / (2 * sh.nw)));
+    // at least one tile per wave of every split (short contexts at small
+    // batch are latency-bound: more splits beat fuller waves)
+    ns = std::min(ns, std::max(1, n_tiles / sh.nw));
   }
   ns = std::max(1, std::min(ns, n_tiles));
   const int per = (n_tiles + ns - 1) / ns;
