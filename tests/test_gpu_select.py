@@ -33,7 +33,10 @@ def test_quest_chunk_score_bit_exact(rng, fp16_meta):
 
 
 @pytest.mark.parametrize("L,k", [(2048, 128), (13120, 100), (131072, 256), (64, 64), (3000, 1),
-                                 (4096, 1638), (1638, 491), (26208, 100), (32768, 7), (32769, 300)])
+                                 (4096, 1638), (1638, 491), (26208, 100), (32768, 7), (32769, 300),
+                                 # register-bucket edges (1024 * R) and k = L - 1
+                                 (4096, 4095), (4097, 5), (8192, 8191), (8193, 64), (16384, 1),
+                                 (16385, 2048), (1025, 1024)])
 def test_topk_exact(rng, L, k):
     from zoomkv_revision_amd.topk import float_topk_3d
     x = rng.standard_normal((2, 3, L)).astype(np.float32)
@@ -180,3 +183,14 @@ def test_gather_concat_reference_cases(bs, kv, L, k, sk, max_sk, seed):
     got = from_torch(out)
     assert np.array_equal(got[..., :k + sk], osel.topk_gather_concat(sc, lut, skipped, k, k + sk))
     assert np.all(got[..., k + sk:] == -5)
+
+
+def test_topk_sentinel_heavy_rows(rng):
+    """Rows shaped like the stage-2 scores (half the slots -1e30 per 16), with
+    k larger than the number of real values in some rows."""
+    from zoomkv_revision_amd.topk import float_topk_3d
+    x = (rng.standard_normal((2, 4, 26208)) * 5).astype(np.float32)
+    x.reshape(2, 4, -1, 16)[..., 8:] = -1e30
+    x[1, 3, 200:] = -1e30                       # only 104 real values, k = 300
+    got = from_torch(float_topk_3d(torch.from_numpy(x).cuda(), 300))
+    assert np.array_equal(got, osel.topk_indices(x, 300))
