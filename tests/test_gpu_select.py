@@ -185,6 +185,21 @@ def test_gather_concat_reference_cases(bs, kv, L, k, sk, max_sk, seed):
     assert np.all(got[..., k + sk:] == -5)
 
 
+@pytest.mark.parametrize("L,k", [(26208, 100), (32768, 512), (32768, 513), (5000, 300), (12000, 1)])
+def test_topk_sampled_prefilter_edges(rng, L, k):
+    """Rows that steer the sampled prefilter of long rows to each outcome:
+    spikes on exactly the 1024 evenly spaced sample positions (fewer keys above
+    the threshold than k), integer scores with heavy ties at the threshold, a
+    row of one value (more candidates than fit), and a plain row."""
+    from zoomkv_revision_amd.topk import float_topk
+    x = rng.standard_normal((4, L)).astype(np.float32)
+    x[0, (np.arange(1024) * L) // 1024] = 1000.0 + np.arange(1024)
+    x[1] = rng.integers(0, 10, L).astype(np.float32)
+    x[2] = 3.0
+    got = from_torch(float_topk(torch.from_numpy(x).cuda(), k))
+    assert np.array_equal(got, osel.topk_indices(x, k))
+
+
 def test_topk_sentinel_heavy_rows(rng):
     """Rows shaped like the stage-2 scores (half the slots -1e30 per 16), with
     k larger than the number of real values in some rows."""

@@ -227,16 +227,267 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(
 // equal-to-T bits; the (row j, wave w) counts, in index order j-major then
 // w, are scanned once, giving every element its rank among the gt and the
 // eq elements of lower index:  pos(i) = #gt below i + min(#eq below i, remain).
+//
+// Long rows with a small k (R >= 8, k <= 512) first narrow the row to a
+// candidate list: tau = the m-th largest of 256 evenly spaced keys (top 16
+// bits), with m set so that about 8k keys of the row are >= tau; the keys >=
+// tau are compacted into LDS in index order.  When there are at least k of
+// them (and no more than 4096) the k-th largest key of the row is >= tau, so
+// every key of the top k, ties included, is a candidate and the selection
+// over the candidates is the selection over the row; otherwise the row takes
+// the full path.
 // ----------------------------------------------------------------------------
+constexpr int kTopkCand = 4096;
+constexpr int kTopkSampledMaxK = 512;
+constexpr int kTopkSample = 256;
+
+__device__ __forceinline__ uint32_t ordered_key_bits(uint32_t b) {
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+// ordered_key(x) >= tau (tau != 0) on the raw bits b of x, as one unsigned
+// compare: ((b - base) < lim) != inv.  For tau >= 2^31 (the key of a
+// non-negative float) the passing bits are [tau - 2^31, 2^31); otherwise all
+// bits except [2^32 - tau, 2^32) (the negative floats whose key is below
+// tau).  Raw bits 0xFFFFFFFF (key 0) never pass.
+struct TauTest {
+  uint32_t base, lim;
+  uint64_t inv;  // all ones when the compare result is inverted
+};
+__device__ __forceinline__ TauTest make_tau_test(uint32_t tau) {
+  if (tau >= 0x80000000u) return {tau ^ 0x80000000u, 0x80000000u - (tau ^ 0x80000000u), 0ull};
+  return {0u - tau, tau, ~0ull};
+}
+
+// Inclusive prefix sum over the 64 lanes of a wave: shifts by 1, 2, 4, 8
+// within each row of 16 lanes, then lane 15 of a row added into the next row
+// (rows 1 and 3) and lane 31 into rows 2 and 3 (DPP row_shr / row_bcast).
+__device__ __forceinline__ int wave_inclusive_sum(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);
+  return v;
+}
+
+// Per-(register row j, wave w) counts live at cnt[w * R + j]; their index
+// order is j-major, then w.  wave_exclusive_scan replaces them, by one wave,
+// with their exclusive prefix in that order and returns the total.
+template <int R>
+__device__ __forceinline__ uint32_t wave_exclusive_scan(uint32_t* cnt, int lane) {
+  constexpr int N = R * kTopkWaves, kPer = N / 64;
+  static_assert(N % 64 == 0, "whole entries per lane");
+  uint32_t v[kPer];
+  uint32_t sum = 0;
+#pragma unroll
+  for (int e = 0; e < kPer; ++e) {
+    const int idx = lane * kPer + e;  // (j, w) = (idx / 16, idx % 16)
+    v[e] = cnt[(idx % kTopkWaves) * R + idx / kTopkWaves];
+    sum += v[e];
+  }
+  const uint32_t inc = static_cast<uint32_t>(wave_inclusive_sum(static_cast<int>(sum)));
+  uint32_t run = inc - sum;
+#pragma unroll
+  for (int e = 0; e < kPer; ++e) {
+    const int idx = lane * kPer + e;
+    cnt[(idx % kTopkWaves) * R + idx / kTopkWaves] = run;
+    run += v[e];
+  }
+  return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(inc), 63));
+}
+
+// A copy of a uniform value that the compiler cannot merge with other uses:
+// the per-row bounds compares are then recomputed where they are used instead
+// of being kept live (in scalar registers that spill) across the barriers.
+__device__ __forceinline__ int opaque(int v) {
+  v = __builtin_amdgcn_readfirstlane(v);
+  asm volatile("" : "+s"(v));
+  return v;
+}
+
+// Rank of this lane's bit among the set bits of a wave mask below it.
+__device__ __forceinline__ int lanes_below(uint64_t m) {
+  return static_cast<int>(__builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
+                                                    __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0)));
+}
+
+// Radix select over the n keys key[j] at list positions tid + 1024 j (later
+// positions are ignored): returns T = the k-th largest key and sets remain =
+// how many keys == T belong to the top k.  hist[0] must be zero on entry.
+// Each round: a block histogram of the next 8 bits, then wave 0 (lane l owns
+// bins 252 - 4l .. 255 - 4l, so a prefix sum over lanes counts the keys in
+// higher bins) finds the bin holding the remain-th key.
+template <int R>
+__device__ __forceinline__ uint32_t radix_select(const uint32_t (&key)[R], int n, int k, int (*hist)[256],
+                                                 int* s_sel, int& remain) {
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  uint32_t prefix = 0, mask = 0;
+  remain = k;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int shift = 24 - 8 * r;
+    int* h = hist[r & 1];
+    const int nr = opaque(n);
+    // clear the other buffer (last read before the previous barrier) for the next round
+    if (tid < 64) reinterpret_cast<int4*>(hist[(r + 1) & 1])[tid] = make_int4(0, 0, 0, 0);
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+      const bool in = tid < nr - kTopkThreads * j && (key[j] & mask) == prefix;
+      const int bin = (key[j] >> shift) & 0xFF;
+      if (r == 0) {
+        // Float keys share few top bytes, so most lanes of a wave hit one or
+        // two bins: the two most common (by first lane) are added once per
+        // wave, the remaining lanes add one each.
+        uint64_t todo = __ballot(in);
+#pragma unroll
+        for (int it = 0; it < 2; ++it) {
+          if (todo != 0) {
+            const int lead = __builtin_ctzll(todo);
+            const int b0 = __builtin_amdgcn_readlane(bin, lead);
+            const uint64_t same = __ballot(bin == b0) & todo;
+            if (lane == lead) atomicAdd(&h[b0], static_cast<int>(__popcll(same)));
+            todo &= ~same;
+          }
+        }
+        if ((todo >> lane) & 1ull) atomicAdd(&h[bin], 1);
+      } else if (in) {
+        atomicAdd(&h[bin], 1);
+      }
+    }
+    __syncthreads();
+    if (wave == 0) {
+      const int4 c = reinterpret_cast<const int4*>(h)[63 - lane];
+      const int lane_sum = c.x + c.y + c.z + c.w;
+      int above = wave_inclusive_sum(lane_sum) - lane_sum;
+      const int cb[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+      for (int j = 3; j >= 0; --j) {
+        const int at_or_above = above + cb[j];
+        if (at_or_above >= remain && above < remain) {
+          s_sel[0] = 4 * (63 - lane) + j;
+          s_sel[1] = remain - above;
+        }
+        above = at_or_above;
+      }
+    }
+    __syncthreads();
+    prefix |= static_cast<uint32_t>(s_sel[0]) << shift;
+    mask |= 0xFFu << shift;
+    remain = s_sel[1];
+  }
+  return prefix;
+}
+
+// Calls emit(pos, p) for every list position p < n in the top k (keys > T,
+// then the first `remain` keys == T), pos = its rank in list order (< k).
+template <int R, typename Emit>
+__device__ __forceinline__ void ordered_emit(const uint32_t (&key)[R], int n, int k, uint32_t T, int remain,
+                                             uint32_t* cnt, Emit&& emit) {
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  uint32_t mine = 0;
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    const bool in_list = tid < n - kTopkThreads * j;
+    const uint64_t gt = __ballot(in_list && key[j] > T), eq = __ballot(in_list && key[j] == T);
+    const uint32_t c = static_cast<uint32_t>(__popcll(gt)) | (static_cast<uint32_t>(__popcll(eq)) << 16);
+    mine = lane == j ? c : mine;
+  }
+  if (lane < R) cnt[wave * R + lane] = mine;
+  __syncthreads();
+  if (wave == 0) wave_exclusive_scan<R>(cnt, lane);
+  __syncthreads();
+  // the ballots are recomputed rather than kept live across the barriers
+  const int n2 = opaque(n);
+  const uint32_t T2 = static_cast<uint32_t>(opaque(static_cast<int>(T)));
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    const bool in_list = tid < n2 - kTopkThreads * j;
+    const bool is_gt = in_list && key[j] > T2, is_eq = in_list && key[j] == T2;
+    const uint64_t gt = __ballot(is_gt), eq = __ballot(is_eq);
+    if ((gt | eq) != 0) {
+      const uint32_t pre = cnt[wave * R + j];
+      const int gt_rank = static_cast<int>(pre & 0xFFFFu) + lanes_below(gt);
+      const int eq_rank = static_cast<int>(pre >> 16) + lanes_below(eq);
+      const int pos = gt_rank + min(eq_rank, remain);
+      if ((is_gt || (is_eq && eq_rank < remain)) && pos < k) emit(pos, tid + kTopkThreads * j);
+    }
+  }
+}
+
+// The candidate path of a sampled row (see above); false when the number of
+// keys >= tau is outside [k, kTopkCand] and the row must take the full path.
+// bits[j]: raw float bits of row index tid + 1024 j, 0xFFFFFFFF past the row.
+// The ballots are recomputed after the barrier rather than kept live.
+template <int R>
+__device__ __forceinline__ bool topk_from_candidates(const uint32_t (&bits)[R], int L, int k, const TauTest tt,
+                                                     uint32_t* s_cnt, uint2* s_cand, int (*s_hist)[256],
+                                                     int* s_sel, uint32_t* s_total, int64_t* o,
+                                                     const int64_t* lrow) {
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  int mine = 0;
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    if (kTopkThreads * j < L) {
+      const uint64_t m = __ballot(bits[j] - tt.base < tt.lim) ^ tt.inv;
+      mine = lane == j ? __popcll(m) : mine;
+    }
+  }
+  if (lane < R) s_cnt[wave * R + lane] = static_cast<uint32_t>(mine);
+  __syncthreads();
+  if (wave == 0) {
+    const uint32_t total = wave_exclusive_scan<R>(s_cnt, lane);
+    if (lane == 0) *s_total = total;
+  }
+  __syncthreads();
+  const int total = static_cast<int>(*s_total);
+  if (total < k || total > kTopkCand) return false;
+  // the ballots are recomputed rather than kept live across the barriers
+  const int L2 = opaque(L);
+  const uint32_t base2 = static_cast<uint32_t>(opaque(static_cast<int>(tt.base)));
+  const uint32_t lim2 = static_cast<uint32_t>(opaque(static_cast<int>(tt.lim)));
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    if (kTopkThreads * j < L2) {
+      const bool pass = bits[j] - base2 < lim2;
+      const uint64_t m = __ballot(pass) ^ tt.inv;
+      if (m != 0) {
+        const int p = static_cast<int>(s_cnt[wave * R + j]) + lanes_below(m);
+        if (pass != (tt.inv != 0) && p < kTopkCand)
+          s_cand[p] = make_uint2(bits[j], static_cast<uint32_t>(tid + kTopkThreads * j));
+      }
+    }
+  }
+  __syncthreads();
+  constexpr int kQ = kTopkCand / kTopkThreads;
+  uint32_t ck[kQ];
+#pragma unroll
+  for (int q = 0; q < kQ; ++q)
+    ck[q] = tid < total - kTopkThreads * q ? ordered_key_bits(s_cand[tid + kTopkThreads * q].x) : 0u;
+  int remain;
+  const uint32_t T = radix_select<kQ>(ck, total, k, s_hist, s_sel, remain);
+  ordered_emit<kQ>(ck, total, k, T, remain, s_cnt, [&](int pos, int p) {
+    const int i = static_cast<int>(s_cand[p].y);
+    o[pos] = lrow ? lrow[i] : i;
+  });
+  return true;
+}
+
 template <int R>
 __global__ __launch_bounds__(kTopkThreads) void topk_reg_kernel(
     const float* __restrict__ in, int64_t in_stride, int L, int k, int64_t* __restrict__ out,
     int64_t out_stride, const int64_t* __restrict__ lut, int64_t lut_stride,
     const int64_t* __restrict__ skipped, int64_t sk_stride, int sk_count, int64_t sentinel) {
-  __shared__ int s_hist[2][kTopkWaves][256];
-  __shared__ int s_merged[256];
-  __shared__ uint32_t s_cnt[R * kTopkWaves];  // (j, w) -> gt | eq << 16, then its exclusive prefix
-  __shared__ int s_bin, s_remain;
+  constexpr bool kSampled = R >= 8;
+  constexpr int kCand = kSampled ? kTopkCand : 1;
+  static_assert(R % 4 == 0 && R * kTopkWaves >= 64, "register rows come in fours");
+  static_assert(kTopkThreads * R <= 65536, "16-bit counts per (j, w) prefix");
+  __shared__ __align__(16) int s_hist[2][256];
+  __shared__ __align__(16) uint32_t s_cnt[R * kTopkWaves];  // [w][j] counts, then their exclusive prefix
+  __shared__ uint2 s_cand[kCand];  // the sample keys, then (raw bits, index) of the candidates
+  __shared__ int s_sel[2];
+  __shared__ uint32_t s_tau, s_total;
   const int row = blockIdx.x;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const float* x = in + row * in_stride;
@@ -248,112 +499,61 @@ __global__ __launch_bounds__(kTopkThreads) void topk_reg_kernel(
     for (int i = tid; i < k; i += kTopkThreads) o[i] = (i < L) ? (lrow ? lrow[i] : i) : sentinel;
     return;
   }
+  // All loads are issued before any is used (addresses clamped into the row),
+  // the sample first, and the threshold search runs while the row arrives.
+  const bool sampled = kSampled && k <= kTopkSampledMaxK;
+  float sample = 0.0f;
+  if constexpr (kSampled) {
+    sample = x[((tid % kTopkSample) * L) / kTopkSample];
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  float v[R];
+#pragma unroll
+  for (int j = 0; j < R; ++j) v[j] = x[kTopkThreads * j + min(tid, L - 1 - kTopkThreads * j)];
+  // every thread stores its (possibly repeated) sample key, so the load is not sunk below the row loads
+  if constexpr (kSampled) reinterpret_cast<uint32_t*>(s_cand)[tid] = ordered_key(sample);
+  if (tid < 128) reinterpret_cast<int4*>(&s_hist[0][0])[tid] = make_int4(0, 0, 0, 0);
+  __syncthreads();
+  uint32_t tau = 0;
+  if constexpr (kSampled) {
+    if (sampled) {
+      if (wave == 0) {
+        constexpr int kPer = kTopkSample / 64;
+        uint32_t sv[kPer];
+#pragma unroll
+        for (int e = 0; e < kPer; ++e) sv[e] = reinterpret_cast<const uint32_t*>(s_cand)[e * 64 + lane];
+        const int target = min(8 * k, kTopkCand / 2);
+        const int m = min(kTopkSample, max(1, (target * kTopkSample + L - 1) / L));
+        uint32_t t = 0;
+        for (int b = 31; b >= 16; --b) {
+          const uint32_t c = t | (1u << b);
+          int cnt = 0;
+#pragma unroll
+          for (int e = 0; e < kPer; ++e) cnt += __popcll(__ballot(sv[e] >= c));
+          if (cnt >= m) t = c;
+        }
+        if (lane == 0) s_tau = t;
+      }
+      __syncthreads();
+      tau = s_tau;
+    }
+  }
+  uint32_t bits[R];
+#pragma unroll
+  for (int j = 0; j < R; ++j) bits[j] = tid < L - kTopkThreads * j ? __float_as_uint(v[j]) : ~0u;
+  if constexpr (kSampled) {
+    if (sampled && tau != 0) {
+      if (topk_from_candidates<R>(bits, L, k, make_tau_test(tau), s_cnt, s_cand, s_hist, s_sel, &s_total, o,
+                                  lrow))
+        return;
+    }
+  }
   uint32_t key[R];
 #pragma unroll
-  for (int j = 0; j < R; ++j) {
-    const int i = tid + kTopkThreads * j;
-    key[j] = i < L ? ordered_key(x[i]) : 0u;
-  }
-  for (int i = tid; i < kTopkWaves * 256; i += kTopkThreads) (&s_hist[0][0][0])[i] = 0;
-  __syncthreads();
-
-  uint32_t prefix = 0, mask = 0;
-  int remain = k;
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int shift = 24 - 8 * r;
-    int (*hist)[256] = s_hist[r & 1];
-    // clear the other buffer (last read two barriers ago) for the next round
-    for (int i = tid; i < kTopkWaves * 256; i += kTopkThreads) (&s_hist[(r + 1) & 1][0][0])[i] = 0;
-#pragma unroll
-    for (int j = 0; j < R; ++j)
-      if (tid + kTopkThreads * j < L && (key[j] & mask) == prefix)
-        atomicAdd(&hist[wave][(key[j] >> shift) & 0xFF], 1);
-    __syncthreads();
-    if (tid < 256) {
-      int c = 0;
-#pragma unroll
-      for (int w = 0; w < kTopkWaves; ++w) c += hist[w][tid];
-      s_merged[tid] = c;
-    }
-    __syncthreads();
-    if (tid < 64) {
-      int c[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) c[j] = s_merged[4 * tid + j];
-      const int lane_sum = c[0] + c[1] + c[2] + c[3];
-      int suf = lane_sum;
-#pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        const int v = __shfl_down(suf, off);
-        if (tid + off < 64) suf += v;
-      }
-      int above = suf - lane_sum;
-#pragma unroll
-      for (int j = 3; j >= 0; --j) {
-        const int at_or_above = above + c[j];
-        if (at_or_above >= remain && above < remain) {
-          s_bin = 4 * tid + j;
-          s_remain = remain - above;
-        }
-        above = at_or_above;
-      }
-    }
-    __syncthreads();
-    prefix |= static_cast<uint32_t>(s_bin) << shift;
-    mask |= 0xFFu << shift;
-    remain = s_remain;
-  }
-  const uint32_t T = prefix;
-  uint64_t bgt[R], beq[R];
-#pragma unroll
-  for (int j = 0; j < R; ++j) {
-    const bool in_row = tid + kTopkThreads * j < L;
-    bgt[j] = __ballot(in_row && key[j] > T);
-    beq[j] = __ballot(in_row && key[j] == T);
-    if (lane == 0)
-      s_cnt[j * kTopkWaves + wave] = static_cast<uint32_t>(__popcll(bgt[j])) |
-                                     (static_cast<uint32_t>(__popcll(beq[j])) << 16);
-  }
-  __syncthreads();
-  if (tid < 64) {
-    // exclusive scan of the R * 16 entries (at most 512: 8 per lane, in order)
-    constexpr int kPer = (R * kTopkWaves + 63) / 64;
-    uint32_t v[kPer];
-    uint32_t sum = 0;
-#pragma unroll
-    for (int e = 0; e < kPer; ++e) {
-      const int idx = tid * kPer + e;
-      v[e] = idx < R * kTopkWaves ? s_cnt[idx] : 0u;
-      sum += v[e];
-    }
-    uint32_t inc = sum;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const uint32_t t = __shfl_up(inc, off);
-      if (tid >= off) inc += t;
-    }
-    uint32_t run = inc - sum;
-#pragma unroll
-    for (int e = 0; e < kPer; ++e) {
-      const int idx = tid * kPer + e;
-      if (idx < R * kTopkWaves) s_cnt[idx] = run;
-      run += v[e];
-    }
-  }
-  __syncthreads();
-  const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-#pragma unroll
-  for (int j = 0; j < R; ++j) {
-    const uint32_t pre = s_cnt[j * kTopkWaves + wave];
-    const int gt_rank = static_cast<int>(pre & 0xFFFFu) + __popcll(bgt[j] & below);
-    const int eq_rank = static_cast<int>(pre >> 16) + __popcll(beq[j] & below);
-    const bool is_gt = (bgt[j] >> lane) & 1ull, is_eq = (beq[j] >> lane) & 1ull;
-    if (is_gt || (is_eq && eq_rank < remain)) {
-      const int i = tid + kTopkThreads * j;
-      o[gt_rank + min(eq_rank, remain)] = lrow ? lrow[i] : i;
-    }
-  }
+  for (int j = 0; j < R; ++j) key[j] = ordered_key_bits(bits[j]);
+  int remain;
+  const uint32_t T = radix_select<R>(key, L, k, s_hist, s_sel, remain);
+  ordered_emit<R>(key, L, k, T, remain, s_cnt, [&](int pos, int i) { o[pos] = lrow ? lrow[i] : i; });
 }
 
 // ----------------------------------------------------------------------------
