@@ -654,9 +654,11 @@ __global__ __launch_bounds__(256) void kivi_qk_kernel(
     float* __restrict__ out_s, int64_t* __restrict__ out_i, int64_t o_sb, int64_t o_sh, int nk,
     int dense_topk, int sparse_topk) {
   constexpr int kChunks = 256 / G;
-  __shared__ float s_q[kChunks][128];
-  __shared__ float s_mn[kChunks][128];
-  __shared__ float s_sc[kChunks][128];
+  // q is the same for every chunk of the block; the per-chunk rows are padded
+  // by 4 floats so that the chunks of one wave read different LDS banks.
+  __shared__ float s_q[128];
+  __shared__ float s_mn[kChunks][132];
+  __shared__ float s_sc[kChunks][132];
   const int b = blockIdx.z, h = blockIdx.y;
   const int local = threadIdx.x / G, lane = threadIdx.x % G;
   const int slot = blockIdx.x * kChunks + local;
@@ -668,13 +670,19 @@ __global__ __launch_bounds__(256) void kivi_qk_kernel(
     dense = dmask[b * dm_sb + h * dm_sh + slot] != 0;
   }
   const bool in_range = cid >= 0 && cid < n_packed;
+  // the code words are loaded before the metadata so both latencies overlap
+  uint32_t words[16];
+  {
+    const int32_t* w = packed + b * pk_sb + h * pk_sh + (valid_slot && in_range ? cid : 0) * (16 * G) + lane;
+#pragma unroll
+    for (int p = 0; p < 16; ++p) words[p] = static_cast<uint32_t>(w[p * G]);
+  }
+  if (threadIdx.x < 128) s_q[threadIdx.x] = bf16_to_f32(q[b * q_sb + h * q_sh + threadIdx.x]);
   if (valid_slot) {
-    const uint16_t* qp = q + b * q_sb + h * q_sh;
     const int64_t mrow = (b * cm_sb + h * cm_sh) + (cid >= 0 && cid < n_max ? cid : 0) * 128;
     for (int d = lane; d < 128; d += G) {
       const float mn = bf16_to_f32(cmin[mrow + d]);
       const float mx = bf16_to_f32(cmax[mrow + d]);
-      s_q[local][d] = bf16_to_f32(qp[d]);
       s_mn[local][d] = mn;
       s_sc[local][d] = bf16r(bf16r(mx - mn) / 15.0f);
     }
@@ -683,25 +691,22 @@ __global__ __launch_bounds__(256) void kivi_qk_kernel(
   float score = -1e30f;
   int token = static_cast<int>(cid) * G + lane;
   if (valid_slot && in_range) {
-    const int32_t* w = packed + b * pk_sb + h * pk_sh + cid * (16 * G) + lane;
     float acc = 0.0f;
-#pragma unroll 2
-    for (int p = 0; p < 16; ++p) {
-      const uint32_t word = static_cast<uint32_t>(w[p * G]);
 #pragma unroll
-      for (int j = 0; j < 8; j += 2) {
-        // channels d, d + 1 side by side (each rounding of the pair is one
-        // packed conversion); the sum stays sequential in d
-        const int d = 8 * p + j;
-        const float2_t code = {static_cast<float>((word >> (4 * j)) & 0xFu),
-                               static_cast<float>((word >> (4 * j + 4)) & 0xFu)};
-        const float2_t sc = {s_sc[local][d], s_sc[local][d + 1]};
-        const float2_t mn = {s_mn[local][d], s_mn[local][d + 1]};
-        const float2_t qq = {s_q[local][d], s_q[local][d + 1]};
-        const float2_t kd = bf16r2(bf16r2(code * sc) + mn);
-        const float2_t pr = bf16r2(kd * qq);
-        acc = acc + pr[0];
-        acc = acc + pr[1];
+    for (int p = 0; p < 16; ++p) {
+      const uint32_t word = words[p];
+      // nibbles 0, 2, 4, 6 (channels 8p, +2, +4, +6) in the bytes of lo,
+      // nibbles 1, 3, 5, 7 in the bytes of hi: one byte-to-float each
+      uint32_t lo = word & 0x0F0F0F0Fu, hi = (word >> 4) & 0x0F0F0F0Fu;
+      // (kept opaque so the byte extraction below stays v_cvt_f32_ubyteN
+      // instead of being folded back into a 4-bit field extract per channel)
+      asm volatile("" : "+v"(lo), "+v"(hi));
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int d = 8 * p + j;  // the sum stays sequential in d
+        const float code = static_cast<float>(((j & 1 ? hi : lo) >> (8 * (j >> 1))) & 0xFFu);
+        const float kd = bf16r(bf16r(code * s_sc[local][d]) + s_mn[local][d]);
+        acc = acc + bf16r(kd * s_q[d]);
       }
     }
     score = acc;

@@ -52,14 +52,18 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float x) {
   return __builtin_bit_cast(uint16_t, static_cast<__bf16>(x));
 }
 
-__device__ __forceinline__ float bf16r(float x) { return static_cast<float>(static_cast<__bf16>(x)); }
-
-// Two roundings in one v_cvt_pk_bf16_f32.
 typedef float float2_t __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ float2_t bf16r2(float2_t x) {
-  return __builtin_convertvector(__builtin_convertvector(x, bf16x2_t), float2_t);
+
+// x rounded to bf16, as an fp32 value: one v_cvt_pk_bf16_f32 with x in the
+// high half and +0 in the low half, whose 32-bit result is exactly the fp32
+// encoding of bf16(x) (no shift or mask to unpack).
+__device__ __forceinline__ float bf16r(float x) {
+  const float2_t v = {0.0f, x};
+  return __builtin_bit_cast(float, __builtin_convertvector(v, bf16x2_t));
 }
+
+__device__ __forceinline__ float2_t bf16r2(float2_t x) { return float2_t{bf16r(x[0]), bf16r(x[1])}; }
 
 __device__ __forceinline__ uint16_t f32_to_f16_bits(float x) {
   _Float16 h = static_cast<_Float16>(x);
