@@ -329,6 +329,36 @@ int zkv_h2d_gather_kv_packed(const void* src_k, const void* src_v, int bs, int k
                              const int32_t* cu_seqlens_topk, const int32_t* cu_seqlens_k, int sl_end,
                              int global_k, zkv_stream_t stream);
 
+/* ---- decode-step model layers (the C5 counterpart of layer_decode) ------ */
+
+/* y = x . w^T for the M <= 16 rows of a decode batch: x [M, K] bf16 (row
+ * stride x_ld, 16-byte aligned), w [N, K] bf16 contiguous, fp32 accumulate,
+ * y [M, N] bf16 (or fp32 holding the bf16 value when out_f32), row stride
+ * out_ld.  K must be a multiple of 128 and M * K * 2 bytes must fit 96 KiB.
+ * norm_w (nullable): x is first replaced by bf16(x * rsqrt(mean(x^2) + eps) *
+ * norm_w) per row.  epilogue 0: none; 1: y = bf16(residual + bf16(x . w^T))
+ * (residual [M, N] bf16, row stride res_ld); 2: w rows [0, N/2) are gate and
+ * [N/2, N) up, y [M, N/2] = bf16(bf16(silu(gate)) * up).
+ * Replaces the torch rmsnorm + F.linear (+ residual add / silu * up) of
+ * Z/model_hub/LLM.py:208-251 and the flashinfer rmsnorm / silu of
+ * Z/model_hub/qwen.py:493-604. */
+int zkv_decode_linear(const uint16_t* x, int64_t x_ld, int M, int K, const uint16_t* w, int N,
+                      const uint16_t* norm_w, float eps, const uint16_t* residual, int64_t res_ld, void* out,
+                      int64_t out_ld, int out_f32, int epilogue, zkv_stream_t stream);
+
+/* qkv [bs, (hq + 2 hkv) * 128] bf16 (row stride qkv_ld): per-head RMSNorm of
+ * the hq q heads (q_norm) and hkv k heads (k_norm), each rounded to bf16, then
+ * rotate-half RoPE with the position's cos / sin rows (fp32 [64]) rounded to
+ * bf16: q to q_out [bs, hq, 128]; k to k_dst + b * k_sb + h * k_sh and v
+ * (copied) to v_dst + b * v_sb + h * v_sh (element strides; 128 contiguous
+ * channels per row).  Replaces the q / k norms and RoPE of
+ * Z/model_hub/qwen.py:493-545 and the cache append of decode_update_kv_cache
+ * (S:1516-1583). */
+int zkv_qk_norm_rope(const uint16_t* qkv, int64_t qkv_ld, int bs, int hq, int hkv, const uint16_t* q_norm,
+                     const uint16_t* k_norm, float eps, const float* cos_row, const float* sin_row,
+                     uint16_t* q_out, uint16_t* k_dst, int64_t k_sb, int64_t k_sh, uint16_t* v_dst,
+                     int64_t v_sb, int64_t v_sh, zkv_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

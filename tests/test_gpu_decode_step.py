@@ -35,3 +35,101 @@ def test_decode_steps_through_polar_cache_with_a_flush(monkeypatch):
     assert ((toks >= 0) & (toks < geo.vocab)).all()
     b = ds.attention_path_bytes(cache, 0)
     assert b["total"] > b["quest"] > 0
+
+
+def _bf16_close(got, ref, ulps=1.0):
+    """Within `ulps` bf16 units at the tensor's largest magnitude (the fp32
+    accumulation order differs from the library GEMM's)."""
+    got, ref = got.float(), ref.float()
+    scale = ref.abs().max().item()
+    tol = ulps * scale * 2.0 ** -7 + 1e-6
+    err = (got - ref).abs().max().item()
+    assert err <= tol, (err, tol)
+
+
+@pytest.mark.parametrize("M,K,N", [(4, 2560, 6144), (1, 512, 1000), (16, 256, 48), (4, 9728, 2560)])
+def test_decode_linear_plain_and_norm(M, K, N):
+    g = torch.Generator(device="cuda").manual_seed(M * 7 + N)
+    x = torch.randn(M, K, generator=g, device="cuda").to(torch.bfloat16)
+    w = (torch.randn(N, K, generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+    nw = (torch.rand(K, generator=g, device="cuda") + 0.5).to(torch.bfloat16)
+    out = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    ds.decode_linear(x, w, out)
+    _bf16_close(out, (x.float() @ w.float().T).to(torch.bfloat16))
+    xn = ds.rms_norm(x, nw, 1e-6)
+    ds.decode_linear(x, w, out, norm_w=nw, eps=1e-6)
+    _bf16_close(out, (xn.float() @ w.float().T).to(torch.bfloat16), ulps=2.0)
+    out32 = torch.empty(M, N, dtype=torch.float32, device="cuda")
+    ds.decode_linear(x, w, out32, norm_w=nw, eps=1e-6)
+    assert torch.equal(out32, out32.to(torch.bfloat16).float())        # bf16 values held in fp32
+    assert torch.equal(out32.to(torch.bfloat16), out)
+
+
+def test_decode_linear_residual_and_silu_mul():
+    g = torch.Generator(device="cuda").manual_seed(5)
+    M, K, F_ = 4, 2560, 9728
+    x = torch.randn(M, K, generator=g, device="cuda").to(torch.bfloat16)
+    w = (torch.randn(2 * F_, K, generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+    act = torch.empty(M, F_, dtype=torch.bfloat16, device="cuda")
+    ds.decode_linear(x, w, act, silu_mul=True)
+    y = (x.float() @ w.float().T).to(torch.bfloat16)
+    ref = torch.nn.functional.silu(y[:, :F_]) * y[:, F_:]
+    _bf16_close(act, ref, ulps=2.0)
+    wo = (torch.randn(K, F_, generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+    res = torch.randn(M, K, generator=g, device="cuda").to(torch.bfloat16)
+    h = torch.empty(M, K, dtype=torch.bfloat16, device="cuda")
+    ds.decode_linear(act, wo, h, residual=res)
+    _bf16_close(h, res + (act.float() @ wo.float().T).to(torch.bfloat16), ulps=2.0)
+
+
+def test_decode_linear_rejects_bad_shapes():
+    from zoomkv_revision_amd._lib import ZkvError
+    x = torch.zeros(4, 200, dtype=torch.bfloat16, device="cuda")
+    w = torch.zeros(16, 200, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(ZkvError):                                        # K not a multiple of 128
+        ds.decode_linear(x, w, torch.empty(4, 16, dtype=torch.bfloat16, device="cuda"))
+
+
+def test_qk_norm_rope_and_append_match_torch():
+    geo = ds.Qwen3Geometry(layers=1, hidden=256, heads=32, kv_heads=8, head_dim=128, ffn=512, vocab=1000)
+    m = ds.RandomQwen3(geo, "cuda", seed=3, max_position=4096)
+    L = m.layers[0]
+    L["q_norm"] = (torch.rand(128, device="cuda") + 0.5).to(torch.bfloat16)
+    L["k_norm"] = (torch.rand(128, device="cuda") + 0.5).to(torch.bfloat16)
+    bs, pos = 3, 3001
+    qkv = torch.randn(bs, (32 + 16) * 128, device="cuda").to(torch.bfloat16)
+    q = torch.empty(bs, 1, 32, 128, dtype=torch.bfloat16, device="cuda")
+    K = torch.zeros(bs, 8, 40, 128, dtype=torch.bfloat16, device="cuda")
+    V = torch.zeros_like(K)
+    ds.qk_norm_rope(qkv, 32, 8, L["q_norm"], L["k_norm"], geo.eps, m.cos[pos], m.sin[pos], q,
+                    K[:, :, 17], V[:, :, 17])
+    qr, kr, vr = qkv.split([32 * 128, 8 * 128, 8 * 128], dim=-1)
+    q_ref = m._rope(ds.rms_norm(qr.reshape(bs, 1, 32, 128), L["q_norm"], geo.eps), pos)
+    k_ref = m._rope(ds.rms_norm(kr.reshape(bs, 1, 8, 128), L["k_norm"], geo.eps), pos)
+    _bf16_close(q, q_ref, ulps=2.0)
+    _bf16_close(K[:, :, 17], k_ref[:, 0], ulps=2.0)
+    assert torch.equal(V[:, :, 17], vr.reshape(bs, 8, 128))
+    assert not K[:, :, 16].any() and not K[:, :, 18].any()              # only the reserved row
+
+
+def test_fused_decode_step_matches_torch_layers(monkeypatch):
+    for k, v in ds.PRODUCTION_ENV.items():
+        monkeypatch.setenv(k, v)
+    monkeypatch.delenv("POLAR_FORCE_CAND_TOKENS", raising=False)
+    geo = ds.Qwen3Geometry(layers=2, hidden=256, heads=32, kv_heads=8, head_dim=128, ffn=512, vocab=1000)
+    dev = torch.device("cuda:0")
+    batch, context = 2, 4096
+    outs = []
+    for fused in (True, False):
+        model = ds.RandomQwen3(geo, dev, seed=42, max_position=8192, fused=fused)
+        cache = ds.build_cache(geo, batch, context, 8, 64, 2048, dev)
+        ds.fill_cache(cache, geo, batch, context, 43, dev)
+        tok = torch.tensor([5, 77], device=dev)
+        logits = [model.decode_step(tok, cache) for _ in range(3)]
+        outs.append((logits, cache))
+    (lf, cf), (lt, ct) = outs
+    assert cf.context == ct.context == context + 3
+    for a, b in zip(lf, lt):
+        _bf16_close(a, b, ulps=8.0)
+    row = ct._near0 + (ct.current_seq_len[0] - 1 - int(ct.cpu_valid_end[0]))
+    _bf16_close(cf.unified_keys[1][:, :, row], ct.unified_keys[1][:, :, row], ulps=8.0)

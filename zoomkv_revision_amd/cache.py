@@ -440,6 +440,17 @@ class polar_cache:
     def decode_update_kv_cache(self, key_states, value_states, layer_idx):
         """Append one token ([bs, 1, kv, 128]) of one layer; the flush runs at
         layer 0 of the step after the near zone filled.  Returns (None, None)."""
+        row = self.decode_reserve_row(layer_idx)
+        self.unified_keys[layer_idx][:, :, row] = key_states[:, 0].to(self.dtype)
+        self.unified_values[layer_idx][:, :, row] = value_states[:, 0].to(self.dtype)
+        return None, None
+
+    def decode_reserve_row(self, layer_idx) -> int:
+        """The bookkeeping of decode_update_kv_cache without the write: runs the
+        flush when due, commits the token and returns the row of
+        unified_keys[layer_idx] / unified_values[layer_idx] ([bs, kv, rows,
+        128]) that the token's K / V must be written to (before the next
+        compute of this layer)."""
         cur = self.current_seq_len[layer_idx]
         if layer_idx == 0:
             near_len = cur - min(self.sink_size, cur) - int(self.cpu_valid_end[0])
@@ -450,15 +461,13 @@ class polar_cache:
         pos = cur - int(self.cpu_valid_end[layer_idx])
         if not 0 <= pos < self.gpu_kv_capacity:
             raise RuntimeError(f"near-zone write at {pos} outside [0, {self.gpu_kv_capacity}) (layer {layer_idx})")
-        self.unified_keys[layer_idx][:, :, self._near0 + pos] = key_states[:, 0].to(self.dtype)
-        self.unified_values[layer_idx][:, :, self._near0 + pos] = value_states[:, 0].to(self.dtype)
         self.current_seq_len[layer_idx] = cur + 1
         if layer_idx == self.layer_num - 1:
             if not all(n == self.current_seq_len[0] for n in self.current_seq_len):
                 raise RuntimeError(f"decode step layer lengths diverged: {self.current_seq_len}")
             self._decode_step_counter += 1
             self.context += 1
-        return None, None
+        return self._near0 + pos
 
     # ------------------------------------------------------------------
     # decode attention (S:1589-1775) and selection (S:2195-2467, 2688-2779)

@@ -1,0 +1,303 @@
+// Model-side kernels of one decode step (the C5 counterpart of the reference
+// runtime's layer_decode, Z/model_hub/LLM.py:208-251, with the rmsnorm /
+// rope / silu pieces of Z/model_hub/qwen.py:493-604):
+//
+//  * decode_linear_kernel: y[m, n] = sum_k x[m, k] * w[n, k] for the few rows
+//    m of a decode batch (M <= 16), bf16 in, fp32 accumulate, bf16 out, with
+//    an optional RMSNorm of x on the way in and an optional epilogue
+//    (residual add, or silu(gate) * up over the two halves of w).  The
+//    weights are streamed once from HBM: a workgroup owns 16 output rows, its
+//    waves split K, each k-block of 128 is four v_mfma_f32_16x16x32_bf16 with
+//    the 16 weight rows as A and the (normalised) x rows, staged in LDS, as
+//    the B columns.
+//  * qk_norm_rope_kernel: per-head RMSNorm of q and k, rotate-half RoPE at
+//    one position, and the k / v rows written straight into the cache.
+//
+// Rounding follows the torch restatement: every bf16 tensor of the
+// reference is rounded (RNE) where the reference materialises it.
+#include "zkv_common.hpp"
+
+namespace zkv {
+namespace {
+
+typedef __bf16 bf16x8v_t __attribute__((ext_vector_type(8)));
+
+constexpr int kLinKBlock = 128;  // four MFMA k-chunks of 32
+constexpr int kLinMaxM = 16;     // MFMA B columns
+
+enum LinearEpilogue : int { kEpiNone = 0, kEpiResidual = 1, kEpiSiluMul = 2 };
+
+struct LinearParams {
+  const uint16_t* x;  // [M, K] bf16, row stride x_ld
+  int64_t x_ld;
+  const uint16_t* w;  // [N, K] bf16, contiguous rows
+  const uint16_t* norm_w;  // [K] bf16 or null
+  float eps;
+  const uint16_t* res;  // [M, N] bf16 (residual epilogue), row stride res_ld
+  int64_t res_ld;
+  void* out;  // [M, N] (or [M, N / 2] for silu * up), row stride out_ld
+  int64_t out_ld;
+  int M, K, N;
+  int out_f32;
+};
+
+__device__ __forceinline__ float wave_sum(float v) {
+  // butterfly over the 64 lanes (every lane ends with the total)
+  v += __shfl_xor(v, 32);
+  v += __shfl_xor(v, 16);
+  v += __shfl_xor(v, 8);
+  v += __shfl_xor(v, 4);
+  v += __shfl_xor(v, 2);
+  v += __shfl_xor(v, 1);
+  return v;
+}
+
+__device__ __forceinline__ void store_y(const LinearParams& p, int m, int n, float y) {
+  if (p.out_f32)
+    reinterpret_cast<float*>(p.out)[m * p.out_ld + n] = y;
+  else
+    reinterpret_cast<uint16_t*>(p.out)[m * p.out_ld + n] = f32_to_bf16_bits(y);
+}
+
+// One workgroup per tile of 16 output rows (silu * up: 8 gate rows and the 8
+// matching up rows), NW waves splitting the K blocks.  Dynamic LDS: the M x K
+// bf16 input rows, then NW x 64 x 4 fp32 partial tiles.
+template <int kEpi, bool kNorm>
+__global__ __launch_bounds__(1024) void decode_linear_kernel(const LinearParams p) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  uint16_t* xs = reinterpret_cast<uint16_t*>(lds);
+  const int nw = blockDim.x >> 6;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int c = lane & 15, g = lane >> 4;
+  const int M = p.M, K = p.K;
+  float* red = reinterpret_cast<float*>(lds + static_cast<size_t>(M) * K * 2);
+
+  // ---- stage x (optionally RMS-normalised: bf16(x * rsqrt(mean(x^2) + eps) * w)) ----
+  const int kv8 = K >> 3;  // 16-byte chunks per row
+  if constexpr (kNorm) {
+    // wave m' reduces rows m = m', m' + nw, ... (fixed order: deterministic)
+    for (int m = wave; m < M; m += nw) {
+      const u32x4_t* xr = reinterpret_cast<const u32x4_t*>(p.x + m * p.x_ld);
+      float ss = 0.0f;
+      for (int i = lane; i < kv8; i += 64) {
+        const u32x4_t v = xr[i];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float lo = __uint_as_float(v[e] << 16), hi = __uint_as_float(v[e] & 0xFFFF0000u);
+          ss = ss + lo * lo;
+          ss = ss + hi * hi;
+        }
+      }
+      // mean as the sum times 1/K (torch's mean), then rsqrt(mean + eps)
+      ss = wave_sum(ss);
+      if (lane == 0) red[m] = rsqrtf(ss * (1.0f / static_cast<float>(K)) + p.eps);
+    }
+    __syncthreads();
+  }
+  for (int i = tid; i < M * kv8; i += blockDim.x) {
+    const int m = i / kv8, k8 = i - m * kv8;
+    u32x4_t v = reinterpret_cast<const u32x4_t*>(p.x + m * p.x_ld)[k8];
+    if constexpr (kNorm) {
+      const float r = red[m];
+      const u32x4_t wv = reinterpret_cast<const u32x4_t*>(p.norm_w)[k8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float lo = bf16r((__uint_as_float(v[e] << 16) * r) * __uint_as_float(wv[e] << 16));
+        const float hi = bf16r((__uint_as_float(v[e] & 0xFFFF0000u) * r) * __uint_as_float(wv[e] & 0xFFFF0000u));
+        v[e] = (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xFFFF0000u);
+      }
+    }
+    reinterpret_cast<u32x4_t*>(xs)[i] = v;
+  }
+  __syncthreads();
+
+  // ---- weight rows of this tile ----
+  const int tile = blockIdx.x;
+  int row;  // weight row of A row c (or -1 past N)
+  if constexpr (kEpi == kEpiSiluMul) {
+    const int half = p.N >> 1, j = tile * 8 + (c & 7);
+    row = j < half ? (c < 8 ? j : half + j) : -1;
+  } else {
+    row = tile * 16 + c < p.N ? tile * 16 + c : -1;
+  }
+  const uint16_t* wr = p.w + static_cast<int64_t>(row < 0 ? 0 : row) * K;
+  const bool col_ok = c < M;
+  const uint16_t* xr = xs + (col_ok ? c : 0) * K;
+
+  float4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  const int nkb = K / kLinKBlock;
+  for (int kb = wave; kb < nkb; kb += nw) {
+    u32x4_t a[4], b[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int k = kb * kLinKBlock + 32 * j + 8 * g;
+      a[j] = row >= 0 ? *reinterpret_cast<const u32x4_t*>(wr + k) : u32x4_t{0u, 0u, 0u, 0u};
+      b[j] = col_ok ? *reinterpret_cast<const u32x4_t*>(xr + k) : u32x4_t{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8v_t, a[j]),
+                                                    __builtin_bit_cast(bf16x8v_t, b[j]), acc, 0, 0, 0);
+  }
+
+  // ---- sum the waves' partial tiles in wave order, then the epilogue ----
+  reinterpret_cast<float4_t*>(red)[wave * 64 + lane] = acc;
+  __syncthreads();
+  if (wave != 0) return;
+  float4_t s = reinterpret_cast<const float4_t*>(red)[lane];
+  for (int w = 1; w < nw; ++w) {
+    const float4_t t = reinterpret_cast<const float4_t*>(red)[w * 64 + lane];
+    s[0] += t[0], s[1] += t[1], s[2] += t[2], s[3] += t[3];
+  }
+  // lane (c, g) holds rows 4g + i of the tile for batch row c
+  if constexpr (kEpi == kEpiSiluMul) {
+    // gate rows sit in g < 2, the matching up rows 32 lanes higher
+    float up[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      up[i] = __uint_as_float(__builtin_amdgcn_permlane32_swap(__float_as_uint(s[i]), __float_as_uint(s[i]),
+                                                               false, false)[1]);
+    if (g >= 2 || !col_ok) return;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int j = tile * 8 + 4 * g + i;
+      if (j >= (p.N >> 1)) continue;
+      const float gt = bf16r(s[i]), u = bf16r(up[i]);
+      const float act = bf16r(gt / (1.0f + expf(-gt)));
+      store_y(p, c, j, bf16r(act * u));
+    }
+  } else {
+    if (!col_ok) return;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int n = tile * 16 + 4 * g + i;
+      if (n >= p.N) continue;
+      float y = bf16r(s[i]);
+      if constexpr (kEpi == kEpiResidual) y = bf16r(bf16_to_f32(p.res[c * p.res_ld + n]) + y);
+      store_y(p, c, n, y);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// q / k: per-head RMSNorm (bf16 out), then rotate-half RoPE at one position
+// (bf16 out); v copied.  One wave per head of one batch row; lane l holds
+// channels l and l + 64 (the two halves RoPE pairs).  Heads [0, hq) are q
+// (to q_out), [hq, hq + hkv) k and [hq + hkv, hq + 2 hkv) v (to the cache).
+// ---------------------------------------------------------------------------
+struct QkParams {
+  const uint16_t* qkv;  // [bs, (hq + 2 hkv) * 128] bf16, row stride qkv_ld
+  int64_t qkv_ld;
+  const uint16_t* q_norm;  // [128] bf16
+  const uint16_t* k_norm;  // [128] bf16
+  float eps;
+  const float* cos;  // [64] fp32 (the position's row)
+  const float* sin;
+  uint16_t* q_out;  // [bs, hq, 128]
+  uint16_t* k_dst;  // row of (b, h): k_dst + b * k_sb + h * k_sh
+  int64_t k_sb, k_sh;
+  uint16_t* v_dst;
+  int64_t v_sb, v_sh;
+  int bs, hq, hkv;
+};
+
+__global__ __launch_bounds__(256) void qk_norm_rope_kernel(const QkParams p) {
+  const int heads = p.hq + 2 * p.hkv;
+  const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (item >= p.bs * heads) return;
+  const int b = item / heads, h = item - b * heads, lane = threadIdx.x & 63;
+  const uint16_t* src = p.qkv + b * p.qkv_ld + h * 128;
+  const float x1 = bf16_to_f32(src[lane]), x2 = bf16_to_f32(src[lane + 64]);
+  if (h >= p.hq + p.hkv) {  // v: straight copy
+    uint16_t* dst = p.v_dst + b * p.v_sb + (h - p.hq - p.hkv) * p.v_sh;
+    dst[lane] = src[lane];
+    dst[lane + 64] = src[lane + 64];
+    return;
+  }
+  const bool is_q = h < p.hq;
+  const uint16_t* nw = is_q ? p.q_norm : p.k_norm;
+  const float ss = wave_sum(x1 * x1 + x2 * x2);
+  const float r = rsqrtf(ss * (1.0f / 128.0f) + p.eps);
+  const float n1 = bf16r((x1 * r) * bf16_to_f32(nw[lane]));
+  const float n2 = bf16r((x2 * r) * bf16_to_f32(nw[lane + 64]));
+  const float cs = p.cos[lane], sn = p.sin[lane];
+  const uint16_t y1 = f32_to_bf16_bits(n1 * cs - n2 * sn);
+  const uint16_t y2 = f32_to_bf16_bits(n2 * cs + n1 * sn);
+  uint16_t* dst = is_q ? p.q_out + (static_cast<int64_t>(b) * p.hq + h) * 128
+                       : p.k_dst + b * p.k_sb + (h - p.hq) * p.k_sh;
+  dst[lane] = y1;
+  dst[lane + 64] = y2;
+}
+
+}  // namespace
+}  // namespace zkv
+
+using namespace zkv;
+
+extern "C" int zkv_decode_linear(const uint16_t* x, int64_t x_ld, int M, int K, const uint16_t* w, int N,
+                                 const uint16_t* norm_w, float eps, const uint16_t* residual, int64_t res_ld,
+                                 void* out, int64_t out_ld, int out_f32, int epilogue, zkv_stream_t stream) {
+  ZKV_REQUIRE(x && w && out, "zkv_decode_linear: null pointer");
+  ZKV_REQUIRE(M >= 1 && M <= kLinMaxM, "zkv_decode_linear: M=%d outside [1, %d]", M, kLinMaxM);
+  ZKV_REQUIRE(K > 0 && K % kLinKBlock == 0, "zkv_decode_linear: K=%d is not a positive multiple of %d", K,
+              kLinKBlock);
+  ZKV_REQUIRE(N > 0, "zkv_decode_linear: N=%d", N);
+  ZKV_REQUIRE(epilogue >= kEpiNone && epilogue <= kEpiSiluMul, "zkv_decode_linear: epilogue %d", epilogue);
+  ZKV_REQUIRE(epilogue != kEpiResidual || residual, "zkv_decode_linear: residual epilogue without residual");
+  ZKV_REQUIRE(epilogue != kEpiSiluMul || N % 2 == 0, "zkv_decode_linear: silu * up needs an even N (%d)", N);
+  ZKV_REQUIRE(x_ld >= K && x_ld % 8 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
+                  (reinterpret_cast<uintptr_t>(w) & 15) == 0 &&
+                  (norm_w == nullptr || (reinterpret_cast<uintptr_t>(norm_w) & 15) == 0),
+              "zkv_decode_linear: x, w and the norm weight need 16-byte aligned rows");
+  const size_t x_bytes = static_cast<size_t>(M) * K * 2;
+  const int n_tiles = epilogue == kEpiSiluMul ? (N / 2 + 7) / 8 : (N + 15) / 16;
+  // waves per workgroup: enough resident waves to keep the weight stream busy
+  const int nkb = K / kLinKBlock;
+  int nw = 1;
+  while (nw < 16 && nw * 2 <= nkb && static_cast<int64_t>(n_tiles) * nw < 4096) nw *= 2;
+  const size_t lds = x_bytes + static_cast<size_t>(nw) * 64 * 16;
+  ZKV_REQUIRE(lds <= 96 * 1024, "zkv_decode_linear: M x K = %d x %d needs %zu bytes of LDS (limit 96 KiB)", M, K,
+              lds);
+  LinearParams p{x, x_ld, w, norm_w, eps, residual, res_ld, out, out_ld, M, K, N, out_f32};
+  auto s = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid(n_tiles), block(64 * nw);
+  // dynamic LDS above 64 KiB has to be allowed per kernel (once)
+#define ZKV_LIN(E, NORM)                                                                              \
+  do {                                                                                                \
+    static bool big_lds_set = false;                                                                  \
+    if (lds > 64 * 1024 && !big_lds_set) {                                                            \
+      if (hipFuncSetAttribute(reinterpret_cast<const void*>(&decode_linear_kernel<E, NORM>),          \
+                              hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024) != hipSuccess)  \
+        return fail(ZKV_EINVAL, "zkv_decode_linear: cannot raise the LDS limit to 96 KiB");           \
+      big_lds_set = true;                                                                             \
+    }                                                                                                 \
+    decode_linear_kernel<E, NORM><<<grid, block, lds, s>>>(p);                                        \
+  } while (0)
+  if (norm_w) {
+    if (epilogue == kEpiNone) ZKV_LIN(kEpiNone, true);
+    else if (epilogue == kEpiResidual) ZKV_LIN(kEpiResidual, true);
+    else ZKV_LIN(kEpiSiluMul, true);
+  } else {
+    if (epilogue == kEpiNone) ZKV_LIN(kEpiNone, false);
+    else if (epilogue == kEpiResidual) ZKV_LIN(kEpiResidual, false);
+    else ZKV_LIN(kEpiSiluMul, false);
+  }
+#undef ZKV_LIN
+  return check_launch("decode_linear_kernel");
+}
+
+extern "C" int zkv_qk_norm_rope(const uint16_t* qkv, int64_t qkv_ld, int bs, int hq, int hkv,
+                                const uint16_t* q_norm, const uint16_t* k_norm, float eps, const float* cos_row,
+                                const float* sin_row, uint16_t* q_out, uint16_t* k_dst, int64_t k_sb,
+                                int64_t k_sh, uint16_t* v_dst, int64_t v_sb, int64_t v_sh, zkv_stream_t stream) {
+  ZKV_REQUIRE(qkv && q_norm && k_norm && cos_row && sin_row && q_out && k_dst && v_dst,
+              "zkv_qk_norm_rope: null pointer");
+  ZKV_REQUIRE(bs > 0 && hq > 0 && hkv > 0 && qkv_ld >= static_cast<int64_t>(hq + 2 * hkv) * 128,
+              "zkv_qk_norm_rope: bad sizes bs=%d hq=%d hkv=%d qkv_ld=%lld", bs, hq, hkv,
+              static_cast<long long>(qkv_ld));
+  const QkParams p{qkv, qkv_ld, q_norm, k_norm, eps, cos_row, sin_row, q_out, k_dst, k_sb, k_sh,
+                   v_dst, v_sb, v_sh, bs, hq, hkv};
+  const int items = bs * (hq + 2 * hkv);
+  qk_norm_rope_kernel<<<(items + 3) / 4, 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(p);
+  return check_launch("qk_norm_rope_kernel");
+}

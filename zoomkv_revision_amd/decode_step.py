@@ -14,10 +14,15 @@ then the final norm, the tied LM head and ``sample_next_token``
 (LLM.py:63-139: temperature, top-k, top-p, multinomial).
 
 The weights are random-init bf16 stand-ins (no checkpoint is available
-offline).  The linear layers are plain library GEMMs (torch.nn.functional
-.linear on hipBLASLt); rmsnorm, RoPE and silu are torch ops (the reference
-calls flashinfer for them, which has no ROCm build).  The attention path --
-the part this package accelerates -- is the cache's own kernels.
+offline).  On the GPU a layer is five launches besides the cache's attention
+path (all in csrc/decode_model.hip): the QKV projection with the input
+RMSNorm fused in, q / k norm + RoPE with the K / V rows written straight into
+the cache, the o-projection with the residual add, the gate / up projection
+with the post-attention RMSNorm and silu * up fused in, and the down
+projection with the residual add.  The torch ops of ``layer_decode_torch``
+(the reference's flashinfer rmsnorm / rope / silu have no ROCm build) are
+the same layer written out op by op: the CPU path, and the check the fused
+kernels are tested against.
 """
 from __future__ import annotations
 
@@ -65,6 +70,46 @@ class Qwen3Geometry:
     eps: float = 1.0e-6
 
 
+def decode_linear(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor, norm_w: torch.Tensor | None = None,
+                  eps: float = 0.0, residual: torch.Tensor | None = None, silu_mul: bool = False) -> torch.Tensor:
+    """out = [silu * up of] [rmsnorm(x) of] x @ w.T [+ residual] on the GPU
+    (zkv_decode_linear): x [M, K] bf16 (M <= 16), w [N, K] bf16, out [M, N]
+    bf16 or fp32 (or [M, N / 2] with silu_mul: w's first half rows are gate)."""
+    from ._lib import check, lib, stream_of
+    M, K = x.shape
+    N = w.shape[0]
+    assert x.dtype == w.dtype == torch.bfloat16 and x.stride(1) == 1 and w.is_contiguous()
+    assert out.dim() == 2 and out.shape[0] == M and out.shape[1] == (N // 2 if silu_mul else N)
+    assert out.stride(1) == 1 and out.dtype in (torch.bfloat16, torch.float32)
+    epi = 2 if silu_mul else (1 if residual is not None else 0)
+    if residual is not None:
+        assert residual.shape == out.shape and residual.dtype == torch.bfloat16 and residual.stride(1) == 1
+    check(lib().zkv_decode_linear(x.data_ptr(), x.stride(0), M, K, w.data_ptr(), N,
+                                  None if norm_w is None else norm_w.data_ptr(), float(eps),
+                                  None if residual is None else residual.data_ptr(),
+                                  0 if residual is None else residual.stride(0), out.data_ptr(), out.stride(0),
+                                  int(out.dtype == torch.float32), epi, stream_of(out)))
+    return out
+
+
+def qk_norm_rope(qkv: torch.Tensor, heads: int, kv_heads: int, q_norm: torch.Tensor, k_norm: torch.Tensor,
+                 eps: float, cos_row: torch.Tensor, sin_row: torch.Tensor, q_out: torch.Tensor,
+                 k_dst: torch.Tensor, v_dst: torch.Tensor) -> None:
+    """q / k per-head RMSNorm + RoPE and the K / V append (zkv_qk_norm_rope):
+    qkv [bs, (heads + 2 kv_heads) * 128] bf16 -> q_out [bs, heads, 128] (any
+    view with contiguous heads), k_dst / v_dst [bs, kv_heads, 128] views (the
+    cache rows)."""
+    from ._lib import check, lib, stream_of
+    bs = qkv.shape[0]
+    assert qkv.stride(1) == 1 and q_out.is_contiguous() and q_out.numel() == bs * heads * 128
+    assert k_dst.shape == v_dst.shape == (bs, kv_heads, 128) and k_dst.stride(2) == v_dst.stride(2) == 1
+    assert cos_row.dtype == sin_row.dtype == torch.float32 and cos_row.is_contiguous() and sin_row.is_contiguous()
+    check(lib().zkv_qk_norm_rope(qkv.data_ptr(), qkv.stride(0), bs, heads, kv_heads, q_norm.data_ptr(),
+                                 k_norm.data_ptr(), float(eps), cos_row.data_ptr(), sin_row.data_ptr(),
+                                 q_out.data_ptr(), k_dst.data_ptr(), k_dst.stride(0), k_dst.stride(1),
+                                 v_dst.data_ptr(), v_dst.stride(0), v_dst.stride(1), stream_of(qkv)))
+
+
 def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
     """RMSNorm over the last dim in fp32, weight applied in fp32, result in x's dtype."""
     xf = x.float()
@@ -75,9 +120,11 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
 class RandomQwen3:
     """Random-init bf16 weights of a Qwen3 decoder (std 0.02, norms at 1), on one GPU."""
 
-    def __init__(self, geo: Qwen3Geometry, device, seed: int = 42, max_position: int = 1 << 17):
+    def __init__(self, geo: Qwen3Geometry, device, seed: int = 42, max_position: int = 1 << 17,
+                 fused: bool = True):
         self.geo = geo
         self.device = torch.device(device)
+        self.fused = fused  # on the GPU: the fused kernels (False: the torch ops, for checks)
         g = torch.Generator(device=self.device)
         g.manual_seed(seed)
         bf = dict(dtype=torch.bfloat16, device=self.device)
@@ -124,6 +171,34 @@ class RandomQwen3:
 
     def layer_decode(self, ldx: int, hidden: torch.Tensor, cache) -> torch.Tensor:
         """One layer of one decode token (LLM.py:208-251); hidden [bs, 1, hidden]."""
+        if hidden.is_cuda and self.fused:
+            return self.layer_decode_fused(ldx, hidden, cache)
+        return self.layer_decode_torch(ldx, hidden, cache)
+
+    def layer_decode_fused(self, ldx: int, hidden: torch.Tensor, cache) -> torch.Tensor:
+        """layer_decode in five kernels around cache.compute (see the module docstring)."""
+        geo, L = self.geo, self.layers[ldx]
+        bs = hidden.shape[0]
+        qd, kd = geo.heads * geo.head_dim, geo.kv_heads * geo.head_dim
+        x = hidden.reshape(bs, geo.hidden)
+        qkv = torch.empty(bs, qd + 2 * kd, dtype=torch.bfloat16, device=hidden.device)
+        decode_linear(x, L["wqkv"], qkv, norm_w=L["input_ln"], eps=geo.eps)
+        pos = cache.context
+        row = cache.decode_reserve_row(ldx)
+        q = torch.empty(bs, 1, geo.heads, geo.head_dim, dtype=torch.bfloat16, device=hidden.device)
+        qk_norm_rope(qkv, geo.heads, geo.kv_heads, L["q_norm"], L["k_norm"], geo.eps, self.cos[pos],
+                     self.sin[pos], q, cache.unified_keys[ldx][:, :, row], cache.unified_values[ldx][:, :, row])
+        attn = cache.compute(q, ldx)                                   # [bs, 1, heads, 128]
+        h1 = torch.empty(bs, geo.hidden, dtype=torch.bfloat16, device=hidden.device)
+        decode_linear(attn.reshape(bs, qd), L["wo"], h1, residual=x)
+        act = torch.empty(bs, geo.ffn, dtype=torch.bfloat16, device=hidden.device)
+        decode_linear(h1, L["gate_up"], act, norm_w=L["post_ln"], eps=geo.eps, silu_mul=True)
+        h2 = torch.empty(bs, geo.hidden, dtype=torch.bfloat16, device=hidden.device)
+        decode_linear(act, L["down"], h2, residual=h1)
+        return h2.view(bs, 1, geo.hidden)
+
+    def layer_decode_torch(self, ldx: int, hidden: torch.Tensor, cache) -> torch.Tensor:
+        """layer_decode op by op in torch (the CPU path, and the fused path's check)."""
         geo, L = self.geo, self.layers[ldx]
         bs = hidden.shape[0]
         residual = hidden
@@ -150,6 +225,11 @@ class RandomQwen3:
         hidden = self.embed[tokens].unsqueeze(1)
         for ldx in range(self.geo.layers):
             hidden = self.layer_decode(ldx, hidden, cache)
+        if hidden.is_cuda and self.fused:
+            bs = hidden.shape[0]
+            logits = torch.empty(bs, self.geo.vocab, dtype=torch.float32, device=hidden.device)
+            return decode_linear(hidden.reshape(bs, self.geo.hidden), self.embed, logits, norm_w=self.final_norm,
+                                 eps=self.geo.eps)
         hidden = rms_norm(hidden, self.final_norm, self.geo.eps)
         return F.linear(hidden[:, 0], self.embed).float()
 
