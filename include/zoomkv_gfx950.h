@@ -334,7 +334,7 @@ int zkv_h2d_gather_kv_packed(const void* src_k, const void* src_v, int bs, int k
 /* y = x . w^T for the M <= 16 rows of a decode batch: x [M, K] bf16 (row
  * stride x_ld, 16-byte aligned), w [N, K] bf16 contiguous, fp32 accumulate,
  * y [M, N] bf16 (or fp32 holding the bf16 value when out_f32), row stride
- * out_ld.  K must be a multiple of 128 and M * K * 2 bytes must fit 96 KiB.
+ * out_ld.  K must be a multiple of 128 and M * K * 2 bytes must fit the LDS (about 120 KiB).
  * norm_w (nullable): x is first replaced by bf16(x * rsqrt(mean(x^2) + eps) *
  * norm_w) per row.  epilogue 0: none; 1: y = bf16(residual + bf16(x . w^T))
  * (residual [M, N] bf16, row stride res_ld); 2: w rows [0, N/2) are gate and

@@ -59,20 +59,13 @@ __device__ __forceinline__ void store_y(const LinearParams& p, int m, int n, flo
     reinterpret_cast<uint16_t*>(p.out)[m * p.out_ld + n] = f32_to_bf16_bits(y);
 }
 
-// One workgroup per tile of 16 output rows (silu * up: 8 gate rows and the 8
-// matching up rows), NW waves splitting the K blocks.  Dynamic LDS: the M x K
-// bf16 input rows, then NW x 64 x 4 fp32 partial tiles.
-template <int kEpi, bool kNorm>
-__global__ __launch_bounds__(1024) void decode_linear_kernel(const LinearParams p) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-  uint16_t* xs = reinterpret_cast<uint16_t*>(lds);
+// Stages the M x K input rows into LDS (xs), RMS-normalised when kNorm:
+// bf16(x * rsqrt(mean(x^2) + eps) * w).  red: M floats of scratch.
+template <bool kNorm>
+__device__ __forceinline__ void stage_x(const LinearParams& p, uint16_t* xs, float* red) {
   const int nw = blockDim.x >> 6;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int c = lane & 15, g = lane >> 4;
   const int M = p.M, K = p.K;
-  float* red = reinterpret_cast<float*>(lds + static_cast<size_t>(M) * K * 2);
-
-  // ---- stage x (optionally RMS-normalised: bf16(x * rsqrt(mean(x^2) + eps) * w)) ----
   const int kv8 = K >> 3;  // 16-byte chunks per row
   if constexpr (kNorm) {
     // wave m' reduces rows m = m', m' + nw, ... (fixed order: deterministic)
@@ -103,13 +96,29 @@ __global__ __launch_bounds__(1024) void decode_linear_kernel(const LinearParams 
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const float lo = bf16r((__uint_as_float(v[e] << 16) * r) * __uint_as_float(wv[e] << 16));
-        const float hi = bf16r((__uint_as_float(v[e] & 0xFFFF0000u) * r) * __uint_as_float(wv[e] & 0xFFFF0000u));
+        const float hi =
+            bf16r((__uint_as_float(v[e] & 0xFFFF0000u) * r) * __uint_as_float(wv[e] & 0xFFFF0000u));
         v[e] = (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xFFFF0000u);
       }
     }
     reinterpret_cast<u32x4_t*>(xs)[i] = v;
   }
   __syncthreads();
+}
+
+// One workgroup per tile of 16 output rows (silu * up: 8 gate rows and the 8
+// matching up rows), NW waves splitting the K blocks.  Dynamic LDS: the M x K
+// bf16 input rows, then NW x 64 x 4 fp32 partial tiles.
+template <int kEpi, bool kNorm>
+__global__ __launch_bounds__(1024) void decode_linear_kernel(const LinearParams p) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  uint16_t* xs = reinterpret_cast<uint16_t*>(lds);
+  const int nw = blockDim.x >> 6;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int c = lane & 15, g = lane >> 4;
+  const int M = p.M, K = p.K;
+  float* red = reinterpret_cast<float*>(lds + static_cast<size_t>(M) * K * 2);
+  stage_x<kNorm>(p, xs, red);
 
   // ---- weight rows of this tile ----
   const int tile = blockIdx.x;
@@ -255,9 +264,11 @@ extern "C" int zkv_decode_linear(const uint16_t* x, int64_t x_ld, int M, int K, 
   const int nkb = K / kLinKBlock;
   int nw = 1;
   while (nw < 16 && nw * 2 <= nkb && static_cast<int64_t>(n_tiles) * nw < 4096) nw *= 2;
+  // and few enough k-blocks per wave that its loads overlap (the waves of a large N)
+  while (nw < 16 && (nkb + nw - 1) / nw > 6) nw *= 2;
   const size_t lds = x_bytes + static_cast<size_t>(nw) * 64 * 16;
-  ZKV_REQUIRE(lds <= 96 * 1024, "zkv_decode_linear: M x K = %d x %d needs %zu bytes of LDS (limit 96 KiB)", M, K,
-              lds);
+  ZKV_REQUIRE(lds <= 160 * 1024, "zkv_decode_linear: M x K = %d x %d needs %zu bytes of LDS (limit 160 KiB)", M,
+              K, lds);
   LinearParams p{x, x_ld, w, norm_w, eps, residual, res_ld, out, out_ld, M, K, N, out_f32};
   auto s = reinterpret_cast<hipStream_t>(stream);
   const dim3 grid(n_tiles), block(64 * nw);
@@ -267,8 +278,8 @@ extern "C" int zkv_decode_linear(const uint16_t* x, int64_t x_ld, int M, int K, 
     static bool big_lds_set = false;                                                                  \
     if (lds > 64 * 1024 && !big_lds_set) {                                                            \
       if (hipFuncSetAttribute(reinterpret_cast<const void*>(&decode_linear_kernel<E, NORM>),          \
-                              hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024) != hipSuccess)  \
-        return fail(ZKV_EINVAL, "zkv_decode_linear: cannot raise the LDS limit to 96 KiB");           \
+                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess) \
+        return fail(ZKV_EINVAL, "zkv_decode_linear: cannot raise the LDS limit to 160 KiB");          \
       big_lds_set = true;                                                                             \
     }                                                                                                 \
     decode_linear_kernel<E, NORM><<<grid, block, lds, s>>>(p);                                        \
