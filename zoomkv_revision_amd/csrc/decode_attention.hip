@@ -300,6 +300,11 @@ __device__ __forceinline__ int bf16_row(const AttnParams& p, const int64_t* idx_
 // One bf16 tile: tokens [base, base + valid) of the list.  Lane (c, g) loads
 // K rows of tokens c and c + 16 (the K-MFMA A rows) and V rows of tokens
 // TAU[g][e] (its V-MFMA k-slice), 16 B per row.
+// kBf16Only (no quantized tile in the kernel): M-tile j of the V-MFMA is
+// channel 8c + j for A row c instead of the quantized tiles' order, so each
+// V row is one 16-byte load per lane; O[j][i] of lane (c, g) is then channel
+// 32g + 8i + j.
+template <bool kBf16Only>
 __device__ __forceinline__ void residual_tile(const AttnParams& p, int b, int h, int base, int valid,
                                               int c, int g, const half8_t qB[4], float qs,
                                               float& m_run, float4_t& L, float4_t O[8],
@@ -339,17 +344,21 @@ __device__ __forceinline__ void residual_tile(const AttnParams& p, int b, int h,
     for (int i = 0; i < 4; ++i)
       if (vrow[i + 4 * m] < 0) S[m][i] = -INFINITY;
   const half8_t pb = softmax_step(S, 1.0f, 0.0f, qs, qs, m_run, L, O, OZ);
-  // V^T operand: element e = token TAU[g][e], row c of M-tile j = channel
-  // 32(j/2) + 2c + j%2 (the quantized tiles' row order): dword 16(j/2) + c of
-  // the row, half j%2
+  // V^T operand: element e = token TAU[g][e]; row c of M-tile j = channel
+  // 32(j/2) + 2c + j%2 (the quantized tiles' row order: dword 16(j/2) + c of
+  // the row, half j%2), or 8c + j when kBf16Only (dword c*4 + j/2, half j%2)
   u32x4_t vx[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     vx[e] = u32x4_t{0u, 0u, 0u, 0u};
     if (vrow[e] >= 0) {
-      const uint32_t* row = reinterpret_cast<const uint32_t*>(vr + vrow[e] * p.vr_st) + c;
+      if constexpr (kBf16Only) {
+        vx[e] = ld16(vr + vrow[e] * p.vr_st + 8 * c);
+      } else {
+        const uint32_t* row = reinterpret_cast<const uint32_t*>(vr + vrow[e] * p.vr_st) + c;
 #pragma unroll
-      for (int G = 0; G < 4; ++G) vx[e][G] = row[16 * G];
+        for (int G = 0; G < 4; ++G) vx[e][G] = row[16 * G];
+      }
     }
   }
 #pragma unroll
@@ -379,7 +388,7 @@ struct KernelShape {
   static constexpr int kWavesPerSimd = std::max(1, std::min(4, (kWgPerCu * NW) / 4));
 };
 
-template <int NW, int D, bool kSparse>
+template <int NW, int D, bool kSparse, bool kBf16Only = false>
 __global__ __launch_bounds__(64 * NW)
 __attribute__((amdgpu_waves_per_eu(KernelShape<NW, D>::kWavesPerSimd)))
 void kivi4_attn_kernel(const AttnParams p) {
@@ -492,7 +501,7 @@ void kivi4_attn_kernel(const AttnParams p) {
   // ---- bf16 residual tiles (at most r_cap / 32 of them, in the last split) ----
   for (int t = max(T0, n_qt) + wave; t < T1; t += NW) {
     const int base = (t - n_qt) * kTile;
-    residual_tile(p, b, h, base, min(kTile, p.res_len - base), c, g, qB, p.qscale, m_run, L, O, OZ);
+    residual_tile<kBf16Only>(p, b, h, base, min(kTile, p.res_len - base), c, g, qB, p.qscale, m_run, L, O, OZ);
   }
 
   // ---- merge the NW waves through LDS (the rings are free now) ----
@@ -502,12 +511,24 @@ void kivi4_attn_kernel(const AttnParams p) {
   float* red_m = red_o + NW * p.gqa * 128;                    // [NW][gqa]
   float* red_l = red_m + NW * p.gqa;                          // [NW][gqa]
   if (col_ok) {
-    float* o = red_o + (wave * p.gqa + c) * 128 + 8 * g;
+    if constexpr (kBf16Only) {
+      // O[j][i] is channel 32g + 8i + j
+      float* o = red_o + (wave * p.gqa + c) * 128 + 32 * g;
 #pragma unroll
-    for (int G = 0; G < 4; ++G) {
-      // O[2G + jp][i] is channel 32G + 8g + 2i + jp
-      *reinterpret_cast<float4_t*>(o + 32 * G) = float4_t{O[2 * G][0], O[2 * G + 1][0], O[2 * G][1], O[2 * G + 1][1]};
-      *reinterpret_cast<float4_t*>(o + 32 * G + 4) = float4_t{O[2 * G][2], O[2 * G + 1][2], O[2 * G][3], O[2 * G + 1][3]};
+      for (int i = 0; i < 4; ++i) {
+        *reinterpret_cast<float4_t*>(o + 8 * i) = float4_t{O[0][i], O[1][i], O[2][i], O[3][i]};
+        *reinterpret_cast<float4_t*>(o + 8 * i + 4) = float4_t{O[4][i], O[5][i], O[6][i], O[7][i]};
+      }
+    } else {
+      float* o = red_o + (wave * p.gqa + c) * 128 + 8 * g;
+#pragma unroll
+      for (int G = 0; G < 4; ++G) {
+        // O[2G + jp][i] is channel 32G + 8g + 2i + jp
+        *reinterpret_cast<float4_t*>(o + 32 * G) =
+            float4_t{O[2 * G][0], O[2 * G + 1][0], O[2 * G][1], O[2 * G + 1][1]};
+        *reinterpret_cast<float4_t*>(o + 32 * G + 4) =
+            float4_t{O[2 * G][2], O[2 * G + 1][2], O[2 * G][3], O[2 * G + 1][3]};
+      }
     }
     if (g == 0) {
       red_m[wave * p.gqa + c] = m_run * p.qscale;  // base-2 scaled units from here on
@@ -706,6 +727,8 @@ void launch_attn(const AttnParams& p, int bs, hipStream_t s) {
   const Shape sh = attn_shape();
   if (p.tile_group != nullptr) {
     kivi4_attn_kernel<8, 2, true><<<grid, 512, 0, s>>>(p);
+  } else if (p.n_groups == 0) {  // bf16 rows only: the 16-byte V layout
+    kivi4_attn_kernel<8, 2, false, true><<<grid, 512, 0, s>>>(p);
   } else if (sh.nw == 8) {
     kivi4_attn_kernel<8, 2, false><<<grid, 512, 0, s>>>(p);
   } else if (sh.nw == 2) {
