@@ -321,13 +321,37 @@ __device__ __forceinline__ void residual_tile(const AttnParams& p, int b, int h,
     const int tok = (e < 4) ? (4 * g + e) : (16 + 4 * g + e - 4);
     vrow[e] = tok < valid ? bf16_row(p, idx_bh, base + tok) : -1;
   }
+  // bf16-only kernels (few live registers) request the V rows together with
+  // the K rows: one memory round trip after the row indices
+  u32x4_t vx[8];
+  auto load_v = [&]() {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      vx[e] = u32x4_t{0u, 0u, 0u, 0u};
+      if (vrow[e] >= 0) {
+        if constexpr (kBf16Only) {
+          vx[e] = ld16(vr + vrow[e] * p.vr_st + 8 * c);
+        } else {
+          const uint32_t* row = reinterpret_cast<const uint32_t*>(vr + vrow[e] * p.vr_st) + c;
+#pragma unroll
+          for (int G = 0; G < 4; ++G) vx[e][G] = row[16 * G];
+        }
+      }
+    }
+  };
+  u32x4_t kx[4][2];
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+      kx[s][m] = krow[m] >= 0 ? ld16(kr + krow[m] * p.kr_st + 8 * (4 * s + g)) : u32x4_t{0u, 0u, 0u, 0u};
+  if constexpr (kBf16Only) load_v();
   float4_t S[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
-      u32x4_t raw = {0u, 0u, 0u, 0u};
-      if (krow[m] >= 0) raw = ld16(kr + krow[m] * p.kr_st + 8 * (4 * s + g));
+      const u32x4_t raw = kx[s][m];
       half8_t a;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
@@ -347,20 +371,7 @@ __device__ __forceinline__ void residual_tile(const AttnParams& p, int b, int h,
   // V^T operand: element e = token TAU[g][e]; row c of M-tile j = channel
   // 32(j/2) + 2c + j%2 (the quantized tiles' row order: dword 16(j/2) + c of
   // the row, half j%2), or 8c + j when kBf16Only (dword c*4 + j/2, half j%2)
-  u32x4_t vx[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    vx[e] = u32x4_t{0u, 0u, 0u, 0u};
-    if (vrow[e] >= 0) {
-      if constexpr (kBf16Only) {
-        vx[e] = ld16(vr + vrow[e] * p.vr_st + 8 * c);
-      } else {
-        const uint32_t* row = reinterpret_cast<const uint32_t*>(vr + vrow[e] * p.vr_st) + c;
-#pragma unroll
-        for (int G = 0; G < 4; ++G) vx[e][G] = row[16 * G];
-      }
-    }
-  }
+  if constexpr (!kBf16Only) load_v();
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     half8_t a;
@@ -390,7 +401,7 @@ struct KernelShape {
 
 template <int NW, int D, bool kSparse, bool kBf16Only = false>
 __global__ __launch_bounds__(64 * NW)
-__attribute__((amdgpu_waves_per_eu(KernelShape<NW, D>::kWavesPerSimd)))
+__attribute__((amdgpu_waves_per_eu(kBf16Only ? 2 : KernelShape<NW, D>::kWavesPerSimd)))
 void kivi4_attn_kernel(const AttnParams p) {
   __shared__ __attribute__((aligned(16))) uint8_t smem[NW][D][kStageBytes];
   const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
@@ -706,9 +717,15 @@ SplitPlan plan_splits(int bs, int kv, int n_groups, int res_len, int n_splits) {
     const int target = 256 * wg_per_cu;  // one resident workgroup per split on 256 CUs
     const int units = bs * kv;
     ns = (target + units - 1) / units;
-    // at least one tile per wave of every split (short contexts at small
-    // batch are latency-bound: more splits beat fuller waves)
-    ns = std::min(ns, std::max(1, n_tiles / sh.nw));
+    if (n_groups > 0) {
+      // at least one tile per wave of every split (short contexts at small
+      // batch are latency-bound: more splits beat fuller waves)
+      ns = std::min(ns, std::max(1, n_tiles / sh.nw));
+    } else {
+      // bf16 rows only: a tile is two dependent memory round trips, so one
+      // workgroup per CU wins even with idle waves in each split
+      ns = std::min((256 + units - 1) / units, n_tiles);
+    }
   }
   ns = std::max(1, std::min(ns, n_tiles));
   const int per = (n_tiles + ns - 1) / ns;
