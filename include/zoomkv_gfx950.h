@@ -174,6 +174,15 @@ int zkv_chunk_density_scores(const int64_t* chunk_ids, int64_t id_sb, int64_t id
 int zkv_dense_mask_from_topk(const int64_t* positions, uint8_t* mask, int rows, int n_dense, int nk,
                              zkv_stream_t stream);
 
+/* The top k of each row (zkv_topk's selection, no lut / skipped tail) with
+ * the dense mask written in the same launch: mask[r, :L] = 0, then 1 at every
+ * selected index (mask uint8 [rows, >= L], row stride mask_stride).  It is
+ * float_topk_3d followed by dense_mask_from_topk in one pass: no counterpart
+ * of its own in the reference; it fuses the two calls of S:2360-2369
+ * (float_topk.cu:51-346 + rerank_topk.cu:926-998). */
+int zkv_topk_dense_mask(const float* scores, int64_t in_stride, int rows, int L, int k, int64_t* out,
+                        int64_t out_stride, uint8_t* mask, int64_t mask_stride, zkv_stream_t stream);
+
 /* GQA-mean query raw_q[b, h] = bf16(sum_i q[b, h*g + i] / g), g = hq / kv
  * (the torch mean of S:1621-1626).  q bf16 [bs, hq, 128] with strides
  * (q_sb, q_sh); out bf16 [bs, kv, 128] contiguous. */

@@ -209,3 +209,20 @@ def test_topk_sentinel_heavy_rows(rng):
     x[1, 3, 200:] = -1e30                       # only 104 real values, k = 300
     got = from_torch(float_topk_3d(torch.from_numpy(x).cuda(), 300))
     assert np.array_equal(got, osel.topk_indices(x, 300))
+
+
+@pytest.mark.parametrize("L,k", [(1638, 491), (4096, 1638), (300, 300), (9000, 64), (40000, 100)])
+def test_topk_dense_mask_fused_matches_two_ops(rng, L, k):
+    """zkv_topk_dense_mask == float_topk_3d then dense_mask_from_topk_cuda."""
+    from zoomkv_revision_amd.rerank import dense_mask_from_topk_cuda, topk_dense_mask
+    from zoomkv_revision_amd.topk import float_topk_3d
+    x = rng.standard_normal((2, 3, L)).astype(np.float32)
+    x[1, 1, ::5] = 0.25                                   # ties
+    xt = torch.from_numpy(x).cuda()
+    ref_idx = float_topk_3d(xt, k)
+    ref_mask = torch.ones(2, 3, L, dtype=torch.bool, device="cuda")
+    dense_mask_from_topk_cuda(ref_idx, ref_mask)
+    mask = torch.ones(2, 3, L, dtype=torch.bool, device="cuda")   # stale contents must be cleared
+    idx = topk_dense_mask(xt, k, mask)
+    assert torch.equal(idx, ref_idx) and torch.equal(mask, ref_mask)
+    assert np.array_equal(from_torch(idx), osel.topk_indices(x, k))

@@ -42,6 +42,7 @@ SIGNATURES = {
     "zkv_chunk_density_scores": (I32, [P, I64, I64, P, I64, I64, I64, P, I64, I64, P, I64, I64,
                                        I32, I32, I32, I32, P]),
     "zkv_dense_mask_from_topk": (I32, [P, P, I32, I32, I32, P]),
+    "zkv_topk_dense_mask": (I32, [P, I64, I32, I32, I32, P, I64, P, I64, P]),
     "zkv_gqa_mean_query": (I32, [P, I64, I64, I32, I32, I32, P, P]),
     "zkv_kivi_qk_dense_sparse": (I32, [P, I64, I64, P, I64, I64, P, I64, I64, I32, P, P, I64, I64,
                                        I32, P, I64, I64, I32, I32, I32, P, P, I64, I64,

@@ -43,7 +43,7 @@ import torch
 from . import kivi
 from .attention import gather_attention
 from .quest import load_kernel_module as _load_quest
-from .rerank import dense_mask_from_topk_cuda, gqa_mean_query, partial_chunk_density_scores_cuda
+from .rerank import gqa_mean_query, partial_chunk_density_scores_cuda, topk_dense_mask
 from .topk import float_topk_3d, float_topk_gather_concat_3d
 
 _FALSY = ("0", "false", "False", "")
@@ -481,11 +481,14 @@ class polar_cache:
         self._quest_kernel.quest_chunk_score(raw_q, self._chunk_key_min_gpu[layer_idx],
                                              self._chunk_key_max_gpu[layer_idx], scores, n_chunks,
                                              self._chunk_valid_mask_gpu[layer_idx])
-        chunk_idx = float_topk_3d(scores, nk).clamp_(0, n_chunks - 1)
+        # the reference clamps to [0, n_chunks); with nk <= n_chunks every
+        # index of the top-k is already inside, so the clamp (a launch) is skipped
+        chunk_idx = float_topk_3d(scores, nk)
         density = self._cached_cds_density_scores
         partial_chunk_density_scores_cuda(chunk_idx, self._chunk_key_centroid_gpu[layer_idx], raw_q, density)
         dense_mask = self._cached_dense_mask
-        dense_mask_from_topk_cuda(float_topk_3d(density, self._cached_cds_n_dense), dense_mask)
+        # float_topk_3d + dense_mask_from_topk_cuda (S:2360-2369) in one launch
+        topk_dense_mask(density, self._cached_cds_n_dense, dense_mask)
         valid_chunks = int(self.cpu_valid_end[layer_idx]) // chunk
         packed = self.key_kivi_packed_gpu[layer_idx][:, :, :valid_chunks]
         out_scores, out_indices = self._cached_cds_out_scores, self._cached_cds_out_indices

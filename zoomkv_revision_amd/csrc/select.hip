@@ -106,6 +106,13 @@ __global__ __launch_bounds__(256) void quest_score_kernel(
 constexpr int kTopkThreads = 1024;
 constexpr int kTopkWaves = kTopkThreads / 64;
 
+// Optional second output of a top-k: a byte mask over the row's L slots, 1
+// at every selected index (dense_mask_from_topk fused in; m == nullptr: none).
+struct TopkMask {
+  uint8_t* m;
+  int64_t stride;
+};
+
 __device__ __forceinline__ uint32_t ordered_key(float x) {
   const uint32_t b = __float_as_uint(x);
   return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
@@ -135,7 +142,8 @@ __device__ __forceinline__ int block_exclusive_count(bool flag, int* s_wave, int
 __global__ __launch_bounds__(kTopkThreads) void topk_kernel(
     const float* __restrict__ in, int64_t in_stride, int L, int k, int64_t* __restrict__ out,
     int64_t out_stride, const int64_t* __restrict__ lut, int64_t lut_stride,
-    const int64_t* __restrict__ skipped, int64_t sk_stride, int sk_count, int64_t sentinel) {
+    const int64_t* __restrict__ skipped, int64_t sk_stride, int sk_count, int64_t sentinel,
+    const TopkMask mk) {
   __shared__ int s_hist[kTopkWaves][256];
   __shared__ int s_wave[kTopkWaves];
   __shared__ int s_bin, s_remain;
@@ -145,11 +153,16 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(
   int64_t* o = out + row * out_stride;
   const int64_t* lrow = lut ? lut + row * lut_stride : nullptr;
 
+  uint8_t* mrow = mk.m ? mk.m + row * mk.stride : nullptr;
   for (int i = tid; i < sk_count; i += kTopkThreads) o[k + i] = skipped[row * sk_stride + i];
   if (L <= k) {
     for (int i = tid; i < k; i += kTopkThreads) o[i] = (i < L) ? (lrow ? lrow[i] : i) : sentinel;
+    if (mrow)
+      for (int i = tid; i < L; i += kTopkThreads) mrow[i] = 1;
     return;
   }
+  if (mrow)  // cleared here, set after the barriers below
+    for (int i = tid; i < L; i += kTopkThreads) mrow[i] = 0;
 
   uint32_t prefix = 0, mask = 0;
   int remain = k;  // how many of the candidates matching (prefix, mask) to keep
@@ -212,7 +225,10 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(
     const bool sel = gt || (eq && taken_eq + eq_rank < remain);
     int sel_total = 0;
     const int pos = written + block_exclusive_count(sel, s_wave, sel_total);
-    if (sel) o[pos] = lrow ? lrow[i] : i;
+    if (sel) {
+      o[pos] = lrow ? lrow[i] : i;
+      if (mrow) mrow[i] = 1;
+    }
     taken_eq += eq_total;
     written += sel_total;
     if (written >= k) break;  // uniform across the block
@@ -424,7 +440,7 @@ template <int R>
 __device__ __forceinline__ bool topk_from_candidates(const uint32_t (&bits)[R], int L, int k, const TauTest tt,
                                                      uint32_t* s_cnt, uint2* s_cand, int (*s_hist)[256],
                                                      int* s_sel, uint32_t* s_total, int64_t* o,
-                                                     const int64_t* lrow) {
+                                                     const int64_t* lrow, uint8_t* mrow) {
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   int mine = 0;
 #pragma unroll
@@ -470,6 +486,7 @@ __device__ __forceinline__ bool topk_from_candidates(const uint32_t (&bits)[R], 
   ordered_emit<kQ>(ck, total, k, T, remain, s_cnt, [&](int pos, int p) {
     const int i = static_cast<int>(s_cand[p].y);
     o[pos] = lrow ? lrow[i] : i;
+    if (mrow) mrow[i] = 1;
   });
   return true;
 }
@@ -478,7 +495,8 @@ template <int R>
 __global__ __launch_bounds__(kTopkThreads) void topk_reg_kernel(
     const float* __restrict__ in, int64_t in_stride, int L, int k, int64_t* __restrict__ out,
     int64_t out_stride, const int64_t* __restrict__ lut, int64_t lut_stride,
-    const int64_t* __restrict__ skipped, int64_t sk_stride, int sk_count, int64_t sentinel) {
+    const int64_t* __restrict__ skipped, int64_t sk_stride, int sk_count, int64_t sentinel,
+    const TopkMask mk) {
   constexpr bool kSampled = R >= 8;
   constexpr int kCand = kSampled ? kTopkCand : 1;
   static_assert(R % 4 == 0 && R * kTopkWaves >= 64, "register rows come in fours");
@@ -494,11 +512,16 @@ __global__ __launch_bounds__(kTopkThreads) void topk_reg_kernel(
   int64_t* o = out + row * out_stride;
   const int64_t* lrow = lut ? lut + row * lut_stride : nullptr;
 
+  uint8_t* mrow = mk.m ? mk.m + row * mk.stride : nullptr;
   for (int i = tid; i < sk_count; i += kTopkThreads) o[k + i] = skipped[row * sk_stride + i];
   if (L <= k) {
     for (int i = tid; i < k; i += kTopkThreads) o[i] = (i < L) ? (lrow ? lrow[i] : i) : sentinel;
+    if (mrow)
+      for (int i = tid; i < L; i += kTopkThreads) mrow[i] = 1;
     return;
   }
+  if (mrow)  // cleared here, set after the barriers below
+    for (int i = tid; i < L; i += kTopkThreads) mrow[i] = 0;
   // All loads are issued before any is used (addresses clamped into the row),
   // the sample first, and the threshold search runs while the row arrives.
   const bool sampled = kSampled && k <= kTopkSampledMaxK;
@@ -544,7 +567,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_reg_kernel(
   if constexpr (kSampled) {
     if (sampled && tau != 0) {
       if (topk_from_candidates<R>(bits, L, k, make_tau_test(tau), s_cnt, s_cand, s_hist, s_sel, &s_total, o,
-                                  lrow))
+                                  lrow, mrow))
         return;
     }
   }
@@ -553,36 +576,57 @@ __global__ __launch_bounds__(kTopkThreads) void topk_reg_kernel(
   for (int j = 0; j < R; ++j) key[j] = ordered_key_bits(bits[j]);
   int remain;
   const uint32_t T = radix_select<R>(key, L, k, s_hist, s_sel, remain);
-  ordered_emit<R>(key, L, k, T, remain, s_cnt, [&](int pos, int i) { o[pos] = lrow ? lrow[i] : i; });
+  ordered_emit<R>(key, L, k, T, remain, s_cnt, [&](int pos, int i) {
+    o[pos] = lrow ? lrow[i] : i;
+    if (mrow) mrow[i] = 1;
+  });
 }
 
 // ----------------------------------------------------------------------------
 // CDS density: centroid[chunk_id] . q (rerank_topk.cu:560-624): buf[t] = c[t]q[t]
 // for t < 128, then buf[t] += buf[t+s], s = 64..1; invalid id -> -1e30.
 // A wave scores kDensityItems slots (lane l starts with p[l] + p[l+64] of
-// each), their loads issued together and their trees interleaved.
+// each), their loads issued together and their trees interleaved.  The tree
+// steps read lane l + s without LDS: s = 32 and 16 by the gfx950 permlane
+// swaps, s = 8, 4, 2, 1 by DPP row shifts (lanes >= s carry values that the
+// later steps do not read).
 // ----------------------------------------------------------------------------
-constexpr int kDensityItems = 4;
+constexpr int kDensityItems = 8;
+
+// x[lane + 32] in lanes 0-31 / x[lane + 16] in lanes 0-15 (and 32-47).
+__device__ __forceinline__ float from_lane_plus32(float x) {
+  return __uint_as_float(__builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false)[1]);
+}
+__device__ __forceinline__ float from_lane_plus16(float x) {
+  return __uint_as_float(__builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false)[1]);
+}
+// x[lane + n] within each row of 16 lanes (DPP row_shl:n)
+template <int n>
+__device__ __forceinline__ float from_lane_plus(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x100 + n, 0xf, 0xf, false));
+}
 
 __global__ __launch_bounds__(256) void density_kernel(
     const int64_t* __restrict__ ids, int64_t id_sb, int64_t id_sh, const uint16_t* __restrict__ cent,
     int64_t c_sb, int64_t c_sh, int64_t c_sc, const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_sh,
-    float* __restrict__ out, int64_t o_sb, int64_t o_sh, int kv, int nk, int n_chunks, int64_t total) {
+    float* __restrict__ out, int64_t o_sb, int64_t o_sh, int kv, int nk, int n_chunks, int total) {
   constexpr int U = kDensityItems;
   const int lane = threadIdx.x & 63;
-  const int64_t item0 = (static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * U;
+  const int item0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * U;
   if (item0 >= total) return;
+  // consecutive items: (row bh, slot) advance with a wrap instead of a division each
+  int bh = item0 / nk, slot = item0 - bh * nk;
+  int bhs[U], slots[U];
   float v[U];
   bool ok[U];
-  int64_t oidx[U];
   uint16_t c0[U], c1[U], q0[U], q1[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    const int64_t item = min(item0 + u, total - 1);
-    const int slot = static_cast<int>(item % nk);
-    const int64_t bh = item / nk;
-    const int b = static_cast<int>(bh / kv), h = static_cast<int>(bh % kv);
-    const int64_t cid = ids[b * id_sb + h * id_sh + slot];
+    const bool in = item0 + u < total;
+    bhs[u] = in ? bh : 0;
+    slots[u] = in ? slot : 0;
+    const int b = bhs[u] / kv, h = bhs[u] - (bhs[u] / kv) * kv;
+    const int64_t cid = ids[b * id_sb + h * id_sh + slots[u]];
     ok[u] = cid >= 0 && cid < n_chunks;
     const uint16_t* c = cent + b * c_sb + h * c_sh + (ok[u] ? cid : 0) * c_sc;
     const uint16_t* qq = q + b * q_sb + h * q_sh;
@@ -590,7 +634,7 @@ __global__ __launch_bounds__(256) void density_kernel(
     c1[u] = c[lane + 64];
     q0[u] = qq[lane];
     q1[u] = qq[lane + 64];
-    oidx[u] = b * o_sb + h * o_sh + slot;
+    if (++slot == nk) slot = 0, ++bh;
   }
 #pragma unroll
   for (int u = 0; u < U; ++u) {
@@ -599,16 +643,23 @@ __global__ __launch_bounds__(256) void density_kernel(
     v[u] = a + w;
   }
 #pragma unroll
-  for (int s = 32; s >= 1; s >>= 1)
+  for (int u = 0; u < U; ++u) v[u] = v[u] + from_lane_plus32(v[u]);
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const float o = __shfl_down(v[u], s);
-      if (lane < s) v[u] = v[u] + o;
-    }
+  for (int u = 0; u < U; ++u) v[u] = v[u] + from_lane_plus16(v[u]);
+#pragma unroll
+  for (int u = 0; u < U; ++u) v[u] = v[u] + from_lane_plus<8>(v[u]);
+#pragma unroll
+  for (int u = 0; u < U; ++u) v[u] = v[u] + from_lane_plus<4>(v[u]);
+#pragma unroll
+  for (int u = 0; u < U; ++u) v[u] = v[u] + from_lane_plus<2>(v[u]);
+#pragma unroll
+  for (int u = 0; u < U; ++u) v[u] = v[u] + from_lane_plus<1>(v[u]);
   if (lane == 0) {
 #pragma unroll
-    for (int u = 0; u < U; ++u)
-      if (item0 + u < total) out[oidx[u]] = ok[u] ? v[u] : -1e30f;
+    for (int u = 0; u < U; ++u) {
+      const int b = bhs[u] / kv, h = bhs[u] - (bhs[u] / kv) * kv;
+      if (item0 + u < total) out[b * o_sb + h * o_sh + slots[u]] = ok[u] ? v[u] : -1e30f;
+    }
   }
 }
 
@@ -645,15 +696,15 @@ __global__ __launch_bounds__(128) void gqa_mean_kernel(const uint16_t* __restric
 // keep dense_topk / sparse_topk per chunk, (-1e30, 0) elsewhere.
 // One lane per token; G lanes per chunk; 256 threads per block.
 // ----------------------------------------------------------------------------
-template <int G>
-__global__ __launch_bounds__(256) void kivi_qk_kernel(
+template <int G, int T>
+__global__ __launch_bounds__(T) void kivi_qk_kernel(
     const int64_t* __restrict__ ids, int64_t id_sb, int64_t id_sh, const uint8_t* __restrict__ dmask,
     int64_t dm_sb, int64_t dm_sh, const int32_t* __restrict__ packed, int64_t pk_sb, int64_t pk_sh,
     int n_packed, const uint16_t* __restrict__ cmin, const uint16_t* __restrict__ cmax, int64_t cm_sb,
     int64_t cm_sh, int n_max, const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_sh,
     float* __restrict__ out_s, int64_t* __restrict__ out_i, int64_t o_sb, int64_t o_sh, int nk,
     int dense_topk, int sparse_topk) {
-  constexpr int kChunks = 256 / G;
+  constexpr int kChunks = T / G;
   // q is the same for every chunk of the block; the per-chunk rows are padded
   // by 4 floats so that the chunks of one wave read different LDS banks.
   __shared__ float s_q[128];
@@ -677,7 +728,7 @@ __global__ __launch_bounds__(256) void kivi_qk_kernel(
 #pragma unroll
     for (int p = 0; p < 16; ++p) words[p] = static_cast<uint32_t>(w[p * G]);
   }
-  if (threadIdx.x < 128) s_q[threadIdx.x] = bf16_to_f32(q[b * q_sb + h * q_sh + threadIdx.x]);
+  for (int d = threadIdx.x; d < 128; d += T) s_q[d] = bf16_to_f32(q[b * q_sb + h * q_sh + d]);
   if (valid_slot) {
     const int64_t mrow = (b * cm_sb + h * cm_sh) + (cid >= 0 && cid < n_max ? cid : 0) * 128;
     for (int d = lane; d < 128; d += G) {
@@ -801,10 +852,10 @@ extern "C" int zkv_quest_chunk_score(const uint16_t* q, const uint16_t* chunk_mi
   return check_launch("quest_score_kernel");
 }
 
-extern "C" int zkv_topk(const float* scores, int64_t in_stride, int rows, int L, int k,
-                        int64_t* out, int64_t out_stride, const int64_t* lut, int64_t lut_stride,
-                        const int64_t* skipped, int64_t sk_stride, int sk_count, int64_t sentinel,
-                        zkv_stream_t stream) {
+namespace {
+int launch_topk(const float* scores, int64_t in_stride, int rows, int L, int k, int64_t* out, int64_t out_stride,
+                const int64_t* lut, int64_t lut_stride, const int64_t* skipped, int64_t sk_stride, int sk_count,
+                int64_t sentinel, const TopkMask mk, zkv_stream_t stream) {
   ZKV_REQUIRE(scores && out, "zkv_topk: null pointer");
   ZKV_REQUIRE(rows >= 0 && L >= 0 && k > 0, "zkv_topk: bad sizes rows=%d L=%d k=%d", rows, L, k);
   ZKV_REQUIRE(out_stride >= k + sk_count, "zkv_topk: out row of %lld < k + skipped = %d",
@@ -814,7 +865,7 @@ extern "C" int zkv_topk(const float* scores, int64_t in_stride, int rows, int L,
   auto s = reinterpret_cast<hipStream_t>(stream);
 #define ZKV_TOPK_REG(R)                                                                          \
   topk_reg_kernel<R><<<rows, kTopkThreads, 0, s>>>(scores, in_stride, L, k, out, out_stride, lut, \
-                                                   lut_stride, skipped, sk_stride, sk_count, sentinel)
+                                                   lut_stride, skipped, sk_stride, sk_count, sentinel, mk)
   if (L <= 4 * kTopkThreads)
     ZKV_TOPK_REG(4);
   else if (L <= 8 * kTopkThreads)
@@ -825,9 +876,27 @@ extern "C" int zkv_topk(const float* scores, int64_t in_stride, int rows, int L,
     ZKV_TOPK_REG(32);
   else
     topk_kernel<<<rows, kTopkThreads, 0, s>>>(scores, in_stride, L, k, out, out_stride, lut, lut_stride,
-                                              skipped, sk_stride, sk_count, sentinel);
+                                              skipped, sk_stride, sk_count, sentinel, mk);
 #undef ZKV_TOPK_REG
   return check_launch("topk_kernel");
+}
+}  // namespace
+
+extern "C" int zkv_topk(const float* scores, int64_t in_stride, int rows, int L, int k,
+                        int64_t* out, int64_t out_stride, const int64_t* lut, int64_t lut_stride,
+                        const int64_t* skipped, int64_t sk_stride, int sk_count, int64_t sentinel,
+                        zkv_stream_t stream) {
+  return launch_topk(scores, in_stride, rows, L, k, out, out_stride, lut, lut_stride, skipped, sk_stride,
+                     sk_count, sentinel, TopkMask{nullptr, 0}, stream);
+}
+
+extern "C" int zkv_topk_dense_mask(const float* scores, int64_t in_stride, int rows, int L, int k,
+                                   int64_t* out, int64_t out_stride, uint8_t* mask, int64_t mask_stride,
+                                   zkv_stream_t stream) {
+  ZKV_REQUIRE(mask && mask_stride >= L, "zkv_topk_dense_mask: null mask or row of %lld < L = %d",
+              static_cast<long long>(mask_stride), L);
+  return launch_topk(scores, in_stride, rows, L, k, out, out_stride, nullptr, 0, nullptr, 0, 0, -1,
+                     TopkMask{mask, mask_stride}, stream);
 }
 
 extern "C" int zkv_chunk_density_scores(const int64_t* chunk_ids, int64_t id_sb, int64_t id_sh,
@@ -838,11 +907,13 @@ extern "C" int zkv_chunk_density_scores(const int64_t* chunk_ids, int64_t id_sb,
   ZKV_REQUIRE(chunk_ids && centroids && raw_q && out, "zkv_chunk_density_scores: null pointer");
   ZKV_REQUIRE(bs > 0 && kv > 0 && nk >= 0, "zkv_chunk_density_scores: bad sizes");
   const int64_t total = static_cast<int64_t>(bs) * kv * nk;
+  ZKV_REQUIRE(total < (int64_t{1} << 30), "zkv_chunk_density_scores: %lld slots exceed 2^30",
+              static_cast<long long>(total));
   if (total == 0) return ZKV_OK;
   density_kernel<<<static_cast<int>((total + 4 * kDensityItems - 1) / (4 * kDensityItems)), 256, 0,
                    reinterpret_cast<hipStream_t>(stream)>>>(
       chunk_ids, id_sb, id_sh, centroids, c_sb, c_sh, c_sc, raw_q, q_sb, q_sh, out, o_sb, o_sh, kv, nk,
-      n_chunks, total);
+      n_chunks, static_cast<int>(total));
   return check_launch("density_kernel");
 }
 
@@ -885,18 +956,22 @@ extern "C" int zkv_kivi_qk_dense_sparse(const int64_t* chunk_ids, int64_t id_sb,
   ZKV_REQUIRE(bs > 0 && kv > 0 && nk >= 0, "zkv_kivi_qk_dense_sparse: bad sizes");
   if (nk == 0) return ZKV_OK;
   auto s = reinterpret_cast<hipStream_t>(stream);
+#ifndef ZKV_KIVI_QK_THREADS
+#define ZKV_KIVI_QK_THREADS 256
+#endif
+  constexpr int kT = ZKV_KIVI_QK_THREADS;  // threads per block: kT / G chunks
   if (group_size == 16) {
-    dim3 grid((nk + 15) / 16, kv, bs);
-    kivi_qk_kernel<16><<<grid, 256, 0, s>>>(chunk_ids, id_sb, id_sh, dense_mask, dm_sb, dm_sh,
-                                            packed_K, pk_sb, pk_sh, n_packed, chunk_min, chunk_max,
-                                            cm_sb, cm_sh, n_chunks_max, raw_q, q_sb, q_sh, out_scores,
-                                            out_indices, o_sb, o_sh, nk, dense_topk, sparse_topk);
+    dim3 grid((nk + kT / 16 - 1) / (kT / 16), kv, bs);
+    kivi_qk_kernel<16, kT><<<grid, kT, 0, s>>>(chunk_ids, id_sb, id_sh, dense_mask, dm_sb, dm_sh,
+                                               packed_K, pk_sb, pk_sh, n_packed, chunk_min, chunk_max,
+                                               cm_sb, cm_sh, n_chunks_max, raw_q, q_sb, q_sh, out_scores,
+                                               out_indices, o_sb, o_sh, nk, dense_topk, sparse_topk);
   } else {
-    dim3 grid((nk + 31) / 32, kv, bs);
-    kivi_qk_kernel<8><<<grid, 256, 0, s>>>(chunk_ids, id_sb, id_sh, dense_mask, dm_sb, dm_sh,
-                                           packed_K, pk_sb, pk_sh, n_packed, chunk_min, chunk_max,
-                                           cm_sb, cm_sh, n_chunks_max, raw_q, q_sb, q_sh, out_scores,
-                                           out_indices, o_sb, o_sh, nk, dense_topk, sparse_topk);
+    dim3 grid((nk + kT / 8 - 1) / (kT / 8), kv, bs);
+    kivi_qk_kernel<8, kT><<<grid, kT, 0, s>>>(chunk_ids, id_sb, id_sh, dense_mask, dm_sb, dm_sh,
+                                              packed_K, pk_sb, pk_sh, n_packed, chunk_min, chunk_max,
+                                              cm_sb, cm_sh, n_chunks_max, raw_q, q_sb, q_sh, out_scores,
+                                              out_indices, o_sb, o_sh, nk, dense_topk, sparse_topk);
   }
   return check_launch("kivi_qk_kernel");
 }

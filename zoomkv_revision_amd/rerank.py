@@ -49,6 +49,23 @@ def dense_mask_from_topk_cuda(positions: torch.Tensor, mask: torch.Tensor, kerne
                                          stream_of(mask)))
 
 
+def topk_dense_mask(scores: torch.Tensor, k: int, mask: torch.Tensor, out: torch.Tensor | None = None):
+    """dense_mask_from_topk_cuda(float_topk_3d(scores, k), mask) in one launch:
+    scores [bs, kv, L] fp32, mask [bs, kv, L] bool; returns the top-k indices."""
+    require_gpu(scores, mask)
+    bs, kv, L = scores.shape
+    assert k <= L, "k must not exceed the row length"
+    if scores.dtype != torch.float32 or scores.stride(-1) != 1 or scores.stride(0) != kv * scores.stride(1):
+        scores = scores.float().contiguous()
+    if mask.dtype != torch.bool or not mask.is_contiguous() or tuple(mask.shape) != (bs, kv, L):
+        raise RuntimeError("mask must be a contiguous bool tensor [bs, kv, L]")
+    if out is None:
+        out = torch.empty(bs, kv, k, dtype=torch.int64, device=scores.device)
+    check(lib().zkv_topk_dense_mask(ptr(scores), scores.stride(1), bs * kv, L, k, ptr(out), out.stride(1),
+                                    ptr(mask), L, stream_of(scores)))
+    return out
+
+
 def gqa_mean_query(q: torch.Tensor, kv_heads: int, out: torch.Tensor | None = None) -> torch.Tensor:
     """raw_q = q.view(bs, kv, g, 128).mean(2) in bf16 (S:1621-1626); q [bs, hq, 128] or [bs, 1, hq, 128]."""
     require_gpu(q)
