@@ -99,6 +99,39 @@ def test_sampling_rules():
     assert len(set(a)) == 1
 
 
+@pytest.mark.parametrize("temperature,top_p,top_k", [(0.6, 0.95, 20), (1.0, 0.5, 5), (0.8, 0.0, 50),
+                                                     (1.3, 0.99, 1), (0.6, 0.95, 0)])
+def test_windowed_sampling_matches_full_vocabulary(temperature, top_p, top_k):
+    """The windowed sampler draws the same token as the op-for-op restatement
+    of LLM.py:63-139 from the same generator state, over rows where the kept
+    set is a handful of tokens (peaked logits) and where it is all of top-k."""
+    gen = torch.Generator().manual_seed(7)
+    for trial in range(60):
+        scale = (0.5, 3.0, 12.0)[trial % 3]
+        logits = torch.randn(4, 3000, generator=gen) * scale
+        s = 1000 + trial
+        a = ds.sample_next_token(logits, temperature, top_p, top_k, torch.Generator().manual_seed(s))
+        b = ds.sample_next_token_full(logits, temperature, top_p, top_k, torch.Generator().manual_seed(s))
+        assert torch.equal(a, b), (trial, a, b)
+
+
+def test_windowed_sampling_ties_at_kth_value():
+    """Ties at the k-th value are all kept by top-k: inside the window they are
+    drawn like any kept token; a tie group larger than the window takes the
+    full-vocabulary path (same draws either way)."""
+    for n_ties in (3, 40):
+        logits = torch.full((2, 500), -5.0)
+        logits[:, :4] = torch.tensor([4.0, 3.0, 2.5, 2.0])
+        logits[:, 100:100 + n_ties] = 1.0           # k = 6: tokens 4.. tie at the 6th value
+        seen = set()
+        for s in range(300):
+            a = ds.sample_next_token(logits, 1.0, 0.999, 6, torch.Generator().manual_seed(s))
+            b = ds.sample_next_token_full(logits, 1.0, 0.999, 6, torch.Generator().manual_seed(s))
+            assert torch.equal(a, b)
+            seen.update(a.tolist())
+        assert seen <= {0, 1, 2, 3} | set(range(100, 100 + n_ties)) and len(seen & set(range(100, 200))) > 1
+
+
 def test_production_env_matches_reference_runner(monkeypatch):
     for k in list(ds.PRODUCTION_ENV) + ["POLAR_FORCE_CAND_TOKENS"]:
         monkeypatch.delenv(k, raising=False)

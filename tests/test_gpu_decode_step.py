@@ -37,6 +37,21 @@ def test_decode_steps_through_polar_cache_with_a_flush(monkeypatch):
     assert b["total"] > b["quest"] > 0
 
 
+def test_windowed_sampling_matches_full_vocabulary_on_device():
+    """On the device generator: the windowed sampler and the op-for-op
+    restatement of LLM.py:63-139 draw the same tokens over a Qwen3-size
+    vocabulary (both consume one Exp(1) row per draw, so the streams stay
+    aligned across calls)."""
+    g = torch.Generator(device="cuda").manual_seed(3)
+    ga = torch.Generator(device="cuda").manual_seed(11)
+    gb = torch.Generator(device="cuda").manual_seed(11)
+    for trial in range(40):
+        logits = torch.randn(4, 151936, generator=g, device="cuda") * (0.5, 4.0, 16.0, 40.0)[trial % 4]
+        a = ds.sample_next_token(logits, 0.6, 0.95, 20, generator=ga)
+        b = ds.sample_next_token_full(logits, 0.6, 0.95, 20, generator=gb)
+        assert torch.equal(a, b), (trial, a, b)
+
+
 def _bf16_close(got, ref, ulps=1.0):
     """Within `ulps` bf16 units at the tensor's largest magnitude (the fp32
     accumulation order differs from the library GEMM's)."""

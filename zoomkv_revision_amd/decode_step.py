@@ -234,11 +234,62 @@ class RandomQwen3:
         return F.linear(hidden[:, 0], self.embed).float()
 
 
+# Candidates kept beyond the k-th by the windowed sampler, so that ties at the
+# k-th value (which top-k keeps) still fall inside the window.
+_SAMPLE_TIE_WINDOW = 16
+
+
 def sample_next_token(logits: torch.Tensor, temperature: float = 1.0, top_p: float = 0.0,
                       top_k: int = 0, generator: torch.Generator | None = None) -> torch.Tensor:
     """Sampling of LLM.py:63-139: greedy below temperature 1e-5, else
     temperature, top-k (ties at the k-th value kept), top-p (the token that
-    crosses top_p kept), softmax, one multinomial draw per row."""
+    crosses top_p kept), softmax, one multinomial draw per row.
+
+    With top-k on, every token the two filters keep lies among the k + 16
+    largest logits unless more than 16 tokens tie with the k-th, so the sort,
+    softmax and cumulative sum of top-p run over that window instead of the
+    vocabulary.  The draw is torch.multinomial's for one sample (q ~ Exp(1)
+    over the whole row from the same generator, then the first index of the
+    largest p / q), with p / q formed only at the window's tokens: the others
+    have p = 0.  Same kept set and same draw as ``sample_next_token_full``;
+    the probabilities agree to rounding (their sums run in another order),
+    and among tokens tied at the top-p cut the kept ones follow torch.topk's
+    order where the reference's follow torch.sort's (neither is specified).
+    A tie group that overflows the window (checked on the device, one host
+    read) takes the full path."""
+    if logits.dim() == 3:
+        logits = logits.squeeze(1)
+    elif logits.dim() == 1:
+        logits = logits.unsqueeze(0)
+    if temperature < 1e-5:
+        return logits.argmax(dim=-1)
+    vocab = logits.size(-1)
+    if top_k <= 0 or min(top_k, vocab) + _SAMPLE_TIE_WINDOW >= vocab:
+        return sample_next_token_full(logits, temperature, top_p, top_k, generator)
+    scaled = logits / temperature
+    k = min(top_k, vocab)
+    vals, idx = torch.topk(scaled, k + _SAMPLE_TIE_WINDOW, dim=-1)
+    kth = vals[..., k - 1:k]
+    if bool((vals[..., -1:] == kth).any()):
+        return sample_next_token_full(logits, temperature, top_p, top_k, generator)
+    win = vals.masked_fill(vals < kth, float("-inf"))
+    if 0.0 < top_p < 1.0:
+        cum = torch.cumsum(F.softmax(win, dim=-1), dim=-1)
+        remove = cum > top_p
+        remove[..., 1:] = remove[..., :-1].clone()
+        remove[..., 0] = False
+        win = win.masked_fill(remove, float("-inf"))
+    probs = F.softmax(win, dim=-1)
+    q = torch.empty_like(scaled).exponential_(1, generator=generator)
+    ratio = probs / q.gather(-1, idx)
+    best = ratio.max(dim=-1, keepdim=True)[0]
+    return torch.where(ratio == best, idx, vocab).min(dim=-1)[0]
+
+
+def sample_next_token_full(logits: torch.Tensor, temperature: float = 1.0, top_p: float = 0.0,
+                           top_k: int = 0, generator: torch.Generator | None = None) -> torch.Tensor:
+    """LLM.py:63-139 over the whole vocabulary, op for op (the check the
+    windowed ``sample_next_token`` is tested against)."""
     if logits.dim() == 3:
         logits = logits.squeeze(1)
     elif logits.dim() == 1:
