@@ -249,8 +249,9 @@ def run_c5(args):
                    "ffn": geo.ffn, "vocab": geo.vocab, "q_heads": geo.heads, "kv_heads": geo.kv_heads,
                    "head_dim": geo.head_dim, "update_interval": interval, "full_attention_threshold": threshold,
                    "sampling": {"temperature": 0.6, "top_p": 0.95, "top_k": 20, "seed": 42},
-                   "attention_path": "polar_cache.compute: Quest stage 1 + CDS density + KIVI 4-bit stage 2 "
-                                     "+ top-100 + gather-free bf16 attention",
+                   "attention_path": "polar_cache.compute: Quest stage 1 + KIVI 4-bit stage 2 (dense = sparse "
+                                     "per-chunk top-k 8, so no density classification) + top-100 + "
+                                     "gather-free bf16 attention",
                    "parallelism": "single GPU"},
         "per_token_latency_ms": ms,
         "flushes_in_timed_region": flushes,

@@ -91,6 +91,14 @@ def test_cache_trace_chunk16_single_sample_prefill(rng, monkeypatch):
     assert 0 < n < 2 * 90
 
 
+def test_cache_trace_equal_dense_sparse_topk(rng, monkeypatch):
+    # the production knobs (dense = sparse = 8): the density classification is
+    # skipped, the selection must still equal the model's, which computes it
+    cache, model = _make(monkeypatch, 16, 0.4, 0.3, 8, 8, **GEO)
+    n = _run(rng, cache, model, GEO, prompt=400, steps=70)
+    assert n == 2 * 70
+
+
 def test_cache_short_prompt_full_attention(rng, monkeypatch):
     geo = dict(GEO, inp=50, new=60)
     cache, model = _make(monkeypatch, 8, 0.2, 0.3, 8, 8, **geo)

@@ -484,18 +484,23 @@ class polar_cache:
         # the reference clamps to [0, n_chunks); with nk <= n_chunks every
         # index of the top-k is already inside, so the clamp (a launch) is skipped
         chunk_idx = float_topk_3d(scores, nk)
-        density = self._cached_cds_density_scores
-        partial_chunk_density_scores_cuda(chunk_idx, self._chunk_key_centroid_gpu[layer_idx], raw_q, density)
+        dense_topk = max(1, min(self.cds_dense_topk, chunk))
+        sparse_topk = max(1, min(self.cds_sparse_topk, chunk))
         dense_mask = self._cached_dense_mask
-        # float_topk_3d + dense_mask_from_topk_cuda (S:2360-2369) in one launch
-        topk_dense_mask(density, self._cached_cds_n_dense, dense_mask)
+        if dense_topk != sparse_topk:
+            density = self._cached_cds_density_scores
+            partial_chunk_density_scores_cuda(chunk_idx, self._chunk_key_centroid_gpu[layer_idx], raw_q, density)
+            # float_topk_3d + dense_mask_from_topk_cuda (S:2360-2369) in one launch
+            topk_dense_mask(density, self._cached_cds_n_dense, dense_mask)
+        # else: every chunk keeps the same number of tokens whichever class it
+        # is in, so the density classification (S:2352-2369) cannot change the
+        # stage-2 output and its two launches are skipped
         valid_chunks = int(self.cpu_valid_end[layer_idx]) // chunk
         packed = self.key_kivi_packed_gpu[layer_idx][:, :, :valid_chunks]
         out_scores, out_indices = self._cached_cds_out_scores, self._cached_cds_out_indices
         kivi.partial_chunk_kivi_qk_dense_sparse_cuda(
             chunk_idx, dense_mask, packed, self._chunk_key_min_gpu[layer_idx], self._chunk_key_max_gpu[layer_idx],
-            raw_q, max(1, min(self.cds_dense_topk, chunk)), max(1, min(self.cds_sparse_topk, chunk)), chunk,
-            out_scores, out_indices)
+            raw_q, dense_topk, sparse_topk, chunk, out_scores, out_indices)
         k = min(self.final_topk, out_scores.shape[-1])
         sk = self._chunk_skipped_count[layer_idx]
         skipped = self._chunk_skipped_indices_gpu[layer_idx][:bs, :, :sk]

@@ -342,7 +342,8 @@ def fill_cache(cache, geo: Qwen3Geometry, batch: int, context: int, seed: int, d
 def attention_path_bytes(cache, layer: int) -> dict:
     """Algorithmic HBM bytes of one layer's attention path (cache.compute with
     the selection running): GQA mean, Quest bounds over the chunk metadata,
-    the two top-k passes, density, KIVI stage 2 over the candidate chunks, the
+    the two top-k passes, density (when the dense and sparse per-chunk top-k
+    differ; with equal values ``compute`` skips it), KIVI stage 2 over the candidate chunks, the
     top-k + gather + concat, and the attention over the selected and near-zone
     rows.  The decode append (one K / V row) is included."""
     bs, kv, d = cache.batch_size, cache.kv_head, cache.head_dim
@@ -356,8 +357,9 @@ def attention_path_bytes(cache, layer: int) -> dict:
     gq = bs * cache.num_heads * d * 2 + units * d * 2
     quest = units * (n_chunks * (2 * d * 2 + 1 + 4) + d * 2)
     topk1 = units * (n_chunks * 4 + nk * 8)
-    density = units * (nk * (8 + d * 2 + 4) + d * 2)
-    topk2 = units * (nk * 4 + nk)
+    classify = max(1, min(cache.cds_dense_topk, chunk)) != max(1, min(cache.cds_sparse_topk, chunk))
+    density = units * (nk * (8 + d * 2 + 4) + d * 2) if classify else 0    # skipped when dense = sparse
+    topk2 = units * (nk * 4 + nk) if classify else 0
     stage2 = units * (nk * (8 + 1 + 16 * chunk * 4 + 2 * d * 2) + nk * chunk * 12)
     gather = units * (nk * chunk * 12 + sk * 8 + (k_final + sk) * 8)
     attn = units * ((k_final + sk + near) * 2 * d * 2 + (k_final + sk) * 8) + 2 * bs * cache.num_heads * d * 2
