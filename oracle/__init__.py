@@ -22,24 +22,36 @@ golden vectors for this path) is listed in ``PINNING`` below and checked by
 
 PINNING = {
     "numerics.bf16_round": "exhaustive against torch's float32->bfloat16 cast",
-    "kivi.kivi_codes": "op-by-op against torch-CPU bfloat16 ops mirroring "
+    "kivi.kivi_codes": "golden vectors of quant_pack.quantize_kcache_4bit "
+                       "(g = 8 / 16 / 32, bit-exact, tests/test_golden.py); "
+                       "op-by-op against torch-CPU bfloat16 ops mirroring "
                        "S:2003-2009 and quant_pack.py:112-121; exhaustive "
                        "divide-vs-reciprocal check over all bf16 diffs; "
                        "invariants (flat group -> 0, max -> 15, range)",
-    "kivi.pack_last_dim": "closed form + brute-force round trip of all 16 "
-                          "code values at every nibble position",
+    "kivi.pack_last_dim": "golden vectors of quant_pack.pack_kcache_4bit + "
+                          "the S:2017 relayout (bit-exact); closed form + "
+                          "brute-force round trip of all 16 code values at "
+                          "every nibble position",
+    "kivi.chunk_minmax_mean / dequant_ref": "golden vectors of torch amin / "
+                                            "amax / mean (S:2133-2135) and "
+                                            "quant_pack.unpack_kcache_4bit",
     "kivi.kivi4_dequant / attention": "textbook softmax attention in float64 "
                                       "over dequantized K/V; LSE split "
                                       "invariance; GQA head independence",
-    "quest.quest_chunk_score": "upper-bound invariant vs brute force "
+    "quest.quest_chunk_score": "golden vectors of QuestPytorch (within the "
+                               "bf16 product-rounding bound); upper-bound "
+                               "invariant vs brute force "
                                "max_t q.k_t; order-independence where sums "
                                "are exact; torch-CPU product identity",
     "topk": "set equality with numpy argsort on tie-free inputs; planted "
             "selections",
-    "stage2.kivi_qk_dense_sparse": "op-by-op bf16 ladder vs torch-CPU "
+    "stage2.kivi_qk_dense_sparse": "golden vectors of qk_dot."
+                                   "partial_chunk_kivi_qk_ref (one bf16 unit, "
+                                   "kept sets); op-by-op bf16 ladder vs torch-CPU "
                                    "(quant_pack/qk_dot ops); bitonic network "
                                    "vs stable sort on tie-free inputs",
     "density": "tree sum equals fsum within 1 ulp; exact on dyadic inputs",
+    "kivi.lse_merge": "golden vectors of lse_merge.lse_merge_torch",
     "rabitq": "popcount identity vs brute-force +-1 dot products; FWHT vs "
               "explicit Hadamard matrix; correction factor closed form",
 }
