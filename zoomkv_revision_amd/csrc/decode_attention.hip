@@ -16,12 +16,13 @@
 //  * nibbles enter the matrix cores undequantized: one v_and_b32 per pair
 //    turns them into exact fp16 subnormals (n * 2^-24 for the low nibble of a
 //    byte, 16n * 2^-24 for the high one) and the scales move to the B operand:
-//      S[t, c]  = sum_d n[t,d] (q[c,d] s_d)       + sum_d q[c,d] (z_d + 8 s_d) - 8 sum_d q[c,d] s_d
-//      O[d, c] += sum_t n[d,t] (P[t,c] s_t,G(d))  + sum_t P[t,c] z_t,G(d)      - ...
-//    with the fp16-rounded products q*s (per channel) and P*s (per token and
-//    32-channel group) shared by the code MFMA and a "-8" centring MFMA, so
-//    the rounding error is that of (n - 8) * q * s, the size of the error of
-//    rounding code*scale + zero to fp16.  Zero points go through their own
+//      S[t, c]  = sum_d n[t,d] (q[c,d] s_d)       + sum_d q[c,d] z_d
+//      O[d, c] += sum_t n[d,t] (P[t,c] s_t,G(d))  + sum_t P[t,c] z_t,G(d)
+//    The K-side product q*s (per channel) enters as an fp16 hi + lo pair
+//    (lo = fp16(q*s - hi) from one fma, exact), so the scores carry no fp16
+//    rounding of q*s: that rounding, scaled by the code, was the largest error
+//    term of peaked softmaxes.  The V-side product 16*P*s (per token and
+//    32-channel group) is one fp16 value.  Zero points go through their own
 //    MFMAs on exact fp16 products;
 //  * S^T[t, c] = sum_d Khat[t, d] q[c, d] and O^T[d, c] += sum_t Vhat[d, t] P[t, c]
 //    run on the matrix cores as v_mfma_f32_16x16x32_f16 (query heads on the N
@@ -216,16 +217,14 @@ constexpr float kTwo24 = 16777216.0f;
 struct TileConsts {
   half8_t qB[4];   // q / 8 (K-MFMA B operand for the zero points)
   half8_t qBm[4];  // q / 8 with 1/16 on elements 2, 3, 6, 7 (times the K scales)
-  half8_t kcen;    // rows c < 8: -8 / -128 (raw-unit K centring); rows c >= 8: 0
   float qs, qs24;  // raw score -> base-2; the same for 2^-24-unit scores
 };
 
 // Tile compute from an LDS stage.
-//   K: S = sum n * fp16(q s) in 2^-24 units (codes are subnormals);
-//      Z rows c < 8: sum q z - 8 sum fp16(q s) (raw units), rows c >= 8:
-//      sum q s (exact products); score = S * 2^24 + Zlow + 8 Zhigh.
-//   V: O[j] += sum n * fp16(16 P s) - 8 sum fp16(16 P s) in 2^-20 units;
-//      OZ rows with bit 2 clear: sum P z of group (row & 3), set: sum P s.
+//   K: S = sum n * (hi + lo)(q s) in 2^-24 units (codes are subnormals);
+//      Z (every row) = sum q z (raw units); score = S * 2^24 + Z.
+//   V: O[j] += sum n * fp16(16 P s) in 2^-20 units; OZ row r = sum P z of
+//      32-channel group r & 3.
 __device__ __forceinline__ void compute_tile(const uint8_t* st, int lane, int c, int g,
                                              const TileConsts& tc, uint32_t half_mask,
                                              float& m_run, float4_t& L, float4_t O[8],
@@ -238,16 +237,19 @@ __device__ __forceinline__ void compute_tile(const uint8_t* st, int lane, int c,
   for (int s = 0; s < 4; ++s) {
     const uint8_t* km = st + 4096 + (4 * s + g) * 32;
     const u32x4_t ks = ld16(km);
-    const u32x4_t kzs = ld16(km + (c < 8 ? 16 : 0));  // zero points (rows < 8) or scales
+    const u32x4_t kz = ld16(km + 16);  // zero points
+    // q s as hi + lo fp16 pair: hi = fp16(q s), lo = fp16(q s - hi) by one fma (exact)
     const half8_t bp = as_half8(ks) * tc.qBm[s];
-    Z = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(kzs), tc.qB[s], Z, 0, 0, 0);
-    Z = __builtin_amdgcn_mfma_f32_16x16x32_f16(tc.kcen, bp, Z, 0, 0, 0);
-    S[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(codes8(kq0[s]), bp, S[0], 0, 0, 0);
-    S[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(codes8(kq1[s]), bp, S[1], 0, 0, 0);
+    const half8_t bl = __builtin_elementwise_fma(as_half8(ks), tc.qBm[s], -bp);
+    Z = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(kz), tc.qB[s], Z, 0, 0, 0);
+    const half8_t n0 = codes8(kq0[s]), n1 = codes8(kq1[s]);
+    S[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(n0, bp, S[0], 0, 0, 0);
+    S[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(n1, bp, S[1], 0, 0, 0);
+    S[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(n0, bl, S[0], 0, 0, 0);
+    S[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(n1, bl, S[1], 0, 0, 0);
   }
-  // rows 0-7 sit in lanes g < 2, rows 8-15 in lanes g >= 2
-  const auto zr = __builtin_amdgcn_permlane32_swap(__float_as_uint(Z[0]), __float_as_uint(Z[0]), false, false);
-  const float zc = __builtin_fmaf(8.0f, __uint_as_float(zr[1]), __uint_as_float(zr[0]));
+  // every row of Z holds sum q z (all A rows are the zero points)
+  const float zc = Z[0];
   // S[m] holds tokens 16m + 4g + i: drop an unselected page (half)
   if (!(half_mask & 1u)) S[0] = float4_t{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
   if (!(half_mask & 2u)) S[1] = float4_t{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
@@ -256,8 +258,8 @@ __device__ __forceinline__ void compute_tile(const uint8_t* st, int lane, int c,
   const u32x4_t vq0 = ld16(st + 2048 + 16 * lane);
   const u32x4_t vq1 = ld16(st + 3072 + 16 * lane);
   const uint8_t* vm = st + 4608;
-  const u32x4_t vzs = ld16(vm + ((c & 3) * 4 + g) * 32 + ((c & 4) ? 0 : 16));
-  OZ = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(vzs), pb, OZ, 0, 0, 0);
+  const u32x4_t vz = ld16(vm + ((c & 3) * 4 + g) * 32 + 16);  // zero points of group c & 3
+  OZ = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(vz), pb, OZ, 0, 0, 0);
   // P * 16 on the low-nibble elements 0, 1, 4, 5
   half8_t pm = pb;
   const half2_t sixteen = {(_Float16)16.0f, (_Float16)16.0f};
@@ -270,8 +272,6 @@ __device__ __forceinline__ void compute_tile(const uint8_t* st, int lane, int c,
     pm[4] = b2[0];
     pm[5] = b2[1];
   }
-  const u32x4_t vcen_bits = {0x80088008u, 0x80808080u, 0x80088008u, 0x80808080u};  // -8, -128 (x 2^-24)
-  const half8_t vcen = as_half8(vcen_bits);
 #pragma unroll
   for (int G = 0; G < 4; ++G) {
     const half8_t bv = as_half8(ld16(vm + (4 * G + g) * 32)) * pm;
@@ -280,7 +280,6 @@ __device__ __forceinline__ void compute_tile(const uint8_t* st, int lane, int c,
       const int j = 2 * G + jp;
       const uint32_t w = j < 4 ? vq0[j] : vq1[j - 4];
       O[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(codes8(w), bv, O[j], 0, 0, 0);
-      O[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vcen, bv, O[j], 0, 0, 0);
     }
   }
 }
@@ -467,11 +466,8 @@ void kivi4_attn_kernel(const AttnParams p) {
   }
   {
     const half8_t inv16 = {1, 1, 0.0625, 0.0625, 1, 1, 0.0625, 0.0625};
-    const half8_t cen = {-8, -8, -128, -128, -8, -8, -128, -128};
-    const half8_t zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
     for (int s = 0; s < 4; ++s) tc.qBm[s] = qB[s] * inv16;
-    tc.kcen = c < 8 ? cen : zero8;
     tc.qs = p.qscale;
     tc.qs24 = p.qscale * kTwo24;
   }
@@ -493,21 +489,12 @@ void kivi4_attn_kernel(const AttnParams p) {
     wait_tiles_in_flight(issued - 1 - k);
     compute_tile(ring[k % D], lane, c, g, tc, half_mask, m_run, L, O, OZ);
   }
-  // O to real units: O * 2^20 + sum P z + 8 sum P s of the row's group (OZ
-  // holds the z sums in rows with bit 2 clear = lanes of even g, the s sums in
-  // the others; group = row & 3 = component)
-  {
-    float zw[4];
+  // O to real units: O * 2^20 + sum P z of the M-tile's group (OZ component
+  // i = row 4g + i holds group i's sum; M-tile j lies in group j / 2)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(OZ[i]), __float_as_uint(OZ[i]), false, false);
-      zw[i] = __builtin_fmaf(8.0f, __uint_as_float(r[1]), __uint_as_float(r[0]));
-    }
+  for (int j = 0; j < 8; ++j)
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) O[j][i] = __builtin_fmaf(O[j][i], kTwo20, zw[j >> 1]);
-  }
+    for (int i = 0; i < 4; ++i) O[j][i] = __builtin_fmaf(O[j][i], kTwo20, OZ[j >> 1]);
 
   // ---- bf16 residual tiles (at most r_cap / 32 of them, in the last split) ----
   for (int t = max(T0, n_qt) + wave; t < T1; t += NW) {
