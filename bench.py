@@ -304,14 +304,14 @@ def run_h2d(args):
 
 
 def run_c3(args):
-    """C3: GQA-mean query -> Quest bounds over fp16 page metadata (2048 pages of
-    16 tokens) -> top-128 pages -> page-sparse 4-bit attention, batch 8,
-    32/8 heads, 32768 tokens; six planted workloads rotate between steps."""
+    """C3: GQA-mean query + Quest bounds over fp16 page metadata (2048 pages of
+    16 tokens, one launch) -> top-128 pages -> page-sparse 4-bit attention,
+    batch 8, 32/8 heads, 32768 tokens; six planted workloads rotate between
+    steps."""
     import numpy as np
     import torch
     from zoomkv_revision_amd import kivi, synthetic
-    from zoomkv_revision_amd.quest import quest_chunk_score
-    from zoomkv_revision_amd.rerank import gqa_mean_query
+    from zoomkv_revision_amd.quest import quest_chunk_score_gqa
     from zoomkv_revision_amd.topk import float_topk_3d
     bs, hq, kv, n_tok, n_sel = 8, 32, 8, 32768, 128
     dev = torch.device("cuda:0")
@@ -324,17 +324,17 @@ def run_c3(args):
 
     def step(i):
         w = ws[i % len(ws)]
-        gqa_mean_query(w["q"], kv, out=raw_q)
-        quest_chunk_score(raw_q, w["page_min"], w["page_max"], scores, n_pages)
+        quest_chunk_score_gqa(w["q"], kv, w["page_min"], w["page_max"], scores, n_pages, None, raw_q)
         sel = float_topk_3d(scores, n_sel)
         kivi.kivi4_sparse_attention(w["q"], w["cache"], sel, out=out)
         if i < len(ws):
             sel_ok.append(sel)
 
     ms = timed_loop(step, args.steps, args.warmup)
-    k_ms = kernel_batch_ms(lambda i: quest_chunk_score(raw_q, ws[i % len(ws)]["page_min"],
-                                                       ws[i % len(ws)]["page_max"], scores, n_pages),
-                           args.steps)
+    w0 = ws[0]
+    k_ms = kernel_batch_ms(lambda i: quest_chunk_score_gqa(w0["q"], kv, ws[i % len(ws)]["page_min"],
+                                                           ws[i % len(ws)]["page_max"], scores, n_pages,
+                                                           None, raw_q), args.steps)
     exact = all(torch.equal(s, ws[j]["planted"]) for j, s in enumerate(sel_ok[:len(ws)]))
     nb = synthetic.c3_algorithmic_bytes(bs, hq, kv, n_pages, n_sel)
     achieved = nb["quest"] / (k_ms * 1e-3) / 1e9
@@ -347,8 +347,8 @@ def run_c3(args):
         "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "fp16 metadata / u4->fp16 (fp32 accumulate)",
         "data": "synthetic (planted pages)",
-        "config": {"workload": "C3: GQA mean -> Quest (fp16 page min/max) -> top-128 of 2048 pages -> "
-                               "page-sparse 4-bit attention", "batch": bs, "q_heads": hq,
+        "config": {"workload": "C3: GQA mean + Quest (fp16 page min/max, one launch) -> top-128 of "
+                               "2048 pages -> page-sparse 4-bit attention", "batch": bs, "q_heads": hq,
                    "kv_heads": kv, "context": n_tok, "page_tokens": 16, "pages_selected": n_sel,
                    "parallelism": "single GPU"},
         "selection_equals_planted": exact,

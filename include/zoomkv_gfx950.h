@@ -146,6 +146,19 @@ int zkv_quest_chunk_score(const uint16_t* q, const uint16_t* chunk_min, const ui
                           int meta_fp16, float* scores, int bs, int kv, int n_chunks,
                           int n_chunks_max, const uint8_t* valid, zkv_stream_t stream);
 
+/* zkv_quest_chunk_score with its query formed in the same launch: the GQA-mean
+ * query raw_q[b, h] = bf16(sum_i q[b, h*g + i] / g), g = hq / kv, of
+ * zkv_gqa_mean_query is scored and also written to raw_q (bf16 [bs, kv, 128],
+ * contiguous, for the later stages).  It fuses the two steps of S:1621-1626
+ * and S:2223 (the torch mean, then quest_chunk_score,
+ * Z/cache_hub/quest/quest_chunk_score.cu:106-154); no counterpart of its own in
+ * the reference.  q bf16 [bs, hq, 128] at element strides (q_sb, q_sh),
+ * multiples of 4; n_chunks >= 1; the other arguments as zkv_quest_chunk_score. */
+int zkv_quest_chunk_score_gqa(const uint16_t* q, int64_t q_sb, int64_t q_sh, int hq, uint16_t* raw_q,
+                              const uint16_t* chunk_min, const uint16_t* chunk_max, int meta_fp16,
+                              float* scores, int bs, int kv, int n_chunks, int n_chunks_max,
+                              const uint8_t* valid, zkv_stream_t stream);
+
 /* Exact top-k of each of `rows` rows of L fp32 scores (row i at
  * scores + i*in_stride): out[i, 0..k) = the indices (or lut[i, index] when lut
  * != NULL) of the k largest scores, ties by lowest index, in increasing index

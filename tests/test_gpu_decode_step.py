@@ -34,7 +34,7 @@ def test_decode_steps_through_polar_cache_with_a_flush(monkeypatch):
     toks = torch.stack(seen)
     assert ((toks >= 0) & (toks < geo.vocab)).all()
     b = ds.attention_path_bytes(cache, 0)
-    assert b["total"] > b["quest"] > 0
+    assert b["total"] > b["quest_gqa"] > 0
 
 
 def test_windowed_sampling_matches_full_vocabulary_on_device():

@@ -32,6 +32,38 @@ def test_quest_chunk_score_bit_exact(rng, fp16_meta):
     assert np.array_equal(from_torch(scores).view(np.uint32), ref.view(np.uint32))
 
 
+@pytest.mark.parametrize("fp16_meta,bs,hq,kv,n_max,n,four_dim", [
+    (False, 2, 32, 8, 40, 37, True),     # the cache's [bs, 1, hq, 128] queries
+    (True, 3, 8, 2, 9, 9, False),
+    (False, 2, 6, 6, 5, 1, False),       # one chunk per (b, h): every chunk of a trip changes (b, h)
+    (False, 1, 16, 2, 8, 3, True),       # 3 chunks: trips straddle (b, h)
+    (True, 4, 32, 4, 600, 523, False),
+])
+def test_quest_chunk_score_gqa_bit_exact(rng, fp16_meta, bs, hq, kv, n_max, n, four_dim):
+    """The fused launch equals the GQA-mean kernel followed by the Quest scan:
+    raw_q bit-exact with the torch-mean restatement, scores bit-exact."""
+    from zoomkv_revision_amd.quest import quest_chunk_score_gqa
+    k = gaussian_bf16(rng, (bs, kv, n_max * 16, 128), outlier_channels=4)
+    mn, mx, _, _ = encode_chunks_ref(k, 16)
+    if fp16_meta:
+        mn, mx = f16_to_f32(f16_bits(mn)), f16_to_f32(f16_bits(mx))
+    q = gaussian_bf16(rng, (bs, hq, 128))
+    valid = rng.random((bs, kv, n_max)) > 0.1
+    raw_ref = osel.gqa_mean_query(q, kv)
+    ref = osel.quest_chunk_score(raw_ref, mn, mx, n, valid)
+    dt = torch.float16 if fp16_meta else torch.bfloat16
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to("cuda", dt)
+    qt = to_bf16(q)
+    if four_dim:
+        qt = qt.unsqueeze(1)
+    scores = torch.empty(bs, kv, n, dtype=torch.float32, device="cuda")
+    raw_q = torch.full((bs, kv, 128), 7.0, dtype=torch.bfloat16, device="cuda")
+    quest_chunk_score_gqa(qt, kv, t(mn), t(mx), scores, n, torch.from_numpy(valid).cuda(), raw_q)
+    torch.cuda.synchronize()
+    assert np.array_equal(from_torch(raw_q), raw_ref)
+    assert np.array_equal(from_torch(scores).view(np.uint32), ref.view(np.uint32))
+
+
 @pytest.mark.parametrize("L,k", [(2048, 128), (13120, 100), (131072, 256), (64, 64), (3000, 1),
                                  (4096, 1638), (1638, 491), (26208, 100), (32768, 7), (32769, 300),
                                  # register-bucket edges (1024 * R) and k = L - 1

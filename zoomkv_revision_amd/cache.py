@@ -43,7 +43,8 @@ import torch
 from . import kivi
 from .attention import gather_attention
 from .quest import load_kernel_module as _load_quest
-from .rerank import gqa_mean_query, partial_chunk_density_scores_cuda, topk_dense_mask
+from .quest import quest_chunk_score_gqa
+from .rerank import partial_chunk_density_scores_cuda, topk_dense_mask
 from .topk import float_topk_3d, float_topk_gather_concat_3d
 
 _FALSY = ("0", "false", "False", "")
@@ -472,15 +473,18 @@ class polar_cache:
     # ------------------------------------------------------------------
     # decode attention (S:1589-1775) and selection (S:2195-2467, 2688-2779)
     # ------------------------------------------------------------------
-    def _select(self, raw_q, layer_idx):
-        """Quest stage 1 + CDS dense / sparse + KIVI stage 2 + global top-k:
-        retrieval-zone token indices [bs, kv, min(final_topk, nk*chunk) + skipped]."""
+    def _select(self, queries, layer_idx):
+        """GQA-mean query + Quest stage 1 (one launch) + CDS dense / sparse +
+        KIVI stage 2 + global top-k: retrieval-zone token indices
+        [bs, kv, min(final_topk, nk*chunk) + skipped]."""
         bs, chunk = self.batch_size, self.quest_chunk_size
         n_chunks, nk = self._cached_quest_n_chunks, self._cached_quest_nk
         scores = self._cached_scores_view
-        self._quest_kernel.quest_chunk_score(raw_q, self._chunk_key_min_gpu[layer_idx],
-                                             self._chunk_key_max_gpu[layer_idx], scores, n_chunks,
-                                             self._chunk_valid_mask_gpu[layer_idx])
+        # raw_q = mean over each KV head's query heads (S:1621-1626), formed by
+        # the Quest scan (S:2223) itself
+        raw_q = quest_chunk_score_gqa(queries, self.kv_head, self._chunk_key_min_gpu[layer_idx],
+                                      self._chunk_key_max_gpu[layer_idx], scores, n_chunks,
+                                      self._chunk_valid_mask_gpu[layer_idx], self._raw_q)
         # the reference clamps to [0, n_chunks); with nk <= n_chunks every
         # index of the top-k is already inside, so the clamp (a launch) is skipped
         chunk_idx = float_topk_3d(scores, nk)
@@ -514,7 +518,6 @@ class polar_cache:
         total = region["total_len"]
         local_len = region["local_len"]
         retrieval_len = int(self.cpu_valid_end[layer_idx])
-        raw_q = gqa_mean_query(queries, self.kv_head, out=self._raw_q)
         min_total = max(self.FULL_ATTENTION_THRESHOLD, self.sink_size + self.local_size + self.final_topk * 2)
         K, V = self.unified_keys[layer_idx], self.unified_values[layer_idx]
         bs = self.batch_size
@@ -526,6 +529,6 @@ class polar_cache:
             idx = self._arange_buffer[:retrieval_len].view(1, 1, -1).expand(bs, self.kv_head, -1)
             self._last_topk_indices = None
         else:
-            idx = self._select(raw_q, layer_idx)
+            idx = self._select(queries, layer_idx)
             self._last_topk_indices = idx
         return gather_attention(queries, K, V, idx if idx.shape[-1] else None, self._near0, near_len)

@@ -93,6 +93,94 @@ __global__ __launch_bounds__(256) void quest_score_kernel(
   }
 }
 
+// Quest bounds with the GQA-mean query formed in the same launch.  Block
+// (x, bh) scores chunks [32x, 32x + 32) of row bh (8 halves of 32 lanes, 4
+// chunks each, the quest_score_kernel lane order and sums).  Its metadata
+// loads are issued first; meanwhile threads 0..127 form raw_q[bh] dim tid =
+// bf16(sum_i q[b, h*group + i][tid] / group) in head order (gqa_mean_kernel's
+// arithmetic) into LDS, and block 0 of the row stores it.
+template <bool kFp16Meta>
+__global__ __launch_bounds__(256) void quest_gqa_kernel(
+    const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_sh, int group, int kv,
+    uint16_t* __restrict__ raw_q_out, const uint16_t* __restrict__ cmin, const uint16_t* __restrict__ cmax,
+    const uint8_t* __restrict__ valid, float* __restrict__ scores, int n_chunks, int n_max) {
+  __shared__ uint16_t s_q[128];
+  const int half = threadIdx.x >> 5, t = threadIdx.x & 31;
+  constexpr int U = kQuestUnroll;
+  const int bh = blockIdx.y;
+  const int c0 = (blockIdx.x * 8 + half) * U;
+  u32x2_t mv[U], xv[U];
+  int row[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int chunk = min(c0 + u, n_chunks - 1);  // past the end re-reads the last chunk
+    row[u] = chunk;
+    const int64_t off = (static_cast<int64_t>(bh) * n_max + chunk) * 128 + 4 * t;
+    mv[u] = *reinterpret_cast<const u32x2_t*>(cmin + off);
+    xv[u] = *reinterpret_cast<const u32x2_t*>(cmax + off);
+  }
+  if (threadIdx.x < 128) {
+    const int b = bh / kv, h = bh - b * kv, d = threadIdx.x;
+    const uint16_t* qp = q + b * q_sb + static_cast<int64_t>(h) * group * q_sh + d;
+    constexpr int kRows = 8;  // head rows requested together, summed in head order
+    uint16_t w[kRows];
+#pragma unroll
+    for (int i = 0; i < kRows; ++i) w[i] = qp[min(i, group - 1) * q_sh];
+    float acc = bf16_to_f32(w[0]);
+#pragma unroll
+    for (int i = 1; i < kRows; ++i)
+      if (i < group) acc = acc + bf16_to_f32(w[i]);
+    for (int i = kRows; i < group; ++i) acc = acc + bf16_to_f32(qp[i * q_sh]);
+    const uint16_t r = f32_to_bf16_bits(acc / static_cast<float>(group));
+    s_q[d] = r;
+    if (blockIdx.x == 0) raw_q_out[static_cast<int64_t>(bh) * 128 + d] = r;
+  }
+  __syncthreads();
+  const u32x2_t qv = *reinterpret_cast<const u32x2_t*>(s_q + 4 * t);
+  float qq[4];
+  qq[0] = __uint_as_float(qv[0] << 16);
+  qq[1] = __uint_as_float(qv[0] & 0xFFFF0000u);
+  qq[2] = __uint_as_float(qv[1] << 16);
+  qq[3] = __uint_as_float(qv[1] & 0xFFFF0000u);
+  float sum[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    float mn[4], mx[4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      mn[2 * i] = meta_to_f32<kFp16Meta>(static_cast<uint16_t>(mv[u][i] & 0xFFFF));
+      mn[2 * i + 1] = meta_to_f32<kFp16Meta>(static_cast<uint16_t>(mv[u][i] >> 16));
+      mx[2 * i] = meta_to_f32<kFp16Meta>(static_cast<uint16_t>(xv[u][i] & 0xFFFF));
+      mx[2 * i + 1] = meta_to_f32<kFp16Meta>(static_cast<uint16_t>(xv[u][i] >> 16));
+    }
+    float sm = fmaxf(qq[0] * mn[0], qq[0] * mx[0]);
+    sm = sm + fmaxf(qq[1] * mn[1], qq[1] * mx[1]);
+    sm = sm + fmaxf(qq[2] * mn[2], qq[2] * mx[2]);
+    sm = sm + fmaxf(qq[3] * mn[3], qq[3] * mx[3]);
+    sum[u] = sm;
+  }
+#pragma unroll
+  for (int off = 16; off > 0; off >>= 1)
+#pragma unroll
+    for (int u = 0; u < U; ++u) sum[u] = sum[u] + __shfl_xor(sum[u], off);
+  if (t < U) {
+    float out = sum[0];
+    int r = row[0];
+#pragma unroll
+    for (int u = 1; u < U; ++u)
+      if (t == u) {
+        out = sum[u];
+        r = row[u];
+      }
+    const int chunk = c0 + t;
+    if (chunk < n_chunks) {
+      const int64_t vr = static_cast<int64_t>(bh) * n_max + r;
+      if (valid != nullptr && !valid[vr]) out = -INFINITY;
+      scores[static_cast<int64_t>(bh) * n_chunks + chunk] = out;
+    }
+  }
+}
+
 // ----------------------------------------------------------------------------
 // Exact top-k of a row (float_topk.cu:51-271 semantics, deterministic):
 // radix select on order-preserving uint32 keys (4 rounds of 8 bits) finds the
@@ -829,6 +917,27 @@ __global__ __launch_bounds__(128) void page_minmax_f16_kernel(
 }  // namespace zkv
 
 using namespace zkv;
+
+extern "C" int zkv_quest_chunk_score_gqa(const uint16_t* q, int64_t q_sb, int64_t q_sh, int hq,
+                                         uint16_t* raw_q, const uint16_t* chunk_min,
+                                         const uint16_t* chunk_max, int meta_fp16, float* scores, int bs,
+                                         int kv, int n_chunks, int n_chunks_max, const uint8_t* valid,
+                                         zkv_stream_t stream) {
+  ZKV_REQUIRE(q && raw_q && chunk_min && chunk_max && scores, "zkv_quest_chunk_score_gqa: null pointer");
+  ZKV_REQUIRE(bs > 0 && kv > 0 && hq > 0 && hq % kv == 0 && n_chunks >= 1 && n_chunks <= n_chunks_max &&
+                  static_cast<int64_t>(bs) * kv <= 65535,
+              "zkv_quest_chunk_score_gqa: bad sizes bs=%d hq=%d kv=%d n_chunks=%d n_chunks_max=%d", bs, hq,
+              kv, n_chunks, n_chunks_max);
+  const dim3 grid((n_chunks + 8 * kQuestUnroll - 1) / (8 * kQuestUnroll), bs * kv);
+  auto s = reinterpret_cast<hipStream_t>(stream);
+  if (meta_fp16)
+    quest_gqa_kernel<true><<<grid, 256, 0, s>>>(q, q_sb, q_sh, hq / kv, kv, raw_q, chunk_min, chunk_max, valid,
+                                                scores, n_chunks, n_chunks_max);
+  else
+    quest_gqa_kernel<false><<<grid, 256, 0, s>>>(q, q_sb, q_sh, hq / kv, kv, raw_q, chunk_min, chunk_max,
+                                                 valid, scores, n_chunks, n_chunks_max);
+  return check_launch("quest_gqa_kernel");
+}
 
 extern "C" int zkv_quest_chunk_score(const uint16_t* q, const uint16_t* chunk_min,
                                      const uint16_t* chunk_max, int meta_fp16, float* scores,

@@ -341,7 +341,7 @@ def fill_cache(cache, geo: Qwen3Geometry, batch: int, context: int, seed: int, d
 
 def attention_path_bytes(cache, layer: int) -> dict:
     """Algorithmic HBM bytes of one layer's attention path (cache.compute with
-    the selection running): GQA mean, Quest bounds over the chunk metadata,
+    the selection running): GQA mean + Quest bounds over the chunk metadata (one launch),
     the two top-k passes, density (when the dense and sparse per-chunk top-k
     differ; with equal values ``compute`` skips it), KIVI stage 2 over the candidate chunks, the
     top-k + gather + concat, and the attention over the selected and near-zone
@@ -354,8 +354,8 @@ def attention_path_bytes(cache, layer: int) -> dict:
     k_final = min(cache.final_topk, nk * chunk)
     region = cache.get_region_indices(layer)
     near = cache.sink_size + region["local_len"]
-    gq = bs * cache.num_heads * d * 2 + units * d * 2
-    quest = units * (n_chunks * (2 * d * 2 + 1 + 4) + d * 2)
+    # the Quest scan forms the GQA-mean query from the query heads and stores it
+    quest = units * n_chunks * (2 * d * 2 + 1 + 4) + bs * cache.num_heads * d * 2 + units * d * 2
     topk1 = units * (n_chunks * 4 + nk * 8)
     classify = max(1, min(cache.cds_dense_topk, chunk)) != max(1, min(cache.cds_sparse_topk, chunk))
     density = units * (nk * (8 + d * 2 + 4) + d * 2) if classify else 0    # skipped when dense = sparse
@@ -364,7 +364,7 @@ def attention_path_bytes(cache, layer: int) -> dict:
     gather = units * (nk * chunk * 12 + sk * 8 + (k_final + sk) * 8)
     attn = units * ((k_final + sk + near) * 2 * d * 2 + (k_final + sk) * 8) + 2 * bs * cache.num_heads * d * 2
     append = 2 * units * d * 2
-    parts = {"gqa_mean": gq, "quest": quest, "topk_chunks": topk1, "density": density,
+    parts = {"quest_gqa": quest, "topk_chunks": topk1, "density": density,
              "topk_dense": topk2, "kivi_stage2": stage2, "topk_gather_concat": gather,
              "attention": attn, "append": append}
     parts["total"] = sum(parts.values())

@@ -77,6 +77,47 @@ def page_minmax_f16(keys: torch.Tensor, page_size: int = 16, n_pages: int | None
     return page_min, page_max
 
 
+def quest_chunk_score_gqa(queries: torch.Tensor, kv_heads: int, chunk_min: torch.Tensor,
+                          chunk_max: torch.Tensor, scores: torch.Tensor, n_chunks: int,
+                          valid: torch.Tensor | None, raw_q: torch.Tensor) -> torch.Tensor:
+    """GQA-mean query (S:1621-1626) and Quest bounds in one launch.
+
+    queries bf16 [bs, hq, 128] or [bs, 1, hq, 128] (last dim contiguous);
+    raw_q bf16 [bs, kv, 128] contiguous receives bf16(mean over each KV
+    head's query heads), the query the bounds are scored with.  The other
+    arguments are those of ``quest_chunk_score``.  Returns raw_q.
+    """
+    q = queries.reshape(queries.shape[0], -1, queries.shape[-1]) if queries.dim() == 4 else queries
+    require_gpu(q, chunk_min, chunk_max, scores, raw_q)
+    if q.dtype != torch.bfloat16 or raw_q.dtype != torch.bfloat16:
+        raise RuntimeError("quest_chunk_score_gqa: queries and raw_q must be bf16")
+    bs, hq, d = q.shape
+    if d != 128 or q.stride(-1) != 1:
+        raise RuntimeError("quest_chunk_score_gqa: queries need head_dim 128, contiguous")
+    kv = int(kv_heads)
+    if hq % kv or tuple(raw_q.shape) != (bs, kv, 128) or not raw_q.is_contiguous():
+        raise RuntimeError("quest_chunk_score_gqa: raw_q must be a contiguous [bs, kv, 128] with kv | hq")
+    if chunk_min.dtype != chunk_max.dtype or chunk_min.dtype not in (torch.bfloat16, torch.float16):
+        raise RuntimeError("quest_chunk_score_gqa: chunk_min / chunk_max must both be bf16 or fp16")
+    n_max = chunk_min.shape[2]
+    n_chunks = int(n_chunks)
+    if not 1 <= n_chunks <= n_max:
+        raise RuntimeError("quest_chunk_score_gqa: need 1 <= n_chunks <= chunk_n_max")
+    if tuple(chunk_min.shape) != (bs, kv, n_max, 128) or chunk_max.shape != chunk_min.shape \
+            or not chunk_min.is_contiguous() or not chunk_max.is_contiguous():
+        raise RuntimeError("chunk_min / chunk_max must be contiguous [bs, kv, n_chunks_max, 128]")
+    if scores.dtype != torch.float32 or scores.numel() != bs * kv * n_chunks or not scores.is_contiguous():
+        raise RuntimeError("scores must be fp32 [bs, kv, n_chunks]")
+    if valid is not None:
+        if valid.dtype != torch.bool or not valid.is_contiguous() or tuple(valid.shape) != (bs, kv, n_max):
+            raise RuntimeError("valid must be a contiguous bool [bs, kv, n_chunks_max]")
+    check(lib().zkv_quest_chunk_score_gqa(
+        ptr(q), q.stride(0), q.stride(1), hq, ptr(raw_q), ptr(chunk_min), ptr(chunk_max),
+        int(chunk_min.dtype == torch.float16), ptr(scores), bs, kv, n_chunks, n_max, ptr(valid),
+        stream_of(q)))
+    return raw_q
+
+
 class QuestKernel:
     """Drop-in for the module ``quest_ops.load_kernel_module()`` returns."""
 

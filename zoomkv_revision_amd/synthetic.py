@@ -123,9 +123,11 @@ def c4_keys(seed: int, n: int, n_clusters: int, device, sigma: float = 0.1) -> t
 
 
 def c3_algorithmic_bytes(bs: int, hq: int, kv: int, n_pages: int, n_sel: int) -> dict:
-    """Bytes of the C3 step's kernels by algorithm: Quest metadata scan, and the
-    sparse attention's selected pages at 160 B per token (codes + metadata)."""
-    quest = bs * kv * (n_pages * 2 * HEAD_DIM * 2 + HEAD_DIM * 2 + n_pages * 4)
+    """Bytes of the C3 step's kernels by algorithm: the Quest metadata scan
+    (with the GQA-mean query formed from the query heads and stored in the
+    same launch), and the sparse attention's selected pages at 160 B per
+    token (codes + metadata)."""
+    quest = bs * kv * (n_pages * 2 * HEAD_DIM * 2 + n_pages * 4 + HEAD_DIM * 2) + bs * hq * HEAD_DIM * 2
     attn = bs * kv * n_sel * 16 * 160 + bs * hq * HEAD_DIM * 2 * 2
     return {"quest": quest, "sparse_attention": attn, "total": quest + attn}
 
