@@ -354,7 +354,7 @@ def run_c3(args):
         "selection_equals_planted": exact,
         "end_to_end_GBps": nb["total"] / (ms * 1e-3) / 1e9,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel": "quest_score_kernel",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel": "quest_gqa_kernel",
                      "kernel_ms": k_ms, "algorithmic_bytes": nb["quest"]},
         "algorithmic_bytes_per_step": nb,
         "cpu_baseline": cpu,
