@@ -99,6 +99,40 @@ def test_search_ties_go_to_lower_index(rng):
     _check_search(rng, 1, 4, 30000, 256, dup=40)
 
 
+@pytest.mark.parametrize("P,Q,N,topk", [
+    (1, 2, 65536, 1024),       # 8 slices x topk 1024 = the 8192-candidate limit
+    (1, 3, 3000, 256),
+    (2, 2, 2048, 300),
+])
+def test_search_more_sizes(rng, P, Q, N, topk):
+    _check_search(rng, P, Q, N, topk)
+
+
+def test_search_all_keys_equal(rng):
+    """Every key identical: every estimate ties, and the top-k are the lowest
+    indices."""
+    _check_search(rng, 1, 2, 20000, 256, dup=1)
+
+
+def test_search_few_planted_winners(rng):
+    """The query itself planted at 32 spread positions: those 32 keys lead the
+    candidates, the other 224 come from the clustered rest."""
+    from zoomkv_revision_amd.rabitq import rabitq_encode, rabitq_search
+    s_np, s_t = _signs()
+    n, topk = 50000, 256
+    keys = orq.clustered_unit_keys(rng, n, 16)
+    qs = orq.clustered_unit_keys(rng, 1, 16)
+    keys[[s * n // 2048 for s in range(32)]] = qs[0]
+    kt = _f16(keys)
+    codes, fac = rabitq_encode(kt, s_t)
+    cand, fidx, fsc = (from_torch(t) for t in rabitq_search(_f16(qs), kt, codes, fac, s_t, topk))
+    ck, fk = orq.encode(keys, s_np)
+    rc, ri, rs = orq.search(qs, keys, ck, fk, s_np, topk)
+    assert set([s * n // 2048 for s in range(32)]) <= set(cand[0].tolist())
+    assert np.array_equal(cand, rc) and np.array_equal(fidx, ri)
+    assert np.array_equal(fsc.view(np.uint32), rs.view(np.uint32))
+
+
 def test_search_c4_full_size(rng):
     """BASELINE config 4: 131072 clustered unit keys, 64 queries, top-256;
     8 of the 64 queries checked against the oracle, all 64 against invariants."""
@@ -128,8 +162,8 @@ def test_search_rejects_bad_sizes():
     f = torch.zeros(100, 2, dtype=torch.float16, device="cuda")
     with pytest.raises(AssertionError):
         rabitq_search(torch.zeros(2, 128, dtype=torch.float16, device="cuda"), k, c, f, s, 101)
-    big = torch.zeros(8193 * 9, 128, dtype=torch.float16, device="cuda")
-    with pytest.raises(RuntimeError, match="candidates"):
+    big = torch.zeros(2000, 128, dtype=torch.float16, device="cuda")
+    with pytest.raises(RuntimeError, match="topk"):                      # topk above 1024
         rabitq_search(torch.zeros(1, 128, dtype=torch.float16, device="cuda"), big,
                       torch.zeros(big.shape[0], 16, dtype=torch.uint8, device="cuda"),
-                      torch.zeros(big.shape[0], 2, dtype=torch.float16, device="cuda"), s, 1000)
+                      torch.zeros(big.shape[0], 2, dtype=torch.float16, device="cuda"), s, 1025)
