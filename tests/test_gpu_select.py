@@ -38,6 +38,7 @@ def test_quest_chunk_score_bit_exact(rng, fp16_meta):
     (False, 2, 6, 6, 5, 1, False),       # one chunk per (b, h): every chunk of a trip changes (b, h)
     (False, 1, 16, 2, 8, 3, True),       # 3 chunks: trips straddle (b, h)
     (True, 4, 32, 4, 600, 523, False),
+    (False, 1, 32, 2, 50, 50, False),    # 16 query heads per KV head: rows past the first 8 summed one by one
 ])
 def test_quest_chunk_score_gqa_bit_exact(rng, fp16_meta, bs, hq, kv, n_max, n, four_dim):
     """The fused launch equals the GQA-mean kernel followed by the Quest scan:
