@@ -83,13 +83,14 @@ struct AttnParams {
   float* ws_ml;    // [bs, kv, n_splits, gqa, 2]
   void* out;       // [bs, kv*gqa, 128], written directly when n_splits == 1
   int out_f32;
-  // page-sparse mode: quantized tile t of (b, kv) is Format Q group
-  // tile_group[bh * tile_cap + t] with halves tile_mask[...] (bit m = tokens
-  // 16m .. 16m+15 selected), tile_count[bh] tiles in all
-  const int32_t* tile_group;
-  const uint8_t* tile_mask;
-  const int32_t* tile_count;
-  int tile_cap;
+  // page-sparse mode: the sorted page list of (b, kv) at pages + b*pg_sb +
+  // h*pg_sh (n_sel ids).  Its tiles: a page 2g joined by a following 2g+1 is
+  // one tile (group g, both halves), any other in-range page a tile of its
+  // own half (bit m of the mask = tokens 16m .. 16m+15); ids outside
+  // [0, 2 n_groups) are skipped.
+  const int64_t* pages;
+  int64_t pg_sb, pg_sh;
+  int n_sel;
 };
 
 // One pipeline stage = one 32-token tile, a byte copy of its Format Q record:
@@ -411,25 +412,53 @@ void kivi4_attn_kernel(const AttnParams p) {
   const bool col_ok = c < p.gqa;
   const int64_t bh = static_cast<int64_t>(b) * p.kv + h;
 
-  const int n_qt = kSparse ? p.tile_count[bh] : p.n_groups;  // quantized tiles of (b, kv)
-  const int n_tiles = n_qt + (p.res_len + kTile - 1) / kTile;
   const int T0 = split * p.tiles_per_split;
+  uint8_t (*ring)[kStageBytes] = smem[wave];
+  int n_qt = p.n_groups;  // quantized tiles of (b, kv)
+  if constexpr (kSparse) {
+    // Every wave walks the page list (64 pages per step, the pairing by
+    // ballot ranks) and keeps the descriptors of its own tiles T0 + wave +
+    // NW*k, k < 64, in its last ring stage, which no DMA has reached yet.
+    int32_t* s_group = reinterpret_cast<int32_t*>(ring[D - 1]);
+    int32_t* s_mask = s_group + 64;
+    const int64_t* pg = p.pages + b * p.pg_sb + h * p.pg_sh;
+    const int64_t n_pages = 2ll * p.n_groups;
+    int base = 0;
+    for (int i0 = 0; i0 < p.n_sel; i0 += 64) {
+      const int i = i0 + lane;
+      const int64_t cur = i < p.n_sel ? pg[i] : -1;
+      const int64_t prev = (i > 0 && i < p.n_sel) ? pg[i - 1] : -1;
+      const int64_t next = (i + 1 < p.n_sel) ? pg[i + 1] : -1;
+      const bool valid = cur >= 0 && cur < n_pages;
+      const bool start = valid && !((cur & 1) && prev == cur - 1);
+      const uint64_t m = __ballot(start);
+      const int t = base + __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
+                                                    __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0));
+      const int rel = t - T0 - wave;
+      if (start && rel >= 0 && rel % NW == 0 && rel / NW < 64) {
+        s_group[rel / NW] = static_cast<int32_t>(cur >> 1);
+        s_mask[rel / NW] = (cur & 1) ? 2 : (next == cur + 1 ? 3 : 1);
+      }
+      base += __popcll(m);
+    }
+    n_qt = base;
+  }
+  const int n_tiles = n_qt + (p.res_len + kTile - 1) / kTile;
   const int T1 = min(T0 + p.tiles_per_split, n_tiles);
   const int TQ = min(T1, n_qt);  // quantized tiles of this workgroup: [T0, TQ)
   // this wave's quantized tiles: T0 + wave + NW*k, k < nq (nq <= 64 in sparse mode)
   const int nq = TQ > T0 + wave ? (TQ - (T0 + wave) + NW - 1) / NW : 0;
-  uint8_t (*ring)[kStageBytes] = smem[wave];
   // sparse mode: lane k holds the group and half mask of this wave's tile k
   int my_group = 0, my_mask = 3;
   if constexpr (kSparse) {
+    const int32_t* s_group = reinterpret_cast<const int32_t*>(ring[D - 1]);
     if (lane < nq) {
-      const int64_t ti = bh * p.tile_cap + T0 + wave + NW * lane;
-      my_group = p.tile_group[ti];
-      my_mask = p.tile_mask[ti];
+      my_group = s_group[lane];
+      my_mask = s_group[64 + lane];
     }
-    // the tile addresses need the list anyway; waiting here (a wait the
-    // compiler sees) keeps it from draining the ring at the mask's first use
-    wait_vmcnt<0>();
+    // the stage is the DMA target of tile D - 1 from here on
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the descriptor reads are done
+    __builtin_amdgcn_sched_barrier(0);
   }
   auto group_of = [&](int k) {
     if constexpr (kSparse)
@@ -595,42 +624,6 @@ __global__ __launch_bounds__(128) void kivi4_combine_kernel(const float* __restr
     reinterpret_cast<uint16_t*>(out)[oi] = f32_to_bf16_bits(r);
 }
 
-// Page list -> tiles for page-sparse attention.  Page P (16 tokens) is half
-// P & 1 of Format Q group P >> 1.  One wave per (b, kv): every listed page
-// starts a tile unless it is the odd half of a group whose even half is the
-// previous entry (then that tile takes both halves).  The tiles cover the
-// listed pages as a multiset: the result equals attention over the
-// concatenated tokens of the list (duplicates attended twice, as a gather
-// would); page ids outside [0, 2 * n_groups) are skipped.
-__global__ __launch_bounds__(64) void sparse_tiles_kernel(
-    const int64_t* __restrict__ pages, int64_t pg_sb, int64_t pg_sh, int n_sel, int kv, int n_groups,
-    int32_t* __restrict__ tile_group, uint8_t* __restrict__ tile_mask, int32_t* __restrict__ tile_count) {
-  const int bh = blockIdx.x;
-  const int b = bh / kv, h = bh - b * kv;
-  const int64_t* pg = pages + b * pg_sb + h * pg_sh;
-  const int lane = threadIdx.x;
-  const int64_t n_pages = 2ll * n_groups;
-  int base = 0;
-  for (int i0 = 0; i0 < n_sel; i0 += 64) {
-    const int i = i0 + lane;
-    const int64_t cur = i < n_sel ? pg[i] : -1;
-    const int64_t prev = (i > 0 && i < n_sel) ? pg[i - 1] : -1;
-    const int64_t next = (i + 1 < n_sel) ? pg[i + 1] : -1;
-    const bool valid = cur >= 0 && cur < n_pages;
-    const bool joins_prev = valid && (cur & 1) && prev == cur - 1;
-    const bool start = valid && !joins_prev;
-    const uint64_t m = __ballot(start);
-    const int rank = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
-                                               __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0));
-    if (start) {
-      const int64_t t = static_cast<int64_t>(bh) * n_sel + base + rank;
-      tile_group[t] = static_cast<int32_t>(cur >> 1);
-      tile_mask[t] = static_cast<uint8_t>((cur & 1) ? 2 : (next == cur + 1 ? 3 : 1));
-    }
-    base += __popcll(m);
-  }
-  if (lane == 0) tile_count[bh] = base;
-}
 
 // Merge of two independently normalised attention outputs by their natural
 // LSEs (lse_merge_torch, Z/cache_hub/lse_merge/lse_merge.py:79-119):
@@ -729,7 +722,7 @@ size_t workspace_bytes_for(int bs, int hq, int /*kv*/, int n_splits) {
 void launch_attn(const AttnParams& p, int bs, hipStream_t s) {
   const dim3 grid(p.n_splits, p.kv, bs);
   const Shape sh = attn_shape();
-  if (p.tile_group != nullptr) {
+  if (p.pages != nullptr) {
     kivi4_attn_kernel<8, 2, true><<<grid, 512, 0, s>>>(p);
   } else if (p.n_groups == 0) {  // bf16 rows only: the 16-byte V layout
     kivi4_attn_kernel<8, 2, false, true><<<grid, 512, 0, s>>>(p);
@@ -766,23 +759,6 @@ struct SparsePages {
   int n_sel;
 };
 
-// Sparse-mode workspace tail after the split partials: tile groups int32,
-// tile masks uint8 (both [bs * kv, n_sel]) and tile counts int32 [bs * kv].
-struct SparseLayout {
-  size_t group, mask, count, total;
-};
-
-size_t align256(size_t b) { return (b + 255) & ~static_cast<size_t>(255); }
-
-SparseLayout sparse_layout(size_t partial_bytes, int bs, int kv, int n_sel) {
-  SparseLayout L;
-  const size_t units = static_cast<size_t>(bs) * kv;
-  L.group = align256(partial_bytes);
-  L.mask = L.group + align256(units * n_sel * 4);
-  L.count = L.mask + align256(units * n_sel);
-  L.total = L.count + align256(units * 4);
-  return L;
-}
 
 // Sparse mode: every split is planned for the longest page list (n_sel
 // tiles); each wave keeps at most 64 tile descriptors in its lanes.
@@ -840,7 +816,7 @@ int attention_launch(const uint16_t* q, int64_t q_sb, int64_t q_sh, const int32_
   const SplitPlan sp = sparse ? plan_sparse_splits(bs, kv, sparse->n_sel, res_len, n_splits)
                               : plan_splits(bs, kv, n_groups, res_len, n_splits);
   const size_t partial = workspace_bytes_for(bs, hq, kv, sp.n_splits);
-  const size_t need = sparse ? sparse_layout(partial, bs, kv, sparse->n_sel).total : partial;
+  const size_t need = partial;
   if (workspace_bytes < need)
     return fail(ZKV_ESPACE, "zkv_kivi4_attention: workspace %zu < %zu bytes", workspace_bytes, need);
   AttnParams p;
@@ -875,25 +851,10 @@ int attention_launch(const uint16_t* q, int64_t q_sb, int64_t q_sh, const int32_
   p.ws_ml = p.ws_o + static_cast<size_t>(bs) * hq * sp.n_splits * 128;
   p.out = out;
   p.out_f32 = out_f32;
-  p.tile_group = nullptr;
-  p.tile_mask = nullptr;
-  p.tile_count = nullptr;
-  p.tile_cap = 0;
-  if (sparse) {
-    const SparseLayout L = sparse_layout(partial, bs, kv, sparse->n_sel);
-    uint8_t* ws = static_cast<uint8_t*>(workspace);
-    int32_t* tg = reinterpret_cast<int32_t*>(ws + L.group);
-    uint8_t* tm = ws + L.mask;
-    int32_t* tc = reinterpret_cast<int32_t*>(ws + L.count);
-    sparse_tiles_kernel<<<bs * kv, 64, 0, s>>>(sparse->pages, sparse->pg_sb, sparse->pg_sh, sparse->n_sel,
-                                              kv, n_groups, tg, tm, tc);
-    const int rc = check_launch("sparse_tiles_kernel");
-    if (rc) return rc;
-    p.tile_group = tg;
-    p.tile_mask = tm;
-    p.tile_count = tc;
-    p.tile_cap = sparse->n_sel;
-  }
+  p.pages = sparse ? sparse->pages : nullptr;
+  p.pg_sb = sparse ? sparse->pg_sb : 0;
+  p.pg_sh = sparse ? sparse->pg_sh : 0;
+  p.n_sel = sparse ? sparse->n_sel : 0;
   if (n_splits_used) *n_splits_used = sp.n_splits;
   launch_attn(p, bs, s);
   int rc = check_launch("kivi4_attn_kernel");
@@ -959,7 +920,7 @@ extern "C" size_t zkv_kivi4_sparse_attention_workspace_size(int bs, int hq, int 
                                                             int res_len, int n_splits) {
   if (bs <= 0 || kv <= 0 || hq <= 0 || n_sel < 0) return 0;
   const SplitPlan sp = plan_sparse_splits(bs, kv, n_sel, res_len, n_splits);
-  return sparse_layout(workspace_bytes_for(bs, hq, kv, sp.n_splits), bs, kv, n_sel).total;
+  return workspace_bytes_for(bs, hq, kv, sp.n_splits);
 }
 
 extern "C" int zkv_kivi4_sparse_attention(const uint16_t* q, int64_t q_sb, int64_t q_sh,
