@@ -143,3 +143,44 @@ def test_c3_full_size_selection_is_the_planted_set():
     # margin of the planted construction: >= 5% between the sets
     s = scores.sort(dim=-1, descending=True).values
     assert bool((s[..., 127] >= 1.05 * s[..., 128]).all())
+
+
+def test_c3_pipeline_graph_replays_match_eager():
+    """The C3 step (GQA mean + Quest, top-k pages, page-sparse attention)
+    captured in a HIP graph: every replay, with eager work on other inputs and
+    synchronisations in between, equals the eager result (no library call in
+    the chain records a memset)."""
+    from zoomkv_revision_amd import kivi, synthetic
+    from zoomkv_revision_amd.quest import quest_chunk_score_gqa
+    from zoomkv_revision_amd.topk import float_topk_3d
+    bs, hq, kv, n_tok, n_sel = 2, 32, 8, 4096, 24
+    ws = [synthetic.c3_workload(11 + i, bs, hq, kv, n_tok, n_sel, "cuda") for i in range(2)]
+    n_pages = ws[0]["n_pages"]
+
+    def step(w, scores, raw_q, out):
+        quest_chunk_score_gqa(w["q"], kv, w["page_min"], w["page_max"], scores, n_pages, None, raw_q)
+        sel = float_topk_3d(scores, n_sel)
+        kivi.kivi4_sparse_attention(w["q"], w["cache"], sel, out=out)
+        return sel
+
+    bufs = [(torch.empty(bs, kv, n_pages, device="cuda"), torch.empty(bs, kv, 128, dtype=torch.bfloat16, device="cuda"),
+             torch.empty(bs, hq, 128, dtype=torch.bfloat16, device="cuda")) for _ in ws]
+    eager = []
+    for w, b in zip(ws, bufs):
+        sel = step(w, *b)
+        eager.append((sel.clone(), b[2].clone()))
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        sel_g = step(ws[0], *bufs[0])
+    for rep in range(4):
+        bufs[0][2].zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(sel_g, eager[0][0]), f"replay {rep}: selection"
+        assert torch.equal(bufs[0][2], eager[0][1]), f"replay {rep}: attention output"
+        assert torch.equal(sel_g, ws[0]["planted"])
+        # eager work on the other workload between replays
+        sel1 = step(ws[1], *bufs[1])
+        torch.cuda.synchronize()
+        assert torch.equal(sel1, eager[1][0]) and torch.equal(bufs[1][2], eager[1][1])
