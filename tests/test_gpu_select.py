@@ -173,6 +173,35 @@ def test_kivi_qk_dense_sparse_bit_exact(rng, g):
     assert np.all(gs[..., nk * g:] == 7.0) and np.all(gi[..., nk * g:] == -9)
 
 
+@pytest.mark.parametrize("q_offset", [0, 1])
+def test_kivi_qk_unaligned_views(rng, q_offset):
+    """Chunk-16 scorer on sliced views: metadata rows from a larger cache, and
+    a query row starting one element (2 bytes) into its storage, which takes
+    the element-wise load path."""
+    from zoomkv_revision_amd.kivi import partial_chunk_kivi_qk_dense_sparse_cuda
+    g, bs, kv, n_chunks, nk = 16, 3, 2, 50, 41
+    keys = gaussian_bf16(rng, (bs, kv, n_chunks * g, 128), outlier_channels=4)
+    mn, mx, _, packed = encode_chunks_ref(keys, g)
+    q = gaussian_bf16(rng, (bs, kv, 128))
+    ids = rng.integers(0, n_chunks, size=(bs, kv, nk))
+    dm = rng.random((bs, kv, nk)) > 0.5
+    big_mn = torch.zeros(bs, kv + 1, n_chunks + 3, 128, dtype=torch.bfloat16, device="cuda")
+    big_mx = torch.zeros_like(big_mn)
+    big_mn[:, 1:, 2:2 + n_chunks] = to_bf16(mn)
+    big_mx[:, 1:, 2:2 + n_chunks] = to_bf16(mx)
+    q_store = torch.zeros(bs, kv, 128 + q_offset + 3, dtype=torch.bfloat16, device="cuda")
+    q_store[..., q_offset:q_offset + 128] = to_bf16(q)
+    os_ = torch.empty((bs, kv, nk * g), device="cuda")
+    oi = torch.empty((bs, kv, nk * g), dtype=torch.int64, device="cuda")
+    partial_chunk_kivi_qk_dense_sparse_cuda(
+        torch.from_numpy(ids).cuda(), torch.from_numpy(dm).cuda(), torch.from_numpy(packed).cuda(),
+        big_mn[:, 1:, 2:2 + n_chunks], big_mx[:, 1:, 2:2 + n_chunks],
+        q_store[..., q_offset:q_offset + 128], 16, 5, g, os_, oi)
+    rs, ri = osel.kivi_qk_dense_sparse(ids, dm, packed, mn, mx, q, 16, 5, g)
+    assert np.array_equal(from_torch(os_).view(np.uint32), rs.view(np.uint32))
+    assert np.array_equal(from_torch(oi), ri)
+
+
 # The reference's own top-k cases (Z/cache_hub/topk/test_float_topk.py:38-149),
 # checked here against the exact oracle instead of an overlap count.
 @pytest.mark.parametrize("case", ["basic", "k1", "k_near_length", "k_equals_length", "negative",

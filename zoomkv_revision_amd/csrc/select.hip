@@ -784,6 +784,130 @@ __global__ __launch_bounds__(128) void gqa_mean_kernel(const uint16_t* __restric
 // keep dense_topk / sparse_topk per chunk, (-1e30, 0) elsewhere.
 // One lane per token; G lanes per chunk; 256 threads per block.
 // ----------------------------------------------------------------------------
+
+// Value v of lane P of this lane's row of 16, for every lane of the row (DPP
+// row_newbcast; it folds into the consuming v_mul / v_add).  The caller keeps
+// all 16 lanes of a row active together.
+template <int P>
+__device__ __forceinline__ float row_bcast(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x150 + P, 0xF,
+                                                            0xF, true));
+}
+
+// Channels 8P..8P+7 of one token: the scale, min and query of channel 8P+j sit
+// in register j of lane P of the row, and reach every lane of the row by DPP.
+template <int P>
+struct QkRowDot {
+  static __device__ __forceinline__ float run(float acc, const uint32_t (&words)[16], const float (&sc)[8],
+                                              const float (&mn)[8], const float (&qv)[8]) {
+    uint32_t lo = words[P] & 0x0F0F0F0Fu, hi = (words[P] >> 4) & 0x0F0F0F0Fu;
+    asm volatile("" : "+v"(lo), "+v"(hi));
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float code = static_cast<float>(((j & 1 ? hi : lo) >> (8 * (j >> 1))) & 0xFFu);
+      const float kd = bf16r(bf16r(code * row_bcast<P>(sc[j])) + row_bcast<P>(mn[j]));
+      acc = acc + bf16r(kd * row_bcast<P>(qv[j]));
+    }
+    return QkRowDot<P + 1>::run(acc, words, sc, mn, qv);
+  }
+};
+template <>
+struct QkRowDot<16> {
+  static __device__ __forceinline__ float run(float acc, const uint32_t (&)[16], const float (&)[8],
+                                              const float (&)[8], const float (&)[8]) {
+    return acc;
+  }
+};
+
+// 8 consecutive bf16 values as fp32; one 16-byte load when kVec (the caller
+// has checked the address is 16-byte aligned).
+template <bool kVec>
+__device__ __forceinline__ void load8_bf16(const uint16_t* p, float (&out)[8]) {
+  if constexpr (kVec) {
+    const uint4 w = *reinterpret_cast<const uint4*>(p);
+    const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      out[2 * i] = __uint_as_float(u[i] << 16);
+      out[2 * i + 1] = __uint_as_float(u[i] & 0xFFFF0000u);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) out[i] = bf16_to_f32(p[i]);
+  }
+}
+
+// Chunks of 16 tokens: one row of 16 lanes per chunk, no LDS.  Lane l of a
+// row scores token l of the chunk and also loads channels 8l..8l+7 of the
+// chunk's min / max and of the query, which the row shares through DPP.  Same
+// arithmetic, in the same order, as kivi_qk_kernel.
+template <int T, bool kVec>
+__global__ __launch_bounds__(T) void kivi_qk_row_kernel(
+    const int64_t* __restrict__ ids, int64_t id_sb, int64_t id_sh, const uint8_t* __restrict__ dmask,
+    int64_t dm_sb, int64_t dm_sh, const int32_t* __restrict__ packed, int64_t pk_sb, int64_t pk_sh,
+    int n_packed, const uint16_t* __restrict__ cmin, const uint16_t* __restrict__ cmax, int64_t cm_sb,
+    int64_t cm_sh, int n_max, const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_sh,
+    float* __restrict__ out_s, int64_t* __restrict__ out_i, int64_t o_sb, int64_t o_sh, int nk,
+    int dense_topk, int sparse_topk) {
+  constexpr int G = 16, kChunks = T / G;
+  const int b = blockIdx.z, h = blockIdx.y;
+  const int local = threadIdx.x / G, lane = threadIdx.x % G;
+  const int slot = blockIdx.x * kChunks + local;
+  const bool valid_slot = slot < nk;  // the same for all 16 lanes of a row
+  int64_t cid = 0;
+  bool dense = false;
+  if (valid_slot) {
+    cid = ids[b * id_sb + h * id_sh + slot];
+    dense = dmask[b * dm_sb + h * dm_sh + slot] != 0;
+  }
+  const bool in_range = cid >= 0 && cid < n_packed;
+  uint32_t words[16];
+  {
+    const int32_t* w = packed + b * pk_sb + h * pk_sh + (valid_slot && in_range ? cid : 0) * (16 * G) + lane;
+#pragma unroll
+    for (int p = 0; p < 16; ++p) words[p] = static_cast<uint32_t>(w[p * G]);
+  }
+  float mn[8], mx[8], qv[8];
+  load8_bf16<kVec>(q + b * q_sb + h * q_sh + 8 * lane, qv);
+  if (valid_slot) {
+    const int64_t mrow = (b * cm_sb + h * cm_sh) + (cid >= 0 && cid < n_max ? cid : 0) * 128 + 8 * lane;
+    load8_bf16<kVec>(cmin + mrow, mn);
+    load8_bf16<kVec>(cmax + mrow, mx);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) mn[j] = mx[j] = 0.0f;
+  }
+  float sc[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) sc[j] = bf16r(bf16r(mx[j] - mn[j]) / 15.0f);
+  // every lane runs the dot (all 16 lanes of a row must be active for DPP);
+  // rows without a valid chunk discard it
+  const float acc = QkRowDot<0>::run(0.0f, words, sc, mn, qv);
+  float score = (valid_slot && in_range) ? acc : -1e30f;
+  int token = static_cast<int>(cid) * G + lane;
+#pragma unroll
+  for (int k2 = 2; k2 <= G; k2 <<= 1) {
+#pragma unroll
+    for (int j = k2 >> 1; j >= 1; j >>= 1) {
+      const float os = __shfl_xor(score, j);
+      const int ot = __shfl_xor(token, j);
+      const bool desc = (lane & k2) == 0;
+      const bool lower = (lane & j) == 0;
+      const bool swap = (desc == lower) ? (os > score) : (os < score);
+      if (swap) {
+        score = os;
+        token = ot;
+      }
+    }
+  }
+  if (valid_slot) {
+    const int64_t oi = b * o_sb + h * o_sh + static_cast<int64_t>(slot) * G + lane;
+    const int keep = dense ? dense_topk : sparse_topk;
+    out_s[oi] = lane < keep ? score : -1e30f;
+    out_i[oi] = lane < keep ? static_cast<int64_t>(token) : 0;
+  }
+}
+
 template <int G, int T>
 __global__ __launch_bounds__(T) void kivi_qk_kernel(
     const int64_t* __restrict__ ids, int64_t id_sb, int64_t id_sh, const uint8_t* __restrict__ dmask,
@@ -1070,11 +1194,27 @@ extern "C" int zkv_kivi_qk_dense_sparse(const int64_t* chunk_ids, int64_t id_sb,
 #endif
   constexpr int kT = ZKV_KIVI_QK_THREADS;  // threads per block: kT / G chunks
   if (group_size == 16) {
-    dim3 grid((nk + kT / 16 - 1) / (kT / 16), kv, bs);
-    kivi_qk_kernel<16, kT><<<grid, kT, 0, s>>>(chunk_ids, id_sb, id_sh, dense_mask, dm_sb, dm_sh,
-                                               packed_K, pk_sb, pk_sh, n_packed, chunk_min, chunk_max,
-                                               cm_sb, cm_sh, n_chunks_max, raw_q, q_sb, q_sh, out_scores,
-                                               out_indices, o_sb, o_sh, nk, dense_topk, sparse_topk);
+    // rows of 16 lanes, metadata and query in registers; 16-byte loads when
+    // every metadata / query row starts 16-byte aligned
+#ifndef ZKV_KIVI_QK_ROW_THREADS
+#define ZKV_KIVI_QK_ROW_THREADS 256
+#endif
+    constexpr int kTr = ZKV_KIVI_QK_ROW_THREADS;
+    dim3 grid((nk + kTr / 16 - 1) / (kTr / 16), kv, bs);
+    const bool vec = ((reinterpret_cast<uintptr_t>(chunk_min) | reinterpret_cast<uintptr_t>(chunk_max) |
+                       reinterpret_cast<uintptr_t>(raw_q)) & 15) == 0 &&
+                     ((cm_sb | cm_sh | q_sb | q_sh) & 7) == 0;
+#define ZKV_KIVI_QK_ROW(V)                                                                              \
+  kivi_qk_row_kernel<kTr, V><<<grid, kTr, 0, s>>>(chunk_ids, id_sb, id_sh, dense_mask, dm_sb, dm_sh,      \
+                                                packed_K, pk_sb, pk_sh, n_packed, chunk_min, chunk_max, \
+                                                cm_sb, cm_sh, n_chunks_max, raw_q, q_sb, q_sh,          \
+                                                out_scores, out_indices, o_sb, o_sh, nk, dense_topk,    \
+                                                sparse_topk)
+    if (vec)
+      ZKV_KIVI_QK_ROW(true);
+    else
+      ZKV_KIVI_QK_ROW(false);
+#undef ZKV_KIVI_QK_ROW
   } else {
     dim3 grid((nk + kT / 8 - 1) / (kT / 8), kv, bs);
     kivi_qk_kernel<8, kT><<<grid, kT, 0, s>>>(chunk_ids, id_sb, id_sh, dense_mask, dm_sb, dm_sh,
