@@ -133,9 +133,12 @@ def test_windowed_sampling_ties_at_kth_value():
 
 
 def test_production_env_matches_reference_runner(monkeypatch):
+    # setenv records each variable's prior state (set or absent), so teardown
+    # restores it whatever apply_production_env sets or pops
     for k in list(ds.PRODUCTION_ENV) + ["POLAR_FORCE_CAND_TOKENS"]:
-        monkeypatch.delenv(k, raising=False)
+        monkeypatch.setenv(k, "unset-by-test")
     ds.apply_production_env()
+    assert "POLAR_FORCE_CAND_TOKENS" not in __import__("os").environ
     import os
     assert os.environ["POLAR_QUEST_CHUNK"] == "16"
     assert os.environ["POLAR_QUEST_DYNAMIC_CAND_RATIOS"] == "0.7,0.5,0.4"

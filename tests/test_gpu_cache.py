@@ -21,6 +21,9 @@ def _make(monkeypatch, chunk, cand, dense_ratio, dense_topk, sparse_topk, **geo)
     monkeypatch.setenv("POLAR_CDS_DENSE_RATIO", str(dense_ratio))
     monkeypatch.setenv("POLAR_CDS_DENSE_TOPK", str(dense_topk))
     monkeypatch.setenv("POLAR_CDS_SPARSE_TOPK", str(sparse_topk))
+    # the cache model uses the fixed candidate ratio: pin the environment to it
+    monkeypatch.setenv("POLAR_QUEST_DYNAMIC_CAND_RATIO", "0")
+    monkeypatch.delenv("POLAR_FORCE_CAND_TOKENS", raising=False)
     g = dict(geo)
     cache = polar_cache(
         valid_start=[0] * g["bs"], layer_num=g["L"], batch_size=g["bs"], max_length=g["inp"] + g["new"],

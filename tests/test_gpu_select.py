@@ -175,9 +175,12 @@ def test_kivi_qk_dense_sparse_bit_exact(rng, g):
 
 @pytest.mark.parametrize("q_offset", [0, 1])
 def test_kivi_qk_unaligned_views(rng, q_offset):
-    """Chunk-16 scorer on sliced views: metadata rows from a larger cache, and
-    a query row starting one element (2 bytes) into its storage, which takes
-    the element-wise load path."""
+    """Chunk-16 scorer on sliced views: metadata rows from a larger cache
+    (nonzero base offset, batch / head strides of the parent), and a query
+    row inside a wider store.  q_offset = 0 keeps every query row 16-byte
+    aligned (row stride 136 elements), so the host picks the 16-byte load
+    path; q_offset = 1 starts each row 2 bytes in (row stride 137), which
+    takes the element-wise load path."""
     from zoomkv_revision_amd.kivi import partial_chunk_kivi_qk_dense_sparse_cuda
     g, bs, kv, n_chunks, nk = 16, 3, 2, 50, 41
     keys = gaussian_bf16(rng, (bs, kv, n_chunks * g, 128), outlier_channels=4)
@@ -189,7 +192,7 @@ def test_kivi_qk_unaligned_views(rng, q_offset):
     big_mx = torch.zeros_like(big_mn)
     big_mn[:, 1:, 2:2 + n_chunks] = to_bf16(mn)
     big_mx[:, 1:, 2:2 + n_chunks] = to_bf16(mx)
-    q_store = torch.zeros(bs, kv, 128 + q_offset + 3, dtype=torch.bfloat16, device="cuda")
+    q_store = torch.zeros(bs, kv, 128 + q_offset + 8, dtype=torch.bfloat16, device="cuda")
     q_store[..., q_offset:q_offset + 128] = to_bf16(q)
     os_ = torch.empty((bs, kv, nk * g), device="cuda")
     oi = torch.empty((bs, kv, nk * g), dtype=torch.int64, device="cuda")

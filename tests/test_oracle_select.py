@@ -180,6 +180,59 @@ def test_correction_factor_closed_form(rng):
     assert np.allclose(f16_to_f32(fac[:, 0]), np.linalg.norm(xx, axis=1), rtol=1e-3)
 
 
+def _vectors_with_srht_images(y: np.ndarray, signs: np.ndarray) -> np.ndarray:
+    """fp16 vectors x whose SRHT image H (signs * x) is y (up to the fp16
+    rounding of x): H H = 128 I for the Sylvester matrix, so x = signs * H y / 128."""
+    H = scipy.linalg.hadamard(128).astype(np.float64)
+    return f16_bits(((y @ H.T) / 128.0 * signs).astype(np.float32))
+
+
+def test_estimate_closed_form_on_hand_built_srht_images():
+    """est(q, k) = ||k|| ||q|| / (alpha_k alpha_q) <sign y_k, sign y_q> / 128,
+    alpha = <sign(y) / sqrt(128), y / ||y||> (the RaBitQ alignment <o_bar, o>,
+    PC:1181-1193 "weight = (r / alpha) ||k||"), computed in float64 from the
+    fp16 inputs.  The images are built by hand with sum|y| far from
+    ||y|| sqrt(128) (alpha 0.4 .. 0.9), so dropping or inverting either
+    correction moves the estimate by 10% or more, far outside the fp16
+    rounding of the stored factors."""
+    D = 128
+    sg = rabitq.srht_signs(5)
+    g = np.random.default_rng(9)
+    mags = [np.r_[np.full(8, 20.0), np.ones(120)],          # alpha ~ 0.43
+            np.r_[np.ones(64), np.full(64, 5.0)],            # alpha ~ 0.83
+            1.0 + np.arange(D) % 7,                           # alpha ~ 0.91
+            np.r_[np.full(32, 9.0), np.full(96, 1.5)],        # alpha ~ 0.68
+            np.geomspace(1.0, 40.0, D)]                       # alpha ~ 0.7
+    def build(n, scale):
+        y = np.stack([mags[i % len(mags)] * g.choice([-1.0, 1.0], size=D) for i in range(n)])
+        return _vectors_with_srht_images(y * scale[:, None], sg)
+    keys = build(12, g.uniform(0.05, 3.0, size=12))
+    qs = build(5, g.uniform(0.05, 3.0, size=5))
+    ck, fk = rabitq.encode(keys, sg)
+    cq, fq = rabitq.encode(qs, sg)
+    est = rabitq.estimate(cq, fq, ck, fk).astype(np.float64)
+
+    H = scipy.linalg.hadamard(D).astype(np.float64)
+    def parts(x16):
+        x = f16_to_f32(x16).astype(np.float64)
+        y = (x * sg) @ H.T
+        s = np.where(y >= 0, 1.0, -1.0)
+        alpha = (s / np.sqrt(D) * (y / np.linalg.norm(y, axis=1, keepdims=True))).sum(1)
+        return np.linalg.norm(x, axis=1), alpha, s
+    nk, ak, sk = parts(keys)
+    nq, aq, sq = parts(qs)
+    assert np.all(ak < 0.92) and np.all(aq < 0.92) and ak.min() < 0.5
+    dots = sq @ sk.T / D
+    expected = nq[:, None] * nk[None, :] / (aq[:, None] * ak[None, :]) * dots
+    tol = 4e-3 * np.abs(expected) + 1e-9
+    assert np.all(np.abs(est - expected) <= tol)
+    # the same check rejects the plausible mistakes (self-test of its power)
+    for wrong in (expected * ak[None, :], expected * aq[:, None],                 # a correction dropped
+                  expected * ak[None, :] ** 2, expected * aq[:, None] ** 2,       # a correction inverted
+                  nq[:, None] * nk[None, :] * dots):                             # both dropped
+        assert not np.all(np.abs(est - wrong) <= 4e-3 * np.abs(wrong) + 1e-9)
+
+
 def test_estimate_tracks_inner_product_and_exact_rerank(rng):
     keys = rabitq.clustered_unit_keys(rng, 4096, 16)
     qs = rabitq.clustered_unit_keys(rng, 4, 16)
