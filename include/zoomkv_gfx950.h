@@ -80,11 +80,21 @@ int zkv_chunk_encode(const uint16_t* keys, int64_t k_sb, int64_t k_sh, int64_t k
  * zkv_kivi4_pack quantizes tokens [32*g0, 32*(g0+n_groups)) of the cache
  * from src tokens [0, 32*n_groups) of k / v.
  * k, v     bf16 [bs, kv, n_tok, 128], strides (sb, sh, st), channel stride 1
+ * range_status  (nullable) device uint32 the kernel ORs ZKV_RANGE_* bits into
+ *          when a group's fp16 scale / zero cannot hold its values: ZKV_RANGE_K
+ *          / ZKV_RANGE_V for a scale or zero beyond fp16 (|value| or range >
+ *          65504), ZKV_RANGE_V_SCALE for a V scale above 2048 (a V range above
+ *          30720 inside one 32-channel group, beyond the decode kernel's fp16
+ *          V operand).  The caller clears it first; the packed records of a
+ *          flagged call must not be attended.
  * ------------------------------------------------------------------------ */
+#define ZKV_RANGE_K 1u
+#define ZKV_RANGE_V 2u
+#define ZKV_RANGE_V_SCALE 4u
 int zkv_kivi4_pack(const uint16_t* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
                    const uint16_t* v, int64_t v_sb, int64_t v_sh, int64_t v_st,
                    int bs, int kv, int n_groups, int g0, int g_cap, int32_t* groups,
-                   zkv_stream_t stream);
+                   uint32_t* range_status, zkv_stream_t stream);
 
 /* ------------------------------------------------------------------------
  * Fused 4-bit decode attention over a Format Q cache plus a bf16 residual

@@ -111,3 +111,66 @@ def test_gather_attention_matches_gathered_oracle(rng, n_idx, tail_start, tail_l
             ref[b, h * g:(h + 1) * g], rlse[b, h * g:(h + 1) * g] = o[0], l[0]
     assert np.abs(from_torch(out)[:, 0] - ref).max() <= ATOL + np.abs(ref).max() * 2 ** -8
     assert np.allclose(from_torch(lse)[..., 0], rlse, rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.parametrize("bs,hq,kv,n,splits", [(2, 32, 8, 420, 0), (1, 32, 8, 930, 0), (1, 16, 1, 2000, 3),
+                                               (3, 8, 2, 1, 0)])
+def test_bf16_attention_fp32_output_strict(rng, bs, hq, kv, n, splits):
+    """The unrounded (fp32) output of flash_attn_with_kvcache_compat within the
+    north star's 2e-3 of the float64 oracle, with no bf16 output slack."""
+    from zoomkv_revision_amd.attention import flash_attn_with_kvcache_compat
+    q = gaussian_bf16(rng, (bs, hq, 128))
+    k = gaussian_bf16(rng, (bs, kv, n, 128), outlier_channels=2)
+    v = gaussian_bf16(rng, (bs, kv, n, 128))
+    out = torch.empty(bs, 1, hq, 128, dtype=torch.float32, device="cuda")
+    flash_attn_with_kvcache_compat(to_bf16(q).unsqueeze(1), to_bf16(k).transpose(1, 2),
+                                   to_bf16(v).transpose(1, 2), out=out, n_splits=splits)
+    ref = okivi.attention(q, k, v, 1 / np.sqrt(128))
+    err = np.abs(from_torch(out)[:, 0] - ref).max()
+    assert err <= ATOL, f"max abs err {err}"
+
+
+@pytest.mark.parametrize("n_idx,tail_start,tail_len", [(100, 300, 40), (612, 400, 100)])
+def test_gather_attention_fp32_output_strict(rng, n_idx, tail_start, tail_len):
+    from zoomkv_revision_amd.attention import gather_attention
+    bs, hq, kv, rows = 2, 32, 8, 1000
+    q = gaussian_bf16(rng, (bs, hq, 128))
+    k = gaussian_bf16(rng, (bs, kv, rows, 128), outlier_channels=2)
+    v = gaussian_bf16(rng, (bs, kv, rows, 128))
+    idx = rng.integers(0, rows, size=(bs, kv, n_idx))
+    out = torch.empty(bs, 1, hq, 128, dtype=torch.float32, device="cuda")
+    gather_attention(to_bf16(q).unsqueeze(1), to_bf16(k), to_bf16(v), torch.from_numpy(idx).cuda(),
+                     tail_start, tail_len, out=out)
+    g = hq // kv
+    ref = np.zeros((bs, hq, 128))
+    for b in range(bs):
+        for h in range(kv):
+            sel = list(idx[b, h]) + list(range(tail_start, tail_start + tail_len))
+            ref[b, h * g:(h + 1) * g] = okivi.attention(q[b:b + 1, h * g:(h + 1) * g], k[b, h, sel][None, None],
+                                                        v[b, h, sel][None, None], 1 / np.sqrt(128))[0]
+    err = np.abs(from_torch(out)[:, 0] - ref).max()
+    assert err <= ATOL, f"max abs err {err}"
+
+
+def test_bf16_attention_values_beyond_fp16(rng):
+    """bf16 K / V enter the bf16 matrix cores unconverted: values far outside
+    fp16's range (|K| up to 3e5, |V| up to 7e4) give finite outputs that match
+    the float64 oracle to 2e-3 relative to the value scale."""
+    from zoomkv_revision_amd.attention import flash_attn_with_kvcache_compat
+    from oracle.numerics import bf16r
+    bs, hq, kv, n = 2, 16, 4, 300
+    q = gaussian_bf16(rng, (bs, hq, 128))
+    k = gaussian_bf16(rng, (bs, kv, n, 128))
+    v = gaussian_bf16(rng, (bs, kv, n, 128))
+    k[0, 1, 17, 5] = bf16r(np.float32(3.0e5))      # one token's key far outside fp16
+    k[1, 2, 200, 9] = bf16r(np.float32(-9.0e4))
+    v[0, 1, 17, :] = bf16r(np.linspace(-7.0e4, 7.0e4, 128, dtype=np.float32))
+    v[1, 3, 33, 40] = bf16r(np.float32(1.0e5))
+    out = torch.empty(bs, 1, hq, 128, dtype=torch.float32, device="cuda")
+    flash_attn_with_kvcache_compat(to_bf16(q).unsqueeze(1), to_bf16(k).transpose(1, 2),
+                                   to_bf16(v).transpose(1, 2), out=out)
+    got = from_torch(out)[:, 0]
+    ref = okivi.attention(q, k, v, 1 / np.sqrt(128))
+    assert np.isfinite(got).all()
+    scale = np.maximum(1.0, np.abs(ref).max(axis=-1, keepdims=True))        # per (batch, query head)
+    assert np.all(np.abs(got - ref) <= ATOL * scale)

@@ -1,0 +1,77 @@
+"""Configuration C2 at the shape its benchmark line is quoted on: batch 16,
+32 / 8 heads, 32640 4-bit tokens (1020 groups of 32) + a 128-token bf16
+residual window, 1% outlier K channels x10 -- the bench's first cache (seed
+1234) and its query rows (seed 42).
+
+* the pack of one whole sequence is bit-exact against the oracle's Format Q
+  quantization of the same bf16 K / V;
+* the fused attention (fp32 output, the automatic split plan) is within the
+  north star's 2e-3 of the float64 oracle over the cache's records, for 4 of
+  the 16 sequences and all 32 query heads;
+* the automatic split plan and a single split agree within 1e-3 on all 16
+  sequences (the splits differ only in fp16 rounding of P relative to each
+  split's running max)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import kivi as okivi
+from tests.helpers import from_torch
+
+pytestmark = pytest.mark.gpu
+
+B, HQ, HKV, NG, R = 16, 32, 8, 1020, 128
+ROWS = (0, 5, 10, 15)
+
+
+@pytest.fixture(scope="module")
+def c2():
+    from zoomkv_revision_amd import synthetic
+    dev = torch.device("cuda:0")
+    cache, kept = synthetic.c2_cache(1234, B, HKV, NG, R, dev, keep_rows=(0,))
+    q = synthetic.c2_query(B, HQ, dev)
+    torch.cuda.synchronize()
+    yield cache, kept, q
+    del cache
+
+
+def _oracle_cache(cache, b):
+    """The GPU cache's records of sequence b as the oracle's Format Q arrays."""
+    f16 = lambda t: t.cpu().view(torch.int16).numpy().view(np.uint16)
+    return okivi.Kivi4Cache(cache.k_codes[b:b + 1].cpu().numpy(), f16(cache.k_meta[b:b + 1]),
+                            cache.v_codes[b:b + 1].cpu().numpy(), f16(cache.v_meta[b:b + 1]))
+
+
+def test_c2_full_shape_pack_bit_exact(c2):
+    cache, kept, _ = c2
+    k, v = kept[0]
+    ref = okivi.quantize_kivi4(k, v)
+    got = _oracle_cache(cache, 0)
+    for name in ("k_codes", "k_meta", "v_codes", "v_meta"):
+        assert np.array_equal(getattr(got, name), getattr(ref, name)), name
+
+
+def test_c2_full_shape_attention_matches_oracle(c2):
+    from zoomkv_revision_amd import kivi
+    cache, _, q = c2
+    out = from_torch(kivi.kivi4_decode_attention(q, cache, NG, R, out_dtype=torch.float32))
+    qn = q.float().cpu().numpy()
+    kr, vr = cache.k_res.float().cpu().numpy(), cache.v_res.float().cpu().numpy()
+    for b in ROWS:
+        ref = okivi.kivi4_decode_attention(qn[b:b + 1], _oracle_cache(cache, b), NG, kr[b:b + 1], vr[b:b + 1], R,
+                                           1 / np.sqrt(128))
+        err = np.abs(out[b:b + 1] - ref).max()
+        print(f"[c2 full] sequence {b}: max abs err {err:.3e}", flush=True)
+        assert err <= 2e-3, f"sequence {b}: max abs err {err}"
+
+
+def test_c2_full_shape_split_plans_agree(c2):
+    from zoomkv_revision_amd import kivi
+    cache, _, q = c2
+    ws = kivi.attention_workspace(B, HQ, HKV, NG, R, 0)
+    _, used = kivi.kivi4_attention_partial(q, cache, NG, R, workspace=ws)
+    assert used > 1                                   # the headline plan splits the context
+    auto = from_torch(kivi.kivi4_decode_attention(q, cache, NG, R, out_dtype=torch.float32))
+    one = from_torch(kivi.kivi4_decode_attention(q, cache, NG, R, out_dtype=torch.float32, n_splits=1))
+    assert np.isfinite(auto).all() and np.isfinite(one).all()
+    assert np.abs(auto - one).max() <= 1e-3

@@ -218,3 +218,75 @@ def test_c1_full_shape_pack_and_attention():
     ref = okivi.kivi4_decode_attention(q, ref_cache, ng, k[:, :, nq:], v[:, :, nq:], res, 1 / np.sqrt(128))
     err = np.abs(from_torch(out) - ref).max()
     assert err <= ATOL, f"max abs err {err}"
+
+
+def test_kivi4_pack_reports_values_beyond_the_fp16_format(rng):
+    """Format Q stores each group's scale and zero point (its minimum) in
+    fp16: a minimum below -65504 or a V scale above the decode kernel's 2048
+    (16 * P * scale must stay inside fp16) makes the pack raise instead of
+    storing inf, which the attention would turn into NaN.  A maximum above
+    65504 is fine: only min and (max - min) / 15 are stored, and the
+    attention then matches the oracle."""
+    zk = _zk()
+    bs, hq, kv, ng = 1, 8, 2, 3
+    k0 = gaussian_bf16(rng, (bs, kv, ng * 32, 128), outlier_channels=1)
+    v0 = gaussian_bf16(rng, (bs, kv, ng * 32, 128))
+    cache = zk.Kivi4Cache.allocate(bs, kv, ng)
+    cases = [("K", "K scale or zero point"), ("V", "V scale or zero point"), ("Vrange", "V scale above 2048")]
+    for which, msg in cases:
+        k, v = k0.copy(), v0.copy()
+        if which == "K":
+            k[0, 1, 50, 7] = -7.0e4
+        elif which == "V":
+            v[0, 0, 40, 70] = -7.0e4
+        else:                                    # range 40000 inside one 32-channel group
+            v[0, 1, 40, 64:96] = np.linspace(-2.0e4, 2.0e4, 32, dtype=np.float32)
+        with pytest.raises(RuntimeError, match=msg):
+            zk.kivi4_pack(to_bf16(k), to_bf16(v), cache, 0)
+    from oracle.numerics import bf16r
+    k = k0.copy()
+    k[0, 1, 50, 7] = bf16r(np.float32(7.0e4))   # a maximum beyond fp16: representable
+    assert zk.kivi4_pack(to_bf16(k), to_bf16(v0), cache, 0) == ng
+    ref_cache = okivi.quantize_kivi4(k, v0)
+    assert np.array_equal(from_torch(cache.k_meta), ref_cache.k_meta)
+    q = gaussian_bf16(rng, (bs, hq, 128))
+    out = from_torch(zk.kivi4_decode_attention(to_bf16(q), cache, ng, 0, out_dtype=torch.float32))
+    z = np.zeros((bs, kv, 0, 128), np.float32)
+    ref = okivi.kivi4_decode_attention(q, ref_cache, ng, z, z, 0, 1 / np.sqrt(128))
+    assert np.isfinite(out).all() and np.abs(out - ref).max() <= ATOL
+
+
+@pytest.mark.parametrize("dominant", [False, True])
+def test_decode_attention_large_v_group(rng, dominant):
+    """One token's 32-channel V group spans [-2500, 2500] (fp16 scale 333,
+    beyond the 255 that 16 * P * scale allowed with probabilities up to 2^4):
+    the output stays finite and within 2e-3 of the oracle relative to half
+    the value range, whether that token carries little weight or dominates
+    the softmax."""
+    zk = _zk()
+    bs, hq, kv, ng, res = 1, 8, 2, 6, 20
+    k = gaussian_bf16(rng, (bs, kv, ng * 32, 128), outlier_channels=1)
+    v = gaussian_bf16(rng, (bs, kv, ng * 32, 128))
+    q = gaussian_bf16(rng, (bs, hq, 128))
+    tok = 77
+    v[0, 1, tok, 32:64] = np.linspace(-2500.0, 2500.0, 32, dtype=np.float32)
+    if dominant:                                  # K row along the group's mean query: top score
+        from oracle.numerics import bf16r
+        qm = q[0, 4:8].mean(0)
+        k[0, 1, tok] = bf16r(qm / np.linalg.norm(qm) * np.float32(20.0))
+    cache = zk.Kivi4Cache.allocate(bs, kv, ng, 32)
+    zk.kivi4_pack(to_bf16(k), to_bf16(v), cache, 0)
+    kr = gaussian_bf16(rng, (bs, kv, 32, 128))
+    vr = gaussian_bf16(rng, (bs, kv, 32, 128))
+    cache.k_res.copy_(to_bf16(kr))
+    cache.v_res.copy_(to_bf16(vr))
+    out = from_torch(zk.kivi4_decode_attention(to_bf16(q), cache, ng, res, out_dtype=torch.float32))
+    ref = okivi.kivi4_decode_attention(q, okivi.quantize_kivi4(k, v), ng, kr, vr, res, 1 / np.sqrt(128))
+    assert np.isfinite(out).all()
+    tol = ATOL * max(1.0, 5000.0 / 2)
+    err = np.abs(out - ref).max()
+    assert err <= tol, f"max abs err {err} (tol {tol})"
+    # the heads of the other KV head see ordinary values: the plain bound holds there
+    assert np.abs(out[:, :4] - ref[:, :4]).max() <= ATOL
+    if dominant:
+        assert np.abs(ref[0, 4:8, 32:64]).max() > 1000.0      # the planted token does dominate

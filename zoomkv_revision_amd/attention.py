@@ -32,14 +32,27 @@ def _workspace(device, nbytes: int) -> torch.Tensor:
     return ws
 
 
+def _check_out(out: torch.Tensor | None, q: torch.Tensor, bs: int, hq: int) -> torch.Tensor:
+    """The caller's output buffer ([bs, 1, hq, 128], contiguous, q's dtype or
+    float32 for an unrounded result), or a new one in q's dtype."""
+    if out is None:
+        return torch.empty(bs, 1, hq, HEAD_DIM, dtype=q.dtype, device=q.device)
+    if out.dtype not in (q.dtype, torch.float32) or not out.is_contiguous() or out.numel() != bs * hq * HEAD_DIM \
+            or out.device != q.device:
+        raise ValueError("out must be a contiguous [bs, 1, hq, 128] tensor of q's dtype or float32 on q's device")
+    return out
+
+
 def flash_attn_with_kvcache_compat(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                                    causal: bool = False, softmax_scale: float | None = None,
                                    return_softmax_lse: bool = False, out: torch.Tensor | None = None,
                                    n_splits: int = 0, **kwargs):
     """softmax(q K^T * scale) V for one query token per sequence.
 
-    Returns out [bs, 1, hq, 128] in q's dtype (bf16), and with
-    ``return_softmax_lse`` also the fp32 LSE [bs, hq, 1].
+    Returns out [bs, 1, hq, 128] in q's dtype (bf16; a float32 ``out`` buffer
+    receives the unrounded result), and with ``return_softmax_lse`` also the
+    fp32 LSE [bs, hq, 1].  K and V enter the matrix cores as stored (bf16),
+    so every finite bf16 value is supported.
     """
     if kwargs:
         raise NotImplementedError(f"flash_attn_with_kvcache_compat: unsupported arguments {sorted(kwargs)}")
@@ -63,10 +76,7 @@ def flash_attn_with_kvcache_compat(q: torch.Tensor, k_cache: torch.Tensor, v_cac
     if v_cache.stride(-1) != 1 or any(s % 8 for s in v_cache.stride()[:3]) or v_cache.data_ptr() % 16:
         v_cache = v_cache.contiguous()
     scale = 1.0 / math.sqrt(HEAD_DIM) if softmax_scale is None else float(softmax_scale)
-    if out is None:
-        out = torch.empty(bs, 1, hq, HEAD_DIM, dtype=q.dtype, device=q.device)
-    elif out.dtype != q.dtype or not out.is_contiguous() or out.numel() != bs * hq * HEAD_DIM:
-        raise ValueError("out must be a contiguous bf16 [bs, 1, hq, 128] tensor")
+    out = _check_out(out, q, bs, hq)
     lse = torch.empty(bs, hq, 1, dtype=torch.float32, device=q.device) if return_softmax_lse else None
     L = lib()
     ws = _workspace(q.device, L.zkv_bf16_attention_workspace_size(bs, hq, kv, n, n_splits))
@@ -74,7 +84,8 @@ def flash_attn_with_kvcache_compat(q: torch.Tensor, k_cache: torch.Tensor, v_cac
         ptr(q3), q3.stride(0), q3.stride(1),
         ptr(k_cache), k_cache.stride(0), k_cache.stride(1), k_cache.stride(2),
         ptr(v_cache), v_cache.stride(0), v_cache.stride(1), v_cache.stride(2),
-        bs, hq, kv, n, scale, ptr(out), 0, ptr(lse), n_splits, ptr(ws), ws.numel(), stream_of(q)))
+        bs, hq, kv, n, scale, ptr(out), int(out.dtype == torch.float32), ptr(lse), n_splits, ptr(ws),
+        ws.numel(), stream_of(q)))
     return (out, lse) if return_softmax_lse else out
 
 
@@ -113,8 +124,7 @@ def gather_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, idx: tor
     if q3.stride(-1) != 1 or q3.stride(1) % 8 or q3.stride(0) % 8 or q3.data_ptr() % 16:
         q3 = q3.contiguous()
     scale = 1.0 / math.sqrt(HEAD_DIM) if softmax_scale is None else float(softmax_scale)
-    if out is None:
-        out = torch.empty(bs, 1, hq, HEAD_DIM, dtype=q.dtype, device=q.device)
+    out = _check_out(out, q, bs, hq)
     lse = torch.empty(bs, hq, 1, dtype=torch.float32, device=q.device) if return_softmax_lse else None
     L = lib()
     ws = _workspace(q.device, L.zkv_bf16_attention_workspace_size(bs, hq, kv, n_idx + tail_len, n_splits))
@@ -122,7 +132,8 @@ def gather_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, idx: tor
         ptr(q3), q3.stride(0), q3.stride(1),
         ptr(k), k.stride(0), k.stride(2), k.stride(1), ptr(v), v.stride(0), v.stride(2), v.stride(1),
         n_rows, ptr(idx), idx.stride(0) if idx is not None else 0, idx.stride(1) if idx is not None else 0,
-        n_idx, int(tail_start), int(tail_len), bs, hq, kv, scale, ptr(out), 0, ptr(lse), n_splits,
+        n_idx, int(tail_start), int(tail_len), bs, hq, kv, scale, ptr(out), int(out.dtype == torch.float32),
+        ptr(lse), n_splits,
         ptr(ws), ws.numel(), stream_of(q)))
     return (out, lse) if return_softmax_lse else out
 

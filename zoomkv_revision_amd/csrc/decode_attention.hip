@@ -167,22 +167,21 @@ __device__ __forceinline__ float wave_max16(float x) {
 }
 
 // A running max is kept while a tile's max exceeds it by at most this many
-// base-2 units (probabilities up to 2^4 in fp16, exact in relative terms);
-// O, L and OZ are rescaled only when some lane's max jumps further.  The
-// bound also keeps the V-side products 16 * P * scale inside fp16 for scales
-// up to 255 (V ranges up to 3800).
-constexpr float kLazyMaxBits = 4.0f;
+// base-2 units (probabilities up to 2^0.5); O, L and OZ are rescaled only when
+// some lane's max jumps further.  The bound keeps the quantized tiles' V-side
+// products 16 * P * scale inside fp16 for every V scale up to 2048 (a V range
+// of 30720 inside one 32-channel group; the pack reports larger ones).
+constexpr float kLazyMaxBits = 0.5f;
 
 // Online-softmax update for one tile.  The raw score of token TAU[g][e] for
 // query head c is S * sc + bias (masked tokens have S = -inf); qs turns a raw
 // score into a base-2 exponent and qsc = qs * sc.  m_run is kept in raw
-// units.  Returns P as the fp16 B operand of the V-MFMA; L accumulates sum(P)
-// with a ones-row MFMA on that same fp16 P (every row of L holds the column
-// sum).  v_exp_f32 flushes results below 2^-126 to zero, which only drops
-// probabilities that are already far below fp16 resolution.
-__device__ __forceinline__ half8_t softmax_step(const float4_t S[2], float sc, float bias, float qs,
-                                                float qsc, float& m_run, float4_t& L, float4_t O[8],
-                                                float4_t& OZ) {
+// units.  Returns the fp32 probabilities P of the lane's 8 tokens relative to
+// the (possibly updated) running max.  v_exp_f32 flushes results below 2^-126
+// to zero, which only drops probabilities far below every operand's resolution.
+__device__ __forceinline__ void softmax_probs(const float4_t S[2], float sc, float bias, float qs,
+                                              float qsc, float& m_run, float4_t& L, float4_t O[8],
+                                              float4_t& OZ, float pr[8]) {
   float sv[8];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -203,12 +202,48 @@ __device__ __forceinline__ half8_t softmax_step(const float4_t S[2], float sc, f
     for (int j = 0; j < 8; ++j) O[j] *= alpha;
   }
   const float b2 = (bias - m_run) * qs;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) pr[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[e], qsc, b2));
+}
+
+// The quantized tiles' P: one fp16 operand; L accumulates sum(P) with a
+// ones-row MFMA on that same fp16 P (every row of L holds the column sum).
+__device__ __forceinline__ half8_t softmax_step(const float4_t S[2], float sc, float bias, float qs,
+                                                float qsc, float& m_run, float4_t& L, float4_t O[8],
+                                                float4_t& OZ) {
+  float pr[8];
+  softmax_probs(S, sc, bias, qs, qsc, m_run, L, O, OZ, pr);
   half8_t pb;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) pb[e] = static_cast<_Float16>(__builtin_amdgcn_exp2f(__builtin_fmaf(sv[e], qsc, b2)));
+  for (int e = 0; e < 8; ++e) pb[e] = static_cast<_Float16>(pr[e]);
   const half8_t ones = {1, 1, 1, 1, 1, 1, 1, 1};
   L = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pb, L, 0, 0, 0);
   return pb;
+}
+
+// The bf16 tiles' P as a bf16 pair hi + lo (hi = bf16(P), lo = bf16(P - hi);
+// the difference is exact in fp32), so P keeps 16 significant bits through
+// the bf16 matrix cores; L sums both with ones-row MFMAs.
+// S is q . K (q unscaled); the running max keeps the quantized tiles' raw
+// units (q / 8), so the raw score is S / 8.
+__device__ __forceinline__ void softmax_step_bf16(const float4_t S[2], float qs, float& m_run,
+                                                  float4_t& L, float4_t O[8], float4_t& OZ,
+                                                  bf16x8_t& phi, bf16x8_t& plo) {
+  float pr[8];
+  softmax_probs(S, 0.125f, 0.0f, qs, qs * 0.125f, m_run, L, O, OZ, pr);
+#pragma unroll
+  for (int e = 0; e < 8; e += 2) {
+    const bf16x2_t h2 = __builtin_convertvector(float2_t{pr[e], pr[e + 1]}, bf16x2_t);
+    const float2_t hf = __builtin_convertvector(h2, float2_t);
+    const bf16x2_t l2 = __builtin_convertvector(float2_t{pr[e] - hf[0], pr[e + 1] - hf[1]}, bf16x2_t);
+    phi[e] = h2[0];
+    phi[e + 1] = h2[1];
+    plo[e] = l2[0];
+    plo[e + 1] = l2[1];
+  }
+  const bf16x8_t ones = __builtin_bit_cast(bf16x8_t, u32x4_t{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
+  L = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, phi, L, 0, 0, 0);
+  L = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, plo, L, 0, 0, 0);
 }
 
 constexpr float kTwo20 = 1048576.0f;
@@ -297,22 +332,24 @@ __device__ __forceinline__ int bf16_row(const AttnParams& p, const int64_t* idx_
   return p.tail_start + (t - p.n_idx);
 }
 
-// One bf16 tile: tokens [base, base + valid) of the list.  Lane (c, g) loads
-// K rows of tokens c and c + 16 (the K-MFMA A rows) and V rows of tokens
-// TAU[g][e] (its V-MFMA k-slice), 16 B per row.
-// kBf16Only (no quantized tile in the kernel): M-tile j of the V-MFMA is
-// channel 8c + j for A row c instead of the quantized tiles' order, so each
-// V row is one 16-byte load per lane; O[j][i] of lane (c, g) is then channel
-// 32g + 8i + j.
+// One bf16 tile: tokens [base, base + valid) of the list, on the bf16 matrix
+// cores (K and V enter as stored: no conversion, any bf16 value).  Lane (c, g)
+// loads the K rows of tokens c and c + 16 (the K-MFMA A rows, dims
+// 8(4s+g) .. +7 in order, against the query qN in the same order) and the V
+// rows of tokens TAU[g][e] (its V-MFMA k-slice), 16 B per row.
+// M-tile j of the V-MFMA, row c: channel 32(j/2) + 2c + j%2 (the quantized
+// tiles' order: dword 16(j/2) + c of the row, half j%2), or, when kBf16Only
+// (no quantized tile in the kernel), channel 8c + j (dword 4c + j/2, half
+// j%2) so that each V row is one 16-byte load per lane; O[j][i] of lane
+// (c, g) is then channel 32g + 8i + j.
 template <bool kBf16Only>
 __device__ __forceinline__ void residual_tile(const AttnParams& p, int b, int h, int base, int valid,
-                                              int c, int g, const half8_t qB[4], float qs,
+                                              int c, int g, const bf16x8_t qN[4], float qs,
                                               float& m_run, float4_t& L, float4_t O[8],
                                               float4_t& OZ) {
   const uint16_t* kr = p.k_res + b * p.kr_sb + h * p.kr_sh;
   const uint16_t* vr = p.v_res + b * p.vr_sb + h * p.vr_sh;
   const int64_t* idx_bh = p.res_idx ? p.res_idx + b * p.ri_sb + h * p.ri_sh : nullptr;
-  constexpr int kslot[8] = {0, 4, 1, 5, 2, 6, 3, 7};
   int krow[2], vrow[8];
 #pragma unroll
   for (int m = 0; m < 2; ++m) krow[m] = c + 16 * m < valid ? bf16_row(p, idx_bh, base + c + 16 * m) : -1;
@@ -348,39 +385,30 @@ __device__ __forceinline__ void residual_tile(const AttnParams& p, int b, int h,
   if constexpr (kBf16Only) load_v();
   float4_t S[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
+  for (int s = 0; s < 4; ++s)
 #pragma unroll
-    for (int m = 0; m < 2; ++m) {
-      const u32x4_t raw = kx[s][m];
-      half8_t a;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const uint32_t wv = raw[kslot[e] >> 1];
-        a[e] = static_cast<_Float16>(__uint_as_float((kslot[e] & 1) ? (wv & 0xFFFF0000u) : (wv << 16)));
-      }
-      S[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qB[s], S[m], 0, 0, 0);
-    }
-  }
+    for (int m = 0; m < 2; ++m)
+      S[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kx[s][m]), qN[s], S[m], 0, 0, 0);
   // S[m][i] is token 4g + i + 16m = TAU[g][i + 4m]
 #pragma unroll
   for (int m = 0; m < 2; ++m)
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       if (vrow[i + 4 * m] < 0) S[m][i] = -INFINITY;
-  const half8_t pb = softmax_step(S, 1.0f, 0.0f, qs, qs, m_run, L, O, OZ);
-  // V^T operand: element e = token TAU[g][e]; row c of M-tile j = channel
-  // 32(j/2) + 2c + j%2 (the quantized tiles' row order: dword 16(j/2) + c of
-  // the row, half j%2), or 8c + j when kBf16Only (dword c*4 + j/2, half j%2)
+  bf16x8_t phi, plo;
+  softmax_step_bf16(S, qs, m_run, L, O, OZ, phi, plo);
   if constexpr (!kBf16Only) load_v();
+  // V^T operand of M-tile j: element e = half j%2 of dword j/2 of token
+  // TAU[g][e]'s loaded row (v_perm_b32 picks the halves of a token pair)
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    half8_t a;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const uint32_t wv = vx[e][j >> 1];
-      a[e] = static_cast<_Float16>(__uint_as_float((j & 1) ? (wv & 0xFFFF0000u) : (wv << 16)));
-    }
-    O[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb, O[j], 0, 0, 0);
+    const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+    const u32x4_t a = {__builtin_amdgcn_perm(vx[1][j >> 1], vx[0][j >> 1], sel),
+                       __builtin_amdgcn_perm(vx[3][j >> 1], vx[2][j >> 1], sel),
+                       __builtin_amdgcn_perm(vx[5][j >> 1], vx[4][j >> 1], sel),
+                       __builtin_amdgcn_perm(vx[7][j >> 1], vx[6][j >> 1], sel)};
+    O[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), phi, O[j], 0, 0, 0);
+    O[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), plo, O[j], 0, 0, 0);
   }
 }
 
@@ -476,59 +504,67 @@ void kivi4_attn_kernel(const AttnParams p) {
       ++issued;
     }
 
-  // ---- q as the K-MFMA B operand (element e of block 4s+g = channel 8(4s+g)+KSLOT[e]) ----
-  TileConsts tc;
-  half8_t (&qB)[4] = tc.qB;
-  {
-    const uint16_t* qp = p.q + b * p.q_sb + static_cast<int64_t>(h * p.gqa + (col_ok ? c : 0)) * p.q_sh;
-    constexpr int kslot[8] = {0, 4, 1, 5, 2, 6, 3, 7};
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const u32x4_t raw = ld16(qp + 8 * (4 * s + g));
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const uint32_t wv = raw[kslot[e] >> 1];
-        const float x = __uint_as_float((kslot[e] & 1) ? (wv & 0xFFFF0000u) : (wv << 16));
-        qB[s][e] = static_cast<_Float16>(col_ok ? x * 0.125f : 0.0f);
-      }
-    }
-  }
-  {
-    const half8_t inv16 = {1, 1, 0.0625, 0.0625, 1, 1, 0.0625, 0.0625};
-#pragma unroll
-    for (int s = 0; s < 4; ++s) tc.qBm[s] = qB[s] * inv16;
-    tc.qs = p.qscale;
-    tc.qs24 = p.qscale * kTwo24;
-  }
-
   float4_t O[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) O[j] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
   float4_t OZ = {0.0f, 0.0f, 0.0f, 0.0f};
   float m_run = kNegBig;
   float4_t L = {0.0f, 0.0f, 0.0f, 0.0f};
+  const uint16_t* qp = p.q + b * p.q_sb + static_cast<int64_t>(h * p.gqa + (col_ok ? c : 0)) * p.q_sh;
 
-  // ---- quantized tiles through this wave's D-stage LDS ring ----
-  for (int k = 0; k < nq; ++k) {
-    if (issued < nq) {
-      issue_tile(p, bh, group_of(issued), lane, ring[issued % D]);
-      ++issued;
+  if constexpr (!kBf16Only) {
+    // ---- q as the K-MFMA B operand (element e of block 4s+g = channel 8(4s+g)+KSLOT[e]) ----
+    TileConsts tc;
+    {
+      constexpr int kslot[8] = {0, 4, 1, 5, 2, 6, 3, 7};
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const u32x4_t raw = ld16(qp + 8 * (4 * s + g));
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t wv = raw[kslot[e] >> 1];
+          const float x = __uint_as_float((kslot[e] & 1) ? (wv & 0xFFFF0000u) : (wv << 16));
+          tc.qB[s][e] = static_cast<_Float16>(col_ok ? x * 0.125f : 0.0f);
+        }
+      }
+      const half8_t inv16 = {1, 1, 0.0625, 0.0625, 1, 1, 0.0625, 0.0625};
+#pragma unroll
+      for (int s = 0; s < 4; ++s) tc.qBm[s] = tc.qB[s] * inv16;
+      tc.qs = p.qscale;
+      tc.qs24 = p.qscale * kTwo24;
     }
-    const uint32_t half_mask = kSparse ? static_cast<uint32_t>(__builtin_amdgcn_readlane(my_mask, k)) : 3u;
-    wait_tiles_in_flight(issued - 1 - k);
-    compute_tile(ring[k % D], lane, c, g, tc, half_mask, m_run, L, O, OZ);
+
+    // ---- quantized tiles through this wave's D-stage LDS ring ----
+    for (int k = 0; k < nq; ++k) {
+      if (issued < nq) {
+        issue_tile(p, bh, group_of(issued), lane, ring[issued % D]);
+        ++issued;
+      }
+      const uint32_t half_mask = kSparse ? static_cast<uint32_t>(__builtin_amdgcn_readlane(my_mask, k)) : 3u;
+      wait_tiles_in_flight(issued - 1 - k);
+      compute_tile(ring[k % D], lane, c, g, tc, half_mask, m_run, L, O, OZ);
+    }
+    // O to real units: O * 2^20 + sum P z of the M-tile's group (OZ component
+    // i = row 4g + i holds group i's sum; M-tile j lies in group j / 2)
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) O[j][i] = __builtin_fmaf(O[j][i], kTwo20, OZ[j >> 1]);
   }
-  // O to real units: O * 2^20 + sum P z of the M-tile's group (OZ component
-  // i = row 4g + i holds group i's sum; M-tile j lies in group j / 2)
-#pragma unroll
-  for (int j = 0; j < 8; ++j)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) O[j][i] = __builtin_fmaf(O[j][i], kTwo20, OZ[j >> 1]);
 
   // ---- bf16 residual tiles (at most r_cap / 32 of them, in the last split) ----
-  for (int t = max(T0, n_qt) + wave; t < T1; t += NW) {
-    const int base = (t - n_qt) * kTile;
-    residual_tile<kBf16Only>(p, b, h, base, min(kTile, p.res_len - base), c, g, qB, p.qscale, m_run, L, O, OZ);
+  if (max(T0, n_qt) + wave < T1) {
+    // q as stored (bf16, dims 8(4s+g) .. +7 in order), the B operand of the
+    // bf16 K-MFMA; read here, after the quantized tiles, to keep registers free
+    bf16x8_t qN[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      qN[s] = __builtin_bit_cast(bf16x8_t, col_ok ? ld16(qp + 8 * (4 * s + g)) : u32x4_t{0u, 0u, 0u, 0u});
+    for (int t = max(T0, n_qt) + wave; t < T1; t += NW) {
+      const int base = (t - n_qt) * kTile;
+      residual_tile<kBf16Only>(p, b, h, base, min(kTile, p.res_len - base), c, g, qN, p.qscale, m_run, L, O,
+                               OZ);
+    }
   }
 
   // ---- merge the NW waves through LDS (the rings are free now) ----

@@ -81,10 +81,14 @@ __constant__ uint8_t kVTok[4][8] = {
     {12, 14, 28, 30, 13, 15, 29, 31},
 };
 
+// fp16 bit pattern h is +-inf or NaN
+__device__ __forceinline__ bool f16_nonfinite(uint16_t h) { return (h & 0x7C00u) == 0x7C00u; }
+constexpr uint16_t kF16VScaleMax = 0x6800u;  // 2048.0: the decode kernel's V-scale limit
+
 __global__ __launch_bounds__(128) void kivi4_pack_kernel(
     const uint16_t* __restrict__ k, int64_t k_sb, int64_t k_sh, int64_t k_st,
     const uint16_t* __restrict__ v, int64_t v_sb, int64_t v_sh, int64_t v_st, int kv, int g0,
-    int g_cap, int32_t* __restrict__ groups) {
+    int g_cap, int32_t* __restrict__ groups, uint32_t* __restrict__ range_status) {
   __shared__ uint8_t kc[32][128];
   __shared__ uint8_t vc[32][128];
   const int g = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
@@ -116,8 +120,10 @@ __global__ __launch_bounds__(128) void kivi4_pack_kernel(
     const int p = d >> 3, j = d & 7;
     const int slot = 2 * (j & 3) + (j >> 2);
     uint16_t* km = k_meta + p * 16;
-    km[slot] = f32_to_f16_bits(scale);
-    km[8 + slot] = f32_to_f16_bits(mn);
+    const uint16_t hs = f32_to_f16_bits(scale), hz = f32_to_f16_bits(mn);
+    km[slot] = hs;
+    km[8 + slot] = hz;
+    if (range_status && (f16_nonfinite(hs) || f16_nonfinite(hz))) atomicOr(range_status, ZKV_RANGE_K);
   }
   // ---- V: lane = (token t, channel group gd), 32 channels ----
   {
@@ -147,8 +153,14 @@ __global__ __launch_bounds__(128) void kivi4_pack_kernel(
     const int r = (t & 15) >> 2;
     const int e = (t & 3) + ((t >> 4) << 2);
     uint16_t* vm = v_meta + (gd * 4 + r) * 16;
-    vm[e] = f32_to_f16_bits(scale);
-    vm[8 + e] = f32_to_f16_bits(mn);
+    const uint16_t hs = f32_to_f16_bits(scale), hz = f32_to_f16_bits(mn);
+    vm[e] = hs;
+    vm[8 + e] = hz;
+    if (range_status) {
+      const uint32_t bad = (f16_nonfinite(hs) || f16_nonfinite(hz) ? ZKV_RANGE_V : 0u) |
+                           ((hs & 0x7FFFu) > kF16VScaleMax ? ZKV_RANGE_V_SCALE : 0u);
+      if (bad) atomicOr(range_status, bad);
+    }
   }
   __syncthreads();
   // ---- K words in MFMA lane order: w = m*256 + l*4 + s, l = 16g + c,
@@ -216,7 +228,7 @@ extern "C" int zkv_chunk_encode(const uint16_t* keys, int64_t k_sb, int64_t k_sh
 extern "C" int zkv_kivi4_pack(const uint16_t* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
                               const uint16_t* v, int64_t v_sb, int64_t v_sh, int64_t v_st, int bs,
                               int kv, int n_groups, int g0, int g_cap, int32_t* groups,
-                              zkv_stream_t stream) {
+                              uint32_t* range_status, zkv_stream_t stream) {
   ZKV_REQUIRE(k && v && groups, "zkv_kivi4_pack: null pointer");
   ZKV_REQUIRE(bs > 0 && kv > 0 && n_groups >= 0 && g0 >= 0,
               "zkv_kivi4_pack: bad sizes bs=%d kv=%d n_groups=%d g0=%d", bs, kv, n_groups, g0);
@@ -228,6 +240,6 @@ extern "C" int zkv_kivi4_pack(const uint16_t* k, int64_t k_sb, int64_t k_sh, int
   if (n_groups == 0) return ZKV_OK;
   dim3 grid(n_groups, kv, bs);
   kivi4_pack_kernel<<<grid, 128, 0, reinterpret_cast<hipStream_t>(stream)>>>(
-      k, k_sb, k_sh, k_st, v, v_sb, v_sh, v_st, kv, g0, g_cap, groups);
+      k, k_sb, k_sh, k_st, v, v_sb, v_sh, v_st, kv, g0, g_cap, groups, range_status);
   return check_launch("kivi4_pack_kernel");
 }

@@ -136,9 +136,30 @@ class Kivi4Cache:
         return 160  # K codes 64 + K meta 16 + V codes 64 + V meta 16
 
 
-def kivi4_pack(k: torch.Tensor, v: torch.Tensor, cache: Kivi4Cache, g0: int) -> int:
+_RANGE_STATUS: dict = {}
+RANGE_K, RANGE_V, RANGE_V_SCALE = 1, 2, 4   # ZKV_RANGE_* bits of the C ABI
+
+
+def _range_status(device: torch.device) -> torch.Tensor:
+    key = (device.type, device.index)
+    t = _RANGE_STATUS.get(key)
+    if t is None:
+        t = torch.zeros(1, dtype=torch.int32, device=device)
+        _RANGE_STATUS[key] = t
+    return t
+
+
+def kivi4_pack(k: torch.Tensor, v: torch.Tensor, cache: Kivi4Cache, g0: int,
+               check_range: bool = True) -> int:
     """Quantize the leading full groups of k / v [bs, kv, n, 128] into groups
-    [g0, g0 + n // 32) of ``cache``; returns the number of groups written."""
+    [g0, g0 + n // 32) of ``cache``; returns the number of groups written.
+
+    With ``check_range`` (the default) the call waits for the pack and raises
+    ``RuntimeError`` when a group's fp16 scale / zero cannot hold its values
+    (|K| or |V| or a group's range beyond 65504) or a V scale exceeds the
+    decode kernel's limit of 2048 (a V range above 30720 inside one
+    32-channel group).  ``check_range=False`` skips the check and its host
+    synchronisation, for callers that bound their values themselves."""
     require_gpu(k, v)
     _check_bf16("k", k)
     _check_bf16("v", v)
@@ -150,11 +171,22 @@ def kivi4_pack(k: torch.Tensor, v: torch.Tensor, cache: Kivi4Cache, g0: int) -> 
     if (bs, kv) != tuple(cache.shape):
         raise ValueError("cache batch / head shape mismatch")
     ng = n // GROUP
+    status = _range_status(k.device) if check_range else None
+    if status is not None:
+        status.zero_()
     check(lib().zkv_kivi4_pack(
         ptr(k), k.stride(0), k.stride(1), k.stride(2),
         ptr(v), v.stride(0), v.stride(1), v.stride(2),
         bs, kv, ng, g0, cache.g_cap,
-        ptr(cache.groups), stream_of(k)))
+        ptr(cache.groups), ptr(status), stream_of(k)))
+    if status is not None:
+        bits = int(status.item())
+        if bits:
+            what = [name for bit, name in ((RANGE_K, "a K scale or zero point beyond fp16 (|K| > 65504)"),
+                                           (RANGE_V, "a V scale or zero point beyond fp16 (|V| > 65504)"),
+                                           (RANGE_V_SCALE, "a V scale above 2048 (V range > 30720 in one "
+                                                           "32-channel group)")) if bits & bit]
+            raise RuntimeError("kivi4_pack: values outside the 4-bit cache's fp16 range: " + "; ".join(what))
     return ng
 
 

@@ -50,28 +50,42 @@ def c1_workload(seed: int = 42) -> dict:
 
 
 def c2_cache(seed: int, bs: int, kv: int, n_groups: int, res_len: int, device,
-             outlier_frac: float = 0.01) -> kivi.Kivi4Cache:
+             outlier_frac: float = 0.01, keep_rows=()):
     """Format Q cache of n_groups * 32 Gaussian tokens (outlier K channels x10)
-    plus res_len bf16 residual tokens, packed on the GPU one sequence at a time."""
+    plus res_len bf16 residual tokens, packed on the GPU one sequence at a time.
+
+    With ``keep_rows`` (batch indices) it returns (cache, kept), kept[b] = the
+    bf16 K and V of sequence b as host float32 arrays [1, kv, n_groups * 32,
+    128], for checking the pack and the attention against a CPU model."""
     g = _gen(seed, device)
     cache = kivi.Kivi4Cache.allocate(bs, kv, n_groups, max(res_len, 1), device=device)
     n = n_groups * 32
     n_out = max(1, round(outlier_frac * HEAD_DIM))
+    kept = {}
     for b in range(bs):
         k = torch.randn(kv, n, HEAD_DIM, generator=g, device=device)
         v = torch.randn(kv, n, HEAD_DIM, generator=g, device=device)
         for h in range(kv):
             ch = torch.randperm(HEAD_DIM, generator=g, device=device)[:n_out]
             k[h, :, ch] *= 10.0
-        kivi.kivi4_pack(k.to(torch.bfloat16)[None], v.to(torch.bfloat16)[None], cache.rows(b, b + 1), 0)
-        del k, v
+        kb, vb = k.to(torch.bfloat16)[None], v.to(torch.bfloat16)[None]
+        kivi.kivi4_pack(kb, vb, cache.rows(b, b + 1), 0)
+        if b in keep_rows:
+            kept[b] = (kb.float().cpu().numpy(), vb.float().cpu().numpy())
+        del k, v, kb, vb
     if res_len:
         cache.k_res[:, :, :res_len].copy_(
             torch.randn(bs, kv, res_len, HEAD_DIM, generator=g, device=device).to(torch.bfloat16))
         cache.v_res[:, :, :res_len].copy_(
             torch.randn(bs, kv, res_len, HEAD_DIM, generator=g, device=device).to(torch.bfloat16))
     cache.n_groups, cache.res_len = n_groups, res_len
-    return cache
+    return (cache, kept) if keep_rows else cache
+
+
+def c2_query(bs: int, hq: int, device, seed: int = 42) -> torch.Tensor:
+    """The C2 benchmark's query rows: bf16 [bs, hq, 128], N(0, 1), seeded on the device."""
+    g = _gen(seed, device)
+    return torch.randn(bs, hq, HEAD_DIM, generator=g, device=device).to(torch.bfloat16)
 
 
 def c3_workload(seed: int, bs: int, hq: int, kv: int, n_tok: int, n_plant: int, device,
