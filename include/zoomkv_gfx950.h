@@ -121,6 +121,23 @@ int zkv_kivi4_decode_attention(const uint16_t* q, int64_t q_sb, int64_t q_sh,
                                float sm_scale, void* out, int out_f32, int n_splits,
                                void* workspace, size_t workspace_bytes, zkv_stream_t stream);
 
+/* zkv_kivi4_decode_attention without a workspace argument, allocating
+ * nothing: no counterpart in the reference.  It is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  The split partials live in a static
+ * device array of ZKV_NOALLOC_SCRATCH_BYTES per GPU, held until the process
+ * ends; a call whose split plan needs more (bs * hq * splits * 520 bytes)
+ * fails with ZKV_ESPACE.  Every call on one GPU shares that GPU's array:
+ * calls that overlap on one GPU (concurrent streams or threads) race.
+ * Results equal zkv_kivi4_decode_attention's for the same arguments. */
+#define ZKV_NOALLOC_SCRATCH_BYTES ((size_t)8 << 20)
+int zkv_kivi4_decode_attention_noalloc(const uint16_t* q, int64_t q_sb, int64_t q_sh,
+                                       const int32_t* groups, int g_cap,
+                                       const uint16_t* k_res, const uint16_t* v_res, int r_cap,
+                                       int bs, int hq, int kv, int n_groups, int res_len,
+                                       float sm_scale, void* out, int out_f32, int n_splits,
+                                       zkv_stream_t stream);
+
 /* Stage 1 of zkv_kivi4_decode_attention: per context split, the unnormalised
  * partial output o, the running max m (log2 units, sm_scale*log2(e) folded in)
  * and the softmax denominator l of every (b, query head), written to

@@ -34,6 +34,8 @@ SIGNATURES = {
     "zkv_kivi4_decode_attention": (I32, [P, I64, I64, P, I32, P, P, I32,
                                          I32, I32, I32, I32, I32, F32, P, I32, I32,
                                          P, SZ, P]),
+    "zkv_kivi4_decode_attention_noalloc": (I32, [P, I64, I64, P, I32, P, P, I32,
+                                                 I32, I32, I32, I32, I32, F32, P, I32, I32, P]),
     "zkv_kivi4_attention_partial": (I32, [P, I64, I64, P, I32, P, P, I32,
                                           I32, I32, I32, I32, I32, F32, I32, P, SZ, P, P]),
     "zkv_attention_merge": (I32, [P, I32, I32, I32, I32, P, I32, P]),

@@ -55,6 +55,7 @@
 
 #include <algorithm>
 #include <cstdlib>
+#include <mutex>
 
 namespace zkv {
 namespace {
@@ -947,6 +948,74 @@ extern "C" int zkv_kivi4_decode_attention(const uint16_t* q, int64_t q_sb, int64
   return attention_launch(q, q_sb, q_sh, groups, g_cap, k_res, v_res,
                           r_cap, bs, hq, kv, n_groups, res_len, sm_scale, n_splits, workspace,
                           workspace_bytes, nullptr, out, out_f32,
+                          reinterpret_cast<hipStream_t>(stream));
+}
+
+// ---- allocation-free variant ----------------------------------------------
+//
+// The split partials of zkv_kivi4_decode_attention_noalloc live in this
+// file-scope device array.  Each GPU the library runs on holds its own copy
+// (until the process ends) at its own address; host code only ever uses that
+// address, taken once per device with hipGetSymbolAddress -- the array's name
+// in host code is a host-side stand-in, not a device pointer.
+namespace zkv {
+namespace {
+
+constexpr size_t kNoAllocScratchBytes = ZKV_NOALLOC_SCRATCH_BYTES;  // 8 MiB per GPU
+__device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The device address of the current device's scratch array (taken once per
+// device, with that device current), or nullptr with the error set.
+void* scratch_for_current_device() {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    fail(ZKV_ELAUNCH, "zkv_kivi4_decode_attention_noalloc: no current HIP device (%s, device %d)",
+         hipGetErrorString(e), dev);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr) {
+      fail(ZKV_ELAUNCH, "zkv_kivi4_decode_attention_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s",
+           dev, hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  return g_scratch_ptr[dev];
+}
+
+}  // namespace
+}  // namespace zkv
+
+extern "C" int zkv_kivi4_decode_attention_noalloc(const uint16_t* q, int64_t q_sb, int64_t q_sh,
+                                                  const int32_t* groups, int g_cap,
+                                                  const uint16_t* k_res, const uint16_t* v_res, int r_cap,
+                                                  int bs, int hq, int kv, int n_groups, int res_len,
+                                                  float sm_scale, void* out, int out_f32, int n_splits,
+                                                  zkv_stream_t stream) {
+  ZKV_REQUIRE(out, "zkv_kivi4_decode_attention_noalloc: null output");
+  ZKV_REQUIRE(bs > 0 && kv > 0 && hq > 0 && hq % kv == 0,
+              "zkv_kivi4_decode_attention_noalloc: bad heads bs=%d hq=%d kv=%d", bs, hq, kv);
+  const SplitPlan sp = plan_splits(bs, kv, n_groups, res_len, n_splits);
+  const size_t need = workspace_bytes_for(bs, hq, kv, sp.n_splits);
+  if (need > kNoAllocScratchBytes)
+    return fail(ZKV_ESPACE,
+                "zkv_kivi4_decode_attention_noalloc: %d splits x %d sequences x %d query heads need %zu bytes of "
+                "split partials, beyond the %zu-byte static scratch (use zkv_kivi4_decode_attention with a "
+                "workspace, or fewer splits)",
+                sp.n_splits, bs, hq, need, kNoAllocScratchBytes);
+  void* ws = scratch_for_current_device();
+  if (ws == nullptr) return ZKV_ELAUNCH;
+  return attention_launch(q, q_sb, q_sh, groups, g_cap, k_res, v_res, r_cap, bs, hq, kv, n_groups, res_len,
+                          sm_scale, n_splits, ws, kNoAllocScratchBytes, nullptr, out, out_f32,
                           reinterpret_cast<hipStream_t>(stream));
 }
 
