@@ -108,6 +108,16 @@ def test_search_more_sizes(rng, P, Q, N, topk):
     _check_search(rng, P, Q, N, topk)
 
 
+@pytest.mark.parametrize("P,Q,N,topk", [
+    (1, 3, 16384, 100),        # filter path, 64 lists: one select pass
+    (2, 2, 200000, 256),       # 782 lists: 8 passes
+    (1, 2, 524288, 300),       # 2048 lists: 16 passes, the filter path's largest pool
+    (1, 2, 600000, 64),        # beyond it: the sliced path
+])
+def test_search_filter_path_passes(rng, P, Q, N, topk):
+    _check_search(rng, P, Q, N, topk)
+
+
 def test_search_all_keys_equal(rng):
     """Every key identical: every estimate ties, and the top-k are the lowest
     indices."""
@@ -167,3 +177,81 @@ def test_search_rejects_bad_sizes():
         rabitq_search(torch.zeros(1, 128, dtype=torch.float16, device="cuda"), big,
                       torch.zeros(big.shape[0], 16, dtype=torch.uint8, device="cuda"),
                       torch.zeros(big.shape[0], 2, dtype=torch.float16, device="cuda"), s, 1025)
+
+
+def _filter_premise(est_row, n, topk):
+    """For the filter path's plan, from the oracle's estimates of one query:
+    the number of keys reaching the threshold and the fullest 256-key list's
+    count.  Plan: s = min(n, 4096) sample keys, 64 blocks of 64 consecutive
+    keys starting at multiples of n // 64 (every key when n < 4096);
+    m = ceil(4 k s / n), at least 8; tau = the lower edge of the bin holding
+    the m-th largest sample among 4096 bins of width 2^shift over the samples'
+    [min, max] (shift = bit length of max - min, less 12, at least 0);
+    lists hold 15 entries."""
+    from oracle.select import ordered_key
+    keys = ordered_key(est_row).astype(np.int64)
+    s = min(n, 4096)
+    i = np.arange(s)
+    sk = keys[(i >> 6) * (n // 64) + (i & 63)] if s == 4096 else keys
+    m = min(s, max(8, -(-4 * topk * s // n)))
+    lo, hi = int(sk.min()), int(sk.max())
+    shift = max((hi - lo).bit_length() - 12, 0)
+    mth = int(np.sort(sk)[::-1][m - 1])
+    tau = lo + (((mth - lo) >> shift) << shift)
+    hit = keys >= tau
+    per_list = np.add.reduceat(hit.astype(np.int64), np.arange(0, n, 256))
+    return int(hit.sum()), int(per_list.max())
+
+
+def _check_planted(rng, n, topk, planted_rows, Q=2, dup=None, premise=None):
+    """Search where the first query is planted at `planted_rows` (its copies
+    estimate highest, all equal); compare everything with the oracle.
+    ``premise(hits, fullest_slice)`` checks which select path the first query
+    takes."""
+    from zoomkv_revision_amd.rabitq import rabitq_encode, rabitq_search
+    s_np, s_t = _signs()
+    keys = orq.clustered_unit_keys(rng, n if dup is None else dup, 16)
+    if dup is not None:
+        keys = keys[rng.integers(0, dup, size=n)]
+    qs = orq.clustered_unit_keys(rng, Q, 16)
+    keys[planted_rows] = qs[0]
+    kt = _f16(keys)
+    codes, fac = rabitq_encode(kt, s_t)
+    cand, fidx, fsc = (from_torch(t) for t in rabitq_search(_f16(qs), kt, codes, fac, s_t, topk))
+    ck, fk = orq.encode(keys, s_np)
+    if premise is not None:
+        cq, fq = orq.encode(qs[:1], s_np)
+        assert premise(*_filter_premise(orq.estimate(cq, fq, ck, fk)[0], n, topk))
+    rc, ri, rs = orq.search(qs, keys, ck, fk, s_np, topk)
+    assert np.array_equal(cand, rc), "candidate set"
+    assert np.array_equal(fidx, ri), "reranked order"
+    assert np.array_equal(fsc.view(np.uint32), rs.view(np.uint32)), "exact scores"
+    return cand
+
+
+def test_search_filter_path_tau_above_the_kth_key(rng):
+    """131072 keys, top-256: tau comes from the 32nd largest of 4096 samples
+    (64 blocks of 64 keys every 2048).  200 copies of the query sit at
+    sampled positions, so tau falls in their estimate's bin and fewer than k
+    keys reach it: the select kernel takes its exact full-pool path."""
+    t = np.arange(200)
+    rows = (t % 64) * 2048 + (t // 64) * 5
+    cand = _check_planted(rng, 131072, 256, rows, premise=lambda hits, full: hits < 256)
+    assert set(rows.tolist()) <= set(cand[0].tolist())
+
+
+def test_search_filter_path_overflowing_slice(rng):
+    """40 consecutive copies of the query fill one 256-key list beyond its
+    15 entries: the select kernel detects the overflow and takes its exact
+    full-pool path."""
+    _check_planted(rng, 65536, 200, np.arange(1024, 1064), premise=lambda hits, full: full > 15)
+
+
+def test_search_filter_path_ties(rng):
+    """Only 40 distinct keys among 131072 (every estimate ties with ~3300
+    others) and only 2 distinct among 40000: ties at the threshold and at the
+    k-th key go to the lowest indices, on the filter path (lists hold all of
+    the >= 256 keys at or above tau) and on the full-pool path."""
+    _check_planted(rng, 131072, 256, np.arange(0), dup=40,
+                   premise=lambda hits, full: 256 <= hits <= 4096 and full <= 15)
+    _check_planted(rng, 40000, 100, np.arange(0), dup=2, premise=lambda hits, full: full > 15)

@@ -121,6 +121,66 @@ __global__ __launch_bounds__(256) void rabitq_estimate_kernel(
 }
 
 // ----------------------------------------------------------------------------
+// Wave primitives on DPP (row shifts / rotations / broadcasts inside the
+// VALU) and ds_swizzle: no LDS bank traffic.
+// ----------------------------------------------------------------------------
+// lanes whose DPP source lies outside the row (or in a masked row) read 0
+#define ZKV_DPP0(v, ctrl, row_mask) __builtin_amdgcn_update_dpp(0, (v), (ctrl), (row_mask), 0xF, false)
+#define ZKV_ROR(v, n) __builtin_amdgcn_update_dpp((v), (v), 0x120 + (n), 0xF, 0xF, false)
+
+// inclusive prefix sum over the wave's lanes
+__device__ __forceinline__ int wave_incl_sum(int v) {
+  v += ZKV_DPP0(v, 0x111, 0xF);  // row_shr:1
+  v += ZKV_DPP0(v, 0x112, 0xF);  // row_shr:2
+  v += ZKV_DPP0(v, 0x114, 0xF);  // row_shr:4
+  v += ZKV_DPP0(v, 0x118, 0xF);  // row_shr:8: each 16-lane row scanned
+  v += ZKV_DPP0(v, 0x142, 0xA);  // row_bcast:15 into rows 1, 3
+  v += ZKV_DPP0(v, 0x143, 0xC);  // row_bcast:31 into rows 2, 3
+  return v;
+}
+
+// every lane of each 16-lane row gets the row's max / min / sum
+__device__ __forceinline__ uint32_t row_max_u32(uint32_t v) {
+  v = max(v, static_cast<uint32_t>(ZKV_ROR(static_cast<int>(v), 8)));
+  v = max(v, static_cast<uint32_t>(ZKV_ROR(static_cast<int>(v), 4)));
+  v = max(v, static_cast<uint32_t>(ZKV_ROR(static_cast<int>(v), 2)));
+  return max(v, static_cast<uint32_t>(ZKV_ROR(static_cast<int>(v), 1)));
+}
+__device__ __forceinline__ uint32_t row_min_u32(uint32_t v) {
+  v = min(v, static_cast<uint32_t>(ZKV_ROR(static_cast<int>(v), 8)));
+  v = min(v, static_cast<uint32_t>(ZKV_ROR(static_cast<int>(v), 4)));
+  v = min(v, static_cast<uint32_t>(ZKV_ROR(static_cast<int>(v), 2)));
+  return min(v, static_cast<uint32_t>(ZKV_ROR(static_cast<int>(v), 1)));
+}
+__device__ __forceinline__ int row_sum(int v) {
+  v += ZKV_ROR(v, 8);
+  v += ZKV_ROR(v, 4);
+  v += ZKV_ROR(v, 2);
+  return v + ZKV_ROR(v, 1);
+}
+__device__ __forceinline__ uint32_t lane_u32(uint32_t v, int lane) {
+  return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), lane));
+}
+// wave-uniform reductions
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = row_max_u32(v);
+  return max(max(lane_u32(v, 0), lane_u32(v, 16)), max(lane_u32(v, 32), lane_u32(v, 48)));
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+  v = row_min_u32(v);
+  return min(min(lane_u32(v, 0), lane_u32(v, 16)), min(lane_u32(v, 32), lane_u32(v, 48)));
+}
+__device__ __forceinline__ int wave_sum(int v) {
+  v = row_sum(v);
+  return static_cast<int>(lane_u32(v, 0) + lane_u32(v, 16) + lane_u32(v, 32) + lane_u32(v, 48));
+}
+// value of lane (l ^ X) inside the lane's 32-lane half (X < 32)
+template <int X>
+__device__ __forceinline__ int swizzle_xor(int v) {
+  return __builtin_amdgcn_ds_swizzle(v, 0x1F | (X << 10));
+}
+
+// ----------------------------------------------------------------------------
 // Block primitives for NT threads (multiple of 64)
 // ----------------------------------------------------------------------------
 template <int NT>
@@ -130,12 +190,7 @@ struct Block {
   // exclusive prefix sum over threads (thread order) and the block total
   __device__ static int excl_scan(int v, int* s_tmp, int& total) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    int incl = v;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const int t = __shfl_up(incl, off);
-      if (lane >= off) incl += t;
-    }
+    const int incl = wave_incl_sum(v);
     if (lane == 63) s_tmp[wave] = incl;
     __syncthreads();
     int before = 0;
@@ -152,11 +207,8 @@ struct Block {
 
   __device__ static void minmax(uint32_t& mn, uint32_t& mx, uint32_t* s_tmp) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-      mn = min(mn, static_cast<uint32_t>(__shfl_xor(static_cast<int>(mn), off)));
-      mx = max(mx, static_cast<uint32_t>(__shfl_xor(static_cast<int>(mx), off)));
-    }
+    mn = wave_min_u32(mn);
+    mx = wave_max_u32(mx);
     if (lane == 0) {
       s_tmp[wave] = mn;
       s_tmp[kWaves + wave] = mx;
@@ -363,8 +415,76 @@ __global__ __launch_bounds__(kNT1) void rabitq_stage1_kernel(
 }
 
 // ----------------------------------------------------------------------------
-// Stage 2: per (query, pool): top-k of the n_cand candidates (positions are in
-// increasing index order), exact rerank, sort by (score desc, index asc).
+// Exact rerank of the k selected indices (s_sel, increasing index order) and
+// the bitonic sort by (score desc, index asc) -> out_idx / out_score.
+// 16-lane groups: lane l holds dims 8l .. 8l+7 of the query and the key.
+// ----------------------------------------------------------------------------
+template <int NT>
+__device__ void rerank_and_sort(const int32_t* s_sel, int k, const uint16_t* __restrict__ qrow,
+                                const uint16_t* __restrict__ kp, int64_t k_row_stride, int64_t n_keys,
+                                float* s_score, uint64_t* s_sort, int64_t* __restrict__ out_idx,
+                                float* __restrict__ out_score) {
+  const int tid = threadIdx.x;
+  const int l = tid & 15;
+  const u32x4_t qw = *reinterpret_cast<const u32x4_t*>(qrow + 8 * l);
+  float qf[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) qf[e] = f16_to_f32(static_cast<uint16_t>(qw[e >> 1] >> (16 * (e & 1))));
+  for (int c0 = 0; c0 < k; c0 += NT / 16) {
+    const int c = c0 + (tid >> 4);
+    float s = 0.0f;
+    // the selection only yields indices inside the pool; a key row is read
+    // only for such an index all the same
+    const int64_t ki = c < k ? static_cast<int64_t>(s_sel[c]) : -1;
+    if (ki >= 0 && ki < n_keys) {
+      const u32x4_t kw = *reinterpret_cast<const u32x4_t*>(kp + ki * k_row_stride + 8 * l);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float pe = qf[e] * f16_to_f32(static_cast<uint16_t>(kw[e >> 1] >> (16 * (e & 1))));
+        s = e == 0 ? pe : s + pe;
+      }
+    }
+#pragma unroll
+    for (int off = 8; off > 0; off >>= 1) s = s + __shfl_xor(s, off);
+    if (c < k && l == 0) s_score[c] = s;
+  }
+  __syncthreads();
+
+  // bitonic sort (descending) of (ordered score of +-0 -> +0, 0xFFFF - slot);
+  // slots are in increasing index order, so ties go to the lower index
+  int P = 1;
+  while (P < k) P <<= 1;
+  for (int i = tid; i < P; i += NT)
+    s_sort[i] = i < k ? (static_cast<uint64_t>(ordered_key_f(s_score[i] + 0.0f)) << 32) |
+                            static_cast<uint64_t>(0xFFFFu - static_cast<uint32_t>(i))
+                      : 0ull;
+  for (int size = 2; size <= P; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      __syncthreads();
+      for (int i = tid; i < P / 2; i += NT) {
+        const int lo = 2 * i - (i & (stride - 1));
+        const int hi = lo + stride;
+        const bool desc = (lo & size) == 0;
+        const uint64_t a = s_sort[lo], b = s_sort[hi];
+        if ((a < b) == desc) {
+          s_sort[lo] = b;
+          s_sort[hi] = a;
+        }
+      }
+    }
+  }
+  __syncthreads();
+  for (int i = tid; i < k; i += NT) {
+    const int slot = static_cast<int>(0xFFFFu - static_cast<uint32_t>(s_sort[i] & 0xFFFFu));
+    out_idx[i] = s_sel[slot];
+    out_score[i] = s_score[slot];
+  }
+}
+
+// ----------------------------------------------------------------------------
+// Stage 2 of the slice path: per (query, pool): top-k of the n_cand
+// candidates (positions are in increasing index order), exact rerank, sort by
+// (score desc, index asc).
 // ----------------------------------------------------------------------------
 __global__ __launch_bounds__(kNT2) void rabitq_stage2_kernel(
     const uint32_t* __restrict__ cand_key, const int32_t* __restrict__ cand_idx, int n_cand, int n_real,
@@ -398,62 +518,733 @@ __global__ __launch_bounds__(kNT2) void rabitq_stage2_kernel(
                                [&](int j, int pos) { s_sel[pos] = ci[base + j]; });
   __syncthreads();
   for (int i = tid; i < k; i += kNT2) out_cand[pq * k + i] = s_sel[i];
+  rerank_and_sort<kNT2>(s_sel, k, q + pq * kD, keys + pool * k_pool_stride, k_row_stride, n_keys, s_score,
+                        s_sort, out_idx + pq * k, out_score + pq * k);
+}
 
-  // exact rerank: 16-lane groups, lane l holds dims 8l .. 8l+7
-  const int l = tid & 15;
-  const u32x4_t qw = *reinterpret_cast<const u32x4_t*>(q + pq * kD + 8 * l);
-  float qf[8];
+// ----------------------------------------------------------------------------
+// Filter path (large pools, n >= 128 k): every code is read once per pass for
+// all queries of its pool.
+//   1. prep, per (query, pool), 4 waves: encode the query (wave 0: the FWHT
+//      across lanes, the factor sums in dimension order by one lane, so the
+//      bits equal rabitq_encode_kernel's), estimate a strided sample of
+//      s = min(n, 4096) keys and take tau = the m-th largest sample key,
+//      m = ceil(4 k s / n) (at least 8): about 4k keys of the pool are
+//      expected at or above tau;
+//   2. filter, one wave per 64 keys: each lane estimates its key against
+//      every query (query code, factor and tau through scalar loads) and the
+//      keys >= tau go to that (query, wave) list of up to kFiltCap entries in
+//      increasing index order (ballot + mbcnt; no atomics, no barriers);
+//   3. select, per (query, pool): the lists hold an exact superset of the
+//      top-k whenever at least k keys reached tau and no list overflowed
+//      (the k-th largest key is then >= tau): their exact top-k is the answer.
+//      Otherwise (ties, adversarial layouts) the block selects over all n
+//      keys, recomputing their estimates, so the result is exact either way.
+//      Then the exact rerank and the sort by (score desc, index asc).
+// ----------------------------------------------------------------------------
+constexpr int kFiltWave = 64;         // keys per filter wave
+constexpr int kFiltList = 256;        // keys per filter list (a 4-wave block)
+constexpr int kBucketWords = 32;      // a list: 128 bytes = count, pad, 15 (key, index) pairs
+constexpr int kFiltCap = 15;          // entries a list holds
+constexpr int kSampleMax = 4096;      // prep: sample keys per query
+constexpr int kBigNT = 1024;          // prep / select blocks
+constexpr int kSelMaxPasses = 16;     // select: bucket chunks per thread (n <= 2048 lists of 256)
+
+struct FilterPlan {
+  int s_count, m;
+};
+
+// m = ceil(4 k s / n), at least 8: about 4k keys are expected at or above the
+// m-th largest of s sample keys, and fewer than k only when m or more of the
+// s samples land among the top k - 1 keys (expected m / 4).
+FilterPlan filter_plan(int64_t n, int topk) {
+  FilterPlan f{};
+  f.s_count = static_cast<int>(n < kSampleMax ? n : kSampleMax);
+  const int64_t m = (4ll * topk * f.s_count + n - 1) / n;
+  f.m = static_cast<int>(m < 8 ? 8 : (m > f.s_count ? f.s_count : m));
+  return f;
+}
+
+// select passes: 1024 threads read 128 buckets (1024 16-byte chunks) per pass
+int select_passes(int64_t n) {
+  const int64_t lists = (n + kFiltList - 1) / kFiltList;
+  int r = 1;
+  while (128ll * r < lists) r <<= 1;
+  return r;
+}
+
+bool use_filter_path(int64_t n, int topk) { return n >= 128ll * topk && select_passes(n) <= kSelMaxPasses; }
+
+// k-th largest key (and how many keys equal to it to take, lowest positions
+// first) among the valid items (bit j of `valid`: item j) of a block of NT
+// threads holding NI keys each; the block holds at least k valid items, whose
+// minimum and maximum are mn and mx.  hist[0 .. 4095] must be zero, with a
+// barrier since the clear.
+// Radix rounds of 12-bit digits over LDS histograms of 4096 bins: the first
+// digit is taken 12 bits below the top bit of the items' range [mn, mx],
+// each later one 12 bits below the previous, so a 32-bit range takes at most
+// three rounds.  Two histograms alternate (hist: 2 x 4096 ints), so a round
+// clears the next one while it counts: three barriers per round.
+// With exact == false it stops after the first round and returns the lower
+// edge of the bin holding the k-th largest item (at least k items are >= it).
+template <int NT, int NI>
+__device__ void block_radix_select12(const uint32_t (&key)[NI], uint32_t valid, int k, uint32_t mn, uint32_t mx,
+                                     int* hist, uint32_t* tmp, uint32_t& T, int& take_eq, bool exact = true) {
+  constexpr int W = NT / 64;
+  constexpr int kBins = 4096, kPerT = kBins / NT;
+  static_assert(kBins % NT == 0, "bins per thread");
+  static_assert(NI <= 32, "validity mask");
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  uint32_t lo = mn, hi = mx;
+  int rem = k;
+  int shift = 0;
+  if (lo != hi) {
+    const int bits = 32 - __clz(static_cast<int>(hi - lo));
+    shift = bits > 12 ? bits - 12 : 0;
+  }
+  int buf = 0;
+  while (lo != hi) {
+    int* h = hist + buf * kBins;
+    int* h_next = hist + (buf ^ 1) * kBins;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) qf[e] = f16_to_f32(static_cast<uint16_t>(qw[e >> 1] >> (16 * (e & 1))));
-  const uint16_t* kp = keys + pool * k_pool_stride;
-  for (int c0 = 0; c0 < k; c0 += kNT2 / 16) {
-    const int c = c0 + (tid >> 4);
-    float s = 0.0f;
-    // stage 1 always writes valid indices; a key row is read only for an
-    // index inside the pool all the same
-    const int64_t ki = c < k ? static_cast<int64_t>(s_sel[c]) : -1;
-    if (ki >= 0 && ki < n_keys) {
-      const u32x4_t kw = *reinterpret_cast<const u32x4_t*>(kp + ki * k_row_stride + 8 * l);
+    for (int j = 0; j < kPerT; ++j) h_next[tid * kPerT + j] = 0;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float pe = qf[e] * f16_to_f32(static_cast<uint16_t>(kw[e >> 1] >> (16 * (e & 1))));
-        s = e == 0 ? pe : s + pe;
+    for (int j = 0; j < NI; ++j) {
+      if (((valid >> j) & 1u) && key[j] >= lo && key[j] <= hi) atomicAdd(&h[(key[j] - lo) >> shift], 1);
+    }
+    __syncthreads();
+    // thread t owns bins t*kPerT .. t*kPerT + kPerT - 1; higher threads hold higher bins
+    int c[kPerT], own = 0;
+#pragma unroll
+    for (int j = 0; j < kPerT; ++j) {
+      c[j] = h[tid * kPerT + j];
+      own += c[j];
+    }
+    const int incl = wave_incl_sum(own);
+    const int wave_total = __builtin_amdgcn_readlane(incl, 63);
+    if (lane == 0) tmp[wave] = static_cast<uint32_t>(wave_total);
+    __syncthreads();
+    int waves_above = 0;
+#pragma unroll
+    for (int w = 0; w < W; ++w) waves_above += w > wave ? static_cast<int>(tmp[w]) : 0;
+    int above = waves_above + wave_total - incl;  // items in higher bins than this thread's
+#pragma unroll
+    for (int j = kPerT - 1; j >= 0; --j) {
+      const int at_or_above = above + c[j];
+      if (at_or_above >= rem && above < rem) {
+        tmp[W] = static_cast<uint32_t>(tid * kPerT + j);
+        tmp[W + 1] = static_cast<uint32_t>(above);
       }
+      above = at_or_above;
+    }
+    __syncthreads();
+    const uint32_t b = tmp[W];
+    rem -= static_cast<int>(tmp[W + 1]);
+    const uint64_t new_lo = static_cast<uint64_t>(lo) + (static_cast<uint64_t>(b) << shift);
+    const uint64_t new_hi = new_lo + (1ull << shift) - 1ull;
+    lo = static_cast<uint32_t>(new_lo);
+    hi = static_cast<uint32_t>(new_hi < hi ? new_hi : hi);
+    if (shift == 0 || !exact) break;
+    shift = shift > 12 ? shift - 12 : 0;
+    buf ^= 1;
+    // the next round's first barrier orders these reads of tmp before its rewrite
+  }
+  T = lo;
+  take_eq = rem;
+}
+
+// ----------------------------------------------------------------------------
+// 1. prep, per (query, pool), 1024 threads: every thread requests its sample
+//    keys first -- s = min(n, 4096) keys in 64 blocks of 64 consecutive keys
+//    spread over the pool (or every key when n < 4096) -- while wave 0
+//    encodes the query (the FWHT across lanes, the factor sums in dimension
+//    order by one lane: the bits of rabitq_encode_kernel); then tau = the
+//    lower edge of the 4096-bin histogram bin (over the samples' range) that
+//    holds the m-th largest sample key.
+// ----------------------------------------------------------------------------
+__global__ __launch_bounds__(kBigNT) void rabitq_prep_kernel(
+    const uint16_t* __restrict__ q, const float* __restrict__ signs, const uint8_t* __restrict__ codes_k,
+    const uint16_t* __restrict__ fac_k, int64_t n, int queries, int s_count, int m,
+    uint8_t* __restrict__ q_codes, uint16_t* __restrict__ q_fac, uint32_t* __restrict__ tau) {
+  constexpr int NI = kSampleMax / kBigNT;
+  __shared__ __attribute__((aligned(16))) float s_x[kD];
+  __shared__ __attribute__((aligned(16))) float s_y[kD];
+  __shared__ u32x4_t s_qc;
+  __shared__ float s_fq;
+  __shared__ int s_hist[2 * 4096];
+  __shared__ uint32_t s_tmp[2 * (kBigNT / 64) + 2];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int64_t pool = blockIdx.y;
+  const int64_t pq = pool * queries + blockIdx.x;
+  // ---- sample rows first: item i of thread t is sample s = i * NT + t ----
+  const u32x4_t* kc = reinterpret_cast<const u32x4_t*>(codes_k) + pool * n;
+  const uint32_t* kf = reinterpret_cast<const uint32_t*>(fac_k) + pool * n;
+  const int64_t blk = n / 64;  // sample block j starts at key j * blk (n >= 4096)
+  u32x4_t sc[NI];
+  uint32_t sf[NI];
+  int valid_n = 0;
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int s = i * kBigNT + tid;
+    const int64_t p = s_count == kSampleMax ? (s >> 6) * blk + (s & 63) : s;
+    const bool ok = s < s_count;
+    const int64_t pp = ok ? p : 0;
+    sc[i] = kc[pp];
+    sf[i] = kf[pp];
+    valid_n += ok;  // valid items lead: s < s_count is monotone in i
+  }
+  if (tid < 64) {
+    // ---- encode (wave 0): lane l holds dims 2l, 2l + 1 ----
+    const uint32_t xw = reinterpret_cast<const uint32_t*>(q + pq * kD)[lane];
+    const float x0 = f16_to_f32(static_cast<uint16_t>(xw)), x1 = f16_to_f32(static_cast<uint16_t>(xw >> 16));
+    float y0 = x0 * signs[2 * lane], y1 = x1 * signs[2 * lane + 1];
+    {  // h = 1: the pair sits in one lane
+      const float a = y0, b = y1;
+      y0 = a + b;
+      y1 = a - b;
     }
 #pragma unroll
-    for (int off = 8; off > 0; off >>= 1) s = s + __shfl_xor(s, off);
-    if (c < k && l == 0) s_score[c] = s;
+    for (int hl = 1; hl < 64; hl <<= 1) {  // h = 2 hl: partner lane l ^ hl
+      const float p0 = __shfl_xor(y0, hl), p1 = __shfl_xor(y1, hl);
+      const bool lower = (lane & hl) == 0;
+      y0 = lower ? y0 + p0 : p0 - y0;
+      y1 = lower ? y1 + p1 : p1 - y1;
+    }
+    // code bit d = (y_d >= 0): dims 2l / 2l + 1 are bit l of the two ballots
+    const uint64_t be = __ballot(y0 >= 0.0f), bo = __ballot(y1 >= 0.0f);
+    s_x[2 * lane] = x0;
+    s_x[2 * lane + 1] = x1;
+    s_y[2 * lane] = y0;
+    s_y[2 * lane + 1] = y1;
+    if (lane < 4) {  // word w = dims 32w .. 32w + 31 = ballot bits 16w .. 16w + 15, interleaved
+      uint32_t word = 0;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        word |= static_cast<uint32_t>((be >> (16 * lane + i)) & 1ull) << (2 * i);
+        word |= static_cast<uint32_t>((bo >> (16 * lane + i)) & 1ull) << (2 * i + 1);
+      }
+      reinterpret_cast<uint32_t*>(q_codes + pq * 16)[lane] = word;
+      reinterpret_cast<uint32_t*>(&s_qc)[lane] = word;
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS writes are done
+    __builtin_amdgcn_wave_barrier();
+    if (lane == 0) {  // sums in dimension order (the encode kernel's arithmetic)
+      float nsq = 0.0f, ysq = 0.0f, yabs = 0.0f;
+#pragma unroll 4
+      for (int c = 0; c < kD / 8; ++c) {
+        float xv[8], yv[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          xv[e] = s_x[8 * c + e];
+          yv[e] = s_y[8 * c + e];
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          nsq = nsq + xv[e] * xv[e];
+          ysq = ysq + yv[e] * yv[e];
+          yabs = yabs + fabsf(yv[e]);
+        }
+      }
+      const float norm = sqrtf(nsq);
+      const float corr = yabs > 0.0f ? (sqrtf(ysq) * kSqrt128) / yabs : 0.0f;
+      const uint16_t hn = f32_to_f16_bits(norm), hc = f32_to_f16_bits(corr);
+      reinterpret_cast<uint32_t*>(q_fac)[pq] = static_cast<uint32_t>(hn) | (static_cast<uint32_t>(hc) << 16);
+      s_fq = f16_to_f32(hn) * f16_to_f32(hc);
+    }
   }
   __syncthreads();
+  const u32x4_t qc = s_qc;
+  const float fq = s_fq;
+  uint32_t key[NI];
+  uint32_t mn = 0xFFFFFFFFu, mx = 0u;
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    key[i] = ordered_key_f(rabitq_estimate(qc, fq, sc[i], sf[i]));
+    if (i < valid_n) {
+      mn = min(mn, key[i]);
+      mx = max(mx, key[i]);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 4096 / kBigNT; ++j) s_hist[tid * (4096 / kBigNT) + j] = 0;
+  Block<kBigNT>::minmax(mn, mx, s_tmp);  // its barriers also order the clear
+  uint32_t T;
+  int take_eq;
+  // one histogram round: tau = the lower edge of the bin holding the m-th
+  // largest sample key (4096 bins over the samples' range), so at least m
+  // samples reach it
+  block_radix_select12<kBigNT, NI>(key, (1u << valid_n) - 1u, m, mn, mx, s_hist, s_tmp, T, take_eq, false);
+  if (tid == 0) tau[pq] = T;
+}
 
-  // bitonic sort (descending) of (ordered score of +-0 -> +0, 0xFFFF - slot);
-  // slots are in increasing index order, so ties go to the lower index
-  int P = 1;
-  while (P < k) P <<= 1;
-  for (int i = tid; i < P; i += kNT2)
-    s_sort[i] = i < k ? (static_cast<uint64_t>(ordered_key_f(s_score[i] + 0.0f)) << 32) |
-                            static_cast<uint64_t>(0xFFFFu - static_cast<uint32_t>(i))
-                      : 0ull;
-  for (int size = 2; size <= P; size <<= 1) {
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      __syncthreads();
-      for (int i = tid; i < P / 2; i += kNT2) {
-        const int lo = 2 * i - (i & (stride - 1));
-        const int hi = lo + stride;
-        const bool desc = (lo & size) == 0;
-        const uint64_t a = s_sort[lo], b = s_sort[hi];
-        if ((a < b) == desc) {
-          s_sort[lo] = b;
-          s_sort[hi] = a;
+// ----------------------------------------------------------------------------
+// 2. filter: lane = query; a block of 4 waves covers 256 consecutive keys (a
+//    list), each wave 64 of them; grid (lists, query groups of 64, pools).
+//    Lane l of a wave loads key l of the wave's 64 (one coalesced request)
+//    into LDS; then every lane holds its query's code, factor and tau and
+//    walks the 64 keys, 8 at a time (their LDS reads first), into a hit mask:
+//    est >= tau compared as floats, before the final 2^-7 scale and the
+//    order-preserving key, so the mask can only hold extra keys (+-0); the
+//    hits are re-checked with the exact keys when they are written.  One
+//    barrier gives each wave its offset in the block's list per query.  A
+//    list is a 128-byte bucket: word 0 the hit count, then the first 15 hits
+//    in increasing index order as (key, index) word pairs from word 2, so
+//    16-byte chunk c of a bucket holds entries 2c - 1 and 2c.  The block's 64
+//    buckets are assembled in LDS and stored as whole lines.  No atomics.
+// ----------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void rabitq_filter_kernel(
+    const uint8_t* __restrict__ q_codes, const uint16_t* __restrict__ q_fac, const uint32_t* __restrict__ tau,
+    const uint8_t* __restrict__ codes_k, const uint16_t* __restrict__ fac_k, int64_t n, int queries,
+    int n_lists, uint32_t* __restrict__ buckets) {
+  __shared__ u32x4_t s_kc[4][kFiltWave];
+  __shared__ float s_fk[4][kFiltWave];
+  __shared__ int s_cnt[4][64];
+  __shared__ uint32_t s_bkt[64][kBucketWords + 1];  // the block's 64 buckets; odd stride: per-lane rows conflict-free
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int list = blockIdx.x;
+  const int64_t pool = blockIdx.z;
+  const int64_t p0 = static_cast<int64_t>(list) * kFiltList + wave * kFiltWave;
+  const int nk = n - p0 < kFiltWave ? static_cast<int>(n - p0 > 0 ? n - p0 : 0) : kFiltWave;
+  {
+    const int64_t row = pool * n + (lane < nk ? p0 + lane : 0);
+    const u32x4_t c = reinterpret_cast<const u32x4_t*>(codes_k)[row];
+    const uint32_t f = reinterpret_cast<const uint32_t*>(fac_k)[row];
+    s_kc[wave][lane] = c;
+    s_fk[wave][lane] = f16_to_f32(static_cast<uint16_t>(f)) * f16_to_f32(static_cast<uint16_t>(f >> 16));
+  }
+  const int qi = blockIdx.y * 64 + lane;
+  const bool q_ok = qi < queries;
+  const int64_t pq = pool * queries + (q_ok ? qi : 0);
+  const u32x4_t qc = *reinterpret_cast<const u32x4_t*>(q_codes + pq * 16);
+  const float fq = query_factor(q_fac, pq);
+  const uint32_t t = tau[pq];
+  // tau as an unscaled float: est * 2^-7 >= tau  <=>  est >= tau * 2^7 (exact
+  // scaling), with the float compare putting -0 with +0
+  const float t128 = __uint_as_float((t & 0x80000000u) ? (t & 0x7FFFFFFFu) : ~t) * 128.0f;
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the wave's LDS writes are done
+  __builtin_amdgcn_wave_barrier();
+  uint64_t hits = 0;  // bit j: key j of the wave's 64 may reach tau
+  constexpr int kG = 8;
+#pragma unroll
+  for (int j0 = 0; j0 < kFiltWave; j0 += kG) {
+    u32x4_t c[kG];
+    float f[kG];
+#pragma unroll
+    for (int g = 0; g < kG; ++g) {
+      c[g] = s_kc[wave][j0 + g];
+      f[g] = s_fk[wave][j0 + g];
+    }
+#pragma unroll
+    for (int g = 0; g < kG; ++g) {
+      int pc = __popc(qc[0] ^ c[g][0]);
+      pc = __popc(qc[1] ^ c[g][1]) + pc;
+      pc = __popc(qc[2] ^ c[g][2]) + pc;
+      pc = __popc(qc[3] ^ c[g][3]) + pc;
+      float e = fq * f[g];  // rabitq_estimate's operations up to the 2^-7 scale
+      e = e * static_cast<float>(kD - 2 * pc);
+      hits |= static_cast<uint64_t>(!(e < t128)) << (j0 + g);  // NaN estimates are candidates too
+    }
+  }
+  hits &= nk >= 64 ? ~0ull : ((1ull << nk) - 1ull);
+  // exact re-check of the (few) candidates, in index order
+  uint64_t exact = 0;
+  for (uint64_t m = hits; m != 0; m &= m - 1) {
+    const int j = __builtin_ctzll(m);
+    const u32x4_t c = s_kc[wave][j];
+    const int pc = __popc(qc[0] ^ c[0]) + __popc(qc[1] ^ c[1]) + __popc(qc[2] ^ c[2]) + __popc(qc[3] ^ c[3]);
+    float est = fq * s_fk[wave][j];
+    est = est * static_cast<float>(kD - 2 * pc);
+    if (ordered_key_f(est * 0.0078125f) >= t) exact |= 1ull << j;
+  }
+  const int mine = __popcll(exact);
+  s_cnt[wave][lane] = mine;
+  __syncthreads();
+  int before = 0, total = 0;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const int c = s_cnt[w][lane];
+    before += w < wave ? c : 0;
+    total += c;
+  }
+  uint32_t* row = s_bkt[lane];
+  if (wave == 0) row[0] = static_cast<uint32_t>(total);
+  int e = before;
+  for (uint64_t m = exact; m != 0 && e < kFiltCap; m &= m - 1, ++e) {
+    const int j = __builtin_ctzll(m);
+    const u32x4_t c = s_kc[wave][j];
+    const int pc = __popc(qc[0] ^ c[0]) + __popc(qc[1] ^ c[1]) + __popc(qc[2] ^ c[2]) + __popc(qc[3] ^ c[3]);
+    float est = fq * s_fk[wave][j];
+    est = est * static_cast<float>(kD - 2 * pc);
+    row[2 + 2 * e] = ordered_key_f(est * 0.0078125f);
+    row[3 + 2 * e] = static_cast<uint32_t>(p0 + j);
+  }
+  __syncthreads();
+  // ---- the buckets out: 4 threads per bucket, 8 words each, as two 16-byte
+  //      stores (entries past the count are left unspecified) ----
+  {
+    const int b = threadIdx.x >> 2, part = threadIdx.x & 3;
+    const int qb = blockIdx.y * 64 + b;
+    if (qb < queries) {
+      const uint32_t* src = s_bkt[b] + 8 * part;
+      u32x4_t lo, hi;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        lo[w] = src[w];
+        hi[w] = src[4 + w];
+      }
+      u32x4_t* dst = reinterpret_cast<u32x4_t*>(buckets + ((pool * queries + qb) * n_lists + list) * kBucketWords +
+                                                8 * part);
+      dst[0] = lo;
+      dst[1] = hi;
+    }
+  }
+}
+
+// Exact k-th largest key over all n positions of a pool, keys recomputed by
+// key_at(p) each round (the select kernel's fallback): the radix_select rounds
+// with the items streamed from the codes instead of held in registers.
+template <int NT, typename KeyAt>
+__device__ void radix_select_stream(KeyAt&& key_at, int64_t n, int k, const SelectSmem& sm, uint32_t& T,
+                                    int& take_eq) {
+  constexpr int W = Block<NT>::kWaves;
+  const int tid = threadIdx.x, wave = tid >> 6;
+  uint32_t lo = 0u, hi = 0xFFFFFFFFu;
+  int rem = k;
+  while (true) {
+    uint32_t mn = 0xFFFFFFFFu, mx = 0u;
+    for (int64_t p = tid; p < n; p += NT) {
+      const uint32_t key = key_at(p);
+      if (key >= lo && key <= hi) {
+        mn = min(mn, key);
+        mx = max(mx, key);
+      }
+    }
+    Block<NT>::minmax(mn, mx, sm.tmp);
+    lo = mn;
+    hi = mx;
+    if (lo == hi) break;
+    const int bits = 32 - __clz(static_cast<int>(hi - lo));
+    const int shift = bits > 8 ? bits - 8 : 0;
+    for (int i = tid; i < W * 256; i += NT) sm.hist[i] = 0;
+    __syncthreads();
+    for (int64_t p = tid; p < n; p += NT) {
+      const uint32_t key = key_at(p);
+      if (key >= lo && key <= hi) atomicAdd(&sm.hist[wave * 256 + ((key - lo) >> shift)], 1);
+    }
+    __syncthreads();
+    for (int b = tid; b < 256; b += NT) {
+      int c = 0;
+#pragma unroll
+      for (int w = 0; w < W; ++w) c += sm.hist[w * 256 + b];
+      sm.hist[b] = c;
+    }
+    __syncthreads();
+    if (tid < 64) {
+      int c[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) c[j] = sm.hist[4 * tid + j];
+      const int lane_sum = c[0] + c[1] + c[2] + c[3];
+      int suf = lane_sum;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const int v = __shfl_down(suf, off);
+        if (tid + off < 64) suf += v;
+      }
+      int above = suf - lane_sum;
+#pragma unroll
+      for (int j = 3; j >= 0; --j) {
+        const int at_or_above = above + c[j];
+        if (at_or_above >= rem && above < rem) {
+          sm.bin[0] = 4 * tid + j;
+          sm.bin[1] = above;
+        }
+        above = at_or_above;
+      }
+    }
+    __syncthreads();
+    const uint32_t b = static_cast<uint32_t>(sm.bin[0]);
+    rem -= sm.bin[1];
+    __syncthreads();
+    const uint64_t new_lo = static_cast<uint64_t>(lo) + (static_cast<uint64_t>(b) << shift);
+    const uint64_t new_hi = new_lo + (1ull << shift) - 1ull;
+    lo = static_cast<uint32_t>(new_lo);
+    hi = static_cast<uint32_t>(new_hi < hi ? new_hi : hi);
+    if (shift == 0) break;
+  }
+  T = lo;
+  take_eq = rem;
+}
+
+// ----------------------------------------------------------------------------
+// 3. select, per (query, pool), 1024 threads.
+//    Gather: pass r reads chunks r*1024 + t of the query's buckets (coalesced);
+//    chunk c of a bucket holds its entries 2c - 1 and 2c, so every thread owns
+//    2 items per pass, straight from the load, in increasing index order
+//    (pass, thread, item); the bucket's count comes from its chunk 0 through
+//    a lane swizzle.  One block reduction gives the overflow flag, the number
+//    of entries and their key range.  The exact k-th key then comes from the
+//    radix rounds over the registers, and one scan per pass of packed
+//    (above, equal) counts places the selected indices in index order.
+//    Otherwise (a list beyond kFiltCap, or fewer than k keys at or above
+//    tau) the block selects over all n keys, estimates recomputed per pass.
+//    Then the exact rerank and the sort by (score desc, index asc).
+// ----------------------------------------------------------------------------
+template <int R>
+__global__ __launch_bounds__(kBigNT) void rabitq_select_kernel(
+    const uint32_t* __restrict__ buckets, int n_lists,
+    const uint8_t* __restrict__ q_codes, const uint16_t* __restrict__ q_fac, const uint8_t* __restrict__ codes_k,
+    const uint16_t* __restrict__ fac_k, int k, const uint16_t* __restrict__ q, const uint16_t* __restrict__ keys,
+    int64_t k_pool_stride, int64_t k_row_stride, int64_t n, int queries, int64_t* __restrict__ out_cand,
+    int64_t* __restrict__ out_idx, float* __restrict__ out_score) {
+  constexpr int NT = kBigNT, W = NT / 64, NI = 2 * R;
+  __shared__ int s_hist[2 * 4096];
+  __shared__ __attribute__((aligned(16))) uint32_t s_tmp[(R > 4 ? R : 4) * W + 2];
+  __shared__ int32_t s_sel[kMaxTopk];
+  __shared__ float s_score[kMaxTopk];
+  __shared__ __attribute__((aligned(16))) uint64_t s_rkey[kMaxTopk + 1];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t pool = blockIdx.y;
+  const int64_t pq = pool * queries + blockIdx.x;
+
+  // ---- gather ----
+  const u32x4_t* bq = reinterpret_cast<const u32x4_t*>(buckets + pq * n_lists * kBucketWords);
+  const int n_chunks = n_lists * (kBucketWords / 4);
+  u32x4_t ch[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int ci = r * NT + tid;
+    ch[r] = ci < n_chunks ? bq[ci] : u32x4_t{0u, 0u, 0u, 0u};
+  }
+#pragma unroll
+  for (int j = 0; j < 4096 / NT; ++j) s_hist[tid * (4096 / NT) + j] = 0;  // the radix's first histogram
+  const int part = tid & 7;  // chunk of the bucket
+  uint32_t key[NI], idx[NI], valid = 0u;
+  int overflow = 0;
+  uint32_t mn = 0xFFFFFFFFu, mx = 0u;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    // the bucket's count from its chunk 0 (lane & ~7 of this 32-lane half);
+    // chunks past the last bucket are zero
+    const int c = __builtin_amdgcn_ds_swizzle(static_cast<int>(ch[r][0]), 0x18);
+    const int kept = c < kFiltCap ? c : kFiltCap;
+    overflow |= c > kFiltCap;
+    key[2 * r] = ch[r][0];      // entry 2 * part - 1 (chunk 0: count and pad)
+    idx[2 * r] = ch[r][1];
+    key[2 * r + 1] = ch[r][2];  // entry 2 * part
+    idx[2 * r + 1] = ch[r][3];
+    if (part >= 1 && 2 * part - 1 < kept) valid |= 1u << (2 * r);
+    if (2 * part < kept) valid |= 1u << (2 * r + 1);
+  }
+#pragma unroll
+  for (int j = 0; j < NI; ++j) {
+    if ((valid >> j) & 1u) {
+      mn = min(mn, key[j]);
+      mx = max(mx, key[j]);
+    }
+  }
+  {  // block reduction: overflow, entries, key range (also orders the clear)
+    const uint32_t w_ovf = wave_max_u32(static_cast<uint32_t>(overflow));
+    const int w_cnt = wave_sum(__popc(valid));
+    const uint32_t w_mn = wave_min_u32(mn), w_mx = wave_max_u32(mx);
+    if (lane == 0) {
+      s_tmp[4 * wave] = w_ovf;
+      s_tmp[4 * wave + 1] = static_cast<uint32_t>(w_cnt);
+      s_tmp[4 * wave + 2] = w_mn;
+      s_tmp[4 * wave + 3] = w_mx;
+    }
+    __syncthreads();
+    overflow = 0;
+    int total = 0;
+    mn = 0xFFFFFFFFu;
+    mx = 0u;
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      const u32x4_t v = reinterpret_cast<const u32x4_t*>(s_tmp)[w];
+      overflow |= static_cast<int>(v[0]);
+      total += static_cast<int>(v[1]);
+      mn = min(mn, v[2]);
+      mx = max(mx, v[3]);
+    }
+    __syncthreads();
+    valid = (overflow == 0 && total >= k) ? valid : 0u;
+    overflow = overflow != 0 || total < k;  // from here: the fallback is needed
+  }
+
+  if (!overflow) {
+    uint32_t T;
+    int take_eq;
+    block_radix_select12<NT, NI>(key, valid, k, mn, mx, s_hist, s_tmp, T, take_eq);
+    __syncthreads();  // its last reads of s_tmp are done
+    // packed (above T, equal to T) counts per pass, scanned over the threads
+    int cnt[R], incl[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      int gt = 0, eq = 0;
+#pragma unroll
+      for (int j = 2 * r; j < 2 * r + 2; ++j) {
+        if ((valid >> j) & 1u) {
+          gt += key[j] > T;
+          eq += key[j] == T;
+        }
+      }
+      cnt[r] = gt | (eq << 16);
+      incl[r] = wave_incl_sum(cnt[r]);
+      if (lane == 63) s_tmp[r * W + wave] = static_cast<uint32_t>(incl[r]);
+    }
+    __syncthreads();
+    int gt_before = 0, eq_before = 0;  // in the passes before r
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      int pass_total = 0, waves_before = 0;
+#pragma unroll
+      for (int w = 0; w < W; ++w) {
+        const int v = static_cast<int>(s_tmp[r * W + w]);
+        pass_total += v;
+        waves_before += w < wave ? v : 0;
+      }
+      const int before = waves_before + incl[r] - cnt[r];
+      int g = gt_before + (before & 0xFFFF), e = eq_before + (before >> 16);
+#pragma unroll
+      for (int j = 2 * r; j < 2 * r + 2; ++j) {
+        if ((valid >> j) & 1u) {
+          if (key[j] > T) {
+            s_sel[g + (e < take_eq ? e : take_eq)] = static_cast<int32_t>(idx[j]);
+            ++g;
+          } else if (key[j] == T) {
+            if (e < take_eq) s_sel[g + e] = static_cast<int32_t>(idx[j]);
+            ++e;
+          }
+        }
+      }
+      gt_before += pass_total & 0xFFFF;
+      eq_before += pass_total >> 16;
+    }
+  } else {
+    // fallback: select over the whole pool, estimates recomputed per pass
+    const u32x4_t qc = *reinterpret_cast<const u32x4_t*>(q_codes + pq * 16);
+    const float fq = query_factor(q_fac, pq);
+    const u32x4_t* kc = reinterpret_cast<const u32x4_t*>(codes_k) + pool * n;
+    const uint32_t* kf = reinterpret_cast<const uint32_t*>(fac_k) + pool * n;
+    auto key_at = [&](int64_t p) { return ordered_key_f(rabitq_estimate(qc, fq, kc[p], kf[p])); };
+    SelectSmem sm{s_hist, s_tmp, reinterpret_cast<int*>(s_tmp + 2 * W)};
+    uint32_t T;
+    int take_eq;
+    radix_select_stream<NT>(key_at, n, k, sm, T, take_eq);
+    // ordered emit: positions in index order, ties at T by lowest index
+    int emitted = 0, eq_seen = 0;
+    for (int64_t c0 = 0; c0 < n; c0 += NT) {
+      const int64_t p = c0 + tid;
+      const uint32_t kp = p < n ? key_at(p) : 0u;
+      const int is_eq = p < n && kp == T;
+      int eq_total = 0;
+      const int eq_b = eq_seen + Block<NT>::excl_scan(is_eq, reinterpret_cast<int*>(s_tmp), eq_total);
+      const int sel = p < n && (kp > T || (is_eq && eq_b < take_eq));
+      int sel_total = 0;
+      const int pos = emitted + Block<NT>::excl_scan(sel, reinterpret_cast<int*>(s_tmp), sel_total);
+      if (sel && pos < k) s_sel[pos] = static_cast<int32_t>(p);
+      emitted += sel_total;
+      eq_seen += eq_total;
+      if (emitted >= k) break;
+    }
+  }
+  __syncthreads();
+  for (int i = tid; i < k; i += NT) out_cand[pq * k + i] = s_sel[i];
+
+  // ---- exact rerank: 16-lane groups (one DPP row), lane l holds dims
+  //      8l .. 8l+7; a group's rows (up to 4 per pass) are requested before
+  //      any is used; the row sum halves by rotations 8, 4, 2, 1 (the same
+  //      pairs as an xor butterfly, so the same sums) ----
+  {
+    const int l = tid & 15, grp = tid >> 4;
+    constexpr int kGroups = NT / 16;
+    constexpr int kRows = 4;
+    const u32x4_t qw = *reinterpret_cast<const u32x4_t*>(q + pq * kD + 8 * l);
+    float qf[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qf[e] = f16_to_f32(static_cast<uint16_t>(qw[e >> 1] >> (16 * (e & 1))));
+    const uint16_t* kp = keys + pool * k_pool_stride;
+    for (int c0 = 0; c0 < k; c0 += kRows * kGroups) {
+      u32x4_t kw[kRows];
+#pragma unroll
+      for (int r = 0; r < kRows; ++r) {
+        const int c = c0 + r * kGroups + grp;
+        const int64_t ki = c < k ? static_cast<int64_t>(s_sel[c]) : -1;
+        kw[r] = (ki >= 0 && ki < n) ? *reinterpret_cast<const u32x4_t*>(kp + ki * k_row_stride + 8 * l)
+                                    : u32x4_t{0u, 0u, 0u, 0u};
+      }
+#pragma unroll
+      for (int r = 0; r < kRows; ++r) {
+        const int c = c0 + r * kGroups + grp;
+        float sc = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float pe = qf[e] * f16_to_f32(static_cast<uint16_t>(kw[r][e >> 1] >> (16 * (e & 1))));
+          sc = e == 0 ? pe : sc + pe;
+        }
+        sc = sc + __int_as_float(ZKV_ROR(__float_as_int(sc), 8));
+        sc = sc + __int_as_float(ZKV_ROR(__float_as_int(sc), 4));
+        sc = sc + __int_as_float(ZKV_ROR(__float_as_int(sc), 2));
+        sc = sc + __int_as_float(ZKV_ROR(__float_as_int(sc), 1));
+        if (c < k && l == 0) {
+          s_score[c] = sc;
+          // (score, slot) -> one key, larger = earlier: +-0 compare equal,
+          // equal scores rank by slot (= by index)
+          s_rkey[c] = (static_cast<uint64_t>(ordered_key_f(sc + 0.0f)) << 32) | (0xFFFFFFFFu - c);
         }
       }
     }
+    if (tid == 0) s_rkey[k] = 0ull;  // pads an odd k's last pair (below every slot key)
   }
   __syncthreads();
-  for (int i = tid; i < k; i += kNT2) {
-    const int slot = static_cast<int>(0xFFFFu - static_cast<uint32_t>(s_sort[i] & 0xFFFFu));
-    out_idx[pq * k + i] = s_sel[slot];
-    out_score[pq * k + i] = s_score[slot];
+  // ---- order: slot i goes to its rank, the number of larger slot keys.
+  //      Groups of P lanes (a power of two <= 16, one DPP row at most) hold 4
+  //      slots each; lane p of a group compares them with the 16-byte key
+  //      pairs p, p + P, ... (adjacent lanes read adjacent pairs: no bank
+  //      conflicts), and the group sums its counts by lane swizzles ----
+  {
+    const int groups = (k + 3) >> 2;
+    int lp = 4;
+    while (lp > 0 && (groups << lp) > NT) --lp;
+    const int P = 1 << lp;
+    const int g = tid >> lp, p = tid & (P - 1);
+    const bool active = g < groups;
+    const u32x4_t* rk = reinterpret_cast<const u32x4_t*>(s_rkey);
+    uint64_t ki[4];
+    {
+      const int gg = active ? g : 0;
+      const u32x4_t a = rk[2 * gg], b = rk[2 * gg + 1];
+      ki[0] = a[0] | (static_cast<uint64_t>(a[1]) << 32);
+      ki[1] = a[2] | (static_cast<uint64_t>(a[3]) << 32);
+      ki[2] = b[0] | (static_cast<uint64_t>(b[1]) << 32);
+      ki[3] = b[2] | (static_cast<uint64_t>(b[3]) << 32);
+    }
+    int rank[4] = {0, 0, 0, 0};
+    const int pairs = (k + 1) >> 1;
+    for (int c = p; c < pairs; c += P) {
+      const u32x4_t v = rk[c];
+      const uint64_t k0 = v[0] | (static_cast<uint64_t>(v[1]) << 32);
+      const uint64_t k1 = v[2] | (static_cast<uint64_t>(v[3]) << 32);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) rank[i] += static_cast<int>(k0 > ki[i]) + static_cast<int>(k1 > ki[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (P > 1) rank[i] += swizzle_xor<1>(rank[i]);
+      if (P > 2) rank[i] += swizzle_xor<2>(rank[i]);
+      if (P > 4) rank[i] += swizzle_xor<4>(rank[i]);
+      if (P > 8) rank[i] += swizzle_xor<8>(rank[i]);
+    }
+    if (active && p == 0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int slot = 4 * g + i;
+        if (slot < k) {
+          out_idx[pq * k + rank[i]] = s_sel[slot];
+          out_score[pq * k + rank[i]] = s_score[slot];
+        }
+      }
+    }
   }
 }
 
@@ -463,20 +1254,36 @@ int stage1_slice(int64_t n, int topk) {
 }
 
 struct SearchLayout {
+  bool filter;
   int slice, n_slices;
-  size_t q_codes, q_fac, cand_key, cand_idx, total;
+  size_t q_codes, q_fac, tau, counts, cand_key, cand_idx, total;
 };
 
 SearchLayout search_layout(int pools, int queries, int64_t n, int topk) {
   SearchLayout L{};
   const int64_t pq = static_cast<int64_t>(pools) * queries;
-  L.slice = stage1_slice(n, topk);
-  L.n_slices = static_cast<int>((n + L.slice - 1) / L.slice);
   auto up = [](size_t b) { return (b + 255) & ~static_cast<size_t>(255); };
+  L.filter = use_filter_path(n, topk);
   L.q_codes = 0;
   L.q_fac = up(pq * 16);
-  L.cand_key = L.q_fac + up(pq * 4);
-  const size_t cand = static_cast<size_t>(pq) * L.n_slices * topk;
+  L.tau = L.q_fac + up(pq * 4);
+  size_t cand;
+  if (L.filter) {
+    // cand_key: the lists' 128-byte buckets
+    L.slice = kFiltList;
+    L.n_slices = static_cast<int>((n + kFiltList - 1) / kFiltList);
+    L.counts = L.tau + up(pq * 4);
+    L.cand_key = L.counts;
+    L.cand_idx = L.cand_key;
+    L.total = L.cand_key + up(static_cast<size_t>(pq) * L.n_slices * kBucketWords * 4);
+    return L;
+  } else {
+    L.slice = stage1_slice(n, topk);
+    L.n_slices = static_cast<int>((n + L.slice - 1) / L.slice);
+    L.counts = L.tau;
+    L.cand_key = L.tau;
+    cand = static_cast<size_t>(pq) * L.n_slices * topk;
+  }
   L.cand_idx = L.cand_key + up(cand * 4);
   L.total = L.cand_idx + up(cand * 4);
   return L;
@@ -541,7 +1348,7 @@ extern "C" int zkv_rabitq_search(const uint16_t* q, const uint16_t* keys, int64_
   ZKV_REQUIRE(topk > 0 && topk <= kMaxTopk && topk <= n,
               "zkv_rabitq_search: topk=%d must be in [1, min(n=%lld, %d)]", topk, (long long)n, kMaxTopk);
   const SearchLayout L = search_layout(pools, queries, n, topk);
-  ZKV_REQUIRE(static_cast<int64_t>(L.n_slices) * topk <= kMaxCand2,
+  ZKV_REQUIRE(L.filter || static_cast<int64_t>(L.n_slices) * topk <= kMaxCand2,
               "zkv_rabitq_search: %d slices of %d keys x topk %d exceed %d candidates per query",
               L.n_slices, L.slice, topk, kMaxCand2);
   ZKV_REQUIRE(workspace_bytes >= L.total, "zkv_rabitq_search: workspace of %zu bytes < %zu",
@@ -556,6 +1363,37 @@ extern "C" int zkv_rabitq_search(const uint16_t* q, const uint16_t* keys, int64_
   uint16_t* q_fac = reinterpret_cast<uint16_t*>(ws + L.q_fac);
   uint32_t* c_key = reinterpret_cast<uint32_t*>(ws + L.cand_key);
   int32_t* c_idx = reinterpret_cast<int32_t*>(ws + L.cand_idx);
+  if (L.filter) {
+    const FilterPlan f = filter_plan(n, topk);
+    uint32_t* tau = reinterpret_cast<uint32_t*>(ws + L.tau);
+    uint32_t* buckets = reinterpret_cast<uint32_t*>(ws + L.cand_key);
+    rabitq_prep_kernel<<<dim3(queries, pools), kBigNT, 0, s>>>(q, signs, codes, factors, n, queries, f.s_count,
+                                                                f.m, q_codes, q_fac, tau);
+    int rc = check_launch("rabitq_prep_kernel");
+    if (rc != ZKV_OK) return rc;
+    rabitq_filter_kernel<<<dim3(L.n_slices, (queries + 63) / 64, pools), 256, 0, s>>>(
+        q_codes, q_fac, tau, codes, factors, n, queries, L.n_slices, buckets);
+    rc = check_launch("rabitq_filter_kernel");
+    if (rc != ZKV_OK) return rc;
+    const dim3 gs(queries, pools);
+    switch (select_passes(n)) {
+#define ZKV_SELECT(R)                                                                                        \
+  case R:                                                                                                    \
+    rabitq_select_kernel<R><<<gs, kBigNT, 0, s>>>(buckets, L.n_slices, q_codes, q_fac, codes, factors, topk, \
+                                                  q, keys, k_pool_stride, k_row_stride, n, queries,         \
+                                                  cand_idx, final_idx, final_scores);                       \
+    break;
+      ZKV_SELECT(1)
+      ZKV_SELECT(2)
+      ZKV_SELECT(4)
+      ZKV_SELECT(8)
+      ZKV_SELECT(16)
+#undef ZKV_SELECT
+      default:
+        return fail(ZKV_EINVAL, "zkv_rabitq_search: no select kernel for n=%lld", (long long)n);
+    }
+    return check_launch("rabitq_select_kernel");
+  }
   int rc = launch_encode(q, kD, static_cast<int64_t>(pools) * queries, signs, q_codes, q_fac, s);
   if (rc != ZKV_OK) return rc;
   dim3 g1(L.n_slices, queries, pools);
