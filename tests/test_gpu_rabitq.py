@@ -164,6 +164,34 @@ def test_search_c4_full_size(rng):
     assert np.array_equal(np.sort(fidx, axis=-1), cand)
 
 
+@pytest.mark.parametrize("N,topk", [(131072, 256), (20000, 256)])
+def test_search_query_encode_in_workspace(rng, N, topk):
+    """The search encodes its queries into the workspace's first two regions
+    (codes [P*Q, 16] at byte 0, factors [P*Q, 2] fp16 at the next 256-byte
+    boundary).  Both paths' encodes equal the oracle's, bits included: the
+    filter path's prep kernel encodes across the lanes of one wave, and a
+    wrong factor would not show in the results (it scales every estimate of
+    its query alike)."""
+    from zoomkv_revision_amd.rabitq import rabitq_encode, rabitq_search, search_workspace
+    s_np, s_t = _signs()
+    P, Q = 2, 5
+    keys = orq.clustered_unit_keys(rng, N, 16)
+    qs = np.concatenate([orq.clustered_unit_keys(rng, P * Q - 2, 16),
+                         f16_bits((rng.standard_normal((1, 128)) * 300).astype(np.float32)),
+                         np.zeros((1, 128), np.uint16)])                    # large norm; zero vector
+    kt = _f16(np.stack([keys, keys]))
+    codes, fac = rabitq_encode(kt, s_t)
+    ws = search_workspace(P, Q, N, topk, "cuda")
+    ws.fill_(0xAB)
+    rabitq_search(_f16(qs.reshape(P, Q, 128)), kt, codes, fac, s_t, topk, workspace=ws)
+    torch.cuda.synchronize()
+    w = from_torch(ws)
+    off = (P * Q * 16 + 255) // 256 * 256
+    cq, fq = orq.encode(qs, s_np)
+    assert np.array_equal(w[:P * Q * 16].reshape(P * Q, 16), cq)
+    assert np.array_equal(w[off:off + P * Q * 4].view(np.uint16).reshape(P * Q, 2), fq)
+
+
 def test_search_rejects_bad_sizes():
     from zoomkv_revision_amd.rabitq import rabitq_search
     s = torch.ones(128, device="cuda")

@@ -565,15 +565,21 @@ FilterPlan filter_plan(int64_t n, int topk) {
   return f;
 }
 
-// select passes: 1024 threads read 128 buckets (1024 16-byte chunks) per pass
-int select_passes(int64_t n) {
+// select block: NT threads read NT / 8 buckets (NT 16-byte chunks) per pass,
+// R passes.  1024 threads: the block's phases are latency-bound, and 16 waves
+// hide more of it than 4 (256 threads took 21 us instead of 13.5 for C4)
+struct SelectShape {
+  int nt, passes;
+};
+SelectShape select_shape(int64_t n) {
   const int64_t lists = (n + kFiltList - 1) / kFiltList;
+  const int nt = kBigNT;
   int r = 1;
-  while (128ll * r < lists) r <<= 1;
-  return r;
+  while (static_cast<int64_t>(nt / 8) * r < lists) r <<= 1;
+  return {nt, r};
 }
 
-bool use_filter_path(int64_t n, int topk) { return n >= 128ll * topk && select_passes(n) <= kSelMaxPasses; }
+bool use_filter_path(int64_t n, int topk) { return n >= 128ll * topk && select_shape(n).passes <= kSelMaxPasses; }
 
 // k-th largest key (and how many keys equal to it to take, lowest positions
 // first) among the valid items (bit j of `valid`: item j) of a block of NT
@@ -628,14 +634,16 @@ __device__ void block_radix_select12(const uint32_t (&key)[NI], uint32_t valid, 
 #pragma unroll
     for (int w = 0; w < W; ++w) waves_above += w > wave ? static_cast<int>(tmp[w]) : 0;
     int above = waves_above + wave_total - incl;  // items in higher bins than this thread's
+    if (above < rem && above + own >= rem) {       // the k-th largest lies in this thread's bins
 #pragma unroll
-    for (int j = kPerT - 1; j >= 0; --j) {
-      const int at_or_above = above + c[j];
-      if (at_or_above >= rem && above < rem) {
-        tmp[W] = static_cast<uint32_t>(tid * kPerT + j);
-        tmp[W + 1] = static_cast<uint32_t>(above);
+      for (int j = kPerT - 1; j >= 0; --j) {
+        const int at_or_above = above + c[j];
+        if (at_or_above >= rem && above < rem) {
+          tmp[W] = static_cast<uint32_t>(tid * kPerT + j);
+          tmp[W + 1] = static_cast<uint32_t>(above);
+        }
+        above = at_or_above;
       }
-      above = at_or_above;
     }
     __syncthreads();
     const uint32_t b = tmp[W];
@@ -667,8 +675,8 @@ __global__ __launch_bounds__(kBigNT) void rabitq_prep_kernel(
     const uint16_t* __restrict__ fac_k, int64_t n, int queries, int s_count, int m,
     uint8_t* __restrict__ q_codes, uint16_t* __restrict__ q_fac, uint32_t* __restrict__ tau) {
   constexpr int NI = kSampleMax / kBigNT;
-  __shared__ __attribute__((aligned(16))) float s_x[kD];
-  __shared__ __attribute__((aligned(16))) float s_y[kD];
+  __shared__ __attribute__((aligned(16))) float s_terms[3][kD + 4];  // x_d^2, y_d^2, |y_d| (rows 4 banks apart)
+  __shared__ float s_sums[3];
   __shared__ u32x4_t s_qc;
   __shared__ float s_fq;
   __shared__ int s_hist[2 * 4096];
@@ -703,48 +711,61 @@ __global__ __launch_bounds__(kBigNT) void rabitq_prep_kernel(
       y0 = a + b;
       y1 = a - b;
     }
-#pragma unroll
-    for (int hl = 1; hl < 64; hl <<= 1) {  // h = 2 hl: partner lane l ^ hl
-      const float p0 = __shfl_xor(y0, hl), p1 = __shfl_xor(y1, hl);
+    // h = 2 hl: partner lane l ^ hl (DPP for 1, 2; swizzles for 4, 8, 16)
+    auto stage = [&](float p0, float p1, int hl) {
       const bool lower = (lane & hl) == 0;
       y0 = lower ? y0 + p0 : p0 - y0;
       y1 = lower ? y1 + p1 : p1 - y1;
-    }
+    };
+    auto fi = [](float v) { return __float_as_int(v); };
+    stage(__int_as_float(__builtin_amdgcn_update_dpp(0, fi(y0), 0xB1, 0xF, 0xF, false)),
+          __int_as_float(__builtin_amdgcn_update_dpp(0, fi(y1), 0xB1, 0xF, 0xF, false)), 1);
+    stage(__int_as_float(__builtin_amdgcn_update_dpp(0, fi(y0), 0x4E, 0xF, 0xF, false)),
+          __int_as_float(__builtin_amdgcn_update_dpp(0, fi(y1), 0x4E, 0xF, 0xF, false)), 2);
+    stage(__int_as_float(swizzle_xor<4>(fi(y0))), __int_as_float(swizzle_xor<4>(fi(y1))), 4);
+    stage(__int_as_float(swizzle_xor<8>(fi(y0))), __int_as_float(swizzle_xor<8>(fi(y1))), 8);
+    stage(__int_as_float(swizzle_xor<16>(fi(y0))), __int_as_float(swizzle_xor<16>(fi(y1))), 16);
+    stage(__shfl_xor(y0, 32), __shfl_xor(y1, 32), 32);
     // code bit d = (y_d >= 0): dims 2l / 2l + 1 are bit l of the two ballots
     const uint64_t be = __ballot(y0 >= 0.0f), bo = __ballot(y1 >= 0.0f);
-    s_x[2 * lane] = x0;
-    s_x[2 * lane + 1] = x1;
-    s_y[2 * lane] = y0;
-    s_y[2 * lane + 1] = y1;
+    // the factor sums' terms, formed in parallel (the same products)
+    s_terms[0][2 * lane] = x0 * x0;
+    s_terms[0][2 * lane + 1] = x1 * x1;
+    s_terms[1][2 * lane] = y0 * y0;
+    s_terms[1][2 * lane + 1] = y1 * y1;
+    s_terms[2][2 * lane] = fabsf(y0);
+    s_terms[2][2 * lane + 1] = fabsf(y1);
     if (lane < 4) {  // word w = dims 32w .. 32w + 31 = ballot bits 16w .. 16w + 15, interleaved
-      uint32_t word = 0;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        word |= static_cast<uint32_t>((be >> (16 * lane + i)) & 1ull) << (2 * i);
-        word |= static_cast<uint32_t>((bo >> (16 * lane + i)) & 1ull) << (2 * i + 1);
-      }
+      auto spread = [](uint32_t v) {  // bit i -> bit 2i (16 bits)
+        v = (v | (v << 8)) & 0x00FF00FFu;
+        v = (v | (v << 4)) & 0x0F0F0F0Fu;
+        v = (v | (v << 2)) & 0x33333333u;
+        return (v | (v << 1)) & 0x55555555u;
+      };
+      const uint32_t word = spread(static_cast<uint32_t>(be >> (16 * lane)) & 0xFFFFu) |
+                            (spread(static_cast<uint32_t>(bo >> (16 * lane)) & 0xFFFFu) << 1);
       reinterpret_cast<uint32_t*>(q_codes + pq * 16)[lane] = word;
       reinterpret_cast<uint32_t*>(&s_qc)[lane] = word;
     }
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS writes are done
     __builtin_amdgcn_wave_barrier();
-    if (lane == 0) {  // sums in dimension order (the encode kernel's arithmetic)
-      float nsq = 0.0f, ysq = 0.0f, yabs = 0.0f;
-#pragma unroll 4
-      for (int c = 0; c < kD / 8; ++c) {
-        float xv[8], yv[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          xv[e] = s_x[8 * c + e];
-          yv[e] = s_y[8 * c + e];
-        }
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          nsq = nsq + xv[e] * xv[e];
-          ysq = ysq + yv[e] * yv[e];
-          yabs = yabs + fabsf(yv[e]);
-        }
+    if (lane < 3) {  // lane j: sum of terms j in dimension order (the encode kernel's arithmetic)
+      const float4* t = reinterpret_cast<const float4*>(s_terms[lane]);
+      float acc = 0.0f;
+#pragma unroll 8
+      for (int c = 0; c < kD / 4; ++c) {
+        const float4 v = t[c];
+        acc = acc + v.x;
+        acc = acc + v.y;
+        acc = acc + v.z;
+        acc = acc + v.w;
       }
+      s_sums[lane] = acc;
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_wave_barrier();
+    if (lane == 0) {
+      const float nsq = s_sums[0], ysq = s_sums[1], yabs = s_sums[2];
       const float norm = sqrtf(nsq);
       const float corr = yabs > 0.0f ? (sqrtf(ysq) * kSqrt128) / yabs : 0.0f;
       const uint16_t hn = f32_to_f16_bits(norm), hc = f32_to_f16_bits(corr);
@@ -990,14 +1011,14 @@ __device__ void radix_select_stream(KeyAt&& key_at, int64_t n, int k, const Sele
 //    tau) the block selects over all n keys, estimates recomputed per pass.
 //    Then the exact rerank and the sort by (score desc, index asc).
 // ----------------------------------------------------------------------------
-template <int R>
-__global__ __launch_bounds__(kBigNT) void rabitq_select_kernel(
+template <int NT, int R>
+__global__ __launch_bounds__(NT) void rabitq_select_kernel(
     const uint32_t* __restrict__ buckets, int n_lists,
     const uint8_t* __restrict__ q_codes, const uint16_t* __restrict__ q_fac, const uint8_t* __restrict__ codes_k,
     const uint16_t* __restrict__ fac_k, int k, const uint16_t* __restrict__ q, const uint16_t* __restrict__ keys,
     int64_t k_pool_stride, int64_t k_row_stride, int64_t n, int queries, int64_t* __restrict__ out_cand,
     int64_t* __restrict__ out_idx, float* __restrict__ out_score) {
-  constexpr int NT = kBigNT, W = NT / 64, NI = 2 * R;
+  constexpr int W = NT / 64, NI = 2 * R;
   __shared__ int s_hist[2 * 4096];
   __shared__ __attribute__((aligned(16))) uint32_t s_tmp[(R > 4 ? R : 4) * W + 2];
   __shared__ int32_t s_sel[kMaxTopk];
@@ -1010,31 +1031,39 @@ __global__ __launch_bounds__(kBigNT) void rabitq_select_kernel(
   // ---- gather ----
   const u32x4_t* bq = reinterpret_cast<const u32x4_t*>(buckets + pq * n_lists * kBucketWords);
   const int n_chunks = n_lists * (kBucketWords / 4);
-  u32x4_t ch[R];
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int ci = r * NT + tid;
-    ch[r] = ci < n_chunks ? bq[ci] : u32x4_t{0u, 0u, 0u, 0u};
-  }
 #pragma unroll
   for (int j = 0; j < 4096 / NT; ++j) s_hist[tid * (4096 / NT) + j] = 0;  // the radix's first histogram
   const int part = tid & 7;  // chunk of the bucket
-  uint32_t key[NI], idx[NI], valid = 0u;
+  // item j: key[j]; its index = bucket * 256 + byte j of idx8 (a bucket is one
+  // 256-key list)
+  uint32_t key[NI], idx8[(NI + 3) / 4], valid = 0u;
+#pragma unroll
+  for (int j = 0; j < (NI + 3) / 4; ++j) idx8[j] = 0u;
   int overflow = 0;
   uint32_t mn = 0xFFFFFFFFu, mx = 0u;
+  constexpr int RB = R < 8 ? R : 8;  // chunks in flight per thread
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    // the bucket's count from its chunk 0 (lane & ~7 of this 32-lane half);
-    // chunks past the last bucket are zero
-    const int c = __builtin_amdgcn_ds_swizzle(static_cast<int>(ch[r][0]), 0x18);
-    const int kept = c < kFiltCap ? c : kFiltCap;
-    overflow |= c > kFiltCap;
-    key[2 * r] = ch[r][0];      // entry 2 * part - 1 (chunk 0: count and pad)
-    idx[2 * r] = ch[r][1];
-    key[2 * r + 1] = ch[r][2];  // entry 2 * part
-    idx[2 * r + 1] = ch[r][3];
-    if (part >= 1 && 2 * part - 1 < kept) valid |= 1u << (2 * r);
-    if (2 * part < kept) valid |= 1u << (2 * r + 1);
+  for (int r0 = 0; r0 < R; r0 += RB) {
+    u32x4_t ch[RB];
+#pragma unroll
+    for (int b = 0; b < RB; ++b) {
+      const int ci = (r0 + b) * NT + tid;
+      ch[b] = ci < n_chunks ? bq[ci] : u32x4_t{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int b = 0; b < RB; ++b) {
+      const int r = r0 + b;
+      // the bucket's count from its chunk 0 (lane & ~7 of this 32-lane half);
+      // chunks past the last bucket are zero
+      const int c = __builtin_amdgcn_ds_swizzle(static_cast<int>(ch[b][0]), 0x18);
+      const int kept = c < kFiltCap ? c : kFiltCap;
+      overflow |= c > kFiltCap;
+      key[2 * r] = ch[b][0];      // entry 2 * part - 1 (chunk 0: count and pad)
+      key[2 * r + 1] = ch[b][2];  // entry 2 * part
+      idx8[r >> 1] |= ((ch[b][1] & 255u) | ((ch[b][3] & 255u) << 8)) << (16 * (r & 1));
+      if (part >= 1 && 2 * part - 1 < kept) valid |= 1u << (2 * r);
+      if (2 * part < kept) valid |= 1u << (2 * r + 1);
+    }
   }
 #pragma unroll
   for (int j = 0; j < NI; ++j) {
@@ -1077,7 +1106,7 @@ __global__ __launch_bounds__(kBigNT) void rabitq_select_kernel(
     block_radix_select12<NT, NI>(key, valid, k, mn, mx, s_hist, s_tmp, T, take_eq);
     __syncthreads();  // its last reads of s_tmp are done
     // packed (above T, equal to T) counts per pass, scanned over the threads
-    int cnt[R], incl[R];
+    int excl[R];  // within the wave
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       int gt = 0, eq = 0;
@@ -1088,37 +1117,41 @@ __global__ __launch_bounds__(kBigNT) void rabitq_select_kernel(
           eq += key[j] == T;
         }
       }
-      cnt[r] = gt | (eq << 16);
-      incl[r] = wave_incl_sum(cnt[r]);
-      if (lane == 63) s_tmp[r * W + wave] = static_cast<uint32_t>(incl[r]);
+      const int cnt = gt | (eq << 16);
+      const int incl = wave_incl_sum(cnt);
+      excl[r] = incl - cnt;
+      if (lane == 63) s_tmp[r * W + wave] = static_cast<uint32_t>(incl);
     }
     __syncthreads();
-    int gt_before = 0, eq_before = 0;  // in the passes before r
+    if (wave == 0) {  // (pass, wave) totals -> exclusive offsets, in index order
+      int carry = 0;
+      for (int i0 = 0; i0 < R * W; i0 += 64) {
+        const bool in = i0 + lane < R * W;
+        const int v = in ? static_cast<int>(s_tmp[i0 + lane]) : 0;
+        const int inc = wave_incl_sum(v);
+        if (in) s_tmp[i0 + lane] = static_cast<uint32_t>(carry + inc - v);
+        carry += __builtin_amdgcn_readlane(inc, 63);
+      }
+    }
+    __syncthreads();
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      int pass_total = 0, waves_before = 0;
-#pragma unroll
-      for (int w = 0; w < W; ++w) {
-        const int v = static_cast<int>(s_tmp[r * W + w]);
-        pass_total += v;
-        waves_before += w < wave ? v : 0;
-      }
-      const int before = waves_before + incl[r] - cnt[r];
-      int g = gt_before + (before & 0xFFFF), e = eq_before + (before >> 16);
+      const int before = static_cast<int>(s_tmp[r * W + wave]) + excl[r];
+      int g = before & 0xFFFF, e = before >> 16;
+      const int32_t list0 = ((r * NT + tid) >> 3) * kFiltList;
 #pragma unroll
       for (int j = 2 * r; j < 2 * r + 2; ++j) {
+        const int32_t ix = list0 + static_cast<int32_t>((idx8[j >> 2] >> (8 * (j & 3))) & 255u);
         if ((valid >> j) & 1u) {
           if (key[j] > T) {
-            s_sel[g + (e < take_eq ? e : take_eq)] = static_cast<int32_t>(idx[j]);
+            s_sel[g + (e < take_eq ? e : take_eq)] = ix;
             ++g;
           } else if (key[j] == T) {
-            if (e < take_eq) s_sel[g + e] = static_cast<int32_t>(idx[j]);
+            if (e < take_eq) s_sel[g + e] = ix;
             ++e;
           }
         }
       }
-      gt_before += pass_total & 0xFFFF;
-      eq_before += pass_total >> 16;
     }
   } else {
     // fallback: select over the whole pool, estimates recomputed per pass
@@ -1152,13 +1185,13 @@ __global__ __launch_bounds__(kBigNT) void rabitq_select_kernel(
   for (int i = tid; i < k; i += NT) out_cand[pq * k + i] = s_sel[i];
 
   // ---- exact rerank: 16-lane groups (one DPP row), lane l holds dims
-  //      8l .. 8l+7; a group's rows (up to 4 per pass) are requested before
+  //      8l .. 8l+7; a pass covers 256 rows, a group's rows requested before
   //      any is used; the row sum halves by rotations 8, 4, 2, 1 (the same
   //      pairs as an xor butterfly, so the same sums) ----
   {
     const int l = tid & 15, grp = tid >> 4;
     constexpr int kGroups = NT / 16;
-    constexpr int kRows = 4;
+    constexpr int kRows = 4096 / NT;  // 256 rows per pass
     const u32x4_t qw = *reinterpret_cast<const u32x4_t*>(q + pq * kD + 8 * l);
     float qf[8];
 #pragma unroll
@@ -1376,18 +1409,19 @@ extern "C" int zkv_rabitq_search(const uint16_t* q, const uint16_t* keys, int64_
     rc = check_launch("rabitq_filter_kernel");
     if (rc != ZKV_OK) return rc;
     const dim3 gs(queries, pools);
-    switch (select_passes(n)) {
-#define ZKV_SELECT(R)                                                                                        \
-  case R:                                                                                                    \
-    rabitq_select_kernel<R><<<gs, kBigNT, 0, s>>>(buckets, L.n_slices, q_codes, q_fac, codes, factors, topk, \
+    const SelectShape sh = select_shape(n);
+    switch (sh.nt * 100 + sh.passes) {
+#define ZKV_SELECT(NT, R)                                                                                     \
+  case NT * 100 + R:                                                                                          \
+    rabitq_select_kernel<NT, R><<<gs, NT, 0, s>>>(buckets, L.n_slices, q_codes, q_fac, codes, factors, topk, \
                                                   q, keys, k_pool_stride, k_row_stride, n, queries,         \
                                                   cand_idx, final_idx, final_scores);                       \
     break;
-      ZKV_SELECT(1)
-      ZKV_SELECT(2)
-      ZKV_SELECT(4)
-      ZKV_SELECT(8)
-      ZKV_SELECT(16)
+      ZKV_SELECT(1024, 1)
+      ZKV_SELECT(1024, 2)
+      ZKV_SELECT(1024, 4)
+      ZKV_SELECT(1024, 8)
+      ZKV_SELECT(1024, 16)
 #undef ZKV_SELECT
       default:
         return fail(ZKV_EINVAL, "zkv_rabitq_search: no select kernel for n=%lld", (long long)n);
