@@ -77,8 +77,9 @@ def cpu_baseline(cache, q, budget_s: float = 12.0):
                       f"calls ({t * 1e3:.0f} ms each); host {os.cpu_count()} logical CPUs, 1 used"}
 
 
-def read_traffic():
-    path = os.path.join(ROOT, "profiles", "kivi4_attn_c2_traffic.json")
+def read_traffic(name: str = "kivi4_attn_c2_traffic.json"):
+    """HBM bytes per launch from a committed counter summary under profiles/."""
+    path = os.path.join(ROOT, "profiles", name)
     try:
         with open(path) as f:
             return json.load(f).get("hbm_bytes_per_launch")
@@ -441,8 +442,8 @@ def run_c4(args):
                    "keys": n, "queries": nq, "topk": topk, "clusters": 64, "pools_rotated": n_pools,
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
-                     "kernel": "rabitq_search (encode + stage 1 + stage 2)", "kernel_ms": k_ms,
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": read_traffic("c4_rabitq_search_traffic.json"),
+                     "kernel": "rabitq_search (prep + filter + select)", "kernel_ms": k_ms,
                      "algorithmic_bytes": algo},
         "cpu_baseline": cpu,
     }
