@@ -311,8 +311,9 @@ def run_h2d(args):
 def run_c3(args):
     """C3: GQA-mean query + Quest bounds over fp16 page metadata (2048 pages of
     16 tokens, one launch) -> top-128 pages -> page-sparse 4-bit attention,
-    batch 8, 32/8 heads, 32768 tokens; six planted workloads rotate between
-    steps."""
+    batch 8, 32/8 heads, 32768 tokens; eight planted workloads rotate between
+    steps (8 x 86 MB touched per step: Quest metadata 67.6 MB plus the selected
+    pages, more than the 256 MB last-level cache)."""
     import numpy as np
     import torch
     from zoomkv_revision_amd import kivi, synthetic
@@ -320,7 +321,7 @@ def run_c3(args):
     from zoomkv_revision_amd.topk import float_topk_3d
     bs, hq, kv, n_tok, n_sel = 8, 32, 8, 32768, 128
     dev = torch.device("cuda:0")
-    ws = [synthetic.c3_workload(100 + i, bs, hq, kv, n_tok, n_sel, dev) for i in range(6)]
+    ws = [synthetic.c3_workload(100 + i, bs, hq, kv, n_tok, n_sel, dev) for i in range(8)]
     n_pages = ws[0]["n_pages"]
     scores = torch.empty(bs, kv, n_pages, device=dev)
     raw_q = torch.empty(bs, kv, 128, dtype=torch.bfloat16, device=dev)

@@ -25,16 +25,23 @@ need no cross-lane movement:
   k_meta   fp16  [bs, kv, G, 16, 2, 8] [..., p, 0, s] = scale of channel
            8p + KSLOT[s], [..., p, 1, s] = zero (min) of that channel,
            KSLOT = (0, 4, 1, 5, 2, 6, 3, 7)
-  v_codes  int32 [bs, kv, G, 512]  word (j//4)*256 + l*4 + j%4 (l = 16g + c) holds,
-           for channel d = 32(j//2) + 2c + j%2, in nibble k the code of token
-           32G + TAU[g][VELEM[k]]
-  v_meta   fp16  [bs, kv, G, 4, 4, 2, 8] [..., gd, r, 0, e] = scale of token
-           32G + TAU[r][e] for channel group gd (channels 32gd..32gd+31),
-           [..., 1, e] = zero
-  TAU[r] = (4r, 4r+1, 4r+2, 4r+3, 16+4r, 17+4r, 18+4r, 19+4r)
-  VELEM[k] = 2*(k % 4) + k // 4
-Word l*4 + s of each 1 KiB half is what MFMA lane l of the decode kernel
-consumes, so a lane's operands are two contiguous 16-byte reads.
+  v_codes  int32 [bs, kv, G, 512]  word m*256 + l*4 + P (l = 16g + c, half m,
+           channel pair P) holds channels d = 32P + 2c and d + 1 of tokens
+           32G + 16m + 4g + i: nibble n is token i = n//4 + 2(n%2) of channel
+           d + (n//2)%2, i.e. nibbles (0, 4, 1, 5) = channel d, tokens
+           (0, 1, 2, 3), nibbles (2, 6, 3, 7) = channel d + 1
+  v_meta   fp16  [bs, kv, G, 2, 4, 4, 2, 4] [..., m, gd, r, 0, i] = scale of
+           token 32G + 16m + 4r + i for channel group gd (channels
+           32gd..32gd+31), [..., 1, i] = zero
+Word l*4 + s of each 1 KiB block is what MFMA lane l of the decode kernel
+consumes, so a lane's operands are contiguous 16-byte reads.  Each 16-token
+half m of a group (one Quest page) has its own K code block (words m*256..),
+V code block and 256-byte V metadata block; only the 512-byte K metadata is
+shared by the two halves, so one page reads 2816 of the record's 5120 bytes.
+The V-MFMA's k-slice of lane group g is tokens TAU[g] = (4g..4g+3,
+16+4g..16+4g+3) -- where the K-MFMA leaves those scores -- so the decode
+kernel takes the half-0 word for its elements 0-3 and the half-1 word for
+4-7.
 """
 from __future__ import annotations
 
@@ -47,9 +54,10 @@ from .numerics import BF16_1EM8, bf16r, f16_bits, f16_to_f32, f32
 LEVELS = 15
 GROUP_Q = 32                       # Format Q: tokens per K group / tile
 KSLOT = np.array([0, 4, 1, 5, 2, 6, 3, 7])
-VELEM = np.array([2 * (k % 4) + k // 4 for k in range(8)])
 TAU = np.array([[4 * r + e if e < 4 else 16 + 4 * r + (e - 4) for e in range(8)]
                 for r in range(4)])
+VNIB_TOK = np.array([n // 4 + 2 * (n % 2) for n in range(8)])   # token i of nibble n
+VNIB_CH = np.array([(n // 2) % 2 for n in range(8)])            # channel d + VNIB_CH[n]
 
 
 # ---------------------------------------------------------------------------
@@ -160,7 +168,7 @@ class Kivi4Cache:
     k_codes: np.ndarray   # int32  [bs, kv, G, 512] (lane order)
     k_meta: np.ndarray    # uint16 (fp16 bits) [bs, kv, G, 16, 2, 8]
     v_codes: np.ndarray   # int32  [bs, kv, G, 512] (lane order)
-    v_meta: np.ndarray    # uint16 (fp16 bits) [bs, kv, G, 4, 4, 2, 8]
+    v_meta: np.ndarray    # uint16 (fp16 bits) [bs, kv, G, 2, 4, 4, 2, 4]
 
     @property
     def n_groups(self) -> int:
@@ -182,23 +190,26 @@ def k_words_from_lane_order(words: np.ndarray) -> np.ndarray:
     return np.ascontiguousarray(w).reshape(sh + (16, 32))
 
 
-def v_words_to_lane_order(words: np.ndarray) -> np.ndarray:
-    """[.., G, 4 (r), 128 (d)] -> [.., G, 512] lane order.
+def v_codes_to_words(vc: np.ndarray) -> np.ndarray:
+    """V codes [.., 32 (token), 128 (channel)] of a group -> [.., 512] int32 words."""
+    sh = vc.shape[:-2]
+    x = vc.astype(np.uint64).reshape(sh + (2, 4, 4, 4, 16, 2))   # [m, g, i, P, c, jp]
+    words = np.zeros(sh + (2, 4, 16, 4), dtype=np.uint64)        # [m, g, c, P]
+    for n in range(8):
+        nib = x[..., VNIB_TOK[n], :, :, VNIB_CH[n]]               # [m, g, P, c]
+        words |= np.swapaxes(nib, -1, -2) << np.uint64(4 * n)
+    return words.astype(np.uint32).view(np.int32).reshape(sh + (512,))
 
-    Word (M-tile j, lane 16r + c) sits at (j // 4) * 256 + (16r + c) * 4 + j % 4
-    and holds channel d = 32 (j // 2) + 2c + j % 2.
-    """
-    sh = words.shape[:-2]
-    w = words.reshape(sh + (4, 2, 2, 16, 2))                # [r, jh, gl, c, jp], j = 4jh + 2gl + jp
-    w = np.moveaxis(w, (-5, -4, -3, -2, -1), (-4, -5, -2, -3, -1))  # -> [jh, r, c, gl, jp]
-    return np.ascontiguousarray(w).reshape(sh + (512,))
 
-
-def v_words_from_lane_order(words: np.ndarray) -> np.ndarray:
+def v_words_to_codes(words: np.ndarray) -> np.ndarray:
+    """Inverse of v_codes_to_words: [.., 512] int32 -> codes [.., 32, 128] uint8."""
     sh = words.shape[:-1]
-    w = words.reshape(sh + (2, 4, 16, 2, 2))                # [jh, r, c, gl, jp]
-    w = np.moveaxis(w, (-5, -4, -3, -2, -1), (-4, -5, -2, -3, -1))  # -> [r, jh, gl, c, jp]
-    return np.ascontiguousarray(w).reshape(sh + (4, 128))
+    w = words.view(np.uint32).astype(np.uint64).reshape(sh + (2, 4, 16, 4))   # [m, g, c, P]
+    vc = np.empty(sh + (2, 4, 4, 4, 16, 2), dtype=np.uint8)                  # [m, g, i, P, c, jp]
+    for n in range(8):
+        nib = ((w >> np.uint64(4 * n)) & np.uint64(15)).astype(np.uint8)
+        vc[..., VNIB_TOK[n], :, :, VNIB_CH[n]] = np.swapaxes(nib, -1, -2)
+    return vc.reshape(sh + (32, 128))
 
 
 def quantize_kivi4(k: np.ndarray, v: np.ndarray) -> Kivi4Cache:
@@ -225,20 +236,13 @@ def quantize_kivi4(k: np.ndarray, v: np.ndarray) -> Kivi4Cache:
     vmn = vg.min(axis=4)
     vmx = vg.max(axis=4)
     vc = kivi_codes(vg, vmn[..., None], vmx[..., None]).reshape(bs, kv, ng, GROUP_Q, d)
-    vsc = kivi_scale(vmn, vmx).reshape(bs, kv, ng, GROUP_Q, 4)
-    vmn_g = vmn.reshape(bs, kv, ng, GROUP_Q, 4)
-    tok = TAU[:, VELEM]                                                 # [4 r, 8 k]
-    v_codes = np.zeros((bs, kv, ng, 4, d), dtype=np.uint64)
-    for kk in range(8):
-        nib = vc[:, :, :, tok[:, kk], :].astype(np.uint64)              # [.., ng, 4, 128]
-        v_codes |= nib << np.uint64(4 * kk)
-    v_codes = v_words_to_lane_order(v_codes.astype(np.uint32).view(np.int32))
-    v_meta = np.empty((bs, kv, ng, 4, 4, 2, 8), dtype=np.uint16)
-    # v_meta[..., gd, r, 0, e] = scale of token TAU[r][e], channel group gd
-    sc_t = vsc[:, :, :, TAU, :]                                         # [.., ng, 4 r, 8 e, 4 gd]
-    mn_t = vmn_g[:, :, :, TAU, :]
-    v_meta[..., 0, :] = f16_bits(np.moveaxis(sc_t, -1, 3))
-    v_meta[..., 1, :] = f16_bits(np.moveaxis(mn_t, -1, 3))
+    v_codes = v_codes_to_words(vc)
+    # v_meta[..., m, gd, r, 0, i] = scale of token 16m + 4r + i, channel group gd
+    vsc = kivi_scale(vmn, vmx).reshape(bs, kv, ng, 2, 4, 4, 4)        # [.., m, r, i, gd]
+    vmn_g = vmn.reshape(bs, kv, ng, 2, 4, 4, 4)
+    v_meta = np.empty((bs, kv, ng, 2, 4, 4, 2, 4), dtype=np.uint16)
+    v_meta[..., 0, :] = f16_bits(np.moveaxis(vsc, -1, -3))
+    v_meta[..., 1, :] = f16_bits(np.moveaxis(vmn_g, -1, -3))
     return Kivi4Cache(k_codes, k_meta, v_codes, v_meta)
 
 
@@ -277,16 +281,10 @@ def dequant_kivi4(c: Kivi4Cache, dtype=np.float64):
     kzr[..., chan] = kmeta[..., 1, :].reshape(bs, kv, ng, 128)
     k_hat = kcodes * ksc[:, :, :, None, :] + kzr[:, :, :, None, :]
     # V
-    vw = v_words_from_lane_order(c.v_codes).view(np.uint32).astype(np.uint64)  # [.., ng, 4, 128]
-    vcode = np.empty((bs, kv, ng, GROUP_Q, 128), dtype=dtype)
-    tok = TAU[:, VELEM]
-    for kk in range(8):
-        vcode[:, :, :, tok[:, kk], :] = ((vw >> np.uint64(4 * kk)) & np.uint64(15)).astype(dtype)
-    vmeta = f16_to_f32(c.v_meta).astype(dtype)                                # [.., ng, gd, r, 2, e]
-    vsc = np.empty((bs, kv, ng, GROUP_Q, 4), dtype=dtype)
-    vzr = np.empty((bs, kv, ng, GROUP_Q, 4), dtype=dtype)
-    vsc[:, :, :, TAU, :] = np.moveaxis(vmeta[..., 0, :], 3, -1)
-    vzr[:, :, :, TAU, :] = np.moveaxis(vmeta[..., 1, :], 3, -1)
+    vcode = v_words_to_codes(c.v_codes).astype(dtype)                          # [.., ng, 32, 128]
+    vmeta = f16_to_f32(c.v_meta).astype(dtype)                                # [.., ng, m, gd, r, 2, i]
+    vsc = np.moveaxis(vmeta[..., 0, :], -3, -1).reshape(bs, kv, ng, GROUP_Q, 4)
+    vzr = np.moveaxis(vmeta[..., 1, :], -3, -1).reshape(bs, kv, ng, GROUP_Q, 4)
     vsc = np.repeat(vsc, 32, axis=-1)
     vzr = np.repeat(vzr, 32, axis=-1)
     v_hat = vcode * vsc + vzr

@@ -133,22 +133,48 @@ def test_lane_order_relayouts_are_the_documented_bijections(rng):
     w = rng.integers(0, 2 ** 31, size=(3, 16, 32)).astype(np.int32)
     lo = kivi.k_words_to_lane_order(w)
     assert np.array_equal(kivi.k_words_from_lane_order(lo), w)
-    v = rng.integers(0, 2 ** 31, size=(3, 4, 128)).astype(np.int32)
-    lv = kivi.v_words_to_lane_order(v)
-    assert np.array_equal(kivi.v_words_from_lane_order(lv), v)
+    vc = rng.integers(0, 16, size=(3, 32, 128)).astype(np.uint8)
+    vw = kivi.v_codes_to_words(vc)
+    assert np.array_equal(kivi.v_words_to_codes(vw), vc)
+    assert np.array_equal(kivi.v_codes_to_words(kivi.v_words_to_codes(
+        rng.integers(-2 ** 31, 2 ** 31, size=(2, 512)).astype(np.int32))).shape, (2, 512))
     for m in range(2):
         for g in range(4):
             for c in range(16):
                 for s in range(4):
                     assert lo[1, m * 256 + (16 * g + c) * 4 + s] == w[1, 4 * s + g, 16 * m + c]
-    # V: word of M-tile j, lane 16g + c is channel 32(j // 2) + 2c + j % 2, so
-    # each 16-row M-tile stays inside one 32-channel scale group
-    for j in range(8):
+    # V: lane 16g + c's word P of half m holds channels 32P + 2c, 32P + 2c + 1
+    # (one 32-channel scale group) and only tokens 16m + 4g .. 16m + 4g + 3
+    for m in range(2):
         for g in range(4):
             for c in range(16):
-                d = 32 * (j // 2) + 2 * c + j % 2
-                assert lv[2, (j // 4) * 256 + (16 * g + c) * 4 + j % 4] == v[2, g, d]
-                assert d // 32 == j // 2
+                for P in range(4):
+                    w = int(vw[2, m * 256 + (16 * g + c) * 4 + P]) & 0xFFFFFFFF
+                    got = sorted(((w >> (4 * n)) & 15) for n in range(8))
+                    want = sorted(int(x) for x in vc[2, 16 * m + 4 * g:16 * m + 4 * g + 4,
+                                                     32 * P + 2 * c:32 * P + 2 * c + 2].reshape(-1))
+                    assert got == want
+
+
+def test_format_q_pages_are_separate_blocks(rng):
+    """A 16-token page (half of a 32-token group) owns K code words m*256..,
+    V code words m*256.. and V metadata block m; changing the other half's
+    tokens leaves them untouched (only the per-channel K metadata is shared)."""
+    k = gaussian_bf16(rng, (1, 2, 64, 128), outlier_channels=2)
+    v = gaussian_bf16(rng, (1, 2, 64, 128))
+    a = kivi.quantize_kivi4(k, v)
+    for m in range(2):
+        k2, v2 = k.copy(), v.copy()
+        other = slice(16 * (1 - m), 16 * (1 - m) + 16)
+        for t in (other, slice(32 + 16 * (1 - m), 32 + 16 * (1 - m) + 16)):
+            v2[:, :, t] = gaussian_bf16(rng, v2[:, :, t].shape)
+            k2[:, :, t] = np.clip(gaussian_bf16(rng, k2[:, :, t].shape), k.min(), k.max())
+        b = kivi.quantize_kivi4(k2, v2)
+        own = slice(256 * m, 256 * m + 256)
+        assert np.array_equal(a.v_codes[..., own], b.v_codes[..., own])
+        assert np.array_equal(a.v_meta[..., m, :, :, :, :], b.v_meta[..., m, :, :, :, :])
+        assert not np.array_equal(a.v_codes[..., 256 * (1 - m):256 * (1 - m) + 256],
+                                  b.v_codes[..., 256 * (1 - m):256 * (1 - m) + 256])
 
 
 def test_format_q_metadata_and_codes_consistent(rng):

@@ -47,7 +47,10 @@
 // V-MFMA (one per j = 0..7): A = V codes^T (row c = channel 32(j/2) + 2c +
 //   j%2, so each M-tile lies in one 32-channel scale group), B = P * scale,
 //   k-slice element e of lane group g is token TAU[g][e] = 4g+e | 16+4g+e-4,
-//   which is exactly where the K-MFMA left that token's score.
+//   which is exactly where the K-MFMA left that token's score.  Elements 0-3
+//   come from the V code word of the first 16-token half, 4-7 from the
+//   second's: every half (one Quest page) has its own K codes, V codes and
+//   V scale/zero block, so the page-sparse mode loads 2816 B for a page.
 // Code operand element order (one int32 word, nibble k = bits 4k..4k+3):
 //   (n0, n4, n1, n5, n2, n6, n3, n7); elements 2, 3, 6, 7 carry a factor 16,
 //   which the B operands undo (1/16 on K's, 16 on V's other elements).
@@ -129,16 +132,57 @@ __device__ __forceinline__ void wait_tiles_in_flight(int later) {
   __builtin_amdgcn_sched_barrier(0);
 }
 
+// The same for tiles of 5 or 3 DMA ops: `ops` ops were issued after the last
+// one of the tile needed now (at most 3 later tiles of 5).
+__device__ __forceinline__ void wait_ops_in_flight(int ops) {
+  switch (ops) {
+    case 0: wait_vmcnt<0>(); break;
+    case 1: wait_vmcnt<1>(); break;
+    case 2: wait_vmcnt<2>(); break;
+    case 3: wait_vmcnt<3>(); break;
+    case 4: wait_vmcnt<4>(); break;
+    case 5: wait_vmcnt<5>(); break;
+    case 6: wait_vmcnt<6>(); break;
+    case 7: wait_vmcnt<7>(); break;
+    case 8: wait_vmcnt<8>(); break;
+    case 9: wait_vmcnt<9>(); break;
+    case 10: wait_vmcnt<10>(); break;
+    case 11: wait_vmcnt<11>(); break;
+    case 12: wait_vmcnt<12>(); break;
+    case 13: wait_vmcnt<13>(); break;
+    case 14: wait_vmcnt<14>(); break;
+    default: wait_vmcnt<15>(); break;
+  }
+  __builtin_amdgcn_sched_barrier(0);
+}
+
 __device__ __forceinline__ u32x4_t ld16(const void* p) {
   return *reinterpret_cast<const u32x4_t*>(p);
 }
 
+using u32x2_t = uint32_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ u32x2_t ld8(const void* p) {
+  return *reinterpret_cast<const u32x2_t*>(p);
+}
+
+// DMA ops of a tile with half mask `mask` (bit m: tokens 16m .. 16m + 15)
+__device__ __forceinline__ int tile_dma_ops(uint32_t mask) { return mask == 3u ? 5 : 3; }
+
 __device__ __forceinline__ void issue_tile(const AttnParams& p, int64_t bh, int gi, int lane,
-                                           uint8_t* stage) {
+                                           uint8_t* stage, uint32_t mask = 3u) {
   // the record is 5 contiguous KiB: 5 loads of 64 lanes x 16 B
   const uint8_t* rec = reinterpret_cast<const uint8_t*>(p.groups + (bh * p.g_cap + gi) * kRecordWords) + 16 * lane;
+  if (mask == 3u) {
 #pragma unroll
-  for (int i = 0; i < 5; ++i) dma16(rec + 1024 * i, stage + 1024 * i);
+    for (int i = 0; i < 5; ++i) dma16(rec + 1024 * i, stage + 1024 * i);
+  } else {
+    // one 16-token half m: its K codes, its V codes, and of the metadata KiB
+    // the K scale/zero (lanes 0-31) and its V scale/zero (lanes 32 + 16m ..)
+    const int m = mask == 2u ? 1 : 0;
+    dma16(rec + 1024 * m, stage + 1024 * m);
+    dma16(rec + 2048 + 1024 * m, stage + 2048 + 1024 * m);
+    if (lane < 32 || (lane >> 4) == 2 + m) dma16(rec + 4096, stage + 4096);
+  }
 }
 
 // One code word as an MFMA operand of exact fp16 subnormals:
@@ -147,6 +191,15 @@ __device__ __forceinline__ void issue_tile(const AttnParams& p, int64_t bh, int 
 __device__ __forceinline__ half8_t codes8(uint32_t w) {
   const uint32_t w8 = w >> 8;
   const u32x4_t r = {w & 0x000F000Fu, w & 0x00F000F0u, w8 & 0x000F000Fu, w8 & 0x00F000F0u};
+  return __builtin_bit_cast(half8_t, r);
+}
+
+// The V-MFMA code operand from the two halves' words of a channel pair:
+// elements 0-3 from h0's nibbles (0, 4, 1, 5) >> shift, elements 4-7 from h1's
+// (shift 0: the pair's first channel, 8: its second), same scaling as codes8.
+__device__ __forceinline__ half8_t codes8_halves(uint32_t h0, uint32_t h1, int shift) {
+  const uint32_t a = h0 >> shift, b = h1 >> shift;
+  const u32x4_t r = {a & 0x000F000Fu, a & 0x00F000F0u, b & 0x000F000Fu, b & 0x00F000F0u};
   return __builtin_bit_cast(half8_t, r);
 }
 
@@ -292,10 +345,19 @@ __device__ __forceinline__ void compute_tile(const uint8_t* st, int lane, int c,
   if (!(half_mask & 2u)) S[1] = float4_t{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
   const half8_t pb = softmax_step(S, kTwo24, zc, tc.qs, tc.qs24, m_run, L, O, OZ);
 
-  const u32x4_t vq0 = ld16(st + 2048 + 16 * lane);
-  const u32x4_t vq1 = ld16(st + 3072 + 16 * lane);
+  // V code words of channel pairs P = 0..3 of each half, and the halves' V
+  // scale/zero blocks (entry (gd, r): 4 scales, then 4 zeros of tokens 16m + 4r
+  // + i); the k-slice's elements 0-3 are half 0, 4-7 half 1.  An unselected
+  // half was not loaded: its scale/zero enter as 0 (its P is 0 as well).
+  const u32x4_t vh0 = ld16(st + 2048 + 16 * lane);
+  const u32x4_t vh1 = ld16(st + 3072 + 16 * lane);
   const uint8_t* vm = st + 4608;
-  const u32x4_t vz = ld16(vm + ((c & 3) * 4 + g) * 32 + 16);  // zero points of group c & 3
+  auto vmeta8 = [&](int entry, int off) {
+    const u32x2_t a = ld8(vm + entry * 16 + off), b2 = ld8(vm + 256 + entry * 16 + off);
+    const bool h0 = half_mask & 1u, h1 = half_mask & 2u;
+    return u32x4_t{h0 ? a[0] : 0u, h0 ? a[1] : 0u, h1 ? b2[0] : 0u, h1 ? b2[1] : 0u};
+  };
+  const u32x4_t vz = vmeta8((c & 3) * 4 + g, 8);  // zero points of group c & 3
   OZ = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(vz), pb, OZ, 0, 0, 0);
   // P * 16 on the low-nibble elements 0, 1, 4, 5
   half8_t pm = pb;
@@ -311,12 +373,11 @@ __device__ __forceinline__ void compute_tile(const uint8_t* st, int lane, int c,
   }
 #pragma unroll
   for (int G = 0; G < 4; ++G) {
-    const half8_t bv = as_half8(ld16(vm + (4 * G + g) * 32)) * pm;
+    const half8_t bv = as_half8(vmeta8(4 * G + g, 0)) * pm;
 #pragma unroll
     for (int jp = 0; jp < 2; ++jp) {
-      const int j = 2 * G + jp;
-      const uint32_t w = j < 4 ? vq0[j] : vq1[j - 4];
-      O[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(codes8(w), bv, O[j], 0, 0, 0);
+      const int j = 2 * G + jp;  // channel 32G + 2c + jp
+      O[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(codes8_halves(vh0[G], vh1[G], 8 * jp), bv, O[j], 0, 0, 0);
     }
   }
 }
@@ -495,13 +556,19 @@ void kivi4_attn_kernel(const AttnParams p) {
     else
       return T0 + wave + NW * k;
   };
+  auto mask_of = [&](int k) -> uint32_t {
+    if constexpr (kSparse)
+      return static_cast<uint32_t>(__builtin_amdgcn_readlane(my_mask, k));
+    else
+      return 3u;
+  };
 
   // Start the HBM stream before anything else.
   int issued = 0;
 #pragma unroll
   for (int k = 0; k < D - 1; ++k)
     if (issued < nq) {
-      issue_tile(p, bh, group_of(issued), lane, ring[issued % D]);
+      issue_tile(p, bh, group_of(issued), lane, ring[issued % D], mask_of(issued));
       ++issued;
     }
 
@@ -538,11 +605,17 @@ void kivi4_attn_kernel(const AttnParams p) {
     // ---- quantized tiles through this wave's D-stage LDS ring ----
     for (int k = 0; k < nq; ++k) {
       if (issued < nq) {
-        issue_tile(p, bh, group_of(issued), lane, ring[issued % D]);
+        issue_tile(p, bh, group_of(issued), lane, ring[issued % D], mask_of(issued));
         ++issued;
       }
-      const uint32_t half_mask = kSparse ? static_cast<uint32_t>(__builtin_amdgcn_readlane(my_mask, k)) : 3u;
-      wait_tiles_in_flight(issued - 1 - k);
+      const uint32_t half_mask = mask_of(k);
+      if constexpr (kSparse) {
+        int later = 0;  // DMA ops issued after tile k's
+        for (int t = k + 1; t < issued; ++t) later += tile_dma_ops(mask_of(t));
+        wait_ops_in_flight(later);
+      } else {
+        wait_tiles_in_flight(issued - 1 - k);
+      }
       compute_tile(ring[k % D], lane, c, g, tc, half_mask, m_run, L, O, OZ);
     }
     // O to real units: O * 2^20 + sum P z of the M-tile's group (OZ component
@@ -705,6 +778,11 @@ struct SplitPlan {
   int n_splits, tiles_per_split;
 };
 
+// Page-sparse shape: a wave holds only a few tiles (C3: ~4), so its loop is a
+// chain of DMA round trips; a 4-stage ring issues them together (8 x 4 x 5 KiB
+// = the 160 KiB of LDS: one workgroup per CU, 2 waves per SIMD).
+constexpr int kSparseNW = 8, kSparseD = 4;
+
 // Kernel shape: NW waves per workgroup, D ring stages per wave.
 // ZKV_ATTN_SHAPE=NWxD (e.g. 4x2) overrides the default for tuning sweeps.
 struct Shape {
@@ -725,9 +803,8 @@ Shape attn_shape() {
   return sh;
 }
 
-SplitPlan plan_splits(int bs, int kv, int n_groups, int res_len, int n_splits) {
+SplitPlan plan_splits(int bs, int kv, int n_groups, int res_len, int n_splits, Shape sh = attn_shape()) {
   const int n_tiles = std::max(n_groups + (res_len + kTile - 1) / kTile, 1);
-  const Shape sh = attn_shape();
   int ns = n_splits;
   if (ns <= 0) {
     const int wg_per_cu = std::max(1, std::min((160 * 1024) / (sh.nw * sh.d * kStageBytes), 16 / sh.nw));
@@ -751,7 +828,10 @@ SplitPlan plan_splits(int bs, int kv, int n_groups, int res_len, int n_splits) {
 }
 
 // Workspace layout: split partials o fp32 [bs, kv, S, gqa, 128] followed by
-// (m, l) fp32 [bs, kv, S, gqa, 2].
+// (m, l) fp32 [bs, kv, S, gqa, 2].  The splits merge in a second kernel: a
+// merge by the last split inside the launch needs a device-scope fence per
+// workgroup, which cost more than that kernel (C2 148 us instead of 129, C3
+// step 43.9 us instead of 38.4).
 size_t workspace_bytes_for(int bs, int hq, int /*kv*/, int n_splits) {
   return static_cast<size_t>(bs) * hq * n_splits * (128 + 2) * sizeof(float);
 }
@@ -760,7 +840,7 @@ void launch_attn(const AttnParams& p, int bs, hipStream_t s) {
   const dim3 grid(p.n_splits, p.kv, bs);
   const Shape sh = attn_shape();
   if (p.pages != nullptr) {
-    kivi4_attn_kernel<8, 2, true><<<grid, 512, 0, s>>>(p);
+    kivi4_attn_kernel<kSparseNW, kSparseD, true><<<grid, 64 * kSparseNW, 0, s>>>(p);
   } else if (p.n_groups == 0) {  // bf16 rows only: the 16-byte V layout
     kivi4_attn_kernel<8, 2, false, true><<<grid, 512, 0, s>>>(p);
   } else if (sh.nw == 8) {
@@ -800,8 +880,8 @@ struct SparsePages {
 // Sparse mode: every split is planned for the longest page list (n_sel
 // tiles); each wave keeps at most 64 tile descriptors in its lanes.
 SplitPlan plan_sparse_splits(int bs, int kv, int n_sel, int res_len, int n_splits) {
-  SplitPlan sp = plan_splits(bs, kv, n_sel, res_len, n_splits);
-  constexpr int kMaxPerSplit = 64 * 8;
+  SplitPlan sp = plan_splits(bs, kv, n_sel, res_len, n_splits, Shape{kSparseNW, kSparseD});
+  constexpr int kMaxPerSplit = 64 * kSparseNW;
   if (sp.tiles_per_split > kMaxPerSplit) {
     const int n_tiles = n_sel + (res_len + kTile - 1) / kTile;
     sp.n_splits = (n_tiles + kMaxPerSplit - 1) / kMaxPerSplit;

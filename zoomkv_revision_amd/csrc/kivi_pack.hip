@@ -68,18 +68,14 @@ __global__ __launch_bounds__(128) void chunk_encode_kernel(
 
 // ------------------------------- Format Q ---------------------------------
 // One 32-token group of one KV head is a 5120-byte record (int32 words):
-//   [0, 512) K code words, [512, 1024) V code words,
-//   [1024, 1152) K scale/zero (fp16 pairs), [1152, 1280) V scale/zero.
+//   [0, 512) K code words (half m = tokens 16m .. 16m + 15 at m*256),
+//   [512, 1024) V code words (half m at 512 + m*256),
+//   [1024, 1152) K scale/zero (fp16 pairs, shared by both halves),
+//   [1152, 1280) V scale/zero (half m at 1152 + m*64).
+// A 16-token page therefore reads 2816 of the 5120 bytes.
 constexpr int kRecordWords = 1280;
 // k_meta slot s of dim-block p holds channel 8p + KSLOT[s]; the inverse map of
-// channel 8p + j is slot 2*(j % 4) + j / 4.  v words: nibble k of word (r, d)
-// holds token VTOK[r][k] = TAU[r][VELEM[k]].
-__constant__ uint8_t kVTok[4][8] = {
-    {0, 2, 16, 18, 1, 3, 17, 19},
-    {4, 6, 20, 22, 5, 7, 21, 23},
-    {8, 10, 24, 26, 9, 11, 25, 27},
-    {12, 14, 28, 30, 13, 15, 29, 31},
-};
+// channel 8p + j is slot 2*(j % 4) + j / 4.
 
 // fp16 bit pattern h is +-inf or NaN
 __device__ __forceinline__ bool f16_nonfinite(uint16_t h) { return (h & 0x7C00u) == 0x7C00u; }
@@ -149,13 +145,12 @@ __global__ __launch_bounds__(128) void kivi4_pack_kernel(
     const float safe = kivi_safe(scale);
 #pragma unroll
     for (int i = 0; i < 32; ++i) vc[t][32 * gd + i] = static_cast<uint8_t>(kivi_code(x[i], mn, safe));
-    // token t sits in octet r at element e (TAU[r][e] == t)
-    const int r = (t & 15) >> 2;
-    const int e = (t & 3) + ((t >> 4) << 2);
-    uint16_t* vm = v_meta + (gd * 4 + r) * 16;
+    // token t = 16m + 4r + i: half m's block, entry (gd, r) = 4 scales then 4 zeros
+    const int m = t >> 4, r = (t >> 2) & 3, i = t & 3;
+    uint16_t* vm = v_meta + m * 128 + (gd * 4 + r) * 8;
     const uint16_t hs = f32_to_f16_bits(scale), hz = f32_to_f16_bits(mn);
-    vm[e] = hs;
-    vm[8 + e] = hz;
+    vm[i] = hs;
+    vm[4 + i] = hz;
     if (range_status) {
       const uint32_t bad = (f16_nonfinite(hs) || f16_nonfinite(hz) ? ZKV_RANGE_V : 0u) |
                            ((hs & 0x7FFFu) > kF16VScaleMax ? ZKV_RANGE_V_SCALE : 0u);
@@ -176,17 +171,21 @@ __global__ __launch_bounds__(128) void kivi4_pack_kernel(
     for (int j = 0; j < 8; ++j) word |= static_cast<uint32_t>((cb >> (8 * j)) & 0xF) << (4 * j);
     k_codes[w] = static_cast<int32_t>(word);
   }
-  // ---- V words in MFMA lane order: w = (j/4)*256 + l*4 + j%4, l = 16r + c,
-  //      word of octet r for channel d = 32(j/2) + 2c + j%2 (M-tile j, row c:
-  //      every M-tile inside one 32-channel scale group) ----
+  // ---- V words in MFMA lane order: w = m*256 + l*4 + P, l = 16r + c: channels
+  //      d = 32P + 2c and d + 1 (one 32-channel scale group) of tokens
+  //      16m + 4r + i; nibbles (0, 4, 1, 5) = channel d, tokens i = 0..3,
+  //      nibbles (2, 6, 3, 7) = channel d + 1 ----
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int w = tid + 128 * i;
-    const int j = 4 * (w >> 8) + (w & 3), l = (w >> 2) & 63;
-    const int r = l >> 4, d = 32 * (j >> 1) + 2 * (l & 15) + (j & 1);
+    const int m = w >> 8, l = (w >> 2) & 63, P = w & 3;
+    const int t0 = 16 * m + 4 * (l >> 4), d = 32 * P + 2 * (l & 15);
     uint32_t word = 0;
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk) word |= static_cast<uint32_t>(vc[kVTok[r][kk]][d]) << (4 * kk);
+    for (int n = 0; n < 8; ++n) {
+      const int tok = t0 + (n >> 2) + 2 * (n & 1), ch = d + ((n >> 1) & 1);
+      word |= static_cast<uint32_t>(vc[tok][ch]) << (4 * n);
+    }
     v_codes[w] = static_cast<int32_t>(word);
   }
 }

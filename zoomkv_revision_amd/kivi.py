@@ -81,8 +81,9 @@ class Kivi4Cache:
     ``groups`` int32 [bs, kv, G_cap, 1280] holds one contiguous 5120-byte
     record per 32-token group: K codes (words 0-511), V codes (512-1023),
     K scale/zero (1024-1151) and V scale/zero (1152-1279), each in the decode
-    kernel's MFMA operand order; ``k_codes`` / ``v_codes`` / ``k_meta`` /
-    ``v_meta`` are views of those parts."""
+    kernel's MFMA operand order; the codes and V scale/zero of each 16-token
+    half (one Quest page) are separate blocks.  ``k_codes`` / ``v_codes`` /
+    ``k_meta`` / ``v_meta`` are views of those parts."""
     groups: torch.Tensor    # int32 [bs, kv, G_cap, 1280]
     k_res: torch.Tensor     # bf16  [bs, kv, R_cap, 128]
     v_res: torch.Tensor     # bf16  [bs, kv, R_cap, 128]
@@ -117,8 +118,8 @@ class Kivi4Cache:
         return self.groups[..., 1024:1152].view(torch.float16).unflatten(-1, (16, 2, 8))
 
     @property
-    def v_meta(self) -> torch.Tensor:    # fp16 [bs, kv, G_cap, 4, 4, 2, 8]
-        return self.groups[..., 1152:1280].view(torch.float16).unflatten(-1, (4, 4, 2, 8))
+    def v_meta(self) -> torch.Tensor:    # fp16 [bs, kv, G_cap, 2, 4, 4, 2, 4]
+        return self.groups[..., 1152:1280].view(torch.float16).unflatten(-1, (2, 4, 4, 2, 4))
 
     @property
     def g_cap(self) -> int:
