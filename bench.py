@@ -207,29 +207,64 @@ def run_c5(args):
     dynamic candidate ratio, CDS 0.3 / 8 / 8, sink 64, local 256, top-100,
     update interval 512, full-attention threshold 2048), sampling at
     temperature 0.6 / top-p 0.95 / top-k 20, seed 42."""
+    import statistics
     import torch
     from zoomkv_revision_amd import decode_step as ds
     ds.apply_production_env()
     geo = ds.Qwen3Geometry()
     batch, context, interval, threshold = 4, 65536, 512, 2048
     dev = torch.device("cuda:0")
-    max_new = args.warmup + args.steps + 64
+    max_new = args.warmup + args.steps + interval + 64
     t0 = time.perf_counter()
     model = ds.RandomQwen3(geo, dev, seed=42)
-    cache = ds.build_cache(geo, batch, context, max_new, interval, threshold, dev)
-    ds.fill_cache(cache, geo, batch, context, 43, dev)
-    torch.cuda.synchronize()
+
+    def run_mode(offload: bool):
+        """Timed steps, then untimed steps up to and through the first flush
+        (every `interval` tokens): the flush step's extra time, amortized."""
+        t_setup = time.perf_counter()
+        cache = ds.build_cache(geo, batch, context, max_new, interval, threshold, dev, offload=offload)
+        ds.fill_cache(cache, geo, batch, context, 43, dev)
+        torch.cuda.synchronize()
+        setup = time.perf_counter() - t_setup
+        print(f"[c5] offload={offload}: cache built and filled in {setup:.1f} s", file=sys.stderr, flush=True)
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(42)
+        state = {"tok": torch.randint(0, geo.vocab, (batch,), generator=gen, device=dev)}
+
+        def step(i):
+            logits = model.decode_step(state["tok"], cache)
+            state["tok"] = ds.sample_next_token(logits, 0.6, 0.95, 20, generator=gen)
+
+        ms = timed_loop(step, args.steps, args.warmup)
+        print(f"[c5] offload={offload}: {ms:.3f} ms per step; stepping to the first flush", file=sys.stderr,
+              flush=True)
+        flushes_timed = cache._decode_step_counter // interval
+        # step until the flush has run, timing each step (host clock, synchronised)
+        times, flush_ms, i = [], None, args.warmup + args.steps
+        while flush_ms is None and i < max_new - 1:
+            before = cache.cpu_valid_end[0]
+            t1 = time.perf_counter()
+            step(i)
+            torch.cuda.synchronize()
+            dt = (time.perf_counter() - t1) * 1e3
+            if cache.cpu_valid_end[0] != before:
+                flush_ms = dt
+            else:
+                times.append(dt)
+            i += 1
+        plain = statistics.median(times[-64:]) if times else ms
+        extra = None if flush_ms is None else flush_ms - plain
+        return cache, step, ms, setup, {
+            "flushes_in_timed_region": flushes_timed,
+            "flush_step_ms": flush_ms, "plain_step_ms": plain, "flush_extra_ms": extra,
+            "flush_amortized_ms_per_step": None if extra is None else extra / interval,
+            "per_token_latency_with_flush_ms": None if extra is None else ms + extra / interval,
+        }
+
+    # the retrieval zone in device memory (the 288 GB part holds it)
+    cache, step, ms, setup_dev, flush_dev = run_mode(False)
     setup_s = time.perf_counter() - t0
-    gen = torch.Generator(device=dev)
-    gen.manual_seed(42)
-    state = {"tok": torch.randint(0, geo.vocab, (batch,), generator=gen, device=dev)}
-
-    def step(i):
-        logits = model.decode_step(state["tok"], cache)
-        state["tok"] = ds.sample_next_token(logits, 0.6, 0.95, 20, generator=gen)
-
-    ms = timed_loop(step, args.steps, args.warmup)
-    flushes = cache._decode_step_counter // interval
+    flushes = flush_dev["flushes_in_timed_region"]
     # device time of one step and of its attention path alone (36 x cache.compute),
     # each queued behind a spin kernel so host launch gaps are not counted
     step_ms = kernel_batch_ms(step, 8, host_us=20000.0)
@@ -243,6 +278,17 @@ def run_c5(args):
     per_layer = [ds.attention_path_bytes(cache, ldx) for ldx in range(geo.layers)]
     attn_bytes = sum(p["total"] for p in per_layer)
     weight_bytes = model.parameter_bytes()
+    del cache, step
+    torch.cuda.empty_cache()
+    # the reference runner's enable_offload=True: retrieval zone in pinned host memory
+    offload = None
+    if not args.no_offload:
+        cache_h, step_h, ms_h, setup_h, flush_h = run_mode(True)
+        offload = {"ms_per_step": ms_h, "tokens_per_s": batch / (ms_h * 1e-3), "setup_s": setup_h, **flush_h,
+                   "host_bytes_pinned": sum(t.numel() * t.element_size()
+                                            for t in cache_h.unified_keys_cpu + cache_h.unified_values_cpu)}
+        del cache_h, step_h
+        torch.cuda.empty_cache()
     return {
         "metric": "C5 full decode step (Qwen3-4B geometry, 36 layers): per-token latency, tokens/s",
         "value": batch / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
@@ -260,6 +306,8 @@ def run_c5(args):
                    "parallelism": "single GPU"},
         "per_token_latency_ms": ms,
         "flushes_in_timed_region": flushes,
+        "flush": {k: v for k, v in flush_dev.items() if k != "flushes_in_timed_region"},
+        "offload_mode": offload,
         "device_ms_per_step": step_ms,
         "attention_path": {"device_ms_per_step": attn_ms, "bytes_per_step": attn_bytes,
                            "GBps": attn_bytes / (attn_ms * 1e-3) / 1e9,
@@ -486,6 +534,8 @@ def main():
     ap.add_argument("--config", choices=["c1", "c2", "c3", "c4", "c5", "h2d"], default="c2",
                     help="c2 (default, the headline line), c1, c3, c4, c5 or h2d")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-offload", action="store_true",
+                    help="c5: skip the run with the retrieval zone in pinned host memory")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run 5 device copies of 1 GiB (scale reference for rocprof "
                          "FETCH_SIZE / WRITE_SIZE counters) and exit")

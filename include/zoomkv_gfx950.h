@@ -378,6 +378,22 @@ int zkv_h2d_gather_kv_packed(const void* src_k, const void* src_v, int bs, int k
                              const int32_t* cu_seqlens_topk, const int32_t* cu_seqlens_k, int sl_end,
                              int global_k, zkv_stream_t stream);
 
+/* Pitched copy on the stream's copy engine: rows x row_bytes from src (row
+ * pitch src_pitch bytes) to dst (pitch dst_pitch), device memory or pinned
+ * host memory on either side.  The offload flush's D2H move of the oldest
+ * near-zone tokens into the pinned retrieval zone, one call per K / V
+ * (replaces the strided dst_keys.copy_(src_keys, non_blocking=True) of
+ * S:1465-1469). */
+int zkv_copy_rows(void* dst, size_t dst_pitch, const void* src, size_t src_pitch, size_t row_bytes,
+                  size_t rows, zkv_stream_t stream);
+
+/* Pinned, device-mapped host memory of exactly `bytes` (*out; ZKV_ESPACE when
+ * the host cannot pin that much) and its release: the offload retrieval zone
+ * (S:561-571 allocates it with torch's pinned allocator, which rounds each
+ * block up to a power of two). */
+int zkv_host_alloc(size_t bytes, void** out);
+int zkv_host_free(void* p);
+
 /* ---- decode-step model layers (the C5 counterpart of layer_decode) ------ */
 
 /* y = x . w^T for the M <= 16 rows of a decode batch: x [M, K] bf16 (row

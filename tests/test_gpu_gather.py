@@ -82,3 +82,50 @@ def test_h2d_gather_c_abi_reports_unmapped_host_memory():
     rc = lib().zkv_h2d_gather_kv(src.ctypes.data, src.ctypes.data, 1, 1, 16, idx.data_ptr(), 4,
                                  dst.data_ptr(), dst.data_ptr(), 4, torch.cuda.current_stream().cuda_stream)
     assert rc == 1 and b"not pinned" in lib().zkv_last_error()
+
+
+def test_copy_rows_between_device_and_pinned_host_rows():
+    """The offload flush's pitched copy: device staging [bs, kv, n, 128] into
+    rows [w0, w0 + n) of a pinned host [bs, kv, cap, 128], and back."""
+    from zoomkv_revision_amd.gather import copy_rows
+    g = torch.Generator(device="cuda")
+    g.manual_seed(5)
+    stage = torch.randn(3, 4, 48, 128, generator=g, device="cuda").to(torch.bfloat16)
+    host = torch.zeros(3, 4, 100, 128, dtype=torch.bfloat16, pin_memory=True)
+    copy_rows(host[:, :, 17:17 + 40], stage[:, :, :40])
+    torch.cuda.synchronize()
+    assert torch.equal(host[:, :, 17:57], stage[:, :, :40].cpu())
+    assert not host[:, :, :17].any() and not host[:, :, 57:].any()
+    back = torch.zeros(3, 4, 40, 128, dtype=torch.bfloat16, device="cuda")
+    copy_rows(back, host[:, :, 17:57])
+    torch.cuda.synchronize()
+    assert torch.equal(back, stage[:, :, :40])
+
+
+def test_pinned_empty_is_pinned_gatherable_and_released():
+    """Exact-size pinned host tensors: torch sees them as pinned, the h2d
+    gather reads them, and dropping the last view releases the memory (72
+    rounds of 1 GiB pass only if each is freed: the host pins about 65 GiB)."""
+    import gc
+    from zoomkv_revision_amd.gather import h2d_gather_kv, pinned_empty
+    k = pinned_empty((2, 3, 50, 128), torch.bfloat16)
+    v = pinned_empty((2, 3, 50, 128), torch.bfloat16)
+    assert k.is_pinned() and v.is_pinned() and k.shape == (2, 3, 50, 128)
+    k.copy_(torch.arange(2 * 3 * 50 * 128, dtype=torch.float32).view(2, 3, 50, 128))
+    v.copy_(-k.float())
+    idx = torch.tensor([[[4, 49, 0]] * 3] * 2, dtype=torch.int64, device="cuda")
+    dk = torch.zeros(2, 3, 3, 128, dtype=torch.bfloat16, device="cuda")
+    dv = torch.zeros_like(dk)
+    h2d_gather_kv(k[:, :, :50], v, idx, dk, dv)
+    torch.cuda.synchronize()
+    assert torch.equal(dk.cpu(), k[:, :, [4, 49, 0]]) and torch.equal(dv.cpu(), v[:, :, [4, 49, 0]])
+    view = k[1, 2]
+    del k
+    gc.collect()
+    assert view.sum().item() != 0                   # a view keeps the block alive
+    del view, v
+    for _ in range(72):
+        t = pinned_empty((1 << 30,), torch.uint8)
+        t[::1 << 20] = 1
+        del t
+        gc.collect()

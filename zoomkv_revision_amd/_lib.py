@@ -66,6 +66,9 @@ SIGNATURES = {
     "zkv_rabitq_search": (I32, [P, P, I64, I64, P, P, P, I32, I32, I64, I32, P, P, P, P, SZ, P]),
     "zkv_h2d_gather_kv": (I32, [P, P, I32, I32, I32, P, I32, P, P, I32, P]),
     "zkv_h2d_gather_kv_packed": (I32, [P, P, I32, I32, I32, P, P, I64, P, I64, P, P, I32, I32, P]),
+    "zkv_copy_rows": (I32, [P, SZ, P, SZ, SZ, SZ, P]),
+    "zkv_host_alloc": (I32, [SZ, P]),
+    "zkv_host_free": (I32, [P]),
     "zkv_decode_linear": (I32, [P, I64, I32, I32, P, I32, P, F32, P, I64, P, I64, I32, I32, P]),
     "zkv_qk_norm_rope": (I32, [P, I64, I32, I32, I32, P, P, F32, P, P, P, P, I64, I64, P, I64, I64, P]),
 }

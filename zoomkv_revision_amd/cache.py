@@ -20,11 +20,20 @@ Token bookkeeping is the reference's default ``enable_offload=True`` path:
   * chunk min / max / centroid and 4-bit codes are written per completed
     chunk, with a carry of the < chunk tail (``S:2025-2157``), and the live
     tail is appended to every selection as "skipped" tokens (``S:1895-1925``).
-The retrieval zone lives in HBM next to the near zone (a 288 GB part holds
-it), so a flush is a device copy and ``compute`` attends the selected rows
-in place with one gather-attention launch instead of h2d-gather + cat +
-flash-attn (``S:1723-1772``).  ``enable_offload`` is accepted for signature
-compatibility; both values give the token selection of the offload path.
+Where the retrieval zone lives follows ``enable_offload`` (``S:519-611``):
+  * ``enable_offload=True`` (the reference's default): in pinned host memory.
+    A flush encodes the oldest local tokens on the device, stages them and
+    moves them to their host rows on a copy stream, one pitched copy per K / V
+    and layer, with a per-layer event (``S:1440-1474``); ``compute`` waits for
+    that event on the device (no host synchronisation), gathers the selected
+    rows over the host link into the first rows of the layer's device buffer
+    (``h2d_gather_kv``) and attends them together with the near zone in one
+    gather-attention launch (``S:1723-1750``).
+  * ``enable_offload=False``: in device memory next to the near zone (a
+    288 GB part holds it), so a flush is a device copy and ``compute`` attends
+    the selected rows in place.
+Both modes select the same tokens and give the same attention output (the
+attended rows and their order are the same).
 
 Per decode step and layer, ``compute`` runs (``S:1589-1775, 2195-2467, 2688-2779``):
 GQA-mean query -> Quest chunk bounds -> top-nk chunks -> CDS density -> top
@@ -42,6 +51,7 @@ import torch
 
 from . import kivi
 from .attention import gather_attention
+from .gather import copy_rows, h2d_gather_kv, pinned_empty
 from .quest import load_kernel_module as _load_quest
 from .quest import quest_chunk_score_gqa
 from .rerank import partial_chunk_density_scores_cuda, topk_dense_mask
@@ -130,7 +140,7 @@ class polar_cache:
         self.current_seq_len = [0] * layer_num
         self.candidate_ratio = candidate_ratio
         self.final_topk = final_topk
-        self.enable_offload = enable_offload
+        self.enable_offload = bool(enable_offload)
         # Quest stage 1 / CDS knobs from the environment (S:178-292)
         self.quest_chunk_size = max(1, int(os.environ.get("POLAR_QUEST_CHUNK", "8")))
         if self.quest_chunk_size not in (8, 16):
@@ -159,12 +169,36 @@ class polar_cache:
         dev = dict(device=self.device)
         chunk = self.quest_chunk_size
         self.unified_kv_capacity = self.input_length + self.max_new_length
-        # near zone [sink | local | update buffer]; retrieval zone rows first
+        # near zone [sink | local | update buffer]
         self.gpu_kv_capacity = sink_size + local_size + self.dynamic_update_interval
         self.cpu_kv_capacity = max(0, self.unified_kv_capacity - sink_size - local_size)
-        self._rows = self.cpu_kv_capacity + self.gpu_kv_capacity
-        self._near0 = self.cpu_kv_capacity
         bs, kv, d = batch_size, num_key_value_heads, head_dim
+        self._min_total = max(self.FULL_ATTENTION_THRESHOLD, sink_size + local_size + self.final_topk * 2)
+        if self.enable_offload:
+            # device rows: [gathered retrieval rows | near zone]; the retrieval
+            # zone in pinned host memory (S:519-611).  The gather area holds a
+            # selection (final_topk + skipped) or, below the retrieval
+            # threshold, the whole (short) retrieval zone.
+            self._gather_rows = max(self.final_topk + self.MAX_SKIPPED_INDICES, self._min_total)
+            self._rows = self._gather_rows + self.gpu_kv_capacity
+            self._near0 = self._gather_rows
+            cap = max(self.cpu_kv_capacity, 1)
+            self.unified_keys_cpu = [pinned_empty((bs, kv, cap, d), dtype) for _ in range(layer_num)]
+            self.unified_values_cpu = [pinned_empty((bs, kv, cap, d), dtype) for _ in range(layer_num)]
+            self._copy_stream = torch.cuda.Stream(device=self.device)
+            self._main_events = [torch.cuda.Event() for _ in range(layer_num)]
+            self._copy_events = [torch.cuda.Event() for _ in range(layer_num)]
+            for e in self._copy_events:           # recorded once: waiting on them is always valid
+                e.record(torch.cuda.current_stream(self.device))
+            n_buf = self.dynamic_update_interval
+            self._offload_keys_buffer = [torch.empty(bs, kv, n_buf, d, dtype=dtype, **dev) for _ in range(layer_num)]
+            self._offload_values_buffer = [torch.empty(bs, kv, n_buf, d, dtype=dtype, **dev)
+                                           for _ in range(layer_num)]
+        else:
+            # device rows: [retrieval zone | near zone]
+            self._rows = self.cpu_kv_capacity + self.gpu_kv_capacity
+            self._near0 = self.cpu_kv_capacity
+            self.unified_keys_cpu = self.unified_values_cpu = None
         self.unified_keys = [torch.zeros(bs, kv, self._rows, d, dtype=dtype, **dev) for _ in range(layer_num)]
         self.unified_values = [torch.zeros(bs, kv, self._rows, d, dtype=dtype, **dev) for _ in range(layer_num)]
         self.cpu_valid_end = [0] * layer_num      # retrieval-zone length per layer (name of S)
@@ -251,15 +285,23 @@ class polar_cache:
         V[rows, :, n0:n0 + self.sink_size] = vt[:, :, vs:sink_end].to(self.dtype)
         K[rows, :, n0 + self.sink_size:n0 + self.sink_size + local_len] = kt[:, :, retrieval_end:seq_len].to(self.dtype)
         V[rows, :, n0 + self.sink_size:n0 + self.sink_size + local_len] = vt[:, :, retrieval_end:seq_len].to(self.dtype)
-        K[rows, :, :retrieval_length] = kt[:, :, retrieval_start:retrieval_end].to(self.dtype)
-        V[rows, :, :retrieval_length] = vt[:, :, retrieval_start:retrieval_end].to(self.dtype)
+        kr = kt[:, :, retrieval_start:retrieval_end].to(self.dtype)
+        vr = vt[:, :, retrieval_start:retrieval_end].to(self.dtype)
+        if self.enable_offload:
+            # the prompt's retrieval zone to its pinned host rows (S:1003-1141)
+            torch.cuda.current_stream(self.device).wait_event(self._copy_events[layer_idx])
+            self.unified_keys_cpu[layer_idx][rows, :, :retrieval_length].copy_(kr)
+            self.unified_values_cpu[layer_idx][rows, :, :retrieval_length].copy_(vr)
+        else:
+            K[rows, :, :retrieval_length] = kr
+            V[rows, :, :retrieval_length] = vr
         self.cpu_valid_end[layer_idx] = retrieval_length
         self.current_seq_len[layer_idx] = seq_len - vs
         # a prefill writes its rows' retrieval zone from offset 0: no earlier
         # carry belongs to them (the reference's per-layer carry would leak the
         # previous row's tail into a one-row prefill)
         self._chunk_carry_count[layer_idx] = 0
-        self._store_chunks(layer_idx, K[rows, :, :retrieval_length], 0, rows)
+        self._store_chunks(layer_idx, kr, 0, rows)
 
     def sync(self, layer_idx, batch_idx):
         """Nothing to wait for: every write is on the caller's stream (S:2789-2793)."""
@@ -427,8 +469,11 @@ class polar_cache:
             w0 = self.cpu_valid_end[ldx]
             if w0 + num_new > self.cpu_kv_capacity:
                 raise RuntimeError(f"layer {ldx}: retrieval zone full ({w0} + {num_new} > {self.cpu_kv_capacity})")
-            K[:, :, w0:w0 + num_new].copy_(K[:, :, oldest])
-            V[:, :, w0:w0 + num_new].copy_(V[:, :, oldest])
+            if self.enable_offload:
+                self._offload(ldx, K[:, :, oldest], V[:, :, oldest], w0, num_new)
+            else:
+                K[:, :, w0:w0 + num_new].copy_(K[:, :, oldest])
+                V[:, :, w0:w0 + num_new].copy_(V[:, :, oldest])
             self.cpu_valid_end[ldx] = w0 + num_new
             # slide: [sink + num_new, sink + local + num_new) -> [sink, sink + local)
             src = slice(n0 + s + num_new, n0 + s + loc + num_new)
@@ -437,6 +482,23 @@ class polar_cache:
             V[:, :, dst] = V[:, :, src].clone()
         self._cached_region_total_len = -1
         self._cached_region_info = None
+
+    def _offload(self, ldx, k_old, v_old, w0, n):
+        """Stage the n oldest near-zone tokens and move them to host rows
+        [w0, w0 + n) on the copy stream (S:1440-1474); _copy_events[ldx] marks
+        the end of the move."""
+        main = torch.cuda.current_stream(self.device)
+        main.wait_event(self._copy_events[ldx])         # the staging buffer's previous move is done
+        sk = self._offload_keys_buffer[ldx][:, :, :n]
+        sv = self._offload_values_buffer[ldx][:, :, :n]
+        sk.copy_(k_old)
+        sv.copy_(v_old)
+        self._main_events[ldx].record(main)
+        self._copy_stream.wait_event(self._main_events[ldx])
+        with torch.cuda.stream(self._copy_stream):
+            copy_rows(self.unified_keys_cpu[ldx][:, :, w0:w0 + n], sk)
+            copy_rows(self.unified_values_cpu[ldx][:, :, w0:w0 + n], sv)
+            self._copy_events[ldx].record(self._copy_stream)
 
     def decode_update_kv_cache(self, key_states, value_states, layer_idx):
         """Append one token ([bs, 1, kv, 128]) of one layer; the flush runs at
@@ -518,17 +580,23 @@ class polar_cache:
         total = region["total_len"]
         local_len = region["local_len"]
         retrieval_len = int(self.cpu_valid_end[layer_idx])
-        min_total = max(self.FULL_ATTENTION_THRESHOLD, self.sink_size + self.local_size + self.final_topk * 2)
         K, V = self.unified_keys[layer_idx], self.unified_values[layer_idx]
         bs = self.batch_size
         if retrieval_len > 0:
             near_len = self.sink_size + local_len
         else:
             near_len = min(total, self.gpu_kv_capacity)      # short prompt: everything sits in the near zone
-        if total < min_total or retrieval_len <= 0 or self._cached_quest_nk <= 0:
+        if total < self._min_total or retrieval_len <= 0 or self._cached_quest_nk <= 0:
             idx = self._arange_buffer[:retrieval_len].view(1, 1, -1).expand(bs, self.kv_head, -1)
             self._last_topk_indices = None
         else:
             idx = self._select(queries, layer_idx)
             self._last_topk_indices = idx
-        return gather_attention(queries, K, V, idx if idx.shape[-1] else None, self._near0, near_len)
+        n = idx.shape[-1]
+        if self.enable_offload and n:
+            # the listed host rows into device rows [0, n) (S:1723-1733), after
+            # this layer's last move to the host
+            torch.cuda.current_stream(self.device).wait_event(self._copy_events[layer_idx])
+            h2d_gather_kv(self.unified_keys_cpu[layer_idx], self.unified_values_cpu[layer_idx], idx, K, V)
+            idx = self._arange_buffer[:n].view(1, 1, -1).expand(bs, self.kv_head, -1)
+        return gather_attention(queries, K, V, idx if n else None, self._near0, near_len)

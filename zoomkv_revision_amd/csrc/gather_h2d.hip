@@ -124,3 +124,42 @@ extern "C" int zkv_h2d_gather_kv_packed(const void* src_k, const void* src_v, in
       total_k, indices_packed, total_topk, cu_seqlens_topk, cu_seqlens_k, sl_end);
   return check_launch("h2d_gather_packed_kernel");
 }
+
+// Pitched copy of `rows` rows of row_bytes each, any direction (device or
+// pinned host on either side), on the stream's copy engine: the offload
+// flush moves the oldest near-zone tokens of every (b, kv head) into their
+// rows of the pinned host retrieval zone in one call.
+extern "C" int zkv_copy_rows(void* dst, size_t dst_pitch, const void* src, size_t src_pitch, size_t row_bytes,
+                             size_t rows, zkv_stream_t stream) {
+  ZKV_REQUIRE(dst && src, "zkv_copy_rows: null pointer");
+  ZKV_REQUIRE(row_bytes <= dst_pitch && row_bytes <= src_pitch,
+              "zkv_copy_rows: row_bytes %zu exceeds a pitch (dst %zu, src %zu)", row_bytes, dst_pitch, src_pitch);
+  if (rows == 0 || row_bytes == 0) return ZKV_OK;
+  const hipError_t e = hipMemcpy2DAsync(dst, dst_pitch, src, src_pitch, row_bytes, rows, hipMemcpyDefault,
+                                        reinterpret_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(ZKV_ELAUNCH, "zkv_copy_rows: %s", hipGetErrorString(e));
+  return ZKV_OK;
+}
+
+// Pinned (page-locked, device-mapped) host memory of exactly `bytes`: the
+// offload retrieval zone.  (torch's pinned allocator rounds each block up to
+// a power of two, which at C5 -- 72 blocks of 539 MB -- doubles the pinned
+// footprint.)
+extern "C" int zkv_host_alloc(size_t bytes, void** out) {
+  ZKV_REQUIRE(out, "zkv_host_alloc: null output pointer");
+  *out = nullptr;
+  ZKV_REQUIRE(bytes > 0, "zkv_host_alloc: zero bytes");
+  const hipError_t e = hipHostMalloc(out, bytes, hipHostMallocDefault);
+  if (e != hipSuccess) {
+    *out = nullptr;
+    return fail(ZKV_ESPACE, "zkv_host_alloc: %zu bytes: %s", bytes, hipGetErrorString(e));
+  }
+  return ZKV_OK;
+}
+
+extern "C" int zkv_host_free(void* p) {
+  if (p == nullptr) return ZKV_OK;
+  const hipError_t e = hipHostFree(p);
+  if (e != hipSuccess) return fail(ZKV_EINVAL, "zkv_host_free: %s", hipGetErrorString(e));
+  return ZKV_OK;
+}

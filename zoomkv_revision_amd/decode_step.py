@@ -312,17 +312,20 @@ def sample_next_token_full(logits: torch.Tensor, temperature: float = 1.0, top_p
 
 
 def build_cache(geo: Qwen3Geometry, batch: int, context: int, max_new: int, interval: int,
-                full_threshold: int, device):
+                full_threshold: int, device, offload: bool = False):
     """polar_cache for `context` prompt tokens plus `max_new` generated ones,
-    with the reference's production knobs."""
+    with the reference's production knobs.  ``offload`` picks the retrieval
+    zone's home: device memory (False: the 288 GB part holds it) or pinned
+    host memory (True: the reference runner's enable_offload)."""
     from .cache import polar_cache
+    knobs = dict(PRODUCTION_CACHE_KNOBS, enable_offload=offload)
     return polar_cache(
         valid_start=[0] * batch, layer_num=geo.layers, batch_size=batch, max_length=context + max_new,
         num_key_value_heads=geo.kv_heads, num_heads=geo.heads, head_dim=geo.head_dim,
         dtype=torch.bfloat16, layer_mapping={str(i): str(device) for i in range(geo.layers)},
         max_new_length=max_new, core=22, nprobe=150, cache_unit_size=8, cache_cluster_num=450,
         num_gpus=1, model_size=4, dynamic_update_interval=interval, full_attention_threshold=full_threshold,
-        **PRODUCTION_CACHE_KNOBS)
+        **knobs)
 
 
 def fill_cache(cache, geo: Qwen3Geometry, batch: int, context: int, seed: int, device) -> None:

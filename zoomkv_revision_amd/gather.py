@@ -74,3 +74,44 @@ def h2d_gather_kv_packed(src_k_caches, src_v_caches, dst_k_packed, dst_v_packed,
         dst_k_packed.shape[0], ptr(indices_packed.contiguous()), indices_packed.numel(),
         ptr(cu_seqlens_topk.contiguous()), ptr(cu_seqlens_k.contiguous()), int(sl_end), int(global_k),
         stream_of(dst_k_packed)))
+
+
+def copy_rows(dst: torch.Tensor, src: torch.Tensor) -> None:
+    """dst.copy_(src) for [rows, n, 128]-shaped views whose last two dims are
+    contiguous (any row stride), as one pitched copy on the current stream:
+    device and pinned host memory on either side, asynchronous like
+    ``copy_(..., non_blocking=True)`` (the flush's D2H move, S:1465-1469)."""
+    assert dst.dtype == src.dtype and dst.shape == src.shape, "copy_rows: shape / dtype mismatch"
+    assert dst.dim() >= 2 and src.dim() >= 2
+    for t in (dst, src):
+        assert t.stride(-1) == 1 and t.stride(-2) == t.shape[-1], "copy_rows: the last two dims must be contiguous"
+        assert t.is_cuda or t.is_pinned(), "copy_rows: host memory must be pinned"
+        # the leading dims must collapse to one row index with a single pitch
+        lead = t.shape[:-2]
+        for i in range(len(lead) - 1):
+            assert t.stride(i) == t.stride(i + 1) * lead[i + 1], "copy_rows: leading dims must collapse"
+    row_bytes = src.shape[-2] * src.shape[-1] * src.element_size()
+    rows = src.numel() // (src.shape[-2] * src.shape[-1]) if src.numel() else 0
+    pitch = lambda t: (t.stride(-3) if t.dim() >= 3 else t.shape[-2] * t.shape[-1]) * t.element_size()
+    dev = dst if dst.is_cuda else src
+    check(lib().zkv_copy_rows(ptr(dst), pitch(dst), ptr(src), pitch(src), row_bytes, rows, stream_of(dev)))
+
+
+def pinned_empty(shape, dtype: torch.dtype) -> torch.Tensor:
+    """An uninitialised pinned host tensor of exactly its size (the library's
+    hipHostMalloc; torch's pinned allocator rounds each block up to a power of
+    two).  The memory is released when the last tensor viewing it is gone."""
+    import ctypes as C
+    n = 1
+    for s in shape:
+        n *= int(s)
+    nbytes = max(n * torch.empty(0, dtype=dtype).element_size(), 1)
+    p = C.c_void_p()
+    check(lib().zkv_host_alloc(nbytes, C.byref(p)))
+    free, addr = lib().zkv_host_free, p.value
+    # the ctypes block owns the allocation: torch.frombuffer keeps it alive
+    # for as long as any view of the storage exists
+    block = type("PinnedBlock", (C.c_uint8 * nbytes,), {"__del__": lambda self: free(addr)})
+    buf = block.from_address(addr)
+    return torch.frombuffer(buf, dtype=torch.uint8)[:n * torch.empty(0, dtype=dtype).element_size()] \
+        .view(dtype).view(*shape)
