@@ -241,7 +241,7 @@ def run_c5(args):
         flushes_timed = cache._decode_step_counter // interval
         # step until the flush has run, timing each step (host clock, synchronised)
         times, flush_ms, i = [], None, args.warmup + args.steps
-        while flush_ms is None and i < max_new - 1:
+        while flush_ms is None and i < max_new - 1 and not args.no_flush:
             before = cache.cpu_valid_end[0]
             t1 = time.perf_counter()
             step(i)
@@ -536,6 +536,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-offload", action="store_true",
                     help="c5: skip the run with the retrieval zone in pinned host memory")
+    ap.add_argument("--no-flush", action="store_true",
+                    help="c5: skip stepping to the first flush (its timing)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run 5 device copies of 1 GiB (scale reference for rocprof "
                          "FETCH_SIZE / WRITE_SIZE counters) and exit")
