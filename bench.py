@@ -24,6 +24,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import statistics
 import sys
@@ -47,34 +48,57 @@ def make_cache(seed: int, device):
     return synthetic.c2_cache(seed, B, HKV, NG, R, device)
 
 
-def cpu_baseline(cache, q, budget_s: float = 12.0):
-    """Time the numpy oracle (dequant + softmax attention, float32, 1 thread) on
-    sequence 0 of the batch: 1 of 16 sequences per call."""
-    import numpy as np
-    from threadpoolctl import threadpool_limits
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
-    from oracle import kivi as okivi
-    c0 = okivi.Kivi4Cache(cache.k_codes[:1].cpu().numpy(),
-                          cache.k_meta[:1].cpu().view(__import__("torch").int16).numpy().view(np.uint16),
-                          cache.v_codes[:1].cpu().numpy(),
-                          cache.v_meta[:1].cpu().view(__import__("torch").int16).numpy().view(np.uint16))
-    kr = cache.k_res[:1].float().cpu().numpy()
-    vr = cache.v_res[:1].float().cpu().numpy()
-    q0 = q[:1].float().cpu().numpy()
-    times = []
-    with threadpool_limits(limits=1):
+
+def cpu_baseline(cache, q, budget_s: float = 10.0, rows=(0,)):
+    """The torch-CPU restatement of the C2 step (oracle/torch_cpu.py: 4-bit
+    unpack + dequant, residual append, float32 SDPA with grouped heads) at
+    the full per-sequence C2 shape (32 query / 8 KV heads, 32640 quantized +
+    128 residual tokens), on a sample of the batch's sequences, timed with 1
+    thread (as the reference cache sets, S:783-789) and with every thread of
+    the process's CPU share."""
+    import numpy as np
+    import torch
+    from oracle import torch_cpu
+    r = list(rows)
+    f16 = lambda t: t[r].cpu().view(torch.int16).numpy().view(np.uint16)
+    prep = torch_cpu.prepare_c2(cache.k_codes[r].cpu().numpy(), f16(cache.k_meta), cache.v_codes[r].cpu().numpy(),
+                                f16(cache.v_meta), cache.k_res[r, :, :R].float().cpu().numpy(),
+                                cache.v_res[r, :, :R].float().cpu().numpy())
+    q0 = q[r].float().cpu()
+    n_all = torch.get_num_threads()
+    res = {}
+    for nt in (1, n_all):
+        torch.set_num_threads(nt)
+        torch_cpu.decode_attention(q0, prep, 1 / math.sqrt(D))            # warm-up
+        times = []
         t_end = time.perf_counter() + budget_s
         while time.perf_counter() < t_end or len(times) < 2:
             t0 = time.perf_counter()
-            okivi.kivi4_decode_attention(q0, c0, NG, kr, vr, R, 1 / np.sqrt(D), dtype=np.float32)
+            torch_cpu.decode_attention(q0, prep, 1 / math.sqrt(D))
             times.append(time.perf_counter() - t0)
             if len(times) >= 20:
                 break
-    t = statistics.median(times)
-    return {"value": 1.0 / t, "unit": "tokens/s", "cores": 1, "kind": "port",
-            "sample": f"numpy oracle (Format Q dequant + float32 softmax attention) on 1 of {B} "
-                      f"sequences ({HKV} KV heads x {T} tokens) per call; median of {len(times)} "
-                      f"calls ({t * 1e3:.0f} ms each); host {os.cpu_count()} logical CPUs, 1 used"}
+        res[nt] = (statistics.median(times), len(times))
+    torch.set_num_threads(n_all)
+    (t1, n1), (tn, nn) = res[1], res[n_all]
+    return {"value": len(r) / t1, "unit": "tokens/s", "cores": 1, "kind": "port",
+            "all_cores": {"value": len(r) / tn, "cores": n_all},
+            "cpu_model": cpu_model(), "host_logical_cpus": os.cpu_count(),
+            "sample": f"torch-CPU restatement (oracle/torch_cpu.py) of the C2 step for {len(r)} of {B} "
+                      f"sequences per call at the full per-sequence shape ({HQ} q / {HKV} KV heads, "
+                      f"{NG * 32} + {R} tokens); median of {n1} calls ({t1:.2f} s) on 1 thread and "
+                      f"{nn} calls ({tn:.2f} s) on {n_all} threads (torch.get_num_threads(), the "
+                      f"process's CPU share; host {os.cpu_count()} logical CPUs, {cpu_model()})"}
 
 
 def read_traffic(name: str = "kivi4_attn_c2_traffic.json"):

@@ -235,3 +235,21 @@ def test_lse_merge_of_two_segments_is_attention_over_both(rng):
     s = np.einsum("bhgd,bhnd->bhgn", q.reshape(2, 2, 4, 128).astype(np.float64), k.astype(np.float64)) * sc
     _, lfull = okivi.attention(q, k, v, sc, return_lse=True)
     assert np.allclose(lfull, np.log(np.exp(s).sum(-1)).reshape(2, 8), atol=1e-10)
+
+
+def test_torch_cpu_restatement_equals_oracle_attention(rng):
+    """The torch-CPU C2 step (bench.py's CPU baseline) against the numpy
+    oracle's dequant + float64 attention on the same Format Q cache."""
+    import torch
+    from oracle import torch_cpu
+    B, KV, HQ, G, R = 2, 2, 8, 3, 40
+    k = gaussian_bf16(rng, (B, KV, G * 32, 128), outlier_channels=2)
+    v = gaussian_bf16(rng, (B, KV, G * 32, 128))
+    c = kivi.quantize_kivi4(k, v)
+    kr = gaussian_bf16(rng, (B, KV, R, 128))
+    vr = gaussian_bf16(rng, (B, KV, R, 128))
+    q = gaussian_bf16(rng, (B, HQ, 128))
+    ref = kivi.kivi4_decode_attention(q, c, G, kr, vr, R, 1 / np.sqrt(128))
+    prep = torch_cpu.prepare_c2(c.k_codes, c.k_meta, c.v_codes, c.v_meta, kr, vr)
+    got = torch_cpu.decode_attention(torch.from_numpy(q.astype(np.float32)), prep, 1 / np.sqrt(128)).numpy()
+    assert got.shape == ref.shape and np.abs(got - ref).max() <= 1e-5
