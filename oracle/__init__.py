@@ -54,4 +54,7 @@ PINNING = {
     "kivi.lse_merge": "golden vectors of lse_merge.lse_merge_torch",
     "rabitq": "popcount identity vs brute-force +-1 dot products; FWHT vs "
               "explicit Hadamard matrix; correction factor closed form",
+    "torch_cpu.decode_attention": "against kivi.kivi4_decode_attention (numpy, float64) on the same "
+                                  "Format Q cache, 1e-5 (tests/test_oracle_kivi.py); it is the timed "
+                                  "CPU baseline of bench.py, not a checker",
 }
