@@ -113,6 +113,22 @@ __device__ __forceinline__ void dma16(const void* src, void* dst) {
   __builtin_amdgcn_global_load_lds(src, (lds_void_t*)(dst), 16, 0, kCachePolicyNT);
 }
 
+// LDS byte address of a pointer into __shared__ memory.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const lds_void_t*)(p)));
+}
+
+// The same DMA as inline asm, which the compiler's wait counting does not see.
+// With the builtin, a loop that mixes these DMAs with VGPR loads gets a drain
+// of every load in flight (vmcnt(0)) at one tile of each unrolled round.  The
+// caller waits for the DMA with an explicit vmcnt; the compiler's own waits for
+// VGPR loads issued around it count one op fewer per DMA, so they are
+// stricter than needed, never short.  `dst` must be wave-uniform (it goes to
+// M0; lane i lands at dst + 16 i).
+__device__ __forceinline__ void dma16_untracked(const void* src, void* dst) {
+  asm volatile("global_load_lds_dwordx4 %0, off nt" : : "v"(src), "{m0}"(lds_addr(dst)) : "memory");
+}
+
 // s_waitcnt vmcnt(n) (gfx9 encoding: vmcnt[3:0] bits 3:0, vmcnt[5:4] bits
 // 15:14; expcnt / lgkmcnt left at "no wait").  The compiler does not track the
 // LDS side of global_load_lds, so the ring's waits are explicit.
@@ -310,22 +326,33 @@ struct TileConsts {
   float qs, qs24;  // raw score -> base-2; the same for 2^-24-unit scores
 };
 
-// Tile compute from an LDS stage.
+// Code words of one tile held by a lane: K halves 0 / 1 (record bytes 16 lane
+// and 1024 + 16 lane), V halves 0 / 1 (2048 + 16 lane, 3072 + 16 lane).
+struct TileCodes {
+  u32x4_t k0, k1, v0, v1;
+};
+
+__device__ __forceinline__ TileCodes codes_from_stage(const uint8_t* st, int lane) {
+  return {ld16(st + 16 * lane), ld16(st + 1024 + 16 * lane), ld16(st + 2048 + 16 * lane),
+          ld16(st + 3072 + 16 * lane)};
+}
+
+// Tile compute from the lane's code words and the record's metadata KiB in
+// LDS (`meta`: K scale/zero slots at +0, V scale/zero at +512).
 //   K: S = sum n * (hi + lo)(q s) in 2^-24 units (codes are subnormals);
 //      Z (every row) = sum q z (raw units); score = S * 2^24 + Z.
 //   V: O[j] += sum n * fp16(16 P s) in 2^-20 units; OZ row r = sum P z of
 //      32-channel group r & 3.
-__device__ __forceinline__ void compute_tile(const uint8_t* st, int lane, int c, int g,
+__device__ __forceinline__ void compute_tile(const TileCodes& cw, const uint8_t* meta, int c, int g,
                                              const TileConsts& tc, uint32_t half_mask,
                                              float& m_run, float4_t& L, float4_t O[8],
                                              float4_t& OZ) {
-  const u32x4_t kq0 = ld16(st + 16 * lane);
-  const u32x4_t kq1 = ld16(st + 1024 + 16 * lane);
+  const u32x4_t kq0 = cw.k0, kq1 = cw.k1;
   float4_t S[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
   float4_t Z = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
-    const uint8_t* km = st + 4096 + (4 * s + g) * 32;
+    const uint8_t* km = meta + (4 * s + g) * 32;
     const u32x4_t ks = ld16(km);
     const u32x4_t kz = ld16(km + 16);  // zero points
     // q s as hi + lo fp16 pair: hi = fp16(q s), lo = fp16(q s - hi) by one fma (exact)
@@ -349,9 +376,8 @@ __device__ __forceinline__ void compute_tile(const uint8_t* st, int lane, int c,
   // scale/zero blocks (entry (gd, r): 4 scales, then 4 zeros of tokens 16m + 4r
   // + i); the k-slice's elements 0-3 are half 0, 4-7 half 1.  An unselected
   // half was not loaded: its scale/zero enter as 0 (its P is 0 as well).
-  const u32x4_t vh0 = ld16(st + 2048 + 16 * lane);
-  const u32x4_t vh1 = ld16(st + 3072 + 16 * lane);
-  const uint8_t* vm = st + 4608;
+  const u32x4_t vh0 = cw.v0, vh1 = cw.v1;
+  const uint8_t* vm = meta + 512;
   auto vmeta8 = [&](int entry, int off) {
     const u32x2_t a = ld8(vm + entry * 16 + off), b2 = ld8(vm + 256 + entry * 16 + off);
     const bool h0 = half_mask & 1u, h1 = half_mask & 2u;
@@ -404,15 +430,22 @@ __device__ __forceinline__ int bf16_row(const AttnParams& p, const int64_t* idx_
 // (no quantized tile in the kernel), channel 8c + j (dword 4c + j/2, half
 // j%2) so that each V row is one 16-byte load per lane; O[j][i] of lane
 // (c, g) is then channel 32g + 8i + j.
+// A residual tile's rows in registers: K rows kx[s][m] (token c + 16m, dims
+// 8(4s+g) .. +7), V rows vx[e] (token TAU[g][e]), and the tokens that exist
+// (bit e: token TAU[g][e] is within the list and not masked).  Rows are loaded
+// without branches: a missing token loads row 0 of the buffer (it exists
+// whenever the wave has a residual tile), its score is masked and its V row
+// zeroed before use (the row may hold any bits).
+struct ResidualTile {
+  u32x4_t kx[4][2];
+  u32x4_t vx[8];
+  uint32_t vvalid;
+};
+
 template <bool kBf16Only>
-__device__ __forceinline__ void residual_tile(const AttnParams& p, int b, int h, int base, int valid,
-                                              int c, int g, const bf16x8_t qN[4], float qs,
-                                              float& m_run, float4_t& L, float4_t O[8],
-                                              float4_t& OZ) {
-  const uint16_t* kr = p.k_res + b * p.kr_sb + h * p.kr_sh;
-  const uint16_t* vr = p.v_res + b * p.vr_sb + h * p.vr_sh;
+__device__ __forceinline__ void residual_rows(const AttnParams& p, int b, int h, int base, int valid, int c, int g,
+                                              int (&krow)[2], int (&vrow)[8]) {
   const int64_t* idx_bh = p.res_idx ? p.res_idx + b * p.ri_sb + h * p.ri_sh : nullptr;
-  int krow[2], vrow[8];
 #pragma unroll
   for (int m = 0; m < 2; ++m) krow[m] = c + 16 * m < valid ? bf16_row(p, idx_bh, base + c + 16 * m) : -1;
 #pragma unroll
@@ -420,57 +453,118 @@ __device__ __forceinline__ void residual_tile(const AttnParams& p, int b, int h,
     const int tok = (e < 4) ? (4 * g + e) : (16 + 4 * g + e - 4);
     vrow[e] = tok < valid ? bf16_row(p, idx_bh, base + tok) : -1;
   }
-  // bf16-only kernels (few live registers) request the V rows together with
-  // the K rows: one memory round trip after the row indices
-  u32x4_t vx[8];
-  auto load_v = [&]() {
+}
+
+// `dummy` (when not null) replaces every address: a wave without a residual
+// tile issues the same loads, all lanes on one line, so that every wave has
+// the same loads in flight (the compiler's wait counting then stays exact).
+template <bool kBf16Only>
+__device__ __forceinline__ void residual_load_v(const AttnParams& p, int b, int h, int c, const int (&vrow)[8],
+                                                ResidualTile& rt, const void* dummy = nullptr) {
+  const uint16_t* vr = p.v_res + b * p.vr_sb + h * p.vr_sh;
+  rt.vvalid = 0;
+  // every row address before the first load: the allocator otherwise reuses
+  // a pending load's register as a don't-care operand of the 64-bit address
+  // arithmetic, which makes the compiler wait for that load
+  const uint32_t* row[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      vx[e] = u32x4_t{0u, 0u, 0u, 0u};
-      if (vrow[e] >= 0) {
-        if constexpr (kBf16Only) {
-          vx[e] = ld16(vr + vrow[e] * p.vr_st + 8 * c);
-        } else {
-          const uint32_t* row = reinterpret_cast<const uint32_t*>(vr + vrow[e] * p.vr_st) + c;
+  for (int e = 0; e < 8; ++e) {
+    rt.vvalid |= vrow[e] >= 0 ? 1u << e : 0u;
+    row[e] = dummy ? reinterpret_cast<const uint32_t*>(dummy)
+                   : reinterpret_cast<const uint32_t*>(vr + static_cast<int64_t>(max(vrow[e], 0)) * p.vr_st) +
+                         (kBf16Only ? 4 * c : c);
+  }
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-          for (int G = 0; G < 4; ++G) vx[e][G] = row[16 * G];
-        }
-      }
+  for (int e = 0; e < 8; ++e) {
+    if constexpr (kBf16Only) {
+      rt.vx[e] = ld16(row[e]);
+    } else {
+#pragma unroll
+      for (int G = 0; G < 4; ++G) rt.vx[e][G] = row[e][dummy ? 0 : 16 * G];
     }
-  };
-  u32x4_t kx[4][2];
+  }
+}
+
+template <bool kBf16Only>
+__device__ __forceinline__ void residual_load_k(const AttnParams& p, int b, int h, int g, const int (&krow)[2],
+                                                ResidualTile& rt, const void* dummy = nullptr) {
+  const uint16_t* kr = p.k_res + b * p.kr_sb + h * p.kr_sh;
+  const uint16_t* row[2];  // addresses first, as in residual_load_v
+#pragma unroll
+  for (int m = 0; m < 2; ++m)
+    row[m] = dummy ? static_cast<const uint16_t*>(dummy)
+                   : kr + static_cast<int64_t>(max(krow[m], 0)) * p.kr_st + 8 * g;
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int s = 0; s < 4; ++s)
 #pragma unroll
-    for (int m = 0; m < 2; ++m)
-      kx[s][m] = krow[m] >= 0 ? ld16(kr + krow[m] * p.kr_st + 8 * (4 * s + g)) : u32x4_t{0u, 0u, 0u, 0u};
-  if constexpr (kBf16Only) load_v();
+    for (int m = 0; m < 2; ++m) rt.kx[s][m] = ld16(row[m] + (dummy ? 0 : 32 * s));
+}
+
+// Scores, online softmax and the V product of a residual tile whose K rows
+// are loaded (and V rows too unless `vrow` is given: then they are requested
+// after the softmax, when fewer registers are live).
+template <bool kBf16Only>
+__device__ __forceinline__ void residual_finish(const AttnParams& p, int b, int h, int c, ResidualTile& rt,
+                                                const bf16x8_t qN[4], float qs, float& m_run, float4_t& L,
+                                                float4_t O[8], float4_t& OZ, const int (*vrow)[8]) {
   float4_t S[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
 #pragma unroll
   for (int s = 0; s < 4; ++s)
 #pragma unroll
     for (int m = 0; m < 2; ++m)
-      S[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kx[s][m]), qN[s], S[m], 0, 0, 0);
+      S[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, rt.kx[s][m]), qN[s], S[m], 0, 0,
+                                                     0);
   // S[m][i] is token 4g + i + 16m = TAU[g][i + 4m]
+  const uint32_t vvalid = vrow ? [&] {
+    uint32_t v = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v |= (*vrow)[e] >= 0 ? 1u << e : 0u;
+    return v;
+  }() : rt.vvalid;
 #pragma unroll
   for (int m = 0; m < 2; ++m)
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      if (vrow[i + 4 * m] < 0) S[m][i] = -INFINITY;
+      if (!(vvalid >> (i + 4 * m) & 1u)) S[m][i] = -INFINITY;
   bf16x8_t phi, plo;
   softmax_step_bf16(S, qs, m_run, L, O, OZ, phi, plo);
-  if constexpr (!kBf16Only) load_v();
+  if (vrow) residual_load_v<kBf16Only>(p, b, h, c, *vrow, rt);
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    if (!(vvalid >> e & 1u)) rt.vx[e] = u32x4_t{0u, 0u, 0u, 0u};
   // V^T operand of M-tile j: element e = half j%2 of dword j/2 of token
   // TAU[g][e]'s loaded row (v_perm_b32 picks the halves of a token pair)
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
-    const u32x4_t a = {__builtin_amdgcn_perm(vx[1][j >> 1], vx[0][j >> 1], sel),
-                       __builtin_amdgcn_perm(vx[3][j >> 1], vx[2][j >> 1], sel),
-                       __builtin_amdgcn_perm(vx[5][j >> 1], vx[4][j >> 1], sel),
-                       __builtin_amdgcn_perm(vx[7][j >> 1], vx[6][j >> 1], sel)};
+    const u32x4_t a = {__builtin_amdgcn_perm(rt.vx[1][j >> 1], rt.vx[0][j >> 1], sel),
+                       __builtin_amdgcn_perm(rt.vx[3][j >> 1], rt.vx[2][j >> 1], sel),
+                       __builtin_amdgcn_perm(rt.vx[5][j >> 1], rt.vx[4][j >> 1], sel),
+                       __builtin_amdgcn_perm(rt.vx[7][j >> 1], rt.vx[6][j >> 1], sel)};
     O[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), phi, O[j], 0, 0, 0);
     O[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), plo, O[j], 0, 0, 0);
+  }
+}
+
+// One whole residual tile.  kEarlyV (kernels with registers to spare)
+// requests the V rows together with the K rows: one memory round trip after
+// the row indices, not two.
+template <bool kBf16Only, bool kEarlyV>
+__device__ __forceinline__ void residual_tile(const AttnParams& p, int b, int h, int base, int valid,
+                                              int c, int g, const bf16x8_t qN[4], float qs,
+                                              float& m_run, float4_t& L, float4_t O[8],
+                                              float4_t& OZ) {
+  int krow[2], vrow[8];
+  residual_rows<kBf16Only>(p, b, h, base, valid, c, g, krow, vrow);
+  ResidualTile rt;
+  residual_load_k<kBf16Only>(p, b, h, g, krow, rt);
+  if constexpr (kEarlyV) {
+    residual_load_v<kBf16Only>(p, b, h, c, vrow, rt);
+    residual_finish<kBf16Only>(p, b, h, c, rt, qN, qs, m_run, L, O, OZ, nullptr);
+  } else {
+    residual_finish<kBf16Only>(p, b, h, c, rt, qN, qs, m_run, L, O, OZ, &vrow);
   }
 }
 
@@ -481,19 +575,47 @@ __device__ __forceinline__ void store_out(const AttnParams& p, int64_t row, int 
     reinterpret_cast<uint16_t*>(p.out)[row * 128 + d] = f32_to_bf16_bits(v);
 }
 
-template <int NW, int D>
+constexpr int kMetaBytes = 1024;  // the record's last KiB: K and V scale/zero
+constexpr int kMaxGqa = 16;       // query heads per KV head (checked on the host)
+// A bf16 residual tile (two dependent memory round trips, 16 KiB) takes a
+// wave about as long as three quantized tiles; splits and waves are balanced
+// with that weight.
+constexpr int kResidualTileWeight = 3;
+// Register budget of the dense kernels, as resident waves per SIMD: a 4-wave
+// workgroup gets 168 VGPRs (3 waves per SIMD, 3 workgroups per CU); an 8-wave
+// workgroup puts 2 waves on each SIMD, and 2 workgroups would need 128 VGPRs,
+// which spills, so it keeps one workgroup per CU with up to 256 VGPRs.
+constexpr int dense_waves_per_simd(int nw) { return nw == 8 ? 2 : 3; }
+
+// LDS of a workgroup: the tile rings, reused by the final merge of the NW
+// waves (o [NW][gqa][128] fp32, then m and l [NW][gqa] each).
+//   dense quantized tiles (kVgpr): the 4 KiB of code words of a tile go
+//     straight to VGPRs (a D-slot register ring); only the metadata KiB
+//     streams through LDS (a D-stage DMA ring per wave).  An LDS-DMA-only
+//     ring streams at ~76% of HBM on gfx950, code words in VGPRs at ~88%.
+//   page-sparse and bf16-only tiles: a D-stage ring of whole 5 KiB records.
+template <int NW, int D, bool kSparse, bool kBf16Only>
 struct KernelShape {
-  static constexpr int kLdsBytes = NW * D * kStageBytes;
+  static constexpr bool kVgpr = !kSparse && !kBf16Only;
+  static constexpr int kStage = kVgpr ? kMetaBytes : kStageBytes;
+  static constexpr int kRingBytes = NW * D * kStage;
+  static constexpr int kMergeBytes = NW * kMaxGqa * (128 + 2) * 4;
+  static constexpr int kLdsBytes = std::max(kRingBytes, kMergeBytes);
   // resident waves per SIMD when LDS (160 KiB per CU) is the limit
   static constexpr int kWgPerCu = (160 * 1024) / kLdsBytes;
   static constexpr int kWavesPerSimd = std::max(1, std::min(4, (kWgPerCu * NW) / 4));
+  // the occupancy the register allocation targets
+  static constexpr int kWavesPerEu = kBf16Only ? 2 : (kVgpr ? dense_waves_per_simd(NW) : kWavesPerSimd);
 };
 
 template <int NW, int D, bool kSparse, bool kBf16Only = false>
 __global__ __launch_bounds__(64 * NW)
-__attribute__((amdgpu_waves_per_eu(kBf16Only ? 2 : KernelShape<NW, D>::kWavesPerSimd)))
+__attribute__((amdgpu_waves_per_eu(KernelShape<NW, D, kSparse, kBf16Only>::kWavesPerEu)))
 void kivi4_attn_kernel(const AttnParams p) {
-  __shared__ __attribute__((aligned(16))) uint8_t smem[NW][D][kStageBytes];
+  using KS = KernelShape<NW, D, kSparse, kBf16Only>;
+  constexpr int kStage = KS::kStage;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[KS::kLdsBytes];
+  __shared__ int s_prog[KS::kVgpr ? NW : 1];  // dense: tiles done per wave
   const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   // wave index through readfirstlane: the compiler then keeps the ring and
   // tile bookkeeping in SGPRs (scalar branches, scalar DMA base addresses)
@@ -503,7 +625,7 @@ void kivi4_attn_kernel(const AttnParams p) {
   const int64_t bh = static_cast<int64_t>(b) * p.kv + h;
 
   const int T0 = split * p.tiles_per_split;
-  uint8_t (*ring)[kStageBytes] = smem[wave];
+  uint8_t (*ring)[kStage] = reinterpret_cast<uint8_t (*)[kStage]>(smem + wave * D * kStage);
   int n_qt = p.n_groups;  // quantized tiles of (b, kv)
   if constexpr (kSparse) {
     // Every wave walks the page list (64 pages per step, the pairing by
@@ -563,14 +685,57 @@ void kivi4_attn_kernel(const AttnParams p) {
       return 3u;
   };
 
-  // Start the HBM stream before anything else.
-  int issued = 0;
+  // dense tiles: tile k's code words into register slot k % D, its metadata
+  // KiB into LDS stage k % D (4 loads + 1 DMA, in that order)
+  TileCodes creg[KS::kVgpr ? D : 1];
+  const uint8_t* rec0 = reinterpret_cast<const uint8_t*>(p.groups + bh * p.g_cap * kRecordWords) + 16 * lane;
+  // tile k of this wave, k clamped to its last tile: the refills past the end
+  // reload that one (record 0 of the sequence for a wave without tiles; the
+  // dense kernels run only when there is at least one quantized group)
+  auto issue_vgpr = [&](int k, TileCodes& cw, uint8_t* stage) {
+    const int gi = nq > 0 ? T0 + wave + NW * min(max(k, 0), nq - 1) : 0;
+    const uint8_t* rec = rec0 + static_cast<int64_t>(gi) * kStageBytes;
+    cw.k0 = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(rec));
+    cw.k1 = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(rec + 1024));
+    cw.v0 = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(rec + 2048));
+    cw.v1 = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(rec + 3072));
+    dma16_untracked(rec + 4096, stage);
+  };
+
+  const uint16_t* qp = p.q + b * p.q_sb + static_cast<int64_t>(h * p.gqa + (col_ok ? c : 0)) * p.q_sh;
+  // q (dims 8(4s+g) .. +7) ahead of the tile stream, whose first tiles would
+  // otherwise have to land before q does
+  u32x4_t q_raw[4];
+  if constexpr (!kBf16Only) {
 #pragma unroll
-  for (int k = 0; k < D - 1; ++k)
-    if (issued < nq) {
-      issue_tile(p, bh, group_of(issued), lane, ring[issued % D], mask_of(issued));
-      ++issued;
+    for (int s = 0; s < 4; ++s) q_raw[s] = ld16(qp + 8 * (4 * s + g));
+  }
+
+  // 8-wave, 2-stage dense kernels (registers to spare) request the rows of their first
+  // residual tile right after q and compute it when the first quantized
+  // round begins: its memory round trip then overlaps the first tiles' loads
+  // instead of running alone after the loop.  Waves without a residual tile
+  // issue the same loads on q's line (no branch around loads: see
+  // residual_load_v).
+  constexpr bool kPrefetchRes = KS::kVgpr && NW == 8 && D == 2;  // (8x3 would spill)
+  const bool has_res = kPrefetchRes && max(T0, n_qt) + wave < T1;
+  bool res_pending = has_res;
+  ResidualTile rt0;
+  if constexpr (kPrefetchRes) {
+    const int base = (max(T0, n_qt) + wave - n_qt) * kTile;
+    int krow[2], vrow[8];
+    if (has_res) {
+      residual_rows<false>(p, b, h, base, min(kTile, p.res_len - base), c, g, krow, vrow);
+    } else {
+#pragma unroll
+      for (int m = 0; m < 2; ++m) krow[m] = -1;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) vrow[e] = -1;
     }
+    const void* dummy = has_res ? nullptr : static_cast<const void*>(p.q + b * p.q_sb + h * p.gqa * p.q_sh);
+    residual_load_k<false>(p, b, h, g, krow, rt0, dummy);
+    residual_load_v<false>(p, b, h, c, vrow, rt0, dummy);
+  }
 
   float4_t O[8];
 #pragma unroll
@@ -578,7 +743,39 @@ void kivi4_attn_kernel(const AttnParams p) {
   float4_t OZ = {0.0f, 0.0f, 0.0f, 0.0f};
   float m_run = kNegBig;
   float4_t L = {0.0f, 0.0f, 0.0f, 0.0f};
-  const uint16_t* qp = p.q + b * p.q_sb + static_cast<int64_t>(h * p.gqa + (col_ok ? c : 0)) * p.q_sh;
+
+  // bf16 residual tiles of this wave (at most r_cap / 32 of them, in the last
+  // splits; tile t goes to wave t - max(T0, n_qt) mod NW), in real units,
+  // from the wave's `first`-th one on
+  auto residual_tiles = [&](int first) {
+    const int t0 = max(T0, n_qt) + wave + NW * first;
+    if (t0 < T1) {
+      // q as stored (bf16, dims 8(4s+g) .. +7 in order), the B operand of the bf16 K-MFMA
+      bf16x8_t qN[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        qN[s] = __builtin_bit_cast(bf16x8_t, col_ok ? ld16(qp + 8 * (4 * s + g)) : u32x4_t{0u, 0u, 0u, 0u});
+      for (int t = t0; t < T1; t += NW) {
+        const int base = (t - n_qt) * kTile;
+        residual_tile<kBf16Only, kBf16Only || (KS::kVgpr && NW == 8)>(p, b, h, base, min(kTile, p.res_len - base),
+                                                                       c, g, qN, p.qscale, m_run, L, O, OZ);
+      }
+    }
+  };
+
+  // Start the HBM stream.
+  int issued = 0;
+  if constexpr (KS::kVgpr) {
+    // (the dense stream starts inside its tile loop, in a first round that
+    // only issues)
+  } else {
+#pragma unroll
+    for (int k = 0; k < D - 1; ++k)
+      if (issued < nq) {
+        issue_tile(p, bh, group_of(issued), lane, ring[issued % D], mask_of(issued));
+        ++issued;
+      }
+  }
 
   if constexpr (!kBf16Only) {
     // ---- q as the K-MFMA B operand (element e of block 4s+g = channel 8(4s+g)+KSLOT[e]) ----
@@ -587,7 +784,7 @@ void kivi4_attn_kernel(const AttnParams p) {
       constexpr int kslot[8] = {0, 4, 1, 5, 2, 6, 3, 7};
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        const u32x4_t raw = ld16(qp + 8 * (4 * s + g));
+        const u32x4_t raw = q_raw[s];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const uint32_t wv = raw[kslot[e] >> 1];
@@ -602,21 +799,88 @@ void kivi4_attn_kernel(const AttnParams p) {
       tc.qs24 = p.qscale * kTwo24;
     }
 
-    // ---- quantized tiles through this wave's D-stage LDS ring ----
-    for (int k = 0; k < nq; ++k) {
-      if (issued < nq) {
-        issue_tile(p, bh, group_of(issued), lane, ring[issued % D], mask_of(issued));
-        ++issued;
+    if constexpr (KS::kVgpr) {
+      // ---- dense quantized tiles: D register slots + D metadata stages,
+      // unrolled by D so that every slot index is static ----
+      // Tile t sits in slot t % D.  Whole rounds of D tiles first, with no
+      // exit inside a round: a conditional refill or an early exit makes the
+      // compiler's wait counting drain every load (vmcnt(0)) at the next tile.
+      //
+      // Waves w and w + 4 of an 8-wave workgroup share a SIMD, whose issue
+      // arbitration favours the older wave: left alone, waves 0-3 finish
+      // their tiles ~6% of the loop ahead of waves 4-7, which then run with
+      // half the SIMD idle.  Each wave publishes its progress (tiles done,
+      // a residual tile counting kResidualTileWeight) and raises its priority
+      // while it is behind its SIMD sibling.  Only the timing changes: every
+      // wave computes the same tiles in the same order.
+      constexpr bool kBalance = NW == 8;
+      int prog = 0;
+      if (kBalance && lane == 0) s_prog[wave] = prog;
+      //
+      // The loop starts one round early (k0 = -D): that round issues tiles
+      // 0 .. D - 2 (and a reload of tile 0) and computes nothing.  With the
+      // first issues inside the loop, each register slot has one definition
+      // and the allocator adds no copies of in-flight loads before the loop
+      // (a copy waits for its load: a separate prologue drained the stream).
+      int k0 = -D;
+      for (; k0 + D <= nq; k0 += D) {
+#pragma unroll
+        for (int j = 0; j < D; ++j) {
+          const int sib = kBalance ? s_prog[wave ^ 4] : 0;  // read early, used after the tile
+          // refill the slot tile k0 + j - 1 used with tile k0 + j + D - 1
+          issue_vgpr(k0 + j + D - 1, creg[(j + D - 1) % D], ring[(j + D - 1) % D]);
+          if (k0 < 0) continue;
+          if (j == 0 && res_pending) {
+            // the prefetched residual tile, while tile 0 lands; the quantized
+            // tiles accumulate O in 2^-20 units, so its part is scaled to
+            // those units (exactly: a power of 2)
+            bf16x8_t qN[4];  // q as stored, the B operand of the bf16 K-MFMA
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+              qN[s] = __builtin_bit_cast(bf16x8_t, col_ok ? q_raw[s] : u32x4_t{0u, 0u, 0u, 0u});
+            residual_finish<false>(p, b, h, c, rt0, qN, p.qscale, m_run, L, O, OZ, nullptr);
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj) O[jj] = O[jj] * (1.0f / kTwo20);
+            res_pending = false;
+            prog += kResidualTileWeight;
+          }
+          // 5 ops per tile, D - 1 tiles issued after tile k0 + j: its
+          // metadata DMA (issued last) has landed once 5 (D - 1) ops remain
+          wait_vmcnt<5 * (D - 1)>();
+          __builtin_amdgcn_sched_barrier(0);
+          compute_tile(creg[j], ring[j], c, g, tc, 3u, m_run, L, O, OZ);
+          if constexpr (kBalance) {
+            ++prog;
+            if (lane == 0) s_prog[wave] = prog;
+            if (prog < __builtin_amdgcn_readfirstlane(sib))
+              __builtin_amdgcn_s_setprio(1);
+            else
+              __builtin_amdgcn_s_setprio(0);
+          }
+        }
       }
-      const uint32_t half_mask = mask_of(k);
-      if constexpr (kSparse) {
+      if constexpr (kBalance) __builtin_amdgcn_s_setprio(0);
+      // the last nq - k0 < D tiles are in slots 0 .. nq - k0 - 1; this wait
+      // also drains the reloads past the end, whose LDS the merge reuses
+      wait_vmcnt<0>();
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int j = 0; j < D - 1; ++j)
+        if (k0 + j < nq) compute_tile(creg[j], ring[j], c, g, tc, 3u, m_run, L, O, OZ);
+    } else {
+      // ---- page-sparse tiles through this wave's D-stage LDS ring ----
+      for (int k = 0; k < nq; ++k) {
+        if (issued < nq) {
+          issue_tile(p, bh, group_of(issued), lane, ring[issued % D], mask_of(issued));
+          ++issued;
+        }
+        const uint32_t half_mask = mask_of(k);
         int later = 0;  // DMA ops issued after tile k's
         for (int t = k + 1; t < issued; ++t) later += tile_dma_ops(mask_of(t));
         wait_ops_in_flight(later);
-      } else {
-        wait_tiles_in_flight(issued - 1 - k);
+        compute_tile(codes_from_stage(ring[k % D], lane), ring[k % D] + 4096, c, g, tc, half_mask, m_run, L,
+                     O, OZ);
       }
-      compute_tile(ring[k % D], lane, c, g, tc, half_mask, m_run, L, O, OZ);
     }
     // O to real units: O * 2^20 + sum P z of the M-tile's group (OZ component
     // i = row 4g + i holds group i's sum; M-tile j lies in group j / 2)
@@ -626,25 +890,27 @@ void kivi4_attn_kernel(const AttnParams p) {
       for (int i = 0; i < 4; ++i) O[j][i] = __builtin_fmaf(O[j][i], kTwo20, OZ[j >> 1]);
   }
 
-  // ---- bf16 residual tiles (at most r_cap / 32 of them, in the last split) ----
-  if (max(T0, n_qt) + wave < T1) {
-    // q as stored (bf16, dims 8(4s+g) .. +7 in order), the B operand of the
-    // bf16 K-MFMA; read here, after the quantized tiles, to keep registers free
-    bf16x8_t qN[4];
+  // ---- bf16 residual tiles after the quantized ones: all of them in the
+  // page-sparse and bf16-only kernels (q read here keeps registers free in
+  // their loops); in the dense kernels the prefetched tile of a wave with no
+  // full quantized round, and the wave's further residual tiles ----
+  if constexpr (kPrefetchRes) {
+    if (res_pending) {
+      bf16x8_t qN[4];
 #pragma unroll
-    for (int s = 0; s < 4; ++s)
-      qN[s] = __builtin_bit_cast(bf16x8_t, col_ok ? ld16(qp + 8 * (4 * s + g)) : u32x4_t{0u, 0u, 0u, 0u});
-    for (int t = max(T0, n_qt) + wave; t < T1; t += NW) {
-      const int base = (t - n_qt) * kTile;
-      residual_tile<kBf16Only>(p, b, h, base, min(kTile, p.res_len - base), c, g, qN, p.qscale, m_run, L, O,
-                               OZ);
+      for (int s = 0; s < 4; ++s)
+        qN[s] = __builtin_bit_cast(bf16x8_t, col_ok ? ld16(qp + 8 * (4 * s + g)) : u32x4_t{0u, 0u, 0u, 0u});
+      residual_finish<false>(p, b, h, c, rt0, qN, p.qscale, m_run, L, O, OZ, nullptr);
     }
+    residual_tiles(1);
+  } else {
+    residual_tiles(0);
   }
 
   // ---- merge the NW waves through LDS (the rings are free now) ----
   const float l_tot = L[0];
   __syncthreads();
-  float* red_o = reinterpret_cast<float*>(&smem[0][0][0]);  // [NW][gqa][128]
+  float* red_o = reinterpret_cast<float*>(smem);  // [NW][gqa][128]
   float* red_m = red_o + NW * p.gqa * 128;                    // [NW][gqa]
   float* red_l = red_m + NW * p.gqa;                          // [NW][gqa]
   if (col_ok) {
@@ -784,7 +1050,7 @@ struct SplitPlan {
 constexpr int kSparseNW = 8, kSparseD = 4;
 
 // Kernel shape: NW waves per workgroup, D ring stages per wave.
-// ZKV_ATTN_SHAPE=NWxD (e.g. 4x2) overrides the default for tuning sweeps.
+// ZKV_ATTN_SHAPE=NWxD (e.g. 4x3) overrides the dense default for tuning sweeps.
 struct Shape {
   int nw, d;
 };
@@ -794,21 +1060,29 @@ Shape attn_shape() {
     Shape s{8, 2};
     if (const char* e = getenv("ZKV_ATTN_SHAPE")) {
       int nw = 0, d = 0;
-      if (sscanf(e, "%dx%d", &nw, &d) == 2 &&
-          ((nw == 4 && (d == 2 || d == 3)) || (nw == 8 && d == 2) || (nw == 2 && (d == 3 || d == 4))))
-        s = {nw, d};
+      if (sscanf(e, "%dx%d", &nw, &d) == 2 && (nw == 4 || nw == 8) && (d == 2 || d == 3)) s = {nw, d};
     }
     return s;
   }();
   return sh;
 }
 
-SplitPlan plan_splits(int bs, int kv, int n_groups, int res_len, int n_splits, Shape sh = attn_shape()) {
+// Resident workgroups per CU: LDS (160 KiB per CU) and waves (4 SIMDs, at most
+// `waves_per_simd` waves each at the kernel's register budget).
+int wgs_per_cu(Shape sh, int stage_bytes, int waves_per_simd) {
+  const int lds = std::max(sh.nw * sh.d * stage_bytes, sh.nw * kMaxGqa * (128 + 2) * 4);
+  return std::max(1, std::min((160 * 1024) / lds, 4 * waves_per_simd / sh.nw));
+}
+
+// Defaults: the dense kernels (metadata-only LDS stages).
+SplitPlan plan_splits(int bs, int kv, int n_groups, int res_len, int n_splits, Shape sh = attn_shape(),
+                      int stage_bytes = kMetaBytes, int waves_per_simd = 0) {
+  if (waves_per_simd <= 0) waves_per_simd = dense_waves_per_simd(sh.nw);
   const int n_tiles = std::max(n_groups + (res_len + kTile - 1) / kTile, 1);
   int ns = n_splits;
   if (ns <= 0) {
-    const int wg_per_cu = std::max(1, std::min((160 * 1024) / (sh.nw * sh.d * kStageBytes), 16 / sh.nw));
-    const int target = 256 * wg_per_cu;  // one resident workgroup per split on 256 CUs
+    // one resident workgroup per split on 256 CUs
+    const int target = 256 * wgs_per_cu(sh, stage_bytes, waves_per_simd);
     const int units = bs * kv;
     ns = (target + units - 1) / units;
     if (n_groups > 0) {
@@ -822,7 +1096,14 @@ SplitPlan plan_splits(int bs, int kv, int n_groups, int res_len, int n_splits, S
     }
   }
   ns = std::max(1, std::min(ns, n_tiles));
-  const int per = (n_tiles + ns - 1) / ns;
+  // contiguous tile ranges [s * per, (s + 1) * per), the residual tiles last:
+  // with quantized tiles present, per covers an equal share of the weighted
+  // work, so the splits holding residual tiles get fewer quantized ones
+  const int n_res_tiles = n_tiles - n_groups;
+  const int64_t work = n_groups > 0 ? static_cast<int64_t>(n_groups) + int64_t{kResidualTileWeight} * n_res_tiles
+                                    : n_tiles;
+  int per = static_cast<int>(std::min<int64_t>((work + ns - 1) / ns, n_tiles));
+  if ((n_tiles + per - 1) / per < ns) per = (n_tiles + ns - 1) / ns;  // keep the split count
   ns = (n_tiles + per - 1) / per;
   return {ns, per};
 }
@@ -844,12 +1125,10 @@ void launch_attn(const AttnParams& p, int bs, hipStream_t s) {
   } else if (p.n_groups == 0) {  // bf16 rows only: the 16-byte V layout
     kivi4_attn_kernel<8, 2, false, true><<<grid, 512, 0, s>>>(p);
   } else if (sh.nw == 8) {
-    kivi4_attn_kernel<8, 2, false><<<grid, 512, 0, s>>>(p);
-  } else if (sh.nw == 2) {
-    if (sh.d == 4)
-      kivi4_attn_kernel<2, 4, false><<<grid, 128, 0, s>>>(p);
+    if (sh.d == 3)
+      kivi4_attn_kernel<8, 3, false><<<grid, 512, 0, s>>>(p);
     else
-      kivi4_attn_kernel<2, 3, false><<<grid, 128, 0, s>>>(p);
+      kivi4_attn_kernel<8, 2, false><<<grid, 512, 0, s>>>(p);
   } else if (sh.d == 3) {
     kivi4_attn_kernel<4, 3, false><<<grid, 256, 0, s>>>(p);
   } else {
@@ -880,7 +1159,7 @@ struct SparsePages {
 // Sparse mode: every split is planned for the longest page list (n_sel
 // tiles); each wave keeps at most 64 tile descriptors in its lanes.
 SplitPlan plan_sparse_splits(int bs, int kv, int n_sel, int res_len, int n_splits) {
-  SplitPlan sp = plan_splits(bs, kv, n_sel, res_len, n_splits, Shape{kSparseNW, kSparseD});
+  SplitPlan sp = plan_splits(bs, kv, n_sel, res_len, n_splits, Shape{kSparseNW, kSparseD}, kStageBytes, 4);
   constexpr int kMaxPerSplit = 64 * kSparseNW;
   if (sp.tiles_per_split > kMaxPerSplit) {
     const int n_tiles = n_sel + (res_len + kTile - 1) / kTile;
