@@ -549,14 +549,106 @@ def c4_cpu_baseline(pool, qs, signs, topk, budget_s: float = 10.0):
                       f"({t * 1e3:.0f} ms each); host {os.cpu_count()} logical CPUs, 1 used"}
 
 
+def run_r4(args):
+    """R4: ParisKV 4-bit RaBitQ codes (1-bit sign + 3-bit magnitude) at the
+    decode shape the reference's rerank module documents
+    (Z/cache_hub/rerank/rerank.py:1-20: one layer, kv_len ~128K, ~13K
+    candidates (10%), final_topk 100).  Per step: the 8 KV heads' queries to
+    SRHT blocks, the 4-bit approximate scores of the candidates, and their
+    top-100 key indices.  4 caches rotate between steps (96 MB of codes and
+    weights each in the reference's [16, seq] layout: 384 MB > the MALL)."""
+    import torch
+    from zoomkv_revision_amd import rabitq4
+    bs, kv, L, C, k, n_caches = 1, 8, 131072, 13108, 100, 4
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(42)
+    signs = (torch.randint(0, 2, (128,), device=dev, generator=gen) * 2 - 1).to(torch.bfloat16)
+    thr, ctr = rabitq4.magnitude_levels(device=dev)
+    caches = []
+    for i in range(n_caches):
+        keys = torch.randn(bs, kv, L, 128, device=dev, generator=gen).to(torch.bfloat16)
+        code, w, packed = rabitq4.batch_encode(keys, signs, thr, ctr)
+        cand = torch.stack([torch.randperm(L, device=dev, generator=gen)[:C] for _ in range(kv)]).view(bs, kv, C)
+        caches.append((packed, w, cand))
+    keys = torch.randn(bs, kv, L, 128, device=dev, generator=gen).to(torch.bfloat16)
+    q = torch.randn(bs, kv, 128, device=dev, generator=gen).to(torch.bfloat16)
+    f32 = torch.empty(bs, kv, C, dtype=torch.float32, device=dev)
+
+    def step(i):
+        packed, w, cand = caches[i % n_caches]
+        qb, qn = rabitq4.encode_query_blocks(q, signs)
+        return rabitq4.rabitq_rerank_topk(cand, packed, w, qb, qn, ctr, k)
+
+    ms = timed_loop(step, args.steps, args.warmup)
+    qb, qn = rabitq4.encode_query_blocks(q, signs)
+    k_ms = kernel_batch_ms(lambda i: rabitq4._rerank(caches[i % n_caches][2], caches[i % n_caches][0],
+                                                     caches[i % n_caches][1], qb, qn, ctr, 16, 8, scores_f32=f32),
+                           args.steps)
+    code_o = torch.empty(bs, kv, 16, L, dtype=torch.uint8, device=dev)
+    w_o = torch.empty(bs, kv, 16, L, dtype=torch.bfloat16, device=dev)
+    p_o = torch.empty(bs, kv, 16, L, 4, dtype=torch.uint8, device=dev)
+    enc_ms = kernel_batch_ms(lambda i: rabitq4.encode_into(keys, signs, thr, ctr, code_o, w_o, p_o, 0), 5)
+    per_cand = 8 + 16 * 4 + 16 * 2 + 4          # index, 16 code words, 16 weights, fp32 score
+    algo = C * kv * per_cand + kv * (256 + 2)
+    achieved = algo / (k_ms * 1e-3) / 1e9
+    enc_bytes = bs * kv * L * (256 + 16 * 7)      # bf16 key in; sign byte, code word, weight out per block
+    cpu = None if args.no_cpu else r4_cpu_baseline(caches[0], q, signs, k)
+    return {
+        "metric": "R4 ParisKV 4-bit RaBitQ rerank + top-100 per decode step: candidates/s",
+        "value": C * kv / (ms * 1e-3), "unit": "candidates/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "u4 codes (sign + 3-bit magnitude) -> bf16 (sequential bf16 sums)",
+        "data": "synthetic (seeded N(0,1) keys and queries, random candidate sets)",
+        "config": {"workload": "R4: query SRHT blocks -> 4-bit scores of the candidates -> top-100 key indices",
+                   "batch": bs, "kv_heads": kv, "keys": L, "candidates": C, "topk": k,
+                   "caches_rotated": n_caches, "layout": "reference [16, seq] codes and weights",
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": read_traffic("r4_rabitq4_rerank_traffic.json"),
+                     "kernel": "rabitq4_rerank_kernel", "kernel_ms": k_ms, "algorithmic_bytes": algo},
+        "key_encode": {"keys_per_s": bs * kv * L / (enc_ms * 1e-3), "kernel_ms": enc_ms,
+                       "GBps": enc_bytes / (enc_ms * 1e-3) / 1e9, "keys": bs * kv * L},
+        "cpu_baseline": cpu,
+    }
+
+
+def r4_cpu_baseline(cache, q, signs, k, budget_s: float = 10.0):
+    """The numpy oracle (oracle/rabitq4.py) of one step for 1 of the 8 heads."""
+    import numpy as np
+    import torch
+    from threadpoolctl import threadpool_limits
+    from oracle import rabitq4 as r4
+    from oracle.numerics import bf16_to_f32
+    packed, w, cand = cache
+    tb = lambda t: bf16_to_f32(t.contiguous().cpu().view(torch.int16).numpy().view(np.uint16))
+    p_np, w_np, c_np = packed[0, 0].cpu().numpy(), tb(w[0, 0]), cand[0, 0].cpu().numpy()
+    q_np, s_np = tb(q[0, 0]), tb(signs)
+    times = []
+    with threadpool_limits(limits=1):
+        t_end = time.perf_counter() + budget_s
+        while time.perf_counter() < t_end or len(times) < 2:
+            t0 = time.perf_counter()
+            qb, qn = r4.encode_query(q_np, s_np)
+            sc = r4.rerank_scores(c_np, p_np, w_np, qb, qn)
+            r4.topk_gather(sc, c_np, k)
+            times.append(time.perf_counter() - t0)
+            if len(times) >= 20:
+                break
+    t = statistics.median(times)
+    return {"value": c_np.shape[0] / t, "unit": "candidates/s", "cores": 1, "kind": "port",
+            "sample": f"numpy oracle step (query blocks, 4-bit scores of {c_np.shape[0]} candidates, top-{k}) "
+                      f"for 1 of the 8 KV heads; median of {len(times)} calls ({t * 1e3:.0f} ms each); "
+                      f"host {os.cpu_count()} logical CPUs, 1 used"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--splits", type=int, default=0)
-    ap.add_argument("--config", choices=["c1", "c2", "c3", "c4", "c5", "h2d"], default="c2",
-                    help="c2 (default, the headline line), c1, c3, c4, c5 or h2d")
+    ap.add_argument("--config", choices=["c1", "c2", "c3", "c4", "c5", "r4", "h2d"], default="c2",
+                    help="c2 (default, the headline line), c1, c3, c4, c5, r4 (ParisKV 4-bit RaBitQ) or h2d")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-offload", action="store_true",
                     help="c5: skip the run with the retrieval zone in pinned host memory")
@@ -576,7 +668,7 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     if args.config != "c2":
-        run = {"c1": run_c1, "c3": run_c3, "c4": run_c4, "c5": run_c5, "h2d": run_h2d}[args.config]
+        run = {"c1": run_c1, "c3": run_c3, "c4": run_c4, "c5": run_c5, "r4": run_r4, "h2d": run_h2d}[args.config]
         print(json.dumps(run(args)))
         return
     if args.calibrate_copy:

@@ -349,6 +349,51 @@ int zkv_rabitq_search(const uint16_t* q, const uint16_t* keys, int64_t k_pool_st
                       int64_t* cand_idx, int64_t* final_idx, float* final_scores, void* workspace,
                       size_t workspace_bytes, zkv_stream_t stream);
 
+/* ---- ParisKV 4-bit RaBitQ codes (1-bit sign + 3-bit magnitude) ---------------
+ * The reference's production RaBitQ format.  Per key (bf16, 128 dims, rows
+ * 16-byte aligned) and per block b of 8 rotated dimensions:
+ *   code   uint8  (bit j = sign of dim 8b + j),       layout [..., 16, seq]
+ *   packed uint32 (nibble j = sign << 3 | magnitude), layout [..., 16, seq]
+ *          (4 bytes, byte k = v[2k] | v[2k+1] << 4)
+ *   weight bf16   (r_b / alpha_b) * ||k||,            layout [..., 16, seq]
+ * Strides are per (batch, head, block) in elements (uint32 units for packed);
+ * the token stride is 1.  signs: the SRHT +-1 vector, bf16 [128]; the
+ * magnitude levels: bf16 thresholds [7] and centers [8] (PC:266-270).
+ * Every value is rounded to bf16 where the reference's torch ops round. */
+
+/* Encode keys [bs, kv, n, 128] (element strides) into token positions
+ * t0 .. t0 + n - 1 of the code / packed / weight arrays.
+ * Replaces batch_encode (Z/cache_hub/polar_cache.py:1130-1195) with
+ * _pack_4bit_codes (:1067-1084). */
+int zkv_rabitq4_encode(const uint16_t* keys, int64_t k_sb, int64_t k_sh, int64_t k_st, int bs, int kv,
+                       int n, const uint16_t* signs, const uint16_t* mag_thresholds,
+                       const uint16_t* mag_centers, uint8_t* code, int64_t c_sb, int64_t c_sh, int64_t c_sB,
+                       uint8_t* packed, int64_t p_sb, int64_t p_sh, int64_t p_sB, uint16_t* weight,
+                       int64_t w_sb, int64_t w_sh, int64_t w_sB, int t0, zkv_stream_t stream);
+
+/* Query blocks: q bf16 rows (row stride q_sr elements) -> q_blocks bf16
+ * [rows, 16, 8] (the SRHT-rotated unit query), q_norm bf16 [rows].
+ * Replaces _encode_query_blocks (Z/cache_hub/polar_cache.py:1108-1124). */
+int zkv_rabitq4_encode_query(const uint16_t* q, int64_t q_sr, int rows, const uint16_t* signs,
+                             uint16_t* q_blocks, uint16_t* q_norm, zkv_stream_t stream);
+
+/* 4-bit approximate inner products of the candidates cand int64 [bs, kv, C]
+ * (strides cd_sb, cd_sh; unit stride along C) with the query blocks
+ * [bs * kv, 16, 8] and q_norm [bs * kv]: per block the sequential bf16 sum of
+ * bf16(+-center[t] * q), times the block weight, summed over the blocks in
+ * bf16, times ||q||.  packed: strides p_sb, p_sh, p_sB, p_st in uint32 units;
+ * weight: w_sb, w_sh, w_sB (unit token stride).  Outputs (any may be null,
+ * not both scores): scores bf16 [bs, kv, C], scores_f32 (the same values),
+ * v4b bf16 [bs, kv, 16, C, 8] (the decoded values).  A candidate outside
+ * [0, kv_len) scores -inf.
+ * Replaces partial_rerank_cuda / partial_rerank_scores_cuda
+ * (Z/cache_hub/rerank/rerank.py:352-440; kernel rerank.cu:52-143). */
+int zkv_rabitq4_rerank(const int64_t* cand, int64_t cd_sb, int64_t cd_sh, int bs, int kv, int C,
+                       const uint8_t* packed, int64_t p_sb, int64_t p_sh, int64_t p_sB, int64_t p_st,
+                       int kv_len, const uint16_t* weight, int64_t w_sb, int64_t w_sh, int64_t w_sB,
+                       const uint16_t* q_blocks, const uint16_t* q_norm, const uint16_t* mag_centers,
+                       uint16_t* scores, float* scores_f32, uint16_t* v4b, zkv_stream_t stream);
+
 /* ---------------------------------------------------------------------------
  * Host-to-device row gather (the UVA gather of
  * Z/cache_hub/gather_trans/trans_h2d.cu:43-188, trans_h2d.py:65-166).

@@ -54,6 +54,14 @@ PINNING = {
     "kivi.lse_merge": "golden vectors of lse_merge.lse_merge_torch",
     "rabitq": "popcount identity vs brute-force +-1 dot products; FWHT vs "
               "explicit Hadamard matrix; correction factor closed form",
+    "rabitq4": "golden vectors of the reference's own ParisKV code run on the CPU "
+               "(tests/golden/make_golden_rabitq4.py: polar_cache.batch_encode / "
+               "_encode_query_blocks / _pack_4bit_codes, rerank._unpack_4bit_codes, "
+               "test_rerank_topk.python_rabitq_scores): codes, weights, query blocks "
+               "and scores bit-exact; closed forms: sign bits and magnitude buckets "
+               "vs an fp64 Hadamard-matrix rotation away from thresholds, weights vs "
+               "(r / alpha) ||k|| in fp64, one-hot scores exact for every (block, "
+               "dimension, 4-bit value); top-k vs a brute-force sort",
     "torch_cpu.decode_attention": "against kivi.kivi4_decode_attention (numpy, float64) on the same "
                                   "Format Q cache, 1e-5 (tests/test_oracle_kivi.py); it is the timed "
                                   "CPU baseline of bench.py, not a checker",

@@ -1,0 +1,239 @@
+"""GPU parity of the ParisKV 4-bit RaBitQ path (zoomkv_revision_amd.rabitq4):
+key codes, block weights, query blocks and rerank scores bit-exact against
+the reference's own vectors (tests/golden/rabitq4_pariskv.npz) and against
+the CPU oracle (oracle/rabitq4.py); the top-k set against the oracle's."""
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import rabitq4 as r4
+from oracle.numerics import bf16_bits, bf16_to_f32, bf16r
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = Path(__file__).parent / "golden" / "rabitq4_pariskv.npz"
+
+
+def _zk():
+    from zoomkv_revision_amd import rabitq4
+    return rabitq4
+
+
+def _bf16(a: np.ndarray) -> torch.Tensor:
+    """float32 values on the bf16 grid -> bf16 device tensor (bit-exact)."""
+    return torch.from_numpy(bf16_bits(a).view(np.int16)).view(torch.bfloat16).cuda()
+
+
+def _bits(t: torch.Tensor) -> np.ndarray:
+    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def _levels(zk):
+    return zk.magnitude_levels(device="cuda")
+
+
+def test_levels_match_oracle():
+    zk = _zk()
+    thr, ctr = _levels(zk)
+    assert np.array_equal(_bits(thr), bf16_bits(r4.MAG_THRESHOLDS))
+    assert np.array_equal(_bits(ctr), bf16_bits(r4.MAG_CENTERS))
+
+
+def test_encode_and_rerank_match_reference_vectors():
+    """The reference's batch_encode / _encode_query_blocks / rerank model on
+    the same keys (zero, tiny, huge and one-zero-block rows included)."""
+    zk = _zk()
+    g = np.load(GOLDEN)
+    signs = _bf16(bf16_to_f32(g["signs"]))
+    keys = _bf16(bf16_to_f32(g["keys"]))
+    thr, ctr = _levels(zk)
+    code, w, packed = zk.batch_encode(keys, signs, thr, ctr)
+    torch.cuda.synchronize()
+    assert np.array_equal(code.cpu().numpy(), g["codebook"])
+    assert np.array_equal(packed.cpu().numpy(), g["packed_4bit"])
+    assert np.array_equal(_bits(w), g["block_weight"])
+    qb, qn = zk.encode_query_blocks(_bf16(bf16_to_f32(g["q"])), signs)
+    assert np.array_equal(_bits(qb), g["q_blocks"])
+    assert np.array_equal(_bits(qn), g["q_norm"])
+    cand = torch.from_numpy(g["cand"]).cuda()
+    scores, v4b = zk.partial_rerank_cuda(cand, packed, w, qb, qn, ctr, 16, 8)
+    torch.cuda.synchronize()
+    assert np.array_equal(_bits(scores), g["scores"])
+    vals = r4.decode_packed(g["packed_4bit"][0, :, :, :, :])                    # [kv, 16, seq, 8]
+    want = np.stack([vals[h][:, g["cand"][0, h]] for h in range(2)])[None]    # [1, kv, 16, C, 8]
+    assert np.array_equal(_bits(v4b), bf16_bits(want))
+
+
+@pytest.mark.parametrize("bs,kv,n,t0,cap", [(1, 1, 1, 0, 1), (2, 3, 97, 5, 130), (1, 8, 1000, 0, 1000)])
+def test_encode_matches_oracle_strided_append(rng, bs, kv, n, t0, cap):
+    """Keys from a strided view (head-major store, row stride 136), written at
+    token t0 of a larger cache; other positions untouched."""
+    zk = _zk()
+    sg = np.where(rng.integers(0, 2, 128) == 1, 1.0, -1.0).astype(np.float32)
+    x = bf16r((rng.standard_normal((bs, kv, n, 128)) * rng.uniform(0.01, 50, (bs, kv, n, 1))).astype(np.float32))
+    if n > 3:
+        x[0, 0, 1] = 0.0
+        x[0, 0, 2, 64:72] = 0.0
+    store = torch.zeros(bs, n, kv, 136, dtype=torch.bfloat16, device="cuda")
+    store[..., :128] = _bf16(x).permute(0, 2, 1, 3)
+    keys = store[..., :128].permute(0, 2, 1, 3)
+    thr, ctr = _levels(zk)
+    code = torch.full((bs, kv, 16, cap), 0xAB, dtype=torch.uint8, device="cuda")
+    w = torch.zeros(bs, kv, 16, cap, dtype=torch.bfloat16, device="cuda")
+    packed = torch.full((bs, kv, 16, cap, 4), 0xCD, dtype=torch.uint8, device="cuda")
+    zk.encode_into(keys, _bf16(sg), thr, ctr, code, w, packed, t0)
+    torch.cuda.synchronize()
+    c_np, p_np, w_np = code.cpu().numpy(), packed.cpu().numpy(), _bits(w)
+    for b in range(bs):
+        for h in range(kv):
+            oc, op, ow = r4.encode_keys(x[b, h], sg)
+            assert np.array_equal(c_np[b, h, :, t0:t0 + n], oc)
+            assert np.array_equal(p_np[b, h, :, t0:t0 + n], op)
+            assert np.array_equal(w_np[b, h, :, t0:t0 + n], bf16_bits(ow))
+    assert (c_np[..., :t0] == 0xAB).all() and (c_np[..., t0 + n:] == 0xAB).all()
+    assert (p_np[..., t0 + n:, :] == 0xCD).all()
+
+
+def test_query_blocks_match_oracle(rng):
+    zk = _zk()
+    sg = np.where(rng.integers(0, 2, 128) == 1, 1.0, -1.0).astype(np.float32)
+    q = bf16r(rng.standard_normal((3, 8, 128)).astype(np.float32))
+    q[0, 0] = 0.0
+    q[1, 2] *= 1e4
+    qb, qn = zk.encode_query_blocks(_bf16(q), _bf16(sg))
+    oqb, oqn = r4.encode_query(q, sg)
+    assert np.array_equal(_bits(qb), bf16_bits(oqb))
+    assert np.array_equal(_bits(qn)[..., 0], bf16_bits(oqn))
+
+
+def _random_cache(rng, bs, kv, L, cap=None, token_major=False):
+    """Random 4-bit codes and bf16 weights (any bit pattern is a valid code)."""
+    cap = cap or L
+    packed = rng.integers(0, 256, (bs, kv, 16, L, 4)).astype(np.uint8)
+    w = bf16r(np.abs(rng.standard_normal((bs, kv, 16, L))).astype(np.float32))
+    if token_major:   # [bs, kv, L, 16, 4] storage viewed as [bs, kv, 16, L, 4]
+        pt = torch.from_numpy(np.ascontiguousarray(packed.transpose(0, 1, 3, 2, 4))).cuda().permute(0, 1, 3, 2, 4)
+    else:
+        full = np.zeros((bs, kv, 16, cap, 4), np.uint8)
+        full[..., :L, :] = packed
+        pt = torch.from_numpy(full).cuda()[..., :L, :]
+    wfull = np.zeros((bs, kv, 16, cap), np.float32)
+    wfull[..., :L] = w
+    wt = _bf16(wfull)[..., :L]
+    return packed, w, pt, wt
+
+
+@pytest.mark.parametrize("token_major", [False, True])
+def test_rerank_matches_oracle(rng, token_major):
+    """Scores bit-exact on random codes, unsorted candidates with repeats and
+    out-of-range entries (-inf), a strided (capacity) or token-major layout."""
+    zk = _zk()
+    bs, kv, L, C = 2, 3, 700, 300
+    packed, w, pt, wt = _random_cache(rng, bs, kv, L, cap=800, token_major=token_major)
+    qb = bf16r(rng.standard_normal((bs, kv, 16, 8)).astype(np.float32))
+    qn = bf16r(np.abs(rng.standard_normal((bs, kv, 1))).astype(np.float32) + 0.1)
+    cand = rng.integers(0, L, (bs, kv, C)).astype(np.int64)
+    cand[0, 0, :3] = [-1, L, L + 5]
+    cand[1, 2, 10:20] = 7
+    _, ctr = _levels(zk)
+    scores, v4b = zk.partial_rerank_cuda(torch.from_numpy(cand).cuda(), pt, wt, _bf16(qb), _bf16(qn), ctr, 16, 8)
+    only = zk.partial_rerank_scores_cuda(torch.from_numpy(cand).cuda(), pt, wt, _bf16(qb), _bf16(qn), ctr, 16, 8)
+    torch.cuda.synchronize()
+    got = _bits(scores)
+    assert np.array_equal(got, _bits(only))
+    for b in range(bs):
+        for h in range(kv):
+            want = r4.rerank_scores(cand[b, h], packed[b, h], w[b, h], qb[b, h], qn[b, h, 0])
+            assert np.array_equal(got[b, h], bf16_bits(want)), (b, h)
+    assert (got[0, 0, :3] == 0xFF80).all()                                   # -inf
+    v = _bits(v4b)
+    ok = (cand >= 0) & (cand < L)
+    dec = r4.decode_packed(packed)                                           # [bs, kv, 16, L, 8]
+    for b in range(bs):
+        for h in range(kv):
+            c = np.where(ok[b, h], cand[b, h], 0)
+            want = np.where(ok[b, h][None, :, None], dec[b, h][:, c], 0.0)
+            assert np.array_equal(v[b, h], bf16_bits(want.astype(np.float32)))
+
+
+@pytest.mark.parametrize("C,k", [(300, 37), (20, 20), (12, 100)])
+def test_rerank_topk_matches_oracle(rng, C, k):
+    """The top-min(k, C) key indices equal the oracle's set (ties to the
+    earlier candidate position), in increasing candidate position."""
+    zk = _zk()
+    bs, kv, L = 1, 4, 500
+    packed, w, pt, wt = _random_cache(rng, bs, kv, L)
+    # few distinct weights -> tied scores
+    w = bf16r(np.round(w * 2) / 2 + 0.5)
+    wt = _bf16(w)
+    qb = bf16r(np.round(rng.standard_normal((bs, kv, 16, 8)) * 2).astype(np.float32) / 2)
+    qn = bf16r(np.full((bs, kv, 1), 2.0, np.float32))
+    cand = np.stack([rng.permutation(L)[:C] for _ in range(bs * kv)]).reshape(bs, kv, C).astype(np.int64)
+    _, ctr = _levels(zk)
+    out, sc = zk.rabitq_rerank_topk(torch.from_numpy(cand).cuda(), pt, wt, _bf16(qb), _bf16(qn), ctr, k,
+                                    return_scores=True)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    assert got.shape == (bs, kv, min(k, C))
+    for h in range(kv):
+        s = r4.rerank_scores(cand[0, h], packed[0, h], w[0, h], qb[0, h], qn[0, h, 0])
+        assert np.array_equal(_bits(sc)[0, h], bf16_bits(s))
+        assert np.array_equal(got[0, h], r4.topk_gather(s, cand[0, h], min(k, C))), h
+
+
+def test_full_size_rerank_sample_and_topk(rng):
+    """The bench workload (8 heads x 131072 keys, 13108 candidates, top-100):
+    encode 131072 keys per head, score all candidates, and compare 512
+    sampled candidates per head and the top-100 set with the oracle (scores
+    of every candidate taken from the GPU for the set check)."""
+    zk = _zk()
+    bs, kv, L, C, k = 1, 8, 131072, 13108, 100
+    sg = np.where(rng.integers(0, 2, 128) == 1, 1.0, -1.0).astype(np.float32)
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    keys = torch.randn(bs, kv, L, 128, device="cuda", generator=gen).to(torch.bfloat16)
+    thr, ctr = _levels(zk)
+    code, w, packed = zk.batch_encode(keys, _bf16(sg), thr, ctr)
+    q = torch.randn(bs, kv, 128, device="cuda", generator=gen).to(torch.bfloat16)
+    qb, qn = zk.encode_query_blocks(q, _bf16(sg))
+    cand = torch.stack([torch.randperm(L, device="cuda", generator=gen)[:C] for _ in range(kv)]).view(bs, kv, C)
+    out, sc = zk.rabitq_rerank_topk(cand, packed, w, qb, qn, ctr, k, return_scores=True)
+    torch.cuda.synchronize()
+    cand_np, sc_bits, out_np = cand.cpu().numpy(), _bits(sc), out.cpu().numpy()
+    keys_np = bf16_to_f32(_bits(keys))
+    p_np, w_np = packed.cpu().numpy(), bf16_to_f32(_bits(w))
+    for h in (0, 5):
+        sel = rng.choice(L, 512, replace=False)
+        oc, op, ow = r4.encode_keys(keys_np[0, h, sel], sg)
+        assert np.array_equal(op, p_np[0, h][:, sel]) and np.array_equal(bf16_bits(ow), bf16_bits(w_np[0, h][:, sel]))
+    qb_np, qn_np = bf16_to_f32(_bits(qb)), bf16_to_f32(_bits(qn))
+    for h in range(kv):
+        pos = rng.choice(C, 512, replace=False)
+        want = r4.rerank_scores(cand_np[0, h, pos], p_np[0, h], w_np[0, h], qb_np[0, h], qn_np[0, h, 0])
+        assert np.array_equal(sc_bits[0, h, pos], bf16_bits(want)), h
+        assert np.array_equal(out_np[0, h], r4.topk_gather(bf16_to_f32(sc_bits[0, h]), cand_np[0, h], k)), h
+
+
+def test_quantizer_loads_sign_codebook(tmp_path):
+    """The codebook JSON format of PC:95-126: config check (ValueError on a
+    mismatch or a malformed file), +-1 signs as bf16 [K_omega, m]."""
+    zk = _zk()
+    import json
+    pats = [[1 if (i >> j) & 1 else -1 for j in range(8)] for i in range(256)]
+    p = tmp_path / "cb.json"
+    p.write_text(json.dumps({"config": {"d": 128, "m": 8, "K_r": 1, "K_omega": 256, "seed": 42},
+                             "angular_signs": pats}))
+    qz = zk.MultiDimBlockQuantizer(128, 8, 1, 256, str(p))
+    assert qz.B == 16 and qz.V_omega_gpu.dtype == torch.bfloat16 and qz.V_omega_gpu.shape == (256, 8)
+    assert torch.equal(qz.V_omega_gpu.float().cpu(), torch.tensor(pats, dtype=torch.float32))
+    s = qz.srht_diagonal_signs[0]
+    assert s.dtype == torch.bfloat16 and s.shape == (128,) and set(s.float().cpu().tolist()) <= {-1.0, 1.0}
+    with pytest.raises(ValueError):
+        zk.MultiDimBlockQuantizer(128, 8, 1, 128, str(p))
+    bad = tmp_path / "bad.json"
+    bad.write_text("{\"config\": {}}")
+    with pytest.raises(ValueError):
+        zk.MultiDimBlockQuantizer(128, 8, 1, 256, str(bad))
+    with pytest.raises(FileNotFoundError):
+        zk.MultiDimBlockQuantizer(128, 8, 1, 256, str(tmp_path / "missing.json"))

@@ -64,6 +64,11 @@ SIGNATURES = {
     "zkv_rabitq_estimate": (I32, [P, P, P, P, I32, I32, I64, P, P]),
     "zkv_rabitq_search_workspace_size": (SZ, [I32, I32, I64, I32]),
     "zkv_rabitq_search": (I32, [P, P, I64, I64, P, P, P, I32, I32, I64, I32, P, P, P, P, SZ, P]),
+    "zkv_rabitq4_encode": (I32, [P, I64, I64, I64, I32, I32, I32, P, P, P, P, I64, I64, I64, P, I64, I64, I64,
+                                 P, I64, I64, I64, I32, P]),
+    "zkv_rabitq4_encode_query": (I32, [P, I64, I32, P, P, P, P]),
+    "zkv_rabitq4_rerank": (I32, [P, I64, I64, I32, I32, I32, P, I64, I64, I64, I64, I32, P, I64, I64, I64,
+                                 P, P, P, P, P, P, P]),
     "zkv_h2d_gather_kv": (I32, [P, P, I32, I32, I32, P, I32, P, P, I32, P]),
     "zkv_h2d_gather_kv_packed": (I32, [P, P, I32, I32, I32, P, P, I64, P, I64, P, P, I32, I32, P]),
     "zkv_copy_rows": (I32, [P, SZ, P, SZ, SZ, SZ, P]),
