@@ -588,8 +588,17 @@ def run_r4(args):
     w_o = torch.empty(bs, kv, 16, L, dtype=torch.bfloat16, device=dev)
     p_o = torch.empty(bs, kv, 16, L, 4, dtype=torch.uint8, device=dev)
     enc_ms = kernel_batch_ms(lambda i: rabitq4.encode_into(keys, signs, thr, ctr, code_o, w_o, p_o, 0), 5)
-    per_cand = 8 + 16 * 4 + 16 * 2 + 4          # index, 16 code words, 16 weights, fp32 score
-    algo = C * kv * per_cand + kv * (256 + 2)
+    # Algorithmic bytes of one rerank call: every 64-byte sector of codes
+    # (16 tokens x 4 B per block) and of weights (32 tokens x 2 B per block)
+    # that holds a candidate -- the least any reader of the [16, seq] layout
+    # moves -- plus the candidate indices in and the fp32 scores out.  The
+    # figure is averaged over the rotated caches' candidate sets.
+    sectors = 0
+    for _, _, cand in caches:
+        for h in range(kv):
+            t = cand[0, h]
+            sectors += 16 * (torch.unique(t // 16).numel() + torch.unique(t // 32).numel())
+    algo = 64 * sectors // n_caches + C * kv * (8 + 4) + kv * (256 + 2)
     achieved = algo / (k_ms * 1e-3) / 1e9
     enc_bytes = bs * kv * L * (256 + 16 * 7)      # bf16 key in; sign byte, code word, weight out per block
     cpu = None if args.no_cpu else r4_cpu_baseline(caches[0], q, signs, k)
@@ -605,7 +614,8 @@ def run_r4(args):
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": read_traffic("r4_rabitq4_rerank_traffic.json"),
-                     "kernel": "rabitq4_rerank_kernel", "kernel_ms": k_ms, "algorithmic_bytes": algo},
+                     "kernel": "rabitq4 rerank call (mark + stream + collect kernels)", "kernel_ms": k_ms,
+                     "algorithmic_bytes": algo},
         "key_encode": {"keys_per_s": bs * kv * L / (enc_ms * 1e-3), "kernel_ms": enc_ms,
                        "GBps": enc_bytes / (enc_ms * 1e-3) / 1e9, "keys": bs * kv * L},
         "cpu_baseline": cpu,

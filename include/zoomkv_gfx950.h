@@ -386,13 +386,29 @@ int zkv_rabitq4_encode_query(const uint16_t* q, int64_t q_sr, int rows, const ui
  * not both scores): scores bf16 [bs, kv, C], scores_f32 (the same values),
  * v4b bf16 [bs, kv, 16, C, 8] (the decoded values).  A candidate outside
  * [0, kv_len) scores -inf.
+ * workspace (optional, device, 16-byte aligned, at least
+ * zkv_rabitq4_rerank_workspace_size(bs, kv, kv_len) bytes) enables the
+ * streamed path for dense candidate lists (C >= kv_len / 16; scores only,
+ * no v4b): its first F = ceil(bs * kv * ceil(kv_len / 1024) * 1024 / 256) * 256
+ * bytes are token flags that must be all zero when the call starts and that
+ * a successful call leaves all zero (a zero-filled buffer qualifies, and
+ * stays qualified for calls of the same bs, kv and kv_len; zero its first F
+ * bytes again before a call of another shape).  Calls that overlap on one
+ * workspace race.  With a null workspace every call takes the direct path;
+ * both give the same scores.
  * Replaces partial_rerank_cuda / partial_rerank_scores_cuda
  * (Z/cache_hub/rerank/rerank.py:352-440; kernel rerank.cu:52-143). */
 int zkv_rabitq4_rerank(const int64_t* cand, int64_t cd_sb, int64_t cd_sh, int bs, int kv, int C,
                        const uint8_t* packed, int64_t p_sb, int64_t p_sh, int64_t p_sB, int64_t p_st,
                        int kv_len, const uint16_t* weight, int64_t w_sb, int64_t w_sh, int64_t w_sB,
                        const uint16_t* q_blocks, const uint16_t* q_norm, const uint16_t* mag_centers,
-                       uint16_t* scores, float* scores_f32, uint16_t* v4b, zkv_stream_t stream);
+                       uint16_t* scores, float* scores_f32, uint16_t* v4b, void* workspace,
+                       size_t workspace_bytes, zkv_stream_t stream);
+
+/* Bytes of the rerank's streamed-path workspace: the token flags (above),
+ * then one fp32 score per token.  0 for an invalid shape.
+ * No reference counterpart (the reference's rerank has no workspace). */
+size_t zkv_rabitq4_rerank_workspace_size(int bs, int kv, int kv_len);
 
 /* ---------------------------------------------------------------------------
  * Host-to-device row gather (the UVA gather of

@@ -237,3 +237,31 @@ def test_quantizer_loads_sign_codebook(tmp_path):
         zk.MultiDimBlockQuantizer(128, 8, 1, 256, str(bad))
     with pytest.raises(FileNotFoundError):
         zk.MultiDimBlockQuantizer(128, 8, 1, 256, str(tmp_path / "missing.json"))
+
+
+def test_streamed_rerank_across_shapes_and_repeats(rng):
+    """Dense candidate lists take the streamed path (token flags + per-token
+    scores in a reused workspace): scores equal the direct path's (the v4b
+    call) and the oracle's through calls of changing shapes, repeated
+    candidates and out-of-range entries, and the flags are all zero after
+    each call."""
+    zk = _zk()
+    _, ctr = _levels(zk)
+    for bs, kv, L, C in [(1, 2, 700, 300), (2, 1, 2100, 900), (1, 2, 700, 300), (1, 3, 33, 40), (1, 1, 4096, 4096)]:
+        packed, w, pt, wt = _random_cache(rng, bs, kv, L)
+        qb = bf16r(rng.standard_normal((bs, kv, 16, 8)).astype(np.float32))
+        qn = bf16r(np.abs(rng.standard_normal((bs, kv, 1))).astype(np.float32) + 0.1)
+        cand = rng.integers(-2, L + 2, (bs, kv, C)).astype(np.int64)
+        cand[..., : C // 4] = cand[..., C // 4: 2 * (C // 4)]                  # repeats
+        ct = torch.from_numpy(cand).cuda()
+        streamed = zk.partial_rerank_scores_cuda(ct, pt, wt, _bf16(qb), _bf16(qn), ctr, 16, 8)
+        direct, _ = zk.partial_rerank_cuda(ct, pt, wt, _bf16(qb), _bf16(qn), ctr, 16, 8)
+        torch.cuda.synchronize()
+        assert np.array_equal(_bits(streamed), _bits(direct)), (bs, kv, L, C)
+        for b in range(bs):
+            for h in range(kv):
+                want = r4.rerank_scores(cand[b, h], packed[b, h], w[b, h], qb[b, h], qn[b, h, 0])
+                assert np.array_equal(_bits(streamed)[b, h], bf16_bits(want)), (bs, kv, L, C, b, h)
+        ws, shape = zk._WS[torch.device("cuda", torch.cuda.current_device())]
+        assert shape == (bs, kv, L)
+        assert int(ws[:zk._flag_bytes(bs, kv, L)].count_nonzero()) == 0

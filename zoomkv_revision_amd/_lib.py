@@ -68,7 +68,8 @@ SIGNATURES = {
                                  P, I64, I64, I64, I32, P]),
     "zkv_rabitq4_encode_query": (I32, [P, I64, I32, P, P, P, P]),
     "zkv_rabitq4_rerank": (I32, [P, I64, I64, I32, I32, I32, P, I64, I64, I64, I64, I32, P, I64, I64, I64,
-                                 P, P, P, P, P, P, P]),
+                                 P, P, P, P, P, P, P, SZ, P]),
+    "zkv_rabitq4_rerank_workspace_size": (SZ, [I32, I32, I32]),
     "zkv_h2d_gather_kv": (I32, [P, P, I32, I32, I32, P, I32, P, P, I32, P]),
     "zkv_h2d_gather_kv_packed": (I32, [P, P, I32, I32, I32, P, P, I64, P, I64, P, P, I32, I32, P]),
     "zkv_copy_rows": (I32, [P, SZ, P, SZ, SZ, SZ, P]),

@@ -193,24 +193,43 @@ struct RerankParams {
 
 constexpr int kRerankThreads = 256;
 
-// One thread per candidate.  The bf16 products bf16(+-center[t] * q[b][j])
-// of every (block, dimension, 4-bit value) are computed once per workgroup
-// into LDS (16 consecutive fp32 entries per (block, dimension): any 4-bit
-// values of a wave read 16 distinct banks, conflict-free); each candidate's
-// 16 code words and 16 weights are requested before the first is used.
-// A candidate index outside [0, kv_len) scores -inf and loads nothing.
+// The bf16 products bf16(+-center[t] * q[b][j]) of every (block b, dimension
+// j, 4-bit value v) into LDS at (8 b + j) * 16 + v: 16 consecutive fp32
+// entries per (block, dimension), so any 4-bit values of a wave read 16
+// distinct banks (conflict-free).
+__device__ __forceinline__ void build_products(float* prod, const uint16_t* qb, const uint16_t* centers) {
+  for (int e = threadIdx.x; e < kBlk * 8 * 16; e += blockDim.x) {
+    const int v = e & 15, bj = e >> 4;  // bj = 8 * block + j
+    const float c = bf16_to_f32(centers[v & 7]);
+    prod[e] = bf16r((v & 8 ? c : -c) * bf16_to_f32(qb[bj]));
+  }
+}
+
+// The score of one candidate from its 16 code words and 16 bf16 weights
+// (all requested before the first is used): per block the sequential bf16
+// sum of the 8 products, times the weight (bf16), added in block order
+// (bf16), times ||q|| (bf16).
+__device__ __forceinline__ float score_one(const float* prod, const uint32_t code[kBlk], const uint16_t wb[kBlk],
+                                           float qn) {
+  float res = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kBlk; ++i) {
+    float dot = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) dot = bf16r(dot + prod[(8 * i + j) * 16 + ((code[i] >> (4 * j)) & 15u)]);
+    res = bf16r(res + bf16r(dot * bf16_to_f32(wb[i])));
+  }
+  return bf16r(res * qn);
+}
+
+// Direct path: one thread per candidate, its 16 code words and 16 weights
+// gathered from wherever they lie.  A candidate index outside [0, kv_len)
+// scores -inf and loads nothing.
 __global__ __launch_bounds__(kRerankThreads) void rabitq4_rerank_kernel(const RerankParams p) {
   __shared__ float prod[kBlk * 8 * 16];
   const int h = blockIdx.y, b = blockIdx.z;
   const int64_t bh = static_cast<int64_t>(b) * p.kv + h;
-  {
-    const uint16_t* qb = p.q_blocks + bh * kDim;
-    for (int e = threadIdx.x; e < kBlk * 8 * 16; e += kRerankThreads) {
-      const int v = e & 15, bj = e >> 4;  // bj = 8 * block + j
-      const float c = bf16_to_f32(p.centers[v & 7]);
-      prod[e] = bf16r((v & 8 ? c : -c) * bf16_to_f32(qb[bj]));
-    }
-  }
+  build_products(prod, p.q_blocks + bh * kDim, p.centers);
   __syncthreads();
   const int ci = blockIdx.x * kRerankThreads + threadIdx.x;
   if (ci >= p.C) return;
@@ -228,15 +247,7 @@ __global__ __launch_bounds__(kRerankThreads) void rabitq4_rerank_kernel(const Re
       code[i] = pk[i * p.p_sB];
       wb[i] = wt[i * p.w_sB];
     }
-    res = 0.0f;
-#pragma unroll
-    for (int i = 0; i < kBlk; ++i) {
-      float dot = 0.0f;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) dot = bf16r(dot + prod[(8 * i + j) * 16 + ((code[i] >> (4 * j)) & 15u)]);
-      res = bf16r(res + bf16r(dot * bf16_to_f32(wb[i])));
-    }
-    res = bf16r(res * bf16_to_f32(p.q_norm[bh]));
+    res = score_one(prod, code, wb, bf16_to_f32(p.q_norm[bh]));
     if (p.v4b) {
       for (int i = 0; i < kBlk; ++i) {
         u32x4_t o;
@@ -261,6 +272,115 @@ __global__ __launch_bounds__(kRerankThreads) void rabitq4_rerank_kernel(const Re
   if (p.scores) p.scores[out] = f32_to_bf16_bits(res);
   if (p.scores_f32) p.scores_f32[out] = res;
 }
+
+// ---- streamed path ----------------------------------------------------------
+// In the reference's [16, seq] layout the 16 code words of a token lie 4*seq
+// bytes apart, so a gather touches 32 lines per candidate; with the
+// candidates a few percent of the tokens or more, nearly every line is read
+// anyway.  The streamed path reads the layout in token order instead:
+//   mark    : a flag byte per candidate token (plain stores; repeats store
+//             the same 1);
+//   stream  : each workgroup owns kStreamTokens tokens, reads their flags
+//             (4 per thread), compacts the flagged tokens in LDS, clears the
+//             flags it read (so the workspace is zero again for the next
+//             call), scores the flagged tokens and writes one fp32 score per
+//             flagged token;
+//   collect : every candidate (repeats included) takes its token's score.
+// The scores are the direct path's, bit for bit.
+constexpr int kStreamThreads = 256;
+constexpr int kStreamTokens = 4 * kStreamThreads;
+
+// Flag bytes per (batch, head) row: kv_len rounded up to whole windows, so
+// every window reads whole, in-bounds flag words (those past kv_len stay 0).
+int64_t flag_row(int kv_len) {
+  return (static_cast<int64_t>(kv_len) + kStreamTokens - 1) / kStreamTokens * kStreamTokens;
+}
+
+__global__ __launch_bounds__(256) void rabitq4_mark_kernel(const RerankParams p, uint8_t* __restrict__ flags,
+                                                           int64_t frow) {
+  const int ci = blockIdx.x * 256 + threadIdx.x;
+  if (ci >= p.C) return;
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int64_t idx = p.cand[b * p.cd_sb + h * p.cd_sh + ci];
+  if (idx < 0 || idx >= p.kv_len) return;
+  flags[(static_cast<int64_t>(b) * p.kv + h) * frow + idx] = 1;
+}
+
+__global__ __launch_bounds__(kStreamThreads) void rabitq4_stream_kernel(const RerankParams p,
+                                                                        uint8_t* __restrict__ flags, int64_t frow,
+                                                                        float* __restrict__ tok_score) {
+  __shared__ float prod[kBlk * 8 * 16];
+  __shared__ int list[kStreamTokens];
+  __shared__ int wave_total[kStreamThreads / 64];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int64_t bh = static_cast<int64_t>(b) * p.kv + h;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kStreamTokens;
+  // flags of tokens t0 + 4 tid .. t0 + 4 tid + 3 (bytes of 0 or 1), read first
+  uint32_t* fw = reinterpret_cast<uint32_t*>(flags + bh * frow + t0) + tid;
+  const uint32_t f = *fw;
+  build_products(prod, p.q_blocks + bh * kDim, p.centers);
+  const int cnt = __popc(f);
+  int inc = cnt;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {  // inclusive scan over the wave
+    const int o = __shfl_up(inc, d, 64);
+    if (lane >= d) inc += o;
+  }
+  if (lane == 63) wave_total[wave] = inc;
+  if (f) *fw = 0u;
+  __syncthreads();
+  int off = inc - cnt, n = 0;
+#pragma unroll
+  for (int w = 0; w < kStreamThreads / 64; ++w) {
+    off += w < wave ? wave_total[w] : 0;
+    n += wave_total[w];
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    if ((f >> (8 * j)) & 1u) list[off++] = 4 * tid + j;
+  __syncthreads();
+  const float qn = bf16_to_f32(p.q_norm[bh]);
+  for (int i = tid; i < n; i += kStreamThreads) {
+    const int64_t t = t0 + list[i];
+    const uint32_t* pk = p.packed + b * p.p_sb + h * p.p_sh + t * p.p_st;
+    const uint16_t* wt = p.weight + b * p.w_sb + h * p.w_sh + t;
+    uint32_t code[kBlk];
+    uint16_t wb[kBlk];
+#pragma unroll
+    for (int k = 0; k < kBlk; ++k) {
+      code[k] = pk[k * p.p_sB];
+      wb[k] = wt[k * p.w_sB];
+    }
+    tok_score[bh * p.kv_len + t] = score_one(prod, code, wb, qn);
+  }
+}
+
+__global__ __launch_bounds__(256) void rabitq4_collect_kernel(const RerankParams p,
+                                                              const float* __restrict__ tok_score) {
+  const int ci = blockIdx.x * 256 + threadIdx.x;
+  if (ci >= p.C) return;
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int64_t bh = static_cast<int64_t>(b) * p.kv + h;
+  const int64_t idx = p.cand[b * p.cd_sb + h * p.cd_sh + ci];
+  const float s = (idx >= 0 && idx < p.kv_len) ? tok_score[bh * p.kv_len + idx] : -INFINITY;
+  const int64_t out = bh * p.C + ci;
+  if (p.scores) p.scores[out] = f32_to_bf16_bits(s);
+  if (p.scores_f32) p.scores_f32[out] = s;
+}
+
+int64_t stream_flag_bytes(int bs, int kv, int kv_len) {
+  return (static_cast<int64_t>(bs) * kv * flag_row(kv_len) + 255) / 256 * 256;
+}
+
+size_t stream_workspace_bytes(int bs, int kv, int kv_len) {
+  return static_cast<size_t>(stream_flag_bytes(bs, kv, kv_len) + static_cast<int64_t>(bs) * kv * kv_len * 4);
+}
+
+// The streamed path pays for reading every line of the codes; it wins once
+// the candidates are dense enough that the direct gathers touch them all
+// (C >= kv_len / 16).
+bool use_stream(int C, int kv_len) { return static_cast<int64_t>(C) * 16 >= kv_len; }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
@@ -328,11 +448,17 @@ extern "C" int zkv_rabitq4_encode_query(const uint16_t* q, int64_t q_sr, int row
   return check_launch("rabitq4_query_kernel");
 }
 
+extern "C" size_t zkv_rabitq4_rerank_workspace_size(int bs, int kv, int kv_len) {
+  if (bs <= 0 || kv <= 0 || kv_len < 0) return 0;
+  return stream_workspace_bytes(bs, kv, kv_len);
+}
+
 extern "C" int zkv_rabitq4_rerank(const int64_t* cand, int64_t cd_sb, int64_t cd_sh, int bs, int kv, int C,
                                   const uint8_t* packed, int64_t p_sb, int64_t p_sh, int64_t p_sB, int64_t p_st,
                                   int kv_len, const uint16_t* weight, int64_t w_sb, int64_t w_sh, int64_t w_sB,
                                   const uint16_t* q_blocks, const uint16_t* q_norm, const uint16_t* mag_centers,
-                                  uint16_t* scores, float* scores_f32, uint16_t* v4b, zkv_stream_t stream) {
+                                  uint16_t* scores, float* scores_f32, uint16_t* v4b, void* workspace,
+                                  size_t workspace_bytes, zkv_stream_t stream) {
   ZKV_REQUIRE(cand && packed && weight && q_blocks && q_norm && mag_centers,
               "zkv_rabitq4_rerank: null pointer");
   ZKV_REQUIRE(scores || scores_f32, "zkv_rabitq4_rerank: no output");
@@ -365,6 +491,23 @@ extern "C" int zkv_rabitq4_rerank(const int64_t* cand, int64_t cd_sb, int64_t cd
   p.v4b = v4b;
   const dim3 grid((C + kRerankThreads - 1) / kRerankThreads, kv, bs);
   ZKV_REQUIRE(kv < 65536 && bs < 65536, "zkv_rabitq4_rerank: grid too large");
-  rabitq4_rerank_kernel<<<grid, kRerankThreads, 0, reinterpret_cast<hipStream_t>(stream)>>>(p);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (workspace && !v4b && kv_len > 0 && use_stream(C, kv_len)) {
+    const size_t need = stream_workspace_bytes(bs, kv, kv_len);
+    ZKV_REQUIRE(workspace_bytes >= need && aligned16(workspace),
+                "zkv_rabitq4_rerank: workspace of %zu bytes (16-byte aligned) needed, got %zu", need,
+                workspace_bytes);
+    const int64_t frow = flag_row(kv_len);
+    uint8_t* flags = static_cast<uint8_t*>(workspace);
+    float* tok = reinterpret_cast<float*>(flags + stream_flag_bytes(bs, kv, kv_len));
+    rabitq4_mark_kernel<<<grid, 256, 0, s>>>(p, flags, frow);
+    if (int rc = check_launch("rabitq4_mark_kernel")) return rc;
+    const dim3 sgrid(static_cast<unsigned>(frow / kStreamTokens), kv, bs);
+    rabitq4_stream_kernel<<<sgrid, kStreamThreads, 0, s>>>(p, flags, frow, tok);
+    if (int rc = check_launch("rabitq4_stream_kernel")) return rc;
+    rabitq4_collect_kernel<<<grid, 256, 0, s>>>(p, tok);
+    return check_launch("rabitq4_collect_kernel");
+  }
+  rabitq4_rerank_kernel<<<grid, kRerankThreads, 0, s>>>(p);
   return check_launch("rabitq4_rerank_kernel");
 }

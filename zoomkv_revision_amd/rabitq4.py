@@ -199,6 +199,31 @@ def _validate(coarse_indices, key_4bit, key_block_weight, q_blocks, q_norm, mag_
     return bs, kv_heads, kv_len
 
 
+# Per-device streamed-path workspace: [tensor, (bs, kv, kv_len) of the last
+# call or None].  Its token flags are zero between calls of one shape (each
+# call leaves them zero); they are zeroed again when the shape changes.
+_WS: dict = {}
+
+
+def _flag_bytes(bs: int, kv: int, kv_len: int) -> int:
+    """The flag prefix of the workspace (one byte per token, rows rounded up
+    to 1024 tokens, the whole to 256 bytes)."""
+    return (bs * kv * ((kv_len + 1023) // 1024) * 1024 + 255) // 256 * 256
+
+
+def _rerank_workspace(device, bs: int, kv: int, kv_len: int):
+    need = lib().zkv_rabitq4_rerank_workspace_size(bs, kv, kv_len)
+    key = torch.device(device)
+    ent = _WS.get(key)
+    if ent is None or ent[0].numel() < need:
+        ent = [torch.zeros(max(need, 1 << 16), dtype=torch.uint8, device=key), (bs, kv, kv_len)]
+        _WS[key] = ent
+    elif ent[1] != (bs, kv, kv_len):
+        ent[0][:_flag_bytes(bs, kv, kv_len)].zero_()
+        ent[1] = (bs, kv, kv_len)
+    return ent
+
+
 def _rerank(coarse_indices, key_4bit, key_block_weight, q_blocks, q_norm, mag_centers, B, m,
             scores=None, scores_f32=None, v4b=None):
     if q_norm.dtype != torch.bfloat16:
@@ -206,11 +231,18 @@ def _rerank(coarse_indices, key_4bit, key_block_weight, q_blocks, q_norm, mag_ce
     bs, kv, kv_len = _validate(coarse_indices, key_4bit, key_block_weight, q_blocks, q_norm, mag_centers, B, m)
     C = coarse_indices.shape[-1]
     ks, ws = key_4bit.stride(), key_block_weight.stride()
-    check(lib().zkv_rabitq4_rerank(
-        ptr(coarse_indices), coarse_indices.stride(0), coarse_indices.stride(1), bs, kv, C,
-        ptr(key_4bit), ks[0] // 4, ks[1] // 4, ks[2] // 4, ks[3] // 4, kv_len,
-        ptr(key_block_weight), ws[0], ws[1], ws[2], ptr(q_blocks), ptr(q_norm), ptr(mag_centers),
-        ptr(scores), ptr(scores_f32), ptr(v4b), stream_of(key_4bit)))
+    ent = _rerank_workspace(key_4bit.device, bs, kv, kv_len) if v4b is None and kv_len > 0 and C > 0 else None
+    try:
+        check(lib().zkv_rabitq4_rerank(
+            ptr(coarse_indices), coarse_indices.stride(0), coarse_indices.stride(1), bs, kv, C,
+            ptr(key_4bit), ks[0] // 4, ks[1] // 4, ks[2] // 4, ks[3] // 4, kv_len,
+            ptr(key_block_weight), ws[0], ws[1], ws[2], ptr(q_blocks), ptr(q_norm), ptr(mag_centers),
+            ptr(scores), ptr(scores_f32), ptr(v4b), None if ent is None else ptr(ent[0]),
+            0 if ent is None else ent[0].numel(), stream_of(key_4bit)))
+    except Exception:
+        if ent is not None:
+            ent[1] = None  # a failed call may leave bits set: zero before the next
+        raise
 
 
 def partial_rerank_cuda(coarse_indices, key_4bit, key_block_weight, q_blocks, q_norm, mag_centers, B, m,
