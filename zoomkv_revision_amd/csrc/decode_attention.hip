@@ -81,7 +81,9 @@ struct AttnParams {
   const int64_t* res_idx;
   int64_t ri_sb, ri_sh;
   int n_idx, tail_start, row_limit;
-  int kv, gqa, n_groups, res_len, n_splits, tiles_per_split;
+  int kv, gqa, n_groups, res_len, n_splits;
+  int tiles_per_split;  // tiles of an even-numbered split
+  int tiles_odd_split;  // tiles of an odd-numbered split
   float qscale;    // raw MFMA score * qscale = base-2 scaled score
   float* ws_o;     // [bs, kv, n_splits, gqa, 128]
   float* ws_ml;    // [bs, kv, n_splits, gqa, 2]
@@ -624,7 +626,7 @@ void kivi4_attn_kernel(const AttnParams p) {
   const bool col_ok = c < p.gqa;
   const int64_t bh = static_cast<int64_t>(b) * p.kv + h;
 
-  const int T0 = split * p.tiles_per_split;
+  const int T0 = (split >> 1) * (p.tiles_per_split + p.tiles_odd_split) + (split & 1) * p.tiles_per_split;
   uint8_t (*ring)[kStage] = reinterpret_cast<uint8_t (*)[kStage]>(smem + wave * D * kStage);
   int n_qt = p.n_groups;  // quantized tiles of (b, kv)
   if constexpr (kSparse) {
@@ -656,7 +658,7 @@ void kivi4_attn_kernel(const AttnParams p) {
     n_qt = base;
   }
   const int n_tiles = n_qt + (p.res_len + kTile - 1) / kTile;
-  const int T1 = min(T0 + p.tiles_per_split, n_tiles);
+  const int T1 = min(T0 + ((split & 1) ? p.tiles_odd_split : p.tiles_per_split), n_tiles);
   const int TQ = min(T1, n_qt);  // quantized tiles of this workgroup: [T0, TQ)
   // this wave's quantized tiles: T0 + wave + NW*k, k < nq (nq <= 64 in sparse mode)
   const int nq = TQ > T0 + wave ? (TQ - (T0 + wave) + NW - 1) / NW : 0;
@@ -1042,12 +1044,15 @@ __global__ __launch_bounds__(256) void lse_merge_kernel(const void* __restrict__
 
 struct SplitPlan {
   int n_splits, tiles_per_split;
+  int tiles_odd_split;  // tiles of the odd-numbered splits (see xcd_skew)
 };
 
 // Page-sparse shape: a wave holds only a few tiles (C3: ~4), so its loop is a
 // chain of DMA round trips; a 4-stage ring issues them together (8 x 4 x 5 KiB
 // = the 160 KiB of LDS: one workgroup per CU, 2 waves per SIMD).
 constexpr int kSparseNW = 8, kSparseD = 4;
+
+constexpr float kXcdSkew = 0.03f;
 
 // Kernel shape: NW waves per workgroup, D ring stages per wave.
 // ZKV_ATTN_SHAPE=NWxD (e.g. 4x3) overrides the dense default for tuning sweeps.
@@ -1067,6 +1072,17 @@ Shape attn_shape() {
   return sh;
 }
 
+// Share of an odd split's tiles moved to its even partner (0 = equal
+// splits).  ZKV_XCD_SKEW overrides it for tuning sweeps.
+float xcd_skew() {
+  static float v = [] {
+    float x = kXcdSkew;
+    if (const char* e = getenv("ZKV_XCD_SKEW")) x = std::max(0.0f, std::min(0.2f, static_cast<float>(atof(e))));
+    return x;
+  }();
+  return v;
+}
+
 // Resident workgroups per CU: LDS (160 KiB per CU) and waves (4 SIMDs, at most
 // `waves_per_simd` waves each at the kernel's register budget).
 int wgs_per_cu(Shape sh, int stage_bytes, int waves_per_simd) {
@@ -1076,7 +1092,7 @@ int wgs_per_cu(Shape sh, int stage_bytes, int waves_per_simd) {
 
 // Defaults: the dense kernels (metadata-only LDS stages).
 SplitPlan plan_splits(int bs, int kv, int n_groups, int res_len, int n_splits, Shape sh = attn_shape(),
-                      int stage_bytes = kMetaBytes, int waves_per_simd = 0) {
+                      int stage_bytes = kMetaBytes, int waves_per_simd = 0, bool xcd_aware = true) {
   if (waves_per_simd <= 0) waves_per_simd = dense_waves_per_simd(sh.nw);
   const int n_tiles = std::max(n_groups + (res_len + kTile - 1) / kTile, 1);
   int ns = n_splits;
@@ -1105,7 +1121,19 @@ SplitPlan plan_splits(int bs, int kv, int n_groups, int res_len, int n_splits, S
   int per = static_cast<int>(std::min<int64_t>((work + ns - 1) / ns, n_tiles));
   if ((n_tiles + per - 1) / per < ns) per = (n_tiles + ns - 1) / ns;  // keep the split count
   ns = (n_tiles + per - 1) / per;
-  return {ns, per};
+  // With an even split count the grid (splits, kv, bs) puts every even split
+  // on an even XCD (workgroups go to the 8 XCDs round-robin by linear id) and
+  // every odd split on an odd one.  The odd XCDs stream more slowly (their
+  // workgroups finish ~4% later at C2), so each (even, odd) pair of splits
+  // moves a share of its tiles to the even split.
+  int odd = per;
+  const float skew = xcd_skew();
+  if (xcd_aware && ns % 2 == 0 && n_groups > 0 && skew > 0.0f) {
+    const int even = std::min(2 * per - 1, static_cast<int>(per * (1.0f + skew) + 0.5f));
+    odd = 2 * per - even;
+    per = even;
+  }
+  return {ns, per, odd};
 }
 
 // Workspace layout: split partials o fp32 [bs, kv, S, gqa, 128] followed by
@@ -1159,12 +1187,14 @@ struct SparsePages {
 // Sparse mode: every split is planned for the longest page list (n_sel
 // tiles); each wave keeps at most 64 tile descriptors in its lanes.
 SplitPlan plan_sparse_splits(int bs, int kv, int n_sel, int res_len, int n_splits) {
-  SplitPlan sp = plan_splits(bs, kv, n_sel, res_len, n_splits, Shape{kSparseNW, kSparseD}, kStageBytes, 4);
+  // (equal splits: a page-sparse split is a short latency chain)
+  SplitPlan sp = plan_splits(bs, kv, n_sel, res_len, n_splits, Shape{kSparseNW, kSparseD}, kStageBytes, 4, false);
   constexpr int kMaxPerSplit = 64 * kSparseNW;
   if (sp.tiles_per_split > kMaxPerSplit) {
     const int n_tiles = n_sel + (res_len + kTile - 1) / kTile;
     sp.n_splits = (n_tiles + kMaxPerSplit - 1) / kMaxPerSplit;
     sp.tiles_per_split = (n_tiles + sp.n_splits - 1) / sp.n_splits;
+    sp.tiles_odd_split = sp.tiles_per_split;
   }
   return sp;
 }
@@ -1242,6 +1272,7 @@ int attention_launch(const uint16_t* q, int64_t q_sb, int64_t q_sh, const int32_
   p.res_len = res_len;
   p.n_splits = sp.n_splits;
   p.tiles_per_split = sp.tiles_per_split;
+  p.tiles_odd_split = sp.tiles_odd_split;
   p.qscale = sm_scale * kLog2e * 8.0f;  // q enters the MFMA as q / 8
   p.ws_o = reinterpret_cast<float*>(workspace);
   p.ws_ml = p.ws_o + static_cast<size_t>(bs) * hq * sp.n_splits * 128;
