@@ -638,11 +638,19 @@ void kivi4_attn_kernel(const AttnParams p) {
     const int64_t* pg = p.pages + b * p.pg_sb + h * p.pg_sh;
     const int64_t n_pages = 2ll * p.n_groups;
     int base = 0;
+    // one load per page: each step requests the next 64 pages before the
+    // neighbours come from lane shuffles, so the first two chunks share one
+    // memory round trip
+    int64_t cur = lane < p.n_sel ? pg[lane] : -1;
+    int64_t before = -1;  // page i0 - 1
     for (int i0 = 0; i0 < p.n_sel; i0 += 64) {
       const int i = i0 + lane;
-      const int64_t cur = i < p.n_sel ? pg[i] : -1;
-      const int64_t prev = (i > 0 && i < p.n_sel) ? pg[i - 1] : -1;
-      const int64_t next = (i + 1 < p.n_sel) ? pg[i + 1] : -1;
+      const int64_t ahead = i + 64 < p.n_sel ? pg[i + 64] : -1;
+      int64_t prev = __shfl_up(cur, 1, 64);
+      if (lane == 0) prev = before;
+      int64_t next = __shfl_down(cur, 1, 64);
+      const int64_t ahead0 = __shfl(ahead, 0, 64);
+      if (lane == 63) next = ahead0;
       const bool valid = cur >= 0 && cur < n_pages;
       const bool start = valid && !((cur & 1) && prev == cur - 1);
       const uint64_t m = __ballot(start);
@@ -654,6 +662,8 @@ void kivi4_attn_kernel(const AttnParams p) {
         s_mask[rel / NW] = (cur & 1) ? 2 : (next == cur + 1 ? 3 : 1);
       }
       base += __popcll(m);
+      before = __shfl(cur, 63, 64);
+      cur = ahead;
     }
     n_qt = base;
   }
@@ -1320,6 +1330,8 @@ extern "C" int zkv_attention_merge(const void* workspace, int bs, int hq, int kv
   ZKV_REQUIRE(workspace && out, "zkv_attention_merge: null pointer");
   ZKV_REQUIRE(bs > 0 && kv > 0 && hq > 0 && hq % kv == 0 && n_splits > 0,
               "zkv_attention_merge: bad sizes bs=%d hq=%d kv=%d n_splits=%d", bs, hq, kv, n_splits);
+  ZKV_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 15) == 0,
+              "zkv_attention_merge: workspace must be 16-byte aligned");
   const float* ws_o = reinterpret_cast<const float*>(workspace);
   const float* ws_ml = ws_o + static_cast<size_t>(bs) * hq * n_splits * 128;
   kivi4_combine_kernel<<<bs * hq, 128, 0, reinterpret_cast<hipStream_t>(stream)>>>(
