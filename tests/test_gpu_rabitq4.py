@@ -247,8 +247,12 @@ def test_streamed_rerank_across_shapes_and_repeats(rng):
     each call."""
     zk = _zk()
     _, ctr = _levels(zk)
-    for bs, kv, L, C in [(1, 2, 700, 300), (2, 1, 2100, 900), (1, 2, 700, 300), (1, 3, 33, 40), (1, 1, 4096, 4096)]:
-        packed, w, pt, wt = _random_cache(rng, bs, kv, L)
+    # part-filled last windows, capacity-strided rows (cap 1104), a single
+    # window of 8 tokens
+    for bs, kv, L, C, cap in [(1, 2, 700, 300, None), (2, 1, 2100, 900, None), (1, 2, 700, 300, None),
+                              (1, 3, 33, 40, None), (1, 1, 4096, 4096, None), (2, 2, 1000, 400, None),
+                              (1, 2, 1000, 100, 1104), (2, 1, 8, 40, None), (1, 2, 1536, 200, None)]:
+        packed, w, pt, wt = _random_cache(rng, bs, kv, L, cap=cap)
         qb = bf16r(rng.standard_normal((bs, kv, 16, 8)).astype(np.float32))
         qn = bf16r(np.abs(rng.standard_normal((bs, kv, 1))).astype(np.float32) + 0.1)
         cand = rng.integers(-2, L + 2, (bs, kv, C)).astype(np.int64)
@@ -264,4 +268,30 @@ def test_streamed_rerank_across_shapes_and_repeats(rng):
                 assert np.array_equal(_bits(streamed)[b, h], bf16_bits(want)), (bs, kv, L, C, b, h)
         ws, shape = zk._WS[torch.device("cuda", torch.cuda.current_device())]
         assert shape == (bs, kv, L)
-        assert int(ws[:zk._flag_bytes(bs, kv, L)].count_nonzero()) == 0
+        assert int(ws[:zk._flag_bytes(bs, kv, L)].count_nonzero()) == 0, (bs, kv, L, C)
+
+
+def test_rerank_empty_candidates_and_empty_cache(rng):
+    """C = 0 gives empty outputs; kv_len = 0 scores every candidate -inf,
+    decodes it to zeros and keeps the first k candidate positions."""
+    zk = _zk()
+    _, ctr = _levels(zk)
+    bs, kv = 1, 2
+    qb = _bf16(bf16r(rng.standard_normal((bs, kv, 16, 8)).astype(np.float32)))
+    qn = _bf16(np.full((bs, kv, 1), 1.5, np.float32))
+    packed, w, pt, wt = _random_cache(rng, bs, kv, 64)
+    none = torch.empty(bs, kv, 0, dtype=torch.int64, device="cuda")
+    s, v = zk.partial_rerank_cuda(none, pt, wt, qb, qn, ctr, 16, 8)
+    assert s.shape == (bs, kv, 0) and v.shape == (bs, kv, 16, 0, 8)
+    assert zk.partial_rerank_scores_cuda(none, pt, wt, qb, qn, ctr, 16, 8).shape == (bs, kv, 0)
+    assert zk.rabitq_rerank_topk(none, pt, wt, qb, qn, ctr, 10).shape == (bs, kv, 0)
+    p0 = torch.empty(bs, kv, 16, 0, 4, dtype=torch.uint8, device="cuda")
+    w0 = torch.empty(bs, kv, 16, 0, dtype=torch.bfloat16, device="cuda")
+    cand = torch.tensor([[[3, 0, 7, -1, 2]] * kv], dtype=torch.int64, device="cuda")
+    s, v = zk.partial_rerank_cuda(cand, p0, w0, qb, qn, ctr, 16, 8)
+    only = zk.partial_rerank_scores_cuda(cand, p0, w0, qb, qn, ctr, 16, 8)
+    out = zk.rabitq_rerank_topk(cand, p0, w0, qb, qn, ctr, 3)
+    torch.cuda.synchronize()
+    assert (_bits(s) == 0xFF80).all() and (_bits(only) == 0xFF80).all()
+    assert (_bits(v) == 0).all()
+    assert np.array_equal(out.cpu().numpy(), cand[..., :3].cpu().numpy())

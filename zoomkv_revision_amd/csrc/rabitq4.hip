@@ -369,6 +369,8 @@ __global__ __launch_bounds__(256) void rabitq4_collect_kernel(const RerankParams
   if (p.scores_f32) p.scores_f32[out] = s;
 }
 
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
 int64_t stream_flag_bytes(int bs, int kv, int kv_len) {
   return (static_cast<int64_t>(bs) * kv * flag_row(kv_len) + 255) / 256 * 256;
 }
@@ -382,7 +384,6 @@ size_t stream_workspace_bytes(int bs, int kv, int kv_len) {
 // (C >= kv_len / 16).
 bool use_stream(int C, int kv_len) { return static_cast<int64_t>(C) * 16 >= kv_len; }
 
-bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 }  // namespace
 }  // namespace zkv
@@ -459,12 +460,13 @@ extern "C" int zkv_rabitq4_rerank(const int64_t* cand, int64_t cd_sb, int64_t cd
                                   const uint16_t* q_blocks, const uint16_t* q_norm, const uint16_t* mag_centers,
                                   uint16_t* scores, float* scores_f32, uint16_t* v4b, void* workspace,
                                   size_t workspace_bytes, zkv_stream_t stream) {
-  ZKV_REQUIRE(cand && packed && weight && q_blocks && q_norm && mag_centers,
-              "zkv_rabitq4_rerank: null pointer");
-  ZKV_REQUIRE(scores || scores_f32, "zkv_rabitq4_rerank: no output");
   ZKV_REQUIRE(bs > 0 && kv > 0 && C >= 0 && kv_len >= 0, "zkv_rabitq4_rerank: bad sizes bs=%d kv=%d C=%d kv_len=%d",
               bs, kv, C, kv_len);
-  if (C == 0) return 0;
+  if (C == 0) return 0;  // (empty arrays may come as null pointers)
+  // with kv_len == 0 every candidate scores -inf and no code is read
+  ZKV_REQUIRE(cand && q_blocks && q_norm && mag_centers && (kv_len == 0 || (packed && weight)),
+              "zkv_rabitq4_rerank: null pointer");
+  ZKV_REQUIRE(scores || scores_f32, "zkv_rabitq4_rerank: no output");
   ZKV_REQUIRE((reinterpret_cast<uintptr_t>(packed) & 3u) == 0 && (!v4b || aligned16(v4b)),
               "zkv_rabitq4_rerank: the 4-bit codes must be 4-byte aligned and v4b 16-byte aligned");
   RerankParams p{};

@@ -276,6 +276,10 @@ def rabitq_rerank_topk(coarse_indices, key_4bit, key_block_weight, q_blocks, q_n
     scores [bs, kv, C]."""
     bs, kv, C = coarse_indices.shape
     k = min(int(final_topk), C)
+    if k <= 0:
+        out = torch.empty(bs, kv, 0, dtype=torch.int64, device=coarse_indices.device)
+        sc = torch.empty(bs, kv, C, dtype=torch.bfloat16, device=coarse_indices.device)
+        return (out, sc) if return_scores else out
     f32 = torch.empty(bs, kv, C, dtype=torch.float32, device=coarse_indices.device)
     sc = torch.empty(bs, kv, C, dtype=torch.bfloat16, device=coarse_indices.device) if return_scores else None
     _rerank(coarse_indices, key_4bit, key_block_weight, q_blocks, q_norm, mag_centers, B, m, scores=sc,
