@@ -295,3 +295,16 @@ def test_rerank_empty_candidates_and_empty_cache(rng):
     assert (_bits(s) == 0xFF80).all() and (_bits(only) == 0xFF80).all()
     assert (_bits(v) == 0).all()
     assert np.array_equal(out.cpu().numpy(), cand[..., :3].cpu().numpy())
+
+
+def test_quantizer_loads_the_reference_sign_codebook():
+    """MultiDimBlockQuantizer on the reference's own codebook file (copied as
+    data): V_omega_gpu is its +-1 rows as bf16, the SRHT signs are seeded."""
+    zk = _zk()
+    import json
+    path = Path(__file__).parent / "golden" / "pariskv_codebooks" / "codebook_d128_m8_Kr1_Kw256_rabitq_sign.json"
+    qz = zk.MultiDimBlockQuantizer(128, 8, 1, 256, str(path))
+    want = torch.tensor(json.loads(path.read_text())["angular_signs"], dtype=torch.float32)
+    assert torch.equal(qz.V_omega_gpu.float().cpu(), torch.where(want >= 0, 1.0, -1.0))
+    again = zk.MultiDimBlockQuantizer(128, 8, 1, 256, str(path))
+    assert torch.equal(qz.srht_diagonal_signs[0], again.srht_diagonal_signs[0])
