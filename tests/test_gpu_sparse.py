@@ -184,3 +184,18 @@ def test_c3_pipeline_graph_replays_match_eager():
         sel1 = step(ws[1], *bufs[1])
         torch.cuda.synchronize()
         assert torch.equal(sel1, eager[1][0]) and torch.equal(bufs[1][2], eager[1][1])
+
+
+def test_sparse_attention_zero_pages_is_residual_only(rng):
+    """An empty page list (n_sel = 0) attends the residual window only."""
+    from zoomkv_revision_amd import kivi
+    ref_cache, cache = _pack(rng, 1, 2, 6)
+    kr = gaussian_bf16(rng, (1, 2, 128, 128))
+    vr = gaussian_bf16(rng, (1, 2, 128, 128))
+    cache.k_res.copy_(to_bf16(kr))
+    cache.v_res.copy_(to_bf16(vr))
+    q = gaussian_bf16(rng, (1, 8, 128))
+    empty = torch.empty(1, 2, 0, dtype=torch.int64, device="cuda")
+    got = from_torch(kivi.kivi4_sparse_attention(to_bf16(q), cache, empty, 6, 40, out_dtype=torch.float32))
+    ref = okivi.kivi4_sparse_attention(q, ref_cache, 6, kr, vr, 40, np.zeros((1, 2, 0), int), 1 / np.sqrt(128))
+    assert np.abs(got - ref).max() <= ATOL

@@ -94,6 +94,7 @@ struct AttnParams {
   // one tile (group g, both halves), any other in-range page a tile of its
   // own half (bit m of the mask = tokens 16m .. 16m+15); ids outside
   // [0, 2 n_groups) are skipped.
+  int page_sparse;  // the page-sparse kernel runs (also for an empty list)
   const int64_t* pages;
   int64_t pg_sb, pg_sh;
   int n_sel;
@@ -1158,7 +1159,7 @@ size_t workspace_bytes_for(int bs, int hq, int /*kv*/, int n_splits) {
 void launch_attn(const AttnParams& p, int bs, hipStream_t s) {
   const dim3 grid(p.n_splits, p.kv, bs);
   const Shape sh = attn_shape();
-  if (p.pages != nullptr) {
+  if (p.page_sparse) {
     kivi4_attn_kernel<kSparseNW, kSparseD, true><<<grid, 64 * kSparseNW, 0, s>>>(p);
   } else if (p.n_groups == 0) {  // bf16 rows only: the 16-byte V layout
     kivi4_attn_kernel<8, 2, false, true><<<grid, 512, 0, s>>>(p);
@@ -1288,6 +1289,7 @@ int attention_launch(const uint16_t* q, int64_t q_sb, int64_t q_sh, const int32_
   p.ws_ml = p.ws_o + static_cast<size_t>(bs) * hq * sp.n_splits * 128;
   p.out = out;
   p.out_f32 = out_f32;
+  p.page_sparse = sparse != nullptr;
   p.pages = sparse ? sparse->pages : nullptr;
   p.pg_sb = sparse ? sparse->pg_sb : 0;
   p.pg_sh = sparse ? sparse->pg_sh : 0;
