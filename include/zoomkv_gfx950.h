@@ -110,7 +110,13 @@ int zkv_kivi4_pack(const uint16_t* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
  * out      [bs, hq, 128] contiguous, bf16 (out_f32 == 0) or fp32 (out_f32 != 0)
  * n_splits context splits per (b, kv head); 0 = automatic
  * workspace device scratch of zkv_kivi4_attention_workspace_size() bytes
- *          (split partials); calls that overlap on one workspace race.
+ *          (split partials, then one 8-byte arrival slot per (b, kv) when
+ *          the plan has more than one split); any initial contents, no
+ *          zeroing needed; calls that overlap on one workspace race.
+ * With more than one split, the splits are merged inside the one launch by
+ * the workgroup that completes each (b, kv) (same bits as the partial + merge
+ * pair below); environment ZKV_SPLIT_MERGE=kernel selects a separate merge
+ * launch instead.
  * ------------------------------------------------------------------------ */
 size_t zkv_kivi4_attention_workspace_size(int bs, int hq, int kv, int n_groups, int res_len,
                                           int n_splits);
@@ -126,8 +132,8 @@ int zkv_kivi4_decode_attention(const uint16_t* q, int64_t q_sb, int64_t q_sh,
  * allocate device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc).  The split partials live in a static
  * device array of ZKV_NOALLOC_SCRATCH_BYTES per GPU, held until the process
- * ends; a call whose split plan needs more (bs * hq * splits * 520 bytes)
- * fails with ZKV_ESPACE.  Every call on one GPU shares that GPU's array:
+ * ends; a call whose split plan needs more (bs * hq * splits * 520 bytes,
+ * plus bs * kv * 8 with more than one split) fails with ZKV_ESPACE.  Every call on one GPU shares that GPU's array:
  * calls that overlap on one GPU (concurrent streams or threads) race.
  * Results equal zkv_kivi4_decode_attention's for the same arguments. */
 #define ZKV_NOALLOC_SCRATCH_BYTES ((size_t)8 << 20)

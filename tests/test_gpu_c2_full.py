@@ -75,3 +75,18 @@ def test_c2_full_shape_split_plans_agree(c2):
     one = from_torch(kivi.kivi4_decode_attention(q, cache, NG, R, out_dtype=torch.float32, n_splits=1))
     assert np.isfinite(auto).all() and np.isfinite(one).all()
     assert np.abs(auto - one).max() <= 1e-3
+
+
+def test_c2_full_shape_in_launch_merge_equals_merge_kernel(c2, monkeypatch):
+    """The headline plan merges its splits inside the attention launch; the
+    result is bit-identical to the partials merged by the separate kernel."""
+    from zoomkv_revision_amd import kivi
+    cache, _, q = c2
+    ws = kivi.attention_workspace(B, HQ, HKV, NG, R, 0)
+    out = torch.empty(B, HQ, 128, dtype=torch.float32, device=q.device)
+    _, used = kivi.kivi4_attention_partial(q, cache, NG, R, workspace=ws)
+    ref = kivi.attention_merge(ws, B, HQ, HKV, used, out).clone()
+    monkeypatch.delenv("ZKV_SPLIT_MERGE", raising=False)
+    for _ in range(3):
+        got = kivi.kivi4_decode_attention(q, cache, NG, R, out_dtype=torch.float32, workspace=ws)
+        assert torch.equal(got.view(torch.int32), ref.view(torch.int32))

@@ -57,6 +57,8 @@
 #include "zkv_common.hpp"
 
 #include <algorithm>
+#include <atomic>
+#include <cstring>
 #include <cstdlib>
 #include <mutex>
 
@@ -89,6 +91,11 @@ struct AttnParams {
   float* ws_ml;    // [bs, kv, n_splits, gqa, 2]
   void* out;       // [bs, kv*gqa, 128], written directly when n_splits == 1
   int out_f32;
+  // in-launch split merge (out != nullptr, n_splits > 1): one arrival slot
+  // per (b, kv) [bs*kv] = (epoch << 8) | splits arrived; the split that
+  // completes the count merges all partials.  nullptr: partials only.
+  unsigned long long* slots;
+  unsigned long long epoch;  // distinct per launch, never 0
   // page-sparse mode: the sorted page list of (b, kv) at pages + b*pg_sb +
   // h*pg_sh (n_sel ids).  Its tiles: a page 2g joined by a following 2g+1 is
   // one tile (group g, both halves), any other in-range page a tile of its
@@ -578,6 +585,106 @@ __device__ __forceinline__ void store_out(const AttnParams& p, int64_t row, int 
     reinterpret_cast<uint16_t*>(p.out)[row * 128 + d] = f32_to_bf16_bits(v);
 }
 
+// Agent-scope (device-coherent) accesses of the split partials that are
+// merged inside the launch: the splits of one (b, kv) run on different XCDs,
+// whose L2s are not coherent with each other.  On gfx950 these are
+// write-through stores and loads that do not hit stale L2 lines (sc1), so
+// no whole-L2 writeback or invalidate is needed.
+__device__ __forceinline__ void store_agent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <bool kAgent>
+__device__ __forceinline__ float load_partial(const float* p) {
+  if constexpr (kAgent)
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else
+    return *p;
+}
+
+// LSE merge of the n_splits partials of one (b, query head) at channel d, in
+// split order 0, 1, ...: the merge kernel and the in-launch merge run the
+// same arithmetic, so they give the same bits.  Returns o; mmax and den are
+// the merged base-2 max and denominator (for the LSE).  Up to kBatch splits,
+// every partial is requested before any is used (unconditional loads, the
+// split index clamped), so the merge costs one memory round trip.
+template <bool kAgent>
+__device__ __forceinline__ float combine_splits(const float* ws_o, const float* ws_ml, int64_t row0, int gqa,
+                                                int n_splits, int d, float& mmax, float& den) {
+  constexpr int kBatch = 8;
+  float num = 0.0f;
+  mmax = kNegBig;
+  den = 0.0f;
+  if (n_splits <= kBatch) {
+    float mv[kBatch], lv[kBatch], ov[kBatch];
+#pragma unroll
+    for (int s = 0; s < kBatch; ++s) {
+      const int64_t row = row0 + static_cast<int64_t>(min(s, n_splits - 1)) * gqa;
+      mv[s] = load_partial<kAgent>(ws_ml + row * 2);
+      lv[s] = load_partial<kAgent>(ws_ml + row * 2 + 1);
+      ov[s] = load_partial<kAgent>(ws_o + row * 128 + d);
+    }
+#pragma unroll
+    for (int s = 0; s < kBatch; ++s) mmax = s < n_splits ? fmaxf(mmax, mv[s]) : mmax;
+#pragma unroll
+    for (int s = 0; s < kBatch; ++s) {
+      const float w = __builtin_amdgcn_exp2f(mv[s] - mmax);
+      den = s < n_splits ? den + w * lv[s] : den;
+      num = s < n_splits ? num + w * ov[s] : num;
+    }
+  } else {
+    for (int s = 0; s < n_splits; ++s)
+      mmax = fmaxf(mmax, load_partial<kAgent>(ws_ml + (row0 + static_cast<int64_t>(s) * gqa) * 2));
+#pragma unroll 4
+    for (int s = 0; s < n_splits; ++s) {
+      const int64_t row = row0 + static_cast<int64_t>(s) * gqa;
+      const float w = __builtin_amdgcn_exp2f(load_partial<kAgent>(ws_ml + row * 2) - mmax);
+      den += w * load_partial<kAgent>(ws_ml + row * 2 + 1);
+      num += w * load_partial<kAgent>(ws_o + row * 128 + d);
+    }
+  }
+  return den > 0.0f ? num / den : 0.0f;
+}
+
+// In-launch split merge, run by every workgroup after its partial stores
+// (store_agent).  Each workgroup waits until its own stores are complete,
+// then one lane counts the workgroup in on the (b, kv) slot with a
+// compare-and-swap: a slot whose epoch is not this launch's is stale (an
+// earlier launch, or fresh memory) and restarts at 1; the last arrival
+// resets the count to 0 under the launch's epoch.  The first attempt
+// expects the count one short of complete, so the last arrival -- the one on
+// the launch's critical path -- needs a single round trip.  The workgroup that
+// brings the count to n_splits merges every split's partial with
+// combine_splits, so which workgroup merges does not change the bits.
+__device__ __forceinline__ void merge_splits_last(const AttnParams& p, int64_t bh, int tid, int nthreads,
+                                                  int* s_last) {
+  __builtin_amdgcn_s_waitcnt(0);  // this lane's partial stores are device-visible
+  __syncthreads();
+  if (tid == 0) {
+    unsigned long long* slot = p.slots + bh;
+    unsigned long long old = (p.epoch << 8) | static_cast<unsigned long long>(p.n_splits - 1);
+    unsigned long long nv = old + 1;
+    while (!__hip_atomic_compare_exchange_strong(slot, &old, nv, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT))
+      nv = (old >> 8) == p.epoch ? old + 1 : ((p.epoch << 8) | 1ull);
+    const bool last = (nv & 0xffull) == static_cast<unsigned long long>(p.n_splits);
+    // the last arrival leaves the count at 0 under this epoch, so a replay of
+    // the same launch (a captured graph keeps its epoch) counts from 0 again
+    if (last) __hip_atomic_store(slot, p.epoch << 8, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *s_last = last;
+  }
+  __syncthreads();
+  if (!*s_last) return;
+  for (int idx = tid; idx < p.gqa * 128; idx += nthreads) {
+    const int cc = idx >> 7, d = idx & 127;
+    const int64_t row0 = bh * p.n_splits * p.gqa + cc;
+    float mmax, den;
+    const float r = combine_splits<true>(p.ws_o, p.ws_ml, row0, p.gqa, p.n_splits, d, mmax, den);
+    const int64_t qrow = bh * p.gqa + cc;  // b*hq + h*gqa + cc
+    store_out(p, qrow, d, r);
+    if (p.lse != nullptr && d == 0) p.lse[qrow] = (mmax + __log2f(den)) * kLn2;
+  }
+}
+
 constexpr int kMetaBytes = 1024;  // the record's last KiB: K and V scale/zero
 constexpr int kMaxGqa = 16;       // query heads per KV head (checked on the host)
 // A bf16 residual tile (two dependent memory round trips, 16 KiB) takes a
@@ -955,6 +1062,7 @@ void kivi4_attn_kernel(const AttnParams p) {
 
   const int n_out = p.gqa * 128;
   const bool final_out = p.out != nullptr && p.n_splits == 1;
+  const bool fused_merge = p.out != nullptr && p.n_splits > 1 && p.slots != nullptr;
   for (int idx = tid; idx < n_out; idx += 64 * NW) {
     const int cc = idx >> 7, d = idx & 127;
     float mm = kNegBig;
@@ -970,6 +1078,13 @@ void kivi4_attn_kernel(const AttnParams p) {
     if (final_out) {
       store_out(p, bh * p.gqa + cc, d, ll > 0.0f ? oo / ll : 0.0f);  // row b*hq + h*gqa + cc
       if (p.lse != nullptr && d == 0) p.lse[bh * p.gqa + cc] = (mm + __log2f(ll)) * kLn2;
+    } else if (fused_merge) {
+      const int64_t row = (bh * p.n_splits + split) * p.gqa + cc;
+      store_agent(p.ws_o + row * 128 + d, oo);
+      if (d == 0) {
+        store_agent(p.ws_ml + row * 2, mm);
+        store_agent(p.ws_ml + row * 2 + 1, ll);
+      }
     } else {
       const int64_t row = (bh * p.n_splits + split) * p.gqa + cc;
       p.ws_o[row * 128 + d] = oo;
@@ -979,6 +1094,10 @@ void kivi4_attn_kernel(const AttnParams p) {
       }
     }
   }
+  // (the flag reuses the first word of smem: merge_splits_last writes it
+  // only after a barrier that follows every read of the reduction above)
+  if (fused_merge)
+    merge_splits_last(p, bh, tid, 64 * NW, reinterpret_cast<int*>(smem));
 }
 
 // Merge the n_splits partials of every (b, query head) with the LSE rule
@@ -994,17 +1113,8 @@ __global__ __launch_bounds__(128) void kivi4_combine_kernel(const float* __restr
   const int h = qh / gqa, c = qh % gqa;
   const int d = threadIdx.x;
   const int64_t row0 = ((static_cast<int64_t>(b) * kv + h) * n_splits) * gqa + c;
-  float mmax = kNegBig;
-  for (int s = 0; s < n_splits; ++s) mmax = fmaxf(mmax, ws_ml[(row0 + s * gqa) * 2]);
-  float num = 0.0f, den = 0.0f;
-#pragma unroll 4
-  for (int s = 0; s < n_splits; ++s) {
-    const int64_t row = row0 + static_cast<int64_t>(s) * gqa;
-    const float w = __builtin_amdgcn_exp2f(ws_ml[row * 2] - mmax);
-    den += w * ws_ml[row * 2 + 1];
-    num += w * ws_o[row * 128 + d];
-  }
-  const float r = den > 0.0f ? num / den : 0.0f;
+  float mmax, den;
+  const float r = combine_splits<false>(ws_o, ws_ml, row0, gqa, n_splits, d, mmax, den);
   if (lse != nullptr && d == 0) lse[bq] = (mmax + __log2f(den)) * kLn2;
   const int64_t oi = static_cast<int64_t>(bq) * 128 + d;
   if (out_f32)
@@ -1147,13 +1257,36 @@ SplitPlan plan_splits(int bs, int kv, int n_groups, int res_len, int n_splits, S
   return {ns, per, odd};
 }
 
-// Workspace layout: split partials o fp32 [bs, kv, S, gqa, 128] followed by
-// (m, l) fp32 [bs, kv, S, gqa, 2].  The splits merge in a second kernel: a
-// merge by the last split inside the launch needs a device-scope fence per
-// workgroup, which cost more than that kernel (C2 148 us instead of 129, C3
-// step 43.9 us instead of 38.4).
-size_t workspace_bytes_for(int bs, int hq, int /*kv*/, int n_splits) {
+// Workspace layout: split partials o fp32 [bs, kv, S, gqa, 128], then (m, l)
+// fp32 [bs, kv, S, gqa, 2], then (S > 1) one 8-byte arrival slot per (b, kv)
+// for the in-launch merge.  The slots need no initial value: each launch
+// carries its own epoch, and a slot holding another epoch counts as empty.
+//
+// The splits merge inside the launch: the workgroup that completes a (b, kv)
+// merges it.  Its partials go out with device-coherent (write-through)
+// stores and are read back with device-coherent loads; a device-scope fence
+// per workgroup (a whole-L2 writeback and invalidate on gfx950) cost more than
+// the separate merge kernel it replaced (C2 148 us instead of 129).
+// ZKV_SPLIT_MERGE=kernel keeps the separate merge kernel (for A/B timing).
+size_t partial_bytes_for(int bs, int hq, int n_splits) {
   return static_cast<size_t>(bs) * hq * n_splits * (128 + 2) * sizeof(float);
+}
+
+size_t workspace_bytes_for(int bs, int hq, int kv, int n_splits) {
+  const size_t slots = n_splits > 1 ? static_cast<size_t>(bs) * kv * sizeof(unsigned long long) : 0;
+  return partial_bytes_for(bs, hq, n_splits) + slots;
+}
+
+bool merge_in_launch() {  // read at every launch, so tests can compare both
+  const char* e = getenv("ZKV_SPLIT_MERGE");
+  return !(e && strcmp(e, "kernel") == 0);
+}
+
+// Epoch of a merging launch: distinct for every launch of the process (56
+// bits: never wraps), never 0.
+unsigned long long next_epoch() {
+  static std::atomic<unsigned long long> counter{0};
+  return (counter.fetch_add(1, std::memory_order_relaxed) + 1) & ((1ull << 56) - 1);
 }
 
 void launch_attn(const AttnParams& p, int bs, hipStream_t s) {
@@ -1289,6 +1422,15 @@ int attention_launch(const uint16_t* q, int64_t q_sb, int64_t q_sh, const int32_
   p.ws_ml = p.ws_o + static_cast<size_t>(bs) * hq * sp.n_splits * 128;
   p.out = out;
   p.out_f32 = out_f32;
+  p.slots = nullptr;
+  p.epoch = 0;
+  // (the slot counts arrivals in 8 bits)
+  const bool merge_here = out != nullptr && sp.n_splits > 1 && sp.n_splits < 256 && merge_in_launch();
+  if (merge_here) {
+    p.slots = reinterpret_cast<unsigned long long*>(static_cast<uint8_t*>(workspace) +
+                                                    partial_bytes_for(bs, hq, sp.n_splits));
+    p.epoch = next_epoch();
+  }
   p.page_sparse = sparse != nullptr;
   p.pages = sparse ? sparse->pages : nullptr;
   p.pg_sb = sparse ? sparse->pg_sb : 0;
@@ -1297,7 +1439,7 @@ int attention_launch(const uint16_t* q, int64_t q_sb, int64_t q_sh, const int32_
   if (n_splits_used) *n_splits_used = sp.n_splits;
   launch_attn(p, bs, s);
   int rc = check_launch("kivi4_attn_kernel");
-  if (rc || out == nullptr || sp.n_splits == 1) return rc;
+  if (rc || out == nullptr || sp.n_splits == 1 || merge_here) return rc;
   kivi4_combine_kernel<<<bs * hq, 128, 0, s>>>(p.ws_o, p.ws_ml, kv, gqa, sp.n_splits, out, out_f32, lse);
   return check_launch("kivi4_combine_kernel");
 }
