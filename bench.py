@@ -703,11 +703,6 @@ def main():
         # completes each (sequence, KV head)
         kivi.kivi4_decode_attention(q, caches[i % 2], NG, R, out=out, n_splits=args.splits, workspace=ws)
 
-    # The dominant kernel's device time first (median of 5 back-to-back
-    # batches): ~25 ms of launches, which also bring a freshly started GPU
-    # to its working clocks before the warm-up and timed steps (measured: the
-    # first ~10 ms of launches in a new process run up to 15% slower).
-    k_ms = statistics.median(kernel_batch_ms(step, max(args.steps, 50)) for _ in range(5))
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
@@ -717,6 +712,7 @@ def main():
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     ms_step = (t1 - t0) * 1e3 / args.steps
+    k_ms = kernel_batch_ms(step, args.steps)
     achieved = ALGO_BYTES / (k_ms * 1e-3) / 1e9
 
     cpu = None if args.no_cpu else cpu_baseline(caches[0], q)

@@ -7,6 +7,9 @@
 // reference's bf16 intrinsics do.
 #include "zkv_common.hpp"
 
+#include <cstdlib>
+#include <type_traits>
+
 namespace zkv {
 namespace {
 
@@ -99,14 +102,13 @@ __global__ __launch_bounds__(256) void quest_score_kernel(
 // loads are issued first; meanwhile threads 0..127 form raw_q[bh] dim tid =
 // bf16(sum_i q[b, h*group + i][tid] / group) in head order (gqa_mean_kernel's
 // arithmetic) into LDS, and block 0 of the row stores it.
-template <bool kFp16Meta>
+template <bool kFp16Meta, int U>
 __global__ __launch_bounds__(256) void quest_gqa_kernel(
     const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_sh, int group, int kv,
     uint16_t* __restrict__ raw_q_out, const uint16_t* __restrict__ cmin, const uint16_t* __restrict__ cmax,
     const uint8_t* __restrict__ valid, float* __restrict__ scores, int n_chunks, int n_max) {
   __shared__ uint16_t s_q[128];
   const int half = threadIdx.x >> 5, t = threadIdx.x & 31;
-  constexpr int U = kQuestUnroll;
   const int bh = blockIdx.y;
   const int c0 = (blockIdx.x * 8 + half) * U;
   u32x2_t mv[U], xv[U];
@@ -1042,6 +1044,21 @@ __global__ __launch_bounds__(128) void page_minmax_f16_kernel(
 
 using namespace zkv;
 
+namespace zkv {
+namespace {
+// Chunks per 32-lane half of the fused GQA-mean Quest launch (loads issued
+// together); ZKV_QUEST_UNROLL=4|8|16 overrides it for tuning sweeps.
+int quest_gqa_unroll() {
+  static int v = [] {
+    int u = 4;
+    if (const char* e = getenv("ZKV_QUEST_UNROLL")) u = atoi(e);
+    return (u == 8 || u == 16) ? u : 4;
+  }();
+  return v;
+}
+}  // namespace
+}  // namespace zkv
+
 extern "C" int zkv_quest_chunk_score_gqa(const uint16_t* q, int64_t q_sb, int64_t q_sh, int hq,
                                          uint16_t* raw_q, const uint16_t* chunk_min,
                                          const uint16_t* chunk_max, int meta_fp16, float* scores, int bs,
@@ -1052,14 +1069,24 @@ extern "C" int zkv_quest_chunk_score_gqa(const uint16_t* q, int64_t q_sb, int64_
                   static_cast<int64_t>(bs) * kv <= 65535,
               "zkv_quest_chunk_score_gqa: bad sizes bs=%d hq=%d kv=%d n_chunks=%d n_chunks_max=%d", bs, hq,
               kv, n_chunks, n_chunks_max);
-  const dim3 grid((n_chunks + 8 * kQuestUnroll - 1) / (8 * kQuestUnroll), bs * kv);
   auto s = reinterpret_cast<hipStream_t>(stream);
-  if (meta_fp16)
-    quest_gqa_kernel<true><<<grid, 256, 0, s>>>(q, q_sb, q_sh, hq / kv, kv, raw_q, chunk_min, chunk_max, valid,
-                                                scores, n_chunks, n_chunks_max);
+  auto launch = [&](auto u_tag) {
+    constexpr int U = decltype(u_tag)::value;
+    const dim3 grid((n_chunks + 8 * U - 1) / (8 * U), bs * kv);
+    if (meta_fp16)
+      quest_gqa_kernel<true, U><<<grid, 256, 0, s>>>(q, q_sb, q_sh, hq / kv, kv, raw_q, chunk_min, chunk_max,
+                                                     valid, scores, n_chunks, n_chunks_max);
+    else
+      quest_gqa_kernel<false, U><<<grid, 256, 0, s>>>(q, q_sb, q_sh, hq / kv, kv, raw_q, chunk_min, chunk_max,
+                                                      valid, scores, n_chunks, n_chunks_max);
+  };
+  const int u = quest_gqa_unroll();
+  if (u == 16)
+    launch(std::integral_constant<int, 16>{});
+  else if (u == 8)
+    launch(std::integral_constant<int, 8>{});
   else
-    quest_gqa_kernel<false><<<grid, 256, 0, s>>>(q, q_sb, q_sh, hq / kv, kv, raw_q, chunk_min, chunk_max,
-                                                 valid, scores, n_chunks, n_chunks_max);
+    launch(std::integral_constant<int, 4>{});
   return check_launch("quest_gqa_kernel");
 }
 
