@@ -657,7 +657,9 @@ __device__ __forceinline__ float combine_splits(const float* ws_o, const float* 
 // combine_splits, so which workgroup merges does not change the bits.
 __device__ __forceinline__ void merge_splits_last(const AttnParams& p, int64_t bh, int tid, int nthreads,
                                                   int* s_last) {
-  __builtin_amdgcn_s_waitcnt(0);  // this lane's partial stores are device-visible
+  // this lane's partial stores are device-visible (the memory clobber keeps
+  // the compiler from moving any store below the wait)
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   if (tid == 0) {
     unsigned long long* slot = p.slots + bh;
