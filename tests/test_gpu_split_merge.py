@@ -25,14 +25,27 @@ def _bits(t):
     return (t.view(torch.int32) if t.dtype == torch.float32 else t.view(torch.int16)).cpu().numpy()
 
 
+def _same_bits(a, b):
+    if isinstance(a, tuple):
+        return all(_same_bits(x, y) for x, y in zip(a, b))
+    return np.array_equal(_bits(a), _bits(b))
+
+
 def _both(monkeypatch, fn):
-    """fn() with the merge kernel, then with the in-launch merge."""
+    """fn() with the merge kernel, then with the in-launch merge (device-
+    coherent partials, the default); the in-launch merge ordered by
+    agent-scope fences (ZKV_SPLIT_MERGE=fence) must give the same bits."""
     monkeypatch.setenv("ZKV_SPLIT_MERGE", "kernel")
     ref = fn()
     torch.cuda.synchronize()
+    monkeypatch.setenv("ZKV_SPLIT_MERGE", "fence")
+    fenced = fn()
+    torch.cuda.synchronize()
+    fenced = tuple(t.clone() for t in fenced) if isinstance(fenced, tuple) else fenced.clone()
     monkeypatch.delenv("ZKV_SPLIT_MERGE")
     got = fn()
     torch.cuda.synchronize()
+    assert _same_bits(fenced, got), "fence-ordered merge differs from the device-coherent one"
     return ref, got
 
 

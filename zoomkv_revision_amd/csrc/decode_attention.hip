@@ -96,6 +96,7 @@ struct AttnParams {
   // completes the count merges all partials.  nullptr: partials only.
   unsigned long long* slots;
   unsigned long long epoch;  // distinct per launch, never 0
+  int merge_fence;           // 1: plain partials ordered by agent-scope fences
   // page-sparse mode: the sorted page list of (b, kv) at pages + b*pg_sb +
   // h*pg_sh (n_sel ids).  Its tiles: a page 2g joined by a following 2g+1 is
   // one tile (group g, both halves), any other in-range page a tile of its
@@ -659,9 +660,12 @@ __device__ __forceinline__ void merge_splits_last(const AttnParams& p, int64_t b
                                                   int* s_last) {
   // this lane's partial stores are device-visible (the memory clobber keeps
   // the compiler from moving any store below the wait)
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  if (!p.merge_fence) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   if (tid == 0) {
+    // fence variant: the workgroup's plain stores, ordered before this lane
+    // by the barrier, are released at agent scope (an L2 writeback)
+    if (p.merge_fence) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
     unsigned long long* slot = p.slots + bh;
     unsigned long long old = (p.epoch << 8) | static_cast<unsigned long long>(p.n_splits - 1);
     unsigned long long nv = old + 1;
@@ -672,10 +676,23 @@ __device__ __forceinline__ void merge_splits_last(const AttnParams& p, int64_t b
     // the last arrival leaves the count at 0 under this epoch, so a replay of
     // the same launch (a captured graph keeps its epoch) counts from 0 again
     if (last) __hip_atomic_store(slot, p.epoch << 8, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (last && p.merge_fence) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     *s_last = last;
   }
   __syncthreads();
   if (!*s_last) return;
+  if (p.merge_fence) {
+    for (int idx = tid; idx < p.gqa * 128; idx += nthreads) {
+      const int cc = idx >> 7, d = idx & 127;
+      const int64_t row0 = bh * p.n_splits * p.gqa + cc;
+      float mmax, den;
+      const float r = combine_splits<false>(p.ws_o, p.ws_ml, row0, p.gqa, p.n_splits, d, mmax, den);
+      const int64_t qrow = bh * p.gqa + cc;
+      store_out(p, qrow, d, r);
+      if (p.lse != nullptr && d == 0) p.lse[qrow] = (mmax + __log2f(den)) * kLn2;
+    }
+    return;
+  }
   for (int idx = tid; idx < p.gqa * 128; idx += nthreads) {
     const int cc = idx >> 7, d = idx & 127;
     const int64_t row0 = bh * p.n_splits * p.gqa + cc;
@@ -1080,7 +1097,7 @@ void kivi4_attn_kernel(const AttnParams p) {
     if (final_out) {
       store_out(p, bh * p.gqa + cc, d, ll > 0.0f ? oo / ll : 0.0f);  // row b*hq + h*gqa + cc
       if (p.lse != nullptr && d == 0) p.lse[bh * p.gqa + cc] = (mm + __log2f(ll)) * kLn2;
-    } else if (fused_merge) {
+    } else if (fused_merge && !p.merge_fence) {
       const int64_t row = (bh * p.n_splits + split) * p.gqa + cc;
       store_agent(p.ws_o + row * 128 + d, oo);
       if (d == 0) {
@@ -1284,6 +1301,11 @@ bool merge_in_launch() {  // read at every launch, so tests can compare both
   return !(e && strcmp(e, "kernel") == 0);
 }
 
+bool merge_with_fence() {
+  const char* e = getenv("ZKV_SPLIT_MERGE");
+  return e && strcmp(e, "fence") == 0;
+}
+
 // Epoch of a merging launch: distinct for every launch of the process (56
 // bits: never wraps), never 0.
 unsigned long long next_epoch() {
@@ -1426,6 +1448,7 @@ int attention_launch(const uint16_t* q, int64_t q_sb, int64_t q_sh, const int32_
   p.out_f32 = out_f32;
   p.slots = nullptr;
   p.epoch = 0;
+  p.merge_fence = merge_with_fence();
   // (the slot counts arrivals in 8 bits)
   const bool merge_here = out != nullptr && sp.n_splits > 1 && sp.n_splits < 256 && merge_in_launch();
   if (merge_here) {
