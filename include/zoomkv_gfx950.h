@@ -116,7 +116,8 @@ int zkv_kivi4_pack(const uint16_t* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
  * With more than one split, the splits are merged inside the one launch by
  * the workgroup that completes each (b, kv) (same bits as the partial + merge
  * pair below); environment ZKV_SPLIT_MERGE=kernel selects a separate merge
- * launch instead.
+ * launch instead, ZKV_SPLIT_MERGE=fence an in-launch merge ordered by
+ * agent-scope fences (slower, same bits).
  * ------------------------------------------------------------------------ */
 size_t zkv_kivi4_attention_workspace_size(int bs, int hq, int kv, int n_groups, int res_len,
                                           int n_splits);
