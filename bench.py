@@ -59,6 +59,29 @@ def cpu_model() -> str:
     return "unknown"
 
 
+def time_cpu_threads(fn, budget_s: float = 10.0, max_calls: int = 20):
+    """Median wall time of fn() on 1 thread and on every thread of the
+    process's CPU share (torch.get_num_threads()), one warm-up call each;
+    returns {threads: (median s, calls)}."""
+    import torch
+    n_all = torch.get_num_threads()
+    res = {}
+    for nt in (1, n_all):
+        torch.set_num_threads(nt)
+        fn()
+        times = []
+        t_end = time.perf_counter() + budget_s
+        while time.perf_counter() < t_end or len(times) < 2:
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
+            if len(times) >= max_calls:
+                break
+        res[nt] = (statistics.median(times), len(times))
+    torch.set_num_threads(n_all)
+    return res
+
+
 def cpu_baseline(cache, q, budget_s: float = 10.0, rows=(0,)):
     """The torch-CPU restatement of the C2 step (oracle/torch_cpu.py: 4-bit
     unpack + dequant, residual append, float32 SDPA with grouped heads) at
@@ -440,42 +463,33 @@ def run_c3(args):
 
 
 def c3_cpu_baseline(w, n_sel, budget_s: float = 10.0):
-    """numpy oracle of the C3 step (Quest bounds, top-k, dequant + sparse
-    attention) for one (batch, kv head) of the 64, one thread."""
+    """The torch-CPU restatement of the C3 step (oracle/torch_cpu.py: Quest
+    bounds over the fp16 page metadata, torch.topk, unpack + dequant of the
+    selected pages, float32 SDPA with grouped heads) at the full C3 shape
+    (batch 8, 32 / 8 heads, 2048 pages, top-128), timed with 1 thread and
+    with every thread of the process's CPU share."""
     import numpy as np
     import torch
-    from threadpoolctl import threadpool_limits
-    from oracle import kivi as okivi
-    from oracle import select as osel
-    f16 = lambda t: t.cpu().view(torch.int16).numpy().view(np.uint16).view(np.float16).astype(np.float32)
-    raw_q = w["raw_q"][:1, :1].float().cpu().numpy()
-    pmin, pmax = f16(w["page_min"][:1, :1]), f16(w["page_max"][:1, :1])
+    from oracle import torch_cpu
+    f16 = lambda t: t.cpu().view(torch.int16).numpy().view(np.uint16)
     c = w["cache"]
-    c0 = okivi.Kivi4Cache(c.k_codes[:1, :1].cpu().numpy(),
-                          c.k_meta[:1, :1].cpu().view(torch.int16).numpy().view(np.uint16),
-                          c.v_codes[:1, :1].cpu().numpy(),
-                          c.v_meta[:1, :1].cpu().view(torch.int16).numpy().view(np.uint16))
-    q = w["q"][:1, :4].float().cpu().numpy()
-    z = np.zeros((1, 1, 0, 128), np.float32)
-    times = []
-    with threadpool_limits(limits=1):
-        t_end = time.perf_counter() + budget_s
-        while time.perf_counter() < t_end or len(times) < 2:
-            t0 = time.perf_counter()
-            sc = osel.quest_chunk_score(raw_q, pmin, pmax, pmin.shape[2])
-            sel = osel.topk_indices(sc, n_sel)
-            okivi.kivi4_sparse_attention(q, c0, c0.k_codes.shape[2], z, z, 0, sel, 1 / np.sqrt(128),
-                                         dtype=np.float32)
-            times.append(time.perf_counter() - t0)
-            if len(times) >= 20:
-                break
-    t = statistics.median(times)
-    units = 8 * 8
-    return {"value": 8 / (t * units), "unit": "tokens/s", "cores": 1, "kind": "port",
-            "sample": f"numpy oracle of one (batch, kv head) of {units}: Quest bounds over 2048 pages, "
-                      f"top-{n_sel}, dequant + float32 attention of 4 query heads; median of "
-                      f"{len(times)} calls ({t * 1e3:.0f} ms each), scaled to the batch of 8; "
-                      f"host {os.cpu_count()} logical CPUs, 1 used"}
+    prep = torch_cpu.prepare_c3(w["raw_q"].float().cpu().numpy(), f16(w["page_min"]), f16(w["page_max"]),
+                                c.k_codes.cpu().numpy(), f16(c.k_meta), c.v_codes.cpu().numpy(), f16(c.v_meta))
+    q = w["q"].float().cpu()
+    sel, _ = torch_cpu.c3_step(q, prep, n_sel, 1 / math.sqrt(D))
+    planted = torch.equal(sel, w["planted"].cpu())
+    res = time_cpu_threads(lambda: torch_cpu.c3_step(q, prep, n_sel, 1 / math.sqrt(D)), budget_s)
+    n_all = max(res)
+    (t1, n1), (tn, nn) = res[1], res[n_all]
+    bs = q.shape[0]
+    return {"value": bs / t1, "unit": "tokens/s", "cores": 1, "kind": "port",
+            "all_cores": {"value": bs / tn, "cores": n_all},
+            "cpu_model": cpu_model(), "host_logical_cpus": os.cpu_count(),
+            "sample": f"torch-CPU restatement (oracle/torch_cpu.py) of the whole C3 step at its full shape "
+                      f"(batch {bs}, Quest over {prep['pmin'].shape[2]} pages, top-{n_sel}, sparse attention; selection equals "
+                      f"the planted pages: {planted}); median of {n1} calls ({t1 * 1e3:.0f} ms) on 1 thread "
+                      f"and {nn} calls ({tn * 1e3:.0f} ms) on {n_all} threads (the process's CPU share; "
+                      f"host {os.cpu_count()} logical CPUs, {cpu_model()})"}
 
 
 def run_c4(args):
@@ -523,30 +537,28 @@ def run_c4(args):
 
 
 def c4_cpu_baseline(pool, qs, signs, topk, budget_s: float = 10.0):
+    """The torch-CPU restatement of the C4 search (oracle/torch_cpu.py: query
+    rotation and codes, XOR + 64-bit bit count over the 131072 key codes for
+    all 64 queries, torch.topk, exact fp32 rerank) at the full C4 shape,
+    timed with 1 thread and with every thread of the process's CPU share."""
     import numpy as np
     import torch
-    from threadpoolctl import threadpool_limits
-    from oracle import rabitq as orq
+    from oracle import torch_cpu
     keys, codes, fac = pool
-    kb = keys.cpu().view(torch.int16).numpy().view(np.uint16)
-    cb = codes.cpu().numpy()
-    fb = fac.cpu().view(torch.int16).numpy().view(np.uint16)
-    qb = qs[:4].cpu().view(torch.int16).numpy().view(np.uint16)
-    s = signs.cpu().numpy()
-    times = []
-    with threadpool_limits(limits=1):
-        t_end = time.perf_counter() + budget_s
-        while time.perf_counter() < t_end or len(times) < 2:
-            t0 = time.perf_counter()
-            orq.search(qb, kb, cb, fb, s, topk)
-            times.append(time.perf_counter() - t0)
-            if len(times) >= 20:
-                break
-    t = statistics.median(times)
-    return {"value": 4 / t, "unit": "queries/s", "cores": 1, "kind": "port",
-            "sample": f"numpy oracle search (encode, estimate over 131072 keys, top-{topk}, exact "
-                      f"rerank) for 4 of the 64 queries per call; median of {len(times)} calls "
-                      f"({t * 1e3:.0f} ms each); host {os.cpu_count()} logical CPUs, 1 used"}
+    f16 = lambda t: t.cpu().view(torch.int16).numpy().view(np.uint16)
+    prep = torch_cpu.prepare_c4(f16(keys), codes.cpu().numpy(), f16(fac), signs.cpu().numpy())
+    q = qs.float().cpu()
+    res = time_cpu_threads(lambda: torch_cpu.c4_search(q, prep, topk), budget_s)
+    n_all = max(res)
+    (t1, n1), (tn, nn) = res[1], res[n_all]
+    nq = q.shape[0]
+    return {"value": nq / t1, "unit": "queries/s", "cores": 1, "kind": "port",
+            "all_cores": {"value": nq / tn, "cores": n_all},
+            "cpu_model": cpu_model(), "host_logical_cpus": os.cpu_count(),
+            "sample": f"torch-CPU restatement (oracle/torch_cpu.py) of the whole C4 search at its full shape "
+                      f"({nq} queries x {keys.shape[0]} keys, top-{topk} + exact rerank); median of {n1} calls "
+                      f"({t1 * 1e3:.0f} ms) on 1 thread and {nn} calls ({tn * 1e3:.0f} ms) on {n_all} threads "
+                      f"(the process's CPU share; host {os.cpu_count()} logical CPUs, {cpu_model()})"}
 
 
 def run_r4(args):

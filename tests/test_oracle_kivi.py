@@ -253,3 +253,64 @@ def test_torch_cpu_restatement_equals_oracle_attention(rng):
     prep = torch_cpu.prepare_c2(c.k_codes, c.k_meta, c.v_codes, c.v_meta, kr, vr)
     got = torch_cpu.decode_attention(torch.from_numpy(q.astype(np.float32)), prep, 1 / np.sqrt(128)).numpy()
     assert got.shape == ref.shape and np.abs(got - ref).max() <= 1e-5
+
+
+def test_torch_cpu_c3_step_equals_oracle(rng):
+    """The torch-CPU C3 step (bench.py's C3 CPU baseline): Quest bounds within
+    fp32 summation-order rounding of the oracle's, the same top pages where
+    the bounds are separated, and the sparse attention over those pages equal
+    to the oracle's dequant + attention."""
+    import torch
+    from oracle import select as osel
+    from oracle import torch_cpu
+    B, KV, HQ, G, n_sel = 2, 2, 8, 8, 5
+    k = gaussian_bf16(rng, (B, KV, G * 32, 128), outlier_channels=2)
+    v = gaussian_bf16(rng, (B, KV, G * 32, 128))
+    q = gaussian_bf16(rng, (B, HQ, 128))
+    c = kivi.quantize_kivi4(k, v)
+    pmin, pmax = osel.page_minmax_f16(k)
+    raw_q = osel.gqa_mean_query(q, KV)
+    prep = torch_cpu.prepare_c3(raw_q, pmin, pmax, c.k_codes, c.k_meta, c.v_codes, c.v_meta)
+    from oracle.numerics import f16_to_f32
+    ref_sc = osel.quest_chunk_score(raw_q, f16_to_f32(pmin), f16_to_f32(pmax), 2 * G)
+    got_sc = torch_cpu.quest_scores(prep).numpy()
+    assert np.abs(got_sc - ref_sc).max() <= 1e-4 * np.abs(ref_sc).max()
+    sel, out = torch_cpu.c3_step(torch.from_numpy(q.astype(np.float32)), prep, n_sel, 1 / np.sqrt(128))
+    ref_sel = osel.topk_indices(ref_sc, n_sel)
+    s = np.sort(ref_sc, axis=-1)[..., ::-1]
+    if (s[..., n_sel - 1] - s[..., n_sel] > 1e-3 * np.abs(s).max()).all():
+        assert np.array_equal(sel.numpy(), np.sort(ref_sel, axis=-1))
+    z = np.zeros((B, KV, 0, 128), np.float32)
+    ref = kivi.kivi4_sparse_attention(q, c, G, z, z, 0, sel.numpy(), 1 / np.sqrt(128))
+    assert np.abs(out.numpy() - ref).max() <= 1e-5
+
+
+def test_torch_cpu_c4_search_equals_oracle():
+    """The torch-CPU C4 search (bench.py's C4 CPU baseline) against the numpy
+    oracle: the query codes, the candidate sets and the exact scores."""
+    import torch
+    from oracle import rabitq as orq
+    from oracle import torch_cpu
+    from oracle.numerics import f16_to_f32
+    rng = np.random.default_rng(5)
+    keys = orq.clustered_unit_keys(rng, 4096, 16)
+    qs = orq.clustered_unit_keys(rng, 12, 16)
+    signs = orq.srht_signs(42)
+    codes, fac = orq.encode(keys, signs)
+    cand_ref, _, _ = orq.search(qs, keys, codes, fac, signs, 64)
+    prep = torch_cpu.prepare_c4(keys, codes, fac, signs)
+    cand, exact = torch_cpu.c4_search(torch.from_numpy(f16_to_f32(qs)), prep, 64, q_block=5)
+    # the popcount path itself: query codes equal the oracle's encode
+    y = (torch.from_numpy(f16_to_f32(qs)) * prep["signs"]) @ prep["H"]
+    bits = (y >= 0).to(torch.int64).view(-1, 16, 8)
+    cq = (bits << torch.arange(8)).sum(-1).to(torch.uint8).numpy()
+    assert np.array_equal(cq, orq.encode(qs, signs)[0])
+    overlap = np.mean([len(set(a) & set(b)) / 64 for a, b in zip(cand.numpy(), cand_ref)])
+    assert overlap >= 0.98
+    ref_exact = orq.exact_scores(qs, keys, cand.numpy())
+    assert np.abs(exact.numpy() - ref_exact).max() <= 1e-5
+    # the 64-bit SWAR bit count against a byte table
+    w = torch.from_numpy(rng.integers(-2**63, 2**63 - 1, size=1000, dtype=np.int64))
+    table = np.array([bin(i).count("1") for i in range(256)])
+    ref_pc = table[w.numpy().view(np.uint8).reshape(-1, 8)].sum(-1)
+    assert np.array_equal(torch_cpu._popc64(w).numpy(), ref_pc)
