@@ -152,3 +152,22 @@ def test_in_launch_merge_graph_replays(monkeypatch):
             assert torch.equal(got.view(torch.int32), eager[1].view(torch.int32)), f"eager after replay {rep}"
         else:
             assert (got - eager[1]).abs().max().item() <= 1e-3
+
+
+@pytest.mark.parametrize("hq,kv,n_splits", [(16, 1, 12), (32, 8, 20), (8, 2, 9)])
+def test_in_launch_merge_many_splits(monkeypatch, hq, kv, n_splits):
+    """More than 8 splits (the merge's unbatched loop) and 16 query heads per
+    KV head: the in-launch merge equals the merge kernel bit for bit."""
+    from zoomkv_revision_amd import kivi, synthetic
+    dev = torch.device("cuda:0")
+    bs, ng, r = 2, 200, 70
+    cache = synthetic.c2_cache(41, bs, kv, ng, r, dev)
+    q = synthetic.c2_query(bs, hq, dev, seed=6)
+    ws = _garbage_workspace(kivi.lib().zkv_kivi4_attention_workspace_size(bs, hq, kv, ng, r, n_splits), 13)
+    print(f"[split merge] many splits hq={hq} kv={kv} n_splits={n_splits}", flush=True)
+    _, used = kivi.kivi4_attention_partial(q, cache, ng, r, n_splits=n_splits, workspace=ws)
+    assert used > 8
+    ref, got = _both(monkeypatch, lambda: kivi.kivi4_decode_attention(
+        q, cache, ng, r, out_dtype=torch.float32, n_splits=n_splits, workspace=ws))
+    assert np.isfinite(ref.cpu().numpy()).all()
+    assert np.array_equal(_bits(ref), _bits(got))
