@@ -681,23 +681,13 @@ __device__ __forceinline__ void merge_splits_last(const AttnParams& p, int64_t b
   }
   __syncthreads();
   if (!*s_last) return;
-  if (p.merge_fence) {
-    for (int idx = tid; idx < p.gqa * 128; idx += nthreads) {
-      const int cc = idx >> 7, d = idx & 127;
-      const int64_t row0 = bh * p.n_splits * p.gqa + cc;
-      float mmax, den;
-      const float r = combine_splits<false>(p.ws_o, p.ws_ml, row0, p.gqa, p.n_splits, d, mmax, den);
-      const int64_t qrow = bh * p.gqa + cc;
-      store_out(p, qrow, d, r);
-      if (p.lse != nullptr && d == 0) p.lse[qrow] = (mmax + __log2f(den)) * kLn2;
-    }
-    return;
-  }
   for (int idx = tid; idx < p.gqa * 128; idx += nthreads) {
     const int cc = idx >> 7, d = idx & 127;
     const int64_t row0 = bh * p.n_splits * p.gqa + cc;
     float mmax, den;
-    const float r = combine_splits<true>(p.ws_o, p.ws_ml, row0, p.gqa, p.n_splits, d, mmax, den);
+    // (fence variant: plain loads after the acquire above)
+    const float r = p.merge_fence ? combine_splits<false>(p.ws_o, p.ws_ml, row0, p.gqa, p.n_splits, d, mmax, den)
+                                  : combine_splits<true>(p.ws_o, p.ws_ml, row0, p.gqa, p.n_splits, d, mmax, den);
     const int64_t qrow = bh * p.gqa + cc;  // b*hq + h*gqa + cc
     store_out(p, qrow, d, r);
     if (p.lse != nullptr && d == 0) p.lse[qrow] = (mmax + __log2f(den)) * kLn2;
@@ -1286,7 +1276,8 @@ SplitPlan plan_splits(int bs, int kv, int n_groups, int res_len, int n_splits, S
 // stores and are read back with device-coherent loads; a device-scope fence
 // per workgroup (a whole-L2 writeback and invalidate on gfx950) cost more than
 // the separate merge kernel it replaced (C2 148 us instead of 129).
-// ZKV_SPLIT_MERGE=kernel keeps the separate merge kernel (for A/B timing).
+// ZKV_SPLIT_MERGE=kernel keeps the separate merge kernel (for A/B timing);
+// ZKV_SPLIT_MERGE=fence orders plain partial stores with agent-scope fences.
 size_t partial_bytes_for(int bs, int hq, int n_splits) {
   return static_cast<size_t>(bs) * hq * n_splits * (128 + 2) * sizeof(float);
 }
