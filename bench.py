@@ -708,8 +708,6 @@ def main():
     ws = kivi.attention_workspace(B, HQ, HKV, NG, R, args.splits, device=dev)
     torch.cuda.synchronize()
 
-    _, used = kivi.kivi4_attention_partial(q, caches[0], NG, R, n_splits=args.splits, workspace=ws)
-
     def step(i):
         # one launch: the context splits, merged by the workgroup that
         # completes each (sequence, KV head)
@@ -725,6 +723,7 @@ def main():
     t1 = time.perf_counter()
     ms_step = (t1 - t0) * 1e3 / args.steps
     k_ms = kernel_batch_ms(step, args.steps)
+    _, used = kivi.kivi4_attention_partial(q, caches[0], NG, R, n_splits=args.splits, workspace=ws)  # the plan
     achieved = ALGO_BYTES / (k_ms * 1e-3) / 1e9
 
     cpu = None if args.no_cpu else cpu_baseline(caches[0], q)
