@@ -48,6 +48,28 @@ def make_cache(seed: int, device):
     return synthetic.c2_cache(seed, B, HKV, NG, R, device)
 
 
+def hbm_reference(caches, q, rounds: int = 6) -> dict:
+    """GB/s of the C2 attention (algorithmic bytes) next to torch's device copy
+    (read + write) and torch.sum (read) over the same byte volume, two
+    alternating buffers each, in back-to-back batches of 20 launches."""
+    import torch
+    from zoomkv_revision_amd import kivi
+    dev = q.device
+    out = torch.empty(B, HQ, D, dtype=torch.bfloat16, device=dev)
+    ws = kivi.attention_workspace(B, HQ, HKV, NG, R, 0, device=dev)
+    srcs = [torch.ones(ALGO_BYTES // 4, dtype=torch.float32, device=dev) for _ in range(2)]
+    dst = torch.empty_like(srcs[0])
+    acc = torch.empty(1, dtype=torch.float32, device=dev)
+    runs = {"c2_attention": (lambda i: kivi.kivi4_decode_attention(q, caches[i % 2], NG, R, out=out, workspace=ws), 1),
+            "torch_copy_read_plus_write": (lambda i: dst.copy_(srcs[i % 2]), 2),
+            "torch_sum_read": (lambda i: torch.sum(srcs[i % 2], dim=0, keepdim=True, out=acc), 1)}
+    res = {k: [] for k in runs}
+    for _ in range(rounds):
+        for k, (fn, passes) in runs.items():
+            res[k].append(passes * ALGO_BYTES / (kernel_batch_ms(fn, 20) * 1e-3) / 1e9)
+    return {"bytes": ALGO_BYTES, "unit": "GB/s", **{k: statistics.median(v) for k, v in res.items()}}
+
+
 def cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
@@ -676,6 +698,9 @@ def main():
                     help="c5: skip the run with the retrieval zone in pinned host memory")
     ap.add_argument("--no-flush", action="store_true",
                     help="c5: skip stepping to the first flush (its timing)")
+    ap.add_argument("--hbm-reference", action="store_true",
+                    help="c2: only compare the attention's stream rate with torch's device copy and "
+                         "torch.sum over the same byte volume (medians of 6 interleaved rounds) and exit")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run 5 device copies of 1 GiB (scale reference for rocprof "
                          "FETCH_SIZE / WRITE_SIZE counters) and exit")
@@ -703,6 +728,9 @@ def main():
         return
     caches = [make_cache(1234 + i, dev) for i in range(2)]
     from zoomkv_revision_amd import synthetic
+    if args.hbm_reference:
+        print(json.dumps(hbm_reference(caches, synthetic.c2_query(B, HQ, dev))))
+        return
     q = synthetic.c2_query(B, HQ, dev)
     out = torch.empty(B, HQ, D, dtype=torch.bfloat16, device=dev)
     ws = kivi.attention_workspace(B, HQ, HKV, NG, R, args.splits, device=dev)
