@@ -171,3 +171,21 @@ def test_in_launch_merge_many_splits(monkeypatch, hq, kv, n_splits):
         q, cache, ng, r, out_dtype=torch.float32, n_splits=n_splits, workspace=ws))
     assert np.isfinite(ref.cpu().numpy()).all()
     assert np.array_equal(_bits(ref), _bits(got))
+
+
+def test_workspace_without_arrival_slots_is_rejected():
+    """A workspace sized for the split partials only (no arrival slots) is
+    too small for a merging launch: the call fails with ZKV_ESPACE and runs
+    nothing."""
+    from zoomkv_revision_amd import kivi, synthetic
+    from zoomkv_revision_amd._lib import ZkvError
+    dev = torch.device("cuda:0")
+    bs, hq, kv, ng, r = 2, 8, 2, 40, 32
+    cache = synthetic.c2_cache(51, bs, kv, ng, r, dev)
+    q = synthetic.c2_query(bs, hq, dev, seed=7)
+    need = kivi.lib().zkv_kivi4_attention_workspace_size(bs, hq, kv, ng, r, 4)
+    partials_only = bs * hq * 4 * (128 + 2) * 4
+    assert need == partials_only + bs * kv * 8
+    ws = torch.zeros(partials_only, dtype=torch.uint8, device=dev)
+    with pytest.raises(ZkvError, match="workspace"):
+        kivi.kivi4_decode_attention(q, cache, ng, r, n_splits=4, workspace=ws)
