@@ -458,6 +458,9 @@ def run_c3(args):
     k_ms = kernel_batch_ms(lambda i: quest_chunk_score_gqa(w0["q"], kv, ws[i % len(ws)]["page_min"],
                                                            ws[i % len(ws)]["page_max"], scores, n_pages,
                                                            None, raw_q), args.steps)
+    sa_ms = kernel_batch_ms(lambda i: kivi.kivi4_sparse_attention(ws[i % len(ws)]["q"], ws[i % len(ws)]["cache"],
+                                                                  ws[i % len(ws)]["planted"], out=out),
+                            args.steps, host_us=30)
     exact = all(torch.equal(s, ws[j]["planted"]) for j, s in enumerate(sel_ok[:len(ws)]))
     nb = synthetic.c3_algorithmic_bytes(bs, hq, kv, n_pages, n_sel)
     achieved = nb["quest"] / (k_ms * 1e-3) / 1e9
@@ -480,6 +483,10 @@ def run_c3(args):
                      "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel": "quest_gqa_kernel",
                      "kernel_ms": k_ms, "algorithmic_bytes": nb["quest"]},
         "algorithmic_bytes_per_step": nb,
+        # the longest kernel of the step: latency-bound (a wave's ~4 page
+        # tiles arrive together after the page walk), so below its HBM line
+        "sparse_attention": {"kernel_ms": sa_ms, "algorithmic_bytes": nb["sparse_attention"],
+                             "GBps": nb["sparse_attention"] / (sa_ms * 1e-3) / 1e9},
         "cpu_baseline": cpu,
     }
 
