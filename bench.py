@@ -202,18 +202,19 @@ def run_c1(args):
     out = torch.empty(1, 32, 128, dtype=torch.bfloat16, device=dev)
     ws = kivi.attention_workspace(1, 32, 8, ng, res, 0, device=dev)
 
-    # the fp16 range check (a host synchronisation) once, outside the timed steps
-    kivi.kivi4_pack(kd[:, :, :nq], vd[:, :, :nq], cache, 0, check_range=True)
+    # the range check records into a device word (no host synchronisation);
+    # it is read once, after the timed steps
+    kivi.kivi4_pack_status(dev)
 
     def step(i):
-        kivi.kivi4_pack(kd[:, :, :nq], vd[:, :, :nq], cache, 0, check_range=False)
+        kivi.kivi4_pack(kd[:, :, :nq], vd[:, :, :nq], cache, 0)
         cache.k_res[:, :, :res].copy_(kd[:, :, nq:])
         cache.v_res[:, :, :res].copy_(vd[:, :, nq:])
         kivi.kivi4_decode_attention(qd, cache, ng, res, out=out, workspace=ws)
 
     ms = timed_loop(step, args.steps, args.warmup)
-    k_ms = kernel_batch_ms(lambda i: kivi.kivi4_pack(kd[:, :, :nq], vd[:, :, :nq], cache, 0, check_range=False),
-                           args.steps)
+    k_ms = kernel_batch_ms(lambda i: kivi.kivi4_pack(kd[:, :, :nq], vd[:, :, :nq], cache, 0), args.steps)
+    kivi.check_kivi4_pack_range(dev)
     pack_bytes = 8 * nq * 512 + 8 * nq * 160          # bf16 K/V in, Format Q out
     attn_bytes = 8 * nq * 160 + 8 * res * 512 + 2 * 32 * 128 * 2
     cpu = None if args.no_cpu else c1_cpu_baseline(w)

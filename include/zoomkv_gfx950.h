@@ -108,11 +108,16 @@ int zkv_kivi4_pack(const uint16_t* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
  * k_res, v_res  bf16 [bs, kv, R_cap, 128] contiguous; tokens [0, res_len) used
  * n_groups groups of the Format Q cache are attended (all bs share lengths)
  * out      [bs, hq, 128] contiguous, bf16 (out_f32 == 0) or fp32 (out_f32 != 0)
+ * lse      optional (NULL to skip) fp32 [bs, hq]: natural-log LSE of the
+ *          scaled scores, the layout of flash-attn's softmax_lse
  * n_splits context splits per (b, kv head); 0 = automatic
  * workspace device scratch of zkv_kivi4_attention_workspace_size() bytes
  *          (split partials, then one 8-byte arrival slot per (b, kv) when
- *          the plan has more than one split); any initial contents, no
- *          zeroing needed; calls that overlap on one workspace race.
+ *          the plan has more than one split); no zeroing needed: each
+ *          launch's slot value (epoch << 8 | count) has bit 63 set and a
+ *          random per-process epoch base, so no non-negative int64 a reused
+ *          buffer holds can read as a live slot, and other bytes match with
+ *          probability 2^-55; calls that overlap on one workspace race.
  * With more than one split, the splits are merged inside the one launch by
  * the workgroup that completes each (b, kv) (same bits as the partial + merge
  * pair below); environment ZKV_SPLIT_MERGE=kernel selects a separate merge
@@ -125,7 +130,7 @@ int zkv_kivi4_decode_attention(const uint16_t* q, int64_t q_sb, int64_t q_sh,
                                const int32_t* groups, int g_cap,
                                const uint16_t* k_res, const uint16_t* v_res, int r_cap,
                                int bs, int hq, int kv, int n_groups, int res_len,
-                               float sm_scale, void* out, int out_f32, int n_splits,
+                               float sm_scale, void* out, int out_f32, float* lse, int n_splits,
                                void* workspace, size_t workspace_bytes, zkv_stream_t stream);
 
 /* zkv_kivi4_decode_attention without a workspace argument, allocating
@@ -142,8 +147,8 @@ int zkv_kivi4_decode_attention_noalloc(const uint16_t* q, int64_t q_sb, int64_t 
                                        const int32_t* groups, int g_cap,
                                        const uint16_t* k_res, const uint16_t* v_res, int r_cap,
                                        int bs, int hq, int kv, int n_groups, int res_len,
-                                       float sm_scale, void* out, int out_f32, int n_splits,
-                                       zkv_stream_t stream);
+                                       float sm_scale, void* out, int out_f32, float* lse,
+                                       int n_splits, zkv_stream_t stream);
 
 /* Stage 1 of zkv_kivi4_decode_attention: per context split, the unnormalised
  * partial output o, the running max m (log2 units, sm_scale*log2(e) folded in)
@@ -279,8 +284,8 @@ int zkv_kivi4_sparse_attention(const uint16_t* q, int64_t q_sb, int64_t q_sh, co
                                int g_cap, const uint16_t* k_res, const uint16_t* v_res, int r_cap,
                                int bs, int hq, int kv, int n_groups, int res_len, const int64_t* pages,
                                int64_t pg_sb, int64_t pg_sh, int n_sel, float sm_scale, void* out,
-                               int out_f32, int n_splits, void* workspace, size_t workspace_bytes,
-                               zkv_stream_t stream);
+                               int out_f32, float* lse, int n_splits, void* workspace,
+                               size_t workspace_bytes, zkv_stream_t stream);
 
 /* Decode attention over bf16 K / V caches k, v [bs, n, kv, 128] at element
  * strides (sb = batch, st = token, sh = head; rows 16-byte aligned), causal

@@ -315,11 +315,12 @@ def attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, sm_scale: float,
 
 
 def kivi4_decode_attention(q, cache: Kivi4Cache, n_groups: int, k_res, v_res,
-                           res_len: int, sm_scale: float, dtype=np.float64):
+                           res_len: int, sm_scale: float, dtype=np.float64, return_lse: bool = False):
     """Decode attention over the first ``n_groups`` groups of a Format Q cache
     plus ``res_len`` full-precision residual tokens.
 
     q [bs, Hq, 128] (bf16 values); k_res / v_res [bs, Hkv, >=res_len, 128].
+    With ``return_lse`` also the natural-log LSE [bs, Hq] of the scaled scores.
     """
     kh, vh = dequant_kivi4(Kivi4Cache(cache.k_codes[:, :, :n_groups],
                                       cache.k_meta[:, :, :n_groups],
@@ -327,16 +328,17 @@ def kivi4_decode_attention(q, cache: Kivi4Cache, n_groups: int, k_res, v_res,
                                       cache.v_meta[:, :, :n_groups]), dtype=dtype)
     k = np.concatenate([kh, k_res[:, :, :res_len].astype(dtype)], axis=2)
     v = np.concatenate([vh, v_res[:, :, :res_len].astype(dtype)], axis=2)
-    return attention(q, k, v, sm_scale, dtype=dtype)
+    return attention(q, k, v, sm_scale, dtype=dtype, return_lse=return_lse)
 
 
 def kivi4_sparse_attention(q, cache: Kivi4Cache, n_groups: int, k_res, v_res, res_len: int,
-                           pages: np.ndarray, sm_scale: float, dtype=np.float64):
+                           pages: np.ndarray, sm_scale: float, dtype=np.float64, return_lse: bool = False):
     """Attention over the gathered tokens of the listed 16-token pages (page P =
     tokens 16P .. 16P+15 of the quantized region; ids outside [0, 2 n_groups)
     skipped, repeats kept) plus the residual window: the reference's
     gather -> flash_attn_with_kvcache(causal=False) (S:1723-1772).
-    pages int [bs, Hkv, n_sel] -> out [bs, Hq, 128]."""
+    pages int [bs, Hkv, n_sel] -> out [bs, Hq, 128] (and with ``return_lse``
+    the natural-log LSE [bs, Hq]; -inf where nothing is attended)."""
     kh, vh = dequant_kivi4(Kivi4Cache(cache.k_codes[:, :, :n_groups],
                                       cache.k_meta[:, :, :n_groups],
                                       cache.v_codes[:, :, :n_groups],
@@ -345,6 +347,7 @@ def kivi4_sparse_attention(q, cache: Kivi4Cache, n_groups: int, k_res, v_res, re
     kv = kh.shape[1]
     gqa = hq // kv
     out = np.zeros((bs, hq, d), dtype=dtype)
+    lse = np.full((bs, hq), -np.inf, dtype=dtype)
     for b in range(bs):
         for h in range(kv):
             p = np.asarray(pages[b, h]).astype(np.int64)
@@ -354,9 +357,11 @@ def kivi4_sparse_attention(q, cache: Kivi4Cache, n_groups: int, k_res, v_res, re
             v = np.concatenate([vh[b, h, tok], v_res[b, h, :res_len].astype(dtype)], axis=0)
             if k.shape[0] == 0:
                 continue
-            out[b, h * gqa:(h + 1) * gqa] = attention(q[b:b + 1, h * gqa:(h + 1) * gqa], k[None, None],
-                                                      v[None, None], sm_scale, dtype=dtype)[0]
-    return out
+            o, l = attention(q[b:b + 1, h * gqa:(h + 1) * gqa], k[None, None], v[None, None], sm_scale,
+                             dtype=dtype, return_lse=True)
+            out[b, h * gqa:(h + 1) * gqa] = o[0]
+            lse[b, h * gqa:(h + 1) * gqa] = l[0]
+    return (out, lse) if return_lse else out
 
 
 def lse_merge(out_a, lse_a, out_b, lse_b, dtype=np.float64):

@@ -7,7 +7,10 @@ residual window, 1% outlier K channels x10 -- the bench's first cache (seed
   quantization of the same bf16 K / V;
 * the fused attention (fp32 output, the automatic split plan) is within the
   north star's 2e-3 of the float64 oracle over the cache's records, for 4 of
-  the 16 sequences and all 32 query heads;
+  the 16 sequences and all 32 query heads, and its natural-log LSE within
+  1e-5 relative (a 32-token tile dropped or counted twice moves the LSE by
+  ~1e-4 relative at this shape, which the 2e-3 output bound alone would not
+  see);
 * the automatic split plan and a single split agree within 1e-3 on all 16
   sequences (the splits differ only in fp16 rounding of P relative to each
   split's running max)."""
@@ -54,15 +57,32 @@ def test_c2_full_shape_pack_bit_exact(c2):
 def test_c2_full_shape_attention_matches_oracle(c2):
     from zoomkv_revision_amd import kivi
     cache, _, q = c2
-    out = from_torch(kivi.kivi4_decode_attention(q, cache, NG, R, out_dtype=torch.float32))
+    out, lse = kivi.kivi4_decode_attention(q, cache, NG, R, out_dtype=torch.float32, return_lse=True)
+    out, lse = from_torch(out), from_torch(lse)
     qn = q.float().cpu().numpy()
     kr, vr = cache.k_res.float().cpu().numpy(), cache.v_res.float().cpu().numpy()
     for b in ROWS:
-        ref = okivi.kivi4_decode_attention(qn[b:b + 1], _oracle_cache(cache, b), NG, kr[b:b + 1], vr[b:b + 1], R,
-                                           1 / np.sqrt(128))
+        ref, ref_lse = okivi.kivi4_decode_attention(qn[b:b + 1], _oracle_cache(cache, b), NG, kr[b:b + 1],
+                                                    vr[b:b + 1], R, 1 / np.sqrt(128), return_lse=True)
         err = np.abs(out[b:b + 1] - ref).max()
-        print(f"[c2 full] sequence {b}: max abs err {err:.3e}", flush=True)
+        lerr = np.abs(lse[b:b + 1] / ref_lse - 1).max()
+        print(f"[c2 full] sequence {b}: max abs err {err:.3e}, LSE rel err {lerr:.3e}", flush=True)
         assert err <= 2e-3, f"sequence {b}: max abs err {err}"
+        assert lerr <= 1e-5, f"sequence {b}: LSE rel err {lerr}"
+
+
+def test_c2_lse_sees_one_dropped_tile(c2):
+    """The LSE bound can see a lost tile: on the oracle side (a planted
+    mistake), dropping the first 32-token group of sequence 0 moves the
+    float64 LSE by more than 3x the 1e-5 tolerance for every query head."""
+    cache, _, q = c2
+    qn = q.float().cpu().numpy()[0:1]
+    kr, vr = cache.k_res.float().cpu().numpy()[0:1], cache.v_res.float().cpu().numpy()[0:1]
+    rec = _oracle_cache(cache, 0)
+    _, full = okivi.kivi4_decode_attention(qn, rec, NG, kr, vr, R, 1 / np.sqrt(128), return_lse=True)
+    drop = okivi.Kivi4Cache(*(getattr(rec, n)[:, :, 1:] for n in ("k_codes", "k_meta", "v_codes", "v_meta")))
+    _, short = okivi.kivi4_decode_attention(qn, drop, NG - 1, kr, vr, R, 1 / np.sqrt(128), return_lse=True)
+    assert (np.abs(short / full - 1) > 3e-5).all()
 
 
 def test_c2_full_shape_split_plans_agree(c2):

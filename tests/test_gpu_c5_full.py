@@ -15,7 +15,12 @@ For the first and the last layer:
   attention over sink + local + the selected rows;
 and the whole fused layer (QKV with the RMSNorm, q / k norm + RoPE, the
 attention, o-projection, MLP) matches the torch ops of the reference's
-layer_decode on the same input and attention output."""
+layer_decode on the same input and attention output.
+
+The last test then decodes on to the first flush (512 tokens past the
+prompt's local window): the flushed rows are the local tokens they were, the
+32 newly encoded chunks' metadata equals the oracle's encode of them, and the
+flush step's selection and attention match the oracle as above."""
 import numpy as np
 import pytest
 import torch
@@ -29,6 +34,7 @@ pytestmark = pytest.mark.gpu
 
 LAYERS = (0, 35)
 BATCH, CONTEXT, INTERVAL, THRESHOLD = 4, 65536, 512, 2048
+MAX_NEW = INTERVAL + 8          # room for the decode steps up to the first flush
 
 
 @pytest.fixture(scope="module")
@@ -41,7 +47,7 @@ def c5(request):
     geo = ds.Qwen3Geometry()
     dev = torch.device("cuda:0")
     model = ds.RandomQwen3(geo, dev, seed=42)
-    cache = ds.build_cache(geo, BATCH, CONTEXT, 16, INTERVAL, THRESHOLD, dev)
+    cache = ds.build_cache(geo, BATCH, CONTEXT, MAX_NEW, INTERVAL, THRESHOLD, dev)
     ds.fill_cache(cache, geo, BATCH, CONTEXT, 43, dev)
     rec = {l: {} for l in LAYERS}
     compute, layer = cache.compute, model.layer_decode
@@ -81,13 +87,24 @@ def test_c5_metadata_and_selection_match_oracle(c5, layer):
     chunk = cache.quest_chunk_size
     n_chunks, nk = cache._cached_quest_n_chunks, cache._cached_quest_nk
     assert (L, chunk, n_chunks, nk) == (CONTEXT - 64 - 256, 16, (CONTEXT - 320) // 16, 1631)
+    _check_selection_and_attention(cache, rec, layer, (0, n_chunks - 64))
+
+
+def _check_selection_and_attention(cache, rec, layer, chunk_starts):
+    """Format R metadata of 64 chunks from each of ``chunk_starts`` against the
+    oracle's encode of the stored keys, the recorded selection against the
+    oracle's, and the recorded attention output against float64 attention
+    over sink + local + the selected rows."""
+    L = int(cache.cpu_valid_end[layer])
+    chunk = cache.quest_chunk_size
+    n_chunks, nk = cache._cached_quest_n_chunks, cache._cached_quest_nk
     mn = _np(cache._chunk_key_min_gpu[layer])
     mx = _np(cache._chunk_key_max_gpu[layer])
     mean = _np(cache._chunk_key_centroid_gpu[layer])
     valid = _np(cache._chunk_valid_mask_gpu[layer]).astype(bool)
     packed = _np(cache.key_kivi_packed_gpu[layer])
     assert valid[:, :, :n_chunks].all() and not valid[:, :, n_chunks:].any()
-    for c0 in (0, n_chunks - 64):
+    for c0 in chunk_starts:
         keys = _np(cache.unified_keys[layer][:, :, c0 * chunk:(c0 + 64) * chunk])
         rmn, rmx, rmean, rpk = encode_chunks_ref(keys, chunk)
         sl = slice(c0, c0 + 64)
@@ -150,3 +167,46 @@ def test_c5_fused_layer_matches_torch_ops(c5, layer):
     gate, up = F.linear(x2, W["gate_up"]).chunk(2, dim=-1)
     h_ref = hidden + F.linear(F.silu(gate) * up, W["down"])
     close(rec["h_out"], h_ref, 8.0)
+
+
+def test_c5_first_flush_matches_oracle(c5):
+    """Runs last (it moves the cache on): decode until the step whose layer 0
+    flushes the oldest 512 local tokens into the retrieval zone.  Then, for
+    the first and last layer, the 512 new retrieval rows are bit-identical to
+    the local rows they came from, the 32 new chunks' Format R metadata
+    equals the oracle's encode of them, the stage-1 sizes follow the new
+    retrieval length, and the flush step's selection and attention match the
+    oracle (as at the prompt's end)."""
+    cache, model, rec = c5["cache"], c5["model"], c5["rec"]
+    L0 = int(cache.cpu_valid_end[0])
+    s, n0 = cache.sink_size, cache._near0
+    oldest = slice(n0 + s, n0 + s + INTERVAL)
+    tok = c5["logits"].argmax(dim=-1)
+    moved, steps = None, 0
+    while int(cache.cpu_valid_end[0]) == L0:
+        near_len = cache.current_seq_len[0] - s - L0
+        if near_len >= cache.local_size + INTERVAL:          # this step's layer 0 flushes
+            moved = {l: (cache.unified_keys[l][:, :, oldest].clone(), cache.unified_values[l][:, :, oldest].clone())
+                     for l in LAYERS}
+        tok = model.decode_step(tok, cache).argmax(dim=-1)
+        steps += 1
+        assert steps <= INTERVAL + 1, "no flush"
+    torch.cuda.synchronize()
+    print(f"[c5 flush] flushed after {steps} more decode steps", flush=True)
+    L1 = L0 + INTERVAL
+    assert moved is not None and all(int(e) == L1 for e in cache.cpu_valid_end)
+    chunk = cache.quest_chunk_size
+    assert cache._cached_quest_n_chunks == L1 // chunk
+    # nk of S:1798-1825 at the new length (dynamic ratio 0.4 above 10001 tokens)
+    assert cache._cached_quest_nk == min(L1 // chunk, -(-int(np.ceil(L1 * 0.4)) // chunk))
+    for layer in LAYERS:
+        k_old, v_old = moved[layer]
+        assert torch.equal(cache.unified_keys[layer][:, :, L0:L1], k_old)
+        assert torch.equal(cache.unified_values[layer][:, :, L0:L1], v_old)
+        rmn, rmx, rmean, rpk = encode_chunks_ref(_np(k_old), chunk)
+        new = slice(L0 // chunk, L1 // chunk)
+        assert np.array_equal(_np(cache._chunk_key_min_gpu[layer])[:, :, new], rmn)
+        assert np.array_equal(_np(cache._chunk_key_max_gpu[layer])[:, :, new], rmx)
+        assert np.array_equal(_np(cache._chunk_key_centroid_gpu[layer])[:, :, new], rmean)
+        assert np.array_equal(_np(cache.key_kivi_packed_gpu[layer])[:, :, new], rpk)
+        _check_selection_and_attention(cache, rec[layer], layer, (0, L0 // chunk - 32))

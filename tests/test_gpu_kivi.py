@@ -223,8 +223,9 @@ def test_c1_full_shape_pack_and_attention():
 def test_kivi4_pack_reports_values_beyond_the_fp16_format(rng):
     """Format Q stores each group's scale and zero point (its minimum) in
     fp16: a minimum below -65504 or a V scale above the decode kernel's 2048
-    (16 * P * scale must stay inside fp16) makes the pack raise instead of
-    storing inf, which the attention would turn into NaN.  A maximum above
+    (16 * P * scale must stay inside fp16) is recorded in the device's status
+    word, without a host synchronisation, and the next range check raises
+    instead of the attention turning the stored inf into NaN.  A maximum above
     65504 is fine: only min and (max - min) / 15 are stored, and the
     attention then matches the oracle."""
     zk = _zk()
@@ -241,12 +242,20 @@ def test_kivi4_pack_reports_values_beyond_the_fp16_format(rng):
             v[0, 0, 40, 70] = -7.0e4
         else:                                    # range 40000 inside one 32-channel group
             v[0, 1, 40, 64:96] = np.linspace(-2.0e4, 2.0e4, 32, dtype=np.float32)
+        zk.kivi4_pack(to_bf16(k), to_bf16(v), cache, 0)     # records, does not synchronise
         with pytest.raises(RuntimeError, match=msg):
-            zk.kivi4_pack(to_bf16(k), to_bf16(v), cache, 0)
+            zk.check_kivi4_pack_range()
+        zk.check_kivi4_pack_range()                          # the check cleared the status
+    zk.kivi4_pack(to_bf16(k0), to_bf16(v0), cache, 0, check_range=False)
+    k = k0.copy()
+    k[0, 1, 50, 7] = -7.0e4
+    zk.kivi4_pack(to_bf16(k), to_bf16(v0), cache, 0, check_range=False)
+    assert zk.kivi4_pack_status() == 0                      # unchecked packs record nothing
     from oracle.numerics import bf16r
     k = k0.copy()
     k[0, 1, 50, 7] = bf16r(np.float32(7.0e4))   # a maximum beyond fp16: representable
     assert zk.kivi4_pack(to_bf16(k), to_bf16(v0), cache, 0) == ng
+    zk.check_kivi4_pack_range()
     ref_cache = okivi.quantize_kivi4(k, v0)
     assert np.array_equal(from_torch(cache.k_meta), ref_cache.k_meta)
     q = gaussian_bf16(rng, (bs, hq, 128))

@@ -266,9 +266,65 @@ def test_streamed_rerank_across_shapes_and_repeats(rng):
             for h in range(kv):
                 want = r4.rerank_scores(cand[b, h], packed[b, h], w[b, h], qb[b, h], qn[b, h, 0])
                 assert np.array_equal(_bits(streamed)[b, h], bf16_bits(want)), (bs, kv, L, C, b, h)
-        ws, shape = zk._WS[torch.device("cuda", torch.cuda.current_device())]
+        ws, shape = zk._WS[_ws_key()]
         assert shape == (bs, kv, L)
         assert int(ws[:zk._flag_bytes(bs, kv, L)].count_nonzero()) == 0, (bs, kv, L, C)
+
+
+def _ws_key():
+    dev = torch.device("cuda", torch.cuda.current_device())
+    return dev, torch.cuda.current_stream(dev).cuda_stream
+
+
+def test_streamed_rerank_ignores_stale_flag_bytes(rng):
+    """Flag bytes other than 0 / 1 (a workspace that was not left zero, e.g.
+    by another user of the buffer) and set flags past kv_len only cost extra
+    work: the scores still equal the direct path's, and the call leaves the
+    flags zero."""
+    zk = _zk()
+    _, ctr = _levels(zk)
+    bs, kv, L, C = 2, 2, 1000, 400                     # kv_len not a whole window
+    packed, w, pt, wt = _random_cache(rng, bs, kv, L)
+    qb = bf16r(rng.standard_normal((bs, kv, 16, 8)).astype(np.float32))
+    qn = bf16r(np.abs(rng.standard_normal((bs, kv, 1))).astype(np.float32) + 0.1)
+    ct = torch.from_numpy(rng.integers(0, L, (bs, kv, C)).astype(np.int64)).cuda()
+    direct, _ = zk.partial_rerank_cuda(ct, pt, wt, _bf16(qb), _bf16(qn), ctr, 16, 8)
+    zk.partial_rerank_scores_cuda(ct, pt, wt, _bf16(qb), _bf16(qn), ctr, 16, 8)   # creates the workspace
+    ws, _ = zk._WS[_ws_key()]
+    for fill in (0xFF, 0x02, 0x01):
+        ws[:zk._flag_bytes(bs, kv, L)].fill_(fill)
+        streamed = zk.partial_rerank_scores_cuda(ct, pt, wt, _bf16(qb), _bf16(qn), ctr, 16, 8)
+        torch.cuda.synchronize()
+        assert np.array_equal(_bits(streamed), _bits(direct)), fill
+        assert int(ws[:zk._flag_bytes(bs, kv, L)].count_nonzero()) == 0, fill
+
+
+def test_streamed_rerank_on_two_streams(rng):
+    """Reranks issued on two streams use one workspace each, so calls that
+    overlap on the device do not share token flags or scores."""
+    zk = _zk()
+    _, ctr = _levels(zk)
+    bs, kv, L, C = 1, 2, 2048, 600
+    cases = []
+    for _ in range(2):
+        packed, w, pt, wt = _random_cache(rng, bs, kv, L)
+        qb = _bf16(bf16r(rng.standard_normal((bs, kv, 16, 8)).astype(np.float32)))
+        qn = _bf16(bf16r(np.abs(rng.standard_normal((bs, kv, 1))).astype(np.float32) + 0.1))
+        ct = torch.from_numpy(rng.integers(0, L, (bs, kv, C)).astype(np.int64)).cuda()
+        direct, _ = zk.partial_rerank_cuda(ct, pt, wt, qb, qn, ctr, 16, 8)
+        cases.append((ct, pt, wt, qb, qn, direct))
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    outs = [[], []]
+    for rep in range(20):
+        for i, st in enumerate(streams):
+            ct, pt, wt, qb, qn, _ = cases[i]
+            with torch.cuda.stream(st):
+                outs[i].append(zk.partial_rerank_scores_cuda(ct, pt, wt, qb, qn, ctr, 16, 8))
+    torch.cuda.synchronize()
+    for i in range(2):
+        for rep, o in enumerate(outs[i]):
+            assert np.array_equal(_bits(o), _bits(cases[i][5])), (i, rep)
 
 
 def test_rerank_empty_candidates_and_empty_cache(rng):

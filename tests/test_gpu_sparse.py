@@ -199,3 +199,38 @@ def test_sparse_attention_zero_pages_is_residual_only(rng):
     got = from_torch(kivi.kivi4_sparse_attention(to_bf16(q), cache, empty, 6, 40, out_dtype=torch.float32))
     ref = okivi.kivi4_sparse_attention(q, ref_cache, 6, kr, vr, 40, np.zeros((1, 2, 0), int), 1 / np.sqrt(128))
     assert np.abs(got - ref).max() <= ATOL
+
+
+def _oracle_records(cache, b):
+    """The GPU cache's Format Q records of sequence b as the oracle's arrays."""
+    f16 = lambda t: t.cpu().view(torch.int16).numpy().view(np.uint16)
+    return okivi.Kivi4Cache(cache.k_codes[b:b + 1].cpu().numpy(), f16(cache.k_meta[b:b + 1]),
+                            cache.v_codes[b:b + 1].cpu().numpy(), f16(cache.v_meta[b:b + 1]))
+
+
+def test_c3_full_shape_sparse_attention_matches_oracle():
+    """BASELINE config 3 at its own shape (batch 8, 32 / 8 heads, 32768 tokens,
+    the 128 planted pages of each (b, kv)), with the bench's automatic plan:
+    4 context splits merged inside the launch.  Outputs of sequences 0 and 7
+    (all 32 query heads) within 2e-3 of the float64 oracle over the cache's
+    records, and their natural-log LSEs within 1e-5 relative (a dropped or
+    repeated tile moves the LSE by ~1e-4 relative here)."""
+    from zoomkv_revision_amd import kivi, synthetic
+    bs, hq, kv, n_tok, n_sel = 8, 32, 8, 32768, 128
+    w = synthetic.c3_workload(42, bs, hq, kv, n_tok, n_sel, "cuda")
+    need = kivi.lib().zkv_kivi4_sparse_attention_workspace_size(bs, hq, kv, n_sel, 0, 0)
+    splits = (need - bs * kv * 8) // (bs * hq * 130 * 4)
+    assert splits == 4 and need == bs * hq * splits * 130 * 4 + bs * kv * 8
+    out, lse = kivi.kivi4_sparse_attention(w["q"], w["cache"], w["planted"], out_dtype=torch.float32,
+                                           return_lse=True)
+    out, lse = from_torch(out), from_torch(lse)
+    qn, pages = from_torch(w["q"]), from_torch(w["planted"])
+    z = np.zeros((1, kv, 0, 128), np.float32)
+    for b in (0, 7):
+        ref, ref_lse = okivi.kivi4_sparse_attention(qn[b:b + 1], _oracle_records(w["cache"], b), n_tok // 32, z, z,
+                                                    0, pages[b:b + 1], 1 / np.sqrt(128), return_lse=True)
+        err = np.abs(out[b:b + 1] - ref).max()
+        lerr = np.abs(lse[b:b + 1] / ref_lse - 1).max()
+        print(f"[c3 full] sequence {b}: max abs err {err:.3e}, LSE rel err {lerr:.3e}", flush=True)
+        assert err <= ATOL, f"sequence {b}: max abs err {err}"
+        assert lerr <= 1e-5, f"sequence {b}: LSE rel err {lerr}"

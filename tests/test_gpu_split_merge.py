@@ -189,3 +189,37 @@ def test_workspace_without_arrival_slots_is_rejected():
     ws = torch.zeros(partials_only, dtype=torch.uint8, device=dev)
     with pytest.raises(ZkvError, match="workspace"):
         kivi.kivi4_decode_attention(q, cache, ng, r, n_splits=4, workspace=ws)
+
+
+def test_in_launch_merge_ignores_small_integer_slots(monkeypatch):
+    """A reused workspace whose arrival slots hold small int64 values of the
+    form (k << 8) | c (token indices, counts: what an allocator hands back
+    after other ops) must never read as a live launch's slot.  Epochs carry
+    bit 55 and a random per-process base, so with k over a wide range and
+    every count c below the split count, a few hundred launches all equal the
+    separate merge kernel bit for bit."""
+    from zoomkv_revision_amd import kivi, synthetic
+    dev = torch.device("cuda:0")
+    bs, hq, kv, ng, r, n_splits = 3, 8, 2, 40, 50, 4
+    cache = synthetic.c2_cache(61, bs, kv, ng, r, dev)
+    q = synthetic.c2_query(bs, hq, dev, seed=9)
+    need = kivi.lib().zkv_kivi4_attention_workspace_size(bs, hq, kv, ng, r, n_splits)
+    slot0 = need - bs * kv * 8
+    ws = torch.zeros(need, dtype=torch.uint8, device=dev)
+    slots = ws[slot0:].view(torch.int64)
+    monkeypatch.setenv("ZKV_SPLIT_MERGE", "kernel")
+    ref = kivi.kivi4_decode_attention(q, cache, ng, r, out_dtype=torch.float32, n_splits=n_splits,
+                                      workspace=ws).clone()
+    monkeypatch.delenv("ZKV_SPLIT_MERGE")
+    out = torch.empty_like(ref)
+    n_slots = bs * kv
+    print(f"[split merge] small-integer slots: 300 launches, {n_slots} slots", flush=True)
+    for rep in range(300):
+        k = torch.arange(rep * n_slots, (rep + 1) * n_slots, dtype=torch.int64, device=dev)
+        slots.copy_((k << 8) | (k % n_splits))
+        out.zero_()
+        kivi.kivi4_decode_attention(q, cache, ng, r, out=out, out_dtype=torch.float32, n_splits=n_splits,
+                                    workspace=ws)
+        if rep % 50 == 49:
+            torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int32), ref.view(torch.int32)), f"launch {rep}"

@@ -30,7 +30,7 @@ def _case(rng, bs, hq, kv, ng, res):
 def _args(q, cache, ng, res, hq, kv, out):
     return (q.data_ptr(), q.stride(0), q.stride(1), cache.groups.data_ptr(), cache.g_cap,
             cache.k_res.data_ptr(), cache.v_res.data_ptr(), cache.r_cap, q.shape[0], hq, kv, ng, res,
-            1.0 / np.sqrt(128), out.data_ptr(), 1)
+            1.0 / np.sqrt(128), out.data_ptr(), 1, None)
 
 
 def test_noalloc_attention_equals_workspace_attention_twice(rng):

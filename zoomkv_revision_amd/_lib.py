@@ -32,10 +32,10 @@ SIGNATURES = {
                              P, P, P]),
     "zkv_kivi4_attention_workspace_size": (SZ, [I32, I32, I32, I32, I32, I32]),
     "zkv_kivi4_decode_attention": (I32, [P, I64, I64, P, I32, P, P, I32,
-                                         I32, I32, I32, I32, I32, F32, P, I32, I32,
+                                         I32, I32, I32, I32, I32, F32, P, I32, P, I32,
                                          P, SZ, P]),
     "zkv_kivi4_decode_attention_noalloc": (I32, [P, I64, I64, P, I32, P, P, I32,
-                                                 I32, I32, I32, I32, I32, F32, P, I32, I32, P]),
+                                                 I32, I32, I32, I32, I32, F32, P, I32, P, I32, P]),
     "zkv_kivi4_attention_partial": (I32, [P, I64, I64, P, I32, P, P, I32,
                                           I32, I32, I32, I32, I32, F32, I32, P, SZ, P, P]),
     "zkv_attention_merge": (I32, [P, I32, I32, I32, I32, P, I32, P]),
@@ -53,7 +53,7 @@ SIGNATURES = {
     "zkv_page_minmax_f16": (I32, [P, I64, I64, I64, I32, I32, I32, I32, I32, P, P, P]),
     "zkv_kivi4_sparse_attention_workspace_size": (SZ, [I32, I32, I32, I32, I32, I32]),
     "zkv_kivi4_sparse_attention": (I32, [P, I64, I64, P, I32, P, P, I32, I32, I32, I32, I32,
-                                         I32, P, I64, I64, I32, F32, P, I32, I32, P, SZ, P]),
+                                         I32, P, I64, I64, I32, F32, P, I32, P, I32, P, SZ, P]),
     "zkv_bf16_attention_workspace_size": (SZ, [I32, I32, I32, I32, I32]),
     "zkv_bf16_decode_attention": (I32, [P, I64, I64, P, I64, I64, I64, P, I64, I64, I64, I32, I32, I32, I32,
                                         F32, P, I32, P, I32, P, SZ, P]),

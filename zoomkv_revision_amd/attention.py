@@ -27,7 +27,7 @@ def _workspace(device, nbytes: int) -> torch.Tensor:
     key = torch.device(device)
     ws = _WS.get(key)
     if ws is None or ws.numel() < nbytes:
-        ws = torch.empty(max(nbytes, 1 << 16), dtype=torch.uint8, device=key)
+        ws = torch.zeros(max(nbytes, 1 << 16), dtype=torch.uint8, device=key)
         _WS[key] = ws
     return ws
 

@@ -10,9 +10,12 @@
 // exactly once for all `gqa` query heads of its KV head:
 //
 //  * a workgroup of NW wave64s owns one (context split, kv head, batch); wave
-//    w walks tiles T0 + w, T0 + w + NW, ... through its own D-stage LDS ring
-//    filled by global_load_lds_dwordx4, so D-1 tiles per wave are in flight
-//    without costing VGPRs;
+//    w walks tiles T0 + w, T0 + w + NW, ...  In the dense kernels a lane
+//    loads its 4 x 16 B of a tile's code words straight into a D-slot
+//    register ring and only the tile's metadata KiB goes through a D-stage
+//    LDS ring (global_load_lds_dwordx4); the page-sparse and bf16-only
+//    kernels stream whole 5 KiB records through the LDS ring.  D-1 tiles per
+//    wave are in flight;
 //  * nibbles enter the matrix cores undequantized: one v_and_b32 per pair
 //    turns them into exact fp16 subnormals (n * 2^-24 for the low nibble of a
 //    byte, 16n * 2^-24 for the high one) and the scales move to the B operand:
@@ -33,10 +36,13 @@
 //    the exponent's fma, so scores are not rounded to fp16; the O rescale is
 //    skipped when no running max moved;
 //  * the NW waves merge through LDS; with one split per KV head the kernel
-//    writes the output, otherwise a second small kernel merges the splits
-//    (a kernel boundary is the cheap cross-XCD fence: a device-scope
-//    __threadfence is an L2 writeback + invalidate on this part), both with
-//    the LSE rule of lse_merge_torch (Z/cache_hub/lse_merge/lse_merge.py:79-119).
+//    writes the output, otherwise the splits merge inside the same launch:
+//    each workgroup stores its partial with device-coherent (write-through)
+//    stores and counts itself in on a per-(b, kv) arrival slot, and the
+//    workgroup that completes the count merges every split's partial
+//    (merge_splits_last), with the LSE rule of lse_merge_torch
+//    (Z/cache_hub/lse_merge/lse_merge.py:79-119).  A separate merge kernel
+//    (kivi4_combine_kernel) gives the same bits.
 //
 // MFMA 16x16x32 operand layout (lane l, c = l % 16, g = l / 16):
 //   A: row c, k-slice g (8 halves);  B: k-slice g, column c;
@@ -58,9 +64,11 @@
 
 #include <algorithm>
 #include <atomic>
+#include <chrono>
 #include <cstring>
 #include <cstdlib>
 #include <mutex>
+#include <random>
 
 namespace zkv {
 namespace {
@@ -1297,11 +1305,25 @@ bool merge_with_fence() {
   return e && strcmp(e, "fence") == 0;
 }
 
-// Epoch of a merging launch: distinct for every launch of the process (56
-// bits: never wraps), never 0.
+// Epoch of a merging launch (56 bits): bit 55 set, the low 55 bits a random
+// per-process base plus a launch counter, so distinct for every launch of the
+// process.  A slot is (epoch << 8) | count, whose bit 63 is therefore set: no
+// non-negative int64 a reused workspace may hold (a token index, a count, a
+// small integer of the form (e << 8) | c) can read as a slot of a live
+// launch, and another process's slots or arbitrary bytes match a given
+// launch's epoch with probability 2^-55.
 unsigned long long next_epoch() {
+  static const unsigned long long base = [] {
+    std::random_device rd;
+    const unsigned long long hi = rd(), lo = rd();
+    const unsigned long long t = static_cast<unsigned long long>(
+        std::chrono::steady_clock::now().time_since_epoch().count());
+    return (hi << 32) ^ lo ^ (t * 0x9E3779B97F4A7C15ull);
+  }();
   static std::atomic<unsigned long long> counter{0};
-  return (counter.fetch_add(1, std::memory_order_relaxed) + 1) & ((1ull << 56) - 1);
+  constexpr unsigned long long kLow55 = (1ull << 55) - 1;
+  const unsigned long long n = counter.fetch_add(1, std::memory_order_relaxed) + 1;
+  return ((base + n) & kLow55) | (1ull << 55);
 }
 
 void launch_attn(const AttnParams& p, int bs, hipStream_t s) {
@@ -1503,14 +1525,14 @@ extern "C" int zkv_kivi4_decode_attention(const uint16_t* q, int64_t q_sb, int64
                                           const int32_t* groups, int g_cap,
                                           const uint16_t* k_res, const uint16_t* v_res, int r_cap,
                                           int bs, int hq, int kv, int n_groups, int res_len,
-                                          float sm_scale, void* out, int out_f32, int n_splits,
-                                          void* workspace, size_t workspace_bytes,
+                                          float sm_scale, void* out, int out_f32, float* lse,
+                                          int n_splits, void* workspace, size_t workspace_bytes,
                                           zkv_stream_t stream) {
   ZKV_REQUIRE(out, "zkv_kivi4_decode_attention: null output");
   return attention_launch(q, q_sb, q_sh, groups, g_cap, k_res, v_res,
                           r_cap, bs, hq, kv, n_groups, res_len, sm_scale, n_splits, workspace,
                           workspace_bytes, nullptr, out, out_f32,
-                          reinterpret_cast<hipStream_t>(stream));
+                          reinterpret_cast<hipStream_t>(stream), nullptr, nullptr, lse);
 }
 
 // ---- allocation-free variant ----------------------------------------------
@@ -1561,8 +1583,8 @@ extern "C" int zkv_kivi4_decode_attention_noalloc(const uint16_t* q, int64_t q_s
                                                   const int32_t* groups, int g_cap,
                                                   const uint16_t* k_res, const uint16_t* v_res, int r_cap,
                                                   int bs, int hq, int kv, int n_groups, int res_len,
-                                                  float sm_scale, void* out, int out_f32, int n_splits,
-                                                  zkv_stream_t stream) {
+                                                  float sm_scale, void* out, int out_f32, float* lse,
+                                                  int n_splits, zkv_stream_t stream) {
   ZKV_REQUIRE(out, "zkv_kivi4_decode_attention_noalloc: null output");
   ZKV_REQUIRE(bs > 0 && kv > 0 && hq > 0 && hq % kv == 0,
               "zkv_kivi4_decode_attention_noalloc: bad heads bs=%d hq=%d kv=%d", bs, hq, kv);
@@ -1578,7 +1600,7 @@ extern "C" int zkv_kivi4_decode_attention_noalloc(const uint16_t* q, int64_t q_s
   if (ws == nullptr) return ZKV_ELAUNCH;
   return attention_launch(q, q_sb, q_sh, groups, g_cap, k_res, v_res, r_cap, bs, hq, kv, n_groups, res_len,
                           sm_scale, n_splits, ws, kNoAllocScratchBytes, nullptr, out, out_f32,
-                          reinterpret_cast<hipStream_t>(stream));
+                          reinterpret_cast<hipStream_t>(stream), nullptr, nullptr, lse);
 }
 
 // ---- page-sparse mode -----------------------------------------------------
@@ -1596,14 +1618,14 @@ extern "C" int zkv_kivi4_sparse_attention(const uint16_t* q, int64_t q_sb, int64
                                           int bs, int hq, int kv, int n_groups, int res_len,
                                           const int64_t* pages, int64_t pg_sb, int64_t pg_sh,
                                           int n_sel, float sm_scale, void* out, int out_f32,
-                                          int n_splits, void* workspace, size_t workspace_bytes,
-                                          zkv_stream_t stream) {
+                                          float* lse, int n_splits, void* workspace,
+                                          size_t workspace_bytes, zkv_stream_t stream) {
   ZKV_REQUIRE(out, "zkv_kivi4_sparse_attention: null output");
   const SparsePages sp{pages, pg_sb, pg_sh, n_sel};
   return attention_launch(q, q_sb, q_sh, groups, g_cap, k_res, v_res,
                           r_cap, bs, hq, kv, n_groups, res_len, sm_scale, n_splits, workspace,
                           workspace_bytes, nullptr, out, out_f32,
-                          reinterpret_cast<hipStream_t>(stream), &sp);
+                          reinterpret_cast<hipStream_t>(stream), &sp, nullptr, lse);
 }
 
 // ---- bf16 K/V decode attention (flash_attn_with_kvcache counterpart) ------

@@ -320,7 +320,14 @@ __global__ __launch_bounds__(kStreamThreads) void rabitq4_stream_kernel(const Re
   uint32_t* fw = reinterpret_cast<uint32_t*>(flags + bh * frow + t0) + tid;
   const uint32_t f = *fw;
   build_products(prod, p.q_blocks + bh * kDim, p.centers);
-  const int cnt = __popc(f);
+  // the tokens to score: flag bit 0 set and inside the row (a flag byte
+  // other than 0 / 1, or one past kv_len, costs at most extra work and is
+  // never counted without a list entry)
+  uint32_t sel = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    sel |= (((f >> (8 * j)) & 1u) && t0 + 4 * tid + j < p.kv_len) ? 1u << j : 0u;
+  const int cnt = __popc(sel);
   int inc = cnt;
 #pragma unroll
   for (int d = 1; d < 64; d <<= 1) {  // inclusive scan over the wave
@@ -338,7 +345,7 @@ __global__ __launch_bounds__(kStreamThreads) void rabitq4_stream_kernel(const Re
   }
 #pragma unroll
   for (int j = 0; j < 4; ++j)
-    if ((f >> (8 * j)) & 1u) list[off++] = 4 * tid + j;
+    if ((sel >> j) & 1u) list[off++] = 4 * tid + j;
   __syncthreads();
   const float qn = bf16_to_f32(p.q_norm[bh]);
   for (int i = tid; i < n; i += kStreamThreads) {

@@ -139,9 +139,14 @@ class Kivi4Cache:
 
 _RANGE_STATUS: dict = {}
 RANGE_K, RANGE_V, RANGE_V_SCALE = 1, 2, 4   # ZKV_RANGE_* bits of the C ABI
+_RANGE_MESSAGES = ((RANGE_K, "a K scale or zero point beyond fp16 (|K| > 65504)"),
+                   (RANGE_V, "a V scale or zero point beyond fp16 (|V| > 65504)"),
+                   (RANGE_V_SCALE, "a V scale above 2048 (V range > 30720 in one 32-channel group)"))
 
 
 def _range_status(device: torch.device) -> torch.Tensor:
+    """The per-device status word that range-checked packs OR their ZKV_RANGE_*
+    bits into (zeroed when created and by ``kivi4_pack_status``)."""
     key = (device.type, device.index)
     t = _RANGE_STATUS.get(key)
     if t is None:
@@ -155,12 +160,14 @@ def kivi4_pack(k: torch.Tensor, v: torch.Tensor, cache: Kivi4Cache, g0: int,
     """Quantize the leading full groups of k / v [bs, kv, n, 128] into groups
     [g0, g0 + n // 32) of ``cache``; returns the number of groups written.
 
-    With ``check_range`` (the default) the call waits for the pack and raises
-    ``RuntimeError`` when a group's fp16 scale / zero cannot hold its values
-    (|K| or |V| or a group's range beyond 65504) or a V scale exceeds the
-    decode kernel's limit of 2048 (a V range above 30720 inside one
-    32-channel group).  ``check_range=False`` skips the check and its host
-    synchronisation, for callers that bound their values themselves."""
+    The call never synchronises the host.  With ``check_range`` (the default)
+    the pack ORs a bit into the device's status word whenever a group's fp16
+    scale / zero cannot hold its values (|K| or |V| or a group's range beyond
+    65504) or a V scale exceeds the decode kernel's limit of 2048 (a V range
+    above 30720 inside one 32-channel group); the caller reads it at its next
+    synchronisation point with ``check_kivi4_pack_range`` (raises
+    ``RuntimeError``) or ``kivi4_pack_status``.  ``check_range=False`` skips
+    the check, for callers that bound their values themselves."""
     require_gpu(k, v)
     _check_bf16("k", k)
     _check_bf16("v", v)
@@ -173,22 +180,35 @@ def kivi4_pack(k: torch.Tensor, v: torch.Tensor, cache: Kivi4Cache, g0: int,
         raise ValueError("cache batch / head shape mismatch")
     ng = n // GROUP
     status = _range_status(k.device) if check_range else None
-    if status is not None:
-        status.zero_()
     check(lib().zkv_kivi4_pack(
         ptr(k), k.stride(0), k.stride(1), k.stride(2),
         ptr(v), v.stride(0), v.stride(1), v.stride(2),
         bs, kv, ng, g0, cache.g_cap,
         ptr(cache.groups), ptr(status), stream_of(k)))
-    if status is not None:
-        bits = int(status.item())
-        if bits:
-            what = [name for bit, name in ((RANGE_K, "a K scale or zero point beyond fp16 (|K| > 65504)"),
-                                           (RANGE_V, "a V scale or zero point beyond fp16 (|V| > 65504)"),
-                                           (RANGE_V_SCALE, "a V scale above 2048 (V range > 30720 in one "
-                                                           "32-channel group)")) if bits & bit]
-            raise RuntimeError("kivi4_pack: values outside the 4-bit cache's fp16 range: " + "; ".join(what))
     return ng
+
+
+def kivi4_pack_status(device: torch.device | str | None = None, clear: bool = True) -> int:
+    """The ZKV_RANGE_* bits that range-checked packs on ``device`` (default: the
+    current device) recorded since the last clear.  Reading the word waits for
+    the packs queued before it on the current stream (a host synchronisation);
+    ``clear`` resets it to 0 afterwards, in stream order."""
+    dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+    t = _range_status(dev)
+    bits = int(t.item())
+    if clear and bits:
+        t.zero_()
+    return bits
+
+
+def check_kivi4_pack_range(device: torch.device | str | None = None) -> None:
+    """Raise ``RuntimeError`` naming what went out of range if any range-checked
+    pack on ``device`` since the last check stored values beyond the 4-bit
+    cache's fp16 range (see ``kivi4_pack``); clears the status."""
+    bits = kivi4_pack_status(device, clear=True)
+    if bits:
+        what = [name for bit, name in _RANGE_MESSAGES if bits & bit]
+        raise RuntimeError("kivi4_pack: values outside the 4-bit cache's fp16 range: " + "; ".join(what))
 
 
 _WORKSPACE: dict = {}
@@ -214,11 +234,14 @@ def attention_workspace(bs: int, hq: int, kv: int, n_groups: int, res_len: int,
 def kivi4_decode_attention(q: torch.Tensor, cache: Kivi4Cache, n_groups: int | None = None,
                            res_len: int | None = None, sm_scale: float | None = None,
                            out: torch.Tensor | None = None, out_dtype: torch.dtype | None = None,
-                           n_splits: int = 0, workspace: torch.Tensor | None = None) -> torch.Tensor:
+                           n_splits: int = 0, workspace: torch.Tensor | None = None,
+                           return_lse: bool = False):
     """Decode attention of q [bs, hq, 128] or [bs, 1, hq, 128] (bf16) over the
     first ``n_groups`` groups and ``res_len`` residual tokens of ``cache``.
 
     Output has q's shape and ``out_dtype`` (default q.dtype; float32 allowed).
+    With ``return_lse`` also the fp32 natural-log LSE [bs, hq] of the scaled
+    scores (flash-attn's softmax_lse).
     """
     require_gpu(q)
     _check_bf16("q", q)
@@ -245,6 +268,7 @@ def kivi4_decode_attention(q: torch.Tensor, cache: Kivi4Cache, n_groups: int | N
         out = torch.empty(bs, hq, HEAD_DIM, dtype=out_dtype, device=q.device)
     elif out.dtype != out_dtype or not out.is_contiguous() or out.numel() != bs * hq * HEAD_DIM:
         raise ValueError("out must be a contiguous [bs, hq, 128] tensor of out_dtype")
+    lse = torch.empty(bs, hq, dtype=torch.float32, device=q.device) if return_lse else None
     L = lib()
     need = L.zkv_kivi4_attention_workspace_size(bs, hq, kv, n_groups, res_len, n_splits)
     ws = _workspace(q.device, need) if workspace is None else workspace
@@ -253,23 +277,25 @@ def kivi4_decode_attention(q: torch.Tensor, cache: Kivi4Cache, n_groups: int | N
         ptr(cache.groups), cache.g_cap,
         ptr(cache.k_res), ptr(cache.v_res), cache.r_cap,
         bs, hq, kv, n_groups, res_len, sm_scale,
-        ptr(out), int(out_dtype == torch.float32), n_splits,
+        ptr(out), int(out_dtype == torch.float32), ptr(lse), n_splits,
         ptr(ws), ws.numel() * ws.element_size(), stream_of(q)))
     out = out.view(bs, hq, HEAD_DIM)
-    return out.unsqueeze(1) if squeeze else out
+    out = out.unsqueeze(1) if squeeze else out
+    return (out, lse) if return_lse else out
 
 
 def kivi4_sparse_attention(q: torch.Tensor, cache: Kivi4Cache, pages: torch.Tensor,
                            n_groups: int | None = None, res_len: int | None = None,
                            sm_scale: float | None = None, out: torch.Tensor | None = None,
                            out_dtype: torch.dtype | None = None, n_splits: int = 0,
-                           workspace: torch.Tensor | None = None) -> torch.Tensor:
+                           workspace: torch.Tensor | None = None, return_lse: bool = False):
     """Decode attention of q (bf16 [bs, hq, 128] or [bs, 1, hq, 128]) over the
     16-token pages listed in ``pages`` (int64 [bs, kv, n_sel]; page P = tokens
     16P .. 16P+15 of the quantized region) plus the bf16 residual window:
     the result of gathering those tokens and attending over them
     (S:1723-1772 after the Quest pick of S:2195-2240).  Sorted page lists let
-    both halves of a 32-token group share one tile."""
+    both halves of a 32-token group share one tile.  With ``return_lse`` also
+    the fp32 natural-log LSE [bs, hq]."""
     require_gpu(q, pages)
     _check_bf16("q", q)
     squeeze = q.dim() == 4
@@ -296,6 +322,7 @@ def kivi4_sparse_attention(q: torch.Tensor, cache: Kivi4Cache, pages: torch.Tens
         out = torch.empty(bs, hq, HEAD_DIM, dtype=out_dtype, device=q.device)
     elif out.dtype != out_dtype or not out.is_contiguous() or out.numel() != bs * hq * HEAD_DIM:
         raise ValueError("out must be a contiguous [bs, hq, 128] tensor of out_dtype")
+    lse = torch.empty(bs, hq, dtype=torch.float32, device=q.device) if return_lse else None
     L = lib()
     need = L.zkv_kivi4_sparse_attention_workspace_size(bs, hq, kv, n_sel, res_len, n_splits)
     ws = _workspace(q.device, need) if workspace is None else workspace
@@ -304,10 +331,11 @@ def kivi4_sparse_attention(q: torch.Tensor, cache: Kivi4Cache, pages: torch.Tens
         ptr(cache.groups), cache.g_cap,
         ptr(cache.k_res), ptr(cache.v_res), cache.r_cap,
         bs, hq, kv, n_groups, res_len, ptr(pages), pages.stride(0), pages.stride(1), n_sel, sm_scale,
-        ptr(out), int(out_dtype == torch.float32), n_splits,
+        ptr(out), int(out_dtype == torch.float32), ptr(lse), n_splits,
         ptr(ws), ws.numel() * ws.element_size(), stream_of(q)))
     out = out.view(bs, hq, HEAD_DIM)
-    return out.unsqueeze(1) if squeeze else out
+    out = out.unsqueeze(1) if squeeze else out
+    return (out, lse) if return_lse else out
 
 
 def kivi4_attention_partial(q: torch.Tensor, cache: Kivi4Cache, n_groups: int, res_len: int,

@@ -199,9 +199,12 @@ def _validate(coarse_indices, key_4bit, key_block_weight, q_blocks, q_norm, mag_
     return bs, kv_heads, kv_len
 
 
-# Per-device streamed-path workspace: [tensor, (bs, kv, kv_len) of the last
-# call or None].  Its token flags are zero between calls of one shape (each
-# call leaves them zero); they are zeroed again when the shape changes.
+# Streamed-path workspace per (device, stream): [tensor, (bs, kv, kv_len) of
+# the last call or None].  Its token flags are zero between calls of one
+# shape (each call leaves them zero); they are zeroed again when the shape
+# changes.  Calls on one stream run in order, so they never share the flags
+# or token scores while another call's kernels still use them; calls on two
+# streams get two workspaces.
 _WS: dict = {}
 
 
@@ -213,10 +216,11 @@ def _flag_bytes(bs: int, kv: int, kv_len: int) -> int:
 
 def _rerank_workspace(device, bs: int, kv: int, kv_len: int):
     need = lib().zkv_rabitq4_rerank_workspace_size(bs, kv, kv_len)
-    key = torch.device(device)
+    dev = torch.device(device)
+    key = (dev, torch.cuda.current_stream(dev).cuda_stream)
     ent = _WS.get(key)
     if ent is None or ent[0].numel() < need:
-        ent = [torch.zeros(max(need, 1 << 16), dtype=torch.uint8, device=key), (bs, kv, kv_len)]
+        ent = [torch.zeros(max(need, 1 << 16), dtype=torch.uint8, device=dev), (bs, kv, kv_len)]
         _WS[key] = ent
     elif ent[1] != (bs, kv, kv_len):
         ent[0][:_flag_bytes(bs, kv, kv_len)].zero_()
