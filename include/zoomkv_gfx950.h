@@ -287,6 +287,36 @@ int zkv_kivi4_sparse_attention(const uint16_t* q, int64_t q_sb, int64_t q_sh, co
                                int out_f32, float* lse, int n_splits, void* workspace,
                                size_t workspace_bytes, zkv_stream_t stream);
 
+/* Token-list decode attention over a Format Q cache plus bf16 rows, one
+ * launch: the 4-bit counterpart of the reference's gather of sink + local +
+ * selected tokens and flash_attn_with_kvcache(causal=False) (S:1723-1772;
+ * the list is the output of float_topk_gather_concat_3d,
+ * Z/cache_hub/topk/float_topk_gather_concat_ops.py:77-125).
+ * toks     int64 [bs, kv, n_tok] at element strides (tk_sb, tk_sh), n_tok <=
+ *          1024; per (b, kv), in any order: an id in [0, 32 n_groups) is that
+ *          token of the Format Q records `groups` (int32 [bs, kv, g_cap,
+ *          1280]); an id in [32 n_groups, 32 n_groups + n_tail) is the bf16
+ *          row tail_row0 + (id - 32 n_groups) of k / v; other ids are
+ *          skipped; a repeated id is attended again (as a repeated gathered
+ *          row would be)
+ * k, v     bf16 rows [bs, kv, n_rows, 128] at element strides (sb, sh, st),
+ *          rows 16-byte aligned; rows [near_row0, near_row0 + near_len) are
+ *          attended after the list
+ * out, lse as zkv_kivi4_decode_attention; workspace of
+ *          zkv_kivi4_token_attention_workspace_size() bytes (same layout and
+ *          rules).
+ * The workgroups sort each list in LDS, so the result does not depend on the
+ * list's order beyond rounding of the online softmax (sorted order is the
+ * computation order). */
+size_t zkv_kivi4_token_attention_workspace_size(int bs, int hq, int kv, int n_tok, int near_len, int n_splits);
+int zkv_kivi4_token_attention(const uint16_t* q, int64_t q_sb, int64_t q_sh, const int32_t* groups, int g_cap,
+                              int n_groups, const uint16_t* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
+                              const uint16_t* v, int64_t v_sb, int64_t v_sh, int64_t v_st, int n_rows,
+                              const int64_t* toks, int64_t tk_sb, int64_t tk_sh, int n_tok, int tail_row0,
+                              int n_tail, int near_row0, int near_len, int bs, int hq, int kv, float sm_scale,
+                              void* out, int out_f32, float* lse, int n_splits, void* workspace,
+                              size_t workspace_bytes, zkv_stream_t stream);
+
 /* Decode attention over bf16 K / V caches k, v [bs, n, kv, 128] at element
  * strides (sb = batch, st = token, sh = head; rows 16-byte aligned), causal
  * off, GQA hq = kv * gqa: the flash_attn_with_kvcache call of

@@ -14,7 +14,11 @@ arrays:
     tokens, else GQA mean -> Quest -> top-nk -> density -> top n_dense ->
     dense mask -> KIVI stage 2 -> global top-k + skipped (S:1589-1775,
     S:2195-2467, S:2688-2779), then attention over sink + local + selected
-    tokens (float64 textbook attention).
+    tokens (float64 textbook attention);
+  * kv_format "kivi4" (the 4-bit K + V retrieval zone, no reference
+    counterpart): the same bookkeeping and selection; the attended retrieval
+    rows are the exact dequant of each complete 32-token group's Format Q
+    quantization, and bf16 for the last (retrieval length % 32) tokens.
 """
 from __future__ import annotations
 
@@ -23,19 +27,21 @@ import math
 import numpy as np
 
 from . import select as osel
-from .kivi import attention, encode_chunks_ref
+from .kivi import attention, dequant_kivi4, encode_chunks_ref, quantize_kivi4
 
 
 class CacheModel:
     def __init__(self, layer_num, bs, kv, hq, input_length, max_new_length, sink, local, interval,
                  chunk, final_topk, full_threshold, cand_ratio, dense_ratio, dense_topk, sparse_topk,
-                 max_skipped=512, force_cand_tokens=None):
+                 max_skipped=512, force_cand_tokens=None, kv_format="bf16"):
         self.L, self.bs, self.kv, self.hq = layer_num, bs, kv, hq
         self.input_length, self.sink, self.local, self.interval = input_length, sink, local, interval
         self.chunk, self.final_topk, self.full_threshold = chunk, final_topk, full_threshold
         self.cand_ratio, self.dense_ratio = cand_ratio, dense_ratio
         self.dense_topk, self.sparse_topk = dense_topk, sparse_topk
         self.max_skipped, self.force_cand_tokens = max_skipped, force_cand_tokens
+        assert kv_format in ("bf16", "kivi4")
+        self.kv_format = kv_format
         cap = input_length + max_new_length
         near_cap = sink + local + interval
         self.near_cap = near_cap
@@ -199,6 +205,21 @@ class CacheModel:
         sk = np.broadcast_to(self.skipped, (self.bs, self.kv, len(self.skipped)))
         return osel.topk_gather_concat(s2, i2, sk, k, k + len(self.skipped))
 
+    def retrieval_rows(self, layer):
+        """The retrieval zone's K / V as attended [bs, kv, rlen, 128] (float64):
+        bf16 rows, or with kv_format "kivi4" the complete 32-token groups as
+        the exact dequant of their Format Q quantization (oracle.kivi) and
+        the last rlen % 32 tokens as bf16 rows."""
+        rlen = self.cpu_valid_end[layer]
+        k = self.ret_k[layer][:, :, :rlen].astype(np.float64)
+        v = self.ret_v[layer][:, :, :rlen].astype(np.float64)
+        if self.kv_format == "kivi4":
+            nq = rlen // 32 * 32
+            if nq:
+                kh, vh = dequant_kivi4(quantize_kivi4(self.ret_k[layer][:, :, :nq], self.ret_v[layer][:, :, :nq]))
+                k[:, :, :nq], v[:, :, :nq] = kh, vh
+        return k, v
+
     def compute(self, q, layer):
         """q [bs, 1, hq, 128] -> (out [bs, hq, 128] float64, selected indices or None)."""
         total = self.seq[layer]
@@ -211,11 +232,12 @@ class CacheModel:
         sel = None if full else self.select(raw_q, layer)
         out = np.zeros((self.bs, self.hq, 128))
         g = self.hq // self.kv
+        ret_k, ret_v = self.retrieval_rows(layer)
         for b in range(self.bs):
             for h in range(self.kv):
                 rows = np.arange(rlen) if full else sel[b, h]
-                k = np.concatenate([self.ret_k[layer][b, h, rows], self.near_k[layer][b, h, :near_len]])
-                v = np.concatenate([self.ret_v[layer][b, h, rows], self.near_v[layer][b, h, :near_len]])
+                k = np.concatenate([ret_k[b, h, rows], self.near_k[layer][b, h, :near_len]])
+                v = np.concatenate([ret_v[b, h, rows], self.near_v[layer][b, h, :near_len]])
                 out[b, h * g:(h + 1) * g] = attention(q[b:b + 1, 0, h * g:(h + 1) * g], k[None, None], v[None, None],
                                                       1 / np.sqrt(128))[0]
         return out, sel

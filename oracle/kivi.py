@@ -364,6 +364,52 @@ def kivi4_sparse_attention(q, cache: Kivi4Cache, n_groups: int, k_res, v_res, re
     return (out, lse) if return_lse else out
 
 
+def kivi4_token_attention(q, cache: Kivi4Cache, n_groups: int, k_rows, v_rows, toks: np.ndarray,
+                          tail_row0: int, n_tail: int, near_row0: int, near_len: int, sm_scale: float,
+                          dtype=np.float64, return_lse: bool = False):
+    """Attention over a token list plus contiguous bf16 rows: the reference's
+    gather of sink + local + the selected tokens followed by
+    flash_attn_with_kvcache(causal=False) (S:1723-1772), with the retrieval
+    zone's complete 32-token groups in Format Q.
+
+    For (b, h), the listed ids in order: an id in [0, 32 n_groups) is that
+    token of the Format Q records (exact dequant), an id in [32 n_groups,
+    32 n_groups + n_tail) is the bf16 row tail_row0 + (id - 32 n_groups) of
+    k_rows / v_rows [bs, Hkv, n_rows, 128]; other ids are skipped and a repeated
+    id is attended again; then rows [near_row0, near_row0 + near_len).
+    toks int [bs, Hkv, n_tok] -> out [bs, Hq, 128] (and the natural-log LSE
+    [bs, Hq], -inf where nothing is attended)."""
+    kh, vh = dequant_kivi4(Kivi4Cache(cache.k_codes[:, :, :n_groups], cache.k_meta[:, :, :n_groups],
+                                      cache.v_codes[:, :, :n_groups], cache.v_meta[:, :, :n_groups]), dtype=dtype)
+    bs, hq, d = q.shape
+    kv = k_rows.shape[1]
+    gqa = hq // kv
+    q_end = 32 * n_groups
+    out = np.zeros((bs, hq, d), dtype=dtype)
+    lse = np.full((bs, hq), -np.inf, dtype=dtype)
+    near = slice(near_row0, near_row0 + near_len)
+    for b in range(bs):
+        for h in range(kv):
+            ids = np.asarray(toks[b, h]).astype(np.int64)
+            ks, vs = [], []
+            for t in ids:
+                if 0 <= t < q_end:
+                    ks.append(kh[b, h, t])
+                    vs.append(vh[b, h, t])
+                elif q_end <= t < q_end + n_tail:
+                    ks.append(k_rows[b, h, tail_row0 + t - q_end].astype(dtype))
+                    vs.append(v_rows[b, h, tail_row0 + t - q_end].astype(dtype))
+            k = np.concatenate([np.array(ks, dtype=dtype).reshape(-1, d), k_rows[b, h, near].astype(dtype)], axis=0)
+            v = np.concatenate([np.array(vs, dtype=dtype).reshape(-1, d), v_rows[b, h, near].astype(dtype)], axis=0)
+            if k.shape[0] == 0:
+                continue
+            o, l = attention(q[b:b + 1, h * gqa:(h + 1) * gqa], k[None, None], v[None, None], sm_scale,
+                             dtype=dtype, return_lse=True)
+            out[b, h * gqa:(h + 1) * gqa] = o[0]
+            lse[b, h * gqa:(h + 1) * gqa] = l[0]
+    return (out, lse) if return_lse else out
+
+
 def lse_merge(out_a, lse_a, out_b, lse_b, dtype=np.float64):
     """lse_merge_torch (Z/cache_hub/lse_merge/lse_merge.py:79-119):
     out_* [bs, heads, dim], lse_* [bs, heads] (natural log)."""

@@ -3,7 +3,10 @@ decode steps (crossing several flushes with a chunk carry and a live skipped
 tail) must give the same bookkeeping, the same selected token indices (exact)
 and attention outputs within 2e-3, layer by layer and step by step -- with the
 retrieval zone in pinned host memory (enable_offload=True) and in device
-memory (False); the two modes give identical selections and outputs."""
+memory (False), and as the 4-bit K + V retrieval zone (kv_format "kivi4",
+Format Q groups plus a bf16 tail, attended by the token-list kernel) against
+the model's dequantized rows; the two bf16 modes give identical selections
+and outputs."""
 import numpy as np
 import pytest
 import torch
@@ -16,7 +19,13 @@ pytestmark = pytest.mark.gpu
 ATOL = 2e-3
 
 
-def _make(monkeypatch, chunk, cand, dense_ratio, dense_topk, sparse_topk, offload=True, **geo):
+STORAGE = ["offload", "device", "kivi4"]
+
+
+def _make(monkeypatch, chunk, cand, dense_ratio, dense_topk, sparse_topk, offload=True, storage=None, **geo):
+    kv_format = "bf16"
+    if storage is not None:
+        offload, kv_format = storage == "offload", ("kivi4" if storage == "kivi4" else "bf16")
     from zoomkv_revision_amd.cache import polar_cache
     monkeypatch.setenv("POLAR_QUEST_CHUNK", str(chunk))
     monkeypatch.setenv("POLAR_QUEST_CAND_RATIO", str(cand))
@@ -33,13 +42,15 @@ def _make(monkeypatch, chunk, cand, dense_ratio, dense_topk, sparse_topk, offloa
         layer_mapping={"0": "cuda:0"}, max_new_length=g["new"], sink_size=g["sink"], local_size=g["local"],
         core=1, nprobe=1, cache_unit_size=1, cache_cluster_num=1, num_gpus=1, model_size=8,
         final_topk=g["topk"], dynamic_update_interval=g["interval"], full_attention_threshold=g["thr"],
-        enable_offload=offload)
-    assert (cache.unified_keys_cpu is not None) == offload
-    if offload:   # host retrieval zone; device rows = gather area + near zone
+        enable_offload=offload, kv_format=kv_format)
+    assert (cache.unified_keys_cpu is not None) == (offload and kv_format == "bf16")
+    if kv_format == "kivi4":   # device rows = 32 tail rows + near zone
+        assert cache.unified_keys[0].shape[2] == 32 + cache.gpu_kv_capacity
+    elif offload:   # host retrieval zone; device rows = gather area + near zone
         assert cache.unified_keys_cpu[0].is_pinned()
         assert cache.unified_keys[0].shape[2] == cache._gather_rows + cache.gpu_kv_capacity
     model = CacheModel(g["L"], g["bs"], g["kv"], g["hq"], g["inp"], g["new"], g["sink"], g["local"], g["interval"],
-                       chunk, g["topk"], g["thr"], cand, dense_ratio, dense_topk, sparse_topk)
+                       chunk, g["topk"], g["thr"], cand, dense_ratio, dense_topk, sparse_topk, kv_format=kv_format)
     return cache, model
 
 
@@ -87,36 +98,60 @@ def _run(rng, cache, model, g, prompt, steps, lockstep=True):
 GEO = dict(L=2, bs=2, kv=2, hq=8, inp=400, new=200, sink=4, local=64, interval=32, topk=16, thr=0)
 
 
-@pytest.mark.parametrize("offload", [True, False])
-def test_cache_trace_chunk8_with_carry_and_flushes(rng, monkeypatch, offload):
+@pytest.mark.parametrize("storage", STORAGE)
+def test_cache_trace_chunk8_with_carry_and_flushes(rng, monkeypatch, storage):
     # retrieval after prefill: 400 - 4 - 64 = 332 = 41 chunks + 4 carried tokens
-    cache, model = _make(monkeypatch, 8, 0.2, 0.3, 8, 4, offload=offload, **GEO)
+    # (kivi4: 10 groups + a 12-token bf16 tail, through every flush)
+    cache, model = _make(monkeypatch, 8, 0.2, 0.3, 8, 4, storage=storage, **GEO)
     n = _run(rng, cache, model, GEO, prompt=400, steps=110)
     assert n == 2 * 110 and cache.cpu_valid_end[0] == 332 + 3 * 32
 
 
-@pytest.mark.parametrize("offload", [True, False])
-def test_cache_trace_chunk16_single_sample_prefill(rng, monkeypatch, offload):
+@pytest.mark.parametrize("storage", STORAGE)
+def test_cache_trace_chunk16_single_sample_prefill(rng, monkeypatch, storage):
     geo = dict(GEO, inp=300, thr=380)       # full attention first, then retrieval after a flush
-    cache, model = _make(monkeypatch, 16, 0.3, 0.3, 16, 8, offload=offload, **geo)
+    cache, model = _make(monkeypatch, 16, 0.3, 0.3, 16, 8, storage=storage, **geo)
     n = _run(rng, cache, model, geo, prompt=300, steps=90, lockstep=False)
     assert 0 < n < 2 * 90
 
 
-@pytest.mark.parametrize("offload", [True, False])
-def test_cache_trace_equal_dense_sparse_topk(rng, monkeypatch, offload):
+@pytest.mark.parametrize("storage", STORAGE)
+def test_cache_trace_equal_dense_sparse_topk(rng, monkeypatch, storage):
     # the production knobs (dense = sparse = 8): the density classification is
     # skipped, the selection must still equal the model's, which computes it
-    cache, model = _make(monkeypatch, 16, 0.4, 0.3, 8, 8, offload=offload, **GEO)
+    cache, model = _make(monkeypatch, 16, 0.4, 0.3, 8, 8, storage=storage, **GEO)
     n = _run(rng, cache, model, GEO, prompt=400, steps=70)
     assert n == 2 * 70
 
 
-@pytest.mark.parametrize("offload", [True, False])
-def test_cache_short_prompt_full_attention(rng, monkeypatch, offload):
+@pytest.mark.parametrize("storage", STORAGE)
+def test_cache_short_prompt_full_attention(rng, monkeypatch, storage):
     geo = dict(GEO, inp=50, new=60)
-    cache, model = _make(monkeypatch, 8, 0.2, 0.3, 8, 8, offload=offload, **geo)
+    cache, model = _make(monkeypatch, 8, 0.2, 0.3, 8, 8, storage=storage, **geo)
     assert _run(rng, cache, model, geo, prompt=50, steps=40) == 0
+
+
+def test_cache_kivi4_aligned_retrieval_and_threshold(rng, monkeypatch):
+    """kivi4 storage with a 32-aligned retrieval zone (no bf16 tail: flushes
+    pack straight from the near zone) and the full-attention threshold
+    crossed during decode (dense 4-bit kernel, then the token-list kernel)."""
+    geo = dict(GEO, inp=388, new=160, thr=470)   # retrieval 388 - 68 = 320 = 10 groups
+    cache, model = _make(monkeypatch, 16, 0.3, 0.3, 16, 8, storage="kivi4", **geo)
+    n = _run(rng, cache, model, geo, prompt=388, steps=120)
+    assert 0 < n < 2 * 120 and cache.cpu_valid_end[0] % 32 == 0
+    cache.check_range()
+
+
+def test_cache_kivi4_stores_no_bf16_retrieval_rows(monkeypatch):
+    """kivi4 storage keeps the retrieval zone as Format Q records only: the
+    device rows are the 32-row tail plus the near zone (no gather area, no
+    host rows), and the records take 160 B per token per KV head."""
+    geo = dict(GEO, inp=400, new=200)
+    cache, _ = _make(monkeypatch, 16, 0.3, 0.3, 16, 8, storage="kivi4", **geo)
+    cap = cache.cpu_kv_capacity
+    assert cache.unified_keys_cpu is None and cache.unified_keys[0].shape[2] == 32 + cache.gpu_kv_capacity
+    g = cache.kivi4_groups[0]
+    assert g.shape[2] == (cap + 31) // 32 and g.element_size() * g.shape[3] == 32 * 160
 
 
 def test_cache_offload_modes_identical(rng, monkeypatch):

@@ -314,3 +314,46 @@ def test_torch_cpu_c4_search_equals_oracle():
     table = np.array([bin(i).count("1") for i in range(256)])
     ref_pc = table[w.numpy().view(np.uint8).reshape(-1, 8)].sum(-1)
     assert np.array_equal(torch_cpu._popc64(w).numpy(), ref_pc)
+
+
+def test_token_attention_oracle_reduces_to_pages_and_dense(rng):
+    """The token-list oracle pinned by the two attention oracles it
+    generalises: listing every token of some 16-token pages (in any order,
+    with bf16 tail rows mapped in) equals the page-sparse oracle over those
+    pages with the same rows as its residual window; listing every quantized
+    token plus the tail equals dense attention over the cache + residual;
+    a repeated token equals attending its duplicated row; ids outside both
+    zones are skipped."""
+    bs, hq, kv, ng, n_tail = 1, 8, 2, 6, 5
+    k = gaussian_bf16(rng, (bs, kv, ng * 32, 128), outlier_channels=1)
+    v = gaussian_bf16(rng, (bs, kv, ng * 32, 128))
+    rec = okivi.quantize_kivi4(k, v)
+    rows_k = gaussian_bf16(rng, (bs, kv, 40, 128))
+    rows_v = gaussian_bf16(rng, (bs, kv, 40, 128))
+    q = gaussian_bf16(rng, (bs, hq, 128))
+    sc = 1 / np.sqrt(128)
+    tail0, near0, near_len = 3, 10, 20
+    q_end = 32 * ng
+    # pages 2, 5, 9, their tokens shuffled, plus two tail tokens; the near rows
+    pages = np.array([[[2, 5, 9]] * kv])
+    toks = (pages[..., None] * 16 + np.arange(16)).reshape(bs, kv, -1)
+    toks = np.stack([[rng.permutation(toks[0, h]) for h in range(kv)]])
+    tl = np.concatenate([toks, np.full((bs, kv, 1), q_end + 1), np.full((bs, kv, 1), q_end + 4)], -1)
+    got, lse = okivi.kivi4_token_attention(q, rec, ng, rows_k, rows_v, tl, tail0, n_tail, near0, near_len, sc,
+                                           return_lse=True)
+    res_k = np.concatenate([rows_k[:, :, [tail0 + 1, tail0 + 4]], rows_k[:, :, near0:near0 + near_len]], 2)
+    res_v = np.concatenate([rows_v[:, :, [tail0 + 1, tail0 + 4]], rows_v[:, :, near0:near0 + near_len]], 2)
+    want, wlse = okivi.kivi4_sparse_attention(q, rec, ng, res_k, res_v, res_k.shape[2], pages, sc, return_lse=True)
+    assert np.allclose(got, want, rtol=1e-12, atol=1e-12) and np.allclose(lse, wlse, rtol=1e-12)
+    # every quantized token + the whole tail = dense attention
+    every = np.broadcast_to(np.arange(q_end + n_tail), (bs, kv, q_end + n_tail))
+    got = okivi.kivi4_token_attention(q, rec, ng, rows_k, rows_v, every, tail0, n_tail, near0, 0, sc)
+    dense = okivi.kivi4_decode_attention(q, rec, ng, rows_k[:, :, tail0:tail0 + n_tail],
+                                         rows_v[:, :, tail0:tail0 + n_tail], n_tail, sc)
+    assert np.allclose(got, dense, rtol=1e-12, atol=1e-12)
+    # a repeated token and skipped ids (negative, past the tail)
+    tl2 = np.array([[[7, 7, -1, q_end + n_tail, 40]] * kv])
+    got = okivi.kivi4_token_attention(q, rec, ng, rows_k, rows_v, tl2, tail0, n_tail, near0, 0, sc)
+    kh, vh = okivi.dequant_kivi4(rec)
+    want = okivi.attention(q, kh[:, :, [7, 7, 40]], vh[:, :, [7, 7, 40]], sc)
+    assert np.allclose(got, want, rtol=1e-12, atol=1e-12)

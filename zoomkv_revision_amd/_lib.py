@@ -54,6 +54,10 @@ SIGNATURES = {
     "zkv_kivi4_sparse_attention_workspace_size": (SZ, [I32, I32, I32, I32, I32, I32]),
     "zkv_kivi4_sparse_attention": (I32, [P, I64, I64, P, I32, P, P, I32, I32, I32, I32, I32,
                                          I32, P, I64, I64, I32, F32, P, I32, P, I32, P, SZ, P]),
+    "zkv_kivi4_token_attention_workspace_size": (SZ, [I32, I32, I32, I32, I32, I32]),
+    "zkv_kivi4_token_attention": (I32, [P, I64, I64, P, I32, I32, P, I64, I64, I64, P, I64, I64, I64, I32,
+                                        P, I64, I64, I32, I32, I32, I32, I32, I32, I32, I32, F32, P, I32, P, I32,
+                                        P, SZ, P]),
     "zkv_bf16_attention_workspace_size": (SZ, [I32, I32, I32, I32, I32]),
     "zkv_bf16_decode_attention": (I32, [P, I64, I64, P, I64, I64, I64, P, I64, I64, I64, I32, I32, I32, I32,
                                         F32, P, I32, P, I32, P, SZ, P]),

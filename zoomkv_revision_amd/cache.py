@@ -105,6 +105,7 @@ class polar_cache:
         adaptive_topk_threshold: float = 0.9,
         adaptive_topk_min_k: int = 100,
         adaptive_topk_max_k: int = 400,
+        kv_format: str | None = None,
     ) -> None:
         # knobs the reference accepts but this path does not use (S:125-148)
         del core, nprobe, cache_unit_size, cache_cluster_num, codebook_path, collision_ratio
@@ -141,6 +142,14 @@ class polar_cache:
         self.candidate_ratio = candidate_ratio
         self.final_topk = final_topk
         self.enable_offload = bool(enable_offload)
+        # storage of the retrieval zone (no reference counterpart: the
+        # reference keeps bf16 K / V, S:561-571): "bf16", or "kivi4" for the
+        # 4-bit K + V cache (Format Q, fp16 scale / zero) in HBM
+        kv_format = kv_format if kv_format is not None else os.environ.get("POLAR_KV_FORMAT", "bf16")
+        if kv_format not in ("bf16", "kivi4"):
+            raise ValueError(f"kv_format must be 'bf16' or 'kivi4' (got {kv_format!r})")
+        self.kv_format = kv_format
+        self._kivi4 = kv_format == "kivi4"
         # Quest stage 1 / CDS knobs from the environment (S:178-292)
         self.quest_chunk_size = max(1, int(os.environ.get("POLAR_QUEST_CHUNK", "8")))
         if self.quest_chunk_size not in (8, 16):
@@ -174,7 +183,20 @@ class polar_cache:
         self.cpu_kv_capacity = max(0, self.unified_kv_capacity - sink_size - local_size)
         bs, kv, d = batch_size, num_key_value_heads, head_dim
         self._min_total = max(self.FULL_ATTENTION_THRESHOLD, sink_size + local_size + self.final_topk * 2)
-        if self.enable_offload:
+        if self._kivi4:
+            # device rows: [retrieval tail | near zone].  The retrieval zone's
+            # complete 32-token groups are Format Q records; its last
+            # L % 32 tokens stay bf16, right-aligned in rows [0, 32), so that
+            # they and the near zone are one run of rows.
+            self._tail_rows = kivi.GROUP
+            self._rows = self._tail_rows + self.gpu_kv_capacity
+            self._near0 = self._tail_rows
+            g_cap = max(1, (self.cpu_kv_capacity + kivi.GROUP - 1) // kivi.GROUP)
+            self.kivi4_groups = [torch.zeros(bs, kv, g_cap, kivi.RECORD_WORDS, dtype=torch.int32, **dev)
+                                 for _ in range(layer_num)]
+            self.unified_keys_cpu = self.unified_values_cpu = None
+            self._kivi4_stage = None                  # [tail | flushed tokens] staging, made on first use
+        elif self.enable_offload:
             # device rows: [gathered retrieval rows | near zone]; the retrieval
             # zone in pinned host memory (S:519-611).  The gather area holds a
             # selection (final_topk + skipped) or, below the retrieval
@@ -287,7 +309,15 @@ class polar_cache:
         V[rows, :, n0 + self.sink_size:n0 + self.sink_size + local_len] = vt[:, :, retrieval_end:seq_len].to(self.dtype)
         kr = kt[:, :, retrieval_start:retrieval_end].to(self.dtype)
         vr = vt[:, :, retrieval_start:retrieval_end].to(self.dtype)
-        if self.enable_offload:
+        if self._kivi4:
+            # complete groups to Format Q, the < 32-token rest to the tail rows
+            ng = kivi.kivi4_pack(kr, vr, self._kivi4_view(layer_idx, rows), 0)
+            t = retrieval_length - kivi.GROUP * ng
+            T = self._tail_rows
+            if t:
+                K[rows, :, T - t:T] = kr[:, :, kivi.GROUP * ng:]
+                V[rows, :, T - t:T] = vr[:, :, kivi.GROUP * ng:]
+        elif self.enable_offload:
             # the prompt's retrieval zone to its pinned host rows (S:1003-1141)
             torch.cuda.current_stream(self.device).wait_event(self._copy_events[layer_idx])
             self.unified_keys_cpu[layer_idx][rows, :, :retrieval_length].copy_(kr)
@@ -469,7 +499,9 @@ class polar_cache:
             w0 = self.cpu_valid_end[ldx]
             if w0 + num_new > self.cpu_kv_capacity:
                 raise RuntimeError(f"layer {ldx}: retrieval zone full ({w0} + {num_new} > {self.cpu_kv_capacity})")
-            if self.enable_offload:
+            if self._kivi4:
+                self._flush_kivi4(ldx, K[:, :, oldest], V[:, :, oldest], w0, num_new)
+            elif self.enable_offload:
                 self._offload(ldx, K[:, :, oldest], V[:, :, oldest], w0, num_new)
             else:
                 K[:, :, w0:w0 + num_new].copy_(K[:, :, oldest])
@@ -482,6 +514,45 @@ class polar_cache:
             V[:, :, dst] = V[:, :, src].clone()
         self._cached_region_total_len = -1
         self._cached_region_info = None
+
+    def _kivi4_view(self, ldx, rows=slice(None)):
+        """The layer's Format Q records as a Kivi4Cache (for the pack)."""
+        return kivi.Kivi4Cache(self.kivi4_groups[ldx][rows], self.unified_keys[ldx][rows],
+                               self.unified_values[ldx][rows])
+
+    def _flush_kivi4(self, ldx, k_old, v_old, w0, n):
+        """Append n flushed tokens to the 4-bit retrieval zone [0, w0): the
+        bf16 tail of w0 % 32 tokens and the new tokens are packed into
+        complete groups from group w0 // 32 on, and the rest becomes the new
+        tail (rows [32 - t, 32))."""
+        G, T = kivi.GROUP, self._tail_rows
+        t = w0 % G
+        K, V = self.unified_keys[ldx], self.unified_values[ldx]
+        if t:
+            bs, kv, _, d = K.shape
+            if self._kivi4_stage is None or self._kivi4_stage[0].shape[2] < t + n:
+                self._kivi4_stage = [torch.empty(bs, kv, t + n, d, dtype=self.dtype, device=self.device)
+                                     for _ in range(2)]
+            sk, sv = self._kivi4_stage[0][:, :, :t + n], self._kivi4_stage[1][:, :, :t + n]
+            sk[:, :, :t].copy_(K[:, :, T - t:T])
+            sv[:, :, :t].copy_(V[:, :, T - t:T])
+            sk[:, :, t:].copy_(k_old)
+            sv[:, :, t:].copy_(v_old)
+        else:
+            sk, sv = k_old, v_old
+        ng = kivi.kivi4_pack(sk, sv, self._kivi4_view(ldx), w0 // G)
+        t2 = t + n - G * ng
+        if t2:
+            K[:, :, T - t2:T].copy_(sk[:, :, G * ng:])
+            V[:, :, T - t2:T].copy_(sv[:, :, G * ng:])
+
+    def check_range(self) -> None:
+        """kivi4 storage: raise RuntimeError if any pack since the last check
+        met values beyond the 4-bit cache's fp16 range (kivi.kivi4_pack); reads
+        a device word, so it waits for the queued work (call it where the
+        caller synchronises anyway)."""
+        if self._kivi4:
+            kivi.check_kivi4_pack_range(self.device)
 
     def _offload(self, ldx, k_old, v_old, w0, n):
         """Stage the n oldest near-zone tokens and move them to host rows
@@ -586,7 +657,10 @@ class polar_cache:
             near_len = self.sink_size + local_len
         else:
             near_len = min(total, self.gpu_kv_capacity)      # short prompt: everything sits in the near zone
-        if total < self._min_total or retrieval_len <= 0 or self._cached_quest_nk <= 0:
+        full = total < self._min_total or retrieval_len <= 0 or self._cached_quest_nk <= 0
+        if self._kivi4:
+            return self._compute_kivi4(queries, layer_idx, retrieval_len, near_len, full)
+        if full:
             idx = self._arange_buffer[:retrieval_len].view(1, 1, -1).expand(bs, self.kv_head, -1)
             self._last_topk_indices = None
         else:
@@ -600,3 +674,20 @@ class polar_cache:
             h2d_gather_kv(self.unified_keys_cpu[layer_idx], self.unified_values_cpu[layer_idx], idx, K, V)
             idx = self._arange_buffer[:n].view(1, 1, -1).expand(bs, self.kv_head, -1)
         return gather_attention(queries, K, V, idx if n else None, self._near0, near_len)
+
+    def _compute_kivi4(self, queries, layer_idx, retrieval_len, near_len, full):
+        """compute with the 4-bit retrieval zone: the same selection, then one
+        launch over the selected tokens (Format Q groups, or the bf16 tail) and
+        the near zone; below the retrieval threshold, the dense 4-bit kernel
+        over every group plus the tail and near rows (one run of rows)."""
+        G, T = kivi.GROUP, self._tail_rows
+        ng, t = retrieval_len // G, retrieval_len % G
+        K, V = self.unified_keys[layer_idx], self.unified_values[layer_idx]
+        if full:
+            self._last_topk_indices = None
+            view = kivi.Kivi4Cache(self.kivi4_groups[layer_idx], K[:, :, T - t:], V[:, :, T - t:])
+            return kivi.kivi4_decode_attention(queries, view, ng, t + near_len)
+        idx = self._select(queries, layer_idx)
+        self._last_topk_indices = idx
+        return kivi.kivi4_token_attention(queries, self.kivi4_groups[layer_idx], ng, K, V, idx, T - t, t, T,
+                                          near_len)

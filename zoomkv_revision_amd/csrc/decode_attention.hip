@@ -114,7 +114,18 @@ struct AttnParams {
   const int64_t* pages;
   int64_t pg_sb, pg_sh;
   int n_sel;
+  // token-list mode (token_list != 0): `pages` holds n_sel int64 token ids
+  // per (b, kv).  Ids in [0, 32 n_groups) are Format Q tokens; ids in
+  // [32 n_groups, 32 n_groups + tok_n_tail) are the bf16 rows tok_tail_row0 +
+  // (id - 32 n_groups); other ids are skipped; a repeated id counts again.
+  // The bf16 tokens are the listed bf16 rows (ascending), then tok_near_len
+  // contiguous rows from tail_start.
+  int token_list;
+  int tok_tail_row0, tok_n_tail, tok_near_len;
 };
+
+// Entries of a token list per (b, kv) (checked on the host).
+constexpr int kMaxListTokens = 1024;
 
 // One pipeline stage = one 32-token tile, a byte copy of its Format Q record:
 //   [0, 2048)    K code words (lane order)   [2048, 4096) V code words
@@ -200,13 +211,23 @@ __device__ __forceinline__ u32x2_t ld8(const void* p) {
   return *reinterpret_cast<const u32x2_t*>(p);
 }
 
-// DMA ops of a tile with half mask `mask` (bit m: tokens 16m .. 16m + 15)
-__device__ __forceinline__ int tile_dma_ops(uint32_t mask) { return mask == 3u ? 5 : 3; }
+// A tile's token mask: bit t = token t of the 32-token group is attended.
+constexpr uint32_t kAllTokens = 0xFFFFFFFFu;
+
+// Halves a token mask touches (bit m: tokens 16m .. 16m + 15): the blocks a
+// tile loads.
+__device__ __forceinline__ uint32_t halves_of(uint32_t tok_mask) {
+  return ((tok_mask & 0xFFFFu) ? 1u : 0u) | ((tok_mask >> 16) ? 2u : 0u);
+}
+
+// DMA ops of a tile with token mask `tok_mask`
+__device__ __forceinline__ int tile_dma_ops(uint32_t tok_mask) { return halves_of(tok_mask) == 3u ? 5 : 3; }
 
 __device__ __forceinline__ void issue_tile(const AttnParams& p, int64_t bh, int gi, int lane,
-                                           uint8_t* stage, uint32_t mask = 3u) {
+                                           uint8_t* stage, uint32_t tok_mask = kAllTokens) {
   // the record is 5 contiguous KiB: 5 loads of 64 lanes x 16 B
   const uint8_t* rec = reinterpret_cast<const uint8_t*>(p.groups + (bh * p.g_cap + gi) * kRecordWords) + 16 * lane;
+  const uint32_t mask = halves_of(tok_mask);
   if (mask == 3u) {
 #pragma unroll
     for (int i = 0; i < 5; ++i) dma16(rec + 1024 * i, stage + 1024 * i);
@@ -363,7 +384,7 @@ __device__ __forceinline__ TileCodes codes_from_stage(const uint8_t* st, int lan
 //   V: O[j] += sum n * fp16(16 P s) in 2^-20 units; OZ row r = sum P z of
 //      32-channel group r & 3.
 __device__ __forceinline__ void compute_tile(const TileCodes& cw, const uint8_t* meta, int c, int g,
-                                             const TileConsts& tc, uint32_t half_mask,
+                                             const TileConsts& tc, uint32_t tok_mask,
                                              float& m_run, float4_t& L, float4_t O[8],
                                              float4_t& OZ) {
   const u32x4_t kq0 = cw.k0, kq1 = cw.k1;
@@ -386,9 +407,17 @@ __device__ __forceinline__ void compute_tile(const TileCodes& cw, const uint8_t*
   }
   // every row of Z holds sum q z (all A rows are the zero points)
   const float zc = Z[0];
-  // S[m] holds tokens 16m + 4g + i: drop an unselected page (half)
-  if (!(half_mask & 1u)) S[0] = float4_t{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-  if (!(half_mask & 2u)) S[1] = float4_t{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+  // S[m][i] holds token 16m + 4g + i: drop the tokens outside the tile's mask
+  // (unselected pages, or unlisted tokens of a token-list tile)
+  if (tok_mask != kAllTokens) {
+    const uint32_t mb = tok_mask >> (4 * g);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (!((mb >> i) & 1u)) S[0][i] = -INFINITY;
+      if (!((mb >> (16 + i)) & 1u)) S[1][i] = -INFINITY;
+    }
+  }
+  const uint32_t half_mask = halves_of(tok_mask);
   const half8_t pb = softmax_step(S, kTwo24, zc, tc.qs, tc.qs24, m_run, L, O, OZ);
 
   // V code words of channel pairs P = 0..3 of each half, and the halves' V
@@ -431,7 +460,12 @@ __device__ __forceinline__ void compute_tile(const TileCodes& cw, const uint8_t*
 // tokens [0, n_idx) are the listed rows (rows outside [0, row_limit) masked),
 // the rest are the contiguous rows tail_start, tail_start + 1, ...  Without a
 // row index (n_idx = 0, tail_start = 0) token t is row t.
-__device__ __forceinline__ int bf16_row(const AttnParams& p, const int64_t* idx_bh, int t) {
+// In the token-list mode the bf16 list comes first: its n_l rows in LDS
+// (l_rows), already resolved and in range.
+__device__ __forceinline__ int bf16_row(const AttnParams& p, const int64_t* idx_bh, int t,
+                                        const int32_t* l_rows = nullptr, int n_l = 0) {
+  if (t < n_l) return l_rows[t];
+  t -= n_l;
   if (t < p.n_idx) {  // n_idx > 0 only with a list (checked on the host)
     const int64_t r = idx_bh[t];
     return (r >= 0 && r < p.row_limit) ? static_cast<int>(r) : -1;
@@ -463,14 +497,16 @@ struct ResidualTile {
 
 template <bool kBf16Only>
 __device__ __forceinline__ void residual_rows(const AttnParams& p, int b, int h, int base, int valid, int c, int g,
-                                              int (&krow)[2], int (&vrow)[8]) {
+                                              int (&krow)[2], int (&vrow)[8], const int32_t* l_rows = nullptr,
+                                              int n_l = 0) {
   const int64_t* idx_bh = p.res_idx ? p.res_idx + b * p.ri_sb + h * p.ri_sh : nullptr;
 #pragma unroll
-  for (int m = 0; m < 2; ++m) krow[m] = c + 16 * m < valid ? bf16_row(p, idx_bh, base + c + 16 * m) : -1;
+  for (int m = 0; m < 2; ++m)
+    krow[m] = c + 16 * m < valid ? bf16_row(p, idx_bh, base + c + 16 * m, l_rows, n_l) : -1;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const int tok = (e < 4) ? (4 * g + e) : (16 + 4 * g + e - 4);
-    vrow[e] = tok < valid ? bf16_row(p, idx_bh, base + tok) : -1;
+    vrow[e] = tok < valid ? bf16_row(p, idx_bh, base + tok, l_rows, n_l) : -1;
   }
 }
 
@@ -574,9 +610,9 @@ template <bool kBf16Only, bool kEarlyV>
 __device__ __forceinline__ void residual_tile(const AttnParams& p, int b, int h, int base, int valid,
                                               int c, int g, const bf16x8_t qN[4], float qs,
                                               float& m_run, float4_t& L, float4_t O[8],
-                                              float4_t& OZ) {
+                                              float4_t& OZ, const int32_t* l_rows, int n_l) {
   int krow[2], vrow[8];
-  residual_rows<kBf16Only>(p, b, h, base, valid, c, g, krow, vrow);
+  residual_rows<kBf16Only>(p, b, h, base, valid, c, g, krow, vrow, l_rows, n_l);
   ResidualTile rt;
   residual_load_k<kBf16Only>(p, b, h, g, krow, rt);
   if constexpr (kEarlyV) {
@@ -735,14 +771,27 @@ struct KernelShape {
   static constexpr int kWavesPerEu = kBf16Only ? 2 : (kVgpr ? dense_waves_per_simd(NW) : kWavesPerSimd);
 };
 
-template <int NW, int D, bool kSparse, bool kBf16Only = false>
+using i32x4_t = int32_t __attribute__((ext_vector_type(4)));
+
+// kToken (with kSparse): the token-list mode.  The workgroup sorts the list
+// in LDS (rank sort: entry i goes to #{j : key_j < key_i} + #{j < i : key_j
+// == key_i}), so the quantized tokens come first, ascending, then the listed
+// bf16 rows.  A run of quantized tokens of one 32-token group is one tile
+// with a token mask; a repeated token starts a new tile, so it counts once
+// per listing.  The splits take contiguous tile ranges of equal weight,
+// computed here from the actual tile counts.
+template <int NW, int D, bool kSparse, bool kBf16Only = false, bool kToken = false>
 __global__ __launch_bounds__(64 * NW)
 __attribute__((amdgpu_waves_per_eu(KernelShape<NW, D, kSparse, kBf16Only>::kWavesPerEu)))
 void kivi4_attn_kernel(const AttnParams p) {
+  static_assert(!kToken || kSparse, "the token-list mode streams whole records");
   using KS = KernelShape<NW, D, kSparse, kBf16Only>;
   constexpr int kStage = KS::kStage;
   __shared__ __attribute__((aligned(16))) uint8_t smem[KS::kLdsBytes];
   __shared__ int s_prog[KS::kVgpr ? NW : 1];  // dense: tiles done per wave
+  // token-list mode: list keys, then tile groups | sorted keys, then the
+  // listed bf16 rows | tile token masks | counters
+  __shared__ __attribute__((aligned(16))) int32_t s_tok[kToken ? 3 * kMaxListTokens + 32 : 4];
   const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   // wave index through readfirstlane: the compiler then keeps the ring and
   // tile bookkeeping in SGPRs (scalar branches, scalar DMA base addresses)
@@ -751,10 +800,109 @@ void kivi4_attn_kernel(const AttnParams p) {
   const bool col_ok = c < p.gqa;
   const int64_t bh = static_cast<int64_t>(b) * p.kv + h;
 
-  const int T0 = (split >> 1) * (p.tiles_per_split + p.tiles_odd_split) + (split & 1) * p.tiles_per_split;
+  int T0 = (split >> 1) * (p.tiles_per_split + p.tiles_odd_split) + (split & 1) * p.tiles_per_split;
+  int T1_token = 0;  // token-list mode: the end of this split's tiles
   uint8_t (*ring)[kStage] = reinterpret_cast<uint8_t (*)[kStage]>(smem + wave * D * kStage);
   int n_qt = p.n_groups;  // quantized tiles of (b, kv)
-  if constexpr (kSparse) {
+  int res_len = p.res_len;
+  const int32_t* l_rows = nullptr;  // token-list mode: rows of the listed bf16 tokens (LDS)
+  int n_lrows = 0;
+  if constexpr (kToken) {
+    int32_t* s_key = s_tok;
+    int32_t* s_sorted = s_tok + kMaxListTokens;
+    uint32_t* s_tmask = reinterpret_cast<uint32_t*>(s_tok + 2 * kMaxListTokens);
+    int* s_cnt = s_tok + 3 * kMaxListTokens;  // [0, NW) tiles started per wave; [16] kept; [17] quantized
+    const int64_t* lst = p.pages + b * p.pg_sb + h * p.pg_sh;
+    const int64_t q_end = 32ll * p.n_groups, t_end = q_end + p.tok_n_tail;
+    const int n = p.n_sel;
+    constexpr int kPer = kMaxListTokens / (64 * NW);
+    if (tid == 0) {
+      s_cnt[16] = 0;
+      s_cnt[17] = 0;
+    }
+    int64_t raw[kPer];
+#pragma unroll
+    for (int e = 0; e < kPer; ++e) {
+      const int i = tid + e * 64 * NW;
+      raw[e] = i < n ? lst[i] : -1;
+    }
+    int32_t key[kPer];
+#pragma unroll
+    for (int e = 0; e < kPer; ++e) {
+      const int i = tid + e * 64 * NW;
+      key[e] = (raw[e] >= 0 && raw[e] < t_end) ? static_cast<int32_t>(raw[e]) : INT32_MAX;
+      s_key[i] = key[e];
+      s_tmask[i] = 0u;
+    }
+    __syncthreads();
+    int kept = 0, kept_q = 0;
+    const int n4 = (n + 3) & ~3;  // keys past n are INT32_MAX
+#pragma unroll
+    for (int e = 0; e < kPer; ++e) {
+      const int i = tid + e * 64 * NW;
+      const int32_t k = key[e];
+      if (k != INT32_MAX) {
+        int rank = 0;
+        for (int j = 0; j < n4; j += 4) {
+          const i32x4_t kk = *reinterpret_cast<const i32x4_t*>(s_key + j);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) rank += (kk[u] < k || (kk[u] == k && j + u < i)) ? 1 : 0;
+        }
+        s_sorted[rank] = k;
+        ++kept;
+        kept_q += k < q_end ? 1 : 0;
+      }
+    }
+    if (kept) atomicAdd(&s_cnt[16], kept);
+    if (kept_q) atomicAdd(&s_cnt[17], kept_q);
+    __syncthreads();
+    const int n_keep = s_cnt[16], n_q = s_cnt[17];
+    // sorted positions r0 = 2 tid and r0 + 1 of the quantized part: a tile
+    // starts at a new group or at a repeated token
+    const int r0 = 2 * tid;
+    const int32_t kp = (r0 >= 1 && r0 - 1 < n_q) ? s_sorted[r0 - 1] : -1;
+    const int32_t k0 = r0 < n_q ? s_sorted[r0] : -1;
+    const int32_t k1 = r0 + 1 < n_q ? s_sorted[r0 + 1] : -1;
+    const bool st0 = r0 < n_q && (r0 == 0 || (k0 >> 5) != (kp >> 5) || k0 == kp);
+    const bool st1 = r0 + 1 < n_q && ((k1 >> 5) != (k0 >> 5) || k1 == k0);
+    const uint64_t b0 = __ballot(st0), b1 = __ballot(st1);
+    const int below = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(b0 >> 32),
+                                                __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(b0), 0)) +
+                      __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(b1 >> 32),
+                                                __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(b1), 0));
+    if (lane == 0) s_cnt[wave] = __popcll(b0) + __popcll(b1);
+    __syncthreads();
+    int base = 0;
+    n_qt = 0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const int cw = s_cnt[w];
+      base += w < wave ? cw : 0;
+      n_qt += cw;
+    }
+    const int t0 = base + below + (st0 ? 1 : 0) - 1;  // tile of position r0
+    const int t1 = t0 + (st1 ? 1 : 0);
+    if (st0) s_key[t0] = k0 >> 5;  // from here on s_key[t] = group of tile t
+    if (st1) s_key[t1] = k1 >> 5;
+    if (r0 < n_q) atomicOr(&s_tmask[t0], 1u << (k0 & 31));
+    if (r0 + 1 < n_q) atomicOr(&s_tmask[t1], 1u << (k1 & 31));
+    // the listed bf16 tokens' rows, in place after the quantized part
+    for (int r = n_q + tid; r < n_keep; r += 64 * NW)
+      s_sorted[r] = p.tok_tail_row0 + (s_sorted[r] - static_cast<int32_t>(q_end));
+    __syncthreads();
+    l_rows = s_sorted + n_q;
+    n_lrows = n_keep - n_q;
+    res_len = n_lrows + p.tok_near_len;
+    // contiguous tile ranges of equal weight (a bf16 tile weighs
+    // kResidualTileWeight quantized ones)
+    const int n_rt = (res_len + kTile - 1) / kTile;
+    const int W = n_qt + kResidualTileWeight * n_rt;
+    auto tile_at = [&](int x) {
+      return x <= n_qt ? x : n_qt + (x - n_qt + kResidualTileWeight - 1) / kResidualTileWeight;
+    };
+    T0 = tile_at((split * W + p.n_splits - 1) / p.n_splits);
+    T1_token = tile_at(((split + 1) * W + p.n_splits - 1) / p.n_splits);
+  } else if constexpr (kSparse) {
     // Every wave walks the page list (64 pages per step, the pairing by
     // ballot ranks) and keeps the descriptors of its own tiles T0 + wave +
     // NW*k, k < 64, in its last ring stage, which no DMA has reached yet.
@@ -784,7 +932,7 @@ void kivi4_attn_kernel(const AttnParams p) {
       const int rel = t - T0 - wave;
       if (start && rel >= 0 && rel % NW == 0 && rel / NW < 64) {
         s_group[rel / NW] = static_cast<int32_t>(cur >> 1);
-        s_mask[rel / NW] = (cur & 1) ? 2 : (next == cur + 1 ? 3 : 1);
+        s_mask[rel / NW] = (cur & 1) ? 0xFFFF0000u : (next == cur + 1 ? kAllTokens : 0x0000FFFFu);
       }
       base += __popcll(m);
       before = __shfl(cur, 63, 64);
@@ -792,14 +940,21 @@ void kivi4_attn_kernel(const AttnParams p) {
     }
     n_qt = base;
   }
-  const int n_tiles = n_qt + (p.res_len + kTile - 1) / kTile;
-  const int T1 = min(T0 + ((split & 1) ? p.tiles_odd_split : p.tiles_per_split), n_tiles);
+  const int n_tiles = n_qt + (res_len + kTile - 1) / kTile;
+  const int T1 = kToken ? T1_token : min(T0 + ((split & 1) ? p.tiles_odd_split : p.tiles_per_split), n_tiles);
   const int TQ = min(T1, n_qt);  // quantized tiles of this workgroup: [T0, TQ)
   // this wave's quantized tiles: T0 + wave + NW*k, k < nq (nq <= 64 in sparse mode)
   const int nq = TQ > T0 + wave ? (TQ - (T0 + wave) + NW - 1) / NW : 0;
   // sparse mode: lane k holds the group and half mask of this wave's tile k
-  int my_group = 0, my_mask = 3;
-  if constexpr (kSparse) {
+  int my_group = 0, my_mask = static_cast<int>(kAllTokens);
+  if constexpr (kToken) {
+    if (lane < nq) {
+      my_group = s_tok[T0 + wave + NW * lane];
+      my_mask = s_tok[2 * kMaxListTokens + T0 + wave + NW * lane];
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    __builtin_amdgcn_sched_barrier(0);
+  } else if constexpr (kSparse) {
     const int32_t* s_group = reinterpret_cast<const int32_t*>(ring[D - 1]);
     if (lane < nq) {
       my_group = s_group[lane];
@@ -819,7 +974,7 @@ void kivi4_attn_kernel(const AttnParams p) {
     if constexpr (kSparse)
       return static_cast<uint32_t>(__builtin_amdgcn_readlane(my_mask, k));
     else
-      return 3u;
+      return kAllTokens;
   };
 
   // dense tiles: tile k's code words into register slot k % D, its metadata
@@ -894,8 +1049,9 @@ void kivi4_attn_kernel(const AttnParams p) {
         qN[s] = __builtin_bit_cast(bf16x8_t, col_ok ? ld16(qp + 8 * (4 * s + g)) : u32x4_t{0u, 0u, 0u, 0u});
       for (int t = t0; t < T1; t += NW) {
         const int base = (t - n_qt) * kTile;
-        residual_tile<kBf16Only, kBf16Only || (KS::kVgpr && NW == 8)>(p, b, h, base, min(kTile, p.res_len - base),
-                                                                       c, g, qN, p.qscale, m_run, L, O, OZ);
+        residual_tile<kBf16Only, kBf16Only || (KS::kVgpr && NW == 8)>(p, b, h, base, min(kTile, res_len - base),
+                                                                       c, g, qN, p.qscale, m_run, L, O, OZ,
+                                                                       l_rows, n_lrows);
       }
     }
   };
@@ -985,7 +1141,7 @@ void kivi4_attn_kernel(const AttnParams p) {
           // metadata DMA (issued last) has landed once 5 (D - 1) ops remain
           wait_vmcnt<5 * (D - 1)>();
           __builtin_amdgcn_sched_barrier(0);
-          compute_tile(creg[j], ring[j], c, g, tc, 3u, m_run, L, O, OZ);
+          compute_tile(creg[j], ring[j], c, g, tc, kAllTokens, m_run, L, O, OZ);
           if constexpr (kBalance) {
             ++prog;
             if (lane == 0) s_prog[wave] = prog;
@@ -1003,7 +1159,7 @@ void kivi4_attn_kernel(const AttnParams p) {
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int j = 0; j < D - 1; ++j)
-        if (k0 + j < nq) compute_tile(creg[j], ring[j], c, g, tc, 3u, m_run, L, O, OZ);
+        if (k0 + j < nq) compute_tile(creg[j], ring[j], c, g, tc, kAllTokens, m_run, L, O, OZ);
     } else {
       // ---- page-sparse tiles through this wave's D-stage LDS ring ----
       for (int k = 0; k < nq; ++k) {
@@ -1011,11 +1167,11 @@ void kivi4_attn_kernel(const AttnParams p) {
           issue_tile(p, bh, group_of(issued), lane, ring[issued % D], mask_of(issued));
           ++issued;
         }
-        const uint32_t half_mask = mask_of(k);
+        const uint32_t tok_mask = mask_of(k);
         int later = 0;  // DMA ops issued after tile k's
         for (int t = k + 1; t < issued; ++t) later += tile_dma_ops(mask_of(t));
         wait_ops_in_flight(later);
-        compute_tile(codes_from_stage(ring[k % D], lane), ring[k % D] + 4096, c, g, tc, half_mask, m_run, L,
+        compute_tile(codes_from_stage(ring[k % D], lane), ring[k % D] + 4096, c, g, tc, tok_mask, m_run, L,
                      O, OZ);
       }
     }
@@ -1326,10 +1482,16 @@ unsigned long long next_epoch() {
   return ((base + n) & kLow55) | (1ull << 55);
 }
 
+// Token-list shape: the rank sort's LDS (12 KiB) beside a 3-stage ring of
+// whole records (8 x 3 x 5 KiB); a wave holds one or two tiles at C5.
+constexpr int kTokenNW = 8, kTokenD = 3;
+
 void launch_attn(const AttnParams& p, int bs, hipStream_t s) {
   const dim3 grid(p.n_splits, p.kv, bs);
   const Shape sh = attn_shape();
-  if (p.page_sparse) {
+  if (p.token_list) {
+    kivi4_attn_kernel<kTokenNW, kTokenD, true, false, true><<<grid, 64 * kTokenNW, 0, s>>>(p);
+  } else if (p.page_sparse) {
     kivi4_attn_kernel<kSparseNW, kSparseD, true><<<grid, 64 * kSparseNW, 0, s>>>(p);
   } else if (p.n_groups == 0) {  // bf16 rows only: the 16-byte V layout
     kivi4_attn_kernel<8, 2, false, true><<<grid, 512, 0, s>>>(p);
@@ -1364,6 +1526,15 @@ struct SparsePages {
   int n_sel;
 };
 
+// Token list of the token-list mode (toks int64 [bs, kv, n_tok] at strides)
+// and where its bf16 tokens live (see AttnParams).
+struct TokenList {
+  const int64_t* toks;
+  int64_t tk_sb, tk_sh;
+  int n_tok;
+  int tail_row0, n_tail, near_row0, near_len;
+};
+
 
 // Sparse mode: every split is planned for the longest page list (n_sel
 // tiles); each wave keeps at most 64 tile descriptors in its lanes.
@@ -1380,13 +1551,27 @@ SplitPlan plan_sparse_splits(int bs, int kv, int n_sel, int res_len, int n_split
   return sp;
 }
 
+// Token-list mode: the split count of the sparse plan for the list's upper
+// bounds (every entry its own quantized tile, every entry a bf16 row), raised
+// so that no split's tile range (computed in the kernel from the actual
+// counts) exceeds the 64 tiles per wave the kernel keeps descriptors for.
+SplitPlan plan_token_splits(int bs, int kv, int n_tok, int near_len, int n_splits) {
+  const int res_max = n_tok + near_len;
+  SplitPlan sp = plan_splits(bs, kv, n_tok, res_max, n_splits, Shape{kTokenNW, kTokenD}, kStageBytes, 4, false);
+  const int64_t w_max = int64_t{n_tok} + int64_t{kResidualTileWeight} * ((res_max + kTile - 1) / kTile);
+  constexpr int64_t kMaxPerSplit = 64 * kTokenNW - 4;
+  const int ns_min = static_cast<int>((w_max + kMaxPerSplit - 1) / kMaxPerSplit);
+  sp.n_splits = std::max(std::max(sp.n_splits, ns_min), 1);
+  return sp;
+}
+
 int attention_launch(const uint16_t* q, int64_t q_sb, int64_t q_sh, const int32_t* groups,
                      int g_cap, const uint16_t* k_res, const uint16_t* v_res, int r_cap, int bs,
                      int hq, int kv, int n_groups, int res_len, float sm_scale, int n_splits,
                      void* workspace, size_t workspace_bytes, int* n_splits_used, void* out,
                      int out_f32, hipStream_t s, const SparsePages* sparse = nullptr,
                      const ResidualLayout* rl = nullptr, float* lse = nullptr,
-                     const RowIndex* ri = nullptr) {
+                     const RowIndex* ri = nullptr, const TokenList* tl = nullptr) {
   ZKV_REQUIRE(q && workspace, "zkv_kivi4_attention: null pointer");
   ZKV_REQUIRE(bs > 0 && kv > 0 && hq > 0 && hq % kv == 0,
               "zkv_kivi4_attention: bad heads bs=%d hq=%d kv=%d", bs, hq, kv);
@@ -1407,7 +1592,7 @@ int attention_launch(const uint16_t* q, int64_t q_sb, int64_t q_sh, const int32_
               "zkv_kivi4_attention: bf16 K / V rows must be 16-byte aligned (K strides %lld %lld %lld, "
               "V strides %lld %lld %lld)", (long long)res.k_sb, (long long)res.k_sh, (long long)res.k_st,
               (long long)res.v_sb, (long long)res.v_sh, (long long)res.v_st);
-  ZKV_REQUIRE(sparse != nullptr || n_groups + res_len > 0, "zkv_kivi4_attention: empty context");
+  ZKV_REQUIRE(sparse != nullptr || tl != nullptr || n_groups + res_len > 0, "zkv_kivi4_attention: empty context");
   ZKV_REQUIRE(n_groups == 0 || groups, "zkv_kivi4_attention: null cache pointer");
   ZKV_REQUIRE((reinterpret_cast<uintptr_t>(groups) & 15) == 0, "zkv_kivi4_attention: records must be 16-byte aligned");
   ZKV_REQUIRE(res_len == 0 || (k_res && v_res), "zkv_kivi4_attention: null residual pointer");
@@ -1420,8 +1605,16 @@ int attention_launch(const uint16_t* q, int64_t q_sb, int64_t q_sh, const int32_
                 "zkv_kivi4_sparse_attention: bad page list (n_sel=%d)", sparse->n_sel);
     ZKV_REQUIRE(g_cap <= (1 << 30), "zkv_kivi4_sparse_attention: g_cap=%d too large", g_cap);
   }
-  const SplitPlan sp = sparse ? plan_sparse_splits(bs, kv, sparse->n_sel, res_len, n_splits)
-                              : plan_splits(bs, kv, n_groups, res_len, n_splits);
+  if (tl) {
+    ZKV_REQUIRE(tl->n_tok >= 0 && tl->n_tok <= kMaxListTokens && (tl->n_tok == 0 || tl->toks),
+                "zkv_kivi4_token_attention: n_tok=%d (at most %d entries per (b, kv))", tl->n_tok,
+                kMaxListTokens);
+    ZKV_REQUIRE(tl->n_tail >= 0 && tl->near_len >= 0 && int64_t{32} * n_groups + tl->n_tail < (int64_t{1} << 31),
+                "zkv_kivi4_token_attention: bad tail n_tail=%d near_len=%d", tl->n_tail, tl->near_len);
+  }
+  const SplitPlan sp = tl       ? plan_token_splits(bs, kv, tl->n_tok, tl->near_len, n_splits)
+                       : sparse ? plan_sparse_splits(bs, kv, sparse->n_sel, res_len, n_splits)
+                                : plan_splits(bs, kv, n_groups, res_len, n_splits);
   const size_t partial = workspace_bytes_for(bs, hq, kv, sp.n_splits);
   const size_t need = partial;
   if (workspace_bytes < need)
@@ -1474,6 +1667,19 @@ int attention_launch(const uint16_t* q, int64_t q_sb, int64_t q_sh, const int32_
   p.pg_sb = sparse ? sparse->pg_sb : 0;
   p.pg_sh = sparse ? sparse->pg_sh : 0;
   p.n_sel = sparse ? sparse->n_sel : 0;
+  p.token_list = tl != nullptr;
+  p.tok_tail_row0 = p.tok_n_tail = p.tok_near_len = 0;
+  if (tl) {
+    p.pages = tl->toks;
+    p.pg_sb = tl->tk_sb;
+    p.pg_sh = tl->tk_sh;
+    p.n_sel = tl->n_tok;
+    p.tok_tail_row0 = tl->tail_row0;
+    p.tok_n_tail = tl->n_tail;
+    p.tok_near_len = tl->near_len;
+    p.tail_start = tl->near_row0;
+    p.res_len = tl->n_tok + tl->near_len;  // (an upper bound; the kernel counts the listed bf16 rows)
+  }
   if (n_splits_used) *n_splits_used = sp.n_splits;
   launch_attn(p, bs, s);
   int rc = check_launch("kivi4_attn_kernel");
@@ -1648,6 +1854,35 @@ extern "C" int zkv_bf16_decode_attention(const uint16_t* q, int64_t q_sb, int64_
   return attention_launch(q, q_sb, q_sh, nullptr, 0, k, v, n, bs, hq, kv, 0,
                           n, sm_scale, n_splits, workspace, workspace_bytes, nullptr, out, out_f32,
                           reinterpret_cast<hipStream_t>(stream), nullptr, &rl, lse);
+}
+
+// ---- token-list mode (4-bit cache + bf16 rows, one launch) -----------------
+
+extern "C" size_t zkv_kivi4_token_attention_workspace_size(int bs, int hq, int kv, int n_tok, int near_len,
+                                                           int n_splits) {
+  if (bs <= 0 || kv <= 0 || hq <= 0 || n_tok < 0 || near_len < 0) return 0;
+  const SplitPlan sp = plan_token_splits(bs, kv, n_tok, near_len, n_splits);
+  return workspace_bytes_for(bs, hq, kv, sp.n_splits);
+}
+
+extern "C" int zkv_kivi4_token_attention(const uint16_t* q, int64_t q_sb, int64_t q_sh, const int32_t* groups,
+                                         int g_cap, int n_groups, const uint16_t* k, int64_t k_sb, int64_t k_sh,
+                                         int64_t k_st, const uint16_t* v, int64_t v_sb, int64_t v_sh, int64_t v_st,
+                                         int n_rows, const int64_t* toks, int64_t tk_sb, int64_t tk_sh, int n_tok,
+                                         int tail_row0, int n_tail, int near_row0, int near_len, int bs, int hq,
+                                         int kv, float sm_scale, void* out, int out_f32, float* lse, int n_splits,
+                                         void* workspace, size_t workspace_bytes, zkv_stream_t stream) {
+  ZKV_REQUIRE(out, "zkv_kivi4_token_attention: null output");
+  ZKV_REQUIRE(n_rows >= 0 && tail_row0 >= 0 && n_tail >= 0 && near_row0 >= 0 && near_len >= 0 &&
+                  int64_t{tail_row0} + n_tail <= n_rows && int64_t{near_row0} + near_len <= n_rows,
+              "zkv_kivi4_token_attention: tail rows [%d, +%d) or near rows [%d, +%d) outside the %d rows", tail_row0,
+              n_tail, near_row0, near_len, n_rows);
+  ZKV_REQUIRE(n_tail + near_len == 0 || (k && v), "zkv_kivi4_token_attention: null bf16 rows");
+  const ResidualLayout rl{k_sb, k_sh, k_st, v_sb, v_sh, v_st};
+  const TokenList tl{toks, tk_sb, tk_sh, n_tok, tail_row0, n_tail, near_row0, near_len};
+  return attention_launch(q, q_sb, q_sh, groups, g_cap, k, v, n_rows, bs, hq, kv, n_groups, n_tok + near_len,
+                          sm_scale, n_splits, workspace, workspace_bytes, nullptr, out, out_f32,
+                          reinterpret_cast<hipStream_t>(stream), nullptr, &rl, lse, nullptr, &tl);
 }
 
 extern "C" int zkv_lse_merge(const void* out_a, const float* lse_a, const void* out_b, const float* lse_b,

@@ -269,13 +269,21 @@ def kivi4_decode_attention(q: torch.Tensor, cache: Kivi4Cache, n_groups: int | N
     elif out.dtype != out_dtype or not out.is_contiguous() or out.numel() != bs * hq * HEAD_DIM:
         raise ValueError("out must be a contiguous [bs, hq, 128] tensor of out_dtype")
     lse = torch.empty(bs, hq, dtype=torch.float32, device=q.device) if return_lse else None
+    # the residual rows may be a row window of a larger buffer: its row
+    # stride per head is the buffer's capacity
+    r_cap = cache.k_res.stride(1) // HEAD_DIM
+    for name, t in (("k_res", cache.k_res), ("v_res", cache.v_res)):
+        if t.stride(3) != 1 or t.stride(2) != HEAD_DIM or t.stride(1) != r_cap * HEAD_DIM or \
+                t.stride(0) != kv * r_cap * HEAD_DIM or t.shape[2] < res_len:
+            raise ValueError(f"{name} must be a token window of a contiguous [bs, kv, R_cap, 128] buffer holding "
+                             f"res_len={res_len} rows")
     L = lib()
     need = L.zkv_kivi4_attention_workspace_size(bs, hq, kv, n_groups, res_len, n_splits)
     ws = _workspace(q.device, need) if workspace is None else workspace
     check(L.zkv_kivi4_decode_attention(
         ptr(q3), q3.stride(0), q3.stride(1),
         ptr(cache.groups), cache.g_cap,
-        ptr(cache.k_res), ptr(cache.v_res), cache.r_cap,
+        ptr(cache.k_res), ptr(cache.v_res), r_cap,
         bs, hq, kv, n_groups, res_len, sm_scale,
         ptr(out), int(out_dtype == torch.float32), ptr(lse), n_splits,
         ptr(ws), ws.numel() * ws.element_size(), stream_of(q)))
@@ -332,6 +340,85 @@ def kivi4_sparse_attention(q: torch.Tensor, cache: Kivi4Cache, pages: torch.Tens
         ptr(cache.k_res), ptr(cache.v_res), cache.r_cap,
         bs, hq, kv, n_groups, res_len, ptr(pages), pages.stride(0), pages.stride(1), n_sel, sm_scale,
         ptr(out), int(out_dtype == torch.float32), ptr(lse), n_splits,
+        ptr(ws), ws.numel() * ws.element_size(), stream_of(q)))
+    out = out.view(bs, hq, HEAD_DIM)
+    out = out.unsqueeze(1) if squeeze else out
+    return (out, lse) if return_lse else out
+
+
+MAX_LIST_TOKENS = 1024   # token-list entries per (b, kv) of kivi4_token_attention
+
+
+def kivi4_token_attention(q: torch.Tensor, groups: torch.Tensor, n_groups: int, k_rows: torch.Tensor,
+                          v_rows: torch.Tensor, toks: torch.Tensor | None, tail_row0: int, n_tail: int,
+                          near_row0: int, near_len: int, sm_scale: float | None = None,
+                          out: torch.Tensor | None = None, out_dtype: torch.dtype | None = None,
+                          n_splits: int = 0, workspace: torch.Tensor | None = None, return_lse: bool = False):
+    """Decode attention of q (bf16 [bs, hq, 128] or [bs, 1, hq, 128]) over a
+    token list plus contiguous bf16 rows, in one launch: the 4-bit
+    counterpart of gathering sink + local + the selected tokens and calling
+    flash_attn_with_kvcache (S:1723-1772).
+
+    ``toks`` int64 [bs, kv, n_tok] (n_tok <= 1024, any order): an id in
+    [0, 32 n_groups) is that token of the Format Q records ``groups`` (int32
+    [bs, kv, G_cap, 1280]); an id in [32 n_groups, 32 n_groups + n_tail) is the
+    bf16 row ``tail_row0 + id - 32 n_groups`` of ``k_rows`` / ``v_rows`` (bf16
+    [bs, kv, n_rows, 128], rows 16-byte aligned); other ids are skipped; a
+    repeated id counts again.  Rows [near_row0, near_row0 + near_len) follow.
+    Output has q's shape and ``out_dtype`` (bf16 default, or float32); with
+    ``return_lse`` also the fp32 natural-log LSE [bs, hq]."""
+    require_gpu(q, groups, k_rows, v_rows, toks)
+    _check_bf16("q", q)
+    squeeze = q.dim() == 4
+    if squeeze and q.shape[1] != 1:
+        raise ValueError("decode attention takes one query token per sequence")
+    q3 = q[:, 0] if squeeze else q
+    _check_last_contig("q", q3)
+    bs, hq, _ = q3.shape
+    if groups.dtype != torch.int32 or groups.dim() != 4 or groups.shape[-1] != RECORD_WORDS or \
+            not groups.is_contiguous():
+        raise ValueError("groups must be contiguous int32 [bs, kv, G_cap, 1280]")
+    gbs, kv, g_cap, _ = groups.shape
+    if gbs != bs or hq % kv != 0:
+        raise ValueError(f"q {tuple(q.shape)} does not match the cache (bs={gbs}, kv={kv})")
+    if not 0 <= int(n_groups) <= g_cap:
+        raise ValueError(f"n_groups {n_groups} outside [0, {g_cap}]")
+    for name, t in (("k_rows", k_rows), ("v_rows", v_rows)):
+        _check_bf16(name, t)
+        if t.dim() != 4 or tuple(t.shape[:2]) != (bs, kv) or t.shape[-1] != HEAD_DIM or t.stride(-1) != 1:
+            raise ValueError(f"{name} must be bf16 [bs, kv, n_rows, 128] with a contiguous last dim")
+        if any(st % 8 for st in t.stride()[:3]) or t.data_ptr() % 16:
+            raise ValueError(f"{name} rows must be 16-byte aligned")
+    if k_rows.shape != v_rows.shape:
+        raise ValueError("k_rows / v_rows shape mismatch")
+    n_rows = k_rows.shape[2]
+    if toks is None:
+        toks = torch.empty(bs, kv, 0, dtype=torch.int64, device=q.device)
+    if toks.dtype != torch.int64 or toks.dim() != 3 or tuple(toks.shape[:2]) != (bs, kv):
+        raise ValueError("toks must be int64 [bs, kv, n_tok]")
+    if toks.shape[2] > MAX_LIST_TOKENS:
+        raise ValueError(f"at most {MAX_LIST_TOKENS} listed tokens per (b, kv); got {toks.shape[2]}")
+    if toks.shape[2] > 1 and toks.stride(2) != 1:
+        toks = toks.contiguous()
+    sm_scale = 1.0 / math.sqrt(HEAD_DIM) if sm_scale is None else float(sm_scale)
+    out_dtype = q.dtype if out_dtype is None else out_dtype
+    if out_dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"out_dtype must be bfloat16 or float32; got {out_dtype}")
+    if out is None:
+        out = torch.empty(bs, hq, HEAD_DIM, dtype=out_dtype, device=q.device)
+    elif out.dtype != out_dtype or not out.is_contiguous() or out.numel() != bs * hq * HEAD_DIM:
+        raise ValueError("out must be a contiguous [bs, hq, 128] tensor of out_dtype")
+    lse = torch.empty(bs, hq, dtype=torch.float32, device=q.device) if return_lse else None
+    L = lib()
+    n_tok = toks.shape[2]
+    need = L.zkv_kivi4_token_attention_workspace_size(bs, hq, kv, n_tok, int(near_len), n_splits)
+    ws = _workspace(q.device, need) if workspace is None else workspace
+    ks, vs = k_rows.stride(), v_rows.stride()
+    check(L.zkv_kivi4_token_attention(
+        ptr(q3), q3.stride(0), q3.stride(1), ptr(groups), g_cap, int(n_groups),
+        ptr(k_rows), ks[0], ks[1], ks[2], ptr(v_rows), vs[0], vs[1], vs[2], n_rows,
+        ptr(toks), toks.stride(0), toks.stride(1), n_tok, int(tail_row0), int(n_tail), int(near_row0),
+        int(near_len), bs, hq, kv, sm_scale, ptr(out), int(out_dtype == torch.float32), ptr(lse), n_splits,
         ptr(ws), ws.numel() * ws.element_size(), stream_of(q)))
     out = out.view(bs, hq, HEAD_DIM)
     out = out.unsqueeze(1) if squeeze else out
