@@ -288,15 +288,17 @@ def run_c5(args):
     t0 = time.perf_counter()
     model = ds.RandomQwen3(geo, dev, seed=42)
 
-    def run_mode(offload: bool):
+    def run_mode(offload: bool, kv_format: str = "bf16"):
         """Timed steps, then untimed steps up to and through the first flush
         (every `interval` tokens): the flush step's extra time, amortized."""
         t_setup = time.perf_counter()
-        cache = ds.build_cache(geo, batch, context, max_new, interval, threshold, dev, offload=offload)
+        cache = ds.build_cache(geo, batch, context, max_new, interval, threshold, dev, offload=offload,
+                               kv_format=kv_format)
         ds.fill_cache(cache, geo, batch, context, 43, dev)
         torch.cuda.synchronize()
         setup = time.perf_counter() - t_setup
-        print(f"[c5] offload={offload}: cache built and filled in {setup:.1f} s", file=sys.stderr, flush=True)
+        print(f"[c5] offload={offload} kv_format={kv_format}: cache built and filled in {setup:.1f} s",
+              file=sys.stderr, flush=True)
         gen = torch.Generator(device=dev)
         gen.manual_seed(42)
         state = {"tok": torch.randint(0, geo.vocab, (batch,), generator=gen, device=dev)}
@@ -331,25 +333,48 @@ def run_c5(args):
             "per_token_latency_with_flush_ms": None if extra is None else ms + extra / interval,
         }
 
+    qs = [torch.randn(batch, 1, geo.heads, geo.head_dim, device=dev).to(torch.bfloat16) for _ in range(geo.layers)]
+
+    def attention_pass_ms(cache):
+        """Device time of the attention path alone (36 x cache.compute)."""
+        def attn_pass(i):
+            for ldx in range(geo.layers):
+                cache.compute(qs[ldx], ldx)
+        return kernel_batch_ms(attn_pass, 8, host_us=15000.0)
+
     # the retrieval zone in device memory (the 288 GB part holds it)
     cache, step, ms, setup_dev, flush_dev = run_mode(False)
     setup_s = time.perf_counter() - t0
     flushes = flush_dev["flushes_in_timed_region"]
-    # device time of one step and of its attention path alone (36 x cache.compute),
-    # each queued behind a spin kernel so host launch gaps are not counted
+    # device time of one step and of its attention path alone, each queued
+    # behind a spin kernel so host launch gaps are not counted
     step_ms = kernel_batch_ms(step, 8, host_us=20000.0)
-    qs = [torch.randn(batch, 1, geo.heads, geo.head_dim, device=dev).to(torch.bfloat16) for _ in range(geo.layers)]
-
-    def attn_pass(i):
-        for ldx in range(geo.layers):
-            cache.compute(qs[ldx], ldx)
-
-    attn_ms = kernel_batch_ms(attn_pass, 8, host_us=15000.0)
+    attn_ms = attention_pass_ms(cache)
     per_layer = [ds.attention_path_bytes(cache, ldx) for ldx in range(geo.layers)]
     attn_bytes = sum(p["total"] for p in per_layer)
+    footprint = ds.cache_footprint(cache)
     weight_bytes = model.parameter_bytes()
     del cache, step
     torch.cuda.empty_cache()
+    # the 4-bit K + V retrieval zone (kv_format="kivi4"): same selection,
+    # token-list 4-bit attention
+    kivi4 = None
+    if not args.no_kivi4:
+        cache_q, step_q, ms_q, setup_q, flush_q = run_mode(False, "kivi4")
+        step_q_ms = kernel_batch_ms(step_q, 8, host_us=20000.0)
+        attn_q_ms = attention_pass_ms(cache_q)
+        per_layer_q = [ds.attention_path_bytes(cache_q, ldx) for ldx in range(geo.layers)]
+        bytes_q = sum(p["total"] for p in per_layer_q)
+        kivi4 = {"ms_per_step": ms_q, "tokens_per_s": batch / (ms_q * 1e-3), "setup_s": setup_q,
+                 "device_ms_per_step": step_q_ms, **flush_q,
+                 "attention_path": {"device_ms_per_step": attn_q_ms, "bytes_per_step": bytes_q,
+                                    "GBps": bytes_q / (attn_q_ms * 1e-3) / 1e9,
+                                    "bytes_per_layer": per_layer_q[0]},
+                 "footprint_bytes": ds.cache_footprint(cache_q),
+                 "per_token_floor_ms": (weight_bytes + bytes_q) / (HBM_PEAK_GBS * 1e9) * 1e3}
+        kivi4["per_token_floor_frac"] = kivi4["per_token_floor_ms"] / ms_q
+        del cache_q, step_q
+        torch.cuda.empty_cache()
     # the reference runner's enable_offload=True: retrieval zone in pinned host memory
     offload = None
     if not args.no_offload:
@@ -375,6 +400,11 @@ def run_c5(args):
                                      "gather-free bf16 attention",
                    "parallelism": "single GPU"},
         "per_token_latency_ms": ms,
+        # weights + attention-path bytes at 8 TB/s, and the step's fraction of it
+        "per_token_floor_ms": (weight_bytes + attn_bytes) / (HBM_PEAK_GBS * 1e9) * 1e3,
+        "per_token_floor_frac": (weight_bytes + attn_bytes) / (HBM_PEAK_GBS * 1e9) * 1e3 / ms,
+        "footprint_bytes": footprint,
+        "kivi4_mode": kivi4,
         "flushes_in_timed_region": flushes,
         "flush": {k: v for k, v in flush_dev.items() if k != "flushes_in_timed_region"},
         "offload_mode": offload,
@@ -704,6 +734,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-offload", action="store_true",
                     help="c5: skip the run with the retrieval zone in pinned host memory")
+    ap.add_argument("--no-kivi4", action="store_true",
+                    help="C5: skip the 4-bit K + V retrieval-zone mode")
     ap.add_argument("--no-flush", action="store_true",
                     help="c5: skip stepping to the first flush (its timing)")
     ap.add_argument("--hbm-reference", action="store_true",

@@ -312,13 +312,14 @@ def sample_next_token_full(logits: torch.Tensor, temperature: float = 1.0, top_p
 
 
 def build_cache(geo: Qwen3Geometry, batch: int, context: int, max_new: int, interval: int,
-                full_threshold: int, device, offload: bool = False):
+                full_threshold: int, device, offload: bool = False, kv_format: str = "bf16"):
     """polar_cache for `context` prompt tokens plus `max_new` generated ones,
-    with the reference's production knobs.  ``offload`` picks the retrieval
-    zone's home: device memory (False: the 288 GB part holds it) or pinned
-    host memory (True: the reference runner's enable_offload)."""
+    with the reference's production knobs.  ``offload`` picks the bf16
+    retrieval zone's home: device memory (False: the 288 GB part holds it) or
+    pinned host memory (True: the reference runner's enable_offload);
+    ``kv_format="kivi4"`` keeps it in device memory as 4-bit K + V instead."""
     from .cache import polar_cache
-    knobs = dict(PRODUCTION_CACHE_KNOBS, enable_offload=offload)
+    knobs = dict(PRODUCTION_CACHE_KNOBS, enable_offload=offload, kv_format=kv_format)
     return polar_cache(
         valid_start=[0] * batch, layer_num=geo.layers, batch_size=batch, max_length=context + max_new,
         num_key_value_heads=geo.kv_heads, num_heads=geo.heads, head_dim=geo.head_dim,
@@ -340,6 +341,24 @@ def fill_cache(cache, geo: Qwen3Geometry, batch: int, context: int, seed: int, d
         v = torch.randn(*shape, generator=g, device=device).to(torch.bfloat16)
         cache.prefill_update_kv_cache(None, k, v, ldx, 0)
         del k, v
+
+
+def cache_footprint(cache) -> dict:
+    """Bytes the cache holds, by part: device K / V rows (bf16), the 4-bit
+    records (kivi4 storage), the Format R selection metadata (chunk min / max
+    / centroid, 4-bit codes, valid mask) and pinned host rows."""
+    nb = lambda ts: sum(t.numel() * t.element_size() for t in ts)
+    parts = {
+        "device_bf16_rows": nb(cache.unified_keys + cache.unified_values),
+        "device_kivi4_records": nb(getattr(cache, "kivi4_groups", None) or []),
+        "device_selection_metadata": nb(cache._chunk_key_min_gpu + cache._chunk_key_max_gpu +
+                                         cache._chunk_key_centroid_gpu + cache.key_kivi_packed_gpu +
+                                         cache._chunk_valid_mask_gpu),
+        "host_pinned_rows": nb((cache.unified_keys_cpu or []) + (cache.unified_values_cpu or [])),
+    }
+    parts["device_total"] = parts["device_bf16_rows"] + parts["device_kivi4_records"] + \
+        parts["device_selection_metadata"]
+    return parts
 
 
 def attention_path_bytes(cache, layer: int) -> dict:
@@ -365,7 +384,14 @@ def attention_path_bytes(cache, layer: int) -> dict:
     topk2 = units * (nk * 4 + nk) if classify else 0
     stage2 = units * (nk * (8 + 1 + 16 * chunk * 4 + 2 * d * 2) + nk * chunk * 12)
     gather = units * (nk * chunk * 12 + sk * 8 + (k_final + sk) * 8)
-    attn = units * ((k_final + sk + near) * 2 * d * 2 + (k_final + sk) * 8) + 2 * bs * cache.num_heads * d * 2
+    if getattr(cache, "kv_format", "bf16") == "kivi4":
+        # the selected tokens from 4-bit records (160 B per token per KV head:
+        # K / V codes and their share of the scale / zero), the skipped tail
+        # and the near zone as bf16 rows
+        attn = units * (k_final * 160 + (sk + near) * 2 * d * 2 + (k_final + sk) * 8) + \
+            2 * bs * cache.num_heads * d * 2
+    else:
+        attn = units * ((k_final + sk + near) * 2 * d * 2 + (k_final + sk) * 8) + 2 * bs * cache.num_heads * d * 2
     append = 2 * units * d * 2
     parts = {"quest_gqa": quest, "topk_chunks": topk1, "density": density,
              "topk_dense": topk2, "kivi_stage2": stage2, "topk_gather_concat": gather,
