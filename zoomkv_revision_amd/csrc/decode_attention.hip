@@ -789,9 +789,10 @@ void kivi4_attn_kernel(const AttnParams p) {
   constexpr int kStage = KS::kStage;
   __shared__ __attribute__((aligned(16))) uint8_t smem[KS::kLdsBytes];
   __shared__ int s_prog[KS::kVgpr ? NW : 1];  // dense: tiles done per wave
-  // token-list mode: list keys, then tile groups | sorted keys, then the
-  // listed bf16 rows | tile token masks | counters
-  __shared__ __attribute__((aligned(16))) int32_t s_tok[kToken ? 3 * kMaxListTokens + 32 : 4];
+  // token-list mode: list keys | sorted keys (the listed bf16 rows after the
+  // quantized ones) | tile token masks | partial ranks | counters; tile
+  // groups overwrite whichever key array is not the sorted one
+  __shared__ __attribute__((aligned(16))) int32_t s_tok[kToken ? 4 * kMaxListTokens + 48 : 4];
   const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   // wave index through readfirstlane: the compiler then keeps the ring and
   // tile bookkeeping in SGPRs (scalar branches, scalar DMA base addresses)
@@ -807,56 +808,102 @@ void kivi4_attn_kernel(const AttnParams p) {
   int res_len = p.res_len;
   const int32_t* l_rows = nullptr;  // token-list mode: rows of the listed bf16 tokens (LDS)
   int n_lrows = 0;
+  const int32_t* s_groups = nullptr;  // token-list mode: group of each tile (LDS)
   if constexpr (kToken) {
-    int32_t* s_key = s_tok;
-    int32_t* s_sorted = s_tok + kMaxListTokens;
+    int32_t* s_key = s_tok;                        // list keys
+    int32_t* s_sorted = s_tok + kMaxListTokens;    // sorted keys (when the list is not sorted)
     uint32_t* s_tmask = reinterpret_cast<uint32_t*>(s_tok + 2 * kMaxListTokens);
-    int* s_cnt = s_tok + 3 * kMaxListTokens;  // [0, NW) tiles started per wave; [16] kept; [17] quantized
+    int32_t* s_rank = s_tok + 3 * kMaxListTokens;  // partial ranks
+    // per wave: [w] tiles started, [16 + w] entries kept, [24 + w] of them
+    // quantized, [32 + w] whether the list descends in the wave's entries
+    int* s_cnt = s_tok + 4 * kMaxListTokens;
     const int64_t* lst = p.pages + b * p.pg_sb + h * p.pg_sh;
     const int64_t q_end = 32ll * p.n_groups, t_end = q_end + p.tok_n_tail;
     const int n = p.n_sel;
     constexpr int kPer = kMaxListTokens / (64 * NW);
-    if (tid == 0) {
-      s_cnt[16] = 0;
-      s_cnt[17] = 0;
-    }
-    int64_t raw[kPer];
+    // entry i and its predecessor (the same cache lines: one round trip)
+    int64_t raw[kPer], prev[kPer];
 #pragma unroll
     for (int e = 0; e < kPer; ++e) {
       const int i = tid + e * 64 * NW;
       raw[e] = i < n ? lst[i] : -1;
+      prev[e] = (i >= 1 && i < n) ? lst[i - 1] : -1;
     }
-    int32_t key[kPer];
-#pragma unroll
-    for (int e = 0; e < kPer; ++e) {
-      const int i = tid + e * 64 * NW;
-      key[e] = (raw[e] >= 0 && raw[e] < t_end) ? static_cast<int32_t>(raw[e]) : INT32_MAX;
-      s_key[i] = key[e];
-      s_tmask[i] = 0u;
-    }
-    __syncthreads();
+    auto key_of = [&](int64_t id) { return (id >= 0 && id < t_end) ? static_cast<int32_t>(id) : INT32_MAX; };
+    // per-wave counts and "the list descends here" flags, one LDS slot per
+    // wave each (summed after the barrier: no zeroing, no atomics)
     int kept = 0, kept_q = 0;
-    const int n4 = (n + 3) & ~3;  // keys past n are INT32_MAX
+    bool descent = false;
 #pragma unroll
     for (int e = 0; e < kPer; ++e) {
       const int i = tid + e * 64 * NW;
-      const int32_t k = key[e];
-      if (k != INT32_MAX) {
-        int rank = 0;
-        for (int j = 0; j < n4; j += 4) {
-          const i32x4_t kk = *reinterpret_cast<const i32x4_t*>(s_key + j);
-#pragma unroll
-          for (int u = 0; u < 4; ++u) rank += (kk[u] < k || (kk[u] == k && j + u < i)) ? 1 : 0;
-        }
-        s_sorted[rank] = k;
-        ++kept;
-        kept_q += k < q_end ? 1 : 0;
-      }
+      const int32_t k = key_of(raw[e]);
+      s_key[i] = k;
+      s_tmask[i] = 0u;
+      s_rank[i] = 0;
+      kept += __popcll(__ballot(k != INT32_MAX));
+      kept_q += __popcll(__ballot(k < q_end));
+      descent = descent || (i >= 1 && i < n && key_of(prev[e]) > k);
     }
-    if (kept) atomicAdd(&s_cnt[16], kept);
-    if (kept_q) atomicAdd(&s_cnt[17], kept_q);
+    const bool wave_descent = __ballot(descent) != 0;
+    if (lane == 0) {
+      s_cnt[16 + wave] = kept;
+      s_cnt[24 + wave] = kept_q;
+      s_cnt[32 + wave] = wave_descent;
+    }
     __syncthreads();
-    const int n_keep = s_cnt[16], n_q = s_cnt[17];
+    int n_keep = 0, n_q = 0, unsorted = 0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      n_keep += s_cnt[16 + w];
+      n_q += s_cnt[24 + w];
+      unsorted |= s_cnt[32 + w];
+    }
+    // An ascending list (skipped ids last) is used as it is; otherwise a rank
+    // sort: entry i goes to #{j : key_j < key_i} + #{j < i : key_j == key_i},
+    // its comparisons split over (64 NW) / E threads (E = n rounded up to a
+    // power of 2), partial ranks summed with LDS atomics.
+    if (unsorted) {
+      int E = 64;
+      while (E < n) E <<= 1;
+      const int S = E >= 64 * NW ? 1 : (64 * NW) / E;  // threads per entry
+      const int n16 = (n + 15) & ~15;                  // keys past n are INT32_MAX
+      const int jlen = ((n16 / 16 + S - 1) / S) * 16;
+      const int part = E >= 64 * NW ? 0 : tid / E;
+      const int j0 = part * jlen, j1 = min(n16, j0 + jlen);
+      for (int i = E >= 64 * NW ? tid : tid % E; i < n; i += 64 * NW) {
+        const int32_t k = s_key[i];
+        if (k == INT32_MAX) continue;
+        // (key, index) as one 64-bit key: j precedes i iff cj < ci (branch-free)
+        const uint64_t ci = (static_cast<uint64_t>(static_cast<uint32_t>(k)) << 10) | static_cast<uint32_t>(i);
+        int rank = 0;
+        for (int j = j0; j < j1; j += 16) {
+          i32x4_t kk[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) kk[u] = *reinterpret_cast<const i32x4_t*>(s_key + j + 4 * u);
+#pragma unroll
+          for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+              const uint64_t cj = (static_cast<uint64_t>(static_cast<uint32_t>(kk[u][w])) << 10) |
+                                  static_cast<uint32_t>(j + 4 * u + w);
+              rank += cj < ci ? 1 : 0;
+            }
+        }
+        if (rank) atomicAdd(&s_rank[i], rank);
+      }
+      __syncthreads();
+#pragma unroll
+      for (int e = 0; e < kPer; ++e) {
+        const int i = tid + e * 64 * NW;
+        const int32_t k = s_key[i];
+        if (i < n && k != INT32_MAX) s_sorted[s_rank[i]] = k;
+      }
+    } else {
+      s_sorted = s_key;
+      s_key = s_tok + kMaxListTokens;
+    }
+    __syncthreads();
     // sorted positions r0 = 2 tid and r0 + 1 of the quantized part: a tile
     // starts at a new group or at a repeated token
     const int r0 = 2 * tid;
@@ -884,6 +931,7 @@ void kivi4_attn_kernel(const AttnParams p) {
     const int t1 = t0 + (st1 ? 1 : 0);
     if (st0) s_key[t0] = k0 >> 5;  // from here on s_key[t] = group of tile t
     if (st1) s_key[t1] = k1 >> 5;
+    s_groups = s_key;
     if (r0 < n_q) atomicOr(&s_tmask[t0], 1u << (k0 & 31));
     if (r0 + 1 < n_q) atomicOr(&s_tmask[t1], 1u << (k1 & 31));
     // the listed bf16 tokens' rows, in place after the quantized part
@@ -949,7 +997,7 @@ void kivi4_attn_kernel(const AttnParams p) {
   int my_group = 0, my_mask = static_cast<int>(kAllTokens);
   if constexpr (kToken) {
     if (lane < nq) {
-      my_group = s_tok[T0 + wave + NW * lane];
+      my_group = s_groups[T0 + wave + NW * lane];
       my_mask = s_tok[2 * kMaxListTokens + T0 + wave + NW * lane];
     }
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
@@ -1049,7 +1097,8 @@ void kivi4_attn_kernel(const AttnParams p) {
         qN[s] = __builtin_bit_cast(bf16x8_t, col_ok ? ld16(qp + 8 * (4 * s + g)) : u32x4_t{0u, 0u, 0u, 0u});
       for (int t = t0; t < T1; t += NW) {
         const int base = (t - n_qt) * kTile;
-        residual_tile<kBf16Only, kBf16Only || (KS::kVgpr && NW == 8)>(p, b, h, base, min(kTile, res_len - base),
+        residual_tile<kBf16Only, kBf16Only || kToken || (KS::kVgpr && NW == 8)>(p, b, h, base,
+                                                                                 min(kTile, res_len - base),
                                                                        c, g, qN, p.qscale, m_run, L, O, OZ,
                                                                        l_rows, n_lrows);
       }
