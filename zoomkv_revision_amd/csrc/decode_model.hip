@@ -17,6 +17,9 @@
 // reference is rounded (RNE) where the reference materialises it.
 #include "zkv_common.hpp"
 
+#include <algorithm>
+#include <cstdlib>
+
 namespace zkv {
 namespace {
 
@@ -189,6 +192,247 @@ __global__ __launch_bounds__(1024) void decode_linear_kernel(const LinearParams 
 }
 
 // ---------------------------------------------------------------------------
+// The same linear for M <= 4 input rows as a weight stream.  A unit of work
+// is kR weight rows over all of K (silu * up: kR / 2 gate rows and the
+// matching up rows); every wave takes units gw, gw + (waves in the grid), ...
+// and walks their (unit, 512-element chunk) items with two items in flight:
+// each item is kR loads of 1 KiB of one weight row (64 lanes x 16 B, whole
+// cache lines, nontemporal) and, without a norm, the x rows' 16 B.  With the
+// norm, the workgroup stages the normalised x rows in LDS once (the grid is
+// at most a few workgroups per CU, so the staging is amortised over many
+// units).  v_dot2_f32_bf16 accumulates w x x in fp32; at the unit's last
+// chunk the lanes' partial sums are reduce-scattered with shuffles and the
+// epilogue (that of decode_linear_kernel) runs by lane pairs.  Waves never
+// wait for each other after the staging.  (The MFMA tile of
+// decode_linear_kernel makes each load instruction touch 16 rows x 64 B and
+// splits K over waves of a 16-row tile.)
+// ---------------------------------------------------------------------------
+constexpr int kGemvMaxM = 4;
+constexpr int kGemvChunk = 512;  // elements of one row read by one wave instruction
+constexpr int kGemvWaves = 4;
+
+typedef __bf16 bf16x2v_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ bf16x2v_t as_bf16x2(uint32_t v) { return __builtin_bit_cast(bf16x2v_t, v); }
+
+// (each dword named: a bit_cast of an indexed vector element in an unrolled
+// loop compiled to four uses of element 0)
+__device__ __forceinline__ float dot8(const u32x4_t w, const u32x4_t x, float acc) {
+  const uint32_t w0 = w.x, w1 = w.y, w2 = w.z, w3 = w.w;
+  const uint32_t x0 = x.x, x1 = x.y, x2 = x.z, x3 = x.w;
+  acc = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(w0), as_bf16x2(x0), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(w1), as_bf16x2(x1), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(w2), as_bf16x2(x2), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(w3), as_bf16x2(x3), acc, false);
+  return acc;
+}
+
+// One step of a reduce-scatter over the lanes: lanes whose `bit` is set keep
+// the upper half of the N values, the others the lower half, each adding its
+// partner's (lane ^ bit) copy of the half it keeps.
+template <int N>
+__device__ __forceinline__ void rs_step(const float (&v)[N], float (&o)[N / 2], int lane, int bit) {
+  const bool hi = lane & bit;
+#pragma unroll
+  for (int j = 0; j < N / 2; ++j) {
+    const float send = hi ? v[j] : v[j + N / 2];
+    const float keep = hi ? v[j + N / 2] : v[j];
+    o[j] = keep + __shfl_xor(send, bit);
+  }
+}
+
+// The sum over the 64 lanes of value idx(lane) = lane >> (6 - log2 kV) of
+// the kV per-lane values (lanes equal in the high bits hold copies).
+template <int kV>
+__device__ __forceinline__ float lane_reduce(const float (&acc)[kV], int lane) {
+  float s;
+  if constexpr (kV == 32) {
+    float a[16], b[8], c[4], d[2], e[1];
+    rs_step<32>(acc, a, lane, 32);
+    rs_step<16>(a, b, lane, 16);
+    rs_step<8>(b, c, lane, 8);
+    rs_step<4>(c, d, lane, 4);
+    rs_step<2>(d, e, lane, 2);
+    s = e[0] + __shfl_xor(e[0], 1);
+  } else if constexpr (kV == 16) {
+    float a[8], b[4], c[2], d[1];
+    rs_step<16>(acc, a, lane, 32);
+    rs_step<8>(a, b, lane, 16);
+    rs_step<4>(b, c, lane, 8);
+    rs_step<2>(c, d, lane, 4);
+    s = d[0] + __shfl_xor(d[0], 2);
+    s = s + __shfl_xor(s, 1);
+  } else {
+    static_assert(kV == 8, "kV is 8, 16 or 32");
+    float a[4], b[2], c[1];
+    rs_step<8>(acc, a, lane, 32);
+    rs_step<4>(a, b, lane, 16);
+    rs_step<2>(b, c, lane, 8);
+    s = c[0] + __shfl_xor(c[0], 4);
+    s = s + __shfl_xor(s, 2);
+    s = s + __shfl_xor(s, 1);
+  }
+  return s;
+}
+
+// kSplit: the narrow projections.  A unit is then worked by the whole
+// workgroup, wave w taking chunks w, w + 4, ... (at least one each: the
+// launcher uses it for K >= 4 chunks), and the waves' partial sums meet in
+// LDS at the unit's end; the workgroups take units blockIdx.x, blockIdx.x +
+// gridDim.x, ...
+template <int kEpi, bool kNorm, int kR, int kD, bool kSplit>
+__global__ __launch_bounds__(64 * kGemvWaves) void decode_stream_kernel(const LinearParams p, int n_units) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  constexpr int kV = kR * kGemvMaxM;  // values per lane: acc[r * 4 + m]
+  constexpr int kShift = kV == 32 ? 1 : (kV == 16 ? 2 : 3);
+  float* rnorm = reinterpret_cast<float*>(lds);  // [4] norm factors
+  float* red = rnorm + kGemvMaxM;                // kSplit: [waves][64] partial sums
+  uint16_t* xs = reinterpret_cast<uint16_t*>(lds + 16 + (kSplit ? kGemvWaves * 64 * 4 : 0));  // normalised x [M][K]
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int M = p.M, K = p.K, N = p.N;
+  const int n_chunks = (K + kGemvChunk - 1) / kGemvChunk;
+  // this wave's units u0, u0 + du, ... and chunks c0, c0 + dc, ... (cnt per unit)
+  const int u0 = kSplit ? blockIdx.x : blockIdx.x * kGemvWaves + wave;
+  const int du = kSplit ? gridDim.x : gridDim.x * kGemvWaves;
+  const int c0 = kSplit ? wave : 0, dc = kSplit ? kGemvWaves : 1;
+  const int cnt = kSplit ? (n_chunks - wave + kGemvWaves - 1) / kGemvWaves : n_chunks;
+  const int n_my = u0 < n_units ? (n_units - 1 - u0) / du + 1 : 0;
+  const int n_items = n_my * cnt;
+  constexpr int kXv = kGemvMaxM;  // the x rows' 16 B (no norm)
+
+  auto unit_row = [&](int u, int r) {
+    if constexpr (kEpi == kEpiSiluMul) {
+      const int half = N >> 1, j = u * (kR / 2) + (r % (kR / 2));
+      return j < half ? (r < kR / 2 ? j : half + j) : -1;
+    } else {
+      const int n = u * kR + r;
+      return n < N ? n : -1;
+    }
+  };
+  // item t of this wave: unit u0 + (t / cnt) du, chunk c0 + (t % cnt) dc
+  auto load_item = [&](int t, u32x4_t (&wv)[kR], u32x4_t (&xv)[kXv]) {
+    const int u = u0 + (t / cnt) * du, ci = c0 + (t % cnt) * dc;
+    const int k = ci * kGemvChunk + 8 * lane;
+    const bool ok = t < n_items && k < K;
+#pragma unroll
+    for (int r = 0; r < kR; ++r) {
+      const int row = unit_row(u, r);
+      wv[r] = ok && row >= 0 ? __builtin_nontemporal_load(
+                                   reinterpret_cast<const u32x4_t*>(p.w + static_cast<int64_t>(row) * K + k))
+                             : u32x4_t{0u, 0u, 0u, 0u};
+    }
+    if constexpr (!kNorm) {
+#pragma unroll
+      for (int m = 0; m < kGemvMaxM; ++m)
+        xv[m] = ok && m < M ? *reinterpret_cast<const u32x4_t*>(p.x + m * p.x_ld + k) : u32x4_t{0u, 0u, 0u, 0u};
+    }
+  };
+  // kD register slots of items in flight
+  u32x4_t wr[kD][kR], xr[kD][kXv];
+#pragma unroll
+  for (int d = 0; d < kD; ++d) load_item(d, wr[d], xr[d]);
+
+  if constexpr (kNorm) {
+    // wave m: the RMS factor of x row m; then the normalised rows to LDS
+    // (the first items' weight loads are in flight)
+    if (wave < M) {
+      const u32x4_t* xrow = reinterpret_cast<const u32x4_t*>(p.x + wave * p.x_ld);
+      float ss = 0.0f;
+      for (int i = lane; i < (K >> 3); i += 64) {
+        const u32x4_t v = xrow[i];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float lo = __uint_as_float(v[e] << 16), hi = __uint_as_float(v[e] & 0xFFFF0000u);
+          ss = ss + lo * lo;
+          ss = ss + hi * hi;
+        }
+      }
+      ss = wave_sum(ss);
+      if (lane == 0) rnorm[wave] = rsqrtf(ss * (1.0f / static_cast<float>(K)) + p.eps);
+    }
+    __syncthreads();
+    for (int i = tid; i < M * (K >> 3); i += 64 * kGemvWaves) {
+      const int m = i / (K >> 3), k8 = i - m * (K >> 3);
+      u32x4_t v = reinterpret_cast<const u32x4_t*>(p.x + m * p.x_ld)[k8];
+      const float r = rnorm[m];
+      const u32x4_t wv = reinterpret_cast<const u32x4_t*>(p.norm_w)[k8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float lo = bf16r((__uint_as_float(v[e] << 16) * r) * __uint_as_float(wv[e] << 16));
+        const float hi = bf16r((__uint_as_float(v[e] & 0xFFFF0000u) * r) * __uint_as_float(wv[e] & 0xFFFF0000u));
+        v[e] = (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xFFFF0000u);
+      }
+      reinterpret_cast<u32x4_t*>(xs)[i] = v;
+    }
+    __syncthreads();
+  }
+
+  float acc[kV];
+#pragma unroll
+  for (int j = 0; j < kV; ++j) acc[j] = 0.0f;
+  auto step = [&](int t, const u32x4_t (&wv)[kR], const u32x4_t (&xv)[kXv]) {
+    const int ci = c0 + (t % cnt) * dc;
+    const int k = ci * kGemvChunk + 8 * lane;
+    u32x4_t xm[kGemvMaxM];
+#pragma unroll
+    for (int m = 0; m < kGemvMaxM; ++m) {
+      if constexpr (kNorm)
+        xm[m] = m < M && k < K ? *reinterpret_cast<const u32x4_t*>(xs + m * K + k) : u32x4_t{0u, 0u, 0u, 0u};
+      else
+        xm[m] = xv[m];
+    }
+#pragma unroll
+    for (int r = 0; r < kR; ++r)
+#pragma unroll
+      for (int m = 0; m < kGemvMaxM; ++m) acc[r * kGemvMaxM + m] = dot8(wv[r], xm[m], acc[r * kGemvMaxM + m]);
+    if (t % cnt != cnt - 1) return;
+    // this wave's last chunk of the unit: sums over the lanes (and, split,
+    // over the waves), epilogue, fresh accumulators
+    const int u = u0 + (t / cnt) * du;
+    float s = lane_reduce<kV>(acc, lane);
+#pragma unroll
+    for (int j = 0; j < kV; ++j) acc[j] = 0.0f;
+    if constexpr (kSplit) {
+      red[wave * 64 + lane] = s;
+      __syncthreads();
+      if (wave == 0) {
+#pragma unroll
+        for (int w = 1; w < kGemvWaves; ++w) s += red[w * 64 + lane];
+      }
+      __syncthreads();  // red is free for the next unit
+      if (wave != 0) return;
+    }
+    const int idx = lane >> kShift, r = idx / kGemvMaxM, m = idx % kGemvMaxM;
+    const bool lead = (lane & ((1 << kShift) - 1)) == 0;
+    const int row = unit_row(u, r);
+    if constexpr (kEpi == kEpiSiluMul) {
+      // the up row of gate row r sits kR / 2 rows (32 lanes) higher
+      const float up = __shfl_xor(s, 32);
+      if (lane >= 32 || !lead || m >= M || row < 0) return;
+      const float gt = bf16r(s), uv = bf16r(up);
+      const float act = bf16r(gt / (1.0f + expf(-gt)));
+      store_y(p, m, row, bf16r(act * uv));
+    } else {
+      if (!lead || m >= M || row < 0) return;
+      float y = bf16r(s);
+      if constexpr (kEpi == kEpiResidual) y = bf16r(bf16_to_f32(p.res[m * p.res_ld + row]) + y);
+      store_y(p, m, row, y);
+    }
+  };
+  // slot d holds items d, d + kD, ...: refilled kD items ahead (every slot
+  // index static)
+  for (int t = 0; t < n_items; t += kD) {
+#pragma unroll
+    for (int d = 0; d < kD; ++d) {
+      if (t + d < n_items) {
+        step(t + d, wr[d], xr[d]);
+        load_item(t + d + kD, wr[d], xr[d]);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // q / k: per-head RMSNorm (bf16 out), then rotate-half RoPE at one position
 // (bf16 out); v copied.  One wave per head of one batch row; lane l holds
 // channels l and l + 64 (the two halves RoPE pairs).  Heads [0, hq) are q
@@ -271,6 +515,55 @@ extern "C" int zkv_decode_linear(const uint16_t* x, int64_t x_ld, int M, int K, 
               K, lds);
   LinearParams p{x, x_ld, w, norm_w, eps, residual, res_ld, out, out_ld, M, K, N, out_f32};
   auto s = reinterpret_cast<hipStream_t>(stream);
+  if (M <= kGemvMaxM && !getenv("ZKV_LINEAR_MFMA")) {
+    // the weight stream: units of 8 rows for the wide projections, 4 or 2
+    // for narrower ones (at least ~2048 units); a few workgroups per CU
+    const int rows = epilogue == kEpiSiluMul ? N / 2 : N;
+    const int n_chunks = (K + kGemvChunk - 1) / kGemvChunk;
+    // narrow projections (fewer rows than ~2 units per wave of a full chip)
+    // split K over the waves of a workgroup
+    const bool split = rows < 8192 && n_chunks >= kGemvWaves && !norm_w;
+    const int R = split ? 4 : (rows >= 16384 ? 8 : (rows >= 8192 ? 4 : 2));
+    const int per_unit = epilogue == kEpiSiluMul ? R / 2 : R;
+    const int n_units = (rows + per_unit - 1) / per_unit;
+    const int grid_g = std::max(1, std::min(split ? n_units : (n_units + kGemvWaves - 1) / kGemvWaves, 768));
+    const size_t lds_g = 16 + (split ? kGemvWaves * 64 * 4 : 0) + (norm_w ? x_bytes : 0);
+    ZKV_REQUIRE(lds_g <= 160 * 1024, "zkv_decode_linear: M x K = %d x %d needs %zu bytes of LDS", M, K, lds_g);
+#define ZKV_GEMV(E, NORM, RR, D, SPLIT)                                                               \
+  do {                                                                                                \
+    static bool big_lds_set = false;                                                                  \
+    if (lds_g > 64 * 1024 && !big_lds_set) {                                                          \
+      if (hipFuncSetAttribute(reinterpret_cast<const void*>(&decode_stream_kernel<E, NORM, RR, D, SPLIT>), \
+                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess) \
+        return fail(ZKV_EINVAL, "zkv_decode_linear: cannot raise the LDS limit to 160 KiB");          \
+      big_lds_set = true;                                                                             \
+    }                                                                                                 \
+    decode_stream_kernel<E, NORM, RR, D, SPLIT><<<grid_g, 64 * kGemvWaves, lds_g, s>>>(p, n_units);   \
+  } while (0)
+#define ZKV_GEMV_R(E, NORM)                 \
+  do {                                      \
+    if (split)                              \
+      ZKV_GEMV(E, NORM, 4, 2, true);        \
+    else if (R == 8)                        \
+      ZKV_GEMV(E, NORM, 8, 2, false);       \
+    else if (R == 4)                        \
+      ZKV_GEMV(E, NORM, 4, 2, false);       \
+    else                                    \
+      ZKV_GEMV(E, NORM, 2, 2, false);       \
+  } while (0)
+    if (norm_w) {
+      if (epilogue == kEpiNone) ZKV_GEMV_R(kEpiNone, true);
+      else if (epilogue == kEpiResidual) ZKV_GEMV_R(kEpiResidual, true);
+      else ZKV_GEMV_R(kEpiSiluMul, true);
+    } else {
+      if (epilogue == kEpiNone) ZKV_GEMV_R(kEpiNone, false);
+      else if (epilogue == kEpiResidual) ZKV_GEMV_R(kEpiResidual, false);
+      else ZKV_GEMV_R(kEpiSiluMul, false);
+    }
+#undef ZKV_GEMV_R
+#undef ZKV_GEMV
+    return check_launch("decode_stream_kernel");
+  }
   const dim3 grid(n_tiles), block(64 * nw);
   // dynamic LDS above 64 KiB has to be allowed per kernel (once)
 #define ZKV_LIN(E, NORM)                                                                              \
