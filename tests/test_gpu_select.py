@@ -291,3 +291,82 @@ def test_topk_dense_mask_fused_matches_two_ops(rng, L, k):
     idx = topk_dense_mask(xt, k, mask)
     assert torch.equal(idx, ref_idx) and torch.equal(mask, ref_mask)
     assert np.array_equal(from_torch(idx), osel.topk_indices(x, k))
+
+
+@pytest.mark.parametrize("bs,hq,kv,n_max,n,k,fp16_meta,with_valid", [
+    (2, 32, 8, 4096, 4076, 1631, False, True),    # a C5 row: 4076 chunks, top-1631
+    (8, 32, 8, 2048, 2048, 128, True, False),      # a C3 row: 2048 fp16 pages, top-128
+    (1, 8, 2, 300, 257, 64, False, True),
+    (1, 8, 2, 100, 50, 50, False, False),          # k == L
+    (1, 8, 2, 100, 30, 40, False, False),          # k > L: every index, then -1
+    (2, 16, 4, 130, 129, 1, True, False),
+    (1, 4, 1, 4096, 4096, 4000, True, True),       # the longest row
+])
+def test_quest_topk_fused_equals_two_launches(rng, bs, hq, kv, n_max, n, k, fp16_meta, with_valid):
+    """GQA mean + Quest + the row's top-k in one launch (the row's last block
+    selects from the device-coherent scores): raw_q and scores bit-identical
+    to quest_chunk_score_gqa, indices identical to float_topk_3d on them, and
+    to the oracle's; the same over repeated launches on one slots buffer."""
+    from zoomkv_revision_amd.quest import quest_chunk_score_gqa, quest_chunk_topk_gqa
+    from zoomkv_revision_amd.topk import float_topk_3d
+    dt = torch.float16 if fp16_meta else torch.bfloat16
+    g = torch.Generator(device="cuda").manual_seed(n + k)
+    mn = torch.randn(bs, kv, n_max, 128, generator=g, device="cuda").to(dt)
+    mx = (mn.float() + torch.rand(bs, kv, n_max, 128, generator=g, device="cuda")).to(dt)
+    q = torch.randn(bs, hq, 128, generator=g, device="cuda").to(torch.bfloat16)
+    valid = (torch.rand(bs, kv, n_max, generator=g, device="cuda") > 0.05) if with_valid else None
+    s1 = torch.empty(bs, kv, n, device="cuda")
+    rq1 = torch.empty(bs, kv, 128, dtype=torch.bfloat16, device="cuda")
+    quest_chunk_score_gqa(q, kv, mn, mx, s1, n, valid, rq1)
+    if k <= n:
+        want = float_topk_3d(s1, k)
+    else:
+        want = torch.cat([torch.arange(n, device="cuda").expand(bs, kv, n),
+                          torch.full((bs, kv, k - n), -1, dtype=torch.int64, device="cuda")], -1)
+    print(f"[quest topk] bs={bs} kv={kv} n={n} k={k}", flush=True)
+    for rep in range(3):
+        s2 = torch.full((bs, kv, n), float("nan"), device="cuda")
+        rq2 = torch.empty_like(rq1)
+        got = quest_chunk_topk_gqa(q, kv, mn, mx, s2, n, valid, rq2, k)
+        torch.cuda.synchronize()
+        assert torch.equal(rq1.view(torch.int16), rq2.view(torch.int16)), rep
+        assert torch.equal(s1.view(torch.int32), s2.view(torch.int32)), rep
+        assert torch.equal(got, want), rep
+    if k <= n and n <= 300:
+        ref = osel.topk_indices(from_torch(s1), k)
+        assert np.array_equal(np.sort(from_torch(got), -1), np.sort(ref, -1))
+
+
+def test_quest_topk_fused_graph_replays():
+    """The fused launch captured in a HIP graph: every replay, with eager
+    launches on other inputs (other epochs, the same slots buffer) in
+    between, equals the eager result."""
+    from zoomkv_revision_amd.quest import quest_chunk_topk_gqa
+    bs, hq, kv, n, k = 2, 32, 8, 2048, 128
+    g = torch.Generator(device="cuda").manual_seed(3)
+    ins = []
+    for _ in range(2):
+        mn = torch.randn(bs, kv, n, 128, generator=g, device="cuda").to(torch.float16)
+        mx = (mn.float() + torch.rand(bs, kv, n, 128, generator=g, device="cuda")).to(torch.float16)
+        q = torch.randn(bs, hq, 128, generator=g, device="cuda").to(torch.bfloat16)
+        ins.append((q, mn, mx))
+    bufs = [(torch.empty(bs, kv, n, device="cuda"), torch.empty(bs, kv, 128, dtype=torch.bfloat16, device="cuda"),
+             torch.empty(bs, kv, k, dtype=torch.int64, device="cuda")) for _ in range(2)]
+    run = lambda i: quest_chunk_topk_gqa(ins[i][0], kv, ins[i][1], ins[i][2], bufs[i][0], n, None, bufs[i][1], k,
+                                         bufs[i][2])
+    eager = []
+    for i in range(2):
+        run(i)
+        eager.append(bufs[i][2].clone())
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        run(0)
+    for rep in range(4):
+        bufs[0][2].fill_(-7)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(bufs[0][2], eager[0]), f"replay {rep}"
+        run(1)
+        torch.cuda.synchronize()
+        assert torch.equal(bufs[1][2], eager[1]), f"eager after replay {rep}"

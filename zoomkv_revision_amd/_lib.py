@@ -41,6 +41,8 @@ SIGNATURES = {
     "zkv_attention_merge": (I32, [P, I32, I32, I32, I32, P, I32, P]),
     "zkv_quest_chunk_score": (I32, [P, P, P, I32, P, I32, I32, I32, I32, P, P]),
     "zkv_quest_chunk_score_gqa": (I32, [P, I64, I64, I32, P, P, P, I32, P, I32, I32, I32, I32, P, P]),
+    "zkv_quest_chunk_topk_gqa": (I32, [P, I64, I64, I32, P, P, P, I32, P, I32, I32, I32, I32, P, I32, P, I64,
+                                       P, SZ, P]),
     "zkv_topk": (I32, [P, I64, I32, I32, I32, P, I64, P, I64, P, I64, I32, I64, P]),
     "zkv_chunk_density_scores": (I32, [P, I64, I64, P, I64, I64, I64, P, I64, I64, P, I64, I64,
                                        I32, I32, I32, I32, P]),

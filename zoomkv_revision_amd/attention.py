@@ -24,10 +24,13 @@ _WS: dict = {}
 
 
 def _workspace(device, nbytes: int) -> torch.Tensor:
-    key = torch.device(device)
+    """Split partials and arrival slots per (device, stream): calls that may
+    overlap on the device (two streams) never share one."""
+    dev = torch.device(device)
+    key = (dev, torch.cuda.current_stream(dev).cuda_stream)
     ws = _WS.get(key)
     if ws is None or ws.numel() < nbytes:
-        ws = torch.zeros(max(nbytes, 1 << 16), dtype=torch.uint8, device=key)
+        ws = torch.zeros(max(nbytes, 1 << 16), dtype=torch.uint8, device=dev)
         _WS[key] = ws
     return ws
 

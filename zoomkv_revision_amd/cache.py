@@ -53,7 +53,7 @@ from . import kivi
 from .attention import gather_attention
 from .gather import copy_rows, h2d_gather_kv, pinned_empty
 from .quest import load_kernel_module as _load_quest
-from .quest import quest_chunk_score_gqa
+from .quest import QUEST_TOPK_MAX_CHUNKS, quest_chunk_score_gqa, quest_chunk_topk_gqa
 from .rerank import partial_chunk_density_scores_cuda, topk_dense_mask
 from .topk import float_topk_3d, float_topk_gather_concat_3d
 
@@ -426,6 +426,7 @@ class polar_cache:
         bs, kv, dev = self.batch_size, self.kv_head, self.device
         self._cached_scores_view = self._quest_scores_buffer[:bs * kv * n_chunks].view(bs, kv, n_chunks)
         self._cached_cds_n_dense = max(1, int(nk * self.cds_dense_ratio))
+        self._cached_chunk_idx = torch.empty(bs, kv, nk, dtype=torch.int64, device=dev)
         self._cached_dense_mask = torch.zeros(bs, kv, nk, dtype=torch.bool, device=dev)
         self._cached_cds_out_scores = torch.empty(bs, kv, nk * chunk, dtype=torch.float32, device=dev)
         self._cached_cds_out_indices = torch.empty(bs, kv, nk * chunk, dtype=torch.int64, device=dev)
@@ -615,12 +616,20 @@ class polar_cache:
         scores = self._cached_scores_view
         # raw_q = mean over each KV head's query heads (S:1621-1626), formed by
         # the Quest scan (S:2223) itself
-        raw_q = quest_chunk_score_gqa(queries, self.kv_head, self._chunk_key_min_gpu[layer_idx],
-                                      self._chunk_key_max_gpu[layer_idx], scores, n_chunks,
-                                      self._chunk_valid_mask_gpu[layer_idx], self._raw_q)
         # the reference clamps to [0, n_chunks); with nk <= n_chunks every
         # index of the top-k is already inside, so the clamp (a launch) is skipped
-        chunk_idx = float_topk_3d(scores, nk)
+        if n_chunks <= QUEST_TOPK_MAX_CHUNKS:
+            # GQA mean + bounds + top-nk chunks in one launch
+            raw_q = self._raw_q
+            chunk_idx = quest_chunk_topk_gqa(queries, self.kv_head, self._chunk_key_min_gpu[layer_idx],
+                                             self._chunk_key_max_gpu[layer_idx], scores, n_chunks,
+                                             self._chunk_valid_mask_gpu[layer_idx], raw_q, nk,
+                                             self._cached_chunk_idx)
+        else:
+            raw_q = quest_chunk_score_gqa(queries, self.kv_head, self._chunk_key_min_gpu[layer_idx],
+                                          self._chunk_key_max_gpu[layer_idx], scores, n_chunks,
+                                          self._chunk_valid_mask_gpu[layer_idx], self._raw_q)
+            chunk_idx = float_topk_3d(scores, nk)
         dense_topk = max(1, min(self.cds_dense_topk, chunk))
         sparse_topk = max(1, min(self.cds_sparse_topk, chunk))
         dense_mask = self._cached_dense_mask

@@ -710,16 +710,9 @@ __device__ __forceinline__ void merge_splits_last(const AttnParams& p, int64_t b
     // fence variant: the workgroup's plain stores, ordered before this lane
     // by the barrier, are released at agent scope (an L2 writeback)
     if (p.merge_fence) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    unsigned long long* slot = p.slots + bh;
-    unsigned long long old = (p.epoch << 8) | static_cast<unsigned long long>(p.n_splits - 1);
-    unsigned long long nv = old + 1;
-    while (!__hip_atomic_compare_exchange_strong(slot, &old, nv, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
-                                                 __HIP_MEMORY_SCOPE_AGENT))
-      nv = (old >> 8) == p.epoch ? old + 1 : ((p.epoch << 8) | 1ull);
-    const bool last = (nv & 0xffull) == static_cast<unsigned long long>(p.n_splits);
-    // the last arrival leaves the count at 0 under this epoch, so a replay of
-    // the same launch (a captured graph keeps its epoch) counts from 0 again
-    if (last) __hip_atomic_store(slot, p.epoch << 8, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // (the last arrival leaves the count at 0 under this epoch, so a replay
+    // of the same launch, a captured graph keeps its epoch, counts from 0)
+    const bool last = arrive_last(p.slots + bh, p.epoch, p.n_splits);
     if (last && p.merge_fence) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     *s_last = last;
   }
@@ -1510,26 +1503,6 @@ bool merge_with_fence() {
   return e && strcmp(e, "fence") == 0;
 }
 
-// Epoch of a merging launch (56 bits): bit 55 set, the low 55 bits a random
-// per-process base plus a launch counter, so distinct for every launch of the
-// process.  A slot is (epoch << 8) | count, whose bit 63 is therefore set: no
-// non-negative int64 a reused workspace may hold (a token index, a count, a
-// small integer of the form (e << 8) | c) can read as a slot of a live
-// launch, and another process's slots or arbitrary bytes match a given
-// launch's epoch with probability 2^-55.
-unsigned long long next_epoch() {
-  static const unsigned long long base = [] {
-    std::random_device rd;
-    const unsigned long long hi = rd(), lo = rd();
-    const unsigned long long t = static_cast<unsigned long long>(
-        std::chrono::steady_clock::now().time_since_epoch().count());
-    return (hi << 32) ^ lo ^ (t * 0x9E3779B97F4A7C15ull);
-  }();
-  static std::atomic<unsigned long long> counter{0};
-  constexpr unsigned long long kLow55 = (1ull << 55) - 1;
-  const unsigned long long n = counter.fetch_add(1, std::memory_order_relaxed) + 1;
-  return ((base + n) & kLow55) | (1ull << 55);
-}
 
 // Token-list shape: the rank sort's LDS (12 KiB) beside a 3-stage ring of
 // whole records (8 x 3 x 5 KiB); a wave holds one or two tiles at C5.
@@ -1976,3 +1949,29 @@ extern "C" int zkv_bf16_gather_attention(const uint16_t* q, int64_t q_sb, int64_
                           kv, 0, n_idx + tail_len, sm_scale, n_splits, workspace, workspace_bytes, nullptr, out,
                           out_f32, reinterpret_cast<hipStream_t>(stream), nullptr, &rl, lse, &ri);
 }
+
+// ---- epochs of the in-launch arrival counts (declared in zkv_common.hpp) ----
+namespace zkv {
+
+// Epoch of a merging launch (56 bits): bit 55 set, the low 55 bits a random
+// per-process base plus a launch counter, so distinct for every launch of the
+// process.  A slot is (epoch << 8) | count, whose bit 63 is therefore set: no
+// non-negative int64 a reused workspace may hold (a token index, a count, a
+// small integer of the form (e << 8) | c) can read as a slot of a live
+// launch, and another process's slots or arbitrary bytes match a given
+// launch's epoch with probability 2^-55.
+unsigned long long next_epoch() {
+  static const unsigned long long base = [] {
+    std::random_device rd;
+    const unsigned long long hi = rd(), lo = rd();
+    const unsigned long long t = static_cast<unsigned long long>(
+        std::chrono::steady_clock::now().time_since_epoch().count());
+    return (hi << 32) ^ lo ^ (t * 0x9E3779B97F4A7C15ull);
+  }();
+  static std::atomic<unsigned long long> counter{0};
+  constexpr unsigned long long kLow55 = (1ull << 55) - 1;
+  const unsigned long long n = counter.fetch_add(1, std::memory_order_relaxed) + 1;
+  return ((base + n) & kLow55) | (1ull << 55);
+}
+
+}  // namespace zkv

@@ -673,6 +673,140 @@ __global__ __launch_bounds__(kTopkThreads) void topk_reg_kernel(
 }
 
 // ----------------------------------------------------------------------------
+// GQA mean + Quest bounds + the row's top-k in one launch
+// (S:1621-1626 + S:2223 + the float_topk_3d of S:2168-2190).  A 1024-thread
+// block scores 32 * kQuestUnroll chunks of one (b, kv) row with the
+// arithmetic of quest_gqa_kernel (so the scores are the same bits), stores
+// them device-coherently (write-through) and counts itself in on the row's
+// arrival slot; the block that completes the row reads the row's scores back
+// with device-coherent loads and runs topk_reg_kernel<4>'s radix select and
+// ordered emit on them (the same indices, in increasing index order).  The
+// other rows' scans hide the selection, and one launch disappears.
+// ----------------------------------------------------------------------------
+constexpr int kQuestTopkChunks = 32 * kQuestUnroll;  // chunks per 1024-thread block
+constexpr int kQuestTopkMaxL = 4 * kTopkThreads;       // rows up to 4096 chunks (4 registers)
+
+template <bool kFp16Meta>
+__global__ __launch_bounds__(kTopkThreads) void quest_topk_kernel(
+    const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_sh, int group, int kv,
+    uint16_t* __restrict__ raw_q_out, const uint16_t* __restrict__ cmin, const uint16_t* __restrict__ cmax,
+    const uint8_t* __restrict__ valid, float* __restrict__ scores, int n_chunks, int n_max, int k,
+    int64_t* __restrict__ out, int64_t out_stride, unsigned long long* __restrict__ slots,
+    unsigned long long epoch) {
+  constexpr int U = kQuestUnroll;
+  __shared__ uint16_t s_q[128];
+  __shared__ __align__(16) int s_hist[2][256];
+  __shared__ __align__(16) uint32_t s_cnt[4 * kTopkWaves];
+  __shared__ int s_sel[2];
+  __shared__ int s_last;
+  const int tid = threadIdx.x, half = tid >> 5, t = tid & 31;
+  const int bh = blockIdx.y;
+  const int c0 = (blockIdx.x * 32 + half) * U;
+  u32x2_t mv[U], xv[U];
+  int row[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int chunk = min(c0 + u, n_chunks - 1);  // past the end re-reads the last chunk
+    row[u] = chunk;
+    const int64_t off = (static_cast<int64_t>(bh) * n_max + chunk) * 128 + 4 * t;
+    mv[u] = *reinterpret_cast<const u32x2_t*>(cmin + off);
+    xv[u] = *reinterpret_cast<const u32x2_t*>(cmax + off);
+  }
+  if (tid < 128) {
+    const int b = bh / kv, h = bh - b * kv, d = tid;
+    const uint16_t* qp = q + b * q_sb + static_cast<int64_t>(h) * group * q_sh + d;
+    constexpr int kRows = 8;  // head rows requested together, summed in head order
+    uint16_t w[kRows];
+#pragma unroll
+    for (int i = 0; i < kRows; ++i) w[i] = qp[min(i, group - 1) * q_sh];
+    float acc = bf16_to_f32(w[0]);
+#pragma unroll
+    for (int i = 1; i < kRows; ++i)
+      if (i < group) acc = acc + bf16_to_f32(w[i]);
+    for (int i = kRows; i < group; ++i) acc = acc + bf16_to_f32(qp[i * q_sh]);
+    const uint16_t r = f32_to_bf16_bits(acc / static_cast<float>(group));
+    s_q[d] = r;
+    if (blockIdx.x == 0) raw_q_out[static_cast<int64_t>(bh) * 128 + d] = r;
+  }
+  if (tid < 128) reinterpret_cast<int4*>(&s_hist[0][0])[tid] = make_int4(0, 0, 0, 0);
+  __syncthreads();
+  const u32x2_t qv = *reinterpret_cast<const u32x2_t*>(s_q + 4 * t);
+  float qq[4];
+  qq[0] = __uint_as_float(qv[0] << 16);
+  qq[1] = __uint_as_float(qv[0] & 0xFFFF0000u);
+  qq[2] = __uint_as_float(qv[1] << 16);
+  qq[3] = __uint_as_float(qv[1] & 0xFFFF0000u);
+  float sum[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    float mn[4], mx[4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      mn[2 * i] = meta_to_f32<kFp16Meta>(static_cast<uint16_t>(mv[u][i] & 0xFFFF));
+      mn[2 * i + 1] = meta_to_f32<kFp16Meta>(static_cast<uint16_t>(mv[u][i] >> 16));
+      mx[2 * i] = meta_to_f32<kFp16Meta>(static_cast<uint16_t>(xv[u][i] & 0xFFFF));
+      mx[2 * i + 1] = meta_to_f32<kFp16Meta>(static_cast<uint16_t>(xv[u][i] >> 16));
+    }
+    float sm = fmaxf(qq[0] * mn[0], qq[0] * mx[0]);
+    sm = sm + fmaxf(qq[1] * mn[1], qq[1] * mx[1]);
+    sm = sm + fmaxf(qq[2] * mn[2], qq[2] * mx[2]);
+    sm = sm + fmaxf(qq[3] * mn[3], qq[3] * mx[3]);
+    sum[u] = sm;
+  }
+#pragma unroll
+  for (int off = 16; off > 0; off >>= 1)
+#pragma unroll
+    for (int u = 0; u < U; ++u) sum[u] = sum[u] + __shfl_xor(sum[u], off);
+  float* srow = scores + static_cast<int64_t>(bh) * n_chunks;
+  if (t < U) {
+    float o = sum[0];
+    int r = row[0];
+#pragma unroll
+    for (int u = 1; u < U; ++u)
+      if (t == u) {
+        o = sum[u];
+        r = row[u];
+      }
+    const int chunk = c0 + t;
+    if (chunk < n_chunks) {
+      const int64_t vr = static_cast<int64_t>(bh) * n_max + r;
+      if (valid != nullptr && !valid[vr]) o = -INFINITY;
+      // device-coherent (write-through): the row's selecting block may run
+      // on another XCD
+      __hip_atomic_store(srow + chunk, o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  // this lane's score stores are device-visible, then one arrival per block
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (tid == 0) s_last = arrive_last(slots + bh, epoch, gridDim.x);
+  __syncthreads();
+  if (!s_last) return;
+
+  // ---- the row's top-k: topk_reg_kernel<4> on the stored scores ----
+  const int L = n_chunks, wave = tid >> 6;
+  int64_t* o = out + static_cast<int64_t>(bh) * out_stride;
+  if (L <= k) {
+    for (int i = tid; i < k; i += kTopkThreads) o[i] = i < L ? i : -1;
+    return;
+  }
+  constexpr int R = 4;
+  float v[R];
+#pragma unroll
+  for (int j = 0; j < R; ++j)
+    v[j] = __hip_atomic_load(srow + kTopkThreads * j + min(tid, L - 1 - kTopkThreads * j), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+  uint32_t key[R];
+#pragma unroll
+  for (int j = 0; j < R; ++j)
+    key[j] = ordered_key_bits(tid < L - kTopkThreads * j ? __float_as_uint(v[j]) : ~0u);
+  (void)wave;
+  int remain;
+  const uint32_t T = radix_select<R>(key, L, k, s_hist, s_sel, remain);
+  ordered_emit<R>(key, L, k, T, remain, s_cnt, [&](int pos, int i) { o[pos] = i; });
+}
+
+// ----------------------------------------------------------------------------
 // CDS density: centroid[chunk_id] . q (rerank_topk.cu:560-624): buf[t] = c[t]q[t]
 // for t < 128, then buf[t] += buf[t+s], s = 64..1; invalid id -> -1e30.
 // A wave scores kDensityItems slots (lane l starts with p[l] + p[l+64] of
@@ -1088,6 +1222,37 @@ extern "C" int zkv_quest_chunk_score_gqa(const uint16_t* q, int64_t q_sb, int64_
   else
     launch(std::integral_constant<int, 4>{});
   return check_launch("quest_gqa_kernel");
+}
+
+extern "C" int zkv_quest_chunk_topk_gqa(const uint16_t* q, int64_t q_sb, int64_t q_sh, int hq, uint16_t* raw_q,
+                                        const uint16_t* chunk_min, const uint16_t* chunk_max, int meta_fp16,
+                                        float* scores, int bs, int kv, int n_chunks, int n_chunks_max,
+                                        const uint8_t* valid, int k, int64_t* out, int64_t out_stride,
+                                        void* slots, size_t slots_bytes, zkv_stream_t stream) {
+  ZKV_REQUIRE(q && raw_q && chunk_min && chunk_max && scores && out && slots,
+              "zkv_quest_chunk_topk_gqa: null pointer");
+  ZKV_REQUIRE(bs > 0 && kv > 0 && hq > 0 && hq % kv == 0 && n_chunks >= 1 && n_chunks <= n_chunks_max &&
+                  n_chunks <= kQuestTopkMaxL && static_cast<int64_t>(bs) * kv <= 65535,
+              "zkv_quest_chunk_topk_gqa: bad sizes bs=%d hq=%d kv=%d n_chunks=%d (at most %d) n_chunks_max=%d", bs,
+              hq, kv, n_chunks, kQuestTopkMaxL, n_chunks_max);
+  ZKV_REQUIRE(k >= 1 && out_stride >= k, "zkv_quest_chunk_topk_gqa: k=%d out_stride=%lld", k,
+              static_cast<long long>(out_stride));
+  ZKV_REQUIRE((reinterpret_cast<uintptr_t>(slots) & 7) == 0 && slots_bytes >= static_cast<size_t>(bs) * kv * 8,
+              "zkv_quest_chunk_topk_gqa: slots need %zu bytes, 8-byte aligned (got %zu)",
+              static_cast<size_t>(bs) * kv * 8, slots_bytes);
+  auto s = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid((n_chunks + kQuestTopkChunks - 1) / kQuestTopkChunks, bs * kv);
+  auto* sl = static_cast<unsigned long long*>(slots);
+  const unsigned long long epoch = next_epoch();
+  if (meta_fp16)
+    quest_topk_kernel<true><<<grid, kTopkThreads, 0, s>>>(q, q_sb, q_sh, hq / kv, kv, raw_q, chunk_min, chunk_max,
+                                                          valid, scores, n_chunks, n_chunks_max, k, out, out_stride,
+                                                          sl, epoch);
+  else
+    quest_topk_kernel<false><<<grid, kTopkThreads, 0, s>>>(q, q_sb, q_sh, hq / kv, kv, raw_q, chunk_min,
+                                                           chunk_max, valid, scores, n_chunks, n_chunks_max, k, out,
+                                                           out_stride, sl, epoch);
+  return check_launch("quest_topk_kernel");
 }
 
 extern "C" int zkv_quest_chunk_score(const uint16_t* q, const uint16_t* chunk_min,

@@ -113,4 +113,31 @@ __device__ __forceinline__ void nibbles_to_half_pairs(uint32_t w, half2_t out[4]
   out[3] = __builtin_elementwise_fma(d, four, m64);
 }
 
+// ---------------------------------------------------------------------------
+// In-launch arrival counts: the workgroups of one unit of work (the context
+// splits of one (b, kv) attention, the score blocks of one top-k row) count
+// themselves in on an 8-byte slot (epoch << 8) | count with one
+// compare-and-swap each; the one that completes the count does the unit's
+// final step.  A slot holding another epoch (an earlier launch, stale bytes)
+// counts as empty, so slots need no zeroing; the last arrival leaves the
+// count at 0 under its epoch, so a captured graph (which keeps its epoch)
+// counts from 0 again on replay.  Epochs (next_epoch, host side, defined in
+// decode_attention.hip) have bit 55 set and a random per-process base.
+// ---------------------------------------------------------------------------
+unsigned long long next_epoch();
+
+// Called by one thread per arriving workgroup, after the workgroup's results
+// are device-visible; true for the n-th arrival.  The first attempt expects
+// the count one short of complete, so the last arrival needs one round trip.
+__device__ __forceinline__ bool arrive_last(unsigned long long* slot, unsigned long long epoch, int n) {
+  unsigned long long old = (epoch << 8) | static_cast<unsigned long long>(n - 1);
+  unsigned long long nv = old + 1;
+  while (!__hip_atomic_compare_exchange_strong(slot, &old, nv, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT))
+    nv = (old >> 8) == epoch ? old + 1 : ((epoch << 8) | 1ull);
+  const bool last = (nv & 0xffull) == static_cast<unsigned long long>(n);
+  if (last) __hip_atomic_store(slot, epoch << 8, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return last;
+}
+
 }  // namespace zkv

@@ -215,8 +215,10 @@ _WORKSPACE: dict = {}
 
 
 def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """Per-device attention workspace (split partials), grown on demand."""
-    key = (device.type, device.index)
+    """Attention workspace (split partials and arrival slots) per (device,
+    stream), grown on demand: calls on one stream run in order, and calls on
+    two streams, which may overlap on the device, get two workspaces."""
+    key = (device.type, device.index, torch.cuda.current_stream(device).cuda_stream)
     ws = _WORKSPACE.get(key)
     if ws is None or ws.numel() < nbytes:
         ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)

@@ -118,6 +118,70 @@ def quest_chunk_score_gqa(queries: torch.Tensor, kv_heads: int, chunk_min: torch
     return raw_q
 
 
+QUEST_TOPK_MAX_CHUNKS = 4096     # rows the fused scan + top-k launch takes
+_SLOTS: dict = {}
+
+
+def _slots(device: torch.device, n: int) -> torch.Tensor:
+    """Arrival slots of the fused launch per (device, stream): concurrent
+    launches never share one (contents need no zeroing)."""
+    key = (device, torch.cuda.current_stream(device).cuda_stream)
+    t = _SLOTS.get(key)
+    if t is None or t.numel() < n:
+        t = torch.zeros(max(n, 256), dtype=torch.int64, device=device)
+        _SLOTS[key] = t
+    return t
+
+
+def quest_chunk_topk_gqa(queries: torch.Tensor, kv_heads: int, chunk_min: torch.Tensor,
+                         chunk_max: torch.Tensor, scores: torch.Tensor, n_chunks: int,
+                         valid: torch.Tensor | None, raw_q: torch.Tensor, k: int,
+                         out: torch.Tensor | None = None) -> torch.Tensor:
+    """``quest_chunk_score_gqa`` and ``float_topk_3d(scores, k)`` in one launch:
+    GQA-mean query, Quest bounds (written to ``scores``, the same bits) and the
+    top-k chunk indices of every (b, kv) row, int64 [bs, kv, k] in increasing
+    index order (the same indices as float_topk_3d; -1 past n_chunks when
+    k > n_chunks).  Rows of up to 4096 chunks.  ``out`` (optional, int64
+    [bs, kv, >= k] with a contiguous last dim) receives the indices; returns
+    them."""
+    q = queries.reshape(queries.shape[0], -1, queries.shape[-1]) if queries.dim() == 4 else queries
+    require_gpu(q, chunk_min, chunk_max, scores, raw_q)
+    bs, hq, _ = q.shape
+    kv = int(kv_heads)
+    n_max = chunk_min.shape[2]
+    n_chunks, k = int(n_chunks), int(k)
+    if not 1 <= n_chunks <= min(n_max, QUEST_TOPK_MAX_CHUNKS):
+        raise RuntimeError(f"quest_chunk_topk_gqa: n_chunks={n_chunks} outside [1, {min(n_max, QUEST_TOPK_MAX_CHUNKS)}]")
+    if not 1 <= k:
+        raise RuntimeError(f"quest_chunk_topk_gqa: k={k}")
+    # the shape / dtype checks of quest_chunk_score_gqa
+    if q.dtype != torch.bfloat16 or raw_q.dtype != torch.bfloat16 or q.shape[-1] != 128 or q.stride(-1) != 1:
+        raise RuntimeError("quest_chunk_topk_gqa: queries and raw_q must be bf16 with head_dim 128")
+    if hq % kv or tuple(raw_q.shape) != (bs, kv, 128) or not raw_q.is_contiguous():
+        raise RuntimeError("quest_chunk_topk_gqa: raw_q must be a contiguous [bs, kv, 128] with kv | hq")
+    if chunk_min.dtype != chunk_max.dtype or chunk_min.dtype not in (torch.bfloat16, torch.float16):
+        raise RuntimeError("quest_chunk_topk_gqa: chunk_min / chunk_max must both be bf16 or fp16")
+    if tuple(chunk_min.shape) != (bs, kv, n_max, 128) or chunk_max.shape != chunk_min.shape \
+            or not chunk_min.is_contiguous() or not chunk_max.is_contiguous():
+        raise RuntimeError("chunk_min / chunk_max must be contiguous [bs, kv, n_chunks_max, 128]")
+    if scores.dtype != torch.float32 or scores.numel() != bs * kv * n_chunks or not scores.is_contiguous():
+        raise RuntimeError("scores must be fp32 [bs, kv, n_chunks]")
+    if valid is not None:
+        if valid.dtype != torch.bool or not valid.is_contiguous() or tuple(valid.shape) != (bs, kv, n_max):
+            raise RuntimeError("valid must be a contiguous bool [bs, kv, n_chunks_max]")
+    if out is None:
+        out = torch.empty(bs, kv, k, dtype=torch.int64, device=q.device)
+    elif out.dtype != torch.int64 or tuple(out.shape[:2]) != (bs, kv) or out.shape[2] < k or out.stride(2) != 1 \
+            or out.stride(0) != kv * out.stride(1):
+        raise RuntimeError("out must be int64 [bs, kv, >= k] with rows at one stride")
+    sl = _slots(q.device, bs * kv)
+    check(lib().zkv_quest_chunk_topk_gqa(
+        ptr(q), q.stride(0), q.stride(1), hq, ptr(raw_q), ptr(chunk_min), ptr(chunk_max),
+        int(chunk_min.dtype == torch.float16), ptr(scores), bs, kv, n_chunks, n_max, ptr(valid), k,
+        ptr(out), out.stride(1), ptr(sl), sl.numel() * 8, stream_of(q)))
+    return out[:, :, :k]
+
+
 class QuestKernel:
     """Drop-in for the module ``quest_ops.load_kernel_module()`` returns."""
 
