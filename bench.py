@@ -495,30 +495,33 @@ def run_c3(args):
     import numpy as np
     import torch
     from zoomkv_revision_amd import kivi, synthetic
-    from zoomkv_revision_amd.quest import quest_chunk_score_gqa
-    from zoomkv_revision_amd.topk import float_topk_3d
+    from zoomkv_revision_amd.quest import quest_chunk_topk_gqa
     bs, hq, kv, n_tok, n_sel = 8, 32, 8, 32768, 128
     dev = torch.device("cuda:0")
     ws = [synthetic.c3_workload(100 + i, bs, hq, kv, n_tok, n_sel, dev) for i in range(8)]
     n_pages = ws[0]["n_pages"]
     scores = torch.empty(bs, kv, n_pages, device=dev)
     raw_q = torch.empty(bs, kv, 128, dtype=torch.bfloat16, device=dev)
+    sels = [torch.empty(bs, kv, n_sel, dtype=torch.int64, device=dev) for _ in range(2)]
     out = torch.empty(bs, hq, 128, dtype=torch.bfloat16, device=dev)
     sel_ok = []
 
+    def select(i):
+        # GQA mean + Quest bounds + top-128 pages: one launch
+        w = ws[i % len(ws)]
+        return quest_chunk_topk_gqa(w["q"], kv, w["page_min"], w["page_max"], scores, n_pages, None, raw_q, n_sel,
+                                    sels[i % 2])
+
     def step(i):
         w = ws[i % len(ws)]
-        quest_chunk_score_gqa(w["q"], kv, w["page_min"], w["page_max"], scores, n_pages, None, raw_q)
-        sel = float_topk_3d(scores, n_sel)
+        sel = select(i)
         kivi.kivi4_sparse_attention(w["q"], w["cache"], sel, out=out)
         if i < len(ws):
-            sel_ok.append(sel)
+            sel_ok.append(sel.clone())
 
     ms = timed_loop(step, args.steps, args.warmup)
-    w0 = ws[0]
-    k_ms = kernel_batch_ms(lambda i: quest_chunk_score_gqa(w0["q"], kv, ws[i % len(ws)]["page_min"],
-                                                           ws[i % len(ws)]["page_max"], scores, n_pages,
-                                                           None, raw_q), args.steps)
+    step_ms = kernel_batch_ms(step, args.steps, host_us=60)
+    k_ms = kernel_batch_ms(select, args.steps)
     sa_ms = kernel_batch_ms(lambda i: kivi.kivi4_sparse_attention(ws[i % len(ws)]["q"], ws[i % len(ws)]["cache"],
                                                                   ws[i % len(ws)]["planted"], out=out),
                             args.steps, host_us=30)
@@ -534,16 +537,22 @@ def run_c3(args):
         "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "fp16 metadata / u4->fp16 (fp32 accumulate)",
         "data": "synthetic (planted pages)",
-        "config": {"workload": "C3: GQA mean + Quest (fp16 page min/max, one launch) -> top-128 of "
-                               "2048 pages -> page-sparse 4-bit attention", "batch": bs, "q_heads": hq,
+        "config": {"workload": "C3: GQA mean + Quest (fp16 page min/max) + top-128 of 2048 pages (one "
+                               "launch) -> page-sparse 4-bit attention", "batch": bs, "q_heads": hq,
                    "kv_heads": kv, "context": n_tok, "page_tokens": 16, "pages_selected": n_sel,
                    "parallelism": "single GPU"},
         "selection_equals_planted": exact,
         "end_to_end_GBps": nb["total"] / (ms * 1e-3) / 1e9,
+        # the step's longest kernel: the fused GQA mean + Quest bounds + top-128
+        # launch over the fp16 page metadata
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel": "quest_gqa_kernel",
-                     "kernel_ms": k_ms, "algorithmic_bytes": nb["quest"]},
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": read_traffic("c3_quest_topk_traffic.json"),
+                     "kernel": "quest_topk_kernel (GQA mean + Quest + top-128 pages)", "kernel_ms": k_ms,
+                     "algorithmic_bytes": nb["quest"]},
         "algorithmic_bytes_per_step": nb,
+        # device time of back-to-back steps (two launches each)
+        "step_device_ms": step_ms,
+        "step_GBps": nb["total"] / (step_ms * 1e-3) / 1e9,
         # the longest kernel of the step: latency-bound (a wave's ~4 page
         # tiles arrive together after the page walk), so below its HBM line
         "sparse_attention": {"kernel_ms": sa_ms, "algorithmic_bytes": nb["sparse_attention"],

@@ -198,6 +198,22 @@ int zkv_quest_chunk_score_gqa(const uint16_t* q, int64_t q_sb, int64_t q_sh, int
                               float* scores, int bs, int kv, int n_chunks, int n_chunks_max,
                               const uint8_t* valid, zkv_stream_t stream);
 
+/* zkv_quest_chunk_score_gqa and the row's exact top-k in one launch: the
+ * float_topk_3d call of S:2168-2190 (Z/cache_hub/float_topk/float_topk.cu:51-271
+ * semantics, as zkv_topk) on the scores just formed.  No counterpart of its
+ * own in the reference.  out int64 [bs, kv, >= k] at row stride out_stride:
+ * the k chunk indices of the largest scores in increasing index order (ties to
+ * the lower index); rows with n_chunks <= k get 0 .. n_chunks - 1, then -1.
+ * scores is still written (fp32 [bs, kv, n_chunks]).  1 <= n_chunks <= 4096.
+ * slots: >= 4 * bs * kv bytes of arrival counters, zeroed once before the
+ * first call and left zero by every call; calls that overlap on one slots
+ * buffer race. */
+int zkv_quest_chunk_topk_gqa(const uint16_t* q, int64_t q_sb, int64_t q_sh, int hq, uint16_t* raw_q,
+                             const uint16_t* chunk_min, const uint16_t* chunk_max, int meta_fp16,
+                             float* scores, int bs, int kv, int n_chunks, int n_chunks_max,
+                             const uint8_t* valid, int k, int64_t* out, int64_t out_stride,
+                             void* slots, size_t slots_bytes, zkv_stream_t stream);
+
 /* Exact top-k of each of `rows` rows of L fp32 scores (row i at
  * scores + i*in_stride): out[i, 0..k) = the indices (or lut[i, index] when lut
  * != NULL) of the k largest scores, ties by lowest index, in increasing index

@@ -675,24 +675,27 @@ __global__ __launch_bounds__(kTopkThreads) void topk_reg_kernel(
 // ----------------------------------------------------------------------------
 // GQA mean + Quest bounds + the row's top-k in one launch
 // (S:1621-1626 + S:2223 + the float_topk_3d of S:2168-2190).  A 1024-thread
-// block scores 32 * kQuestUnroll chunks of one (b, kv) row with the
-// arithmetic of quest_gqa_kernel (so the scores are the same bits), stores
-// them device-coherently (write-through) and counts itself in on the row's
-// arrival slot; the block that completes the row reads the row's scores back
-// with device-coherent loads and runs topk_reg_kernel<4>'s radix select and
-// ordered emit on them (the same indices, in increasing index order).  The
-// other rows' scans hide the selection, and one launch disappears.
+// block scores TR trips of 32 * kQuestUnroll chunks of one (b, kv) row (all
+// trips' loads issued first) with the arithmetic of quest_gqa_kernel (so the
+// scores are the same bits), stores them device-coherently (write-through)
+// and counts itself in on the row's arrival slot.  The arrival is one
+// fetch-and-add (the blocks of a row finish close together; compare-and-swap
+// retries serialised them, 41 us against 27 at 64 rows x 2048 chunks), and TR
+// is chosen so that the grid is one wave of blocks: each block waits for its
+// stores' acknowledgement once (27 us with 1024 blocks, 20 with 512 of two
+// trips).  The block that completes the row reads the row's scores back with
+// device-coherent loads and runs topk_reg_kernel<4>'s radix select and
+// ordered emit on them (the same indices, in increasing index order).
 // ----------------------------------------------------------------------------
-constexpr int kQuestTopkChunks = 32 * kQuestUnroll;  // chunks per 1024-thread block
+constexpr int kQuestTopkChunks = 32 * kQuestUnroll;  // chunks per 1024-thread block per trip
 constexpr int kQuestTopkMaxL = 4 * kTopkThreads;       // rows up to 4096 chunks (4 registers)
 
-template <bool kFp16Meta>
+template <bool kFp16Meta, int TR>
 __global__ __launch_bounds__(kTopkThreads) void quest_topk_kernel(
     const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_sh, int group, int kv,
     uint16_t* __restrict__ raw_q_out, const uint16_t* __restrict__ cmin, const uint16_t* __restrict__ cmax,
     const uint8_t* __restrict__ valid, float* __restrict__ scores, int n_chunks, int n_max, int k,
-    int64_t* __restrict__ out, int64_t out_stride, unsigned long long* __restrict__ slots,
-    unsigned long long epoch) {
+    int64_t* __restrict__ out, int64_t out_stride, unsigned int* __restrict__ slots) {
   constexpr int U = kQuestUnroll;
   __shared__ uint16_t s_q[128];
   __shared__ __align__(16) int s_hist[2][256];
@@ -701,17 +704,18 @@ __global__ __launch_bounds__(kTopkThreads) void quest_topk_kernel(
   __shared__ int s_last;
   const int tid = threadIdx.x, half = tid >> 5, t = tid & 31;
   const int bh = blockIdx.y;
-  const int c0 = (blockIdx.x * 32 + half) * U;
-  u32x2_t mv[U], xv[U];
-  int row[U];
+  // trip r of this block covers chunks [(x TR + r) 128, +128); every trip's
+  // loads are issued before any score is formed
+  u32x2_t mv[TR][U], xv[TR][U];
 #pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const int chunk = min(c0 + u, n_chunks - 1);  // past the end re-reads the last chunk
-    row[u] = chunk;
-    const int64_t off = (static_cast<int64_t>(bh) * n_max + chunk) * 128 + 4 * t;
-    mv[u] = *reinterpret_cast<const u32x2_t*>(cmin + off);
-    xv[u] = *reinterpret_cast<const u32x2_t*>(cmax + off);
-  }
+  for (int r = 0; r < TR; ++r)
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int chunk = min(((blockIdx.x * TR + r) * 32 + half) * U + u, n_chunks - 1);  // past the end re-reads
+      const int64_t off = (static_cast<int64_t>(bh) * n_max + chunk) * 128 + 4 * t;
+      mv[r][u] = *reinterpret_cast<const u32x2_t*>(cmin + off);
+      xv[r][u] = *reinterpret_cast<const u32x2_t*>(cmax + off);
+    }
   if (tid < 128) {
     const int b = bh / kv, h = bh - b * kv, d = tid;
     const uint16_t* qp = q + b * q_sb + static_cast<int64_t>(h) * group * q_sh + d;
@@ -736,50 +740,49 @@ __global__ __launch_bounds__(kTopkThreads) void quest_topk_kernel(
   qq[1] = __uint_as_float(qv[0] & 0xFFFF0000u);
   qq[2] = __uint_as_float(qv[1] << 16);
   qq[3] = __uint_as_float(qv[1] & 0xFFFF0000u);
-  float sum[U];
-#pragma unroll
-  for (int u = 0; u < U; ++u) {
-    float mn[4], mx[4];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      mn[2 * i] = meta_to_f32<kFp16Meta>(static_cast<uint16_t>(mv[u][i] & 0xFFFF));
-      mn[2 * i + 1] = meta_to_f32<kFp16Meta>(static_cast<uint16_t>(mv[u][i] >> 16));
-      mx[2 * i] = meta_to_f32<kFp16Meta>(static_cast<uint16_t>(xv[u][i] & 0xFFFF));
-      mx[2 * i + 1] = meta_to_f32<kFp16Meta>(static_cast<uint16_t>(xv[u][i] >> 16));
-    }
-    float sm = fmaxf(qq[0] * mn[0], qq[0] * mx[0]);
-    sm = sm + fmaxf(qq[1] * mn[1], qq[1] * mx[1]);
-    sm = sm + fmaxf(qq[2] * mn[2], qq[2] * mx[2]);
-    sm = sm + fmaxf(qq[3] * mn[3], qq[3] * mx[3]);
-    sum[u] = sm;
-  }
-#pragma unroll
-  for (int off = 16; off > 0; off >>= 1)
-#pragma unroll
-    for (int u = 0; u < U; ++u) sum[u] = sum[u] + __shfl_xor(sum[u], off);
   float* srow = scores + static_cast<int64_t>(bh) * n_chunks;
-  if (t < U) {
-    float o = sum[0];
-    int r = row[0];
 #pragma unroll
-    for (int u = 1; u < U; ++u)
-      if (t == u) {
-        o = sum[u];
-        r = row[u];
+  for (int r = 0; r < TR; ++r) {
+    const int c0 = ((blockIdx.x * TR + r) * 32 + half) * U;
+    float sum[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float mn[4], mx[4];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        mn[2 * i] = meta_to_f32<kFp16Meta>(static_cast<uint16_t>(mv[r][u][i] & 0xFFFF));
+        mn[2 * i + 1] = meta_to_f32<kFp16Meta>(static_cast<uint16_t>(mv[r][u][i] >> 16));
+        mx[2 * i] = meta_to_f32<kFp16Meta>(static_cast<uint16_t>(xv[r][u][i] & 0xFFFF));
+        mx[2 * i + 1] = meta_to_f32<kFp16Meta>(static_cast<uint16_t>(xv[r][u][i] >> 16));
       }
-    const int chunk = c0 + t;
-    if (chunk < n_chunks) {
-      const int64_t vr = static_cast<int64_t>(bh) * n_max + r;
-      if (valid != nullptr && !valid[vr]) o = -INFINITY;
-      // device-coherent (write-through): the row's selecting block may run
-      // on another XCD
-      __hip_atomic_store(srow + chunk, o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      float sm = fmaxf(qq[0] * mn[0], qq[0] * mx[0]);
+      sm = sm + fmaxf(qq[1] * mn[1], qq[1] * mx[1]);
+      sm = sm + fmaxf(qq[2] * mn[2], qq[2] * mx[2]);
+      sm = sm + fmaxf(qq[3] * mn[3], qq[3] * mx[3]);
+      sum[u] = sm;
+    }
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1)
+#pragma unroll
+      for (int u = 0; u < U; ++u) sum[u] = sum[u] + __shfl_xor(sum[u], off);
+    if (t < U) {
+      float o = sum[0];
+#pragma unroll
+      for (int u = 1; u < U; ++u)
+        if (t == u) o = sum[u];
+      const int chunk = c0 + t;
+      if (chunk < n_chunks) {
+        if (valid != nullptr && !valid[static_cast<int64_t>(bh) * n_max + chunk]) o = -INFINITY;
+        // device-coherent (write-through): the row's selecting block may run
+        // on another XCD
+        __hip_atomic_store(srow + chunk, o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
     }
   }
   // this lane's score stores are device-visible, then one arrival per block
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  if (tid == 0) s_last = arrive_last(slots + bh, epoch, gridDim.x);
+  if (tid == 0) s_last = arrive_last_count(slots + bh, gridDim.x);
   __syncthreads();
   if (!s_last) return;
 
@@ -1237,21 +1240,34 @@ extern "C" int zkv_quest_chunk_topk_gqa(const uint16_t* q, int64_t q_sb, int64_t
               hq, kv, n_chunks, kQuestTopkMaxL, n_chunks_max);
   ZKV_REQUIRE(k >= 1 && out_stride >= k, "zkv_quest_chunk_topk_gqa: k=%d out_stride=%lld", k,
               static_cast<long long>(out_stride));
-  ZKV_REQUIRE((reinterpret_cast<uintptr_t>(slots) & 7) == 0 && slots_bytes >= static_cast<size_t>(bs) * kv * 8,
-              "zkv_quest_chunk_topk_gqa: slots need %zu bytes, 8-byte aligned (got %zu)",
-              static_cast<size_t>(bs) * kv * 8, slots_bytes);
+  ZKV_REQUIRE((reinterpret_cast<uintptr_t>(slots) & 3) == 0 && slots_bytes >= static_cast<size_t>(bs) * kv * 4,
+              "zkv_quest_chunk_topk_gqa: slots need %zu bytes, 4-byte aligned (got %zu)",
+              static_cast<size_t>(bs) * kv * 4, slots_bytes);
   auto s = reinterpret_cast<hipStream_t>(stream);
-  const dim3 grid((n_chunks + kQuestTopkChunks - 1) / kQuestTopkChunks, bs * kv);
-  auto* sl = static_cast<unsigned long long*>(slots);
-  const unsigned long long epoch = next_epoch();
-  if (meta_fp16)
-    quest_topk_kernel<true><<<grid, kTopkThreads, 0, s>>>(q, q_sb, q_sh, hq / kv, kv, raw_q, chunk_min, chunk_max,
-                                                          valid, scores, n_chunks, n_chunks_max, k, out, out_stride,
-                                                          sl, epoch);
-  else
-    quest_topk_kernel<false><<<grid, kTopkThreads, 0, s>>>(q, q_sb, q_sh, hq / kv, kv, raw_q, chunk_min,
-                                                           chunk_max, valid, scores, n_chunks, n_chunks_max, k, out,
-                                                           out_stride, sl, epoch);
+  auto* sl = static_cast<unsigned int*>(slots);
+  // trips per block: the fewest that keep the grid within two 1024-thread
+  // blocks per CU (one wave of blocks: each pays its store acknowledgement
+  // and arrival once)
+  const int rows = bs * kv;
+  auto blocks_per_row = [&](int tr) { return (n_chunks + tr * kQuestTopkChunks - 1) / (tr * kQuestTopkChunks); };
+  int tr = 1;
+  while (tr < 4 && static_cast<int64_t>(rows) * blocks_per_row(tr) > 512) tr *= 2;
+  if (const char* e = getenv("ZKV_QUEST_TRIPS")) tr = atoi(e) >= 4 ? 4 : (atoi(e) >= 2 ? 2 : 1);
+  const dim3 grid(blocks_per_row(tr), rows);
+  auto launch = [&](auto f16_tag, auto tr_tag) {
+    constexpr bool F16 = decltype(f16_tag)::value;
+    constexpr int TR = decltype(tr_tag)::value;
+    quest_topk_kernel<F16, TR><<<grid, kTopkThreads, 0, s>>>(q, q_sb, q_sh, hq / kv, kv, raw_q, chunk_min,
+                                                             chunk_max, valid, scores, n_chunks, n_chunks_max, k,
+                                                             out, out_stride, sl);
+  };
+  auto by_trips = [&](auto f16_tag) {
+    if (tr == 4) launch(f16_tag, std::integral_constant<int, 4>{});
+    else if (tr == 2) launch(f16_tag, std::integral_constant<int, 2>{});
+    else launch(f16_tag, std::integral_constant<int, 1>{});
+  };
+  if (meta_fp16) by_trips(std::true_type{});
+  else by_trips(std::false_type{});
   return check_launch("quest_topk_kernel");
 }
 

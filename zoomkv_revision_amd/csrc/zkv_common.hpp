@@ -140,4 +140,17 @@ __device__ __forceinline__ bool arrive_last(unsigned long long* slot, unsigned l
   return last;
 }
 
+// A plain arrival count for units with many workgroups (no compare-and-swap
+// retries under contention): one fetch-and-add per workgroup on a slot that
+// is 0 between launches; the n-th arrival finds n - 1, does the unit's final
+// step and puts the slot back to 0.  Slots must be zeroed once before first
+// use (a captured graph's replays leave them at 0 as well); launches that
+// overlap on one slot race.
+__device__ __forceinline__ bool arrive_last_count(unsigned int* slot, int n) {
+  const unsigned int old = __hip_atomic_fetch_add(slot, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const bool last = old == static_cast<unsigned int>(n - 1);
+  if (last) __hip_atomic_store(slot, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return last;
+}
+
 }  // namespace zkv

@@ -123,12 +123,12 @@ _SLOTS: dict = {}
 
 
 def _slots(device: torch.device, n: int) -> torch.Tensor:
-    """Arrival slots of the fused launch per (device, stream): concurrent
-    launches never share one (contents need no zeroing)."""
+    """Arrival counters of the fused launch per (device, stream): zeroed when
+    made, left zero by every launch; concurrent launches never share one."""
     key = (device, torch.cuda.current_stream(device).cuda_stream)
     t = _SLOTS.get(key)
     if t is None or t.numel() < n:
-        t = torch.zeros(max(n, 256), dtype=torch.int64, device=device)
+        t = torch.zeros(max(n, 256), dtype=torch.int32, device=device)
         _SLOTS[key] = t
     return t
 
@@ -178,7 +178,7 @@ def quest_chunk_topk_gqa(queries: torch.Tensor, kv_heads: int, chunk_min: torch.
     check(lib().zkv_quest_chunk_topk_gqa(
         ptr(q), q.stride(0), q.stride(1), hq, ptr(raw_q), ptr(chunk_min), ptr(chunk_max),
         int(chunk_min.dtype == torch.float16), ptr(scores), bs, kv, n_chunks, n_max, ptr(valid), k,
-        ptr(out), out.stride(1), ptr(sl), sl.numel() * 8, stream_of(q)))
+        ptr(out), out.stride(1), ptr(sl), sl.numel() * 4, stream_of(q)))
     return out[:, :, :k]
 
 
