@@ -105,11 +105,11 @@ struct AttnParams {
   unsigned long long* slots;
   unsigned long long epoch;  // distinct per launch, never 0
   int merge_fence;           // 1: plain partials ordered by agent-scope fences
-  // page-sparse mode: the sorted page list of (b, kv) at pages + b*pg_sb +
-  // h*pg_sh (n_sel ids).  Its tiles: a page 2g joined by a following 2g+1 is
-  // one tile (group g, both halves), any other in-range page a tile of its
-  // own half (bit m of the mask = tokens 16m .. 16m+15); ids outside
-  // [0, 2 n_groups) are skipped.
+  // page-sparse mode: the page list of (b, kv) at pages + b*pg_sb + h*pg_sh
+  // (n_sel ids, any order; page 2g + m = tokens 16m .. 16m + 15 of group g).
+  // Ids outside [0, 2 n_groups) are skipped; the others, in list order, pair
+  // up into tiles of two pages (the last one alone when their count is odd);
+  // a repeated id counts again.
   int page_sparse;  // the page-sparse kernel runs (also for an empty list)
   const int64_t* pages;
   int64_t pg_sb, pg_sh;
@@ -132,6 +132,11 @@ constexpr int kMaxListTokens = 1024;
 //   [4096, 4608) K scale/zero slots          [4608, 5120) V scale/zero
 constexpr int kStageBytes = 5120;
 constexpr int kRecordWords = kStageBytes / 4;
+// A page-sparse stage holds two 16-token pages, each from any group, in the
+// two halves' places of a record ([0, 5120) as above; a page B that is the
+// first half of its group takes the second half's places, which the tile
+// compute treats alike), plus page B's K scale/zero slots at [5120, 5632).
+constexpr int kPairStageBytes = 5632;
 // cache policy of the tile loads: nt (streamed once, not kept in the caches)
 constexpr int kCachePolicyNT = 2;
 
@@ -241,6 +246,34 @@ __device__ __forceinline__ void issue_tile(const AttnParams& p, int64_t bh, int 
   }
 }
 
+// DMA ops of a paired-page tile: with page B, 6 (K codes A, K codes B, V codes
+// A, V codes B, metadata A + V meta B, K meta B); without, 3.
+__device__ __forceinline__ int pair_dma_ops(int page_b) { return page_b >= 0 ? 6 : 3; }
+
+// Pages pa (always) and pb (or -1) of (b, kv) into a paired-page stage: page
+// x = 2 gi + m is half m of group gi; its blocks go to the places of half 0
+// (page A) or half 1 (page B) whatever m is.
+__device__ __forceinline__ void issue_pair(const AttnParams& p, int64_t bh, int pa, int pb, int lane,
+                                           uint8_t* stage) {
+  const uint8_t* base = reinterpret_cast<const uint8_t*>(p.groups + bh * p.g_cap * kRecordWords) + 16 * lane;
+  const uint8_t* ra = base + static_cast<int64_t>(pa >> 1) * kStageBytes;
+  const int ma = pa & 1;
+  dma16(ra + 1024 * ma, stage);
+  dma16(ra + 2048 + 1024 * ma, stage + 2048);
+  if (pb >= 0) {
+    const uint8_t* rb = base + static_cast<int64_t>(pb >> 1) * kStageBytes;
+    const int mb = pb & 1;
+    dma16(rb + 1024 * mb, stage + 1024);
+    dma16(rb + 2048 + 1024 * mb, stage + 3072);
+    // lanes 0-31: A's K scale/zero; 32-47: A's V scale/zero; 48-63: B's
+    const uint8_t* src = lane < 32 ? ra + 4096 : (lane < 48 ? ra + 4096 + 256 * ma : rb + 4096 + 256 * mb - 256);
+    dma16(src, stage + 4096);
+    if (lane < 32) dma16(rb + 4096, stage + 5120);
+  } else {
+    if (lane < 48) dma16(lane < 32 ? ra + 4096 : ra + 4096 + 256 * ma, stage + 4096);
+  }
+}
+
 // One code word as an MFMA operand of exact fp16 subnormals:
 // (n0, n4) * 2^-24, (n1, n5) * 16 * 2^-24, (n2, n6) * 2^-24, (n3, n7) * 16 * 2^-24.
 // fp16 subnormal inputs are exact on the gfx950 matrix cores.
@@ -289,18 +322,28 @@ constexpr float kLazyMaxBits = 0.5f;
 // units.  Returns the fp32 probabilities P of the lane's 8 tokens relative to
 // the (possibly updated) running max.  v_exp_f32 flushes results below 2^-126
 // to zero, which only drops probabilities far below every operand's resolution.
+// kTwoBias: the halves' scores carry their own bias (bias for S[0], bias1
+// for S[1]: a paired-page tile's two pages have their own K zero points).
+template <bool kTwoBias = false>
 __device__ __forceinline__ void softmax_probs(const float4_t S[2], float sc, float bias, float qs,
                                               float qsc, float& m_run, float4_t& L, float4_t O[8],
-                                              float4_t& OZ, float pr[8]) {
+                                              float4_t& OZ, float pr[8], float bias1 = 0.0f) {
   float sv[8];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     sv[i] = S[0][i];
     sv[4 + i] = S[1][i];
   }
-  const float mx8 = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
-                          fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
-  const float mx = wave_max16(__builtin_fmaf(mx8, sc, bias));
+  float mx;
+  if constexpr (kTwoBias) {
+    const float m0 = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+    const float m1 = fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7]));
+    mx = wave_max16(fmaxf(__builtin_fmaf(m0, sc, bias), __builtin_fmaf(m1, sc, bias1)));
+  } else {
+    const float mx8 = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])),
+                            fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
+    mx = wave_max16(__builtin_fmaf(mx8, sc, bias));
+  }
   const bool up = (mx - m_run) * qs > kLazyMaxBits;
   if (__any(up)) {
     const float m_new = up ? mx : m_run;
@@ -312,17 +355,19 @@ __device__ __forceinline__ void softmax_probs(const float4_t S[2], float sc, flo
     for (int j = 0; j < 8; ++j) O[j] *= alpha;
   }
   const float b2 = (bias - m_run) * qs;
+  const float b2h = kTwoBias ? (bias1 - m_run) * qs : b2;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) pr[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[e], qsc, b2));
+  for (int e = 0; e < 8; ++e) pr[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[e], qsc, e < 4 ? b2 : b2h));
 }
 
 // The quantized tiles' P: one fp16 operand; L accumulates sum(P) with a
 // ones-row MFMA on that same fp16 P (every row of L holds the column sum).
+template <bool kTwoBias = false>
 __device__ __forceinline__ half8_t softmax_step(const float4_t S[2], float sc, float bias, float qs,
                                                 float qsc, float& m_run, float4_t& L, float4_t O[8],
-                                                float4_t& OZ) {
+                                                float4_t& OZ, float bias1 = 0.0f) {
   float pr[8];
-  softmax_probs(S, sc, bias, qs, qsc, m_run, L, O, OZ, pr);
+  softmax_probs<kTwoBias>(S, sc, bias, qs, qsc, m_run, L, O, OZ, pr, bias1);
   half8_t pb;
 #pragma unroll
   for (int e = 0; e < 8; ++e) pb[e] = static_cast<_Float16>(pr[e]);
@@ -378,11 +423,14 @@ __device__ __forceinline__ TileCodes codes_from_stage(const uint8_t* st, int lan
 }
 
 // Tile compute from the lane's code words and the record's metadata KiB in
-// LDS (`meta`: K scale/zero slots at +0, V scale/zero at +512).
+// LDS (`meta`: K scale/zero slots at +0, V scale/zero at +512).  kPair: the
+// halves are two pages of a paired-page stage, half 1's K scale/zero slots at
+// meta + 1024 (its scores get their own hi / lo products and zero-point sum).
 //   K: S = sum n * (hi + lo)(q s) in 2^-24 units (codes are subnormals);
 //      Z (every row) = sum q z (raw units); score = S * 2^24 + Z.
 //   V: O[j] += sum n * fp16(16 P s) in 2^-20 units; OZ row r = sum P z of
 //      32-channel group r & 3.
+template <bool kPair = false>
 __device__ __forceinline__ void compute_tile(const TileCodes& cw, const uint8_t* meta, int c, int g,
                                              const TileConsts& tc, uint32_t tok_mask,
                                              float& m_run, float4_t& L, float4_t O[8],
@@ -390,6 +438,7 @@ __device__ __forceinline__ void compute_tile(const TileCodes& cw, const uint8_t*
   const u32x4_t kq0 = cw.k0, kq1 = cw.k1;
   float4_t S[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
   float4_t Z = {0.0f, 0.0f, 0.0f, 0.0f};
+  float4_t Z1 = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
     const uint8_t* km = meta + (4 * s + g) * 32;
@@ -401,9 +450,19 @@ __device__ __forceinline__ void compute_tile(const TileCodes& cw, const uint8_t*
     Z = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(kz), tc.qB[s], Z, 0, 0, 0);
     const half8_t n0 = codes8(kq0[s]), n1 = codes8(kq1[s]);
     S[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(n0, bp, S[0], 0, 0, 0);
-    S[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(n1, bp, S[1], 0, 0, 0);
     S[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(n0, bl, S[0], 0, 0, 0);
-    S[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(n1, bl, S[1], 0, 0, 0);
+    if constexpr (kPair) {
+      const u32x4_t ks1 = ld16(km + 1024);
+      const u32x4_t kz1 = ld16(km + 1024 + 16);
+      const half8_t bp1 = as_half8(ks1) * tc.qBm[s];
+      const half8_t bl1 = __builtin_elementwise_fma(as_half8(ks1), tc.qBm[s], -bp1);
+      Z1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_half8(kz1), tc.qB[s], Z1, 0, 0, 0);
+      S[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(n1, bp1, S[1], 0, 0, 0);
+      S[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(n1, bl1, S[1], 0, 0, 0);
+    } else {
+      S[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(n1, bp, S[1], 0, 0, 0);
+      S[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(n1, bl, S[1], 0, 0, 0);
+    }
   }
   // every row of Z holds sum q z (all A rows are the zero points)
   const float zc = Z[0];
@@ -418,7 +477,11 @@ __device__ __forceinline__ void compute_tile(const TileCodes& cw, const uint8_t*
     }
   }
   const uint32_t half_mask = halves_of(tok_mask);
-  const half8_t pb = softmax_step(S, kTwo24, zc, tc.qs, tc.qs24, m_run, L, O, OZ);
+  // (a paired tile without page B keeps half 1's bias finite: its K slots
+  // hold stale bytes, and its scores are -inf already)
+  const half8_t pb = kPair ? softmax_step<true>(S, kTwo24, zc, tc.qs, tc.qs24, m_run, L, O, OZ,
+                                                (half_mask & 2u) ? Z1[0] : zc)
+                           : softmax_step(S, kTwo24, zc, tc.qs, tc.qs24, m_run, L, O, OZ);
 
   // V code words of channel pairs P = 0..3 of each half, and the halves' V
   // scale/zero blocks (entry (gd, r): 4 scales, then 4 zeros of tokens 16m + 4r
@@ -749,11 +812,13 @@ constexpr int dense_waves_per_simd(int nw) { return nw == 8 ? 2 : 3; }
 //     straight to VGPRs (a D-slot register ring); only the metadata KiB
 //     streams through LDS (a D-stage DMA ring per wave).  An LDS-DMA-only
 //     ring streams at ~76% of HBM on gfx950, code words in VGPRs at ~88%.
-//   page-sparse and bf16-only tiles: a D-stage ring of whole 5 KiB records.
-template <int NW, int D, bool kSparse, bool kBf16Only>
+//   page-sparse tiles: a D-stage ring of paired-page stages (5.5 KiB).
+//   token-list and bf16-only tiles: a D-stage ring of whole 5 KiB records.
+template <int NW, int D, bool kSparse, bool kBf16Only, bool kToken = false>
 struct KernelShape {
   static constexpr bool kVgpr = !kSparse && !kBf16Only;
-  static constexpr int kStage = kVgpr ? kMetaBytes : kStageBytes;
+  static constexpr bool kPaired = kSparse && !kToken;
+  static constexpr int kStage = kVgpr ? kMetaBytes : (kPaired ? kPairStageBytes : kStageBytes);
   static constexpr int kRingBytes = NW * D * kStage;
   static constexpr int kMergeBytes = NW * kMaxGqa * (128 + 2) * 4;
   static constexpr int kLdsBytes = std::max(kRingBytes, kMergeBytes);
@@ -775,10 +840,11 @@ using i32x4_t = int32_t __attribute__((ext_vector_type(4)));
 // computed here from the actual tile counts.
 template <int NW, int D, bool kSparse, bool kBf16Only = false, bool kToken = false>
 __global__ __launch_bounds__(64 * NW)
-__attribute__((amdgpu_waves_per_eu(KernelShape<NW, D, kSparse, kBf16Only>::kWavesPerEu)))
+__attribute__((amdgpu_waves_per_eu(KernelShape<NW, D, kSparse, kBf16Only, kToken>::kWavesPerEu)))
 void kivi4_attn_kernel(const AttnParams p) {
   static_assert(!kToken || kSparse, "the token-list mode streams whole records");
-  using KS = KernelShape<NW, D, kSparse, kBf16Only>;
+  using KS = KernelShape<NW, D, kSparse, kBf16Only, kToken>;
+  constexpr bool kPaired = KS::kPaired;
   constexpr int kStage = KS::kStage;
   __shared__ __attribute__((aligned(16))) uint8_t smem[KS::kLdsBytes];
   __shared__ int s_prog[KS::kVgpr ? NW : 1];  // dense: tiles done per wave
@@ -944,49 +1010,42 @@ void kivi4_attn_kernel(const AttnParams p) {
     T0 = tile_at((split * W + p.n_splits - 1) / p.n_splits);
     T1_token = tile_at(((split + 1) * W + p.n_splits - 1) / p.n_splits);
   } else if constexpr (kSparse) {
-    // Every wave walks the page list (64 pages per step, the pairing by
-    // ballot ranks) and keeps the descriptors of its own tiles T0 + wave +
-    // NW*k, k < 64, in its last ring stage, which no DMA has reached yet.
-    int32_t* s_group = reinterpret_cast<int32_t*>(ring[D - 1]);
-    int32_t* s_mask = s_group + 64;
+    // Every wave walks the page list (64 pages per step): the in-range pages,
+    // in list order, pair up into tiles (ranks 2t and 2t + 1 form tile t, by
+    // ballot ranks), and the wave keeps the page ids of its own tiles T0 +
+    // wave + NW*k, k < 64, in its last ring stage, which no DMA has reached
+    // yet (page B = -1: a tile of one page).
+    int32_t* s_pa = reinterpret_cast<int32_t*>(ring[D - 1]);
+    int32_t* s_pb = s_pa + 64;
     const int64_t* pg = p.pages + b * p.pg_sb + h * p.pg_sh;
     const int64_t n_pages = 2ll * p.n_groups;
     int base = 0;
-    // one load per page: each step requests the next 64 pages before the
-    // neighbours come from lane shuffles, so the first two chunks share one
-    // memory round trip
+    s_pb[lane] = -1;  // (a lane's own store first: it precedes the walk's)
+    // one load per page: the next 64 pages are requested before this step's
+    // ballot, so the first two steps share one memory round trip
     int64_t cur = lane < p.n_sel ? pg[lane] : -1;
-    int64_t before = -1;  // page i0 - 1
     for (int i0 = 0; i0 < p.n_sel; i0 += 64) {
       const int i = i0 + lane;
       const int64_t ahead = i + 64 < p.n_sel ? pg[i + 64] : -1;
-      int64_t prev = __shfl_up(cur, 1, 64);
-      if (lane == 0) prev = before;
-      int64_t next = __shfl_down(cur, 1, 64);
-      const int64_t ahead0 = __shfl(ahead, 0, 64);
-      if (lane == 63) next = ahead0;
-      const bool valid = cur >= 0 && cur < n_pages;
-      const bool start = valid && !((cur & 1) && prev == cur - 1);
-      const uint64_t m = __ballot(start);
-      const int t = base + __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
+      const bool valid = i < p.n_sel && cur >= 0 && cur < n_pages;
+      const uint64_t m = __ballot(valid);
+      const int r = base + __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
                                                     __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0));
-      const int rel = t - T0 - wave;
-      if (start && rel >= 0 && rel % NW == 0 && rel / NW < 64) {
-        s_group[rel / NW] = static_cast<int32_t>(cur >> 1);
-        s_mask[rel / NW] = (cur & 1) ? 0xFFFF0000u : (next == cur + 1 ? kAllTokens : 0x0000FFFFu);
-      }
+      const int rel = (r >> 1) - T0 - wave;
+      if (valid && rel >= 0 && rel % NW == 0 && rel / NW < 64)
+        ((r & 1) ? s_pb : s_pa)[rel / NW] = static_cast<int32_t>(cur);
       base += __popcll(m);
-      before = __shfl(cur, 63, 64);
       cur = ahead;
     }
-    n_qt = base;
+    n_qt = (base + 1) >> 1;
   }
   const int n_tiles = n_qt + (res_len + kTile - 1) / kTile;
   const int T1 = kToken ? T1_token : min(T0 + ((split & 1) ? p.tiles_odd_split : p.tiles_per_split), n_tiles);
   const int TQ = min(T1, n_qt);  // quantized tiles of this workgroup: [T0, TQ)
   // this wave's quantized tiles: T0 + wave + NW*k, k < nq (nq <= 64 in sparse mode)
   const int nq = TQ > T0 + wave ? (TQ - (T0 + wave) + NW - 1) / NW : 0;
-  // sparse mode: lane k holds the group and half mask of this wave's tile k
+  // token-list mode: lane k holds the group and token mask of this wave's
+  // tile k; page-sparse mode: its pages A and B (B = -1: none)
   int my_group = 0, my_mask = static_cast<int>(kAllTokens);
   if constexpr (kToken) {
     if (lane < nq) {
@@ -1012,10 +1071,26 @@ void kivi4_attn_kernel(const AttnParams p) {
       return T0 + wave + NW * k;
   };
   auto mask_of = [&](int k) -> uint32_t {
-    if constexpr (kSparse)
+    if constexpr (kPaired)
+      return __builtin_amdgcn_readlane(my_mask, k) >= 0 ? kAllTokens : 0x0000FFFFu;
+    else if constexpr (kSparse)
       return static_cast<uint32_t>(__builtin_amdgcn_readlane(my_mask, k));
     else
       return kAllTokens;
+  };
+  // the next tile of the LDS ring: token-list tiles are one group's record
+  // (its halves per the token mask), page-sparse tiles two pages
+  auto issue_next = [&](int k) {
+    if constexpr (kPaired)
+      issue_pair(p, bh, group_of(k), __builtin_amdgcn_readlane(my_mask, k), lane, ring[k % D]);
+    else
+      issue_tile(p, bh, group_of(k), lane, ring[k % D], mask_of(k));
+  };
+  auto dma_ops_of = [&](int k) {
+    if constexpr (kPaired)
+      return pair_dma_ops(__builtin_amdgcn_readlane(my_mask, k));
+    else
+      return tile_dma_ops(mask_of(k));
   };
 
   // dense tiles: tile k's code words into register slot k % D, its metadata
@@ -1107,7 +1182,7 @@ void kivi4_attn_kernel(const AttnParams p) {
 #pragma unroll
     for (int k = 0; k < D - 1; ++k)
       if (issued < nq) {
-        issue_tile(p, bh, group_of(issued), lane, ring[issued % D], mask_of(issued));
+        issue_next(issued);
         ++issued;
       }
   }
@@ -1206,15 +1281,15 @@ void kivi4_attn_kernel(const AttnParams p) {
       // ---- page-sparse tiles through this wave's D-stage LDS ring ----
       for (int k = 0; k < nq; ++k) {
         if (issued < nq) {
-          issue_tile(p, bh, group_of(issued), lane, ring[issued % D], mask_of(issued));
+          issue_next(issued);
           ++issued;
         }
         const uint32_t tok_mask = mask_of(k);
         int later = 0;  // DMA ops issued after tile k's
-        for (int t = k + 1; t < issued; ++t) later += tile_dma_ops(mask_of(t));
+        for (int t = k + 1; t < issued; ++t) later += dma_ops_of(t);
         wait_ops_in_flight(later);
-        compute_tile(codes_from_stage(ring[k % D], lane), ring[k % D] + 4096, c, g, tc, tok_mask, m_run, L,
-                     O, OZ);
+        compute_tile<kPaired>(codes_from_stage(ring[k % D], lane), ring[k % D] + 4096, c, g, tc, tok_mask,
+                              m_run, L, O, OZ);
       }
     }
     // O to real units: O * 2^20 + sum P z of the M-tile's group (OZ component
@@ -1383,10 +1458,10 @@ struct SplitPlan {
   int tiles_odd_split;  // tiles of the odd-numbered splits (see xcd_skew)
 };
 
-// Page-sparse shape: a wave holds only a few tiles (C3: ~4), so its loop is a
-// chain of DMA round trips; a 4-stage ring issues them together (8 x 4 x 5 KiB
-// = the 160 KiB of LDS: one workgroup per CU, 2 waves per SIMD).
-constexpr int kSparseNW = 8, kSparseD = 4;
+// Page-sparse shape: a wave holds only a few paired-page tiles (C3: 2), so its
+// loop is a chain of DMA round trips; a 3-stage ring issues them together
+// (8 x 3 x 5.5 KiB = 132 KiB of LDS: one workgroup per CU, 2 waves per SIMD).
+constexpr int kSparseNW = 8, kSparseD = 3;
 
 constexpr float kXcdSkew = 0.03f;
 
@@ -1559,13 +1634,16 @@ struct TokenList {
 
 
 // Sparse mode: every split is planned for the longest page list (n_sel
-// tiles); each wave keeps at most 64 tile descriptors in its lanes.
+// pages, (n_sel + 1) / 2 paired tiles); each wave keeps at most 64 tile
+// descriptors in its lanes.
 SplitPlan plan_sparse_splits(int bs, int kv, int n_sel, int res_len, int n_splits) {
+  const int n_pair = (n_sel + 1) / 2;
   // (equal splits: a page-sparse split is a short latency chain)
-  SplitPlan sp = plan_splits(bs, kv, n_sel, res_len, n_splits, Shape{kSparseNW, kSparseD}, kStageBytes, 4, false);
+  SplitPlan sp = plan_splits(bs, kv, n_pair, res_len, n_splits, Shape{kSparseNW, kSparseD}, kPairStageBytes, 4,
+                             false);
   constexpr int kMaxPerSplit = 64 * kSparseNW;
   if (sp.tiles_per_split > kMaxPerSplit) {
-    const int n_tiles = n_sel + (res_len + kTile - 1) / kTile;
+    const int n_tiles = n_pair + (res_len + kTile - 1) / kTile;
     sp.n_splits = (n_tiles + kMaxPerSplit - 1) / kMaxPerSplit;
     sp.tiles_per_split = (n_tiles + sp.n_splits - 1) / sp.n_splits;
     sp.tiles_odd_split = sp.tiles_per_split;
