@@ -18,6 +18,7 @@
 #include "zkv_common.hpp"
 
 #include <algorithm>
+#include <cstdio>
 #include <cstdlib>
 
 namespace zkv {
@@ -522,8 +523,19 @@ extern "C" int zkv_decode_linear(const uint16_t* x, int64_t x_ld, int M, int K, 
     const int n_chunks = (K + kGemvChunk - 1) / kGemvChunk;
     // narrow projections (fewer rows than ~2 units per wave of a full chip)
     // split K over the waves of a workgroup
-    const bool split = rows < 8192 && n_chunks >= kGemvWaves && !norm_w;
-    const int R = split ? 4 : (rows >= 16384 ? 8 : (rows >= 8192 ? 4 : 2));
+    // (QKV, 6144 rows: 4 rows per unit 11.7 us, 2 rows 12.4; two or four
+    // items in flight per wave: the same or slower at every projection)
+    bool split = rows < 8192 && n_chunks >= kGemvWaves && !norm_w;
+    int R = split ? 4 : (rows >= 16384 ? 8 : (rows >= 4096 ? 4 : 2));
+    // ZKV_GEMV_SHAPE=R[,s] overrides the shape for tuning sweeps (s: split K)
+    if (const char* e = getenv("ZKV_GEMV_SHAPE")) {
+      int r = 0;
+      char sp = 0;
+      if (sscanf(e, "%d,%c", &r, &sp) >= 1 && (r == 2 || r == 4 || r == 8)) {
+        R = r;
+        split = sp == 's' && !norm_w && R == 4;
+      }
+    }
     const int per_unit = epilogue == kEpiSiluMul ? R / 2 : R;
     const int n_units = (rows + per_unit - 1) / per_unit;
     const int grid_g = std::max(1, std::min(split ? n_units : (n_units + kGemvWaves - 1) / kGemvWaves, 768));
