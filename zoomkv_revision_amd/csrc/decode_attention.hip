@@ -796,6 +796,10 @@ __device__ __forceinline__ void merge_splits_last(const AttnParams& p, int64_t b
 
 constexpr int kMetaBytes = 1024;  // the record's last KiB: K and V scale/zero
 constexpr int kMaxGqa = 16;       // query heads per KV head (checked on the host)
+// Row stride (floats) of the final merge's per-(wave, head) output rows: 4
+// banks of skew between the heads' rows, so the 16-byte stores of the lanes
+// of one channel block (one per head) hit different banks.
+constexpr int kRedStride = 132;
 // A bf16 residual tile (two dependent memory round trips, 16 KiB) takes a
 // wave about as long as three quantized tiles; splits and waves are balanced
 // with that weight.
@@ -820,7 +824,7 @@ struct KernelShape {
   static constexpr bool kPaired = kSparse && !kToken;
   static constexpr int kStage = kVgpr ? kMetaBytes : (kPaired ? kPairStageBytes : kStageBytes);
   static constexpr int kRingBytes = NW * D * kStage;
-  static constexpr int kMergeBytes = NW * kMaxGqa * (128 + 2) * 4;
+  static constexpr int kMergeBytes = NW * kMaxGqa * (kRedStride + 2) * 4;
   static constexpr int kLdsBytes = std::max(kRingBytes, kMergeBytes);
   // resident waves per SIMD when LDS (160 KiB per CU) is the limit
   static constexpr int kWgPerCu = (160 * 1024) / kLdsBytes;
@@ -1320,20 +1324,20 @@ void kivi4_attn_kernel(const AttnParams p) {
   // ---- merge the NW waves through LDS (the rings are free now) ----
   const float l_tot = L[0];
   __syncthreads();
-  float* red_o = reinterpret_cast<float*>(smem);  // [NW][gqa][128]
-  float* red_m = red_o + NW * p.gqa * 128;                    // [NW][gqa]
+  float* red_o = reinterpret_cast<float*>(smem);  // [NW][gqa][kRedStride]
+  float* red_m = red_o + NW * p.gqa * kRedStride;                    // [NW][gqa]
   float* red_l = red_m + NW * p.gqa;                          // [NW][gqa]
   if (col_ok) {
     if constexpr (kBf16Only) {
       // O[j][i] is channel 32g + 8i + j
-      float* o = red_o + (wave * p.gqa + c) * 128 + 32 * g;
+      float* o = red_o + (wave * p.gqa + c) * kRedStride + 32 * g;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         *reinterpret_cast<float4_t*>(o + 8 * i) = float4_t{O[0][i], O[1][i], O[2][i], O[3][i]};
         *reinterpret_cast<float4_t*>(o + 8 * i + 4) = float4_t{O[4][i], O[5][i], O[6][i], O[7][i]};
       }
     } else {
-      float* o = red_o + (wave * p.gqa + c) * 128 + 8 * g;
+      float* o = red_o + (wave * p.gqa + c) * kRedStride + 8 * g;
 #pragma unroll
       for (int G = 0; G < 4; ++G) {
         // O[2G + jp][i] is channel 32G + 8g + 2i + jp
@@ -1363,7 +1367,7 @@ void kivi4_attn_kernel(const AttnParams p) {
     for (int w = 0; w < NW; ++w) {
       const float wt = __builtin_amdgcn_exp2f(red_m[w * p.gqa + cc] - mm);
       ll += wt * red_l[w * p.gqa + cc];
-      oo += wt * red_o[(w * p.gqa + cc) * 128 + d];
+      oo += wt * red_o[(w * p.gqa + cc) * kRedStride + d];
     }
     if (final_out) {
       store_out(p, bh * p.gqa + cc, d, ll > 0.0f ? oo / ll : 0.0f);  // row b*hq + h*gqa + cc
@@ -1497,7 +1501,7 @@ float xcd_skew() {
 // Resident workgroups per CU: LDS (160 KiB per CU) and waves (4 SIMDs, at most
 // `waves_per_simd` waves each at the kernel's register budget).
 int wgs_per_cu(Shape sh, int stage_bytes, int waves_per_simd) {
-  const int lds = std::max(sh.nw * sh.d * stage_bytes, sh.nw * kMaxGqa * (128 + 2) * 4);
+  const int lds = std::max(sh.nw * sh.d * stage_bytes, sh.nw * kMaxGqa * (kRedStride + 2) * 4);
   return std::max(1, std::min((160 * 1024) / lds, 4 * waves_per_simd / sh.nw));
 }
 
