@@ -86,6 +86,8 @@ def test_kivi4_pack_strided_input(rng):
     (1, 32, 8, 9, 128, 3),    # Qwen3-8B heads, full residual window
     (3, 4, 4, 4, 0, 0),       # MHA, no residual
     (1, 16, 1, 3, 17, 2),     # 16 query heads per KV head
+    (2, 16, 2, 6, 33, 0),     # 8 query heads per KV head
+    (1, 12, 1, 4, 9, 0),      # 12 per KV head
     (2, 8, 2, 0, 77, 0),      # residual only
 ])
 def test_decode_attention_matches_oracle(rng, bs, hq, kv, ng, res, splits):

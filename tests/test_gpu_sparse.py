@@ -68,6 +68,8 @@ def _pages(rng, kind, bs, kv, ng, n_sel):
     (1, 8, 2, 12, 0, 1, "sorted", 0),
     (2, 8, 2, 20, 0, 16, "sorted", 1),
     (1, 8, 2, 600, 0, 1100, "sorted", 1),   # > 512 tiles: the planner splits anyway
+    (1, 16, 1, 30, 10, 21, "messy", 0),     # 16 query heads per KV head
+    (2, 16, 2, 30, 10, 21, "unsorted", 0),  # 8 query heads per KV head
 ])
 def test_sparse_attention_matches_oracle(rng, bs, hq, kv, ng, res, n_sel, kind, splits):
     from zoomkv_revision_amd import kivi

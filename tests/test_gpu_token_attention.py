@@ -68,6 +68,8 @@ def _list(rng, kind, bs, kv, ng, n_tail, n):
     (2, 16, 4, 50, 5, 200, 113, "c5", 3),
     (1, 8, 2, 64, 16, 900, 1024, "messy", 0),     # the longest list, several splits
     (1, 8, 1, 64, 16, 100, 1024, "shuffled", 1),  # the longest list in one split: raised to fit
+    (1, 16, 1, 30, 9, 70, 150, "messy", 0),       # 16 query heads per KV head
+    (2, 16, 2, 30, 9, 70, 150, "shuffled", 0),    # 8 query heads per KV head
     (2, 8, 2, 0, 10, 40, 10, "shuffled", 0),      # no quantized groups
 ])
 def test_token_attention_matches_oracle(rng, bs, hq, kv, ng, n_tail, near, n, kind, splits):
