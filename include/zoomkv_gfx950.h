@@ -291,7 +291,7 @@ int zkv_page_minmax_f16(const uint16_t* keys, int64_t k_sb, int64_t k_sh, int64_
  * 16P+15, i.e. half P & 1 of Format Q group P >> 1), followed by the bf16
  * residual window.  Equals attention over the gathered tokens of the listed
  * pages (a page listed twice counts twice; ids outside [0, 2 * n_groups) are
- * skipped); sorted lists let both halves of a group share one tile.
+ * skipped); any two listed pages share one 32-token tile, in list order.
  * Counterpart of the Quest select -> gather -> flash_attn_with_kvcache
  * sequence (S:2195-2240, S:1723-1772). */
 size_t zkv_kivi4_sparse_attention_workspace_size(int bs, int hq, int kv, int n_sel, int res_len,
