@@ -1045,11 +1045,12 @@ __global__ __launch_bounds__(NT) void rabitq_select_kernel(
 #pragma unroll
   for (int r0 = 0; r0 < R; r0 += RB) {
     u32x4_t ch[RB];
+    // (a clamped address, then zero past the last bucket: no branch per load)
 #pragma unroll
-    for (int b = 0; b < RB; ++b) {
-      const int ci = (r0 + b) * NT + tid;
-      ch[b] = ci < n_chunks ? bq[ci] : u32x4_t{0u, 0u, 0u, 0u};
-    }
+    for (int b = 0; b < RB; ++b) ch[b] = bq[min((r0 + b) * NT + tid, n_chunks - 1)];
+#pragma unroll
+    for (int b = 0; b < RB; ++b)
+      if ((r0 + b) * NT + tid >= n_chunks) ch[b] = u32x4_t{0u, 0u, 0u, 0u};
 #pragma unroll
     for (int b = 0; b < RB; ++b) {
       const int r = r0 + b;
@@ -1061,6 +1062,9 @@ __global__ __launch_bounds__(NT) void rabitq_select_kernel(
       key[2 * r] = ch[b][0];      // entry 2 * part - 1 (chunk 0: count and pad)
       key[2 * r + 1] = ch[b][2];  // entry 2 * part
       idx8[r >> 1] |= ((ch[b][1] & 255u) | ((ch[b][3] & 255u) << 8)) << (16 * (r & 1));
+      // packed here, so the chunk's index words die now (with 16 passes the
+      // compiler would otherwise keep them all until the placement)
+      if constexpr (R > 8) asm volatile("" : "+v"(idx8[r >> 1]));
       if (part >= 1 && 2 * part - 1 < kept) valid |= 1u << (2 * r);
       if (2 * part < kept) valid |= 1u << (2 * r + 1);
     }
@@ -1105,10 +1109,11 @@ __global__ __launch_bounds__(NT) void rabitq_select_kernel(
     int take_eq;
     block_radix_select12<NT, NI>(key, valid, k, mn, mx, s_hist, s_tmp, T, take_eq);
     __syncthreads();  // its last reads of s_tmp are done
-    // packed (above T, equal to T) counts per pass, scanned over the threads
-    int excl[R];  // within the wave
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
+    // packed (above T, equal to T) counts per pass, scanned over the threads;
+    // with 16 passes the per-pass prefixes are recomputed after the barriers
+    // instead of kept live (32 keys per thread leave no registers for them)
+    constexpr bool kKeepExcl = R <= 8;
+    auto pass_count = [&](int r) {
       int gt = 0, eq = 0;
 #pragma unroll
       for (int j = 2 * r; j < 2 * r + 2; ++j) {
@@ -1117,9 +1122,14 @@ __global__ __launch_bounds__(NT) void rabitq_select_kernel(
           eq += key[j] == T;
         }
       }
-      const int cnt = gt | (eq << 16);
+      return gt | (eq << 16);
+    };
+    int excl[kKeepExcl ? R : 1];  // within the wave
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int cnt = pass_count(r);
       const int incl = wave_incl_sum(cnt);
-      excl[r] = incl - cnt;
+      if constexpr (kKeepExcl) excl[r] = incl - cnt;
       if (lane == 63) s_tmp[r * W + wave] = static_cast<uint32_t>(incl);
     }
     __syncthreads();
@@ -1136,7 +1146,14 @@ __global__ __launch_bounds__(NT) void rabitq_select_kernel(
     __syncthreads();
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const int before = static_cast<int>(s_tmp[r * W + wave]) + excl[r];
+      int ex;
+      if constexpr (kKeepExcl) {
+        ex = excl[r];
+      } else {
+        const int cnt = pass_count(r);
+        ex = wave_incl_sum(cnt) - cnt;
+      }
+      const int before = static_cast<int>(s_tmp[r * W + wave]) + ex;
       int g = before & 0xFFFF, e = before >> 16;
       const int32_t list0 = ((r * NT + tid) >> 3) * kFiltList;
 #pragma unroll
