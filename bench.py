@@ -607,10 +607,12 @@ def run_c4(args):
         pools.append((keys, codes, fac))
     qs = synthetic.c4_keys(7, nq, 64, dev)
     ws = rabitq.search_workspace(1, nq, n, topk, dev)
+    outs = (torch.empty(nq, topk, dtype=torch.int64, device=dev), torch.empty(nq, topk, dtype=torch.int64, device=dev),
+            torch.empty(nq, topk, dtype=torch.float32, device=dev))
 
     def step(i):
         keys, codes, fac = pools[i % n_pools]
-        rabitq.rabitq_search(qs, keys, codes, fac, signs, topk, workspace=ws)
+        rabitq.rabitq_search(qs, keys, codes, fac, signs, topk, workspace=ws, out=outs)
 
     ms = timed_loop(step, args.steps, args.warmup)
     k_ms = kernel_batch_ms(lambda i: rabitq.rabitq_search(qs, *pools[i % n_pools][:3], signs, topk, workspace=ws),

@@ -143,6 +143,27 @@ def test_search_few_planted_winners(rng):
     assert np.array_equal(fsc.view(np.uint32), rs.view(np.uint32))
 
 
+def test_search_into_preallocated_outputs(rng):
+    """out= writes the same bits into the caller's tensors, call after call."""
+    from zoomkv_revision_amd.rabitq import rabitq_encode, rabitq_search, search_workspace
+    _, s_t = _signs()
+    n, nq, topk = 40000, 3, 128
+    kt = _f16(orq.clustered_unit_keys(rng, n, 16))
+    qt = _f16(orq.clustered_unit_keys(rng, nq, 16))
+    codes, fac = rabitq_encode(kt, s_t)
+    ref = rabitq_search(qt, kt, codes, fac, s_t, topk)
+    ws = search_workspace(1, nq, n, topk, qt.device)
+    outs = (torch.full((nq, topk), -7, dtype=torch.int64, device=qt.device),
+            torch.full((nq, topk), -7, dtype=torch.int64, device=qt.device),
+            torch.full((nq, topk), float("nan"), device=qt.device))
+    for _ in range(2):
+        got = rabitq_search(qt, kt, codes, fac, s_t, topk, workspace=ws, out=outs)
+        for a, b, o in zip(got, ref, outs):
+            assert a.data_ptr() == o.data_ptr()
+            assert torch.equal(a.view(torch.int32) if a.dtype == torch.float32 else a,
+                               b.view(torch.int32) if b.dtype == torch.float32 else b)
+
+
 def test_search_c4_full_size(rng):
     """BASELINE config 4: 131072 clustered unit keys, 64 queries, top-256;
     8 of the 64 queries checked against the oracle, all 64 against invariants."""

@@ -115,9 +115,13 @@ def check(rc: int) -> None:
         raise ZkvError(f"zoomkv_gfx950 error {rc}: {msg}")
 
 
+_raw_stream = torch._C._cuda_getCurrentRawStream
+
+
 def stream_of(t: torch.Tensor) -> int:
-    """The current HIP stream of t's device (what the reference's kernels use)."""
-    return torch.cuda.current_stream(t.device).cuda_stream
+    """The current HIP stream of t's device (what the reference's kernels use),
+    as its raw handle (no Stream object is built per call)."""
+    return _raw_stream(t.get_device())
 
 
 def ptr(t: torch.Tensor | None) -> int | None:

@@ -98,7 +98,8 @@ def search_workspace(pools: int, queries: int, n: int, topk: int, device) -> tor
 
 
 def rabitq_search(q: torch.Tensor, keys: torch.Tensor, codes: torch.Tensor, factors: torch.Tensor,
-                  signs: torch.Tensor, topk: int, workspace: torch.Tensor | None = None):
+                  signs: torch.Tensor, topk: int, workspace: torch.Tensor | None = None,
+                  out: tuple | None = None):
     """Top-``topk`` keys per query by RaBitQ estimate, reranked exactly.
 
     q fp16 [P, Q, 128] (or [Q, 128]); keys fp16 [P, N, 128] (or [N, 128]; row
@@ -106,6 +107,8 @@ def rabitq_search(q: torch.Tensor, keys: torch.Tensor, codes: torch.Tensor, fact
     [P, N, 16]; factors fp16 [P, N, 2].  Returns (cand_idx int64 [P, Q, topk]
     in increasing index order, final_idx int64 [P, Q, topk], final_scores
     fp32 [P, Q, topk]) with the final pair ordered by (score desc, index asc).
+    ``out``: the three output tensors, preallocated with those shapes and
+    dtypes (contiguous), written in place and returned.
     """
     require_gpu(q, keys, codes, factors, signs)
     _check_signs(signs)
@@ -123,9 +126,16 @@ def rabitq_search(q: torch.Tensor, keys: torch.Tensor, codes: torch.Tensor, fact
         kk = kk.contiguous()
     assert 0 < topk <= N, f"topk={topk} must be in [1, {N}]"
     ws = workspace if workspace is not None else search_workspace(P, Q, N, topk, q.device)
-    cand = torch.empty(P, Q, topk, dtype=torch.int64, device=q.device)
-    fidx = torch.empty_like(cand)
-    fsc = torch.empty(P, Q, topk, dtype=torch.float32, device=q.device)
+    if out is None:
+        cand = torch.empty(P, Q, topk, dtype=torch.int64, device=q.device)
+        fidx = torch.empty_like(cand)
+        fsc = torch.empty(P, Q, topk, dtype=torch.float32, device=q.device)
+    else:
+        cand, fidx, fsc = out
+        for t, dt in ((cand, torch.int64), (fidx, torch.int64), (fsc, torch.float32)):
+            assert t.dtype == dt and t.is_contiguous() and t.numel() == P * Q * topk and t.device == q.device, \
+                "out tensors: contiguous int64, int64, fp32 with P * Q * topk elements on q's device"
+        cand, fidx, fsc = cand.view(P, Q, topk), fidx.view(P, Q, topk), fsc.view(P, Q, topk)
     check(lib().zkv_rabitq_search(ptr(qq), ptr(kk), kk.stride(0), kk.stride(1), ptr(cc), ptr(ff),
                                   ptr(signs), P, Q, N, topk, ptr(cand), ptr(fidx), ptr(fsc), ptr(ws),
                                   ws.numel(), stream_of(q)))
