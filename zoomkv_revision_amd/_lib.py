@@ -118,6 +118,12 @@ def check(rc: int) -> None:
 _raw_stream = torch._C._cuda_getCurrentRawStream
 
 
+def device_stream(device: torch.device) -> int:
+    """The raw handle of the current stream of a torch device."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    return _raw_stream(idx)
+
+
 def stream_of(t: torch.Tensor) -> int:
     """The current HIP stream of t's device (what the reference's kernels use),
     as its raw handle (no Stream object is built per call)."""

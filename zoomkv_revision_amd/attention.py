@@ -17,7 +17,7 @@ import math
 
 import torch
 
-from ._lib import check, lib, ptr, require_gpu, stream_of
+from ._lib import check, device_stream, lib, ptr, require_gpu, stream_of
 
 HEAD_DIM = 128
 _WS: dict = {}
@@ -27,7 +27,7 @@ def _workspace(device, nbytes: int) -> torch.Tensor:
     """Split partials and arrival slots per (device, stream): calls that may
     overlap on the device (two streams) never share one."""
     dev = torch.device(device)
-    key = (dev, torch.cuda.current_stream(dev).cuda_stream)
+    key = (dev, device_stream(dev))
     ws = _WS.get(key)
     if ws is None or ws.numel() < nbytes:
         ws = torch.zeros(max(nbytes, 1 << 16), dtype=torch.uint8, device=dev)

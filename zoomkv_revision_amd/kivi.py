@@ -14,7 +14,7 @@ from dataclasses import dataclass
 
 import torch
 
-from ._lib import check, lib, ptr, require_gpu, stream_of
+from ._lib import check, device_stream, lib, ptr, require_gpu, stream_of
 
 HEAD_DIM = 128
 GROUP = 32  # Format Q tokens per group
@@ -218,7 +218,7 @@ def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     """Attention workspace (split partials and arrival slots) per (device,
     stream), grown on demand: calls on one stream run in order, and calls on
     two streams, which may overlap on the device, get two workspaces."""
-    key = (device.type, device.index, torch.cuda.current_stream(device).cuda_stream)
+    key = (device.type, device.index, device_stream(device))
     ws = _WORKSPACE.get(key)
     if ws is None or ws.numel() < nbytes:
         ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)

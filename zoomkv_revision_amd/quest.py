@@ -10,7 +10,7 @@ from __future__ import annotations
 
 import torch
 
-from ._lib import check, lib, ptr, require_gpu, stream_of
+from ._lib import check, device_stream, lib, ptr, require_gpu, stream_of
 
 
 def quest_chunk_score(q: torch.Tensor, chunk_min: torch.Tensor, chunk_max: torch.Tensor,
@@ -125,7 +125,7 @@ _SLOTS: dict = {}
 def _slots(device: torch.device, n: int) -> torch.Tensor:
     """Arrival counters of the fused launch per (device, stream): zeroed when
     made, left zero by every launch; concurrent launches never share one."""
-    key = (device, torch.cuda.current_stream(device).cuda_stream)
+    key = (device, device_stream(device))
     t = _SLOTS.get(key)
     if t is None or t.numel() < n:
         t = torch.zeros(max(n, 256), dtype=torch.int32, device=device)

@@ -33,7 +33,7 @@ import json
 import torch
 
 from . import topk as _topk_mod
-from ._lib import check, lib, ptr, require_gpu, stream_of
+from ._lib import check, device_stream, lib, ptr, require_gpu, stream_of
 
 HEAD_DIM = 128
 DEFAULT_SRHT_ROUNDS = 1  # PC:35
@@ -217,7 +217,7 @@ def _flag_bytes(bs: int, kv: int, kv_len: int) -> int:
 def _rerank_workspace(device, bs: int, kv: int, kv_len: int):
     need = lib().zkv_rabitq4_rerank_workspace_size(bs, kv, kv_len)
     dev = torch.device(device)
-    key = (dev, torch.cuda.current_stream(dev).cuda_stream)
+    key = (dev, device_stream(dev))
     ent = _WS.get(key)
     if ent is None or ent[0].numel() < need:
         ent = [torch.zeros(max(need, 1 << 16), dtype=torch.uint8, device=dev), (bs, kv, kv_len)]
