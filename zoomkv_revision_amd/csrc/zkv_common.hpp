@@ -115,9 +115,8 @@ __device__ __forceinline__ void nibbles_to_half_pairs(uint32_t w, half2_t out[4]
 
 // ---------------------------------------------------------------------------
 // In-launch arrival counts: the workgroups of one unit of work (the context
-// splits of one (b, kv) attention, the score blocks of one top-k row) count
-// themselves in on an 8-byte slot (epoch << 8) | count with one
-// compare-and-swap each; the one that completes the count does the unit's
+// splits of one (b, kv) attention) count themselves in on an 8-byte slot
+// (epoch << 8) | count; the one that completes the count does the unit's
 // final step.  A slot holding another epoch (an earlier launch, stale bytes)
 // counts as empty, so slots need no zeroing; the last arrival leaves the
 // count at 0 under its epoch, so a captured graph (which keeps its epoch)
@@ -127,16 +126,23 @@ __device__ __forceinline__ void nibbles_to_half_pairs(uint32_t w, half2_t out[4]
 unsigned long long next_epoch();
 
 // Called by one thread per arriving workgroup, after the workgroup's results
-// are device-visible; true for the n-th arrival.  The first attempt expects
-// the count one short of complete, so the last arrival needs one round trip.
+// are device-visible; true for the n-th arrival.  A slot still under another
+// epoch is first claimed for this one (reset to count 0 by a compare-and-swap
+// that only succeeds while the stale value is there: once any arrival has
+// claimed it, the others see the epoch and stop); then every arrival counts
+// itself in with one fetch-and-add.  At most three round trips per arrival
+// however many arrive together (compare-and-swap counting retried once per
+// competitor: 16 splits of one (b, kv) took up to 17 us to count in).
 __device__ __forceinline__ bool arrive_last(unsigned long long* slot, unsigned long long epoch, int n) {
-  unsigned long long old = (epoch << 8) | static_cast<unsigned long long>(n - 1);
-  unsigned long long nv = old + 1;
-  while (!__hip_atomic_compare_exchange_strong(slot, &old, nv, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
-                                               __HIP_MEMORY_SCOPE_AGENT))
-    nv = (old >> 8) == epoch ? old + 1 : ((epoch << 8) | 1ull);
-  const bool last = (nv & 0xffull) == static_cast<unsigned long long>(n);
-  if (last) __hip_atomic_store(slot, epoch << 8, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const unsigned long long base = epoch << 8;
+  unsigned long long cur = __hip_atomic_load(slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  while ((cur >> 8) != epoch &&
+         !__hip_atomic_compare_exchange_strong(slot, &cur, base, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT)) {
+  }
+  const unsigned long long old = __hip_atomic_fetch_add(slot, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const bool last = (old & 0xffull) == static_cast<unsigned long long>(n - 1);
+  if (last) __hip_atomic_store(slot, base, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   return last;
 }
 
