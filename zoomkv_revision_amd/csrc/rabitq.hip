@@ -581,11 +581,13 @@ SelectShape select_shape(int64_t n) {
 
 bool use_filter_path(int64_t n, int topk) { return n >= 128ll * topk && select_shape(n).passes <= kSelMaxPasses; }
 
-// k-th largest key (and how many keys equal to it to take, lowest positions
-// first) among the valid items (bit j of `valid`: item j) of a block of NT
-// threads holding NI keys each; the block holds at least k valid items, whose
-// minimum and maximum are mn and mx.  hist[0 .. 4095] must be zero, with a
-// barrier since the clear.
+// Threshold T and how many items equal to it to take (lowest positions
+// first), such that the items > T and those taken == T are the top k among
+// the valid items (bit j of `valid`: item j) of a block of NT threads holding
+// NI keys each; the block holds at least k valid items, whose minimum and
+// maximum are mn and mx.  T is the k-th largest item, or the lower edge of a
+// bin that the top k take whole (the rounds stop there).  hist[0 .. 4095]
+// must be zero, with a barrier since the clear; tmp holds W + 3 words.
 // Radix rounds of 12-bit digits over LDS histograms of 4096 bins: the first
 // digit is taken 12 bits below the top bit of the items' range [mn, mx],
 // each later one 12 bits below the previous, so a 32-bit range takes at most
@@ -641,6 +643,7 @@ __device__ void block_radix_select12(const uint32_t (&key)[NI], uint32_t valid, 
         if (at_or_above >= rem && above < rem) {
           tmp[W] = static_cast<uint32_t>(tid * kPerT + j);
           tmp[W + 1] = static_cast<uint32_t>(above);
+          tmp[W + 2] = static_cast<uint32_t>(c[j]);
         }
         above = at_or_above;
       }
@@ -653,6 +656,9 @@ __device__ void block_radix_select12(const uint32_t (&key)[NI], uint32_t valid, 
     lo = static_cast<uint32_t>(new_lo);
     hi = static_cast<uint32_t>(new_hi < hi ? new_hi : hi);
     if (shift == 0 || !exact) break;
+    // the top k take the whole bin: T = its lower edge, and rem (the bin's
+    // count) covers every item == T
+    if (rem == static_cast<int>(tmp[W + 2])) break;
     shift = shift > 12 ? shift - 12 : 0;
     buf ^= 1;
     // the next round's first barrier orders these reads of tmp before its rewrite

@@ -420,11 +420,14 @@ __device__ __forceinline__ int lanes_below(uint64_t m) {
 }
 
 // Radix select over the n keys key[j] at list positions tid + 1024 j (later
-// positions are ignored): returns T = the k-th largest key and sets remain =
-// how many keys == T belong to the top k.  hist[0] must be zero on entry.
-// Each round: a block histogram of the next 8 bits, then wave 0 (lane l owns
-// bins 252 - 4l .. 255 - 4l, so a prefix sum over lanes counts the keys in
-// higher bins) finds the bin holding the remain-th key.
+// positions are ignored): returns T and remain such that the top k are the
+// keys > T and the first `remain` keys == T in list order.  hist[0] must be
+// zero on entry (both histograms are left dirty).  Each round: a block
+// histogram of the next 8 bits, then wave 0 (lane l owns bins 252 - 4l ..
+// 255 - 4l, so a prefix sum over lanes counts the keys in higher bins) finds
+// the bin holding the remain-th key.  When the top k take every key of that
+// bin, the rounds stop: T = the bin's lowest key value (prefix, low bits 0)
+// and remain = the bin's count, which covers every key == T in it.
 template <int R>
 __device__ __forceinline__ uint32_t radix_select(const uint32_t (&key)[R], int n, int k, int (*hist)[256],
                                                  int* s_sel, int& remain) {
@@ -474,6 +477,7 @@ __device__ __forceinline__ uint32_t radix_select(const uint32_t (&key)[R], int n
         if (at_or_above >= remain && above < remain) {
           s_sel[0] = 4 * (63 - lane) + j;
           s_sel[1] = remain - above;
+          s_sel[2] = cb[j];
         }
         above = at_or_above;
       }
@@ -482,6 +486,7 @@ __device__ __forceinline__ uint32_t radix_select(const uint32_t (&key)[R], int n
     prefix |= static_cast<uint32_t>(s_sel[0]) << shift;
     mask |= 0xFFu << shift;
     remain = s_sel[1];
+    if (remain == s_sel[2]) break;  // the whole bin is in the top k (uniform)
   }
   return prefix;
 }
@@ -594,7 +599,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_reg_kernel(
   __shared__ __align__(16) int s_hist[2][256];
   __shared__ __align__(16) uint32_t s_cnt[R * kTopkWaves];  // [w][j] counts, then their exclusive prefix
   __shared__ uint2 s_cand[kCand];  // the sample keys, then (raw bits, index) of the candidates
-  __shared__ int s_sel[2];
+  __shared__ int s_sel[3];
   __shared__ uint32_t s_tau, s_total;
   const int row = blockIdx.x;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -700,7 +705,7 @@ __global__ __launch_bounds__(kTopkThreads) void quest_topk_kernel(
   __shared__ uint16_t s_q[128];
   __shared__ __align__(16) int s_hist[2][256];
   __shared__ __align__(16) uint32_t s_cnt[4 * kTopkWaves];
-  __shared__ int s_sel[2];
+  __shared__ int s_sel[3];
   __shared__ int s_last;
   const int tid = threadIdx.x, half = tid >> 5, t = tid & 31;
   const int bh = blockIdx.y;
