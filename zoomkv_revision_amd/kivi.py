@@ -9,6 +9,7 @@ reference, S:561-571).
 """
 from __future__ import annotations
 
+import functools
 import math
 from dataclasses import dataclass
 
@@ -214,6 +215,11 @@ def check_kivi4_pack_range(device: torch.device | str | None = None) -> None:
 _WORKSPACE: dict = {}
 
 
+@functools.lru_cache(maxsize=256)
+def _sparse_ws_bytes(bs: int, hq: int, kv: int, n_sel: int, res_len: int, n_splits: int) -> int:
+    return lib().zkv_kivi4_sparse_attention_workspace_size(bs, hq, kv, n_sel, res_len, n_splits)
+
+
 def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     """Attention workspace (split partials and arrival slots) per (device,
     stream), grown on demand: calls on one stream run in order, and calls on
@@ -317,7 +323,7 @@ def kivi4_sparse_attention(q: torch.Tensor, cache: Kivi4Cache, pages: torch.Tens
     kbs, kv = cache.shape
     if kbs != bs or hq % kv != 0:
         raise ValueError(f"q {tuple(q.shape)} does not match cache (bs={kbs}, kv={kv})")
-    if pages.dtype != torch.int64 or pages.dim() != 3 or tuple(pages.shape[:2]) != (bs, kv):
+    if pages.dtype != torch.int64 or pages.dim() != 3 or pages.shape[0] != bs or pages.shape[1] != kv:
         raise ValueError("pages must be int64 [bs, kv, n_sel]")
     if pages.shape[2] > 1 and pages.stride(2) != 1:
         pages = pages.contiguous()
@@ -334,8 +340,9 @@ def kivi4_sparse_attention(q: torch.Tensor, cache: Kivi4Cache, pages: torch.Tens
         raise ValueError("out must be a contiguous [bs, hq, 128] tensor of out_dtype")
     lse = torch.empty(bs, hq, dtype=torch.float32, device=q.device) if return_lse else None
     L = lib()
-    need = L.zkv_kivi4_sparse_attention_workspace_size(bs, hq, kv, n_sel, res_len, n_splits)
-    ws = _workspace(q.device, need) if workspace is None else workspace
+    ws = workspace
+    if ws is None:
+        ws = _workspace(q.device, _sparse_ws_bytes(bs, hq, kv, n_sel, res_len, n_splits))
     check(L.zkv_kivi4_sparse_attention(
         ptr(q3), q3.stride(0), q3.stride(1),
         ptr(cache.groups), cache.g_cap,
@@ -343,7 +350,8 @@ def kivi4_sparse_attention(q: torch.Tensor, cache: Kivi4Cache, pages: torch.Tens
         bs, hq, kv, n_groups, res_len, ptr(pages), pages.stride(0), pages.stride(1), n_sel, sm_scale,
         ptr(out), int(out_dtype == torch.float32), ptr(lse), n_splits,
         ptr(ws), ws.numel() * ws.element_size(), stream_of(q)))
-    out = out.view(bs, hq, HEAD_DIM)
+    if out.dim() != 3 or out.shape[1] != hq:
+        out = out.view(bs, hq, HEAD_DIM)
     out = out.unsqueeze(1) if squeeze else out
     return (out, lse) if return_lse else out
 

@@ -95,7 +95,7 @@ def quest_chunk_score_gqa(queries: torch.Tensor, kv_heads: int, chunk_min: torch
     if d != 128 or q.stride(-1) != 1:
         raise RuntimeError("quest_chunk_score_gqa: queries need head_dim 128, contiguous")
     kv = int(kv_heads)
-    if hq % kv or tuple(raw_q.shape) != (bs, kv, 128) or not raw_q.is_contiguous():
+    if hq % kv or raw_q.shape != (bs, kv, 128) or not raw_q.is_contiguous():
         raise RuntimeError("quest_chunk_score_gqa: raw_q must be a contiguous [bs, kv, 128] with kv | hq")
     if chunk_min.dtype != chunk_max.dtype or chunk_min.dtype not in (torch.bfloat16, torch.float16):
         raise RuntimeError("quest_chunk_score_gqa: chunk_min / chunk_max must both be bf16 or fp16")
@@ -103,7 +103,7 @@ def quest_chunk_score_gqa(queries: torch.Tensor, kv_heads: int, chunk_min: torch
     n_chunks = int(n_chunks)
     if not 1 <= n_chunks <= n_max:
         raise RuntimeError("quest_chunk_score_gqa: need 1 <= n_chunks <= chunk_n_max")
-    if tuple(chunk_min.shape) != (bs, kv, n_max, 128) or chunk_max.shape != chunk_min.shape \
+    if chunk_min.shape != (bs, kv, n_max, 128) or chunk_max.shape != chunk_min.shape \
             or not chunk_min.is_contiguous() or not chunk_max.is_contiguous():
         raise RuntimeError("chunk_min / chunk_max must be contiguous [bs, kv, n_chunks_max, 128]")
     if scores.dtype != torch.float32 or scores.numel() != bs * kv * n_chunks or not scores.is_contiguous():
@@ -157,11 +157,11 @@ def quest_chunk_topk_gqa(queries: torch.Tensor, kv_heads: int, chunk_min: torch.
     # the shape / dtype checks of quest_chunk_score_gqa
     if q.dtype != torch.bfloat16 or raw_q.dtype != torch.bfloat16 or q.shape[-1] != 128 or q.stride(-1) != 1:
         raise RuntimeError("quest_chunk_topk_gqa: queries and raw_q must be bf16 with head_dim 128")
-    if hq % kv or tuple(raw_q.shape) != (bs, kv, 128) or not raw_q.is_contiguous():
+    if hq % kv or raw_q.shape != (bs, kv, 128) or not raw_q.is_contiguous():
         raise RuntimeError("quest_chunk_topk_gqa: raw_q must be a contiguous [bs, kv, 128] with kv | hq")
     if chunk_min.dtype != chunk_max.dtype or chunk_min.dtype not in (torch.bfloat16, torch.float16):
         raise RuntimeError("quest_chunk_topk_gqa: chunk_min / chunk_max must both be bf16 or fp16")
-    if tuple(chunk_min.shape) != (bs, kv, n_max, 128) or chunk_max.shape != chunk_min.shape \
+    if chunk_min.shape != (bs, kv, n_max, 128) or chunk_max.shape != chunk_min.shape \
             or not chunk_min.is_contiguous() or not chunk_max.is_contiguous():
         raise RuntimeError("chunk_min / chunk_max must be contiguous [bs, kv, n_chunks_max, 128]")
     if scores.dtype != torch.float32 or scores.numel() != bs * kv * n_chunks or not scores.is_contiguous():
@@ -171,7 +171,7 @@ def quest_chunk_topk_gqa(queries: torch.Tensor, kv_heads: int, chunk_min: torch.
             raise RuntimeError("valid must be a contiguous bool [bs, kv, n_chunks_max]")
     if out is None:
         out = torch.empty(bs, kv, k, dtype=torch.int64, device=q.device)
-    elif out.dtype != torch.int64 or tuple(out.shape[:2]) != (bs, kv) or out.shape[2] < k or out.stride(2) != 1 \
+    elif out.dtype != torch.int64 or out.shape[0] != bs or out.shape[1] != kv or out.shape[2] < k or out.stride(2) != 1 \
             or out.stride(0) != kv * out.stride(1):
         raise RuntimeError("out must be int64 [bs, kv, >= k] with rows at one stride")
     sl = _slots(q.device, bs * kv)
@@ -179,7 +179,7 @@ def quest_chunk_topk_gqa(queries: torch.Tensor, kv_heads: int, chunk_min: torch.
         ptr(q), q.stride(0), q.stride(1), hq, ptr(raw_q), ptr(chunk_min), ptr(chunk_max),
         int(chunk_min.dtype == torch.float16), ptr(scores), bs, kv, n_chunks, n_max, ptr(valid), k,
         ptr(out), out.stride(1), ptr(sl), sl.numel() * 4, stream_of(q)))
-    return out[:, :, :k]
+    return out if out.shape[2] == k else out[:, :, :k]
 
 
 class QuestKernel:

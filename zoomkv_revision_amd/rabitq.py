@@ -20,7 +20,7 @@ from __future__ import annotations
 
 import torch
 
-from ._lib import check, lib, ptr, require_gpu, stream_of
+from ._lib import check, device_stream, lib, ptr, require_gpu, stream_of
 
 HEAD_DIM = 128
 CODE_BYTES = 16
@@ -88,13 +88,19 @@ _WS: dict = {}
 
 
 def search_workspace(pools: int, queries: int, n: int, topk: int, device) -> torch.Tensor:
+    """The search workspace cached per (device, current stream): searches on
+    one stream run in order; searches on two streams get two workspaces."""
     nbytes = lib().zkv_rabitq_search_workspace_size(pools, queries, n, topk)
-    key = torch.device(device)
+    dev = torch.device(device)
+    key = (dev, device_stream(dev))
     ws = _WS.get(key)
     if ws is None or ws.numel() < nbytes:
-        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=key)
+        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
         _WS[key] = ws
     return ws
+
+
+_F16, _U8, _I64, _F32 = torch.float16, torch.uint8, torch.int64, torch.float32
 
 
 def rabitq_search(q: torch.Tensor, keys: torch.Tensor, codes: torch.Tensor, factors: torch.Tensor,
@@ -110,6 +116,9 @@ def rabitq_search(q: torch.Tensor, keys: torch.Tensor, codes: torch.Tensor, fact
     ``out``: the three output tensors, preallocated with those shapes and
     dtypes (contiguous), written in place and returned.
     """
+    # (the checks are ordered so that the common call -- 3-D pools,
+    # contiguous operands, preallocated outputs -- costs a few microseconds
+    # of host time: the search itself takes ~30 us of device time)
     require_gpu(q, keys, codes, factors, signs)
     _check_signs(signs)
     squeeze = q.dim() == 2
@@ -117,28 +126,38 @@ def rabitq_search(q: torch.Tensor, keys: torch.Tensor, codes: torch.Tensor, fact
     kk = _pools(keys, HEAD_DIM)
     cc = _pools(codes, CODE_BYTES).contiguous()
     ff = _pools(factors, 2).contiguous()
-    assert qq.dtype == torch.float16 and kk.dtype == torch.float16, "q and keys must be fp16"
-    assert cc.dtype == torch.uint8 and ff.dtype == torch.float16
+    assert qq.dtype == _F16 and kk.dtype == _F16, "q and keys must be fp16"
+    assert cc.dtype == _U8 and ff.dtype == _F16
     P, Q, _ = qq.shape
     N = kk.shape[1]
-    assert kk.shape[0] == P and cc.shape[:2] == (P, N) and ff.shape[:2] == (P, N), "pool/key shape mismatch"
-    if kk.stride(-1) != 1 or kk.stride(1) % 8 or kk.stride(0) % 8 or kk.data_ptr() % 16:
+    assert kk.shape[0] == P and cc.shape[0] == P and cc.shape[1] == N and ff.shape[0] == P and \
+        ff.shape[1] == N, "pool/key shape mismatch"
+    ks0, ks1 = kk.stride(0), kk.stride(1)
+    if kk.stride(2) != 1 or ks1 % 8 or ks0 % 8 or kk.data_ptr() % 16:
         kk = kk.contiguous()
+        ks0, ks1 = kk.stride(0), kk.stride(1)
     assert 0 < topk <= N, f"topk={topk} must be in [1, {N}]"
     ws = workspace if workspace is not None else search_workspace(P, Q, N, topk, q.device)
     if out is None:
-        cand = torch.empty(P, Q, topk, dtype=torch.int64, device=q.device)
+        cand = torch.empty(P, Q, topk, dtype=_I64, device=q.device)
         fidx = torch.empty_like(cand)
-        fsc = torch.empty(P, Q, topk, dtype=torch.float32, device=q.device)
+        fsc = torch.empty(P, Q, topk, dtype=_F32, device=q.device)
     else:
         cand, fidx, fsc = out
-        for t, dt in ((cand, torch.int64), (fidx, torch.int64), (fsc, torch.float32)):
-            assert t.dtype == dt and t.is_contiguous() and t.numel() == P * Q * topk and t.device == q.device, \
+        shape = (P, Q, topk)
+        dev = q.device
+        for t, dt in ((cand, _I64), (fidx, _I64), (fsc, _F32)):
+            assert t.dtype == dt and t.is_contiguous() and t.numel() == P * Q * topk and t.device == dev, \
                 "out tensors: contiguous int64, int64, fp32 with P * Q * topk elements on q's device"
-        cand, fidx, fsc = cand.view(P, Q, topk), fidx.view(P, Q, topk), fsc.view(P, Q, topk)
-    check(lib().zkv_rabitq_search(ptr(qq), ptr(kk), kk.stride(0), kk.stride(1), ptr(cc), ptr(ff),
-                                  ptr(signs), P, Q, N, topk, ptr(cand), ptr(fidx), ptr(fsc), ptr(ws),
-                                  ws.numel(), stream_of(q)))
+        if cand.shape != shape:
+            cand = cand.view(shape)
+        if fidx.shape != shape:
+            fidx = fidx.view(shape)
+        if fsc.shape != shape:
+            fsc = fsc.view(shape)
+    check(lib().zkv_rabitq_search(qq.data_ptr(), kk.data_ptr(), ks0, ks1, cc.data_ptr(), ff.data_ptr(),
+                                  signs.data_ptr(), P, Q, N, topk, cand.data_ptr(), fidx.data_ptr(),
+                                  fsc.data_ptr(), ws.data_ptr(), ws.numel(), stream_of(q)))
     if squeeze:
         return cand[0], fidx[0], fsc[0]
     return cand, fidx, fsc
