@@ -41,8 +41,14 @@ __global__ __launch_bounds__(128) void chunk_encode_kernel(
     acc = acc + x[t];  // canonical sequential fp32 sum over the chunk's tokens
   }
   const float safe = kivi_safe(kivi_scale(mn, mx));
+  if (safe < INFINITY) {
+    const float r = 1.0f / safe;
 #pragma unroll
-  for (int t = 0; t < G; ++t) codes[t][d] = static_cast<uint8_t>(kivi_code(x[t], mn, safe));
+    for (int t = 0; t < G; ++t) codes[t][d] = static_cast<uint8_t>(kivi_code_r(x[t], mn, safe, r));
+  } else {
+#pragma unroll
+    for (int t = 0; t < G; ++t) codes[t][d] = static_cast<uint8_t>(kivi_code(x[t], mn, safe));
+  }
 
   const int64_t bh = static_cast<int64_t>(b) * kv + h;
   const int64_t chunk = bh * n_chunks_max + chunk_start + c;
@@ -111,8 +117,14 @@ __global__ __launch_bounds__(128) void kivi4_pack_kernel(
     }
     const float scale = kivi_scale(mn, mx);
     const float safe = kivi_safe(scale);
+    if (safe < INFINITY) {
+      const float r = 1.0f / safe;
 #pragma unroll
-    for (int t = 0; t < 32; ++t) kc[t][d] = static_cast<uint8_t>(kivi_code(x[t], mn, safe));
+      for (int t = 0; t < 32; ++t) kc[t][d] = static_cast<uint8_t>(kivi_code_r(x[t], mn, safe, r));
+    } else {
+#pragma unroll
+      for (int t = 0; t < 32; ++t) kc[t][d] = static_cast<uint8_t>(kivi_code(x[t], mn, safe));
+    }
     const int p = d >> 3, j = d & 7;
     const int slot = 2 * (j & 3) + (j >> 2);
     uint16_t* km = k_meta + p * 16;
@@ -143,8 +155,14 @@ __global__ __launch_bounds__(128) void kivi4_pack_kernel(
     }
     const float scale = kivi_scale(mn, mx);
     const float safe = kivi_safe(scale);
+    if (safe < INFINITY) {
+      const float r = 1.0f / safe;
 #pragma unroll
-    for (int i = 0; i < 32; ++i) vc[t][32 * gd + i] = static_cast<uint8_t>(kivi_code(x[i], mn, safe));
+      for (int i = 0; i < 32; ++i) vc[t][32 * gd + i] = static_cast<uint8_t>(kivi_code_r(x[i], mn, safe, r));
+    } else {
+#pragma unroll
+      for (int i = 0; i < 32; ++i) vc[t][32 * gd + i] = static_cast<uint8_t>(kivi_code(x[i], mn, safe));
+    }
     // token t = 16m + 4r + i: half m's block, entry (gd, r) = 4 scales then 4 zeros
     const int m = t >> 4, r = (t >> 2) & 3, i = t & 3;
     uint16_t* vm = v_meta + m * 128 + (gd * 4 + r) * 8;

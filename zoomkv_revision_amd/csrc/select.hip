@@ -1023,7 +1023,7 @@ __global__ __launch_bounds__(T) void kivi_qk_row_kernel(
   }
   float sc[8];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) sc[j] = bf16r(bf16r(mx[j] - mn[j]) / 15.0f);
+  for (int j = 0; j < 8; ++j) sc[j] = kivi_scale(mn[j], mx[j]);
   // every lane runs the dot (all 16 lanes of a row must be active for DPP);
   // rows without a valid chunk discard it
   const float acc = QkRowDot<0>::run(0.0f, words, sc, mn, qv);
@@ -1091,7 +1091,7 @@ __global__ __launch_bounds__(T) void kivi_qk_kernel(
       const float mn = bf16_to_f32(cmin[mrow + d]);
       const float mx = bf16_to_f32(cmax[mrow + d]);
       s_mn[local][d] = mn;
-      s_sc[local][d] = bf16r(bf16r(mx - mn) / 15.0f);
+      s_sc[local][d] = kivi_scale(mn, mx);
     }
   }
   __syncthreads();

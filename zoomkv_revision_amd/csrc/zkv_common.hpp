@@ -77,6 +77,33 @@ __device__ __forceinline__ uint32_t half2_as_u32(half2_t h) { return __builtin_b
 // scalar converted to bf16.
 constexpr float kBf16OneEm8 = __builtin_bit_cast(float, 0x322C0000u);  // bf16(1e-8)
 
+// Correctly rounded fp32 quotient x / b from r = 1 / b (itself correctly
+// rounded): q = x r, then one fused multiply-add step with the exact
+// remainder x - q b (Markstein's correction).  For bf16 values x and b with b,
+// r and the quotient normal, the result is x / b bit for bit: the rounding
+// depends only on the significands there, and every pair of bf16
+// significands, and every bf16 x over b = 15, was checked against the IEEE
+// division (tests/test_division_step.py).  Three VALU instructions against
+// the ten of an IEEE division.
+__device__ __forceinline__ float div_recip(float x, float b, float r) {
+  const float q = x * r;
+  return __builtin_fmaf(__builtin_fmaf(-q, b, x), r, q);
+}
+
+// x / 15 for a bf16 x: the multiply-add step where the quotient is normal
+// and finite or x is a zero (kept with its sign: the step turns -0 into +0),
+// the IEEE division otherwise (subnormal results, inf, NaN: a per-lane branch
+// that ordinary inputs never take).
+__device__ __forceinline__ float div15_bf16(float x) {
+  constexpr float kRecip15 = 1.0f / 15.0f;  // correctly rounded by the compiler
+  const float ax = fabsf(x);
+  if ((ax >= 0x1p-120f && ax <= 0x1p127f) || ax == 0.0f) {
+    const float q = div_recip(x, 15.0f, kRecip15);
+    return ax == 0.0f ? x : q;
+  }
+  return x / 15.0f;
+}
+
 // One step of the KIVI bf16 ladder: integer code of x in [mn, mn + 15*scale].
 //   scale = bf16(bf16(mx - mn) / 15); safe = max(scale, bf16(1e-8))
 //   code  = rne(clamp(bf16(bf16(x - mn) / safe), 0, 15))
@@ -89,8 +116,21 @@ __device__ __forceinline__ uint32_t kivi_code(float x, float mn, float safe) {
   return static_cast<uint32_t>(__builtin_rintf(qv));
 }
 
+// kivi_code with the division as div_recip(d, safe, r), r = 1 / safe, for a
+// finite safe (the caller branches to kivi_code otherwise).  safe >= bf16(1e-8)
+// and safe <= bf16max / 15 keep safe and r normal, and d = bf16(x - mn) <=
+// bf16(mx - mn) is finite; where the quotient or the remainder leaves the
+// normal range (d below ~2^-118) the quotient is below 2^-90 and both forms
+// give code 0.
+__device__ __forceinline__ uint32_t kivi_code_r(float x, float mn, float safe, float r) {
+  float d = bf16r(x - mn);
+  float qv = bf16r(div_recip(d, safe, r));
+  qv = fminf(fmaxf(qv, 0.0f), 15.0f);
+  return static_cast<uint32_t>(__builtin_rintf(qv));
+}
+
 __device__ __forceinline__ float kivi_scale(float mn, float mx) {
-  return bf16r(bf16r(mx - mn) / 15.0f);
+  return bf16r(div15_bf16(bf16r(mx - mn)));
 }
 
 // ---------------------------------------------------------------------------
