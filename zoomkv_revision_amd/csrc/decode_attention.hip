@@ -714,7 +714,8 @@ __device__ __forceinline__ float load_partial(const float* p) {
 // same arithmetic, so they give the same bits.  Returns o; mmax and den are
 // the merged base-2 max and denominator (for the LSE).  Up to kBatch splits,
 // every partial is requested before any is used (unconditional loads, the
-// split index clamped), so the merge costs one memory round trip.
+// split index clamped), so the merge costs one memory round trip; more
+// splits take two per batch of kBatch.
 template <bool kAgent>
 __device__ __forceinline__ float combine_splits(const float* ws_o, const float* ws_ml, int64_t row0, int gqa,
                                                 int n_splits, int d, float& mmax, float& den) {
@@ -740,14 +741,32 @@ __device__ __forceinline__ float combine_splits(const float* ws_o, const float* 
       num = s < n_splits ? num + w * ov[s] : num;
     }
   } else {
-    for (int s = 0; s < n_splits; ++s)
-      mmax = fmaxf(mmax, load_partial<kAgent>(ws_ml + (row0 + static_cast<int64_t>(s) * gqa) * 2));
-#pragma unroll 4
-    for (int s = 0; s < n_splits; ++s) {
-      const int64_t row = row0 + static_cast<int64_t>(s) * gqa;
-      const float w = __builtin_amdgcn_exp2f(load_partial<kAgent>(ws_ml + row * 2) - mmax);
-      den += w * load_partial<kAgent>(ws_ml + row * 2 + 1);
-      num += w * load_partial<kAgent>(ws_o + row * 128 + d);
+    // batches of kBatch splits, each batch's loads issued together (the
+    // split index clamped): two round trips per batch instead of one per
+    // split; the same max and the same sums in split order
+    for (int s0 = 0; s0 < n_splits; s0 += kBatch) {
+      float mv[kBatch];
+#pragma unroll
+      for (int s = 0; s < kBatch; ++s)
+        mv[s] = load_partial<kAgent>(ws_ml + (row0 + static_cast<int64_t>(min(s0 + s, n_splits - 1)) * gqa) * 2);
+#pragma unroll
+      for (int s = 0; s < kBatch; ++s) mmax = fmaxf(mmax, mv[s]);
+    }
+    for (int s0 = 0; s0 < n_splits; s0 += kBatch) {
+      float mv[kBatch], lv[kBatch], ov[kBatch];
+#pragma unroll
+      for (int s = 0; s < kBatch; ++s) {
+        const int64_t row = row0 + static_cast<int64_t>(min(s0 + s, n_splits - 1)) * gqa;
+        mv[s] = load_partial<kAgent>(ws_ml + row * 2);
+        lv[s] = load_partial<kAgent>(ws_ml + row * 2 + 1);
+        ov[s] = load_partial<kAgent>(ws_o + row * 128 + d);
+      }
+#pragma unroll
+      for (int s = 0; s < kBatch; ++s) {
+        const float w = __builtin_amdgcn_exp2f(mv[s] - mmax);
+        den = s0 + s < n_splits ? den + w * lv[s] : den;
+        num = s0 + s < n_splits ? num + w * ov[s] : num;
+      }
     }
   }
   return den > 0.0f ? num / den : 0.0f;
@@ -755,14 +774,13 @@ __device__ __forceinline__ float combine_splits(const float* ws_o, const float* 
 
 // In-launch split merge, run by every workgroup after its partial stores
 // (store_agent).  Each workgroup waits until its own stores are complete,
-// then one lane counts the workgroup in on the (b, kv) slot with a
-// compare-and-swap: a slot whose epoch is not this launch's is stale (an
-// earlier launch, or fresh memory) and restarts at 1; the last arrival
-// resets the count to 0 under the launch's epoch.  The first attempt
-// expects the count one short of complete, so the last arrival -- the one on
-// the launch's critical path -- needs a single round trip.  The workgroup that
-// brings the count to n_splits merges every split's partial with
-// combine_splits, so which workgroup merges does not change the bits.
+// then one lane counts the workgroup in on the (b, kv) slot (arrive_last: a
+// slot whose epoch is not this launch's is stale -- an earlier launch, or
+// fresh memory -- and is claimed for this epoch at count 0, then every
+// arrival adds 1; the last arrival resets the count to 0 under the launch's
+// epoch).  The workgroup that brings the count to n_splits merges every
+// split's partial with combine_splits, so which workgroup merges does not
+// change the bits.
 __device__ __forceinline__ void merge_splits_last(const AttnParams& p, int64_t bh, int tid, int nthreads,
                                                   int* s_last) {
   // this lane's partial stores are device-visible (the memory clobber keeps
