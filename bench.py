@@ -258,7 +258,8 @@ def run_c1(args):
                    "batch": 1, "q_heads": 32, "kv_heads": 8, "head_dim": 128, "context": 4096,
                    "outlier_key_channels": 4, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": pack_bytes / (k_ms * 1e-3) / 1e9, "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": pack_bytes / (k_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, "traffic": None,
+                     "unit": "GB/s", "frac": pack_bytes / (k_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                     "traffic": read_traffic("c1_kivi4_pack_traffic.json"),
                      "kernel": "kivi4_pack_kernel", "kernel_ms": k_ms, "algorithmic_bytes": pack_bytes},
         "algorithmic_bytes_per_step": {"pack": pack_bytes, "attention": attn_bytes},
         "cpu_baseline": cpu,
