@@ -275,6 +275,22 @@ int zkv_kivi_qk_dense_sparse(const int64_t* chunk_ids, int64_t id_sb, int64_t id
                              float* out_scores, int64_t* out_indices, int64_t o_sb, int64_t o_sh,
                              int bs, int kv, int nk, zkv_stream_t stream);
 
+/* zkv_kivi_qk_dense_sparse with a compact output: slot i's lanes 0 ..
+ * out_width-1 at i*out_width (max(dense_topk, sparse_topk) <= out_width <=
+ * group_size; out_scores / out_indices [bs, kv, >= nk*out_width]).  No
+ * counterpart in the reference: polar_cache.compute uses it so the global
+ * top-k reads only the kept lanes (the entries it drops are the (-1e30, 0)
+ * fillers, in the same relative order otherwise, so a top-k that takes no
+ * filler selects the same tokens). */
+int zkv_kivi_qk_dense_sparse_compact(const int64_t* chunk_ids, int64_t id_sb, int64_t id_sh,
+                                     const uint8_t* dense_mask, int64_t dm_sb, int64_t dm_sh,
+                                     const int32_t* packed_K, int64_t pk_sb, int64_t pk_sh, int n_packed,
+                                     const uint16_t* chunk_min, const uint16_t* chunk_max, int64_t cm_sb,
+                                     int64_t cm_sh, int n_chunks_max, const uint16_t* raw_q, int64_t q_sb,
+                                     int64_t q_sh, int dense_topk, int sparse_topk, int group_size,
+                                     int out_width, float* out_scores, int64_t* out_indices, int64_t o_sb,
+                                     int64_t o_sh, int bs, int kv, int nk, zkv_stream_t stream);
+
 /* Quest page metadata of a paged cache in fp16: per (b, kv, page, channel)
  * min (rounded toward -inf) and max (toward +inf) of bf16 keys [bs, kv, n_tok,
  * 128] at element strides (k_sb, k_sh, k_st), pages of page_size tokens ->

@@ -173,6 +173,62 @@ def test_kivi_qk_dense_sparse_bit_exact(rng, g):
     assert np.all(gs[..., nk * g:] == 7.0) and np.all(gi[..., nk * g:] == -9)
 
 
+@pytest.mark.parametrize("g,dense_topk,sparse_topk,width", [(16, 8, 8, 8), (16, 8, 4, 8), (16, 6, 3, 7),
+                                                            (8, 4, 2, 4)])
+def test_kivi_qk_compact_output(rng, g, dense_topk, sparse_topk, width):
+    """The compact stage-2 output (out_width lanes per chunk) holds the
+    oracle's kept lanes at slot * width, leaves the rest of the buffer alone,
+    and the global top-k + gather over it picks the same tokens as over the
+    full layout whenever no (-1e30, 0) filler can be reached."""
+    from zoomkv_revision_amd.kivi import partial_chunk_kivi_qk_dense_sparse_cuda
+    from zoomkv_revision_amd.topk import float_topk_gather_concat_3d
+    bs, kv, n_chunks, nk, k, sk = 2, 3, 90, 64, 40, 5
+    keys = gaussian_bf16(rng, (bs, kv, n_chunks * g, 128), outlier_channels=4)
+    mn, mx, _, packed = encode_chunks_ref(keys, g)
+    q = gaussian_bf16(rng, (bs, kv, 128))
+    ids = rng.integers(0, n_chunks, size=(bs, kv, nk))
+    dm = rng.random((bs, kv, nk)) > 0.6
+    rs, ri = osel.kivi_qk_dense_sparse(ids, dm, packed, mn, mx, q, dense_topk, sparse_topk, g)
+    args = (torch.from_numpy(ids).cuda(), torch.from_numpy(dm).cuda(), torch.from_numpy(packed).cuda(),
+            to_bf16(mn), to_bf16(mx), to_bf16(q), dense_topk, sparse_topk, g)
+    cs = torch.full((bs, kv, nk * width + 3), 7.0, device="cuda")
+    ci = torch.full((bs, kv, nk * width + 3), -9, dtype=torch.int64, device="cuda")
+    partial_chunk_kivi_qk_dense_sparse_cuda(*args, cs, ci, out_width=width)
+    gs, gi = from_torch(cs), from_torch(ci)
+    want_s = rs.reshape(bs, kv, nk, g)[..., :width].reshape(bs, kv, nk * width)
+    want_i = ri.reshape(bs, kv, nk, g)[..., :width].reshape(bs, kv, nk * width)
+    assert np.array_equal(gs[..., :nk * width].view(np.uint32), want_s.view(np.uint32))
+    assert np.array_equal(gi[..., :nk * width], want_i)
+    assert np.all(gs[..., nk * width:] == 7.0) and np.all(gi[..., nk * width:] == -9)
+    # the same final selection as over the full layout (nk * min(keep) >= k)
+    assert nk * min(dense_topk, sparse_topk) >= k
+    fs = torch.empty(bs, kv, nk * g, device="cuda")
+    fi = torch.empty(bs, kv, nk * g, dtype=torch.int64, device="cuda")
+    partial_chunk_kivi_qk_dense_sparse_cuda(*args, fs, fi)
+    skipped = torch.from_numpy(rng.integers(0, 10 ** 6, size=(bs, kv, sk))).cuda()
+    out_full = torch.empty(bs, kv, k + sk, dtype=torch.int64, device="cuda")
+    out_compact = torch.empty_like(out_full)
+    float_topk_gather_concat_3d(fs, fi, skipped, out_full, k)
+    float_topk_gather_concat_3d(cs[..., :nk * width], ci[..., :nk * width], skipped, out_compact, k)
+    assert torch.equal(out_full, out_compact)
+
+
+def test_kivi_qk_compact_rejects_narrow_width(rng):
+    from zoomkv_revision_amd._lib import ZkvError
+    from zoomkv_revision_amd.kivi import partial_chunk_kivi_qk_dense_sparse_cuda
+    g, nk = 16, 4
+    keys = gaussian_bf16(rng, (1, 1, 8 * g, 128))
+    mn, mx, _, packed = encode_chunks_ref(keys, g)
+    q = gaussian_bf16(rng, (1, 1, 128))
+    ids = torch.zeros(1, 1, nk, dtype=torch.int64, device="cuda")
+    dm = torch.ones(1, 1, nk, dtype=torch.bool, device="cuda")
+    o = torch.empty(1, 1, nk * g, device="cuda")
+    oi = torch.empty(1, 1, nk * g, dtype=torch.int64, device="cuda")
+    with pytest.raises(ZkvError, match="out_width"):
+        partial_chunk_kivi_qk_dense_sparse_cuda(ids, dm, torch.from_numpy(packed).cuda(), to_bf16(mn), to_bf16(mx),
+                                                to_bf16(q), 8, 8, g, o, oi, out_width=6)
+
+
 @pytest.mark.parametrize("q_offset", [0, 1])
 def test_kivi_qk_unaligned_views(rng, q_offset):
     """Chunk-16 scorer on sliced views: metadata rows from a larger cache

@@ -52,6 +52,9 @@ SIGNATURES = {
     "zkv_kivi_qk_dense_sparse": (I32, [P, I64, I64, P, I64, I64, P, I64, I64, I32, P, P, I64, I64,
                                        I32, P, I64, I64, I32, I32, I32, P, P, I64, I64,
                                        I32, I32, I32, P]),
+    "zkv_kivi_qk_dense_sparse_compact": (I32, [P, I64, I64, P, I64, I64, P, I64, I64, I32, P, P, I64, I64,
+                                               I32, P, I64, I64, I32, I32, I32, I32, P, P, I64, I64,
+                                               I32, I32, I32, P]),
     "zkv_page_minmax_f16": (I32, [P, I64, I64, I64, I32, I32, I32, I32, I32, P, P, P]),
     "zkv_kivi4_sparse_attention_workspace_size": (SZ, [I32, I32, I32, I32, I32, I32]),
     "zkv_kivi4_sparse_attention": (I32, [P, I64, I64, P, I32, P, P, I32, I32, I32, I32, I32,

@@ -607,6 +607,23 @@ class polar_cache:
     # ------------------------------------------------------------------
     # decode attention (S:1589-1775) and selection (S:2195-2467, 2688-2779)
     # ------------------------------------------------------------------
+    def _stage2_out_width(self, layer_idx) -> int | None:
+        """Lanes per chunk that stage 2 writes (its compact output), or None
+        for the full chunk.  Only the kept lanes are written when the global
+        top-k cannot reach a (-1e30, 0) filler: every chunk id is in range
+        (the packed chunks cover the Quest chunks) and the chunks keep at least
+        final_topk tokens.  The top-k then reads half the entries at the
+        production knobs (8 of 16) and picks the same tokens."""
+        chunk = self.quest_chunk_size
+        n_chunks, nk = self._cached_quest_n_chunks, self._cached_quest_nk
+        dense_topk = max(1, min(self.cds_dense_topk, chunk))
+        sparse_topk = max(1, min(self.cds_sparse_topk, chunk))
+        width = max(dense_topk, sparse_topk)
+        valid_chunks = int(self.cpu_valid_end[layer_idx]) // chunk
+        if width < chunk and valid_chunks >= n_chunks and nk * min(dense_topk, sparse_topk) >= self.final_topk:
+            return width
+        return None
+
     def _select(self, queries, layer_idx):
         """GQA-mean query + Quest stage 1 (one launch) + CDS dense / sparse +
         KIVI stage 2 + global top-k: retrieval-zone token indices
@@ -644,9 +661,12 @@ class polar_cache:
         valid_chunks = int(self.cpu_valid_end[layer_idx]) // chunk
         packed = self.key_kivi_packed_gpu[layer_idx][:, :, :valid_chunks]
         out_scores, out_indices = self._cached_cds_out_scores, self._cached_cds_out_indices
+        width = self._stage2_out_width(layer_idx)
+        if width is not None:
+            out_scores, out_indices = out_scores[:, :, :nk * width], out_indices[:, :, :nk * width]
         kivi.partial_chunk_kivi_qk_dense_sparse_cuda(
             chunk_idx, dense_mask, packed, self._chunk_key_min_gpu[layer_idx], self._chunk_key_max_gpu[layer_idx],
-            raw_q, dense_topk, sparse_topk, chunk, out_scores, out_indices)
+            raw_q, dense_topk, sparse_topk, chunk, out_scores, out_indices, out_width=width)
         k = min(self.final_topk, out_scores.shape[-1])
         sk = self._chunk_skipped_count[layer_idx]
         skipped = self._chunk_skipped_indices_gpu[layer_idx][:bs, :, :sk]

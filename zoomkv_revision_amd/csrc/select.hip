@@ -992,7 +992,7 @@ __global__ __launch_bounds__(T) void kivi_qk_row_kernel(
     int n_packed, const uint16_t* __restrict__ cmin, const uint16_t* __restrict__ cmax, int64_t cm_sb,
     int64_t cm_sh, int n_max, const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_sh,
     float* __restrict__ out_s, int64_t* __restrict__ out_i, int64_t o_sb, int64_t o_sh, int nk,
-    int dense_topk, int sparse_topk) {
+    int dense_topk, int sparse_topk, int out_w) {
   constexpr int G = 16, kChunks = T / G;
   const int b = blockIdx.z, h = blockIdx.y;
   const int local = threadIdx.x / G, lane = threadIdx.x % G;
@@ -1044,8 +1044,8 @@ __global__ __launch_bounds__(T) void kivi_qk_row_kernel(
       }
     }
   }
-  if (valid_slot) {
-    const int64_t oi = b * o_sb + h * o_sh + static_cast<int64_t>(slot) * G + lane;
+  if (valid_slot && lane < out_w) {
+    const int64_t oi = b * o_sb + h * o_sh + static_cast<int64_t>(slot) * out_w + lane;
     const int keep = dense ? dense_topk : sparse_topk;
     out_s[oi] = lane < keep ? score : -1e30f;
     out_i[oi] = lane < keep ? static_cast<int64_t>(token) : 0;
@@ -1059,7 +1059,7 @@ __global__ __launch_bounds__(T) void kivi_qk_kernel(
     int n_packed, const uint16_t* __restrict__ cmin, const uint16_t* __restrict__ cmax, int64_t cm_sb,
     int64_t cm_sh, int n_max, const uint16_t* __restrict__ q, int64_t q_sb, int64_t q_sh,
     float* __restrict__ out_s, int64_t* __restrict__ out_i, int64_t o_sb, int64_t o_sh, int nk,
-    int dense_topk, int sparse_topk) {
+    int dense_topk, int sparse_topk, int out_w) {
   constexpr int kChunks = T / G;
   // q is the same for every chunk of the block; the per-chunk rows are padded
   // by 4 floats so that the chunks of one wave read different LDS banks.
@@ -1134,8 +1134,8 @@ __global__ __launch_bounds__(T) void kivi_qk_kernel(
       }
     }
   }
-  if (valid_slot) {
-    const int64_t oi = b * o_sb + h * o_sh + static_cast<int64_t>(slot) * G + lane;
+  if (valid_slot && lane < out_w) {
+    const int64_t oi = b * o_sb + h * o_sh + static_cast<int64_t>(slot) * out_w + lane;
     const int keep = dense ? dense_topk : sparse_topk;
     out_s[oi] = lane < keep ? score : -1e30f;
     out_i[oi] = lane < keep ? static_cast<int64_t>(token) : 0;
@@ -1380,16 +1380,14 @@ extern "C" int zkv_gqa_mean_query(const uint16_t* q, int64_t q_sb, int64_t q_sh,
   return check_launch("gqa_mean_kernel");
 }
 
-extern "C" int zkv_kivi_qk_dense_sparse(const int64_t* chunk_ids, int64_t id_sb, int64_t id_sh,
-                                        const uint8_t* dense_mask, int64_t dm_sb, int64_t dm_sh,
-                                        const int32_t* packed_K, int64_t pk_sb, int64_t pk_sh,
-                                        int n_packed, const uint16_t* chunk_min,
-                                        const uint16_t* chunk_max, int64_t cm_sb, int64_t cm_sh,
-                                        int n_chunks_max, const uint16_t* raw_q, int64_t q_sb,
-                                        int64_t q_sh, int dense_topk, int sparse_topk,
-                                        int group_size, float* out_scores, int64_t* out_indices,
-                                        int64_t o_sb, int64_t o_sh, int bs, int kv, int nk,
-                                        zkv_stream_t stream) {
+namespace {
+int kivi_qk_launch(const int64_t* chunk_ids, int64_t id_sb, int64_t id_sh, const uint8_t* dense_mask,
+                   int64_t dm_sb, int64_t dm_sh, const int32_t* packed_K, int64_t pk_sb, int64_t pk_sh,
+                   int n_packed, const uint16_t* chunk_min, const uint16_t* chunk_max, int64_t cm_sb,
+                   int64_t cm_sh, int n_chunks_max, const uint16_t* raw_q, int64_t q_sb, int64_t q_sh,
+                   int dense_topk, int sparse_topk, int group_size, int out_width, float* out_scores,
+                   int64_t* out_indices, int64_t o_sb, int64_t o_sh, int bs, int kv, int nk,
+                   zkv_stream_t stream) {
   ZKV_REQUIRE(chunk_ids && dense_mask && packed_K && chunk_min && chunk_max && raw_q && out_scores &&
                   out_indices,
               "zkv_kivi_qk_dense_sparse: null pointer");
@@ -1399,6 +1397,9 @@ extern "C" int zkv_kivi_qk_dense_sparse(const int64_t* chunk_ids, int64_t id_sb,
                   sparse_topk <= group_size,
               "zkv_kivi_qk_dense_sparse: dense_topk=%d sparse_topk=%d out of [1, %d]", dense_topk,
               sparse_topk, group_size);
+  ZKV_REQUIRE(out_width >= (dense_topk > sparse_topk ? dense_topk : sparse_topk) && out_width <= group_size,
+              "zkv_kivi_qk_dense_sparse: out_width=%d outside [max(dense_topk, sparse_topk), %d]", out_width,
+              group_size);
   ZKV_REQUIRE(bs > 0 && kv > 0 && nk >= 0, "zkv_kivi_qk_dense_sparse: bad sizes");
   if (nk == 0) return ZKV_OK;
   auto s = reinterpret_cast<hipStream_t>(stream);
@@ -1422,7 +1423,7 @@ extern "C" int zkv_kivi_qk_dense_sparse(const int64_t* chunk_ids, int64_t id_sb,
                                                 packed_K, pk_sb, pk_sh, n_packed, chunk_min, chunk_max, \
                                                 cm_sb, cm_sh, n_chunks_max, raw_q, q_sb, q_sh,          \
                                                 out_scores, out_indices, o_sb, o_sh, nk, dense_topk,    \
-                                                sparse_topk)
+                                                sparse_topk, out_width)
     if (vec)
       ZKV_KIVI_QK_ROW(true);
     else
@@ -1433,9 +1434,43 @@ extern "C" int zkv_kivi_qk_dense_sparse(const int64_t* chunk_ids, int64_t id_sb,
     kivi_qk_kernel<8, kT><<<grid, kT, 0, s>>>(chunk_ids, id_sb, id_sh, dense_mask, dm_sb, dm_sh,
                                               packed_K, pk_sb, pk_sh, n_packed, chunk_min, chunk_max,
                                               cm_sb, cm_sh, n_chunks_max, raw_q, q_sb, q_sh, out_scores,
-                                              out_indices, o_sb, o_sh, nk, dense_topk, sparse_topk);
+                                              out_indices, o_sb, o_sh, nk, dense_topk, sparse_topk,
+                                              out_width);
   }
   return check_launch("kivi_qk_kernel");
+}
+}  // namespace
+
+extern "C" int zkv_kivi_qk_dense_sparse(const int64_t* chunk_ids, int64_t id_sb, int64_t id_sh,
+                                        const uint8_t* dense_mask, int64_t dm_sb, int64_t dm_sh,
+                                        const int32_t* packed_K, int64_t pk_sb, int64_t pk_sh,
+                                        int n_packed, const uint16_t* chunk_min,
+                                        const uint16_t* chunk_max, int64_t cm_sb, int64_t cm_sh,
+                                        int n_chunks_max, const uint16_t* raw_q, int64_t q_sb,
+                                        int64_t q_sh, int dense_topk, int sparse_topk,
+                                        int group_size, float* out_scores, int64_t* out_indices,
+                                        int64_t o_sb, int64_t o_sh, int bs, int kv, int nk,
+                                        zkv_stream_t stream) {
+  return kivi_qk_launch(chunk_ids, id_sb, id_sh, dense_mask, dm_sb, dm_sh, packed_K, pk_sb, pk_sh, n_packed,
+                        chunk_min, chunk_max, cm_sb, cm_sh, n_chunks_max, raw_q, q_sb, q_sh, dense_topk,
+                        sparse_topk, group_size, group_size, out_scores, out_indices, o_sb, o_sh, bs, kv, nk,
+                        stream);
+}
+
+extern "C" int zkv_kivi_qk_dense_sparse_compact(const int64_t* chunk_ids, int64_t id_sb, int64_t id_sh,
+                                                const uint8_t* dense_mask, int64_t dm_sb, int64_t dm_sh,
+                                                const int32_t* packed_K, int64_t pk_sb, int64_t pk_sh,
+                                                int n_packed, const uint16_t* chunk_min,
+                                                const uint16_t* chunk_max, int64_t cm_sb, int64_t cm_sh,
+                                                int n_chunks_max, const uint16_t* raw_q, int64_t q_sb,
+                                                int64_t q_sh, int dense_topk, int sparse_topk,
+                                                int group_size, int out_width, float* out_scores,
+                                                int64_t* out_indices, int64_t o_sb, int64_t o_sh, int bs,
+                                                int kv, int nk, zkv_stream_t stream) {
+  return kivi_qk_launch(chunk_ids, id_sb, id_sh, dense_mask, dm_sb, dm_sh, packed_K, pk_sb, pk_sh, n_packed,
+                        chunk_min, chunk_max, cm_sb, cm_sh, n_chunks_max, raw_q, q_sb, q_sh, dense_topk,
+                        sparse_topk, group_size, out_width, out_scores, out_indices, o_sb, o_sh, bs, kv, nk,
+                        stream);
 }
 
 extern "C" int zkv_page_minmax_f16(const uint16_t* keys, int64_t k_sb, int64_t k_sh, int64_t k_st,

@@ -382,8 +382,11 @@ def attention_path_bytes(cache, layer: int) -> dict:
     classify = max(1, min(cache.cds_dense_topk, chunk)) != max(1, min(cache.cds_sparse_topk, chunk))
     density = units * (nk * (8 + d * 2 + 4) + d * 2) if classify else 0    # skipped when dense = sparse
     topk2 = units * (nk * 4 + nk) if classify else 0
-    stage2 = units * (nk * (8 + 1 + 16 * chunk * 4 + 2 * d * 2) + nk * chunk * 12)
-    gather = units * (nk * chunk * 12 + sk * 8 + (k_final + sk) * 8)
+    # stage 2 writes (and the top-k reads) width lanes per chunk: the kept ones
+    # when compute uses the compact output, else the whole chunk
+    width = cache._stage2_out_width(layer) or chunk
+    stage2 = units * (nk * (8 + 1 + 16 * chunk * 4 + 2 * d * 2) + nk * width * 12)
+    gather = units * (nk * width * 12 + sk * 8 + (k_final + sk) * 8)
     if getattr(cache, "kv_format", "bf16") == "kivi4":
         # the selected tokens from 4-bit records (160 B per token per KV head:
         # K / V codes and their share of the scale / zero), the skipped tail

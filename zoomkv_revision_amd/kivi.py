@@ -468,9 +468,15 @@ def attention_merge(workspace: torch.Tensor, bs: int, hq: int, kv: int, n_splits
 
 def partial_chunk_kivi_qk_dense_sparse_cuda(chunk_ids, dense_mask, packed_K, chunk_min, chunk_max,
                                             raw_q, dense_topk, sparse_topk, group_size, out_scores,
-                                            out_indices, kernel=None) -> None:
+                                            out_indices, kernel=None, out_width=None) -> None:
     """KIVI stage-2 scorer on a Format R cache, in place (signature of
-    Z/cache_hub/kivi/kivi_qk_dot_ops.py:29-67; ``kernel`` is ignored)."""
+    Z/cache_hub/kivi/kivi_qk_dot_ops.py:29-67; ``kernel`` is ignored).
+
+    ``out_width`` (an extension, default group_size): slot i's lanes
+    0 .. out_width-1 go to ``i * out_width`` of the outputs, which then need
+    nk * out_width entries; max(dense_topk, sparse_topk) <= out_width <=
+    group_size.  Only the (-1e30, 0) fillers past the kept lanes are left
+    out, so a top-k over the outputs that takes no filler is unchanged."""
     require_gpu(chunk_ids, dense_mask, packed_K, chunk_min, chunk_max, raw_q, out_scores, out_indices)
     if chunk_ids.dtype != torch.int64:
         chunk_ids = chunk_ids.to(torch.int64)
@@ -500,13 +506,17 @@ def partial_chunk_kivi_qk_dense_sparse_cuda(chunk_ids, dense_mask, packed_K, chu
     if out_scores.stride()[:2] != out_indices.stride()[:2]:
         raise RuntimeError("out_scores / out_indices must share batch / head strides")
     bs, kv, nk = chunk_ids.shape
-    if out_scores.shape[2] < nk * g or out_indices.shape[2] < nk * g:
-        raise RuntimeError(f"outputs too small: need {nk * g}")
-    check(lib().zkv_kivi_qk_dense_sparse(
-        ptr(chunk_ids), chunk_ids.stride(0), chunk_ids.stride(1),
-        ptr(dense_mask), dense_mask.stride(0), dense_mask.stride(1),
-        ptr(packed_K), packed_K.stride(0), packed_K.stride(1), packed_K.shape[2],
-        ptr(chunk_min), ptr(chunk_max), chunk_min.stride(0), chunk_min.stride(1), chunk_min.shape[2],
-        ptr(raw_q), raw_q.stride(0), raw_q.stride(1), int(dense_topk), int(sparse_topk), g,
-        ptr(out_scores), ptr(out_indices), out_scores.stride(0), out_scores.stride(1), bs, kv, nk,
-        stream_of(raw_q)))
+    w = g if out_width is None else int(out_width)
+    if out_scores.shape[2] < nk * w or out_indices.shape[2] < nk * w:
+        raise RuntimeError(f"outputs too small: need {nk * w}")
+    args = (ptr(chunk_ids), chunk_ids.stride(0), chunk_ids.stride(1),
+            ptr(dense_mask), dense_mask.stride(0), dense_mask.stride(1),
+            ptr(packed_K), packed_K.stride(0), packed_K.stride(1), packed_K.shape[2],
+            ptr(chunk_min), ptr(chunk_max), chunk_min.stride(0), chunk_min.stride(1), chunk_min.shape[2],
+            ptr(raw_q), raw_q.stride(0), raw_q.stride(1), int(dense_topk), int(sparse_topk), g)
+    tail = (ptr(out_scores), ptr(out_indices), out_scores.stride(0), out_scores.stride(1), bs, kv, nk,
+            stream_of(raw_q))
+    if w == g:
+        check(lib().zkv_kivi_qk_dense_sparse(*args, *tail))
+    else:
+        check(lib().zkv_kivi_qk_dense_sparse_compact(*args, w, *tail))
