@@ -237,15 +237,15 @@ def run_c1(args):
     kivi.kivi4_pack_status(dev)
 
     def step(i):
-        kivi.kivi4_pack(kd[:, :, :nq], vd[:, :, :nq], cache, 0)
-        cache.k_res[:, :, :res].copy_(kd[:, :, nq:])
-        cache.v_res[:, :, :res].copy_(vd[:, :, nq:])
+        # one launch packs the 124 groups and copies the 128 residual rows
+        kivi.kivi4_prefill(kd, vd, cache, res)
         kivi.kivi4_decode_attention(qd, cache, ng, res, out=out, workspace=ws)
 
     ms = timed_loop(step, args.steps, args.warmup)
-    k_ms = kernel_batch_ms(lambda i: kivi.kivi4_pack(kd[:, :, :nq], vd[:, :, :nq], cache, 0), args.steps)
+    k_ms = kernel_batch_ms(lambda i: kivi.kivi4_prefill(kd, vd, cache, res), args.steps)
     kivi.check_kivi4_pack_range(dev)
-    pack_bytes = 8 * nq * 512 + 8 * nq * 160          # bf16 K/V in, Format Q out
+    # bf16 K/V in (all 4096 tokens), Format Q records and the bf16 residual rows out
+    pack_bytes = 8 * (nq + res) * 512 + 8 * nq * 160 + 8 * res * 512
     attn_bytes = 8 * nq * 160 + 8 * res * 512 + 2 * 32 * 128 * 2
     cpu = None if args.no_cpu else c1_cpu_baseline(w)
     return {
@@ -260,7 +260,8 @@ def run_c1(args):
         "roofline": {"bound": "hbm", "achieved": pack_bytes / (k_ms * 1e-3) / 1e9, "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": pack_bytes / (k_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
                      "traffic": read_traffic("c1_kivi4_pack_traffic.json"),
-                     "kernel": "kivi4_pack_kernel", "kernel_ms": k_ms, "algorithmic_bytes": pack_bytes},
+                     "kernel": "kivi4_pack_kernel (prefill: pack + residual rows)", "kernel_ms": k_ms,
+                     "algorithmic_bytes": pack_bytes},
         "algorithmic_bytes_per_step": {"pack": pack_bytes, "attention": attn_bytes},
         "cpu_baseline": cpu,
     }

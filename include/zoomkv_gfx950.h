@@ -96,6 +96,20 @@ int zkv_kivi4_pack(const uint16_t* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
                    int bs, int kv, int n_groups, int g0, int g_cap, int32_t* groups,
                    uint32_t* range_status, zkv_stream_t stream);
 
+/* Prefill in one launch: zkv_kivi4_pack of tokens [0, 32*n_groups) of k / v
+ * into groups [g0, g0 + n_groups), and tokens [32*n_groups, 32*n_groups +
+ * res_len) copied as bf16 rows into rows [res_row0, res_row0 + res_len) of the
+ * residual windows k_res / v_res (contiguous bf16 [bs, kv, r_cap, 128], the
+ * decode attention's layout).  With res_len > 0 the k rows and the windows
+ * must be 16-byte aligned.  No separate counterpart in the reference: its
+ * prefill quantizes the full chunks and keeps the newest tokens as bf16 in
+ * two steps (S:1379-1512). */
+int zkv_kivi4_prefill(const uint16_t* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
+                      const uint16_t* v, int64_t v_sb, int64_t v_sh, int64_t v_st,
+                      int bs, int kv, int n_groups, int g0, int g_cap, int32_t* groups,
+                      uint32_t* range_status, uint16_t* k_res, uint16_t* v_res, int r_cap,
+                      int res_row0, int res_len, zkv_stream_t stream);
+
 /* ------------------------------------------------------------------------
  * Fused 4-bit decode attention over a Format Q cache plus a bf16 residual
  * window: out = softmax(q K^T * sm_scale) V, causal = False, with GQA

@@ -67,6 +67,50 @@ def test_kivi4_pack_bit_exact(rng):
     assert not from_torch(cache.k_codes)[:, :, :3].any()
 
 
+@pytest.mark.parametrize("ng,res", [(5, 0), (5, 5), (4, 32), (3, 100), (0, 128), (6, 128)])
+def test_kivi4_prefill_packs_and_copies_the_residual(rng, ng, res):
+    """One launch: the first 32 ng tokens packed as the oracle's records, the
+    last res tokens copied into the residual window; the rest of the window
+    and the other records stay untouched."""
+    zk = _zk()
+    bs, kv, r_cap = 2, 3, 128
+    n = 32 * ng + res
+    k = gaussian_bf16(rng, (bs, kv, n, 128), outlier_channels=2)
+    v = gaussian_bf16(rng, (bs, kv, n, 128))
+    cache = zk.Kivi4Cache.allocate(bs, kv, 8, r_cap)
+    cache.k_res.fill_(3.0)
+    cache.v_res.fill_(-3.0)
+    got = zk.kivi4_prefill(to_bf16(k), to_bf16(v), cache, res)
+    torch.cuda.synchronize()
+    assert got == (ng, res)
+    assert zk.kivi4_pack_status(clear=True) == 0
+    if ng:
+        ref = okivi.quantize_kivi4(k[:, :, :32 * ng], v[:, :, :32 * ng])
+        assert np.array_equal(from_torch(cache.k_codes)[:, :, :ng], ref.k_codes)
+        assert np.array_equal(from_torch(cache.k_meta)[:, :, :ng], ref.k_meta)
+        assert np.array_equal(from_torch(cache.v_codes)[:, :, :ng], ref.v_codes)
+        assert np.array_equal(from_torch(cache.v_meta)[:, :, :ng], ref.v_meta)
+    assert not from_torch(cache.groups)[:, :, ng:].any()
+    kr, vr = from_torch(cache.k_res), from_torch(cache.v_res)
+    assert np.array_equal(bf16_bits(kr[:, :, :res]), bf16_bits(k[:, :, 32 * ng:]))
+    assert np.array_equal(bf16_bits(vr[:, :, :res]), bf16_bits(v[:, :, 32 * ng:]))
+    assert np.all(kr[:, :, res:] == 3.0) and np.all(vr[:, :, res:] == -3.0)
+
+
+def test_kivi4_prefill_rejects_bad_splits(rng):
+    zk = _zk()
+    k = to_bf16(gaussian_bf16(rng, (1, 2, 70, 128)))
+    cache = zk.Kivi4Cache.allocate(1, 2, 4, 64)
+    with pytest.raises(ValueError, match="multiple of 32"):
+        zk.kivi4_prefill(k, k, cache, 5)             # 65 quantized tokens
+    k2 = to_bf16(gaussian_bf16(rng, (1, 2, 32 + 100, 128)))
+    with pytest.raises(ValueError, match="capacity"):
+        zk.kivi4_prefill(k2, k2, cache, 100)          # 100 residual rows > 64
+    k3 = to_bf16(gaussian_bf16(rng, (1, 2, 5 * 32, 128)))
+    with pytest.raises(ValueError, match="capacity"):
+        zk.kivi4_prefill(k3, k3, cache, 0)            # 5 groups > 4
+
+
 def test_kivi4_pack_strided_input(rng):
     zk = _zk()
     bs, kv, n = 2, 2, 64

@@ -30,6 +30,8 @@ SIGNATURES = {
                                P, P, P, P, P, P]),
     "zkv_kivi4_pack": (I32, [P, I64, I64, I64, P, I64, I64, I64, I32, I32, I32, I32, I32,
                              P, P, P]),
+    "zkv_kivi4_prefill": (I32, [P, I64, I64, I64, P, I64, I64, I64, I32, I32, I32, I32, I32,
+                                P, P, P, P, I32, I32, I32, P]),
     "zkv_kivi4_attention_workspace_size": (SZ, [I32, I32, I32, I32, I32, I32]),
     "zkv_kivi4_decode_attention": (I32, [P, I64, I64, P, I32, P, P, I32,
                                          I32, I32, I32, I32, I32, F32, P, I32, P, I32,

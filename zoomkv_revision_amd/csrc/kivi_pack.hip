@@ -87,14 +87,57 @@ constexpr int kRecordWords = 1280;
 __device__ __forceinline__ bool f16_nonfinite(uint16_t h) { return (h & 0x7C00u) == 0x7C00u; }
 constexpr uint16_t kF16VScaleMax = 0x6800u;  // 2048.0: the decode kernel's V-scale limit
 
+// The bf16 residual rows of a prefill (zkv_kivi4_prefill): tokens
+// [32 n_groups, 32 n_groups + res_len) of k / v go to rows [res_row0, ..) of
+// the contiguous [bs, kv, r_cap, 128] residual windows.  The pack launch runs
+// them as extra workgroups (blockIdx.x >= n_groups), 32 tokens each, so a
+// prefill is one launch.
+struct ResidualCopy {
+  uint16_t* k_res;
+  uint16_t* v_res;
+  int r_cap, res_row0, res_len, n_groups;
+};
+
+// 32 tokens x 256 bytes of K and of V: 16-byte chunks, 4 per thread per tensor.
+__device__ __forceinline__ void copy_residual_rows(const uint16_t* __restrict__ k, int64_t k_sb, int64_t k_sh,
+                                                   int64_t k_st, const uint16_t* __restrict__ v, int64_t v_sb,
+                                                   int64_t v_sh, int64_t v_st, int kv, const ResidualCopy& rc,
+                                                   int blk, int h, int b, int tid) {
+  const int t0 = 32 * blk;  // first residual token of this workgroup
+  const int64_t src_tok0 = static_cast<int64_t>(rc.n_groups) * 32 + t0;
+  const int64_t dst_row0 = (static_cast<int64_t>(b) * kv + h) * rc.r_cap + rc.res_row0 + t0;
+  u32x4_t kw[4], vw[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c = tid + 128 * i, t = c >> 4, part = c & 15;
+    const bool ok = t0 + t < rc.res_len;
+    const int64_t tok = src_tok0 + (ok ? t : 0);
+    kw[i] = *reinterpret_cast<const u32x4_t*>(k + b * k_sb + h * k_sh + tok * k_st + 8 * part);
+    vw[i] = *reinterpret_cast<const u32x4_t*>(v + b * v_sb + h * v_sh + tok * v_st + 8 * part);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c = tid + 128 * i, t = c >> 4, part = c & 15;
+    if (t0 + t < rc.res_len) {
+      const int64_t o = (dst_row0 + t) * 128 + 8 * part;
+      *reinterpret_cast<u32x4_t*>(rc.k_res + o) = kw[i];
+      *reinterpret_cast<u32x4_t*>(rc.v_res + o) = vw[i];
+    }
+  }
+}
+
 __global__ __launch_bounds__(128) void kivi4_pack_kernel(
     const uint16_t* __restrict__ k, int64_t k_sb, int64_t k_sh, int64_t k_st,
     const uint16_t* __restrict__ v, int64_t v_sb, int64_t v_sh, int64_t v_st, int kv, int g0,
-    int g_cap, int32_t* __restrict__ groups, uint32_t* __restrict__ range_status) {
+    int g_cap, int32_t* __restrict__ groups, uint32_t* __restrict__ range_status, const ResidualCopy rc) {
   __shared__ uint8_t kc[32][128];
   __shared__ uint8_t vc[32][128];
   const int g = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x;
+  if (g >= rc.n_groups) {  // (uniform) a residual-row workgroup of a prefill
+    copy_residual_rows(k, k_sb, k_sh, k_st, v, v_sb, v_sh, v_st, kv, rc, g - rc.n_groups, h, b, tid);
+    return;
+  }
   const int64_t bhg = (static_cast<int64_t>(b) * kv + h) * g_cap + g0 + g;
   int32_t* const rec = groups + bhg * kRecordWords;
   int32_t* const k_codes = rec;
@@ -256,7 +299,38 @@ extern "C" int zkv_kivi4_pack(const uint16_t* k, int64_t k_sb, int64_t k_sh, int
               "zkv_kivi4_pack: v rows must be 16-byte aligned");
   if (n_groups == 0) return ZKV_OK;
   dim3 grid(n_groups, kv, bs);
+  const ResidualCopy rc{nullptr, nullptr, 0, 0, 0, n_groups};
   kivi4_pack_kernel<<<grid, 128, 0, reinterpret_cast<hipStream_t>(stream)>>>(
-      k, k_sb, k_sh, k_st, v, v_sb, v_sh, v_st, kv, g0, g_cap, groups, range_status);
+      k, k_sb, k_sh, k_st, v, v_sb, v_sh, v_st, kv, g0, g_cap, groups, range_status, rc);
+  return check_launch("kivi4_pack_kernel");
+}
+
+extern "C" int zkv_kivi4_prefill(const uint16_t* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
+                                 const uint16_t* v, int64_t v_sb, int64_t v_sh, int64_t v_st, int bs,
+                                 int kv, int n_groups, int g0, int g_cap, int32_t* groups,
+                                 uint32_t* range_status, uint16_t* k_res, uint16_t* v_res, int r_cap,
+                                 int res_row0, int res_len, zkv_stream_t stream) {
+  ZKV_REQUIRE(k && v && groups, "zkv_kivi4_prefill: null pointer");
+  ZKV_REQUIRE(bs > 0 && kv > 0 && n_groups >= 0 && g0 >= 0 && res_len >= 0 && res_row0 >= 0,
+              "zkv_kivi4_prefill: bad sizes bs=%d kv=%d n_groups=%d g0=%d res_len=%d res_row0=%d", bs, kv,
+              n_groups, g0, res_len, res_row0);
+  ZKV_REQUIRE(g0 + n_groups <= g_cap, "zkv_kivi4_prefill: group end %d exceeds capacity %d", g0 + n_groups,
+              g_cap);
+  ZKV_REQUIRE(res_len == 0 || (k_res && v_res), "zkv_kivi4_prefill: null residual window");
+  ZKV_REQUIRE(res_row0 + res_len <= r_cap, "zkv_kivi4_prefill: residual rows end %d exceed capacity %d",
+              res_row0 + res_len, r_cap);
+  ZKV_REQUIRE((reinterpret_cast<uintptr_t>(v) & 15) == 0 && (v_st % 8) == 0 && (v_sh % 8) == 0 &&
+                  (v_sb % 8) == 0,
+              "zkv_kivi4_prefill: v rows must be 16-byte aligned");
+  ZKV_REQUIRE(res_len == 0 || ((reinterpret_cast<uintptr_t>(k) & 15) == 0 && (k_st % 8) == 0 && (k_sh % 8) == 0 &&
+                               (k_sb % 8) == 0 &&
+                               ((reinterpret_cast<uintptr_t>(k_res) | reinterpret_cast<uintptr_t>(v_res)) & 15) == 0),
+              "zkv_kivi4_prefill: k rows and the residual windows must be 16-byte aligned");
+  const int res_blocks = (res_len + 31) / 32;
+  if (n_groups + res_blocks == 0) return ZKV_OK;
+  dim3 grid(n_groups + res_blocks, kv, bs);
+  const ResidualCopy rc{k_res, v_res, r_cap, res_row0, res_len, n_groups};
+  kivi4_pack_kernel<<<grid, 128, 0, reinterpret_cast<hipStream_t>(stream)>>>(
+      k, k_sb, k_sh, k_st, v, v_sb, v_sh, v_st, kv, g0, g_cap, groups, range_status, rc);
   return check_launch("kivi4_pack_kernel");
 }

@@ -189,6 +189,41 @@ def kivi4_pack(k: torch.Tensor, v: torch.Tensor, cache: Kivi4Cache, g0: int,
     return ng
 
 
+def kivi4_prefill(k: torch.Tensor, v: torch.Tensor, cache: Kivi4Cache, res_len: int,
+                  check_range: bool = True) -> tuple[int, int]:
+    """Prefill of a Format Q cache in one launch: of the n tokens of k / v
+    [bs, kv, n, 128], the first n - res_len (a multiple of 32) are quantized
+    into groups [0, (n - res_len) / 32) as ``kivi4_pack`` does, and the last
+    ``res_len`` are copied as bf16 rows into rows [0, res_len) of the residual
+    window.  Returns (n_groups, res_len), the arguments the decode attention
+    takes.  The range check is ``kivi4_pack``'s (asynchronous)."""
+    require_gpu(k, v)
+    _check_bf16("k", k)
+    _check_bf16("v", v)
+    _check_last_contig("k", k)
+    _check_last_contig("v", v)
+    if k.shape != v.shape:
+        raise ValueError(f"k / v shape mismatch {tuple(k.shape)} vs {tuple(v.shape)}")
+    bs, kv, n, _ = k.shape
+    if (bs, kv) != tuple(cache.shape):
+        raise ValueError("cache batch / head shape mismatch")
+    res_len = int(res_len)
+    nq = n - res_len
+    if res_len < 0 or nq < 0 or nq % GROUP:
+        raise ValueError(f"n - res_len = {nq} must be a non-negative multiple of {GROUP}")
+    if res_len > cache.r_cap or nq // GROUP > cache.g_cap:
+        raise ValueError("prefill exceeds the cache capacity")
+    if not (cache.k_res.is_contiguous() and cache.v_res.is_contiguous()):
+        raise ValueError("the residual windows must be contiguous [bs, kv, r_cap, 128]")
+    status = _range_status(k.device) if check_range else None
+    check(lib().zkv_kivi4_prefill(
+        ptr(k), k.stride(0), k.stride(1), k.stride(2),
+        ptr(v), v.stride(0), v.stride(1), v.stride(2),
+        bs, kv, nq // GROUP, 0, cache.g_cap, ptr(cache.groups), ptr(status),
+        ptr(cache.k_res), ptr(cache.v_res), cache.r_cap, 0, res_len, stream_of(k)))
+    return nq // GROUP, res_len
+
+
 def kivi4_pack_status(device: torch.device | str | None = None, clear: bool = True) -> int:
     """The ZKV_RANGE_* bits that range-checked packs on ``device`` (default: the
     current device) recorded since the last clear.  Reading the word waits for
