@@ -528,7 +528,7 @@ __global__ __launch_bounds__(kNT2) void rabitq_stage2_kernel(
 //   1. prep, per (query, pool), 4 waves: encode the query (wave 0: the FWHT
 //      across lanes, the factor sums in dimension order by one lane, so the
 //      bits equal rabitq_encode_kernel's), estimate a strided sample of
-//      s = min(n, 4096) keys and take tau = the m-th largest sample key,
+//      s = min(n, 2048) keys and take tau = the m-th largest sample key,
 //      m = ceil(4 k s / n) (at least 8): about 4k keys of the pool are
 //      expected at or above tau;
 //   2. filter, one wave per 64 keys: each lane estimates its key against
@@ -546,7 +546,7 @@ constexpr int kFiltWave = 64;         // keys per filter wave
 constexpr int kFiltList = 256;        // keys per filter list (a 4-wave block)
 constexpr int kBucketWords = 32;      // a list: 128 bytes = count, pad, 15 (key, index) pairs
 constexpr int kFiltCap = 15;          // entries a list holds
-constexpr int kSampleMax = 4096;      // prep: sample keys per query
+constexpr int kSampleMax = 2048;      // prep: sample keys per query (64 runs of kSampleMax / 64)
 constexpr int kBigNT = 1024;          // prep / select blocks
 constexpr int kSelMaxPasses = 16;     // select: bucket chunks per thread (n <= 2048 lists of 256)
 
@@ -669,8 +669,8 @@ __device__ void block_radix_select12(const uint32_t (&key)[NI], uint32_t valid, 
 
 // ----------------------------------------------------------------------------
 // 1. prep, per (query, pool), 1024 threads: every thread requests its sample
-//    keys first -- s = min(n, 4096) keys in 64 blocks of 64 consecutive keys
-//    spread over the pool (or every key when n < 4096) -- while wave 0
+//    keys first -- s = min(n, 2048) keys in 64 runs of 32 consecutive keys
+//    spread over the pool (or every key when n < 2048) -- while wave 0
 //    encodes the query (the FWHT across lanes, the factor sums in dimension
 //    order by one lane: the bits of rabitq_encode_kernel); then tau = the
 //    lower edge of the 4096-bin histogram bin (over the samples' range) that
@@ -693,14 +693,15 @@ __global__ __launch_bounds__(kBigNT) void rabitq_prep_kernel(
   // ---- sample rows first: item i of thread t is sample s = i * NT + t ----
   const u32x4_t* kc = reinterpret_cast<const u32x4_t*>(codes_k) + pool * n;
   const uint32_t* kf = reinterpret_cast<const uint32_t*>(fac_k) + pool * n;
-  const int64_t blk = n / 64;  // sample block j starts at key j * blk (n >= 4096)
+  const int64_t blk = n / 64;  // sample run j starts at key j * blk (n >= kSampleMax)
+  constexpr int kRun = kSampleMax / 64;
   u32x4_t sc[NI];
   uint32_t sf[NI];
   int valid_n = 0;
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
     const int s = i * kBigNT + tid;
-    const int64_t p = s_count == kSampleMax ? (s >> 6) * blk + (s & 63) : s;
+    const int64_t p = s_count == kSampleMax ? (s / kRun) * blk + (s % kRun) : s;
     const bool ok = s < s_count;
     const int64_t pp = ok ? p : 0;
     sc[i] = kc[pp];
