@@ -304,3 +304,33 @@ def test_search_filter_path_ties(rng):
     _check_planted(rng, 131072, 256, np.arange(0), dup=40,
                    premise=lambda hits, full: 256 <= hits <= 4096 and full <= 15)
     _check_planted(rng, 40000, 100, np.arange(0), dup=2, premise=lambda hits, full: full > 15)
+
+
+def test_search_plan_reads_current_contents(rng):
+    """A SearchPlan checks its buffers once; each run searches what they hold
+    then (queries rewritten in place between runs) with rabitq_search's bits."""
+    from zoomkv_revision_amd.rabitq import SearchPlan, rabitq_encode, rabitq_search
+    _, s_t = _signs()
+    n, nq, topk = 40000, 4, 64
+    kt = _f16(orq.clustered_unit_keys(rng, n, 16))
+    codes, fac = rabitq_encode(kt, s_t)
+    q_buf = torch.empty(nq, 128, dtype=torch.float16, device=kt.device)
+    plan = SearchPlan(q_buf, kt, codes, fac, s_t, topk)
+    for _ in range(2):
+        qt = _f16(orq.clustered_unit_keys(rng, nq, 16))
+        q_buf.copy_(qt)
+        got = plan.run()
+        ref = rabitq_search(qt, kt, codes, fac, s_t, topk)
+        for a, b in zip(got, ref):
+            assert torch.equal(a.view(torch.int32) if a.dtype == torch.float32 else a,
+                               b.view(torch.int32) if b.dtype == torch.float32 else b)
+
+
+def test_search_plan_rejects_operands_it_would_copy(rng):
+    from zoomkv_revision_amd.rabitq import SearchPlan, rabitq_encode
+    _, s_t = _signs()
+    kt = _f16(orq.clustered_unit_keys(rng, 4096, 8))
+    codes, fac = rabitq_encode(kt, s_t)
+    q = torch.zeros(128, 6, dtype=torch.float16, device=kt.device).t()   # non-contiguous [6, 128]
+    with pytest.raises(AssertionError, match="in place"):
+        SearchPlan(q, kt, codes, fac, s_t, 16)

@@ -116,16 +116,51 @@ def rabitq_search(q: torch.Tensor, keys: torch.Tensor, codes: torch.Tensor, fact
     ``out``: the three output tensors, preallocated with those shapes and
     dtypes (contiguous), written in place and returned.
     """
+    args, outs, _ = _search_args(q, keys, codes, factors, signs, topk, workspace, out, copies=True)
+    check(lib().zkv_rabitq_search(*args, stream_of(q)))
+    return outs
+
+
+class SearchPlan:
+    """``rabitq_search`` with its argument checks done once, for searches
+    repeated over the same buffers (a serving loop: new query and key
+    contents, the same tensors).  ``run()`` searches the buffers' current
+    contents with one C-ABI call on the current stream, allocates nothing and
+    returns the output tensors.  q, codes and factors must be contiguous and
+    the key rows 16-byte aligned (the plan reads them in place, never a
+    copy); the tensors and the workspace must stay alive and keep their
+    shapes and strides while the plan is used.  Without a ``workspace`` the
+    plan takes the one cached for the stream current at its creation: run it
+    on that stream (overlapping searches on one workspace race)."""
+
+    def __init__(self, q, keys, codes, factors, signs, topk, workspace=None, out=None):
+        self._q = q
+        self._args, self.out, self._keep = _search_args(q, keys, codes, factors, signs, topk, workspace, out,
+                                                        copies=False)
+        self._fn = lib().zkv_rabitq_search
+
+    def run(self):
+        check(self._fn(*self._args, stream_of(self._q)))
+        return self.out
+
+
+def _search_args(q, keys, codes, factors, signs, topk, workspace, out, copies: bool):
+    """The checked arguments of zkv_rabitq_search (all but the stream), the
+    outputs to return, and the tensors the pointers belong to.  With
+    ``copies`` False an operand that would need a contiguous copy is an
+    error."""
     # (the checks are ordered so that the common call -- 3-D pools,
     # contiguous operands, preallocated outputs -- costs a few microseconds
     # of host time: the search itself takes ~30 us of device time)
     require_gpu(q, keys, codes, factors, signs)
     _check_signs(signs)
     squeeze = q.dim() == 2
-    qq = _pools(q, HEAD_DIM).contiguous()
-    kk = _pools(keys, HEAD_DIM)
-    cc = _pools(codes, CODE_BYTES).contiguous()
-    ff = _pools(factors, 2).contiguous()
+    qq, kk = _pools(q, HEAD_DIM), _pools(keys, HEAD_DIM)
+    cc, ff = _pools(codes, CODE_BYTES), _pools(factors, 2)
+    if not copies:
+        assert qq.is_contiguous() and cc.is_contiguous() and ff.is_contiguous(), \
+            "a search plan reads q, codes and factors in place: they must be contiguous"
+    qq, cc, ff = qq.contiguous(), cc.contiguous(), ff.contiguous()
     assert qq.dtype == _F16 and kk.dtype == _F16, "q and keys must be fp16"
     assert cc.dtype == _U8 and ff.dtype == _F16
     P, Q, _ = qq.shape
@@ -134,6 +169,7 @@ def rabitq_search(q: torch.Tensor, keys: torch.Tensor, codes: torch.Tensor, fact
         ff.shape[1] == N, "pool/key shape mismatch"
     ks0, ks1 = kk.stride(0), kk.stride(1)
     if kk.stride(2) != 1 or ks1 % 8 or ks0 % 8 or kk.data_ptr() % 16:
+        assert copies, "a search plan reads the keys in place: their rows must be 16-byte aligned"
         kk = kk.contiguous()
         ks0, ks1 = kk.stride(0), kk.stride(1)
     assert 0 < topk <= N, f"topk={topk} must be in [1, {N}]"
@@ -155,9 +191,8 @@ def rabitq_search(q: torch.Tensor, keys: torch.Tensor, codes: torch.Tensor, fact
             fidx = fidx.view(shape)
         if fsc.shape != shape:
             fsc = fsc.view(shape)
-    check(lib().zkv_rabitq_search(qq.data_ptr(), kk.data_ptr(), ks0, ks1, cc.data_ptr(), ff.data_ptr(),
-                                  signs.data_ptr(), P, Q, N, topk, cand.data_ptr(), fidx.data_ptr(),
-                                  fsc.data_ptr(), ws.data_ptr(), ws.numel(), stream_of(q)))
-    if squeeze:
-        return cand[0], fidx[0], fsc[0]
-    return cand, fidx, fsc
+    args = (qq.data_ptr(), kk.data_ptr(), ks0, ks1, cc.data_ptr(), ff.data_ptr(), signs.data_ptr(), P, Q, N,
+            topk, cand.data_ptr(), fidx.data_ptr(), fsc.data_ptr(), ws.data_ptr(), ws.numel())
+    outs = (cand[0], fidx[0], fsc[0]) if squeeze else (cand, fidx, fsc)
+    # the tensors whose pointers the arguments hold (contiguous copies included)
+    return args, outs, (qq, kk, cc, ff, signs, ws, cand, fidx, fsc)
