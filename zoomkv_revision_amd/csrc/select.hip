@@ -984,7 +984,9 @@ __device__ __forceinline__ void load8_bf16(const uint16_t* p, float (&out)[8]) {
 // Chunks of 16 tokens: one row of 16 lanes per chunk, no LDS.  Lane l of a
 // row scores token l of the chunk and also loads channels 8l..8l+7 of the
 // chunk's min / max and of the query, which the row shares through DPP.  Same
-// arithmetic, in the same order, as kivi_qk_kernel.
+// arithmetic, in the same order, as kivi_qk_kernel.  Both kernels write
+// lanes 0 .. out_w-1 of slot i at i * out_w (out_w = G: the reference's
+// layout; less: only the kept lanes, the compact output).
 template <int T, bool kVec>
 __global__ __launch_bounds__(T) void kivi_qk_row_kernel(
     const int64_t* __restrict__ ids, int64_t id_sb, int64_t id_sh, const uint8_t* __restrict__ dmask,
