@@ -497,7 +497,7 @@ def run_c3(args):
     import numpy as np
     import torch
     from zoomkv_revision_amd import kivi, synthetic
-    from zoomkv_revision_amd.quest import quest_chunk_topk_gqa
+    from zoomkv_revision_amd.quest import QuestTopkPlan, quest_chunk_topk_gqa
     bs, hq, kv, n_tok, n_sel = 8, 32, 8, 32768, 128
     dev = torch.device("cuda:0")
     ws = [synthetic.c3_workload(100 + i, bs, hq, kv, n_tok, n_sel, dev) for i in range(8)]
@@ -514,15 +514,22 @@ def run_c3(args):
         return quest_chunk_topk_gqa(w["q"], kv, w["page_min"], w["page_max"], scores, n_pages, None, raw_q, n_sel,
                                     sels[i % 2])
 
-    def step(i):
-        w = ws[i % len(ws)]
-        sel = select(i)
-        kivi.kivi4_sparse_attention(w["q"], w["cache"], sel, out=out)
+    # a decode loop runs the same buffers every step: the argument checks run
+    # once per workload (QuestTopkPlan, SparseAttentionPlan), a step is two
+    # C-ABI calls
+    qplans = [QuestTopkPlan(w["q"], kv, w["page_min"], w["page_max"], scores, n_pages, None, raw_q, n_sel,
+                            sels[j % 2]) for j, w in enumerate(ws)]
+    splans = [kivi.SparseAttentionPlan(w["q"], w["cache"], sels[j % 2], out=out) for j, w in enumerate(ws)]
 
-    # the selection of every workload, checked against its planted pages
-    # (outside the timed steps)
+    def step(i):
+        j = i % len(ws)
+        qplans[j].run()
+        splans[j].run()
+
+    # the selection of every workload through the timed path's plans, checked
+    # against its planted pages (outside the timed steps)
     for j in range(len(ws)):
-        sel_ok.append(select(j).clone())
+        sel_ok.append(qplans[j].run().clone())
     ms = timed_loop(step, args.steps, args.warmup)
     step_ms = kernel_batch_ms(step, args.steps, host_us=60)
     k_ms = kernel_batch_ms(select, args.steps)

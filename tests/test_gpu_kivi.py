@@ -97,6 +97,25 @@ def test_kivi4_prefill_packs_and_copies_the_residual(rng, ng, res):
     assert np.all(kr[:, :, res:] == 3.0) and np.all(vr[:, :, res:] == -3.0)
 
 
+def test_kivi4_prefill_strided_input(rng):
+    """k / v handed over as [bs, n, kv, 128] views (the model's layout): the
+    packed records and the residual rows are the contiguous input's."""
+    zk = _zk()
+    bs, kv, ng, res = 2, 2, 3, 40
+    n = 32 * ng + res
+    k = gaussian_bf16(rng, (bs, n, kv, 128))
+    v = gaussian_bf16(rng, (bs, n, kv, 128))
+    cache = zk.Kivi4Cache.allocate(bs, kv, ng, 64)
+    zk.kivi4_prefill(to_bf16(k).transpose(1, 2), to_bf16(v).transpose(1, 2), cache, res)
+    torch.cuda.synchronize()
+    kc, vc = np.swapaxes(k, 1, 2), np.swapaxes(v, 1, 2)
+    ref = okivi.quantize_kivi4(kc[:, :, :32 * ng], vc[:, :, :32 * ng])
+    assert np.array_equal(from_torch(cache.k_codes), ref.k_codes)
+    assert np.array_equal(from_torch(cache.v_meta), ref.v_meta)
+    assert np.array_equal(bf16_bits(from_torch(cache.k_res)[:, :, :res]), bf16_bits(kc[:, :, 32 * ng:]))
+    assert np.array_equal(bf16_bits(from_torch(cache.v_res)[:, :, :res]), bf16_bits(vc[:, :, 32 * ng:]))
+
+
 def test_kivi4_prefill_rejects_bad_splits(rng):
     zk = _zk()
     k = to_bf16(gaussian_bf16(rng, (1, 2, 70, 128)))

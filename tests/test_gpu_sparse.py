@@ -236,3 +236,43 @@ def test_c3_full_shape_sparse_attention_matches_oracle():
         print(f"[c3 full] sequence {b}: max abs err {err:.3e}, LSE rel err {lerr:.3e}", flush=True)
         assert err <= ATOL, f"sequence {b}: max abs err {err}"
         assert lerr <= 1e-5, f"sequence {b}: LSE rel err {lerr}"
+
+
+def test_c3_plans_match_the_calls():
+    """QuestTopkPlan and SparseAttentionPlan (checks once, one C-ABI call per
+    run) give the calls' bits on the buffers' current contents: the query is
+    rewritten in place between runs."""
+    from zoomkv_revision_amd import kivi, synthetic
+    from zoomkv_revision_amd.quest import QuestTopkPlan, quest_chunk_topk_gqa
+    bs, hq, kv, n_tok, n_sel = 2, 16, 4, 4096, 24
+    ws = [synthetic.c3_workload(300 + i, bs, hq, kv, n_tok, n_sel, torch.device("cuda")) for i in range(2)]
+    n_pages = ws[0]["n_pages"]
+    scores = torch.empty(bs, kv, n_pages, device="cuda")
+    raw_q = torch.empty(bs, kv, 128, dtype=torch.bfloat16, device="cuda")
+    sel = torch.empty(bs, kv, n_sel, dtype=torch.int64, device="cuda")
+    out = torch.empty(bs, hq, 128, dtype=torch.float32, device="cuda")
+    q_buf = ws[0]["q"].clone()
+    w = ws[0]
+    qplan = QuestTopkPlan(q_buf, kv, w["page_min"], w["page_max"], scores, n_pages, None, raw_q, n_sel, sel)
+    splan = kivi.SparseAttentionPlan(q_buf, w["cache"], sel, out=out, out_dtype=torch.float32, return_lse=True)
+    for src in (ws[0]["q"], ws[1]["q"]):
+        q_buf.copy_(src)
+        got_sel = qplan.run().clone()
+        got_out, got_lse = splan.run()
+        want_sel = quest_chunk_topk_gqa(src, kv, w["page_min"], w["page_max"], torch.empty_like(scores), n_pages,
+                                        None, torch.empty_like(raw_q), n_sel)
+        want_out, want_lse = kivi.kivi4_sparse_attention(src, w["cache"], want_sel, out_dtype=torch.float32,
+                                                         return_lse=True)
+        assert torch.equal(got_sel, want_sel)
+        assert torch.equal(got_out.view(torch.int32), want_out.view(torch.int32))
+        assert torch.equal(got_lse.view(torch.int32), want_lse.view(torch.int32))
+
+
+def test_sparse_plan_rejects_a_strided_page_list(rng):
+    from zoomkv_revision_amd import kivi
+    bs, hq, kv = 1, 8, 2
+    cache = kivi.Kivi4Cache.allocate(bs, kv, 4, 32)
+    q = to_bf16(gaussian_bf16(rng, (bs, hq, 128)))
+    pages = torch.zeros(bs, kv, 8, 2, dtype=torch.int64, device="cuda")[..., 0]   # last-dim stride 2
+    with pytest.raises(ValueError, match="in place"):
+        kivi.SparseAttentionPlan(q, cache, pages, 4, 0)

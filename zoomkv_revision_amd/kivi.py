@@ -347,6 +347,39 @@ def kivi4_sparse_attention(q: torch.Tensor, cache: Kivi4Cache, pages: torch.Tens
     (S:1723-1772 after the Quest pick of S:2195-2240).  Sorted page lists let
     both halves of a 32-token group share one tile.  With ``return_lse`` also
     the fp32 natural-log LSE [bs, hq]."""
+    args, ret, _ = _sparse_args(q, cache, pages, n_groups, res_len, sm_scale, out, out_dtype, n_splits,
+                                workspace, return_lse, copies=True)
+    check(lib().zkv_kivi4_sparse_attention(*args, stream_of(q)))
+    return ret
+
+
+class SparseAttentionPlan:
+    """``kivi4_sparse_attention`` with its checks done once for fixed buffers
+    (a decode loop: new query, page-list and cache contents, the same
+    tensors): ``run()`` is one C-ABI call on the current stream and returns
+    the output (and LSE).  The page list must have a contiguous last dim (the
+    plan reads it in place); the tensors must stay alive and keep their
+    shapes and strides; without a ``workspace`` the plan takes the one cached
+    for the stream current at creation, so run it on that stream."""
+
+    def __init__(self, q, cache, pages, n_groups=None, res_len=None, sm_scale=None, out=None, out_dtype=None,
+                 n_splits=0, workspace=None, return_lse=False):
+        self._q = q
+        self._args, self.out, self._keep = _sparse_args(q, cache, pages, n_groups, res_len, sm_scale, out,
+                                                        out_dtype, n_splits, workspace, return_lse, copies=False)
+        self._fn = lib().zkv_kivi4_sparse_attention
+
+    def run(self):
+        check(self._fn(*self._args, stream_of(self._q)))
+        return self.out
+
+
+def _sparse_args(q, cache, pages, n_groups, res_len, sm_scale, out, out_dtype, n_splits, workspace, return_lse,
+                 copies: bool):
+    """Checked arguments of zkv_kivi4_sparse_attention (all but the stream),
+    the result to return and the tensors the pointers belong to; with
+    ``copies`` False a page list that would need a contiguous copy is an
+    error."""
     require_gpu(q, pages)
     _check_bf16("q", q)
     squeeze = q.dim() == 4
@@ -361,6 +394,8 @@ def kivi4_sparse_attention(q: torch.Tensor, cache: Kivi4Cache, pages: torch.Tens
     if pages.dtype != torch.int64 or pages.dim() != 3 or pages.shape[0] != bs or pages.shape[1] != kv:
         raise ValueError("pages must be int64 [bs, kv, n_sel]")
     if pages.shape[2] > 1 and pages.stride(2) != 1:
+        if not copies:
+            raise ValueError("a sparse-attention plan reads the page list in place: its last dim must be contiguous")
         pages = pages.contiguous()
     n_sel = pages.shape[2]
     n_groups = cache.n_groups if n_groups is None else int(n_groups)
@@ -374,21 +409,22 @@ def kivi4_sparse_attention(q: torch.Tensor, cache: Kivi4Cache, pages: torch.Tens
     elif out.dtype != out_dtype or not out.is_contiguous() or out.numel() != bs * hq * HEAD_DIM:
         raise ValueError("out must be a contiguous [bs, hq, 128] tensor of out_dtype")
     lse = torch.empty(bs, hq, dtype=torch.float32, device=q.device) if return_lse else None
-    L = lib()
     ws = workspace
     if ws is None:
         ws = _workspace(q.device, _sparse_ws_bytes(bs, hq, kv, n_sel, res_len, n_splits))
-    check(L.zkv_kivi4_sparse_attention(
-        ptr(q3), q3.stride(0), q3.stride(1),
-        ptr(cache.groups), cache.g_cap,
-        ptr(cache.k_res), ptr(cache.v_res), cache.r_cap,
-        bs, hq, kv, n_groups, res_len, ptr(pages), pages.stride(0), pages.stride(1), n_sel, sm_scale,
-        ptr(out), int(out_dtype == torch.float32), ptr(lse), n_splits,
-        ptr(ws), ws.numel() * ws.element_size(), stream_of(q)))
+    args = (ptr(q3), q3.stride(0), q3.stride(1),
+            ptr(cache.groups), cache.g_cap,
+            ptr(cache.k_res), ptr(cache.v_res), cache.r_cap,
+            bs, hq, kv, n_groups, res_len, ptr(pages), pages.stride(0), pages.stride(1), n_sel, sm_scale,
+            ptr(out), int(out_dtype == torch.float32), ptr(lse), n_splits,
+            ptr(ws), ws.numel() * ws.element_size())
+    owners = (q3, cache.groups, cache.k_res, cache.v_res, pages, out, lse, ws)
     if out.dim() != 3 or out.shape[1] != hq:
         out = out.view(bs, hq, HEAD_DIM)
     out = out.unsqueeze(1) if squeeze else out
-    return (out, lse) if return_lse else out
+    return args, ((out, lse) if return_lse else out), owners
+
+
 
 
 MAX_LIST_TOKENS = 1024   # token-list entries per (b, kv) of kivi4_token_attention

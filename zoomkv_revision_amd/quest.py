@@ -144,6 +144,33 @@ def quest_chunk_topk_gqa(queries: torch.Tensor, kv_heads: int, chunk_min: torch.
     k > n_chunks).  Rows of up to 4096 chunks.  ``out`` (optional, int64
     [bs, kv, >= k] with a contiguous last dim) receives the indices; returns
     them."""
+    args, q, ret, _ = _quest_topk_args(queries, kv_heads, chunk_min, chunk_max, scores, n_chunks, valid, raw_q,
+                                       k, out)
+    check(lib().zkv_quest_chunk_topk_gqa(*args, stream_of(q)))
+    return ret
+
+
+class QuestTopkPlan:
+    """``quest_chunk_topk_gqa`` with its checks done once for fixed buffers (a
+    decode loop: new query and metadata contents, the same tensors): ``run()``
+    is one C-ABI call on the current stream and returns the indices.  The
+    tensors must stay alive and keep their shapes and strides; the arrival
+    counters are the ones cached for the stream current at creation, so run
+    the plan on that stream."""
+
+    def __init__(self, queries, kv_heads, chunk_min, chunk_max, scores, n_chunks, valid, raw_q, k, out=None):
+        self._args, self._q, self.out, self._keep = _quest_topk_args(queries, kv_heads, chunk_min, chunk_max,
+                                                                     scores, n_chunks, valid, raw_q, k, out)
+        self._fn = lib().zkv_quest_chunk_topk_gqa
+
+    def run(self) -> torch.Tensor:
+        check(self._fn(*self._args, stream_of(self._q)))
+        return self.out
+
+
+def _quest_topk_args(queries, kv_heads, chunk_min, chunk_max, scores, n_chunks, valid, raw_q, k, out):
+    """Checked arguments of zkv_quest_chunk_topk_gqa (all but the stream), the
+    query view, the indices to return and the tensors the pointers belong to."""
     q = queries.reshape(queries.shape[0], -1, queries.shape[-1]) if queries.dim() == 4 else queries
     require_gpu(q, chunk_min, chunk_max, scores, raw_q)
     bs, hq, _ = q.shape
@@ -175,11 +202,11 @@ def quest_chunk_topk_gqa(queries: torch.Tensor, kv_heads: int, chunk_min: torch.
             or out.stride(0) != kv * out.stride(1):
         raise RuntimeError("out must be int64 [bs, kv, >= k] with rows at one stride")
     sl = _slots(q.device, bs * kv)
-    check(lib().zkv_quest_chunk_topk_gqa(
-        ptr(q), q.stride(0), q.stride(1), hq, ptr(raw_q), ptr(chunk_min), ptr(chunk_max),
-        int(chunk_min.dtype == torch.float16), ptr(scores), bs, kv, n_chunks, n_max, ptr(valid), k,
-        ptr(out), out.stride(1), ptr(sl), sl.numel() * 4, stream_of(q)))
-    return out if out.shape[2] == k else out[:, :, :k]
+    args = (ptr(q), q.stride(0), q.stride(1), hq, ptr(raw_q), ptr(chunk_min), ptr(chunk_max),
+            int(chunk_min.dtype == torch.float16), ptr(scores), bs, kv, n_chunks, n_max, ptr(valid), k,
+            ptr(out), out.stride(1), ptr(sl), sl.numel() * 4)
+    owners = (q, chunk_min, chunk_max, scores, valid, raw_q, out, sl)
+    return args, q, (out if out.shape[2] == k else out[:, :, :k]), owners
 
 
 class QuestKernel:
