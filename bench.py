@@ -236,10 +236,15 @@ def run_c1(args):
     # it is read once, after the timed steps
     kivi.kivi4_pack_status(dev)
 
+    # the same buffers every call: the argument checks run once (PrefillPlan,
+    # DecodeAttentionPlan), a step is two C-ABI calls
+    prefill = kivi.PrefillPlan(kd, vd, cache, res)
+    attend = kivi.DecodeAttentionPlan(qd, cache, ng, res, out=out, workspace=ws)
+
     def step(i):
         # one launch packs the 124 groups and copies the 128 residual rows
-        kivi.kivi4_prefill(kd, vd, cache, res)
-        kivi.kivi4_decode_attention(qd, cache, ng, res, out=out, workspace=ws)
+        prefill.run()
+        attend.run()
 
     ms = timed_loop(step, args.steps, args.warmup)
     k_ms = kernel_batch_ms(lambda i: kivi.kivi4_prefill(kd, vd, cache, res), args.steps)

@@ -364,3 +364,31 @@ def test_decode_attention_large_v_group(rng, dominant):
     assert np.abs(out[:, :4] - ref[:, :4]).max() <= ATOL
     if dominant:
         assert np.abs(ref[0, 4:8, 32:64]).max() > 1000.0      # the planted token does dominate
+
+
+def test_prefill_and_decode_plans_match_the_calls(rng):
+    """PrefillPlan and DecodeAttentionPlan (checks once, one C-ABI call per
+    run) give the calls' bits on the buffers' current contents."""
+    zk = _zk()
+    bs, hq, kv, ng, res = 2, 16, 4, 3, 40
+    n = 32 * ng + res
+    k_buf = to_bf16(gaussian_bf16(rng, (bs, kv, n, 128)))
+    v_buf = to_bf16(gaussian_bf16(rng, (bs, kv, n, 128)))
+    q_buf = to_bf16(gaussian_bf16(rng, (bs, hq, 128)))
+    cache = zk.Kivi4Cache.allocate(bs, kv, ng, 64)
+    ref_cache = zk.Kivi4Cache.allocate(bs, kv, ng, 64)
+    out = torch.empty(bs, hq, 128, dtype=torch.float32, device="cuda")
+    prefill = zk.PrefillPlan(k_buf, v_buf, cache, res)
+    attend = zk.DecodeAttentionPlan(q_buf, cache, ng, res, out=out, out_dtype=torch.float32, return_lse=True)
+    for _ in range(2):
+        k_buf.copy_(to_bf16(gaussian_bf16(rng, (bs, kv, n, 128))))
+        v_buf.copy_(to_bf16(gaussian_bf16(rng, (bs, kv, n, 128))))
+        q_buf.copy_(to_bf16(gaussian_bf16(rng, (bs, hq, 128))))
+        assert prefill.run() == (ng, res)
+        got, got_lse = attend.run()
+        zk.kivi4_prefill(k_buf, v_buf, ref_cache, res)
+        want, want_lse = zk.kivi4_decode_attention(q_buf, ref_cache, ng, res, out_dtype=torch.float32,
+                                                   return_lse=True)
+        assert torch.equal(cache.groups, ref_cache.groups) and torch.equal(cache.k_res, ref_cache.k_res)
+        assert torch.equal(got.view(torch.int32), want.view(torch.int32))
+        assert torch.equal(got_lse.view(torch.int32), want_lse.view(torch.int32))

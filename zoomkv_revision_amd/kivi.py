@@ -197,6 +197,30 @@ def kivi4_prefill(k: torch.Tensor, v: torch.Tensor, cache: Kivi4Cache, res_len: 
     ``res_len`` are copied as bf16 rows into rows [0, res_len) of the residual
     window.  Returns (n_groups, res_len), the arguments the decode attention
     takes.  The range check is ``kivi4_pack``'s (asynchronous)."""
+    args, ret, _ = _prefill_args(k, v, cache, res_len, check_range)
+    check(lib().zkv_kivi4_prefill(*args, stream_of(k)))
+    return ret
+
+
+class PrefillPlan:
+    """``kivi4_prefill`` with its checks done once for fixed buffers: ``run()``
+    is one C-ABI call on the current stream over the buffers' current
+    contents and returns (n_groups, res_len).  The tensors must stay alive
+    and keep their shapes and strides."""
+
+    def __init__(self, k, v, cache, res_len, check_range=True):
+        self._k = k
+        self._args, self.result, self._keep = _prefill_args(k, v, cache, res_len, check_range)
+        self._fn = lib().zkv_kivi4_prefill
+
+    def run(self) -> tuple[int, int]:
+        check(self._fn(*self._args, stream_of(self._k)))
+        return self.result
+
+
+def _prefill_args(k, v, cache, res_len, check_range):
+    """Checked arguments of zkv_kivi4_prefill (all but the stream), the
+    result to return and the tensors the pointers belong to."""
     require_gpu(k, v)
     _check_bf16("k", k)
     _check_bf16("v", v)
@@ -216,12 +240,11 @@ def kivi4_prefill(k: torch.Tensor, v: torch.Tensor, cache: Kivi4Cache, res_len: 
     if not (cache.k_res.is_contiguous() and cache.v_res.is_contiguous()):
         raise ValueError("the residual windows must be contiguous [bs, kv, r_cap, 128]")
     status = _range_status(k.device) if check_range else None
-    check(lib().zkv_kivi4_prefill(
-        ptr(k), k.stride(0), k.stride(1), k.stride(2),
-        ptr(v), v.stride(0), v.stride(1), v.stride(2),
-        bs, kv, nq // GROUP, 0, cache.g_cap, ptr(cache.groups), ptr(status),
-        ptr(cache.k_res), ptr(cache.v_res), cache.r_cap, 0, res_len, stream_of(k)))
-    return nq // GROUP, res_len
+    args = (ptr(k), k.stride(0), k.stride(1), k.stride(2),
+            ptr(v), v.stride(0), v.stride(1), v.stride(2),
+            bs, kv, nq // GROUP, 0, cache.g_cap, ptr(cache.groups), ptr(status),
+            ptr(cache.k_res), ptr(cache.v_res), cache.r_cap, 0, res_len)
+    return args, (nq // GROUP, res_len), (k, v, cache.groups, cache.k_res, cache.v_res, status)
 
 
 def kivi4_pack_status(device: torch.device | str | None = None, clear: bool = True) -> int:
@@ -248,6 +271,11 @@ def check_kivi4_pack_range(device: torch.device | str | None = None) -> None:
 
 
 _WORKSPACE: dict = {}
+
+
+@functools.lru_cache(maxsize=256)
+def _decode_ws_bytes(bs: int, hq: int, kv: int, n_groups: int, res_len: int, n_splits: int) -> int:
+    return lib().zkv_kivi4_attention_workspace_size(bs, hq, kv, n_groups, res_len, n_splits)
 
 
 @functools.lru_cache(maxsize=256)
@@ -286,6 +314,35 @@ def kivi4_decode_attention(q: torch.Tensor, cache: Kivi4Cache, n_groups: int | N
     With ``return_lse`` also the fp32 natural-log LSE [bs, hq] of the scaled
     scores (flash-attn's softmax_lse).
     """
+    args, ret, _ = _decode_args(q, cache, n_groups, res_len, sm_scale, out, out_dtype, n_splits, workspace,
+                                return_lse)
+    check(lib().zkv_kivi4_decode_attention(*args, stream_of(q)))
+    return ret
+
+
+class DecodeAttentionPlan:
+    """``kivi4_decode_attention`` with its checks done once for fixed buffers
+    (a decode loop: new query and cache contents, the same tensors and
+    lengths): ``run()`` is one C-ABI call on the current stream and returns
+    the output (and LSE).  The tensors must stay alive and keep their shapes
+    and strides; without a ``workspace`` the plan takes the one cached for the
+    stream current at creation, so run it on that stream."""
+
+    def __init__(self, q, cache, n_groups=None, res_len=None, sm_scale=None, out=None, out_dtype=None, n_splits=0,
+                 workspace=None, return_lse=False):
+        self._q = q
+        self._args, self.out, self._keep = _decode_args(q, cache, n_groups, res_len, sm_scale, out, out_dtype,
+                                                        n_splits, workspace, return_lse)
+        self._fn = lib().zkv_kivi4_decode_attention
+
+    def run(self):
+        check(self._fn(*self._args, stream_of(self._q)))
+        return self.out
+
+
+def _decode_args(q, cache, n_groups, res_len, sm_scale, out, out_dtype, n_splits, workspace, return_lse):
+    """Checked arguments of zkv_kivi4_decode_attention (all but the stream),
+    the result to return and the tensors the pointers belong to."""
     require_gpu(q)
     _check_bf16("q", q)
     squeeze = False
@@ -320,19 +377,20 @@ def kivi4_decode_attention(q: torch.Tensor, cache: Kivi4Cache, n_groups: int | N
                 t.stride(0) != kv * r_cap * HEAD_DIM or t.shape[2] < res_len:
             raise ValueError(f"{name} must be a token window of a contiguous [bs, kv, R_cap, 128] buffer holding "
                              f"res_len={res_len} rows")
-    L = lib()
-    need = L.zkv_kivi4_attention_workspace_size(bs, hq, kv, n_groups, res_len, n_splits)
-    ws = _workspace(q.device, need) if workspace is None else workspace
-    check(L.zkv_kivi4_decode_attention(
-        ptr(q3), q3.stride(0), q3.stride(1),
-        ptr(cache.groups), cache.g_cap,
-        ptr(cache.k_res), ptr(cache.v_res), r_cap,
-        bs, hq, kv, n_groups, res_len, sm_scale,
-        ptr(out), int(out_dtype == torch.float32), ptr(lse), n_splits,
-        ptr(ws), ws.numel() * ws.element_size(), stream_of(q)))
-    out = out.view(bs, hq, HEAD_DIM)
+    ws = workspace
+    if ws is None:
+        ws = _workspace(q.device, _decode_ws_bytes(bs, hq, kv, n_groups, res_len, n_splits))
+    args = (ptr(q3), q3.stride(0), q3.stride(1),
+            ptr(cache.groups), cache.g_cap,
+            ptr(cache.k_res), ptr(cache.v_res), r_cap,
+            bs, hq, kv, n_groups, res_len, sm_scale,
+            ptr(out), int(out_dtype == torch.float32), ptr(lse), n_splits,
+            ptr(ws), ws.numel() * ws.element_size())
+    owners = (q3, cache.groups, cache.k_res, cache.v_res, out, lse, ws)
+    if out.dim() != 3 or out.shape[1] != hq:
+        out = out.view(bs, hq, HEAD_DIM)
     out = out.unsqueeze(1) if squeeze else out
-    return (out, lse) if return_lse else out
+    return args, ((out, lse) if return_lse else out), owners
 
 
 def kivi4_sparse_attention(q: torch.Tensor, cache: Kivi4Cache, pages: torch.Tensor,
@@ -423,8 +481,6 @@ def _sparse_args(q, cache, pages, n_groups, res_len, sm_scale, out, out_dtype, n
         out = out.view(bs, hq, HEAD_DIM)
     out = out.unsqueeze(1) if squeeze else out
     return args, ((out, lse) if return_lse else out), owners
-
-
 
 
 MAX_LIST_TOKENS = 1024   # token-list entries per (b, kv) of kivi4_token_attention
