@@ -231,17 +231,17 @@ def test_search_rejects_bad_sizes():
 def _filter_premise(est_row, n, topk):
     """For the filter path's plan, from the oracle's estimates of one query:
     the number of keys reaching the threshold and the fullest 256-key list's
-    count.  Plan: s = min(n, 4096) sample keys, 64 blocks of 64 consecutive
-    keys starting at multiples of n // 64 (every key when n < 4096);
+    count.  Plan: s = min(n, 2048) sample keys, 64 runs of 32 consecutive
+    keys starting at multiples of n // 64 (every key when n < 2048);
     m = ceil(4 k s / n), at least 8; tau = the lower edge of the bin holding
     the m-th largest sample among 4096 bins of width 2^shift over the samples'
     [min, max] (shift = bit length of max - min, less 12, at least 0);
     lists hold 15 entries."""
     from oracle.select import ordered_key
     keys = ordered_key(est_row).astype(np.int64)
-    s = min(n, 4096)
+    s = min(n, 2048)
     i = np.arange(s)
-    sk = keys[(i >> 6) * (n // 64) + (i & 63)] if s == 4096 else keys
+    sk = keys[(i >> 5) * (n // 64) + (i & 31)] if s == 2048 else keys
     m = min(s, max(8, -(-4 * topk * s // n)))
     lo, hi = int(sk.min()), int(sk.max())
     shift = max((hi - lo).bit_length() - 12, 0)
@@ -279,8 +279,8 @@ def _check_planted(rng, n, topk, planted_rows, Q=2, dup=None, premise=None):
 
 
 def test_search_filter_path_tau_above_the_kth_key(rng):
-    """131072 keys, top-256: tau comes from the 32nd largest of 4096 samples
-    (64 blocks of 64 keys every 2048).  200 copies of the query sit at
+    """131072 keys, top-256: tau comes from the 16th largest of 2048 samples
+    (64 runs of 32 keys every 2048).  200 copies of the query sit at
     sampled positions, so tau falls in their estimate's bin and fewer than k
     keys reach it: the select kernel takes its exact full-pool path."""
     t = np.arange(200)
@@ -304,6 +304,13 @@ def test_search_filter_path_ties(rng):
     _check_planted(rng, 131072, 256, np.arange(0), dup=40,
                    premise=lambda hits, full: 256 <= hits <= 4096 and full <= 15)
     _check_planted(rng, 40000, 100, np.arange(0), dup=2, premise=lambda hits, full: full > 15)
+
+
+def test_search_filter_path_beyond_compaction(rng):
+    """262144 keys, top-1024: 4281 keys reach tau, more than the 4096 entries
+    the select kernel compacts into LDS, with every list within its 15
+    entries: the kernel selects and places them from its registers."""
+    _check_planted(rng, 262144, 1024, np.arange(0), premise=lambda hits, full: 4096 < hits and full <= 15)
 
 
 def test_search_plan_reads_current_contents(rng):

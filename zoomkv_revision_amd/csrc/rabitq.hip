@@ -152,12 +152,6 @@ __device__ __forceinline__ uint32_t row_min_u32(uint32_t v) {
   v = min(v, static_cast<uint32_t>(ZKV_ROR(static_cast<int>(v), 2)));
   return min(v, static_cast<uint32_t>(ZKV_ROR(static_cast<int>(v), 1)));
 }
-__device__ __forceinline__ int row_sum(int v) {
-  v += ZKV_ROR(v, 8);
-  v += ZKV_ROR(v, 4);
-  v += ZKV_ROR(v, 2);
-  return v + ZKV_ROR(v, 1);
-}
 __device__ __forceinline__ uint32_t lane_u32(uint32_t v, int lane) {
   return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), lane));
 }
@@ -169,10 +163,6 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
   v = row_min_u32(v);
   return min(min(lane_u32(v, 0), lane_u32(v, 16)), min(lane_u32(v, 32), lane_u32(v, 48)));
-}
-__device__ __forceinline__ int wave_sum(int v) {
-  v = row_sum(v);
-  return static_cast<int>(lane_u32(v, 0) + lane_u32(v, 16) + lane_u32(v, 32) + lane_u32(v, 48));
 }
 // value of lane (l ^ X) inside the lane's 32-lane half (X < 32)
 template <int X>
@@ -595,9 +585,18 @@ bool use_filter_path(int64_t n, int topk) { return n >= 128ll * topk && select_s
 // clears the next one while it counts: three barriers per round.
 // With exact == false it stops after the first round and returns the lower
 // edge of the bin holding the k-th largest item (at least k items are >= it).
+// With first_counted the caller has done the first round's counting: every
+// item into hist[(key - mn) >> radix12_first_shift(mn, mx)], hist[4096 ..
+// 8191] cleared, a barrier since.
+__device__ __forceinline__ int radix12_first_shift(uint32_t mn, uint32_t mx) {
+  if (mn == mx) return 0;
+  const int bits = 32 - __clz(static_cast<int>(mx - mn));
+  return bits > 12 ? bits - 12 : 0;
+}
 template <int NT, int NI>
 __device__ void block_radix_select12(const uint32_t (&key)[NI], uint32_t valid, int k, uint32_t mn, uint32_t mx,
-                                     int* hist, uint32_t* tmp, uint32_t& T, int& take_eq, bool exact = true) {
+                                     int* hist, uint32_t* tmp, uint32_t& T, int& take_eq, bool exact = true,
+                                     bool first_counted = false) {
   constexpr int W = NT / 64;
   constexpr int kBins = 4096, kPerT = kBins / NT;
   static_assert(kBins % NT == 0, "bins per thread");
@@ -605,22 +604,22 @@ __device__ void block_radix_select12(const uint32_t (&key)[NI], uint32_t valid, 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   uint32_t lo = mn, hi = mx;
   int rem = k;
-  int shift = 0;
-  if (lo != hi) {
-    const int bits = 32 - __clz(static_cast<int>(hi - lo));
-    shift = bits > 12 ? bits - 12 : 0;
-  }
+  int shift = radix12_first_shift(mn, mx);
   int buf = 0;
+  bool counted = first_counted;
   while (lo != hi) {
     int* h = hist + buf * kBins;
     int* h_next = hist + (buf ^ 1) * kBins;
+    if (!counted) {
 #pragma unroll
-    for (int j = 0; j < kPerT; ++j) h_next[tid * kPerT + j] = 0;
+      for (int j = 0; j < kPerT; ++j) h_next[tid * kPerT + j] = 0;
 #pragma unroll
-    for (int j = 0; j < NI; ++j) {
-      if (((valid >> j) & 1u) && key[j] >= lo && key[j] <= hi) atomicAdd(&h[(key[j] - lo) >> shift], 1);
+      for (int j = 0; j < NI; ++j) {
+        if (((valid >> j) & 1u) && key[j] >= lo && key[j] <= hi) atomicAdd(&h[(key[j] - lo) >> shift], 1);
+      }
+      __syncthreads();
     }
-    __syncthreads();
+    counted = false;
     // thread t owns bins t*kPerT .. t*kPerT + kPerT - 1; higher threads hold higher bins
     int c[kPerT], own = 0;
 #pragma unroll
@@ -1010,10 +1009,13 @@ __device__ void radix_select_stream(KeyAt&& key_at, int64_t n, int k, const Sele
 //    chunk c of a bucket holds its entries 2c - 1 and 2c, so every thread owns
 //    2 items per pass, straight from the load, in increasing index order
 //    (pass, thread, item); the bucket's count comes from its chunk 0 through
-//    a lane swizzle.  One block reduction gives the overflow flag, the number
-//    of entries and their key range.  The exact k-th key then comes from the
-//    radix rounds over the registers, and one scan per pass of packed
-//    (above, equal) counts places the selected indices in index order.
+//    a lane swizzle.  One block reduction gives the overflow flag, the key
+//    range and, from per-pass entry counts scanned over the threads, every
+//    entry's position in index order.  Up to 4 NT entries move to LDS there
+//    (thread t then holds entries t*C .. t*C + C - 1, C = ceil(entries / NT)),
+//    and the exact k-th key comes from the radix rounds over those, one scan
+//    of packed (above, equal) counts placing the selected indices in index
+//    order; more entries stay in the registers, with one scan per pass.
 //    Otherwise (a list beyond kFiltCap, or fewer than k keys at or above
 //    tau) the block selects over all n keys, estimates recomputed per pass.
 //    Then the exact rerank and the sort by (score desc, index asc).
@@ -1027,7 +1029,11 @@ __global__ __launch_bounds__(NT) void rabitq_select_kernel(
     int64_t* __restrict__ out_idx, float* __restrict__ out_score) {
   constexpr int W = NT / 64, NI = 2 * R;
   __shared__ int s_hist[2 * 4096];
+  constexpr int kCap = 4 * NT;  // compacted entries: up to 4 per thread
   __shared__ __attribute__((aligned(16))) uint32_t s_tmp[(R > 4 ? R : 4) * W + 2];
+  __shared__ __attribute__((aligned(16))) uint32_t s_red[4 * W];
+  __shared__ uint32_t s_ckey[kCap];
+  __shared__ int32_t s_cidx[kCap];
   __shared__ int32_t s_sel[kMaxTopk];
   __shared__ float s_score[kMaxTopk];
   __shared__ __attribute__((aligned(16))) uint64_t s_rkey[kMaxTopk + 1];
@@ -1083,35 +1089,132 @@ __global__ __launch_bounds__(NT) void rabitq_select_kernel(
       mx = max(mx, key[j]);
     }
   }
-  {  // block reduction: overflow, entries, key range (also orders the clear)
+  // per-pass entry counts scanned over the threads: entry positions in index
+  // order (pass, thread, item); with 16 passes the in-wave prefixes are
+  // recomputed where they are used instead of kept live
+  constexpr bool kKeepExcl = R <= 8;
+  auto pass_entries = [&](int r) { return __popc((valid >> (2 * r)) & 3u); };
+  int pos_ex[kKeepExcl ? R : 1];  // within the wave
+  int total = 0;
+  {  // block reduction: overflow, key range, entry offsets (also orders the clear)
     const uint32_t w_ovf = wave_max_u32(static_cast<uint32_t>(overflow));
-    const int w_cnt = wave_sum(__popc(valid));
     const uint32_t w_mn = wave_min_u32(mn), w_mx = wave_max_u32(mx);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int cnt = pass_entries(r);
+      const int incl = wave_incl_sum(cnt);
+      if constexpr (kKeepExcl) pos_ex[r] = incl - cnt;
+      if (lane == 63) s_tmp[r * W + wave] = static_cast<uint32_t>(incl);
+    }
     if (lane == 0) {
-      s_tmp[4 * wave] = w_ovf;
-      s_tmp[4 * wave + 1] = static_cast<uint32_t>(w_cnt);
-      s_tmp[4 * wave + 2] = w_mn;
-      s_tmp[4 * wave + 3] = w_mx;
+      s_red[4 * wave] = w_ovf;
+      s_red[4 * wave + 1] = w_mn;
+      s_red[4 * wave + 2] = w_mx;
     }
     __syncthreads();
+    if (wave == 0) {  // (pass, wave) totals -> exclusive offsets; the sum after them
+      int carry = 0;
+      for (int i0 = 0; i0 < R * W; i0 += 64) {
+        const bool in = i0 + lane < R * W;
+        const int v = in ? static_cast<int>(s_tmp[i0 + lane]) : 0;
+        const int inc = wave_incl_sum(v);
+        if (in) s_tmp[i0 + lane] = static_cast<uint32_t>(carry + inc - v);
+        carry += __builtin_amdgcn_readlane(inc, 63);
+      }
+      if (lane == 0) s_tmp[R * W] = static_cast<uint32_t>(carry);
+    }
     overflow = 0;
-    int total = 0;
     mn = 0xFFFFFFFFu;
     mx = 0u;
 #pragma unroll
     for (int w = 0; w < W; ++w) {
-      const u32x4_t v = reinterpret_cast<const u32x4_t*>(s_tmp)[w];
+      const u32x4_t v = reinterpret_cast<const u32x4_t*>(s_red)[w];
       overflow |= static_cast<int>(v[0]);
-      total += static_cast<int>(v[1]);
-      mn = min(mn, v[2]);
-      mx = max(mx, v[3]);
+      mn = min(mn, v[1]);
+      mx = max(mx, v[2]);
     }
     __syncthreads();
+    total = static_cast<int>(s_tmp[R * W]);
     valid = (overflow == 0 && total >= k) ? valid : 0u;
     overflow = overflow != 0 || total < k;  // from here: the fallback is needed
   }
 
-  if (!overflow) {
+  if (!overflow && total <= kCap) {
+    // compaction: the entries move to LDS in index order, then thread t
+    // holds entries t*C .. t*C + C - 1 (C = ceil(total / NT) <= 4), so the
+    // later radix rounds and the placement touch ~total / NT slots per
+    // thread instead of all 2 R; the radix's first round counts here, from
+    // the registers, and clears its second histogram
+    const int shift0 = radix12_first_shift(mn, mx);
+#pragma unroll
+    for (int j = 0; j < 4096 / NT; ++j) s_hist[4096 + tid * (4096 / NT) + j] = 0;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      int ex;
+      if constexpr (kKeepExcl) {
+        ex = pos_ex[r];
+      } else {
+        const int cnt = pass_entries(r);
+        ex = wave_incl_sum(cnt) - cnt;
+      }
+      int p = static_cast<int>(s_tmp[r * W + wave]) + ex;
+      const int32_t list0 = ((r * NT + tid) >> 3) * kFiltList;
+#pragma unroll
+      for (int j = 2 * r; j < 2 * r + 2; ++j) {
+        if ((valid >> j) & 1u) {
+          s_ckey[p] = key[j];
+          s_cidx[p] = list0 + static_cast<int32_t>((idx8[j >> 2] >> (8 * (j & 3))) & 255u);
+          ++p;
+          atomicAdd(&s_hist[(key[j] - mn) >> shift0], 1);
+        }
+      }
+    }
+    __syncthreads();
+    const int C = (total + NT - 1) / NT;
+    uint32_t ck[4], cv = 0u;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int sl = tid * C + j;
+      const bool ok = j < C && sl < total;
+      ck[j] = ok ? s_ckey[sl] : 0u;
+      cv |= static_cast<uint32_t>(ok) << j;
+    }
+    uint32_t T;
+    int take_eq;
+    block_radix_select12<NT, 4>(ck, cv, k, mn, mx, s_hist, s_tmp, T, take_eq, true, true);
+    __syncthreads();  // its last reads of s_tmp are done
+    // packed (above T, equal to T) counts, scanned over the threads (whose
+    // slots are in index order)
+    int gt = 0, eq = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if ((cv >> j) & 1u) {
+        gt += ck[j] > T;
+        eq += ck[j] == T;
+      }
+    }
+    const int cnt = gt | (eq << 16);
+    const int incl = wave_incl_sum(cnt);
+    if (lane == 63) s_tmp[wave] = static_cast<uint32_t>(incl);
+    __syncthreads();
+    int before = incl - cnt;
+#pragma unroll
+    for (int w = 0; w < W; ++w) before += w < wave ? static_cast<int>(s_tmp[w]) : 0;
+    int g = before & 0xFFFF, e = before >> 16;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if ((cv >> j) & 1u) {
+        const int32_t ix = s_cidx[tid * C + j];
+        if (ck[j] > T) {
+          s_sel[g + (e < take_eq ? e : take_eq)] = ix;
+          ++g;
+        } else if (ck[j] == T) {
+          if (e < take_eq) s_sel[g + e] = ix;
+          ++e;
+        }
+      }
+    }
+  } else if (!overflow) {
     uint32_t T;
     int take_eq;
     block_radix_select12<NT, NI>(key, valid, k, mn, mx, s_hist, s_tmp, T, take_eq);
@@ -1119,7 +1222,6 @@ __global__ __launch_bounds__(NT) void rabitq_select_kernel(
     // packed (above T, equal to T) counts per pass, scanned over the threads;
     // with 16 passes the per-pass prefixes are recomputed after the barriers
     // instead of kept live (32 keys per thread leave no registers for them)
-    constexpr bool kKeepExcl = R <= 8;
     auto pass_count = [&](int r) {
       int gt = 0, eq = 0;
 #pragma unroll
