@@ -313,6 +313,31 @@ def test_search_filter_path_beyond_compaction(rng):
     _check_planted(rng, 262144, 1024, np.arange(0), premise=lambda hits, full: 4096 < hits and full <= 15)
 
 
+def test_search_filter_path_negative_tau(rng):
+    """One cluster and queries opposite its keys: the 256th largest estimate,
+    and so tau, is negative, where the filter re-checks its hits with the
+    exact keys instead of taking the float compare's mask as it is."""
+    from zoomkv_revision_amd.rabitq import rabitq_encode, rabitq_search
+    s_np, s_t = _signs()
+    n, topk = 131072, 256
+    keys = orq.clustered_unit_keys(rng, n, 1)
+    qs = keys[:2] ^ np.uint16(0x8000)
+    ck, fk = orq.encode(keys, s_np)
+    cq, fq = orq.encode(qs, s_np)
+    est = orq.estimate(cq, fq, ck, fk)
+    for row in est:
+        assert np.sort(row)[-topk] < 0
+        hits, full = _filter_premise(row, n, topk)
+        assert hits >= topk and full <= 15
+    kt = _f16(keys)
+    codes, fac = rabitq_encode(kt, s_t)
+    cand, fidx, fsc = (from_torch(t) for t in rabitq_search(_f16(qs), kt, codes, fac, s_t, topk))
+    rc, ri, rs = orq.search(qs, keys, ck, fk, s_np, topk)
+    assert np.array_equal(cand, rc), "candidate set"
+    assert np.array_equal(fidx, ri), "reranked order"
+    assert np.array_equal(fsc.view(np.uint32), rs.view(np.uint32)), "exact scores"
+
+
 def test_search_plan_reads_current_contents(rng):
     """A SearchPlan checks its buffers once; each run searches what they hold
     then (queries rewritten in place between runs) with rabitq_search's bits."""

@@ -97,6 +97,24 @@ __device__ __forceinline__ float rabitq_estimate(u32x4_t qc, float fq, u32x4_t k
   return t * 0.0078125f;
 }
 
+// popc(a ^ b) over 128 bits as one chain of count-and-add instructions
+__device__ __forceinline__ int popc_xor128(u32x4_t a, u32x4_t b) {
+  uint32_t pc;
+  asm("v_bcnt_u32_b32 %0, %1, 0" : "=v"(pc) : "v"(a[0] ^ b[0]));
+  asm("v_bcnt_u32_b32 %0, %1, %2" : "=v"(pc) : "v"(a[1] ^ b[1]), "v"(pc));
+  asm("v_bcnt_u32_b32 %0, %1, %2" : "=v"(pc) : "v"(a[2] ^ b[2]), "v"(pc));
+  asm("v_bcnt_u32_b32 %0, %1, %2" : "=v"(pc) : "v"(a[3] ^ b[3]), "v"(pc));
+  return static_cast<int>(pc);
+}
+
+// w * 2 + (this lane's bit of the lane mask m), one add with carry-in
+__device__ __forceinline__ uint32_t shift_in(uint32_t w, uint64_t m) {
+  uint32_t r;
+  uint64_t carry_out;
+  asm("v_addc_co_u32_e64 %0, %1, %2, %2, %3" : "=v"(r), "=s"(carry_out) : "v"(w), "s"(m));
+  return r;
+}
+
 __device__ __forceinline__ float query_factor(const uint16_t* fac_q, int64_t pq) {
   const uint32_t f = reinterpret_cast<const uint32_t*>(fac_q)[pq];
   return f16_to_f32(static_cast<uint16_t>(f)) * f16_to_f32(static_cast<uint16_t>(f >> 16));
@@ -811,8 +829,10 @@ __global__ __launch_bounds__(kBigNT) void rabitq_prep_kernel(
 //    into LDS; then every lane holds its query's code, factor and tau and
 //    walks the 64 keys, 8 at a time (their LDS reads first), into a hit mask:
 //    est >= tau compared as floats, before the final 2^-7 scale and the
-//    order-preserving key, so the mask can only hold extra keys (+-0); the
-//    hits are re-checked with the exact keys when they are written.  One
+//    order-preserving key, so the mask can only hold extra keys (+-0, the
+//    2^-7 scale's underflow, NaN); the hits are re-checked with the exact
+//    keys, unless tau is a positive normal float and every factor finite,
+//    where the two compares agree.  One
 //    barrier gives each wave its offset in the block's list per query.  A
 //    list is a 128-byte bucket: word 0 the hit count, then the first 15 hits
 //    in increasing index order as (key, index) word pairs from word 2, so
@@ -833,12 +853,14 @@ __global__ __launch_bounds__(256) void rabitq_filter_kernel(
   const int64_t pool = blockIdx.z;
   const int64_t p0 = static_cast<int64_t>(list) * kFiltList + wave * kFiltWave;
   const int nk = n - p0 < kFiltWave ? static_cast<int>(n - p0 > 0 ? n - p0 : 0) : kFiltWave;
+  float fk;
   {
     const int64_t row = pool * n + (lane < nk ? p0 + lane : 0);
     const u32x4_t c = reinterpret_cast<const u32x4_t*>(codes_k)[row];
     const uint32_t f = reinterpret_cast<const uint32_t*>(fac_k)[row];
     s_kc[wave][lane] = c;
-    s_fk[wave][lane] = f16_to_f32(static_cast<uint16_t>(f)) * f16_to_f32(static_cast<uint16_t>(f >> 16));
+    fk = f16_to_f32(static_cast<uint16_t>(f)) * f16_to_f32(static_cast<uint16_t>(f >> 16));
+    s_fk[wave][lane] = fk;
   }
   const int qi = blockIdx.y * 64 + lane;
   const bool q_ok = qi < queries;
@@ -851,10 +873,12 @@ __global__ __launch_bounds__(256) void rabitq_filter_kernel(
   const float t128 = __uint_as_float((t & 0x80000000u) ? (t & 0x7FFFFFFFu) : ~t) * 128.0f;
   __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the wave's LDS writes are done
   __builtin_amdgcn_wave_barrier();
-  uint64_t hits = 0;  // bit j: key j of the wave's 64 may reach tau
+  // bit j of h[j / 32]: key j of the wave's 64 may reach tau; the keys are
+  // walked from the last, each compare shifted in at bit 0 (h + h + bit)
+  uint32_t h[2] = {0u, 0u};
   constexpr int kG = 8;
 #pragma unroll
-  for (int j0 = 0; j0 < kFiltWave; j0 += kG) {
+  for (int j0 = kFiltWave - kG; j0 >= 0; j0 -= kG) {
     u32x4_t c[kG];
     float f[kG];
 #pragma unroll
@@ -863,20 +887,25 @@ __global__ __launch_bounds__(256) void rabitq_filter_kernel(
       f[g] = s_fk[wave][j0 + g];
     }
 #pragma unroll
-    for (int g = 0; g < kG; ++g) {
-      int pc = __popc(qc[0] ^ c[g][0]);
-      pc = __popc(qc[1] ^ c[g][1]) + pc;
-      pc = __popc(qc[2] ^ c[g][2]) + pc;
-      pc = __popc(qc[3] ^ c[g][3]) + pc;
+    for (int g = kG - 1; g >= 0; --g) {
+      const int pc = popc_xor128(qc, c[g]);
       float e = fq * f[g];  // rabitq_estimate's operations up to the 2^-7 scale
-      e = e * static_cast<float>(kD - 2 * pc);
-      hits |= static_cast<uint64_t>(!(e < t128)) << (j0 + g);  // NaN estimates are candidates too
+      e = e * fmaf(-2.0f, static_cast<float>(pc), static_cast<float>(kD));  // = float(kD - 2 pc), exactly
+      uint32_t& hw = h[(j0 + g) >> 5];
+      hw = shift_in(hw, __builtin_amdgcn_ballot_w64(!(e < t128)));  // NaN estimates are candidates too
     }
   }
+  uint64_t hits = h[0] | (static_cast<uint64_t>(h[1]) << 32);
   hits &= nk >= 64 ? ~0ull : ((1ull << nk) - 1ull);
-  // exact re-check of the (few) candidates, in index order
-  uint64_t exact = 0;
-  for (uint64_t m = hits; m != 0; m &= m - 1) {
+  // exact re-check of the (few) candidates, in index order.  None is needed
+  // when tau * 2^7 is a normal float in [2^-100, FLT_MAX] and no estimate can
+  // be NaN (the query's and the 64 keys' factors finite, so every product is
+  // finite): then a hit's estimate is >= 2^-100, its 2^-7 scale is exact and
+  // ordered the same as the float compare, and a miss scales to below tau
+  const bool keys_finite = __builtin_amdgcn_ballot_w64(!__builtin_isfinite(fk)) == 0;
+  const bool direct = keys_finite && __builtin_isfinite(fq) && t128 >= 0x1p-100f && t128 <= 0x1.fffffep127f;
+  uint64_t exact = direct ? hits : 0;
+  for (uint64_t m = direct ? 0 : hits; m != 0; m &= m - 1) {
     const int j = __builtin_ctzll(m);
     const u32x4_t c = s_kc[wave][j];
     const int pc = __popc(qc[0] ^ c[0]) + __popc(qc[1] ^ c[1]) + __popc(qc[2] ^ c[2]) + __popc(qc[3] ^ c[3]);
