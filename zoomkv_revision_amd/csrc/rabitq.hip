@@ -925,15 +925,25 @@ __global__ __launch_bounds__(256) void rabitq_filter_kernel(
   }
   uint32_t* row = s_bkt[lane];
   if (wave == 0) row[0] = static_cast<uint32_t>(total);
-  int e = before;
-  for (uint64_t m = exact; m != 0 && e < kFiltCap; m &= m - 1, ++e) {
-    const int j = __builtin_ctzll(m);
-    const u32x4_t c = s_kc[wave][j];
-    const int pc = __popc(qc[0] ^ c[0]) + __popc(qc[1] ^ c[1]) + __popc(qc[2] ^ c[2]) + __popc(qc[3] ^ c[3]);
-    float est = fq * s_fk[wave][j];
-    est = est * static_cast<float>(kD - 2 * pc);
+  // two entries per step, both keys' LDS reads first
+  auto put = [&](int e, int j, const u32x4_t c, float f) {
+    float est = fq * f;
+    est = est * static_cast<float>(kD - 2 * popc_xor128(qc, c));
     row[2 + 2 * e] = ordered_key_f(est * 0.0078125f);
     row[3 + 2 * e] = static_cast<uint32_t>(p0 + j);
+  };
+  int e = before;
+  for (uint64_t m = exact; m != 0 && e < kFiltCap;) {
+    const int j0 = __builtin_ctzll(m);
+    m &= m - 1;
+    const bool two = m != 0 && e + 1 < kFiltCap;
+    const int j1 = two ? __builtin_ctzll(m) : j0;
+    if (two) m &= m - 1;
+    const u32x4_t c0 = s_kc[wave][j0], c1 = s_kc[wave][j1];
+    const float f0 = s_fk[wave][j0], f1 = s_fk[wave][j1];
+    put(e, j0, c0, f0);
+    if (two) put(e + 1, j1, c1, f1);
+    e += two ? 2 : 1;
   }
   __syncthreads();
   // ---- the buckets out: 4 threads per bucket, 8 words each, as two 16-byte
@@ -1409,13 +1419,21 @@ __global__ __launch_bounds__(NT) void rabitq_select_kernel(
     }
     int rank[4] = {0, 0, 0, 0};
     const int pairs = (k + 1) >> 1;
-    for (int c = p; c < pairs; c += P) {
-      const u32x4_t v = rk[c];
+    auto count = [&](const u32x4_t v) {
       const uint64_t k0 = v[0] | (static_cast<uint64_t>(v[1]) << 32);
       const uint64_t k1 = v[2] | (static_cast<uint64_t>(v[3]) << 32);
 #pragma unroll
       for (int i = 0; i < 4; ++i) rank[i] += static_cast<int>(k0 > ki[i]) + static_cast<int>(k1 > ki[i]);
+    };
+    int c = p;
+    for (; c + 3 * P < pairs; c += 4 * P) {  // four pair reads in flight
+      const u32x4_t v0 = rk[c], v1 = rk[c + P], v2 = rk[c + 2 * P], v3 = rk[c + 3 * P];
+      count(v0);
+      count(v1);
+      count(v2);
+      count(v3);
     }
+    for (; c < pairs; c += P) count(rk[c]);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       if (P > 1) rank[i] += swizzle_xor<1>(rank[i]);
