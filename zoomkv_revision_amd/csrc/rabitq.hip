@@ -701,10 +701,9 @@ __global__ __launch_bounds__(kBigNT) void rabitq_prep_kernel(
   __shared__ __attribute__((aligned(16))) float s_terms[3][kD + 4];  // x_d^2, y_d^2, |y_d| (rows 4 banks apart)
   __shared__ float s_sums[3];
   __shared__ u32x4_t s_qc;
-  __shared__ float s_fq;
   __shared__ int s_hist[2 * 4096];
   __shared__ uint32_t s_tmp[2 * (kBigNT / 64) + 2];
-  const int tid = threadIdx.x, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t pool = blockIdx.y;
   const int64_t pq = pool * queries + blockIdx.x;
   // ---- sample rows first: item i of thread t is sample s = i * NT + t ----
@@ -771,35 +770,34 @@ __global__ __launch_bounds__(kBigNT) void rabitq_prep_kernel(
       reinterpret_cast<uint32_t*>(q_codes + pq * 16)[lane] = word;
       reinterpret_cast<uint32_t*>(&s_qc)[lane] = word;
     }
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS writes are done
-    __builtin_amdgcn_wave_barrier();
-    if (lane < 3) {  // lane j: sum of terms j in dimension order (the encode kernel's arithmetic)
-      const float4* t = reinterpret_cast<const float4*>(s_terms[lane]);
-      float acc = 0.0f;
-#pragma unroll 8
-      for (int c = 0; c < kD / 4; ++c) {
-        const float4 v = t[c];
-        acc = acc + v.x;
-        acc = acc + v.y;
-        acc = acc + v.z;
-        acc = acc + v.w;
-      }
-      s_sums[lane] = acc;
+  }
+  __syncthreads();
+  // ---- the factor sums (waves 0, 1, 2: sum w), each in dimension order as a
+  //      chain along the lanes: step i hands the running sum from lane l - 1
+  //      to lane l (DPP wave shift right), which adds dims 2l and 2l + 1; after
+  //      64 steps lane 63 holds ((0 + t_0) + t_1) + ... + t_127, the encode
+  //      kernel's order ----
+  if (wave < 3) {
+    const float2 t = reinterpret_cast<const float2*>(s_terms[wave])[lane];
+    float acc = 0.0f;
+#pragma unroll 16
+    for (int i = 0; i < 64; ++i) {
+      acc = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(acc), 0x138, 0xF, 0xF, false)) + t.x;
+      acc = acc + t.y;
     }
-    __builtin_amdgcn_s_waitcnt(0xC07F);
-    __builtin_amdgcn_wave_barrier();
-    if (lane == 0) {
-      const float nsq = s_sums[0], ysq = s_sums[1], yabs = s_sums[2];
-      const float norm = sqrtf(nsq);
-      const float corr = yabs > 0.0f ? (sqrtf(ysq) * kSqrt128) / yabs : 0.0f;
-      const uint16_t hn = f32_to_f16_bits(norm), hc = f32_to_f16_bits(corr);
-      reinterpret_cast<uint32_t*>(q_fac)[pq] = static_cast<uint32_t>(hn) | (static_cast<uint32_t>(hc) << 16);
-      s_fq = f16_to_f32(hn) * f16_to_f32(hc);
-    }
+    if (lane == 63) s_sums[wave] = acc;
   }
   __syncthreads();
   const u32x4_t qc = s_qc;
-  const float fq = s_fq;
+  float fq;
+  {  // the query factor (every thread; thread 0 stores it)
+    const float nsq = s_sums[0], ysq = s_sums[1], yabs = s_sums[2];
+    const float norm = sqrtf(nsq);
+    const float corr = yabs > 0.0f ? (sqrtf(ysq) * kSqrt128) / yabs : 0.0f;
+    const uint16_t hn = f32_to_f16_bits(norm), hc = f32_to_f16_bits(corr);
+    if (tid == 0) reinterpret_cast<uint32_t*>(q_fac)[pq] = static_cast<uint32_t>(hn) | (static_cast<uint32_t>(hc) << 16);
+    fq = f16_to_f32(hn) * f16_to_f32(hc);
+  }
   uint32_t key[NI];
   uint32_t mn = 0xFFFFFFFFu, mx = 0u;
 #pragma unroll
@@ -810,16 +808,59 @@ __global__ __launch_bounds__(kBigNT) void rabitq_prep_kernel(
       mx = max(mx, key[i]);
     }
   }
+  constexpr int W = kBigNT / 64, kPerT = 4096 / kBigNT;
 #pragma unroll
-  for (int j = 0; j < 4096 / kBigNT; ++j) s_hist[tid * (4096 / kBigNT) + j] = 0;
-  Block<kBigNT>::minmax(mn, mx, s_tmp);  // its barriers also order the clear
-  uint32_t T;
-  int take_eq;
-  // one histogram round: tau = the lower edge of the bin holding the m-th
-  // largest sample key (4096 bins over the samples' range), so at least m
-  // samples reach it
-  block_radix_select12<kBigNT, NI>(key, (1u << valid_n) - 1u, m, mn, mx, s_hist, s_tmp, T, take_eq, false);
-  if (tid == 0) tau[pq] = T;
+  for (int j = 0; j < kPerT; ++j) s_hist[tid * kPerT + j] = 0;
+  // the samples' range: one barrier, which also orders the clear before the
+  // counts (the reads of s_tmp here all precede the counts' barrier, after
+  // which s_tmp is rewritten)
+  mn = wave_min_u32(mn);
+  mx = wave_max_u32(mx);
+  if (lane == 0) {
+    s_tmp[wave] = mn;
+    s_tmp[W + wave] = mx;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int w = 0; w < W; ++w) {
+    mn = min(mn, s_tmp[w]);
+    mx = max(mx, s_tmp[W + w]);
+  }
+  // one 12-bit histogram round over [mn, mx] (block_radix_select12's first
+  // round): tau = the lower edge of the bin holding the m-th largest sample,
+  // so at least m samples reach it; the thread owning that bin stores it
+  if (mn == mx) {
+    if (tid == 0) tau[pq] = mn;
+    return;
+  }
+  const int shift = radix12_first_shift(mn, mx);
+#pragma unroll
+  for (int i = 0; i < NI; ++i)
+    if (i < valid_n) atomicAdd(&s_hist[(key[i] - mn) >> shift], 1);
+  __syncthreads();
+  int c[kPerT], own = 0;
+#pragma unroll
+  for (int j = 0; j < kPerT; ++j) {
+    c[j] = s_hist[tid * kPerT + j];
+    own += c[j];
+  }
+  const int incl = wave_incl_sum(own);
+  const int wave_total = __builtin_amdgcn_readlane(incl, 63);
+  if (lane == 0) s_tmp[wave] = static_cast<uint32_t>(wave_total);
+  __syncthreads();
+  int above = wave_total - incl;  // samples in higher bins than this thread's
+#pragma unroll
+  for (int w = 0; w < W; ++w) above += w > wave ? static_cast<int>(s_tmp[w]) : 0;
+  if (above < m && above + own >= m) {
+#pragma unroll
+    for (int j = kPerT - 1; j >= 0; --j) {
+      const int at_or_above = above + c[j];
+      if (at_or_above >= m && above < m)
+        tau[pq] = static_cast<uint32_t>(static_cast<uint64_t>(mn) +
+                                        (static_cast<uint64_t>(tid * kPerT + j) << shift));
+      above = at_or_above;
+    }
+  }
 }
 
 // ----------------------------------------------------------------------------
