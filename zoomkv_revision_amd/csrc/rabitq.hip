@@ -115,6 +115,35 @@ __device__ __forceinline__ uint32_t shift_in(uint32_t w, uint64_t m) {
   return r;
 }
 
+// lane L of v = the (uniform) value x
+template <int L>
+__device__ __forceinline__ void write_lane(uint32_t& v, uint32_t x) {
+  asm("v_writelane_b32 %0, %1, %2" : "+v"(v) : "s"(x), "n"(L));
+}
+
+// The filter's per-register step for the 32 x 32 result of query rows
+// 32 RB .. 32 RB + 31: register R holds rows 8 (R / 4) + R % 4 (lanes 0-31)
+// and + 4 (lanes 32-63) against column lane % 32; the compare's lane mask
+// halves are those two queries' hit words, written into their lanes
+template <int RB, int R>
+struct FilterEpilogue {
+  static __device__ __forceinline__ void run(const i32x16_t& acc, const float (&fqr)[16], const float (&tr)[16],
+                                             float fk, uint32_t& h) {
+    float e = fqr[R] * fk;  // rabitq_estimate's operations up to the 2^-7 scale
+    e = e * static_cast<float>(acc[R]);
+    const uint64_t m = __builtin_amdgcn_ballot_w64(!(e < tr[R]));  // NaN estimates are candidates too
+    constexpr int q0 = 32 * RB + 8 * (R >> 2) + (R & 3);
+    write_lane<q0>(h, static_cast<uint32_t>(m));
+    write_lane<q0 + 4>(h, static_cast<uint32_t>(m >> 32));
+    FilterEpilogue<RB, R + 1>::run(acc, fqr, tr, fk, h);
+  }
+};
+template <int RB>
+struct FilterEpilogue<RB, 16> {
+  static __device__ __forceinline__ void run(const i32x16_t&, const float (&)[16], const float (&)[16], float,
+                                             uint32_t&) {}
+};
+
 __device__ __forceinline__ float query_factor(const uint16_t* fac_q, int64_t pq) {
   const uint32_t f = reinterpret_cast<const uint32_t*>(fac_q)[pq];
   return f16_to_f32(static_cast<uint16_t>(f)) * f16_to_f32(static_cast<uint16_t>(f >> 16));
@@ -886,6 +915,8 @@ __global__ __launch_bounds__(256) void rabitq_filter_kernel(
     int n_lists, uint32_t* __restrict__ buckets) {
   __shared__ u32x4_t s_kc[4][kFiltWave];
   __shared__ float s_fk[4][kFiltWave];
+  __shared__ __attribute__((aligned(16))) float s_qf[4][2][64];  // per wave: the queries' factors, tau * 2^7
+  __shared__ uint64_t s_lut[4][256];                             // per wave: byte -> 8 +-1 bytes
   __shared__ int s_cnt[4][64];
   __shared__ uint32_t s_bkt[64][kBucketWords + 1];  // the block's 64 buckets; odd stride: per-lane rows conflict-free
   const int lane = threadIdx.x & 63;
@@ -912,28 +943,79 @@ __global__ __launch_bounds__(256) void rabitq_filter_kernel(
   // tau as an unscaled float: est * 2^-7 >= tau  <=>  est >= tau * 2^7 (exact
   // scaling), with the float compare putting -0 with +0
   const float t128 = __uint_as_float((t & 0x80000000u) ? (t & 0x7FFFFFFFu) : ~t) * 128.0f;
+  const int half = lane >> 5, col = lane & 31;
+  s_qf[wave][0][lane] = fq;
+  s_qf[wave][1][lane] = t128;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {  // lut[x]: byte i = +1 if bit i of x, else -1
+    const uint32_t x = static_cast<uint32_t>(lane + 64 * e);
+    const uint32_t lo = ((x & 15u) * 0x204081u) & 0x01010101u, hi = ((x >> 4) * 0x204081u) & 0x01010101u;
+    s_lut[wave][x] = static_cast<uint64_t>(~(lo * 0xFEu)) | (static_cast<uint64_t>(~(hi * 0xFEu)) << 32);
+  }
   __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the wave's LDS writes are done
   __builtin_amdgcn_wave_barrier();
-  // bit j of h[j / 32]: key j of the wave's 64 may reach tau; the keys are
-  // walked from the last, each compare shifted in at bit 0 (h + h + bit)
-  uint32_t h[2] = {0u, 0u};
-  constexpr int kG = 8;
+  // ---- the +-1 dot products 128 - 2 popc(q ^ k) of 64 queries (rows) x the
+  //      wave's 64 keys (columns), exact in int8 MFMAs (32 x 32 x 16): two
+  //      row blocks of 32 queries, two column blocks of 32 keys.  Lane l
+  //      supplies row / column l % 32, dims 16 s + 8 (l / 32) .. + 7 of K
+  //      step s; register r of a 32 x 32 result holds row 8 (r / 4) + 4 (l /
+  //      32) + r % 4, column l % 32.  Then per register: the estimate's two
+  //      multiplies (fq fk) dot, the compare with tau * 2^7 as one lane mask,
+  //      whose halves are the hit words of two queries over 32 keys, written
+  //      into those queries' lanes ----
+  // A operands: query 32 rb + col's code (this lane's own for rb = half, the
+  // lane 32 apart's for the other) as +-1 bytes
+  int64_t qa[2][8];
+  {
+    u32x4_t other;
 #pragma unroll
-  for (int j0 = kFiltWave - kG; j0 >= 0; j0 -= kG) {
-    u32x4_t c[kG];
-    float f[kG];
+    for (int w = 0; w < 4; ++w) other[w] = static_cast<uint32_t>(__shfl_xor(static_cast<int>(qc[w]), 32));
 #pragma unroll
-    for (int g = 0; g < kG; ++g) {
-      c[g] = s_kc[wave][j0 + g];
-      f[g] = s_fk[wave][j0 + g];
+    for (int rb = 0; rb < 2; ++rb) {
+      const u32x4_t c = rb == half ? qc : other;
+#pragma unroll
+      for (int st = 0; st < 8; ++st)
+        qa[rb][st] = static_cast<int64_t>(s_lut[wave][(c[st >> 1] >> (8 * ((2 * st + half) & 3))) & 255u]);
+    }
+  }
+  int64_t kb[2][8];
+  float fkc[2];
+#pragma unroll
+  for (int cb = 0; cb < 2; ++cb) {
+    const u32x4_t c = s_kc[wave][32 * cb + col];
+    fkc[cb] = s_fk[wave][32 * cb + col];
+#pragma unroll
+    for (int st = 0; st < 8; ++st) {
+      const uint32_t x = (c[st >> 1] >> (8 * ((2 * st + half) & 3))) & 255u;
+      kb[cb][st] = static_cast<int64_t>(s_lut[wave][x]);
+    }
+  }
+  uint32_t h[2] = {0u, 0u};  // bit j of h[j / 32] (this lane's query): key j of the wave's 64 may reach tau
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb) {
+    i32x16_t acc[2];
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) acc[cb] = i32x16_t{};
+#pragma unroll
+    for (int st = 0; st < 8; ++st) {
+#pragma unroll
+      for (int cb = 0; cb < 2; ++cb)
+        acc[cb] = __builtin_amdgcn_mfma_i32_32x32x16_i8(qa[rb][st], kb[cb][st], acc[cb], 0, 0, 0);
+    }
+    float fqr[16], tr[16];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const float4 f4 = *reinterpret_cast<const float4*>(&s_qf[wave][0][32 * rb + 8 * g + 4 * half]);
+      const float4 t4 = *reinterpret_cast<const float4*>(&s_qf[wave][1][32 * rb + 8 * g + 4 * half]);
+      fqr[4 * g] = f4.x; fqr[4 * g + 1] = f4.y; fqr[4 * g + 2] = f4.z; fqr[4 * g + 3] = f4.w;
+      tr[4 * g] = t4.x; tr[4 * g + 1] = t4.y; tr[4 * g + 2] = t4.z; tr[4 * g + 3] = t4.w;
     }
 #pragma unroll
-    for (int g = kG - 1; g >= 0; --g) {
-      const int pc = popc_xor128(qc, c[g]);
-      float e = fq * f[g];  // rabitq_estimate's operations up to the 2^-7 scale
-      e = e * fmaf(-2.0f, static_cast<float>(pc), static_cast<float>(kD));  // = float(kD - 2 pc), exactly
-      uint32_t& hw = h[(j0 + g) >> 5];
-      hw = shift_in(hw, __builtin_amdgcn_ballot_w64(!(e < t128)));  // NaN estimates are candidates too
+    for (int cb = 0; cb < 2; ++cb) {
+      if (rb == 0)
+        FilterEpilogue<0, 0>::run(acc[cb], fqr, tr, fkc[cb], h[cb]);
+      else
+        FilterEpilogue<1, 0>::run(acc[cb], fqr, tr, fkc[cb], h[cb]);
     }
   }
   uint64_t hits = h[0] | (static_cast<uint64_t>(h[1]) << 32);

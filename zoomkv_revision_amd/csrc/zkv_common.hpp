@@ -36,6 +36,7 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef int i32x16_t __attribute__((ext_vector_type(16)));
 
 // ---------------------------------------------------------------------------
 // Exact bf16 / fp16 arithmetic helpers (IEEE fp32 op, then RNE)
