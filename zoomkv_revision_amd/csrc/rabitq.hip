@@ -107,14 +107,6 @@ __device__ __forceinline__ int popc_xor128(u32x4_t a, u32x4_t b) {
   return static_cast<int>(pc);
 }
 
-// w * 2 + (this lane's bit of the lane mask m), one add with carry-in
-__device__ __forceinline__ uint32_t shift_in(uint32_t w, uint64_t m) {
-  uint32_t r;
-  uint64_t carry_out;
-  asm("v_addc_co_u32_e64 %0, %1, %2, %2, %3" : "=v"(r), "=s"(carry_out) : "v"(w), "s"(m));
-  return r;
-}
-
 // lane L of v = the (uniform) value x
 template <int L>
 __device__ __forceinline__ void write_lane(uint32_t& v, uint32_t x) {
@@ -896,8 +888,9 @@ __global__ __launch_bounds__(kBigNT) void rabitq_prep_kernel(
 // 2. filter: lane = query; a block of 4 waves covers 256 consecutive keys (a
 //    list), each wave 64 of them; grid (lists, query groups of 64, pools).
 //    Lane l of a wave loads key l of the wave's 64 (one coalesced request)
-//    into LDS; then every lane holds its query's code, factor and tau and
-//    walks the 64 keys, 8 at a time (their LDS reads first), into a hit mask:
+//    into LDS and holds query l's code, factor and tau.  The 64 x 64 +-1 dot
+//    products come from int8 MFMAs, and each result register's compare gives
+//    two queries' hit words over 32 keys (the mask lane = query, bit = key):
 //    est >= tau compared as floats, before the final 2^-7 scale and the
 //    order-preserving key, so the mask can only hold extra keys (+-0, the
 //    2^-7 scale's underflow, NaN); the hits are re-checked with the exact
