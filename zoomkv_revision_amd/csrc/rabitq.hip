@@ -622,8 +622,6 @@ bool use_filter_path(int64_t n, int topk) { return n >= 128ll * topk && select_s
 // each later one 12 bits below the previous, so a 32-bit range takes at most
 // three rounds.  Two histograms alternate (hist: 2 x 4096 ints), so a round
 // clears the next one while it counts: three barriers per round.
-// With exact == false it stops after the first round and returns the lower
-// edge of the bin holding the k-th largest item (at least k items are >= it).
 // With first_counted the caller has done the first round's counting: every
 // item into hist[(key - mn) >> radix12_first_shift(mn, mx)], hist[4096 ..
 // 8191] cleared, a barrier since.
@@ -634,7 +632,7 @@ __device__ __forceinline__ int radix12_first_shift(uint32_t mn, uint32_t mx) {
 }
 template <int NT, int NI>
 __device__ void block_radix_select12(const uint32_t (&key)[NI], uint32_t valid, int k, uint32_t mn, uint32_t mx,
-                                     int* hist, uint32_t* tmp, uint32_t& T, int& take_eq, bool exact = true,
+                                     int* hist, uint32_t* tmp, uint32_t& T, int& take_eq,
                                      bool first_counted = false) {
   constexpr int W = NT / 64;
   constexpr int kBins = 4096, kPerT = kBins / NT;
@@ -693,7 +691,7 @@ __device__ void block_radix_select12(const uint32_t (&key)[NI], uint32_t valid, 
     const uint64_t new_hi = new_lo + (1ull << shift) - 1ull;
     lo = static_cast<uint32_t>(new_lo);
     hi = static_cast<uint32_t>(new_hi < hi ? new_hi : hi);
-    if (shift == 0 || !exact) break;
+    if (shift == 0) break;
     // the top k take the whole bin: T = its lower edge, and rem (the bin's
     // count) covers every item == T
     if (rem == static_cast<int>(tmp[W + 2])) break;
@@ -709,10 +707,11 @@ __device__ void block_radix_select12(const uint32_t (&key)[NI], uint32_t valid, 
 // 1. prep, per (query, pool), 1024 threads: every thread requests its sample
 //    keys first -- s = min(n, 2048) keys in 64 runs of 32 consecutive keys
 //    spread over the pool (or every key when n < 2048) -- while wave 0
-//    encodes the query (the FWHT across lanes, the factor sums in dimension
-//    order by one lane: the bits of rabitq_encode_kernel); then tau = the
-//    lower edge of the 4096-bin histogram bin (over the samples' range) that
-//    holds the m-th largest sample key.
+//    encodes the query (the FWHT across lanes) and waves 0-2 form the three
+//    factor sums in dimension order as lane chains (the bits of
+//    rabitq_encode_kernel); then tau = the lower edge of the 4096-bin
+//    histogram bin (over the samples' range) that holds the m-th largest
+//    sample key.
 // ----------------------------------------------------------------------------
 __global__ __launch_bounds__(kBigNT) void rabitq_prep_kernel(
     const uint16_t* __restrict__ q, const float* __restrict__ signs, const uint8_t* __restrict__ codes_k,
@@ -1336,7 +1335,7 @@ __global__ __launch_bounds__(NT) void rabitq_select_kernel(
     }
     uint32_t T;
     int take_eq;
-    block_radix_select12<NT, 4>(ck, cv, k, mn, mx, s_hist, s_tmp, T, take_eq, true, true);
+    block_radix_select12<NT, 4>(ck, cv, k, mn, mx, s_hist, s_tmp, T, take_eq, true);
     __syncthreads();  // its last reads of s_tmp are done
     // packed (above T, equal to T) counts, scanned over the threads (whose
     // slots are in index order)
