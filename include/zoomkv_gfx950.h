@@ -573,6 +573,33 @@ int zkv_qk_norm_rope(const uint16_t* qkv, int64_t qkv_ld, int bs, int hq, int hk
                      uint16_t* q_out, uint16_t* k_dst, int64_t k_sb, int64_t k_sh, uint16_t* v_dst,
                      int64_t v_sb, int64_t v_sh, zkv_stream_t stream);
 
+/* Next-token sampling of one decode step over the top-window logits, one
+ * launch: replaces the sampling chain of Z/model_hub/LLM.py:63-139
+ * (temperature, top-k keeping ties at the k-th value, top-p keeping the token
+ * that crosses top_p, softmax, torch.multinomial for one sample).
+ * logits   fp32 [bs, vocab], row stride ld; scaled by inv_temperature (the
+ *          fp32 reciprocal, as torch scales a CUDA tensor by a Python float)
+ * window   k + W <= 64 (W = 16 in the decode step), with
+ *          ceil(vocab / 8192) * window <= 2048: the row's `window` largest
+ *          scaled logits under (value desc, index asc) are ranked; top-k and
+ *          top-p act inside them
+ * top_p    applied when 0 < top_p < 1
+ * expo     fp32 [bs, vocab] (row stride expo_ld) of Exp(1) draws: the token is
+ *          the lowest index of the largest p / expo over the window, the draw
+ *          torch.multinomial(probs, 1) makes from the same Exp(1) row
+ * tokens   int64 [bs]; overflow int32 [bs]: 1 when the window's last value
+ *          equals the k-th (the tie group may reach past the window: the
+ *          caller then draws over the whole vocabulary with the same expo)
+ * workspace zkv_sample_window_workspace_size() bytes, 256-byte aligned: the
+ *          per-row arrival counters (the first 4 bs bytes, rounded up to 256)
+ *          must be zero before the first call with a given bs, and every call
+ *          leaves them zero; the candidates follow.  Calls that overlap on
+ *          one workspace race. */
+size_t zkv_sample_window_workspace_size(int bs, int vocab, int window);
+int zkv_sample_window(const float* logits, int64_t ld, int bs, int vocab, float inv_temperature, int top_k,
+                      int window, float top_p, const float* expo, int64_t expo_ld, int64_t* tokens,
+                      int32_t* overflow, void* workspace, size_t workspace_bytes, zkv_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -52,6 +52,76 @@ def test_windowed_sampling_matches_full_vocabulary_on_device():
         assert torch.equal(a, b), (trial, a, b)
 
 
+@pytest.mark.parametrize("bs,vocab", [(4, 151936), (1, 8192 + 10), (3, 40), (8, 3000), (2, 16384)])
+@pytest.mark.parametrize("temperature,top_p,top_k", [(0.6, 0.95, 20), (1.0, 0.5, 5), (0.8, 0.0, 48),
+                                                     (1.3, 0.99, 1)])
+def test_hip_sampler_matches_full_vocabulary(bs, vocab, temperature, top_p, top_k):
+    """The one-launch sampler (zkv_sample_window) against the op-for-op
+    restatement of LLM.py:63-139 from the same device generator state: vocab
+    sizes with a slice shorter than the window (8202, 40), a single slice
+    (3000) and exact multiples; peaked and flat rows."""
+    if top_k + 16 >= vocab:
+        pytest.skip("the window covers the vocabulary: the full path runs")
+    g = torch.Generator(device="cuda").manual_seed(vocab + top_k)
+    ga = torch.Generator(device="cuda").manual_seed(5)
+    gb = torch.Generator(device="cuda").manual_seed(5)
+    for trial in range(12):
+        logits = torch.randn(bs, vocab, generator=g, device="cuda") * (0.5, 4.0, 16.0)[trial % 3]
+        a = ds.sample_next_token(logits, temperature, top_p, top_k, generator=ga)
+        b = ds.sample_next_token_full(logits, temperature, top_p, top_k, generator=gb)
+        assert a.dtype == torch.int64 and a.shape == (bs,)
+        assert torch.equal(a, b), (trial, a, b)
+        # the launch itself (no tie overflow on these rows, so no full-vocabulary draw)
+        expo = torch.empty_like(logits).exponential_(1, generator=g)
+        tok, flags = ds.sample_window_launch(logits, temperature, top_p, top_k, expo)
+        assert int(flags.abs().sum()) == 0
+        assert torch.equal(tok, ds.draw_full_vocabulary(logits, temperature, top_p, top_k, expo)), trial
+
+
+def test_hip_sampler_ties_at_kth_value():
+    """Ties at the k-th value: a group inside the window is drawn like any
+    kept token; one wider than the window sets the row's overflow flag and the
+    draw runs over the whole vocabulary with the same Exp(1) row."""
+    for n_ties in (3, 40):
+        logits = torch.full((2, 20000), -5.0, device="cuda")
+        logits[:, 7:11] = torch.tensor([4.0, 3.0, 2.5, 2.0], device="cuda")
+        logits[:, 9000:9000 + n_ties] = 1.0           # k = 6: the 6th value is a tie
+        expo = torch.empty_like(logits).exponential_(1)
+        _, flags = ds.sample_window_launch(logits, 1.0, 0.999, 6, expo)
+        assert flags.tolist() == [int(n_ties > 16)] * 2
+        ga = torch.Generator(device="cuda").manual_seed(1)
+        gb = torch.Generator(device="cuda").manual_seed(1)
+        seen = set()
+        for _ in range(200):
+            a = ds.sample_next_token(logits, 1.0, 0.999, 6, generator=ga)
+            b = ds.sample_next_token_full(logits, 1.0, 0.999, 6, generator=gb)
+            assert torch.equal(a, b)
+            seen.update(a.tolist())
+        assert seen <= set(range(7, 11)) | set(range(9000, 9000 + n_ties))
+        assert len(seen & set(range(9000, 9000 + n_ties))) > 1
+
+
+def test_hip_sampler_rejects_bad_arguments():
+    from zoomkv_revision_amd._lib import ZkvError, check, lib, ptr
+    L = lib()
+    x = torch.randn(2, 1000, device="cuda")
+    e = torch.ones_like(x)
+    tok = torch.empty(2, dtype=torch.int64, device="cuda")
+    fl = torch.empty(2, dtype=torch.int32, device="cuda")
+    ws = torch.zeros(1 << 16, dtype=torch.uint8, device="cuda")
+    args = lambda k, w, nbytes: (ptr(x), 1000, 2, 1000, 1.0, k, w, 0.9, ptr(e), 1000, ptr(tok), ptr(fl),
+                                 ptr(ws), nbytes, 0)
+    with pytest.raises(ZkvError):
+        check(L.zkv_sample_window(*args(20, 65, ws.numel())))        # window over one wave
+    with pytest.raises(ZkvError):
+        check(L.zkv_sample_window(*args(20, 20, ws.numel())))        # window not past k
+    with pytest.raises(ZkvError):
+        check(L.zkv_sample_window(*args(20, 36, 16)))                # workspace too small
+    check(L.zkv_sample_window(*args(20, 36, ws.numel())))
+    torch.cuda.synchronize()
+    assert ((tok >= 0) & (tok < 1000)).all() and (fl == 0).all()
+
+
 def _bf16_close(got, ref, ulps=1.0):
     """Within `ulps` bf16 units at the tensor's largest magnitude (the fp32
     accumulation order differs from the library GEMM's)."""

@@ -88,6 +88,8 @@ SIGNATURES = {
     "zkv_host_free": (I32, [P]),
     "zkv_decode_linear": (I32, [P, I64, I32, I32, P, I32, P, F32, P, I64, P, I64, I32, I32, P]),
     "zkv_qk_norm_rope": (I32, [P, I64, I32, I32, I32, P, P, F32, P, P, P, P, I64, I64, P, I64, I64, P]),
+    "zkv_sample_window_workspace_size": (SZ, [I32, I32, I32]),
+    "zkv_sample_window": (I32, [P, I64, I32, I32, F32, I32, I32, F32, P, I64, P, P, P, SZ, P]),
 }
 
 _lib = None

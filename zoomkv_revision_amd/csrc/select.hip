@@ -815,6 +815,146 @@ __global__ __launch_bounds__(kTopkThreads) void quest_topk_kernel(
 }
 
 // ----------------------------------------------------------------------------
+// Next-token sampling over the top-(k + W) window (Z/model_hub/LLM.py:63-139:
+// temperature, top-k with ties at the k-th value kept, top-p keeping the token
+// that crosses top_p, softmax, one multinomial draw), one launch per step.
+// Block (x, row) takes the row's logits [x S, (x + 1) S), S = 8192, scaled as
+// torch scales a CUDA tensor by a Python float (times the fp32 reciprocal),
+// and stores its W' = k + W largest under the strict order (value desc, index
+// asc) device-coherently: key bits << 32 | ~index.  The block that completes
+// the row ranks the row's candidates in LDS (the row's first W' under the same
+// order, sorted), and wave 0 holds the window, lane i its i-th largest:
+//  * overflow: the last window value equals the k-th, so the tie group may
+//    reach past the window; the host then draws over the whole vocabulary;
+//  * top-k keeps the values >= the k-th; top-p (0 < p < 1) drops the tokens
+//    after the first whose cumulative probability (summed in window order)
+//    exceeds p;
+//  * softmax as torch's warp softmax (max, exp of the difference, xor
+//    butterfly sum over 64 lanes, division), then the draw of
+//    torch.multinomial for one sample: the first index of the largest
+//    p / e, e = the caller's Exp(1) row drawn from the generator.
+// ----------------------------------------------------------------------------
+constexpr int kSampleR = 8;
+constexpr int kSampleSlice = kSampleR * kTopkThreads;  // logits per block
+constexpr int kSampleMaxWindow = 64;                   // k + W: one wave holds the window
+constexpr int kSampleMaxCand = 2 * kTopkThreads;       // slices x window ranked per row
+
+__device__ __forceinline__ float wave_max_xor(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum_xor(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = v + __shfl_xor(v, off);
+  return v;
+}
+
+// softmax over the 64 lanes (-inf lanes give 0)
+__device__ __forceinline__ float wave_softmax(float x) {
+  const float mx = wave_max_xor(x);
+  const float e = expf(x - mx);
+  return e / wave_sum_xor(e);
+}
+
+__global__ __launch_bounds__(kTopkThreads) void sample_window_kernel(
+    const float* __restrict__ logits, int64_t ld, int vocab, float inv_t, int k, int win, float top_p,
+    const float* __restrict__ expo, int64_t e_ld, uint64_t* __restrict__ cand, unsigned int* __restrict__ slots,
+    int64_t* __restrict__ tokens, int32_t* __restrict__ overflow) {
+  constexpr int R = kSampleR;
+  __shared__ __align__(16) int s_hist[2][256];
+  __shared__ __align__(16) uint32_t s_cnt[R * kTopkWaves];
+  __shared__ int s_sel[3];
+  __shared__ int s_last;
+  __shared__ uint64_t s_c[kSampleMaxCand];
+  __shared__ uint64_t s_win[kSampleMaxWindow];
+  const int tid = threadIdx.x, row = blockIdx.y, nb = gridDim.x;
+  const int x0 = blockIdx.x * kSampleSlice;
+  const int L = min(kSampleSlice, vocab - x0);
+  const float* x = logits + row * ld + x0;
+  uint64_t* crow = cand + (static_cast<int64_t>(row) * nb + blockIdx.x) * win;
+  auto put = [&](int pos, int p) {  // position p of the slice as candidate pos
+    const uint64_t c = (static_cast<uint64_t>(ordered_key(x[p] * inv_t)) << 32) |
+                       static_cast<uint32_t>(~static_cast<uint32_t>(x0 + p));
+    __hip_atomic_store(crow + pos, c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  };
+  if (L <= win) {
+    for (int i = tid; i < win; i += kTopkThreads) {
+      if (i < L) put(i, i);
+      else __hip_atomic_store(crow + i, uint64_t{0}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  } else {
+    uint32_t key[R];
+#pragma unroll
+    for (int j = 0; j < R; ++j) key[j] = ordered_key(x[min(tid + kTopkThreads * j, L - 1)] * inv_t);
+    if (tid < 128) reinterpret_cast<int4*>(&s_hist[0][0])[tid] = make_int4(0, 0, 0, 0);
+    __syncthreads();
+    int remain;
+    const uint32_t T = radix_select<R>(key, L, win, s_hist, s_sel, remain);
+    ordered_emit<R>(key, L, win, T, remain, s_cnt, put);
+  }
+  // this lane's candidate stores are device-visible, then one arrival per block
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (tid == 0) s_last = arrive_last_count(slots + row, nb);
+  __syncthreads();
+  if (!s_last) return;
+
+  // ---- the row's window: rank the nb * win candidates (distinct indices) ----
+  const int nc = nb * win;
+  uint64_t c[kSampleMaxCand / kTopkThreads];
+#pragma unroll
+  for (int h = 0; h < kSampleMaxCand / kTopkThreads; ++h) {
+    const int i = tid + h * kTopkThreads;
+    c[h] = i < nc ? __hip_atomic_load(cand + static_cast<int64_t>(row) * nc + i, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT)
+                  : uint64_t{0};
+    s_c[i] = c[h];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int h = 0; h < kSampleMaxCand / kTopkThreads; ++h) {
+    if (tid + h * kTopkThreads < nc) {
+      int rank = 0;
+      for (int j = 0; j < nc; ++j) rank += s_c[j] > c[h] ? 1 : 0;
+      if (rank < win) s_win[rank] = c[h];
+    }
+  }
+  __syncthreads();
+  if (tid >= 64) return;
+  const int lane = tid;
+  const bool in = lane < win;
+  const uint64_t cw = in ? s_win[lane] : uint64_t{0};
+  const uint32_t kb = static_cast<uint32_t>(cw >> 32);
+  const float val = __uint_as_float((kb & 0x80000000u) ? (kb & 0x7FFFFFFFu) : ~kb);
+  const int idx = static_cast<int>(~static_cast<uint32_t>(cw));
+  const float kth = __shfl(val, k - 1), last = __shfl(val, win - 1);
+  float w = in && !(val < kth) ? val : -INFINITY;
+  if (top_p > 0.0f && top_p < 1.0f) {
+    const float p = wave_softmax(w);
+    float cum = 0.0f;  // p_0 + ... + p_lane, left to right
+    for (int j = 0; j < win; ++j) {
+      const float pj = __shfl(p, j);
+      if (j <= lane) cum = cum + pj;
+    }
+    const float before = __shfl_up(cum, 1);
+    if (lane >= 1 && before > top_p) w = -INFINITY;
+  }
+  const float prob = wave_softmax(w);
+  const float e = expo[row * e_ld + (in ? idx : 0)];
+  const float ratio = in ? prob / e : -INFINITY;
+  const float best = wave_max_xor(ratio);
+  int tok = in && ratio == best ? idx : vocab;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) tok = min(tok, __shfl_xor(tok, off));
+  if (lane == 0) {
+    tokens[row] = tok;
+    overflow[row] = last == kth ? 1 : 0;
+  }
+}
+
+// ----------------------------------------------------------------------------
 // CDS density: centroid[chunk_id] . q (rerank_topk.cu:560-624): buf[t] = c[t]q[t]
 // for t < 128, then buf[t] += buf[t+s], s = 64..1; invalid id -> -1e30.
 // A wave scores kDensityItems slots (lane l starts with p[l] + p[l+64] of
@@ -1473,6 +1613,42 @@ extern "C" int zkv_kivi_qk_dense_sparse_compact(const int64_t* chunk_ids, int64_
                         chunk_min, chunk_max, cm_sb, cm_sh, n_chunks_max, raw_q, q_sb, q_sh, dense_topk,
                         sparse_topk, group_size, out_width, out_scores, out_indices, o_sb, o_sh, bs, kv, nk,
                         stream);
+}
+
+namespace {
+// the arrival counters lead the workspace: their place depends on bs only
+size_t sample_slot_bytes(int bs) { return (static_cast<size_t>(bs) * 4 + 255) / 256 * 256; }
+}  // namespace
+
+extern "C" size_t zkv_sample_window_workspace_size(int bs, int vocab, int window) {
+  if (bs <= 0 || vocab <= 0 || window <= 0) return 0;
+  const size_t nb = (static_cast<size_t>(vocab) + kSampleSlice - 1) / kSampleSlice;
+  return sample_slot_bytes(bs) + static_cast<size_t>(bs) * nb * window * 8;
+}
+
+extern "C" int zkv_sample_window(const float* logits, int64_t ld, int bs, int vocab, float inv_temperature,
+                                 int top_k, int window, float top_p, const float* expo, int64_t expo_ld,
+                                 int64_t* tokens, int32_t* overflow, void* workspace, size_t workspace_bytes,
+                                 zkv_stream_t stream) {
+  ZKV_REQUIRE(logits && expo && tokens && overflow && workspace, "zkv_sample_window: null pointer");
+  ZKV_REQUIRE(bs > 0 && bs <= 65535 && vocab > 0 && ld >= vocab && expo_ld >= vocab,
+              "zkv_sample_window: bad sizes bs=%d vocab=%d ld=%lld expo_ld=%lld", bs, vocab,
+              static_cast<long long>(ld), static_cast<long long>(expo_ld));
+  ZKV_REQUIRE(top_k >= 1 && window > top_k && window <= kSampleMaxWindow && window < vocab,
+              "zkv_sample_window: need 1 <= top_k < window <= %d and window < vocab (top_k=%d window=%d vocab=%d)",
+              kSampleMaxWindow, top_k, window, vocab);
+  const int nb = (vocab + kSampleSlice - 1) / kSampleSlice;
+  ZKV_REQUIRE(static_cast<int64_t>(nb) * window <= kSampleMaxCand,
+              "zkv_sample_window: %d slices of %d logits x window %d exceed %d candidates per row", nb,
+              kSampleSlice, window, kSampleMaxCand);
+  const size_t need = zkv_sample_window_workspace_size(bs, vocab, window);
+  ZKV_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 255) == 0 && workspace_bytes >= need,
+              "zkv_sample_window: workspace needs %zu bytes, 256-byte aligned (got %zu)", need, workspace_bytes);
+  auto* slots = static_cast<unsigned int*>(workspace);
+  auto* cand = reinterpret_cast<uint64_t*>(static_cast<uint8_t*>(workspace) + sample_slot_bytes(bs));
+  sample_window_kernel<<<dim3(nb, bs), kTopkThreads, 0, reinterpret_cast<hipStream_t>(stream)>>>(
+      logits, ld, vocab, inv_temperature, top_k, window, top_p, expo, expo_ld, cand, slots, tokens, overflow);
+  return check_launch("sample_window_kernel");
 }
 
 extern "C" int zkv_page_minmax_f16(const uint16_t* keys, int64_t k_sb, int64_t k_sh, int64_t k_st,

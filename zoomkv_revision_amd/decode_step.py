@@ -237,6 +237,7 @@ class RandomQwen3:
 # Candidates kept beyond the k-th by the windowed sampler, so that ties at the
 # k-th value (which top-k keeps) still fall inside the window.
 _SAMPLE_TIE_WINDOW = 16
+_SAMPLE_HIP_MAX_WINDOW = 64   # zkv_sample_window: one wave holds the window
 
 
 def sample_next_token(logits: torch.Tensor, temperature: float = 1.0, top_p: float = 0.0,
@@ -256,7 +257,12 @@ def sample_next_token(logits: torch.Tensor, temperature: float = 1.0, top_p: flo
     and among tokens tied at the top-p cut the kept ones follow torch.topk's
     order where the reference's follow torch.sort's (neither is specified).
     A tie group that overflows the window (checked on the device, one host
-    read) takes the full path."""
+    read) takes the full path.
+
+    A CUDA row with k + 16 <= 64 (and a vocabulary of at most 2048 / (k + 16)
+    slices of 8192) runs the whole chain as one HIP launch
+    (``zkv_sample_window``) after torch draws the Exp(1) row; other rows run
+    the same steps as torch ops."""
     if logits.dim() == 3:
         logits = logits.squeeze(1)
     elif logits.dim() == 1:
@@ -266,6 +272,9 @@ def sample_next_token(logits: torch.Tensor, temperature: float = 1.0, top_p: flo
     vocab = logits.size(-1)
     if top_k <= 0 or min(top_k, vocab) + _SAMPLE_TIE_WINDOW >= vocab:
         return sample_next_token_full(logits, temperature, top_p, top_k, generator)
+    window = min(top_k, vocab) + _SAMPLE_TIE_WINDOW
+    if logits.is_cuda and window <= _SAMPLE_HIP_MAX_WINDOW and -(-vocab // 8192) * window <= 2048:
+        return _sample_window_hip(logits, temperature, top_p, min(top_k, vocab), generator)
     scaled = logits / temperature
     k = min(top_k, vocab)
     vals, idx = torch.topk(scaled, k + _SAMPLE_TIE_WINDOW, dim=-1)
@@ -296,6 +305,12 @@ def sample_next_token_full(logits: torch.Tensor, temperature: float = 1.0, top_p
         logits = logits.unsqueeze(0)
     if temperature < 1e-5:
         return logits.argmax(dim=-1)
+    probs = _full_probs(logits, temperature, top_p, top_k)
+    return torch.multinomial(probs, num_samples=1, generator=generator).squeeze(-1)
+
+
+def _full_probs(logits: torch.Tensor, temperature: float, top_p: float, top_k: int) -> torch.Tensor:
+    """The probabilities LLM.py:63-139 draws from, over the whole vocabulary."""
     logits = logits / temperature
     if top_k > 0:
         top_k = min(top_k, logits.size(-1))
@@ -307,8 +322,67 @@ def sample_next_token_full(logits: torch.Tensor, temperature: float = 1.0, top_p
         remove[..., 1:] = remove[..., :-1].clone()
         remove[..., 0] = False
         logits = logits.masked_fill(remove.scatter(-1, sorted_idx, remove), float("-inf"))
-    probs = F.softmax(logits, dim=-1)
-    return torch.multinomial(probs, num_samples=1, generator=generator).squeeze(-1)
+    return F.softmax(logits, dim=-1)
+
+
+_SAMPLE_WS: dict = {}
+
+
+def sample_window_launch(logits: torch.Tensor, temperature: float, top_p: float, k: int,
+                         expo: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """One ``zkv_sample_window`` launch over fp32 rows [bs, vocab] with the
+    Exp(1) rows ``expo``: (tokens int64 [bs], overflow flags int32 [bs])."""
+    from ._lib import check, lib, ptr, stream_of
+    bs, vocab = logits.shape
+    dev = logits.device
+    window = k + _SAMPLE_TIE_WINDOW
+    L = lib()
+    need = L.zkv_sample_window_workspace_size(bs, vocab, window)
+    key = (dev, stream_of(logits))
+    ent = _SAMPLE_WS.get(key)
+    if ent is None or ent[0].numel() < need:
+        ent = [torch.zeros(max(need, 1 << 12), dtype=torch.uint8, device=dev), bs]
+        _SAMPLE_WS[key] = ent
+    elif ent[1] != bs:
+        # the arrival counters sit in the first 4 bs bytes (rounded up to 256):
+        # zero them for the new row count
+        ent[0][:(bs * 4 + 255) // 256 * 256].zero_()
+        ent[1] = bs
+    ws = ent[0]
+    tokens = torch.empty(bs, dtype=torch.int64, device=dev)
+    flags = torch.empty(bs, dtype=torch.int32, device=dev)
+    # torch scales a CUDA tensor by a Python float as a product with the fp32 reciprocal
+    inv_t = float(torch.tensor(1.0, dtype=torch.float32) / torch.tensor(temperature, dtype=torch.float32))
+    check(L.zkv_sample_window(ptr(logits), logits.stride(0), bs, vocab, inv_t, k, window, float(top_p),
+                              ptr(expo), expo.stride(0), ptr(tokens), ptr(flags), ptr(ws), ws.numel(),
+                              stream_of(logits)))
+    return tokens, flags
+
+
+def _sample_window_hip(logits: torch.Tensor, temperature: float, top_p: float, k: int,
+                       generator: torch.Generator | None) -> torch.Tensor:
+    """sample_next_token on a CUDA row: torch draws the Exp(1) row that
+    torch.multinomial would draw from the generator, then one launch ranks the
+    top-(k + 16) window and applies top-k, top-p, the softmax and the draw.  A
+    tie group that overflows the window draws over the whole vocabulary with
+    the same Exp(1) row (one host read of the per-row flags)."""
+    if logits.dtype != torch.float32 or logits.stride(-1) != 1:
+        logits = logits.float().contiguous()
+    expo = torch.empty_like(logits).exponential_(1, generator=generator)
+    tokens, flags = sample_window_launch(logits, temperature, top_p, k, expo)
+    if bool(flags.cpu().any()):
+        return draw_full_vocabulary(logits, temperature, top_p, k, expo)
+    return tokens
+
+
+def draw_full_vocabulary(logits: torch.Tensor, temperature: float, top_p: float, top_k: int,
+                         expo: torch.Tensor) -> torch.Tensor:
+    """torch.multinomial(probs, 1)'s draw from the Exp(1) rows ``expo``: the
+    lowest index of the largest probs / expo, probs those of LLM.py:63-139."""
+    ratio = _full_probs(logits, temperature, top_p, top_k) / expo
+    best = ratio.max(dim=-1, keepdim=True)[0]
+    vocab = logits.size(-1)
+    return torch.where(ratio == best, torch.arange(vocab, device=logits.device), vocab).min(dim=-1)[0]
 
 
 def build_cache(geo: Qwen3Geometry, batch: int, context: int, max_new: int, interval: int,
