@@ -901,31 +901,43 @@ __global__ __launch_bounds__(kTopkThreads) void sample_window_kernel(
   __syncthreads();
   if (!s_last) return;
 
-  // ---- the row's window: rank the nb * win candidates (distinct indices) ----
+  // ---- the row's window: the top `win` of its nb * win candidates ----
+  // Candidate positions run in index order (slices in order, each slice's
+  // candidates in index order), so the radix select's (key desc, position asc)
+  // is (value desc, index asc).  The winners, emitted in position order, are
+  // then ranked among themselves.
+  constexpr int RC = 4;  // register rows of the radix helpers (positions past nc are ignored)
+  static_assert(kSampleMaxCand <= RC * kTopkThreads, "candidates per row within the register rows");
   const int nc = nb * win;
-  uint64_t c[kSampleMaxCand / kTopkThreads];
+  uint32_t ck[RC] = {0u, 0u, 0u, 0u};
 #pragma unroll
   for (int h = 0; h < kSampleMaxCand / kTopkThreads; ++h) {
     const int i = tid + h * kTopkThreads;
-    c[h] = i < nc ? __hip_atomic_load(cand + static_cast<int64_t>(row) * nc + i, __ATOMIC_RELAXED,
-                                      __HIP_MEMORY_SCOPE_AGENT)
-                  : uint64_t{0};
-    s_c[i] = c[h];
+    const uint64_t c = i < nc ? __hip_atomic_load(cand + static_cast<int64_t>(row) * nc + i, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT)
+                              : uint64_t{0};
+    s_c[i] = c;
+    ck[h] = static_cast<uint32_t>(c >> 32);
+  }
+  if (tid < 128) reinterpret_cast<int4*>(&s_hist[0][0])[tid] = make_int4(0, 0, 0, 0);
+  __syncthreads();
+  {
+    int remain;
+    const uint32_t T = radix_select<RC>(ck, nc, win, s_hist, s_sel, remain);
+    ordered_emit<RC>(ck, nc, win, T, remain, s_cnt, [&](int pos, int p) { s_win[pos] = s_c[p]; });
   }
   __syncthreads();
-#pragma unroll
-  for (int h = 0; h < kSampleMaxCand / kTopkThreads; ++h) {
-    if (tid + h * kTopkThreads < nc) {
-      int rank = 0;
-      for (int j = 0; j < nc; ++j) rank += s_c[j] > c[h] ? 1 : 0;
-      if (rank < win) s_win[rank] = c[h];
-    }
+  if (tid < win) {
+    const uint64_t c = s_win[tid];
+    int rank = 0;
+    for (int j = 0; j < win; ++j) rank += s_win[j] > c ? 1 : 0;
+    s_c[rank] = c;  // s_c is free again: the window in rank order
   }
   __syncthreads();
   if (tid >= 64) return;
   const int lane = tid;
   const bool in = lane < win;
-  const uint64_t cw = in ? s_win[lane] : uint64_t{0};
+  const uint64_t cw = in ? s_c[lane] : uint64_t{0};
   const uint32_t kb = static_cast<uint32_t>(cw >> 32);
   const float val = __uint_as_float((kb & 0x80000000u) ? (kb & 0x7FFFFFFFu) : ~kb);
   const int idx = static_cast<int>(~static_cast<uint32_t>(cw));
